@@ -1,0 +1,131 @@
+"""ctypes binding of ``libavattn.so`` (declared in ``include/avattn.h``).
+
+The library is loaded lazily on first use and never silently replaced: if it
+is missing or fails to load, every operation raises.  There is no CPU or
+PyTorch fallback for the attention path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("AVATTN_LIB", _PKG / "libavattn.so"))
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_ptr = ctypes.c_void_p
+c_f32 = ctypes.c_float
+c_size = ctypes.c_size_t
+c_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> (restype, argtypes); must mirror include/avattn.h exactly.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "avattn_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "avattn_abi_version": (ctypes.c_int, []),
+    "avattn_fwd": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p,
+         c_ptr,
+         c_ptr],
+    ),
+    "avattn_bwd_workspace_size": (c_size, [c_i32, c_i32, c_i32]),
+    "avattn_bwd": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_i64p, c_i64p, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
+         c_ptr, c_size,
+         c_ptr],
+    ),
+    "avattn_lse_merge": (ctypes.c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i32, c_i32, c_ptr]),
+    "avattn_rope_tables": (
+        ctypes.c_int,
+        [c_ptr, c_i64, c_i64, c_i32, c_i32, c_i32,
+         c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_ptr, c_ptr, c_ptr],
+    ),
+    "avattn_rope_apply": (
+        ctypes.c_int,
+        [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_ptr, c_i64, c_i32,
+         c_ptr, c_i64p, c_ptr],
+    ),
+}
+
+# Status codes (include/avattn.h).
+OK = 0
+ERR_NULL_POINTER = 1
+ERR_BAD_SHAPE = 2
+ERR_HEAD_DIM = 3
+ERR_GQA = 4
+ERR_LAYOUT = 5
+ERR_WORKSPACE = 6
+ERR_LAUNCH = 7
+ERR_TOO_LARGE = 8
+ERR_ARGUMENT = 9
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class AvattnError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, status: int, where: str, message: str) -> None:
+        super().__init__(f"{where}: {message} (avattn status {status})")
+        self.status = status
+
+
+def load() -> ctypes.CDLL:
+    """Load and bind the library once; raise if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"avattn HIP library not found at {LIB_PATH}; build it with "
+                "`python -m avgen_amd.build` (no fallback path exists)"
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def strerror(status: int) -> str:
+    """Text of a status code."""
+    return load().avattn_strerror(status).decode()
+
+
+def check(status: int, where: str) -> None:
+    """Raise :class:`AvattnError` (or a mapped builtin) for a failing status."""
+    if status == OK:
+        return
+    msg = strerror(status)
+    if status in (ERR_BAD_SHAPE, ERR_HEAD_DIM, ERR_GQA, ERR_TOO_LARGE):
+        raise ValueError(f"{where}: {msg}")
+    raise AvattnError(status, where, msg)
+
+
+def i64_array(values) -> ctypes.Array:
+    """A C ``int64_t[]`` holding ``values``."""
+    vals = [int(v) for v in values]
+    return (ctypes.c_int64 * len(vals))(*vals)

@@ -1,0 +1,231 @@
+// C ABI entry points (include/avattn.h): argument validation, then kernel
+// launches on the caller's stream.  Validation happens before any HIP call, so
+// a rejected call touches no device state.
+#include "avattn.h"
+
+#include <math.h>
+
+#include "avattn_kernels.h"
+
+using namespace avattn;
+
+namespace {
+
+constexpr int64_t kMaxI32 = 2147483647;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Row starts must stay 16-byte aligned: every stride a multiple of 8 bf16.
+bool strides_ok(const int64_t* s) { return s && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+
+int check_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32_t D) {
+  if (B < 0 || Hq < 0 || Hkv < 0 || Lq < 0 || Lk < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (D != 64 && D != 128) return AVATTN_ERR_HEAD_DIM;
+  if (Hkv == 0 || Hq == 0) return (B == 0) ? AVATTN_OK : AVATTN_ERR_GQA;
+  if (Hq % Hkv != 0) return AVATTN_ERR_GQA;
+  // Grid sizes and per-(b,h) row indices are 32-bit.
+  const int64_t qtiles = ((int64_t)Lq + 127) / 128;
+  const int64_t ktiles = ((int64_t)Lk + 127) / 128;
+  if (qtiles * B * Hq > kMaxI32 || ktiles * B * Hkv > kMaxI32) return AVATTN_ERR_TOO_LARGE;
+  if ((int64_t)B * Hq * Lq > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
+  return AVATTN_OK;
+}
+
+int launch_status(hipError_t e) { return e == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH; }
+
+}  // namespace
+
+extern "C" {
+
+const char* avattn_strerror(int status) {
+  switch (status) {
+    case AVATTN_OK: return "success";
+    case AVATTN_ERR_NULL_POINTER: return "a required pointer argument is NULL";
+    case AVATTN_ERR_BAD_SHAPE: return "invalid (negative) size";
+    case AVATTN_ERR_HEAD_DIM: return "unsupported head_dim (supported: 64, 128)";
+    case AVATTN_ERR_GQA: return "heads_q must be a positive multiple of heads_kv";
+    case AVATTN_ERR_LAYOUT:
+      return "misaligned tensor: pointers must be 16-byte aligned, head_dim contiguous and "
+             "batch/head/seq strides multiples of 8 elements";
+    case AVATTN_ERR_WORKSPACE: return "workspace missing or smaller than avattn_bwd_workspace_size()";
+    case AVATTN_ERR_LAUNCH: return "HIP kernel launch failed";
+    case AVATTN_ERR_TOO_LARGE: return "problem size exceeds the 32-bit grid/index range";
+    case AVATTN_ERR_ARGUMENT: return "invalid argument";
+    default: return "unknown avattn status";
+  }
+}
+
+int avattn_abi_version(void) { return 1; }
+
+int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_strides, const int64_t* k_strides,
+               const int64_t* v_strides, int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
+               int32_t len_k, int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+               const float* rope_cos_q, const float* rope_sin_q, int64_t rope_batch_stride, float scale, void* out,
+               const int64_t* out_strides, float* lse, avattn_stream_t stream) {
+  int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  if (!q_strides || !k_strides || !v_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
+  if (!(scale > 0.f) || !isfinite(scale)) return AVATTN_ERR_ARGUMENT;
+  if ((rope_cos_q == nullptr) != (rope_sin_q == nullptr)) return AVATTN_ERR_ARGUMENT;
+  const int64_t rows = (int64_t)batch * heads_q * len_q;
+  if (rows == 0) return AVATTN_OK;
+  if (!q || !out || !lse) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(q) || !aligned16(out) || !strides_ok(q_strides) || !strides_ok(out_strides))
+    return AVATTN_ERR_LAYOUT;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (len_k == 0)
+    return launch_status(launch_empty(static_cast<bf16*>(out), out_strides[0], out_strides[1], out_strides[2], batch,
+                                      heads_q, len_q, head_dim, lse, s));
+  if (!k || !v) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(k) || !aligned16(v) || !strides_ok(k_strides) || !strides_ok(v_strides)) return AVATTN_ERR_LAYOUT;
+  if (rope_cos_q && (!aligned16(rope_cos_q) || !aligned16(rope_sin_q) || rope_batch_stride % 4 != 0))
+    return AVATTN_ERR_LAYOUT;
+  if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
+
+  FwdArgs a;
+  a.q = static_cast<const bf16*>(q);
+  a.k = static_cast<const bf16*>(k);
+  a.v = static_cast<const bf16*>(v);
+  a.qsb = q_strides[0]; a.qsh = q_strides[1]; a.qsl = q_strides[2];
+  a.ksb = k_strides[0]; a.ksh = k_strides[1]; a.ksl = k_strides[2];
+  a.vsb = v_strides[0]; a.vsh = v_strides[1]; a.vsl = v_strides[2];
+  a.B = batch; a.Hq = heads_q; a.Hkv = heads_kv; a.Lq = len_q; a.Lk = len_k;
+  a.mask = key_mask;
+  a.msb = key_mask_batch_stride;
+  a.cos_q = rope_cos_q;
+  a.sin_q = rope_sin_q;
+  a.rsb = rope_batch_stride;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.o = static_cast<bf16*>(out);
+  a.osb = out_strides[0]; a.osh = out_strides[1]; a.osl = out_strides[2];
+  a.lse = lse;
+  return launch_status(launch_fwd(a, head_dim, s));
+}
+
+size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q) {
+  if (batch <= 0 || heads_q <= 0 || len_q <= 0) return 0;
+  return (size_t)2 * (size_t)batch * (size_t)heads_q * (size_t)len_q * sizeof(float);
+}
+
+int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out, const float* lse,
+               const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
+               const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
+               int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+               int64_t key_mask_batch_stride, float scale, void* dq, const int64_t* dq_strides, void* dk,
+               const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
+               size_t workspace_bytes, avattn_stream_t stream) {
+  int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  if (!dout_strides || !q_strides || !k_strides || !v_strides || !out_strides || !dq_strides || !dk_strides ||
+      !dv_strides)
+    return AVATTN_ERR_NULL_POINTER;
+  if (!(scale > 0.f) || !isfinite(scale)) return AVATTN_ERR_ARGUMENT;
+  if ((int64_t)batch * heads_q == 0) return AVATTN_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool have_q = len_q > 0, have_k = len_k > 0;
+  if (have_q && (!dq || !aligned16(dq) || !strides_ok(dq_strides)))
+    return !dq ? AVATTN_ERR_NULL_POINTER : AVATTN_ERR_LAYOUT;
+  if (have_k && (!dk || !dv)) return AVATTN_ERR_NULL_POINTER;
+  if (have_k && (!aligned16(dk) || !aligned16(dv) || !strides_ok(dk_strides) || !strides_ok(dv_strides)))
+    return AVATTN_ERR_LAYOUT;
+  if (!have_q || !have_k) {
+    // Empty attention: every gradient is zero.
+    hipError_t e = hipSuccess;
+    if (have_q)
+      e = launch_zero_rows(static_cast<bf16*>(dq), dq_strides[0], dq_strides[1], dq_strides[2], batch, heads_q, len_q,
+                           head_dim, s);
+    if (e == hipSuccess && have_k)
+      e = launch_zero_rows(static_cast<bf16*>(dk), dk_strides[0], dk_strides[1], dk_strides[2], batch, heads_kv,
+                           len_k, head_dim, s);
+    if (e == hipSuccess && have_k)
+      e = launch_zero_rows(static_cast<bf16*>(dv), dv_strides[0], dv_strides[1], dv_strides[2], batch, heads_kv,
+                           len_k, head_dim, s);
+    return launch_status(e);
+  }
+  if (!dout || !q || !k || !v || !out || !lse) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(dout) || !aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out) ||
+      !strides_ok(dout_strides) || !strides_ok(q_strides) || !strides_ok(k_strides) || !strides_ok(v_strides) ||
+      !strides_ok(out_strides))
+    return AVATTN_ERR_LAYOUT;
+  if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
+  const size_t need = avattn_bwd_workspace_size(batch, heads_q, len_q);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
+
+  BwdArgs a;
+  a.dout = static_cast<const bf16*>(dout);
+  a.q = static_cast<const bf16*>(q);
+  a.k = static_cast<const bf16*>(k);
+  a.v = static_cast<const bf16*>(v);
+  a.out = static_cast<const bf16*>(out);
+  a.lse = lse;
+  a.dosb = dout_strides[0]; a.dosh = dout_strides[1]; a.dosl = dout_strides[2];
+  a.qsb = q_strides[0]; a.qsh = q_strides[1]; a.qsl = q_strides[2];
+  a.ksb = k_strides[0]; a.ksh = k_strides[1]; a.ksl = k_strides[2];
+  a.vsb = v_strides[0]; a.vsh = v_strides[1]; a.vsl = v_strides[2];
+  a.osb = out_strides[0]; a.osh = out_strides[1]; a.osl = out_strides[2];
+  a.B = batch; a.Hq = heads_q; a.Hkv = heads_kv; a.Lq = len_q; a.Lk = len_k;
+  a.mask = key_mask;
+  a.msb = key_mask_batch_stride;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.dq = static_cast<bf16*>(dq);
+  a.dqsb = dq_strides[0]; a.dqsh = dq_strides[1]; a.dqsl = dq_strides[2];
+  a.dk = static_cast<bf16*>(dk);
+  a.dksb = dk_strides[0]; a.dksh = dk_strides[1]; a.dksl = dk_strides[2];
+  a.dv = static_cast<bf16*>(dv);
+  a.dvsb = dv_strides[0]; a.dvsh = dv_strides[1]; a.dvsl = dv_strides[2];
+  const int64_t rows = (int64_t)batch * heads_q * len_q;
+  a.delta = static_cast<float*>(workspace);
+  a.lse2 = static_cast<float*>(workspace) + rows;
+  return launch_status(launch_bwd(a, head_dim, s));
+}
+
+int avattn_lse_merge(float* out_acc, float* lse_acc, const void* out_blk, const float* lse_blk, int64_t n_rows,
+                     int32_t head_dim, int32_t blk_is_bf16, avattn_stream_t stream) {
+  if (n_rows < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return AVATTN_ERR_HEAD_DIM;
+  if (n_rows == 0) return AVATTN_OK;
+  if (!out_acc || !lse_acc || !out_blk || !lse_blk) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(out_acc) || !aligned16(out_blk)) return AVATTN_ERR_LAYOUT;
+  if (n_rows > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
+  return launch_status(launch_lse_merge(out_acc, lse_acc, out_blk, lse_blk, n_rows, head_dim, blk_is_bf16 != 0,
+                                        reinterpret_cast<hipStream_t>(stream)));
+}
+
+int avattn_rope_tables(const float* coords, int64_t coords_batch_stride, int64_t coords_row_stride, int32_t batch,
+                       int32_t len, int32_t pairs, const float* inv_freq, const int32_t* axis_of_pair,
+                       const int32_t* apply_mul, const float* pos_mul, const int32_t* apply_div,
+                       const float* pos_div, float* cos_out, float* sin_out, avattn_stream_t stream) {
+  if (batch < 0 || len < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (pairs < 3 || pairs > 64) return AVATTN_ERR_HEAD_DIM;
+  if (!inv_freq || !axis_of_pair || !apply_mul || !pos_mul || !apply_div || !pos_div) return AVATTN_ERR_NULL_POINTER;
+  for (int p = 0; p < pairs; ++p)
+    if (axis_of_pair[p] < 0 || axis_of_pair[p] > 2) return AVATTN_ERR_ARGUMENT;
+  if ((int64_t)batch * len == 0) return AVATTN_OK;
+  if (!coords || !cos_out || !sin_out) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * len > kMaxI32) return AVATTN_ERR_TOO_LARGE;
+  return launch_status(launch_rope_tables(coords, coords_batch_stride, coords_row_stride, batch, len, pairs, inv_freq,
+                                          axis_of_pair, apply_mul, pos_mul, apply_div, pos_div, cos_out, sin_out,
+                                          reinterpret_cast<hipStream_t>(stream)));
+}
+
+int avattn_rope_apply(const void* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,
+                      int32_t head_dim, const float* cos_tab, const float* sin_tab, int64_t table_batch_stride,
+                      int32_t inverse, void* out, const int64_t* out_strides, avattn_stream_t stream) {
+  if (batch < 0 || heads < 0 || len < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (head_dim < 8 || head_dim > 128 || head_dim % 8 != 0) return AVATTN_ERR_HEAD_DIM;
+  if (!x_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * heads * len == 0) return AVATTN_OK;
+  if (!x || !out || !cos_tab || !sin_tab) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(x) || !aligned16(out) || !aligned16(cos_tab) || !aligned16(sin_tab) || !strides_ok(x_strides) ||
+      !strides_ok(out_strides) || table_batch_stride % 4 != 0)
+    return AVATTN_ERR_LAYOUT;
+  if ((int64_t)batch * heads > kMaxI32 || len > kMaxI32) return AVATTN_ERR_TOO_LARGE;
+  return launch_status(launch_rope_apply(static_cast<const bf16*>(x), x_strides[0], x_strides[1], x_strides[2], batch,
+                                         heads, len, head_dim, cos_tab, sin_tab, table_batch_stride, inverse != 0,
+                                         static_cast<bf16*>(out), out_strides[0], out_strides[1], out_strides[2],
+                                         reinterpret_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,243 @@
+// Device-side building blocks shared by the gfx950 attention kernels.
+//
+// MFMA used throughout: v_mfma_f32_32x32x16_bf16 (wave64).
+//   A operand (8 bf16 per lane): row i = lane % 32, k = 8*(lane/32) + e.
+//   B operand (8 bf16 per lane): col j = lane % 32, k = 8*(lane/32) + e.
+//   C/D (16 fp32 per lane):      col j = lane % 32,
+//                                row i = 8*(r/4) + 4*(lane/32) + (r%4).
+// Only the pairing of A's and B's (lane/32, e) slots matters for the sum, so a
+// kernel may assign any bijection of key/query indices to the k slots as long
+// as both operands use the same one.  The kernels exploit this to feed the C
+// layout of one product straight into the B operand of the next without a
+// register shuffle.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace avattn {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr float kPosInf = __builtin_huge_valf();
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Combine a value with the one held by the lane 32 positions away.
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with the
+// lower 32 lanes of its second; with both operands equal, every lane ends up
+// holding its own value in one result and its partner's in the other, so the
+// symmetric combinations below do not depend on which is which.
+__device__ __forceinline__ float halves_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ bf16 to_bf16(float x) { return (bf16)x; }
+
+__device__ __forceinline__ float bf16_to_f32(bf16 x) { return (float)x; }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (bf16)lo;
+  v[1] = (bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ bf16x8 bits_to_bf16x8(const u32x4& u) {
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+__device__ __forceinline__ u32x4 bf16x8_to_bits(const bf16x8& v) {
+  return __builtin_bit_cast(u32x4, v);
+}
+
+__device__ __forceinline__ bf16x8 cat4(const u32x2& lo, const u32x2& hi) {
+  u32x4 u;
+  u[0] = lo[0];
+  u[1] = lo[1];
+  u[2] = hi[0];
+  u[3] = hi[1];
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// Pack the low (hi == 0) or high (hi == 1) 16-bit halves of a and b as
+// (a.half, b.half).
+__device__ __forceinline__ uint32_t pack_halves(uint32_t a, uint32_t b, int hi) {
+  return hi ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+}
+
+// Interleaved-pair rotation of 8 consecutive channels (4 pairs) in fp32 with
+// every product rounded separately (no FMA contraction), then rounded to
+// bf16.  Matches src/avgen/models/rope.py:332-338 bit for bit.
+__device__ __forceinline__ u32x4 rotate8(const u32x4& x, const f32x4& c, const f32x4& s, bool inverse) {
+  u32x4 r;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float e = __uint_as_float(x[p] << 16);
+    const float o = __uint_as_float(x[p] & 0xffff0000u);
+    float a, b;
+    if (!inverse) {
+      a = __fsub_rn(__fmul_rn(e, c[p]), __fmul_rn(o, s[p]));
+      b = __fadd_rn(__fmul_rn(e, s[p]), __fmul_rn(o, c[p]));
+    } else {
+      a = __fadd_rn(__fmul_rn(e, c[p]), __fmul_rn(o, s[p]));
+      b = __fsub_rn(__fmul_rn(o, c[p]), __fmul_rn(e, s[p]));
+    }
+    r[p] = pack_bf16x2(a, b);
+  }
+  return r;
+}
+
+// Map a linear block id so that consecutive *logical* ids land on the same
+// XCD.  The dispatcher places block i on XCD (i % 8); logical neighbours (the
+// query tiles of one head) then share that XCD's L2 for their K/V reads.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  constexpr int kXcds = 8;
+  const int xcd = bid % kXcds;
+  const int local = bid / kXcds;
+  const int per = total / kXcds;
+  const int rem = total % kXcds;
+  return xcd * per + (xcd < rem ? xcd : rem) + local;
+}
+
+// ---------------------------------------------------------------------------
+// Tile staging helpers: global (row-major, head_dim contiguous) -> registers
+// -> LDS.  The register step lets a kernel issue the global loads of tile
+// t+1 before computing on tile t.
+// ---------------------------------------------------------------------------
+
+// Row-major tile ROWS x D staged by NT threads: each 16-byte chunk (8
+// channels) goes to lds[row * (D + 8) + col].  The +8 pad makes rows 4 banks
+// apart so eight lanes reading the same column of consecutive rows with
+// ds_read_b128 hit distinct banks.
+template <int ROWS, int D, int NT>
+struct RowTile {
+  static constexpr int kStride = D + 8;
+  static constexpr int kChunks = ROWS * D / 8;
+  static constexpr int kPer = (kChunks + NT - 1) / NT;
+  u32x4 reg[kPer];
+
+  __device__ __forceinline__ void load(const bf16* base, int64_t row_stride, int rows_valid, int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / (D / 8);
+      const int col = (c % (D / 8)) * 8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (c < kChunks && row < rows_valid)
+        v = *reinterpret_cast<const u32x4*>(base + (int64_t)row * row_stride + col);
+      reg[i] = v;
+    }
+  }
+  __device__ __forceinline__ void store(bf16* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + i * NT;
+      if (c < kChunks) {
+        const int row = c / (D / 8);
+        const int col = (c % (D / 8)) * 8;
+        *reinterpret_cast<u32x4*>(lds + row * kStride + col) = reg[i];
+      }
+    }
+  }
+};
+
+// Transposed tile: global rows x D -> lds_t[d * (ROWS + 4) + row].  A unit of
+// work is 4 rows x 8 channels (four 16-byte loads); the thread transposes it
+// in registers and writes eight 8-byte runs (4 consecutive rows of one
+// channel).  Units are numbered so that the 16 lanes of one write pass cover
+// 16 consecutive row groups of a single channel row: a contiguous,
+// conflict-free 128-byte LDS span for ROWS = 64.  Readers fetch 4 consecutive
+// rows of one channel per 8-byte read; the ROWS+4 pad puts consecutive
+// channel rows 2 banks apart.
+template <int ROWS, int D, int NT>
+struct TransTile {
+  static constexpr int kStride = ROWS + 4;
+  static constexpr int kRowGroups = ROWS / 4;
+  static constexpr int kUnits = kRowGroups * (D / 8);
+  static constexpr int kPer = (kUnits + NT - 1) / NT;
+  u32x4 reg[kPer][4];
+
+  __device__ __forceinline__ void load(const bf16* base, int64_t row_stride, int rows_valid, int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * NT;
+      const int rg = u % kRowGroups;
+      const int dg = u / kRowGroups;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = rg * 4 + r;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (u < kUnits && row < rows_valid)
+          v = *reinterpret_cast<const u32x4*>(base + (int64_t)row * row_stride + dg * 8);
+        reg[i][r] = v;
+      }
+    }
+  }
+  // Also write the row-major copy of the same data (used by kernels that
+  // need both orientations of one tile).
+  template <int RSTRIDE>
+  __device__ __forceinline__ void store_rowmajor(bf16* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * NT;
+      if (u < kUnits) {
+        const int rg = u % kRowGroups;
+        const int dg = u / kRowGroups;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<u32x4*>(lds + (rg * 4 + r) * RSTRIDE + dg * 8) = reg[i][r];
+      }
+    }
+  }
+  __device__ __forceinline__ void store(bf16* lds_t, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int u = tid + i * NT;
+      if (u < kUnits) {
+        const int rg = u % kRowGroups;
+        const int dg = u / kRowGroups;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          // channel pair (2w, 2w+1) of the 8 channels, 4 rows each.
+          const uint32_t a0 = reg[i][0][w], a1 = reg[i][1][w], a2 = reg[i][2][w], a3 = reg[i][3][w];
+          u32x2 lo, hi;
+          lo[0] = pack_halves(a0, a1, 0);
+          lo[1] = pack_halves(a2, a3, 0);
+          hi[0] = pack_halves(a0, a1, 1);
+          hi[1] = pack_halves(a2, a3, 1);
+          const int d = dg * 8 + 2 * w;
+          *reinterpret_cast<u32x2*>(lds_t + d * kStride + rg * 4) = lo;
+          *reinterpret_cast<u32x2*>(lds_t + (d + 1) * kStride + rg * 4) = hi;
+        }
+      }
+    }
+  }
+};
+
+}  // namespace avattn

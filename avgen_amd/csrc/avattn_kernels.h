@@ -1,0 +1,76 @@
+// Kernel argument blocks and launchers shared between the kernel files and
+// the C-ABI layer.  All strides are in elements; head_dim is contiguous.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "avattn_device.h"
+
+namespace avattn {
+
+struct FwdArgs {
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  int64_t qsb, qsh, qsl;
+  int64_t ksb, ksh, ksl;
+  int64_t vsb, vsh, vsl;
+  int B, Hq, Hkv, Lq, Lk;
+  const uint8_t* mask;
+  int64_t msb;
+  const float* cos_q;
+  const float* sin_q;
+  int64_t rsb;
+  float scale;       // softmax scale applied to q.k
+  float scale_log2;  // scale * log2(e)
+  bf16* o;
+  int64_t osb, osh, osl;
+  float* lse;
+};
+
+struct BwdArgs {
+  const bf16* dout;
+  const bf16* q;
+  const bf16* k;
+  const bf16* v;
+  const bf16* out;
+  const float* lse;
+  int64_t dosb, dosh, dosl;
+  int64_t qsb, qsh, qsl;
+  int64_t ksb, ksh, ksl;
+  int64_t vsb, vsh, vsl;
+  int64_t osb, osh, osl;
+  int B, Hq, Hkv, Lq, Lk;
+  const uint8_t* mask;
+  int64_t msb;
+  float scale;
+  float scale_log2;
+  bf16* dq;
+  int64_t dqsb, dqsh, dqsl;
+  bf16* dk;
+  int64_t dksb, dksh, dksl;
+  bf16* dv;
+  int64_t dvsb, dvsh, dvsl;
+  // Workspace: per query row (b, hq, i) at index (b*Hq + hq)*Lq + i.
+  float* delta;  // rowsum(dout * out)
+  float* lse2;   // lse * log2(e); +inf for rows with lse == -inf
+};
+
+hipError_t launch_fwd(const FwdArgs& a, int head_dim, hipStream_t stream);
+hipError_t launch_empty(bf16* o, int64_t osb, int64_t osh, int64_t osl, int B, int H, int L, int D, float* lse,
+                        hipStream_t stream);
+hipError_t launch_bwd(const BwdArgs& a, int head_dim, hipStream_t stream);
+hipError_t launch_zero_rows(bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
+                            hipStream_t stream);
+hipError_t launch_lse_merge(float* out_acc, float* lse_acc, const void* out_blk, const float* lse_blk, int64_t rows,
+                            int D, bool blk_bf16, hipStream_t stream);
+hipError_t launch_rope_tables(const float* coords, int64_t csb, int64_t csr, int B, int L, int P,
+                              const float* inv_freq, const int32_t* axis_of_pair, const int32_t* apply_mul,
+                              const float* pos_mul, const int32_t* apply_div, const float* pos_div, float* cos_out,
+                              float* sin_out, hipStream_t stream);
+hipError_t launch_rope_apply(const bf16* x, int64_t xsb, int64_t xsh, int64_t xsl, int B, int H, int L, int D,
+                             const float* cos_tab, const float* sin_tab, int64_t tsb, bool inverse, bf16* out,
+                             int64_t osb, int64_t osh, int64_t osl, hipStream_t stream);
+
+}  // namespace avattn

@@ -1,0 +1,378 @@
+"""Tensor-level wrappers over the C ABI, registered as ``torch.library`` ops.
+
+Every function here validates shapes/dtypes/devices, allocates outputs with
+PyTorch's caching allocator, and launches through ``libavattn.so`` on the
+current HIP stream.  There is no fallback: a CPU tensor or a missing library
+is an error.
+
+Ops (namespace ``avgen_amd``):
+
+* ``flash_fwd(q, k, v, key_mask, rope_cos, rope_sin, scale) -> (out, lse)`` —
+  the ring local step (torch/.../_context_parallel/_attention.py:468-474);
+  differentiable in q/k/v (``lse`` is a non-differentiable output).
+* ``flash_bwd(dout, q, k, v, out, lse, key_mask, scale) -> (dq, dk, dv)`` —
+  the ring backward step (torch/.../_context_parallel/_attention.py:567-575).
+* ``rope_apply(x, cos, sin, inverse) -> x_rot`` — src/avgen/models/rope.py
+  :297-338, differentiable.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "flash_fwd",
+    "flash_bwd",
+    "lse_merge_",
+    "rope_apply",
+    "rope_tables",
+    "default_scale",
+]
+
+SUPPORTED_HEAD_DIMS = (64, 128)
+
+
+def default_scale(head_dim: int) -> float:
+    """``1/sqrt(head_dim)``, SDPA's default (src/avgen/models/attention.py:265-273)."""
+    return 1.0 / math.sqrt(head_dim)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _strides3(t: torch.Tensor) -> ctypes.Array:
+    return _lib.i64_array(t.stride()[:3])
+
+
+def _require_gpu(name: str, *tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                f"{name}: avgen_amd runs only on a ROCm GPU (got a tensor on {t.device}); "
+                "there is no CPU path"
+            )
+
+
+def _check_qkv(name: str, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    for label, t in (("query", q), ("key", k), ("value", v)):
+        if t.ndim != 4:
+            raise ValueError(f"{name}: {label} must be (batch, heads, seq, head_dim); got {tuple(t.shape)}")
+        if t.dtype is not torch.bfloat16:
+            raise TypeError(f"{name}: {label} must be bfloat16; got {t.dtype}")
+    if k.shape != v.shape:
+        raise ValueError(f"{name}: key {tuple(k.shape)} and value {tuple(v.shape)} shapes differ")
+    if q.shape[0] != k.shape[0]:
+        raise ValueError(f"{name}: batch mismatch between query {tuple(q.shape)} and key {tuple(k.shape)}")
+    if q.shape[-1] != k.shape[-1]:
+        raise ValueError(f"{name}: head_dim mismatch between query and key")
+    if q.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{name}: head_dim {q.shape[-1]} not supported (supported: {SUPPORTED_HEAD_DIMS})")
+    if k.shape[1] == 0 or q.shape[1] % k.shape[1] != 0:
+        raise ValueError(f"{name}: query heads {q.shape[1]} must be a multiple of key heads {k.shape[1]}")
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """Make the last dim contiguous and row starts 16-byte aligned."""
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+    ok = ok and all(s % 8 == 0 or n == 1 for s, n in zip(t.stride()[:3], t.shape[:3]))
+    return t if ok else t.contiguous()
+
+
+def _normalise_mask(name: str, key_mask: Optional[torch.Tensor], batch: int, len_k: int):
+    """(B|1, Lk) bool/uint8 -> (uint8 tensor, batch stride) or (None, 0)."""
+    if key_mask is None:
+        return None, 0
+    if key_mask.ndim != 2 or key_mask.shape[-1] != len_k or key_mask.shape[0] not in (1, batch):
+        raise ValueError(f"{name}: key mask must be (batch, keys) = ({batch}, {len_k}); got {tuple(key_mask.shape)}")
+    if key_mask.dtype not in (torch.bool, torch.uint8):
+        raise TypeError(f"{name}: key mask must be bool; got {key_mask.dtype}")
+    m = key_mask if key_mask.stride(-1) == 1 else key_mask.contiguous()
+    if m.dtype is torch.bool:
+        m = m.view(torch.uint8)
+    stride_b = 0 if m.shape[0] == 1 else m.stride(0)
+    return m, stride_b
+
+
+def _check_tables(name: str, cos: torch.Tensor, sin: torch.Tensor, batch: int, length: int, head_dim: int):
+    if cos.ndim != 4 or cos.shape != sin.shape:
+        raise ValueError(f"{name}: rotary tables must be (batch, 1, length, pairs) and agree")
+    if cos.dtype is not torch.float32 or sin.dtype is not torch.float32:
+        raise TypeError(f"{name}: rotary tables must be float32")
+    if cos.shape[-1] * 2 != head_dim:
+        raise ValueError(
+            f"{name}: head_dim {head_dim} does not match rotary tables built for head_dim {2 * cos.shape[-1]}"
+        )
+    if cos.shape[-2] != length:
+        raise ValueError(
+            f"{name}: sequence length {length} does not match rotary tables built for length {cos.shape[-2]}"
+        )
+    if cos.shape[0] not in (1, batch) or cos.shape[1] != 1:
+        raise ValueError(f"{name}: rotary tables batch {cos.shape[0]} does not broadcast to {batch}")
+    cos = cos if cos.is_contiguous() else cos.contiguous()
+    sin = sin if sin.is_contiguous() else sin.contiguous()
+    stride_b = 0 if cos.shape[0] == 1 else cos.stride(0)
+    return cos, sin, stride_b
+
+
+# ---------------------------------------------------------------------------
+# Eager implementations (called by the custom ops)
+# ---------------------------------------------------------------------------
+
+
+def _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale):
+    name = "avgen_amd.flash_fwd"
+    _check_qkv(name, q, k, v)
+    _require_gpu(name, q, k, v, key_mask, rope_cos, rope_sin)
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    rsb = 0
+    if (rope_cos is None) != (rope_sin is None):
+        raise ValueError(f"{name}: pass both rotary tables or neither")
+    if rope_cos is not None:
+        rope_cos, rope_sin, rsb = _check_tables(name, rope_cos, rope_sin, B, Lq, D)
+    out = torch.empty_like(q, memory_format=torch.preserve_format)
+    out = _kernel_ready(out)
+    lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    st = lib.avattn_fwd(
+        _ptr(q), _ptr(k), _ptr(v), _strides3(q), _strides3(k), _strides3(v),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        _ptr(rope_cos), _ptr(rope_sin), rsb,
+        float(scale),
+        _ptr(out), _strides3(out), _ptr(lse),
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return out, lse
+
+
+def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale):
+    name = "avgen_amd.flash_bwd"
+    _check_qkv(name, q, k, v)
+    _require_gpu(name, dout, q, k, v, out, lse, key_mask)
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if dout.shape != q.shape or out.shape != q.shape:
+        raise ValueError(f"{name}: grad_out/out must have the query's shape {tuple(q.shape)}")
+    if dout.dtype is not torch.bfloat16 or out.dtype is not torch.bfloat16:
+        raise TypeError(f"{name}: grad_out and out must be bfloat16")
+    if lse.shape != (B, Hq, Lq) or lse.dtype is not torch.float32:
+        raise ValueError(f"{name}: logsumexp must be float32 (batch, heads, queries)")
+    dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
+    lse = lse.contiguous()
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    dq = _kernel_ready(torch.empty_like(q))
+    dk = _kernel_ready(torch.empty_like(k))
+    dv = _kernel_ready(torch.empty_like(v))
+    lib = _lib.load()
+    ws_bytes = lib.avattn_bwd_workspace_size(B, Hq, Lq)
+    ws = torch.empty(max(ws_bytes // 4, 4), device=q.device, dtype=torch.float32)
+    st = lib.avattn_bwd(
+        _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+        _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        float(scale),
+        _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
+        _ptr(ws), ws.numel() * 4,
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return dq, dk, dv
+
+
+def _rope_apply_impl(x, cos, sin, inverse):
+    name = "avgen_amd.rope_apply"
+    if x.ndim != 4:
+        raise ValueError(f"rotary input must be (batch, heads, length, head_dim); got {tuple(x.shape)}")
+    if x.dtype is not torch.bfloat16:
+        raise TypeError(f"{name}: input must be bfloat16; got {x.dtype}")
+    B, H, L, D = x.shape
+    cos, sin, tsb = _check_tables(name, cos, sin, B, L, D)
+    _require_gpu(name, x, cos, sin)
+    x = _kernel_ready(x)
+    out = torch.empty((B, H, L, D), device=x.device, dtype=x.dtype)
+    st = _lib.load().avattn_rope_apply(
+        _ptr(x), _strides3(x), B, H, L, D, _ptr(cos), _ptr(sin), tsb, 1 if inverse else 0,
+        _ptr(out), _strides3(out), _stream(x.device),
+    )
+    _lib.check(st, name)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration
+# ---------------------------------------------------------------------------
+
+
+@torch.library.custom_op("avgen_amd::flash_fwd", mutates_args=())
+def flash_fwd(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    key_mask: Optional[torch.Tensor],
+    rope_cos: Optional[torch.Tensor],
+    rope_sin: Optional[torch.Tensor],
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Attention forward over one KV chunk: ``(out, lse)``; see module docstring."""
+    return _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale)
+
+
+@flash_fwd.register_fake
+def _(q, k, v, key_mask, rope_cos, rope_sin, scale):
+    return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
+
+
+@torch.library.custom_op("avgen_amd::flash_bwd", mutates_args=())
+def flash_bwd(
+    dout: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    key_mask: Optional[torch.Tensor],
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Attention backward over one KV chunk given the (possibly merged) out/lse."""
+    return _bwd_impl(dout, q, k, v, out, lse, key_mask, scale)
+
+
+@flash_bwd.register_fake
+def _(dout, q, k, v, out, lse, key_mask, scale):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+@torch.library.custom_op("avgen_amd::rope_apply", mutates_args=())
+def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, inverse: bool) -> torch.Tensor:
+    """Interleaved-pair rotation (or its transpose) of ``x``."""
+    return _rope_apply_impl(x, cos, sin, inverse)
+
+
+@rope_apply.register_fake
+def _(x, cos, sin, inverse):
+    return x.new_empty(x.shape)
+
+
+def _fwd_setup(ctx, inputs, output):
+    q, k, v, key_mask, rope_cos, rope_sin, scale = inputs
+    out, lse = output
+    ctx.scale = scale
+    ctx.save_for_backward(q, k, v, out, lse, key_mask, rope_cos, rope_sin)
+    ctx.mark_non_differentiable(lse)
+
+
+def _fwd_backward(ctx, dout, _dlse):
+    q, k, v, out, lse, key_mask, rope_cos, rope_sin = ctx.saved_tensors
+    if rope_cos is not None:
+        q_rot = rope_apply(q, rope_cos, rope_sin, False)
+        dq_rot, dk, dv = flash_bwd(dout.contiguous(), q_rot, k, v, out, lse, key_mask, ctx.scale)
+        dq = rope_apply(dq_rot, rope_cos, rope_sin, True)
+    else:
+        dq, dk, dv = flash_bwd(dout.contiguous(), q, k, v, out, lse, key_mask, ctx.scale)
+    return dq, dk, dv, None, None, None, None
+
+
+torch.library.register_autograd("avgen_amd::flash_fwd", _fwd_backward, setup_context=_fwd_setup)
+
+
+def _rope_setup(ctx, inputs, output):
+    _x, cos, sin, inverse = inputs
+    ctx.inverse = inverse
+    ctx.save_for_backward(cos, sin)
+
+
+def _rope_backward(ctx, grad):
+    cos, sin = ctx.saved_tensors
+    return rope_apply(grad.contiguous(), cos, sin, not ctx.inverse), None, None, None
+
+
+torch.library.register_autograd("avgen_amd::rope_apply", _rope_backward, setup_context=_rope_setup)
+
+
+# ---------------------------------------------------------------------------
+# Non-differentiable helpers
+# ---------------------------------------------------------------------------
+
+
+def lse_merge_(out_acc: torch.Tensor, lse_acc: torch.Tensor, out_blk: torch.Tensor, lse_blk: torch.Tensor) -> None:
+    """In-place fp32 online-softmax merge (torch/.../_attention.py:182-183).
+
+    ``out_acc``: fp32 contiguous (..., D); ``lse_acc``: fp32 contiguous (...);
+    ``out_blk``: bf16 or fp32 with out_acc's shape; ``lse_blk``: lse_acc's shape.
+    """
+    name = "avgen_amd.lse_merge_"
+    _require_gpu(name, out_acc, lse_acc, out_blk, lse_blk)
+    if out_acc.dtype is not torch.float32 or lse_acc.dtype is not torch.float32 or lse_blk.dtype is not torch.float32:
+        raise TypeError(f"{name}: accumulators and block LSE must be float32")
+    if out_blk.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{name}: block output must be bfloat16 or float32")
+    if out_blk.shape != out_acc.shape or lse_acc.shape != lse_blk.shape or out_acc.shape[:-1] != lse_acc.shape:
+        raise ValueError(f"{name}: shapes disagree")
+    if not (out_acc.is_contiguous() and lse_acc.is_contiguous()):
+        raise ValueError(f"{name}: accumulators must be contiguous (they are updated in place)")
+    out_blk = out_blk.contiguous()
+    lse_blk = lse_blk.contiguous()
+    D = out_acc.shape[-1]
+    rows = lse_acc.numel()
+    st = _lib.load().avattn_lse_merge(
+        _ptr(out_acc), _ptr(lse_acc), _ptr(out_blk), _ptr(lse_blk), rows, D,
+        1 if out_blk.dtype is torch.bfloat16 else 0, _stream(out_acc.device),
+    )
+    _lib.check(st, name)
+
+
+def rope_tables(
+    coords: torch.Tensor,
+    inv_freq: list[float],
+    axis_of_pair: list[int],
+    pos_mul: tuple[Optional[float], Optional[float], Optional[float]],
+    pos_div: tuple[Optional[float], Optional[float], Optional[float]],
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin tables ``(B, 1, L, pairs)`` from ``coords (B, L, 3)`` on the GPU.
+
+    ``pos_mul[a]`` / ``pos_div[a]`` are ``None`` when that step is skipped for
+    axis ``a`` (src/avgen/models/rope.py:270-277).
+    """
+    name = "avgen_amd.rope_tables"
+    _require_gpu(name, coords)
+    if coords.dtype is not torch.float32:
+        raise TypeError(f"{name}: coords must be float32; got {coords.dtype}")
+    if coords.stride(-1) != 1:
+        coords = coords.contiguous()
+    B, L, _ = coords.shape
+    P = len(inv_freq)
+    cos = torch.empty((B, 1, L, P), device=coords.device, dtype=torch.float32)
+    sin = torch.empty_like(cos)
+    f32 = ctypes.c_float
+    i32 = ctypes.c_int32
+    inv = (f32 * P)(*inv_freq)
+    axes = (i32 * P)(*axis_of_pair)
+    am = (i32 * 3)(*[0 if m is None else 1 for m in pos_mul])
+    pm = (f32 * 3)(*[1.0 if m is None else m for m in pos_mul])
+    ad = (i32 * 3)(*[0 if d is None else 1 for d in pos_div])
+    pd = (f32 * 3)(*[1.0 if d is None else d for d in pos_div])
+    st = _lib.load().avattn_rope_tables(
+        _ptr(coords), coords.stride(0), coords.stride(1), B, L, P,
+        ctypes.cast(inv, ctypes.c_void_p), ctypes.cast(axes, ctypes.c_void_p),
+        ctypes.cast(am, ctypes.c_void_p), ctypes.cast(pm, ctypes.c_void_p),
+        ctypes.cast(ad, ctypes.c_void_p), ctypes.cast(pd, ctypes.c_void_p),
+        _ptr(cos), _ptr(sin), _stream(coords.device),
+    )
+    _lib.check(st, name)
+    return cos, sin

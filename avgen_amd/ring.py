@@ -1,0 +1,246 @@
+"""Ring-attention local step, LSE merge and a one-GPU emulated ring.
+
+The callables here keep the shapes of what PyTorch's context-parallel ring
+calls for each KV chunk, so they drop into that loop
+(torch/distributed/tensor/experimental/_context_parallel/_attention.py):
+
+* :func:`flash_attention_op` — the ``op(q, k, v, is_causal=..., **kwargs)``
+  of :309-478 (aten::_scaled_dot_product_flash_attention's 9-tuple);
+* :func:`flash_attention_backward_op` — the backward ``op(grad_out=...,
+  query=..., key=..., value=..., out=..., logsumexp=..., ...)`` of :567-575;
+* :class:`SDPAMerger` — ``_SDPAMerger`` (:138-223): ``step(out, lse,
+  partial)`` / ``results()``, fp32 accumulation, merge in a HIP kernel.
+
+:func:`ring_attention_forward` / :func:`ring_attention_backward` replay the
+non-causal ring (:422-478 and :514-646) on one GPU by looping over the KV
+chunks in order, with no collectives; :func:`ring_attention` wraps both as a
+differentiable function over contiguous shards
+(src/avgen/parallel/context.py:58-80).
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+from typing import Any, Optional
+
+import torch
+
+from . import ops
+from .context import shard_bounds
+
+__all__ = [
+    "SDPAMerger",
+    "flash_attention_backward_op",
+    "flash_attention_op",
+    "ring_attention",
+    "ring_attention_backward",
+    "ring_attention_forward",
+]
+
+
+def _key_mask(attn_mask: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+    if attn_mask is None:
+        return None
+    if attn_mask.ndim == 4:
+        if attn_mask.shape[1] != 1 or attn_mask.shape[2] != 1:
+            raise NotImplementedError("only key-padding masks (batch, 1, 1, keys) are supported")
+        return attn_mask[:, 0, 0, :]
+    return attn_mask
+
+
+def flash_attention_op(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    dropout_p: float = 0.0,
+    is_causal: bool = False,
+    return_debug_mask: bool = False,
+    *,
+    scale: Optional[float] = None,
+    attn_mask: Optional[torch.Tensor] = None,
+) -> tuple[Any, ...]:
+    """One ring step: attention of the local query shard against one KV chunk.
+
+    Returns aten::_scaled_dot_product_flash_attention's 9-tuple ``(output,
+    logsumexp, cum_seq_q, cum_seq_k, max_q, max_k, rng_state, unused,
+    debug_attn_mask)``; only the first two carry data.  ``logsumexp`` is
+    ``(batch, heads, queries)`` float32, natural log, -inf for rows with no
+    valid key.  ``attn_mask`` (an extension) is a key-padding mask.
+    """
+    if dropout_p != 0.0:
+        raise NotImplementedError("dropout is not supported")
+    if is_causal:
+        raise NotImplementedError("the video DiT ring step is non-causal")
+    if return_debug_mask:
+        raise NotImplementedError("return_debug_mask is not supported")
+    s = ops.default_scale(query.shape[-1]) if scale is None else float(scale)
+    out, lse = ops.flash_fwd(query, key, value, _key_mask(attn_mask), None, None, s)
+    empty = query.new_empty(0)
+    return out, lse, None, None, query.shape[-2], key.shape[-2], empty, empty, empty
+
+
+def flash_attention_backward_op(
+    grad_out: torch.Tensor,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    out: torch.Tensor,
+    logsumexp: torch.Tensor,
+    cum_seq_q: Any = None,
+    cum_seq_k: Any = None,
+    max_q: int = 0,
+    max_k: int = 0,
+    dropout_p: float = 0.0,
+    is_causal: bool = False,
+    philox_seed: Any = None,
+    philox_offset: Any = None,
+    *,
+    scale: Optional[float] = None,
+    attn_mask: Optional[torch.Tensor] = None,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of one ring step given the *merged* ``out``/``logsumexp``
+    (torch/.../_attention.py:567-575).  Returns this chunk's ``(dq, dk, dv)``
+    in the input dtype."""
+    del cum_seq_q, cum_seq_k, max_q, max_k, philox_seed, philox_offset
+    if dropout_p != 0.0 or is_causal:
+        raise NotImplementedError("only non-causal, dropout-free attention is supported")
+    s = ops.default_scale(query.shape[-1]) if scale is None else float(scale)
+    return ops.flash_bwd(grad_out, query, key, value, out, logsumexp, _key_mask(attn_mask), s)
+
+
+class SDPAMerger:
+    """Running merge of per-chunk ``(out, lse)`` (torch/.../_attention.py:138-223).
+
+    ``convert_to_f32`` must be True (the accumulator is fp32, as torch's
+    default ``_cp_options.convert_to_f32``); ``partial`` (round-robin
+    load balancing, causal only) is not supported.
+    """
+
+    def __init__(self, convert_to_f32: bool = True, seq_dim: int = 2) -> None:
+        if not convert_to_f32:
+            raise NotImplementedError("the merge accumulates in float32")
+        if seq_dim != 2:
+            raise NotImplementedError("sequence dim must be 2 for (batch, heads, seq, dim)")
+        self._out: Optional[torch.Tensor] = None
+        self._lse: Optional[torch.Tensor] = None
+        self._out_dtype = torch.float32
+        self._lse_dtype = torch.float32
+
+    def step(self, out: torch.Tensor, lse: torch.Tensor, partial: bool = False) -> None:
+        """Merge one chunk's output (bf16 or fp32) and LSE (fp32)."""
+        if partial:
+            raise NotImplementedError("partial (causal load-balanced) merges are not supported")
+        self._out_dtype = out.dtype
+        self._lse_dtype = lse.dtype
+        if self._out is None:
+            self._out = out.to(torch.float32, memory_format=torch.contiguous_format).clone()
+            self._lse = lse.to(torch.float32).contiguous().clone()
+            return
+        ops.lse_merge_(self._out, self._lse, out, lse.to(torch.float32))
+
+    def results(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(out, lse)`` cast back to the dtypes of the last step."""
+        assert self._out is not None and self._lse is not None
+        return self._out.to(self._out_dtype), self._lse.to(self._lse_dtype)
+
+
+def _chunk_masks(key_masks, n):
+    if key_masks is None:
+        return [None] * n
+    if len(key_masks) != n:
+        raise ValueError(f"{len(key_masks)} key masks for {n} chunks")
+    return list(key_masks)
+
+
+def ring_attention_forward(
+    query: torch.Tensor,
+    keys: Sequence[torch.Tensor],
+    values: Sequence[torch.Tensor],
+    *,
+    key_masks: Optional[Sequence[Optional[torch.Tensor]]] = None,
+    scale: Optional[float] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Non-causal ring forward over KV chunks in ring order
+    (torch/.../_attention.py:422-478): per chunk ``flash_attention_op`` then
+    ``SDPAMerger.step``.  Returns ``(out, lse)``."""
+    if len(keys) != len(values) or not keys:
+        raise ValueError("need the same, non-zero number of key and value chunks")
+    masks = _chunk_masks(key_masks, len(keys))
+    merger = SDPAMerger(True, 2)
+    for k, v, m in zip(keys, values, masks):
+        out, lse, *_ = flash_attention_op(query, k, v, scale=scale, attn_mask=m)
+        merger.step(out, lse, False)
+    return merger.results()
+
+
+def ring_attention_backward(
+    grad_out: torch.Tensor,
+    query: torch.Tensor,
+    keys: Sequence[torch.Tensor],
+    values: Sequence[torch.Tensor],
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    *,
+    key_masks: Optional[Sequence[Optional[torch.Tensor]]] = None,
+    scale: Optional[float] = None,
+) -> tuple[torch.Tensor, list[torch.Tensor], list[torch.Tensor]]:
+    """Non-causal ring backward (torch/.../_attention.py:514-646): each chunk's
+    backward uses the merged ``out``/``lse``; dq accumulates in fp32 and is
+    cast once; each chunk's dk/dv is that chunk's gradient (on a real ring it
+    travels back to the chunk's owner)."""
+    masks = _chunk_masks(key_masks, len(keys))
+    dq_acc = torch.zeros(query.shape, dtype=torch.float32, device=query.device)
+    dks, dvs = [], []
+    for k, v, m in zip(keys, values, masks):
+        dq_i, dk_i, dv_i = flash_attention_backward_op(
+            grad_out, query, k, v, out, lse, scale=scale, attn_mask=m
+        )
+        dq_acc += dq_i
+        dks.append(dk_i)
+        dvs.append(dv_i)
+    return dq_acc.to(query.dtype), dks, dvs
+
+
+class _RingAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, query, key, value, key_mask, cp, scale):
+        L = key.shape[2]
+        bounds = [shard_bounds(L, cp, r) for r in range(cp)]
+        keys = [key[:, :, a:b] for a, b in bounds]
+        values = [value[:, :, a:b] for a, b in bounds]
+        masks = None if key_mask is None else [key_mask[:, a:b] for a, b in bounds]
+        out, lse = ring_attention_forward(query, keys, values, key_masks=masks, scale=scale)
+        ctx.save_for_backward(query, key, value, out, lse, key_mask)
+        ctx.cp = cp
+        ctx.scale = scale
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_out, _grad_lse):
+        query, key, value, out, lse, key_mask = ctx.saved_tensors
+        L = key.shape[2]
+        bounds = [shard_bounds(L, ctx.cp, r) for r in range(ctx.cp)]
+        keys = [key[:, :, a:b] for a, b in bounds]
+        values = [value[:, :, a:b] for a, b in bounds]
+        masks = None if key_mask is None else [key_mask[:, a:b] for a, b in bounds]
+        dq, dks, dvs = ring_attention_backward(
+            grad_out.contiguous(), query, keys, values, out, lse, key_masks=masks, scale=ctx.scale
+        )
+        return dq, torch.cat(dks, dim=2), torch.cat(dvs, dim=2), None, None, None
+
+
+def ring_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    cp: int,
+    key_mask: Optional[torch.Tensor] = None,
+    scale: Optional[float] = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Differentiable emulated ring: ``key``/``value`` (full sequence) are split
+    into ``cp`` contiguous chunks (ragged lengths raise, as
+    src/avgen/parallel/context.py:74-79), the local ``query`` shard attends to
+    each in ring order, and results merge online.  Returns ``(out, lse)``."""
+    return _RingAttention.apply(query, key, value, key_mask, cp, scale)

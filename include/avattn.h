@@ -1,0 +1,184 @@
+/*
+ * avattn.h — C ABI of the MI355X (gfx950) video-DiT attention hot path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * launches on the caller's HIP stream, never allocates and never frees, and
+ * returns an AVATTN_* status code (0 = success).  No call synchronises the
+ * device.  Inputs are read-only.
+ *
+ * Tensor conventions (matching the reference's Python boundary):
+ *   q, k, v, out, dq, dk, dv : bf16, logical shape (batch, heads, seq, head_dim),
+ *                              arbitrary batch/head/seq strides (in elements),
+ *                              head_dim contiguous, 16-byte aligned rows.
+ *   lse                      : float32, contiguous (batch, heads_q, len_q),
+ *                              natural log; -inf for a query whose keys are all
+ *                              masked (its output row is 0).
+ *   key_mask                 : uint8/bool (batch, len_k), nonzero = attend;
+ *                              NULL = every key valid.
+ *   rope cos/sin tables      : float32 (batch, 1, seq, head_dim/2).
+ *
+ * Reference interfaces replaced (paths relative to the avgen source tree,
+ * torch/... = the installed PyTorch):
+ *   avattn_fwd          src/avgen/models/attention.py:227-273 (attention ->
+ *                       F.scaled_dot_product_attention) and the ring local
+ *                       step torch/.../_context_parallel/_attention.py:468-474
+ *                       (aten::_scaled_dot_product_flash_attention -> out, lse)
+ *   avattn_bwd          torch/.../_context_parallel/_attention.py:567-575
+ *                       (aten::_scaled_dot_product_flash_attention_backward)
+ *   avattn_lse_merge    torch/.../_context_parallel/_attention.py:138-223
+ *                       (_SDPAMerger._merge_one, formula :182-183)
+ *   avattn_rope_tables  src/avgen/models/rope.py:218-294 (build_rotary_tables)
+ *   avattn_rope_apply   src/avgen/models/rope.py:297-338 (apply_rotary) and
+ *                       its autograd backward
+ */
+#ifndef AVATTN_H
+#define AVATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque HIP stream handle (hipStream_t); NULL = the default stream. */
+typedef void* avattn_stream_t;
+
+/* Status codes. */
+#define AVATTN_OK                   0
+#define AVATTN_ERR_NULL_POINTER     1  /* a required pointer is NULL               */
+#define AVATTN_ERR_BAD_SHAPE        2  /* negative/zero size where not allowed     */
+#define AVATTN_ERR_HEAD_DIM         3  /* head_dim not supported (64 or 128)       */
+#define AVATTN_ERR_GQA              4  /* heads_q not a multiple of heads_kv       */
+#define AVATTN_ERR_LAYOUT           5  /* misaligned pointer / row stride          */
+#define AVATTN_ERR_WORKSPACE        6  /* workspace missing or too small           */
+#define AVATTN_ERR_LAUNCH           7  /* HIP reported an error at launch          */
+#define AVATTN_ERR_TOO_LARGE        8  /* a size exceeds the 32-bit index range    */
+#define AVATTN_ERR_ARGUMENT         9  /* other invalid argument                   */
+
+/* Human-readable text for a status code (static storage, never NULL). */
+const char* avattn_strerror(int status);
+
+/* ABI version; bumped on any signature change. */
+int avattn_abi_version(void);
+
+/*
+ * Forward: out = softmax(scale * q k^T + mask_bias) v, lse = logsumexp rows.
+ * Replaces attention() (src/avgen/models/attention.py:227-273) and the ring
+ * local step op (torch/.../_context_parallel/_attention.py:468-474).
+ *
+ * q_strides/k_strides/v_strides/out_strides: 3 entries each (batch, head, seq),
+ * in elements.  heads_kv must divide heads_q (grouped-query attention).
+ * key_mask may be NULL; otherwise key_mask[b * key_mask_batch_stride + j].
+ * rope_cos_q/rope_sin_q may be NULL; when given, q is rotated on load with the
+ * interleaved-pair rotation of src/avgen/models/rope.py:332-338 (fp32 math,
+ * bf16 round) before q k^T — table element (b, 0, i, p) at
+ * b * rope_batch_stride + i * (head_dim/2) + p.
+ * A zero len_q or len_k writes zeros to out (and -inf to lse) without a
+ * compute launch (src/avgen/models/attention.py:261-262).
+ */
+int avattn_fwd(const void* q, const void* k, const void* v,
+               const int64_t* q_strides, const int64_t* k_strides,
+               const int64_t* v_strides,
+               int32_t batch, int32_t heads_q, int32_t heads_kv,
+               int32_t len_q, int32_t len_k, int32_t head_dim,
+               const uint8_t* key_mask, int64_t key_mask_batch_stride,
+               const float* rope_cos_q, const float* rope_sin_q,
+               int64_t rope_batch_stride,
+               float scale,
+               void* out, const int64_t* out_strides,
+               float* lse,
+               avattn_stream_t stream);
+
+/*
+ * Workspace bytes avattn_bwd needs for these sizes (per-row softmax
+ * statistics: 2 floats per query row).
+ */
+size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q);
+
+/*
+ * Backward of avattn_fwd with recomputation of the probabilities from
+ * (q, k, lse): given dout, returns dq, dk, dv.  Replaces
+ * aten::_scaled_dot_product_flash_attention_backward as called by the ring
+ * (torch/.../_context_parallel/_attention.py:567-575): out/lse may be the
+ * *merged* output and LSE of all KV chunks, in which case dq/dk/dv are this
+ * chunk's contributions.  dk/dv of a masked key are exactly 0.  With
+ * heads_kv < heads_q, dk/dv sum over the query heads of each group.
+ * workspace must hold avattn_bwd_workspace_size() bytes; it is scratch for
+ * this call only.
+ */
+int avattn_bwd(const void* dout, const void* q, const void* k, const void* v,
+               const void* out, const float* lse,
+               const int64_t* dout_strides, const int64_t* q_strides,
+               const int64_t* k_strides, const int64_t* v_strides,
+               const int64_t* out_strides,
+               int32_t batch, int32_t heads_q, int32_t heads_kv,
+               int32_t len_q, int32_t len_k, int32_t head_dim,
+               const uint8_t* key_mask, int64_t key_mask_batch_stride,
+               float scale,
+               void* dq, const int64_t* dq_strides,
+               void* dk, const int64_t* dk_strides,
+               void* dv, const int64_t* dv_strides,
+               void* workspace, size_t workspace_bytes,
+               avattn_stream_t stream);
+
+/*
+ * Online-softmax merge of one chunk's (out_blk, lse_blk) into the running
+ * (out_acc, lse_acc), in place, in fp32:
+ *   out_acc <- out_acc - sigmoid(lse_blk - lse_acc) * (out_acc - out_blk)
+ *   lse_acc <- lse_acc - logsigmoid(lse_acc - lse_blk)
+ * (torch/.../_context_parallel/_attention.py:182-183).  Rows are
+ * (batch*heads*len_q) contiguous rows of head_dim.  out_blk is bf16 when
+ * blk_is_bf16 != 0, else fp32.  -inf LSEs (fully masked rows) merge as the
+ * identity element: a -inf block leaves the accumulator unchanged and a -inf
+ * accumulator takes the block (torch's formula returns NaN there).
+ */
+int avattn_lse_merge(float* out_acc, float* lse_acc,
+                     const void* out_blk, const float* lse_blk,
+                     int64_t n_rows, int32_t head_dim, int32_t blk_is_bf16,
+                     avattn_stream_t stream);
+
+/*
+ * Rotary tables from physical coordinates (src/avgen/models/rope.py:218-294).
+ * coords: float32, element (b, i, a) at b*coords_batch_stride +
+ * i*coords_row_stride + a.  inv_freq[p] and axis_of_pair[p] (0=time,
+ * 1=height, 2=width) give each pair's inverse frequency and axis; for each
+ * axis a, the position is coords[..., a], then multiplied by pos_mul[a] if
+ * apply_mul[a] != 0, then divided by pos_div[a] if apply_div[a] != 0 (the
+ * time_scale and linear-scaling steps of rope.py:270-277, in that order).
+ * inv_freq, axis_of_pair, apply_mul, pos_mul, apply_div and pos_div are HOST
+ * pointers (pairs <= 64 entries, or 3 per-axis entries); their values are
+ * copied into the launch.  coords, cos_out and sin_out are device pointers.
+ * Writes contiguous cos/sin of shape (batch, 1, len, pairs).
+ */
+int avattn_rope_tables(const float* coords, int64_t coords_batch_stride,
+                       int64_t coords_row_stride,
+                       int32_t batch, int32_t len, int32_t pairs,
+                       const float* inv_freq, const int32_t* axis_of_pair,
+                       const int32_t* apply_mul, const float* pos_mul,
+                       const int32_t* apply_div, const float* pos_div,
+                       float* cos_out, float* sin_out,
+                       avattn_stream_t stream);
+
+/*
+ * Interleaved-pair rotation of x (src/avgen/models/rope.py:297-338), fp32
+ * math with each product rounded separately, result rounded to bf16.
+ * inverse == 0: forward rotation (e*c - o*s, e*s + o*c).
+ * inverse != 0: the transpose (e*c + o*s, o*c - e*s), i.e. the gradient of the
+ * forward rotation as torch autograd evaluates it.
+ * x/out strides: 3 entries (batch, head, seq), head_dim contiguous.  The
+ * tables are indexed (b, 0, i, p) at b*table_batch_stride + i*pairs + p.
+ */
+int avattn_rope_apply(const void* x, const int64_t* x_strides,
+                      int32_t batch, int32_t heads, int32_t len,
+                      int32_t head_dim,
+                      const float* cos_tab, const float* sin_tab,
+                      int64_t table_batch_stride, int32_t inverse,
+                      void* out, const int64_t* out_strides,
+                      avattn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AVATTN_H */

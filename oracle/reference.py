@@ -1,0 +1,354 @@
+"""numpy restatement of the reference's attention hot path (test oracle only).
+
+Conventions: tensors are numpy arrays shaped like the reference's torch
+tensors; ``q, k, v`` are ``(B, H, L, D)``; LSE is ``(B, H, Lq)`` natural log.
+bf16 values are carried as float32 arrays holding exactly-representable
+bf16 numbers (see :func:`bf16_round`).
+"""
+
+from __future__ import annotations
+
+import math
+from collections.abc import Sequence
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# bf16 helpers
+# ---------------------------------------------------------------------------
+
+
+def bf16_round(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest bf16 (ties to even), returned as float32.
+
+    Same rounding as torch's float32 -> bfloat16 cast (round-to-nearest-even);
+    NaN stays NaN.
+    """
+    f = np.asarray(x, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    r = np.where(np.isnan(f), np.uint32(0x7FC0), r)
+    return (r.astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """uint16 bit patterns of float32 values that are exactly bf16."""
+    return (np.asarray(x, dtype=np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# 3D RoPE  (src/avgen/models/rope.py)
+# ---------------------------------------------------------------------------
+
+
+def rope_axis_pairs(head_dim: int) -> tuple[int, int, int]:
+    """src/avgen/models/rope.py:128-157 — time takes the remainder."""
+    if head_dim < 6 or head_dim % 2 != 0:
+        raise ValueError(f"head_dim must be an even integer of at least 6; got {head_dim!r}")
+    pairs = head_dim // 2
+    spatial = pairs // 3
+    return (pairs - 2 * spatial, spatial, spatial)
+
+
+def axis_plan(
+    head_dim: int, theta: float, scaling: tuple[str, float, float] = ("none", 1.0, 1.0)
+) -> list[tuple[int, float, float | None]]:
+    """Per axis ``(pairs, axis_theta, linear_factor_or_None)``
+    (src/avgen/models/rope.py:259-285).  ``scaling`` = (mode, time, spatial)."""
+    mode, tf, sf = scaling
+    plan = []
+    for axis, (pairs, factor) in enumerate(zip(rope_axis_pairs(head_dim), (tf, sf, sf))):
+        axis_theta = theta
+        div = None
+        if mode == "linear" and factor != 1.0:
+            div = factor
+        elif mode == "ntk" and factor != 1.0:
+            dim = 2 * pairs
+            if dim > 2:
+                axis_theta = theta * factor ** (dim / (dim - 2))
+        plan.append((pairs, axis_theta, div))
+    return plan
+
+
+def rotary_tables_f64(
+    coords: np.ndarray,
+    head_dim: int,
+    theta: float = 10000.0,
+    time_scale: float = 1.0,
+    scaling: tuple[str, float, float] = ("none", 1.0, 1.0),
+) -> tuple[np.ndarray, np.ndarray]:
+    """Exact (float64) cos/sin tables ``(B, 1, L, pairs)``
+    (src/avgen/models/rope.py:264-294): per axis ``angle = pos * theta_a^(-k/pairs_a)``
+    with ``pos`` multiplied by time_scale on axis 0 and divided by the linear
+    factor; axes concatenated t | h | w."""
+    coords = np.asarray(coords, dtype=np.float64)
+    angles = []
+    for axis, (pairs, axis_theta, div) in enumerate(axis_plan(head_dim, theta, scaling)):
+        pos = coords[..., axis]
+        if axis == 0 and time_scale != 1.0:
+            pos = pos * time_scale
+        if div is not None:
+            pos = pos / div
+        inv = axis_theta ** (-(np.arange(pairs, dtype=np.float64) / pairs))
+        angles.append(pos[..., None] * inv)
+    phase = np.concatenate(angles, axis=-1)[:, None]
+    return np.cos(phase), np.sin(phase)
+
+
+def apply_rotary_bf16(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, inverse: bool = False) -> np.ndarray:
+    """Interleaved-pair rotation exactly as src/avgen/models/rope.py:332-338
+    evaluates it: float32 math, ``even*cos - odd*sin`` and ``even*sin +
+    odd*cos`` with every product and sum rounded to float32 separately, then
+    one round to bf16.  ``inverse`` gives the transpose ``(e*c + o*s, o*c -
+    e*s)``, which is what torch autograd computes for the gradient of the
+    forward rotation (each product rounded, then one add).
+
+    x: ``(B, H, L, D)`` float32 holding bf16 values; tables float32 ``(B|1, 1, L, D/2)``.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    c = np.asarray(cos, dtype=np.float32)
+    s = np.asarray(sin, dtype=np.float32)
+    e = x[..., 0::2]
+    o = x[..., 1::2]
+    with np.errstate(over="ignore", invalid="ignore"):
+        if not inverse:
+            a = (e * c).astype(np.float32) - (o * s).astype(np.float32)
+            b = (e * s).astype(np.float32) + (o * c).astype(np.float32)
+        else:
+            a = (e * c).astype(np.float32) + (o * s).astype(np.float32)
+            b = (o * c).astype(np.float32) - (e * s).astype(np.float32)
+    out = np.empty_like(x)
+    out[..., 0::2] = a
+    out[..., 1::2] = b
+    return bf16_round(out)
+
+
+def video_coords(frames: int, height: int, width: int, fps: float = 8.0,
+                 patch: tuple[int, int] = (2, 2), batch: int = 1) -> np.ndarray:
+    """``(B, F*H*W, 3)`` float32 ``(seconds, row*patch_h, col*patch_w)``, token
+    order time -> row -> column (src/avgen/core/patchify.py:45-105 with
+    temporal patch 1; 8 fps is the synthetic default, src/avgen/data/
+    synthetic.py:160-161)."""
+    t = (np.arange(frames, dtype=np.float32) / np.float32(fps)).astype(np.float32)
+    r = np.arange(height, dtype=np.float32) * np.float32(patch[0])
+    c = np.arange(width, dtype=np.float32) * np.float32(patch[1])
+    tg, rg, cg = np.meshgrid(t, r, c, indexing="ij")
+    xyz = np.stack([tg.reshape(-1), rg.reshape(-1), cg.reshape(-1)], axis=-1).astype(np.float32)
+    return np.broadcast_to(xyz, (batch,) + xyz.shape).copy()
+
+
+# ---------------------------------------------------------------------------
+# Attention with key-padding mask and LSE  (src/avgen/models/attention.py)
+# ---------------------------------------------------------------------------
+
+
+def key_padding_mask(mask: np.ndarray | None, assume_dense: bool = False) -> np.ndarray | None:
+    """src/avgen/models/attention.py:183-224: None when absent, assumed dense
+    or all valid; else ``mask[:, None, None, :]``."""
+    if mask is None or assume_dense:
+        return None
+    mask = np.asarray(mask)
+    if mask.ndim != 2:
+        raise ValueError("key mask must have rank 2 (batch, keys)")
+    if mask.dtype != np.bool_:
+        raise TypeError("key mask must be bool")
+    if mask.size == 0 or bool(mask.all()):
+        return None
+    return mask[:, None, None, :]
+
+
+def _expand_kv(k: np.ndarray, hq: int) -> np.ndarray:
+    hk = k.shape[1]
+    return np.repeat(k, hq // hk, axis=1) if hk != hq else k
+
+
+def attention_f64(
+    q: np.ndarray, k: np.ndarray, v: np.ndarray, key_mask: np.ndarray | None = None,
+    scale: float | None = None,
+) -> tuple[np.ndarray, np.ndarray]:
+    """Softmax attention in float64 (the math of F.scaled_dot_product_attention
+    called at src/avgen/models/attention.py:265-273, default scale 1/sqrt(D)).
+
+    key_mask: ``(B|1, Lk)`` bool, True = attend.  Returns ``(out, lse)``:
+    ``out (B, H, Lq, D)``, ``lse (B, H, Lq)`` natural log.  A row with no
+    valid key gives out = 0 (what F.scaled_dot_product_attention returns) and
+    lse = -inf.  Zero-length keys give zeros (src/avgen/models/attention.py
+    :261-262).
+    """
+    q = np.asarray(q, np.float64)
+    k = _expand_kv(np.asarray(k, np.float64), q.shape[1])
+    v = _expand_kv(np.asarray(v, np.float64), q.shape[1])
+    B, H, Lq, D = q.shape
+    if Lq == 0 or k.shape[2] == 0:
+        return np.zeros_like(q), np.full((B, H, Lq), -np.inf)
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    s = np.einsum("bhqd,bhkd->bhqk", q, k) * scale
+    if key_mask is not None:
+        m = np.asarray(key_mask, bool)[:, None, None, :]
+        s = np.where(m, s, -np.inf)
+    mx = s.max(axis=-1, keepdims=True)
+    safe = np.where(np.isfinite(mx), mx, 0.0)
+    p = np.exp(s - safe)
+    l = p.sum(axis=-1, keepdims=True)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        out = np.where(l > 0, np.einsum("bhqk,bhkd->bhqd", p, v) / np.where(l > 0, l, 1.0), 0.0)
+        lse = np.where(l[..., 0] > 0, np.log(np.where(l[..., 0] > 0, l[..., 0], 1.0)) + safe[..., 0], -np.inf)
+    return out, lse
+
+
+def attention_bwd_f64(
+    dout: np.ndarray, q: np.ndarray, k: np.ndarray, v: np.ndarray, out: np.ndarray, lse: np.ndarray,
+    key_mask: np.ndarray | None = None, scale: float | None = None,
+) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Flash-attention backward in float64 given (possibly merged) ``out``/``lse``
+    (what the ring backward hands the op, torch/.../_attention.py:567-575):
+    ``P = exp(s*QK^T - lse)``, ``dV = P^T dO``, ``dP = dO V^T``,
+    ``Dr = rowsum(dO * O)``, ``dS = P * (dP - Dr)``, ``dQ = s dS K``,
+    ``dK = s dS^T Q``.  With grouped KV heads, dK/dV sum over each group."""
+    q = np.asarray(q, np.float64)
+    hq, hk = q.shape[1], np.asarray(k).shape[1]
+    kk = _expand_kv(np.asarray(k, np.float64), hq)
+    vv = _expand_kv(np.asarray(v, np.float64), hq)
+    do = np.asarray(dout, np.float64)
+    o = np.asarray(out, np.float64)
+    lse = np.asarray(lse, np.float64)
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    s = np.einsum("bhqd,bhkd->bhqk", q, kk) * scale
+    lse_b = np.where(np.isfinite(lse), lse, np.inf)[..., None]
+    p = np.exp(s - lse_b)
+    if key_mask is not None:
+        p = np.where(np.asarray(key_mask, bool)[:, None, None, :], p, 0.0)
+    dv = np.einsum("bhqk,bhqd->bhkd", p, do)
+    dp = np.einsum("bhqd,bhkd->bhqk", do, vv)
+    dr = (do * o).sum(-1, keepdims=True)
+    ds = p * (dp - dr)
+    dq = np.einsum("bhqk,bhkd->bhqd", ds, kk) * scale
+    dk = np.einsum("bhqk,bhqd->bhkd", ds, q) * scale
+    if hk != hq:
+        g = hq // hk
+        dk = dk.reshape(dk.shape[0], hk, g, *dk.shape[2:]).sum(2)
+        dv = dv.reshape(dv.shape[0], hk, g, *dv.shape[2:]).sum(2)
+    return dq, dk, dv
+
+
+# ---------------------------------------------------------------------------
+# Ring merge and ring loops  (torch/.../_context_parallel/_attention.py)
+# ---------------------------------------------------------------------------
+
+
+def _sigmoid_f32(x: np.ndarray) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        return (np.float32(1) / (np.float32(1) + np.exp(-x))).astype(np.float32)
+
+
+def _logsigmoid_f32(x: np.ndarray) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        return (np.minimum(x, np.float32(0)) - np.log1p(np.exp(-np.abs(x)))).astype(np.float32)
+
+
+def lse_merge_f32(out: np.ndarray, lse: np.ndarray, out_b: np.ndarray, lse_b: np.ndarray):
+    """One ``_SDPAMerger._merge_one`` step (torch/.../_attention.py:182-183) in
+    float32: ``out - sigmoid(lse_b - lse) * (out - out_b)`` and ``lse -
+    logsigmoid(lse - lse_b)``.  A -inf LSE is the identity element (a block of
+    fully masked rows changes nothing; an empty accumulator takes the block),
+    where torch's formula would give NaN.  lse shapes are ``(..., )`` without
+    the trailing singleton."""
+    out = np.asarray(out, np.float32)
+    out_b = np.asarray(out_b, np.float32)
+    lse = np.asarray(lse, np.float32)
+    lse_b = np.asarray(lse_b, np.float32)
+    with np.errstate(invalid="ignore"):
+        w = _sigmoid_f32((lse_b - lse).astype(np.float32))[..., None]
+        merged = (out - (w * (out - out_b)).astype(np.float32)).astype(np.float32)
+        mlse = (lse - _logsigmoid_f32((lse - lse_b).astype(np.float32))).astype(np.float32)
+    b_empty = np.isneginf(lse_b)
+    a_empty = np.isneginf(lse) & ~b_empty
+    merged = np.where(b_empty[..., None], out, np.where(a_empty[..., None], out_b, merged))
+    mlse = np.where(b_empty, lse, np.where(a_empty, lse_b, mlse))
+    return merged.astype(np.float32), mlse.astype(np.float32)
+
+
+def lse_merge_f64(out: np.ndarray, lse: np.ndarray, out_b: np.ndarray, lse_b: np.ndarray):
+    """Exact (float64) combination of two partial softmax results: weights
+    ``exp(lse - L)`` and ``exp(lse_b - L)`` with ``L = logaddexp(lse, lse_b)``."""
+    lse = np.asarray(lse, np.float64)
+    lse_b = np.asarray(lse_b, np.float64)
+    L = np.logaddexp(lse, lse_b)
+    with np.errstate(invalid="ignore"):
+        wa = np.where(np.isneginf(lse), 0.0, np.exp(lse - np.where(np.isneginf(L), 0.0, L)))
+        wb = np.where(np.isneginf(lse_b), 0.0, np.exp(lse_b - np.where(np.isneginf(L), 0.0, L)))
+    return wa[..., None] * np.asarray(out, np.float64) + wb[..., None] * np.asarray(out_b, np.float64), L
+
+
+def ring_forward_f64(q, keys: Sequence, values: Sequence, masks: Sequence | None = None, scale=None):
+    """Non-causal ring forward (torch/.../_attention.py:422-478): per chunk
+    attention, then merge in ring order.  Float64 throughout."""
+    masks = masks if masks is not None else [None] * len(keys)
+    out, lse = attention_f64(q, keys[0], values[0], masks[0], scale)
+    for k, v, m in zip(keys[1:], values[1:], masks[1:]):
+        ob, lb = attention_f64(q, k, v, m, scale)
+        out, lse = lse_merge_f64(out, lse, ob, lb)
+    return out, lse
+
+
+def ring_backward_f64(dout, q, keys, values, out, lse, masks=None, scale=None):
+    """Non-causal ring backward (torch/.../_attention.py:514-646): each
+    chunk's backward with the merged out/lse; dq summed over chunks."""
+    masks = masks if masks is not None else [None] * len(keys)
+    dq = np.zeros(np.shape(q))
+    dks, dvs = [], []
+    for k, v, m in zip(keys, values, masks):
+        a, b, c = attention_bwd_f64(dout, q, k, v, out, lse, m, scale)
+        dq = dq + a
+        dks.append(b)
+        dvs.append(c)
+    return dq, dks, dvs
+
+
+# ---------------------------------------------------------------------------
+# Context-parallel shard rules  (src/avgen/parallel/context.py)
+# ---------------------------------------------------------------------------
+
+
+def sharded_length(total: int, shards: int) -> int:
+    """src/avgen/parallel/context.py:58-80."""
+    if total % shards != 0:
+        raise ValueError(f"sequence length {total} is not divisible by context-parallel degree {shards}")
+    return total // shards
+
+
+def shard_bounds(total: int, shards: int, index: int) -> tuple[int, int]:
+    """src/avgen/parallel/context.py:159-163."""
+    local = sharded_length(total, shards)
+    return index * local, (index + 1) * local
+
+
+def pad_to_multiple(tokens: np.ndarray, coords: np.ndarray, mask: np.ndarray, multiple: int):
+    """src/avgen/parallel/context.py:83-139: zero tokens/coords, False mask."""
+    if multiple < 1:
+        raise ValueError("multiple must be positive")
+    L = tokens.shape[1]
+    pad = (-L) % multiple
+    if pad == 0:
+        return tokens, coords, mask
+
+    def _pad(t):
+        shape = list(t.shape)
+        shape[1] = pad
+        return np.concatenate([t, np.zeros(shape, dtype=t.dtype)], axis=1)
+
+    return _pad(tokens), _pad(coords), _pad(mask)
+
+
+# ---------------------------------------------------------------------------
+# FLOP convention  (src/avgen/simulate/compute.py:126,142)
+# ---------------------------------------------------------------------------
+
+
+def attention_flops(batch: int, heads: int, len_q: int, len_k: int, head_dim: int, backward: bool = True) -> float:
+    """Algorithmic attention FLOPs: ``2*2*Lq*Lk*D`` per (batch, head) forward
+    (scores + value-weighted sum, src/avgen/simulate/compute.py:126), times 3
+    with the backward (:142).  The backward's recompute of QK^T is not counted."""
+    fwd = 4.0 * batch * heads * len_q * len_k * head_dim
+    return fwd * (3.0 if backward else 1.0)

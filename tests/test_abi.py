@@ -1,0 +1,133 @@
+"""The C-ABI library: loads without a GPU, exports every symbol declared in
+include/avattn.h, and rejects bad arguments before touching the device.
+
+None of these calls launches a kernel: every case returns from argument
+validation, which runs before any HIP API call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from avgen_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "avattn.h"
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(avattn_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built; run `python -m avgen_amd.build`")
+    return _lib.load()
+
+
+def _no_device() -> bool:
+    import torch
+
+    return not torch.cuda.is_available()
+
+
+# The validation cases pass fake device addresses.  They are meant to return
+# from argument checking, but if a check regressed the call would launch a
+# kernel on garbage pointers, so they only run where no GPU is visible.
+cpu_only = pytest.mark.skipif(not _no_device(), reason="fake-pointer validation tests run only without a GPU")
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    names = _declared_functions()
+    assert names == sorted(_lib.SIGNATURES), "ctypes signature table out of sync with include/avattn.h"
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_strerror_and_version(lib):
+    assert lib.avattn_abi_version() == 1
+    for code in range(0, 10):
+        assert lib.avattn_strerror(code)
+    assert b"unknown" in lib.avattn_strerror(12345)
+
+
+def test_workspace_size(lib):
+    assert lib.avattn_bwd_workspace_size(2, 40, 18900) == 2 * 2 * 40 * 18900 * 4
+    assert lib.avattn_bwd_workspace_size(0, 40, 10) == 0
+
+
+def _fwd(lib, **over):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+    args = dict(q=16, k=16, v=16, qs=s, ks=s, vs=s, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
+                cos=None, sin=None, rsb=0, scale=0.125, out=16, os=s, lse=16, stream=None)
+    args.update(over)
+    return lib.avattn_fwd(args["q"], args["k"], args["v"], args["qs"], args["ks"], args["vs"], args["B"],
+                          args["Hq"], args["Hkv"], args["Lq"], args["Lk"], args["D"], args["mask"], args["msb"],
+                          args["cos"], args["sin"], args["rsb"], args["scale"], args["out"], args["os"],
+                          args["lse"], args["stream"])
+
+
+@cpu_only
+def test_fwd_validation_paths(lib):
+    # Fake (never dereferenced) but aligned addresses; each case fails validation.
+    assert _fwd(lib, D=96) == _lib.ERR_HEAD_DIM
+    assert _fwd(lib, Hq=3, Hkv=2) == _lib.ERR_GQA
+    assert _fwd(lib, Lq=-1) == _lib.ERR_BAD_SHAPE
+    assert _fwd(lib, scale=0.0) == _lib.ERR_ARGUMENT
+    assert _fwd(lib, scale=float("nan")) == _lib.ERR_ARGUMENT
+    assert _fwd(lib, cos=16) == _lib.ERR_ARGUMENT
+    assert _fwd(lib, q=None) == _lib.ERR_NULL_POINTER
+    assert _fwd(lib, qs=None) == _lib.ERR_NULL_POINTER
+    assert _fwd(lib, q=8) == _lib.ERR_LAYOUT
+    assert _fwd(lib, qs=_lib.i64_array([1024 * 128, 1024 * 128, 100])) == _lib.ERR_LAYOUT
+    assert _fwd(lib, k=None) == _lib.ERR_NULL_POINTER
+    assert _fwd(lib, mask=16, msb=2) == _lib.ERR_ARGUMENT
+    assert _fwd(lib, B=1, Hq=1 << 30, Hkv=1, Lq=1 << 20) == _lib.ERR_TOO_LARGE
+    # empty problems succeed without any launch
+    assert _fwd(lib, Lq=0) == _lib.OK
+    assert _fwd(lib, B=0) == _lib.OK
+
+
+@cpu_only
+def test_bwd_validation_paths(lib):
+    s = _lib.i64_array([1 << 17, 1 << 17, 128])
+    base = [16, 16, 16, 16, 16, 16, s, s, s, s, s, 1, 2, 2, 4, 4, 128, None, 0, 0.125,
+            16, s, 16, s, 16, s, 16, 8, None]
+    assert lib.avattn_bwd(*base) == _lib.ERR_WORKSPACE  # 8 bytes < 2*1*2*4*4
+    bad = list(base)
+    bad[16] = 80
+    assert lib.avattn_bwd(*bad) == _lib.ERR_HEAD_DIM
+    bad = list(base)
+    bad[20] = None
+    assert lib.avattn_bwd(*bad) == _lib.ERR_NULL_POINTER
+    bad = list(base)
+    bad[0] = 24
+    bad[27] = 1 << 20
+    assert lib.avattn_bwd(*bad) == _lib.ERR_LAYOUT
+
+
+@cpu_only
+def test_merge_and_rope_validation_paths(lib):
+    assert lib.avattn_lse_merge(16, 16, 16, 16, 10, 96, 1, None) == _lib.ERR_HEAD_DIM
+    assert lib.avattn_lse_merge(None, 16, 16, 16, 10, 128, 1, None) == _lib.ERR_NULL_POINTER
+    assert lib.avattn_lse_merge(8, 16, 16, 16, 10, 128, 1, None) == _lib.ERR_LAYOUT
+    assert lib.avattn_lse_merge(16, 16, 16, 16, 0, 128, 1, None) == _lib.OK
+    s = _lib.i64_array([1 << 16, 1 << 14, 128])
+    assert lib.avattn_rope_apply(16, s, 1, 1, 4, 100, 16, 16, 0, 0, 16, s, None) == _lib.ERR_HEAD_DIM
+    assert lib.avattn_rope_apply(None, s, 1, 1, 4, 128, 16, 16, 0, 0, 16, s, None) == _lib.ERR_NULL_POINTER
+    assert lib.avattn_rope_apply(16, s, 1, 1, 4, 128, 16, 16, 2, 0, 16, s, None) == _lib.ERR_LAYOUT
+    f = (ctypes.c_float * 64)()
+    ax = (ctypes.c_int32 * 64)(*([3] * 64))
+    z = (ctypes.c_int32 * 3)()
+    f3 = (ctypes.c_float * 3)()
+    cast = lambda a: ctypes.cast(a, ctypes.c_void_p)  # noqa: E731
+    assert lib.avattn_rope_tables(16, 3, 3, 1, 4, 64, cast(f), cast(ax), cast(z), cast(f3), cast(z), cast(f3),
+                                  16, 16, None) == _lib.ERR_ARGUMENT
+    assert lib.avattn_rope_tables(16, 3, 3, 1, 4, 2, cast(f), cast(ax), cast(z), cast(f3), cast(z), cast(f3),
+                                  16, 16, None) == _lib.ERR_HEAD_DIM

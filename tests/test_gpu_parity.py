@@ -1,0 +1,353 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Tolerances: output max-abs <= 2e-2 and LSE <= 1e-3 for
+bf16 inputs against a float64 evaluation of the same bf16 values; masks and
+padding bit-exact (masked keys contribute exactly nothing: identical output
+bits when masked K/V change, exactly zero dK/dV).  The RoPE rotation is
+bit-exact against the reference's float32 chain.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as R
+from oracle import torch_path as T
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 2e-2
+LSE_TOL = 1e-3
+# Gradients: max-abs error relative to the largest reference magnitude.
+GRAD_REL_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def amd():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    import avgen_amd
+
+    avgen_amd.ops  # noqa: B018 — loads the library lazily on first call
+    return avgen_amd
+
+
+def _gen(seed):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return g
+
+
+def _randn(shape, seed, scale=1.0):
+    return (torch.randn(shape, generator=_gen(seed)) * scale).to(torch.bfloat16)
+
+
+def _f64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _key_mask(B, Lk, seed, full_rows=(), empty_rows=()):
+    g = _gen(seed)
+    lengths = torch.randint(1, Lk + 1, (B,), generator=g)
+    m = torch.arange(Lk)[None, :] < lengths[:, None]
+    for b in full_rows:
+        m[b] = True
+    for b in empty_rows:
+        m[b] = False
+    return m
+
+
+FWD_CASES = [
+    # B, Hq, Hkv, Lq, Lk, D
+    (1, 2, 2, 128, 128, 128),
+    (2, 3, 3, 200, 333, 128),
+    (1, 4, 4, 1024, 1024, 64),
+    (1, 4, 2, 130, 257, 128),
+    (2, 2, 1, 65, 64, 64),
+    (1, 1, 1, 1, 1, 128),
+    (1, 2, 2, 300, 5, 128),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D", FWD_CASES)
+@pytest.mark.parametrize("masked", [False, True])
+def test_forward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
+    q = _randn((B, Hq, Lq, D), 0)
+    k = _randn((B, Hkv, Lk, D), 1)
+    v = _randn((B, Hkv, Lk, D), 2)
+    mask = _key_mask(B, Lk, 4, empty_rows=(0,) if (masked and B > 1) else ()) if masked else None
+    print(f"fwd case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked}", flush=True)
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), None if mask is None else mask.cuda(), None, None,
+                                 D ** -0.5)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), None if mask is None else mask.numpy())
+    o = _f64(out)
+    l = lse.cpu().numpy().astype(np.float64)
+    assert np.isfinite(o).all()
+    assert np.abs(o - ro).max() <= OUT_TOL
+    fin = np.isfinite(rl)
+    assert np.array_equal(np.isneginf(l), ~fin)
+    assert np.abs(l[fin] - rl[fin]).max(initial=0.0) <= LSE_TOL
+    if masked and B > 1:
+        assert np.all(o[0] == 0)
+
+
+def test_attention_dropin_matches_torch_restatement(amd):
+    q, k, v = _randn((1, 4, 256, 128), 10), _randn((1, 4, 384, 128), 11), _randn((1, 4, 384, 128), 12)
+    out = amd.attention.attention(q.cuda(), k.cuda(), v.cuda())
+    ref = T.sdpa(q.float(), k.float(), v.float()).numpy()
+    assert np.abs(_f64(out) - ref).max() <= OUT_TOL
+    # key-padding mask path with key_padding_mask's (B,1,1,Lk) form
+    m = _key_mask(1, 384, 3)
+    km = amd.attention.key_padding_mask(m.cuda())
+    out_m = amd.attention.attention(q.cuda(), k.cuda(), v.cuda(), attn_mask=km)
+    ref_m = T.sdpa(q.float(), k.float(), v.float(), m).numpy()
+    assert np.abs(_f64(out_m) - ref_m).max() <= OUT_TOL
+
+
+def test_strided_blhd_inputs(amd):
+    # (B, L, H, D) storage viewed as (B, H, L, D), as SelfAttention._heads does
+    # (src/avgen/models/layers.py:496-504).
+    base = _randn((2, 200, 3, 128), 20).cuda()
+    kb = _randn((2, 150, 3, 128), 21).cuda()
+    vb = _randn((2, 150, 3, 128), 22).cuda()
+    q, k, v = base.transpose(1, 2), kb.transpose(1, 2), vb.transpose(1, 2)
+    out, lse = amd.ops.flash_fwd(q, k, v, None, None, None, 128 ** -0.5)
+    out_c, lse_c = amd.ops.flash_fwd(q.contiguous(), k.contiguous(), v.contiguous(), None, None, None, 128 ** -0.5)
+    assert torch.equal(out.contiguous(), out_c) and torch.equal(lse, lse_c)
+
+
+def test_zero_length_sequences(amd):
+    q = _randn((1, 2, 16, 128), 1).cuda()
+    k = _randn((1, 2, 0, 128), 2).cuda()
+    out = amd.attention.attention(q, k, k)
+    assert out.shape == q.shape and torch.all(out == 0)
+    out2, lse2 = amd.ops.flash_fwd(q, k, k, None, None, None, 0.1)
+    assert torch.all(out2 == 0) and torch.all(torch.isneginf(lse2))
+    q0 = _randn((1, 2, 0, 128), 3).cuda()
+    assert amd.attention.attention(q0, q, q).shape == q0.shape
+
+
+def test_masked_keys_are_bit_exact(amd):
+    B, H, Lq, Lk, D = 2, 2, 96, 200, 128
+    q, k, v = _randn((B, H, Lq, D), 30), _randn((B, H, Lk, D), 31), _randn((B, H, Lk, D), 32)
+    m = _key_mask(B, Lk, 5)
+    m[1, 150:] = False
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), m.cuda(), None, None, D ** -0.5)
+    k2, v2 = k.clone(), v.clone()
+    garbage = _randn((B, H, Lk, D), 33, scale=50.0)
+    sel = (~m)[:, None, :, None].expand_as(k2)
+    k2[sel] = garbage[sel]
+    v2[sel] = garbage[sel]
+    out2, lse2 = amd.ops.flash_fwd(q.cuda(), k2.cuda(), v2.cuda(), m.cuda(), None, None, D ** -0.5)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    do = _randn((B, H, Lq, D), 34).cuda()
+    dq, dk, dv = amd.ops.flash_bwd(do, q.cuda(), k.cuda(), v.cuda(), out, lse, m.cuda(), D ** -0.5)
+    dq2, dk2, dv2 = amd.ops.flash_bwd(do, q.cuda(), k2.cuda(), v2.cuda(), out2, lse2, m.cuda(), D ** -0.5)
+    msk = (~m.cuda())[:, None, :, None].expand_as(dk)
+    assert torch.all(dk[msk] == 0) and torch.all(dv[msk] == 0)
+    assert torch.equal(dq, dq2) and torch.equal(dk[~msk], dk2[~msk]) and torch.equal(dv[~msk], dv2[~msk])
+
+
+BWD_CASES = [
+    (1, 2, 2, 128, 128, 128, False),
+    (2, 3, 3, 200, 333, 128, True),
+    (1, 4, 2, 130, 257, 128, False),
+    (1, 4, 4, 512, 512, 64, False),
+    (2, 2, 1, 65, 97, 64, True),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,masked", BWD_CASES)
+def test_backward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
+    q, k, v = _randn((B, Hq, Lq, D), 40), _randn((B, Hkv, Lk, D), 41), _randn((B, Hkv, Lk, D), 42)
+    do = _randn((B, Hq, Lq, D), 43)
+    m = _key_mask(B, Lk, 6, empty_rows=(1,) if B > 1 else ()) if masked else None
+    print(f"bwd case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked}", flush=True)
+    mc = None if m is None else m.cuda()
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), mc, None, None, D ** -0.5)
+    dq, dk, dv = amd.ops.flash_bwd(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, mc, D ** -0.5)
+    mn = None if m is None else m.numpy()
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), mn)
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, mn)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        g = _f64(got)
+        assert np.isfinite(g).all(), name
+        err = np.abs(g - ref).max()
+        scale = max(np.abs(ref).max(), 1e-3)
+        print(f"  {name}: max err {err:.3e} (ref max {scale:.3e})", flush=True)
+        assert err <= GRAD_REL_TOL * scale, name
+
+
+def test_autograd_through_dropin(amd):
+    q = _randn((1, 2, 96, 128), 50).cuda().requires_grad_(True)
+    k = _randn((1, 2, 80, 128), 51).cuda().requires_grad_(True)
+    v = _randn((1, 2, 80, 128), 52).cuda().requires_grad_(True)
+    do = _randn((1, 2, 96, 128), 53).cuda()
+    amd.attention.attention(q, k, v).backward(do)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v))
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl)
+    for got, ref in ((q.grad, rq), (k.grad, rk), (v.grad, rv)):
+        assert np.abs(_f64(got) - ref).max() <= GRAD_REL_TOL * np.abs(ref).max()
+
+
+# ---------------------------------------------------------------------------
+# RoPE
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_rope_tables_match_oracle(amd, head_dim):
+    coords = torch.from_numpy(R.video_coords(4, 6, 8, batch=2))
+    tabs = amd.rope.build_rotary_tables(coords.cuda(), head_dim=head_dim, time_scale=1.5,
+                                        scaling=amd.rope.RoPEScaling("ntk", 2.0, 1.5))
+    c64, s64 = R.rotary_tables_f64(coords.numpy(), head_dim, time_scale=1.5, scaling=("ntk", 2.0, 1.5))
+    ct, st = T.rotary_tables(coords, head_dim, time_scale=1.5, scaling=("ntk", 2.0, 1.5))
+    c, s = tabs.cos.cpu().numpy(), tabs.sin.cpu().numpy()
+    assert np.abs(c - c64).max() < 1e-5 and np.abs(s - s64).max() < 1e-5
+    # same fp32 angles as the torch restatement; only cos/sin rounding differs
+    assert np.abs(c - ct.numpy()).max() < 5e-7 and np.abs(s - st.numpy()).max() < 5e-7
+    zero = amd.rope.build_rotary_tables(torch.zeros(1, 5, 3).cuda(), head_dim=head_dim)
+    assert torch.all(zero.cos == 1) and torch.all(zero.sin == 0)
+
+
+def test_rope_linear_scaling_tables(amd):
+    coords = torch.from_numpy(R.video_coords(3, 4, 5))
+    tabs = amd.rope.build_rotary_tables(coords.cuda(), head_dim=128, scaling=amd.rope.RoPEScaling("linear", 2.0, 3.0))
+    ct, st = T.rotary_tables(coords, 128, scaling=("linear", 2.0, 3.0))
+    assert np.abs(tabs.cos.cpu().numpy() - ct.numpy()).max() < 5e-7
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_rope_apply_bit_exact(amd, head_dim):
+    coords = torch.from_numpy(R.video_coords(5, 6, 7, batch=2))
+    cos, sin = T.rotary_tables(coords, head_dim)
+    x = _randn((2, 3, coords.shape[1], head_dim), 60, scale=3.0)
+    tabs = amd.rope.RotaryTables(cos.cuda(), sin.cuda())
+    got = amd.rope.apply_rotary(x.cuda(), tabs).cpu()
+    ref = T.apply_rotary(x, cos, sin)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    inv = amd.ops.rope_apply(x.cuda(), tabs.cos, tabs.sin, True).cpu().float().numpy()
+    ref_inv = R.apply_rotary_bf16(x.float().numpy(), cos.numpy(), sin.numpy(), inverse=True)
+    assert np.array_equal(inv.view(np.uint32), ref_inv.view(np.uint32))
+
+
+def test_rope_autograd_bit_exact(amd):
+    coords = torch.from_numpy(R.video_coords(2, 4, 4))
+    cos, sin = T.rotary_tables(coords, 128)
+    x = _randn((1, 2, 32, 128), 61)
+    g = _randn((1, 2, 32, 128), 62)
+    xg = x.cuda().requires_grad_(True)
+    amd.rope.apply_rotary(xg, amd.rope.RotaryTables(cos.cuda(), sin.cuda())).backward(g.cuda())
+    xr = x.clone().requires_grad_(True)
+    T.apply_rotary(xr, cos, sin).backward(g)
+    assert torch.equal(xg.grad.cpu().view(torch.int16), xr.grad.view(torch.int16))
+
+
+def test_fused_rope_forward_equals_unfused(amd):
+    B, H, L, D = 1, 2, 300, 128
+    coords = torch.from_numpy(R.video_coords(3, 10, 10, batch=B))
+    cos, sin = T.rotary_tables(coords, D)
+    tabs = amd.rope.RotaryTables(cos.cuda(), sin.cuda())
+    q, k, v = _randn((B, H, L, D), 70).cuda(), _randn((B, H, L, D), 71).cuda(), _randn((B, H, L, D), 72).cuda()
+    fused = amd.attention.rotary_attention(q, k, v, tabs)
+    qr = amd.rope.apply_rotary(q, tabs)
+    kr = amd.rope.apply_rotary(k, tabs)
+    unfused = amd.attention.attention(qr, kr, v)
+    assert torch.equal(fused, unfused)
+    # and gradients agree with the unfused composition through autograd
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    qb, kb, vb = (t.clone().requires_grad_(True) for t in (q, k, v))
+    do = _randn((B, H, L, D), 73).cuda()
+    amd.attention.rotary_attention(qa, ka, va, tabs).backward(do)
+    amd.attention.attention(amd.rope.apply_rotary(qb, tabs), amd.rope.apply_rotary(kb, tabs), vb).backward(do)
+    assert torch.equal(qa.grad, qb.grad) and torch.equal(ka.grad, kb.grad) and torch.equal(va.grad, vb.grad)
+
+
+# ---------------------------------------------------------------------------
+# Merge and emulated ring
+# ---------------------------------------------------------------------------
+
+
+def test_lse_merge_kernel_matches_oracle(amd):
+    g = _gen(80)
+    out = torch.randn(2, 3, 50, 128, generator=g)
+    lse = torch.randn(2, 3, 50, generator=g) * 4
+    out_b = torch.randn(2, 3, 50, 128, generator=g).to(torch.bfloat16)
+    lse_b = torch.randn(2, 3, 50, generator=g) * 4
+    lse[0, 0, :5] = float("-inf")
+    lse_b[0, 1, :5] = float("-inf")
+    lse[1, 2, :3] = float("-inf")
+    lse_b[1, 2, :3] = float("-inf")
+    oa, la = out.cuda(), lse.cuda()
+    amd.ops.lse_merge_(oa, la, out_b.cuda(), lse_b.cuda())
+    ro, rl = R.lse_merge_f32(out.numpy(), lse.numpy(), out_b.float().numpy(), lse_b.numpy())
+    assert np.allclose(oa.cpu().numpy(), ro, atol=2e-6, rtol=0)
+    lg = la.cpu().numpy()
+    assert np.array_equal(np.isneginf(lg), np.isneginf(rl))
+    fin = np.isfinite(rl)
+    assert np.allclose(lg[fin], rl[fin], atol=2e-6, rtol=0)
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_emulated_ring_matches_unchunked(amd, masked):
+    B, H, Lq, L, D, cp = 1, 3, 256, 1024, 128, 4
+    q, k, v = _randn((B, H, Lq, D), 90), _randn((B, H, L, D), 91), _randn((B, H, L, D), 92)
+    do = _randn((B, H, Lq, D), 93)
+    m = None
+    if masked:
+        m = torch.ones(B, L, dtype=torch.bool)
+        m[:, 700:] = False  # last chunk fully masked, third partly
+    mc = None if m is None else m.cuda()
+    qg, kg, vg = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    out, lse = amd.ring.ring_attention(qg, kg, vg, cp=cp, key_mask=mc)
+    out.backward(do.cuda())
+    mn = None if m is None else m.numpy()
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), mn)
+    assert np.abs(_f64(out) - ro).max() <= OUT_TOL
+    assert np.abs(lse.cpu().numpy() - rl).max() <= LSE_TOL
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, mn)
+    for got, ref in ((qg.grad, rq), (kg.grad, rk), (vg.grad, rv)):
+        assert np.abs(_f64(got) - ref).max() <= GRAD_REL_TOL * np.abs(ref).max()
+
+
+def test_ring_step_signatures_drop_into_torch_loop(amd):
+    # Call the local-step ops exactly as torch's ring does
+    # (torch/.../_attention.py:468-475 and 567-575).
+    q, k, v = _randn((1, 2, 128, 128), 100).cuda(), _randn((1, 2, 256, 128), 101).cuda(), _randn(
+        (1, 2, 256, 128), 102).cuda()
+    merger = amd.ring.SDPAMerger(True, seq_dim=2)
+    for kk, vv in zip(k.chunk(2, dim=2), v.chunk(2, dim=2)):
+        out, logsumexp, *rest = amd.ring.flash_attention_op(q, kk, vv, is_causal=False, dropout_p=0.0, scale=None)
+        assert len(rest) == 7
+        merger.step(out, logsumexp, False)
+    out, lse = merger.results()
+    full, full_lse = amd.ops.flash_fwd(q, k, v, None, None, None, 128 ** -0.5)
+    assert (out.float() - full.float()).abs().max().item() <= 2e-2
+    assert (lse - full_lse).abs().max().item() <= 1e-3
+    do = _randn((1, 2, 128, 128), 103).cuda()
+    dq, dk, dv, *rest = amd.ring.flash_attention_backward_op(
+        grad_out=do, query=q, key=k, value=v, out=out, logsumexp=lse, is_causal=False, dropout_p=0.0,
+        cum_seq_q=None, cum_seq_k=None, max_q=128, max_k=256, philox_seed=None, philox_offset=None, scale=None)
+    assert dq.shape == q.shape and dk.shape == k.shape and dv.shape == v.shape
+
+
+# ---------------------------------------------------------------------------
+# Errors surface like the reference's
+# ---------------------------------------------------------------------------
+
+
+def test_error_types(amd):
+    q = _randn((1, 2, 16, 128), 1).cuda()
+    with pytest.raises(TypeError):
+        amd.ops.flash_fwd(q.float(), q, q, None, None, None, 0.1)
+    with pytest.raises(ValueError):
+        amd.ops.flash_fwd(q[..., :96].contiguous(), q[..., :96].contiguous(), q[..., :96].contiguous(), None, None,
+                          None, 0.1)
+    with pytest.raises(NotImplementedError):
+        amd.attention.attention(q, q, q, is_causal=True)
+    with pytest.raises(NotImplementedError):
+        amd.attention.attention(q, q, q, dropout_p=0.1)
+    with pytest.raises(RuntimeError):
+        amd.ops.flash_fwd(q.cpu(), q.cpu(), q.cpu(), None, None, None, 0.1)

@@ -1,0 +1,431 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+Each oracle function is checked against something other than its own
+formula: closed forms and textbook special cases, an independent
+implementation (PyTorch's CPU SDPA kernels and autograd), finite
+differences, or invariants chosen so that a plausible slip (wrong pairing,
+wrong sign, wrong exponent denominator, transposed operand, dropped term)
+fails.  The reference ships no golden vectors for this path.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import reference as R
+from oracle import torch_path as T
+
+
+# ---------------------------------------------------------------------------
+# bf16 rounding
+# ---------------------------------------------------------------------------
+
+
+def test_bf16_round_matches_torch_cast(rng):
+    x = rng.standard_normal(20000).astype(np.float32) * 10.0
+    edge = np.array(
+        [0.0, -0.0, 1.0, 1.00390625, 1.005859375, 1.001953125, 3.0e38, -3.0e38, 1e-40, -1e-40, np.inf, -np.inf],
+        dtype=np.float32,
+    )
+    # ties: bf16(1 + 2^-8) is a tie between 1 and 1+2^-7
+    x = np.concatenate([x, edge, np.nextafter(edge, np.float32(np.inf)).astype(np.float32)])
+    ours = R.bf16_round(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ours.view(np.uint32), theirs.view(np.uint32))
+
+
+def test_bf16_round_keeps_nan():
+    assert np.isnan(R.bf16_round(np.array([np.nan], np.float32)))[0]
+
+
+# ---------------------------------------------------------------------------
+# rope_axis_pairs / tables (src/avgen/models/rope.py:128-294)
+# ---------------------------------------------------------------------------
+
+
+def test_rope_axis_pairs_closed_form():
+    # values stated in the reference's own docstring and in the BASELINE configs
+    assert R.rope_axis_pairs(64) == (12, 10, 10)
+    assert R.rope_axis_pairs(128) == (22, 21, 21)
+    assert R.rope_axis_pairs(6) == (1, 1, 1)
+    assert R.rope_axis_pairs(8) == (2, 1, 1)
+    for d in range(6, 258, 2):
+        t, h, w = R.rope_axis_pairs(d)
+        assert t + h + w == d // 2 and h == w and t >= h and t - h <= 2
+    for bad in (0, 4, 5, 7, 127, -6):
+        with pytest.raises(ValueError):
+            R.rope_axis_pairs(bad)
+
+
+def test_tables_zero_coords_are_identity():
+    cos, sin = R.rotary_tables_f64(np.zeros((2, 5, 3), np.float32), 128)
+    assert cos.shape == (2, 1, 5, 64)
+    assert np.all(cos == 1.0) and np.all(sin == 0.0)
+
+
+def test_tables_per_axis_denominator_known_values():
+    # d=12 -> 2 pairs per axis; axis frequencies 1 and theta^(-1/2) = 0.01.
+    # (A denominator of head_dim/2 instead of the axis's pair count would give
+    # theta^(-1/6).)
+    coords = np.array([[[1.0, 0.0, 0.0], [0.0, 1.0, 0.0], [0.0, 0.0, 3.0]]], np.float32)
+    cos, sin = R.rotary_tables_f64(coords, 12, theta=10000.0)
+    ang = np.arccos(np.clip(cos[0, 0], -1, 1)) * np.sign(sin[0, 0] + 1e-300)
+    expected = np.array(
+        [[1.0, 0.01, 0, 0, 0, 0], [0, 0, 1.0, 0.01, 0, 0], [0, 0, 0, 0, 3.0, 0.03]]
+    )
+    assert np.allclose(ang, expected, atol=1e-12)
+
+
+def test_tables_time_scale_linear_and_ntk():
+    coords = np.array([[[2.0, 4.0, 6.0]]], np.float32)
+    base_c, base_s = R.rotary_tables_f64(coords, 12)
+    c, s = R.rotary_tables_f64(coords, 12, time_scale=0.5)
+    # time_scale 0.5 on t=2 equals t=1 unscaled
+    c1, s1 = R.rotary_tables_f64(np.array([[[1.0, 4.0, 6.0]]], np.float32), 12)
+    assert np.allclose(c, c1) and np.allclose(s, s1)
+    # linear: positions divided by the factor (time factor 2, spatial 2)
+    cl, sl = R.rotary_tables_f64(coords, 12, scaling=("linear", 2.0, 2.0))
+    ch, sh = R.rotary_tables_f64(coords / 2, 12)
+    assert np.allclose(cl, ch) and np.allclose(sl, sh)
+    # ntk: dim = 4 per axis -> theta * f^(4/2); pair 1 frequency = (theta f^2)^(-1/2)
+    cn, sn = R.rotary_tables_f64(np.array([[[1.0, 0.0, 0.0]]], np.float32), 12, scaling=("ntk", 3.0, 1.0))
+    assert math.isclose(math.atan2(sn[0, 0, 0, 1], cn[0, 0, 0, 1]), 1.0 / (100.0 * 3.0), rel_tol=1e-12)
+    assert base_c.shape == (1, 1, 1, 6)
+
+
+@pytest.mark.parametrize("head_dim", [12, 64, 128])
+def test_tables_f64_agree_with_torch_restatement(head_dim):
+    coords = torch.from_numpy(R.video_coords(3, 4, 5))
+    ct, st = T.rotary_tables(coords, head_dim, time_scale=1.7, scaling=("ntk", 2.0, 1.5))
+    c, s = R.rotary_tables_f64(coords.numpy(), head_dim, time_scale=1.7, scaling=("ntk", 2.0, 1.5))
+    # fp32 angle rounding bounds the difference: |angle| * 2^-23 + a few ulp
+    tol = 2e-6 + 3e-7 * 12.0
+    assert np.abs(ct.numpy() - c).max() < tol and np.abs(st.numpy() - s).max() < tol
+
+
+# ---------------------------------------------------------------------------
+# apply_rotary (src/avgen/models/rope.py:297-338)
+# ---------------------------------------------------------------------------
+
+
+def _rand_bf16(rng, shape, scale=1.0):
+    return R.bf16_round((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+def test_rotation_is_interleaved_with_standard_sign():
+    # x = e_0 rotates to (cos, sin) in channels (0, 1); x = e_1 to (-sin, cos).
+    theta0 = 0.7
+    cos = np.full((1, 1, 1, 3), 1.0, np.float32)
+    sin = np.zeros((1, 1, 1, 3), np.float32)
+    cos[..., 0] = np.float32(math.cos(theta0))
+    sin[..., 0] = np.float32(math.sin(theta0))
+    e0 = np.zeros((1, 1, 1, 6), np.float32)
+    e0[..., 0] = 1.0
+    e1 = np.zeros((1, 1, 1, 6), np.float32)
+    e1[..., 1] = 1.0
+    r0 = R.apply_rotary_bf16(e0, cos, sin)[0, 0, 0]
+    r1 = R.apply_rotary_bf16(e1, cos, sin)[0, 0, 0]
+    assert np.array_equal(r0, R.bf16_round(np.array([cos[0, 0, 0, 0], sin[0, 0, 0, 0], 0, 0, 0, 0], np.float32)))
+    assert np.array_equal(r1, R.bf16_round(np.array([-sin[0, 0, 0, 0], cos[0, 0, 0, 0], 0, 0, 0, 0], np.float32)))
+
+
+def test_rotation_identity_at_zero_coords(rng):
+    x = _rand_bf16(rng, (2, 3, 7, 12))
+    cos, sin = R.rotary_tables_f64(np.zeros((2, 7, 3), np.float32), 12)
+    out = R.apply_rotary_bf16(x, cos.astype(np.float32), sin.astype(np.float32))
+    assert np.array_equal(out.view(np.uint32), x.view(np.uint32))
+
+
+def test_rotation_matches_torch_restatement_bitwise(rng):
+    coords = R.video_coords(3, 4, 5, batch=2)
+    cos, sin = T.rotary_tables(torch.from_numpy(coords), 64)
+    x = torch.randn(2, 3, coords.shape[1], 64).to(torch.bfloat16)
+    ref = T.apply_rotary(x, cos, sin).float().numpy()
+    ours = R.apply_rotary_bf16(x.float().numpy(), cos.numpy(), sin.numpy())
+    assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
+
+
+def test_inverse_rotation_is_torch_autograd_gradient(rng):
+    coords = R.video_coords(2, 3, 4)
+    cos, sin = T.rotary_tables(torch.from_numpy(coords), 64)
+    x = torch.randn(1, 2, coords.shape[1], 64).to(torch.bfloat16).requires_grad_(True)
+    g = torch.randn(1, 2, coords.shape[1], 64).to(torch.bfloat16)
+    T.apply_rotary(x, cos, sin).backward(g)
+    ours = R.apply_rotary_bf16(g.float().numpy(), cos.numpy(), sin.numpy(), inverse=True)
+    assert np.array_equal(ours.view(np.uint32), x.grad.float().numpy().view(np.uint32))
+
+
+def test_rotation_norm_and_relative_position(rng):
+    # Rotation is orthogonal per pair: norms preserved (up to the bf16 round),
+    # and <R(p) q, R(p') k> depends only on p - p'.
+    q = _rand_bf16(rng, (1, 1, 1, 12))
+    k = _rand_bf16(rng, (1, 1, 1, 12))
+
+    def rot(x, pos):
+        c, s = R.rotary_tables_f64(np.array([[pos]], np.float32), 12)
+        return R.apply_rotary_bf16(x, c.astype(np.float32), s.astype(np.float32)).astype(np.float64)
+
+    for pos in ([0.5, 3.0, 7.0], [2.0, 0.0, 11.0]):
+        r = rot(q, pos)
+        pr = r.reshape(-1, 2)
+        p0 = q.astype(np.float64).reshape(-1, 2)
+        assert np.allclose(np.linalg.norm(pr, axis=1), np.linalg.norm(p0, axis=1), rtol=2 ** -7)
+    d1 = float((rot(q, [1.0, 2.0, 3.0]) * rot(k, [0.5, 1.0, 1.0])).sum())
+    d2 = float((rot(q, [2.5, 5.0, 10.0]) * rot(k, [2.0, 4.0, 8.0])).sum())
+    assert abs(d1 - d2) < 0.05 * (1 + abs(d1))
+
+
+# ---------------------------------------------------------------------------
+# Attention + LSE (src/avgen/models/attention.py:227-273 -> SDPA)
+# ---------------------------------------------------------------------------
+
+
+def _qkv(rng, B=2, H=3, Hk=None, Lq=9, Lk=13, D=16):
+    Hk = H if Hk is None else Hk
+    return (rng.standard_normal((B, H, Lq, D)), rng.standard_normal((B, Hk, Lk, D)),
+            rng.standard_normal((B, Hk, Lk, D)))
+
+
+def test_attention_matches_torch_sdpa_float64(rng):
+    q, k, v = _qkv(rng)
+    mask = rng.random((2, 13)) > 0.3
+    mask[:, 0] = True
+    out, lse = R.attention_f64(q, k, v, mask)
+    ref = F.scaled_dot_product_attention(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+        attn_mask=torch.from_numpy(mask)[:, None, None, :],
+    ).numpy()
+    assert np.abs(out - ref).max() < 1e-12
+    # LSE against PyTorch's CPU flash kernel (float32 inputs)
+    _, lse_t = T.chunk_fwd(torch.from_numpy(q).float(), torch.from_numpy(k).float(),
+                           torch.from_numpy(v).float(), torch.from_numpy(mask))
+    assert np.abs(lse - lse_t.numpy()).max() < 1e-5
+
+
+def test_attention_special_cases(rng):
+    q, k, v = _qkv(rng, B=1, H=1, Lq=4, Lk=6, D=8)
+    # identical keys -> uniform weights: out = mean(v), lse = s + log(Lk)
+    k_same = np.repeat(k[:, :, :1], 6, axis=2)
+    out, lse = R.attention_f64(q, k_same, v)
+    s = (q @ k_same[0, 0, 0]) / math.sqrt(8)
+    assert np.allclose(out, v.mean(axis=2, keepdims=True).repeat(4, axis=2))
+    assert np.allclose(lse, s + math.log(6))
+    # one key -> out = v, lse = score
+    out1, lse1 = R.attention_f64(q, k[:, :, :1], v[:, :, :1])
+    assert np.allclose(out1, np.repeat(v[:, :, :1], 4, axis=2))
+    assert np.allclose(lse1, (q @ k[0, 0, 0]) / math.sqrt(8))
+    # empty keys -> zeros (src/avgen/models/attention.py:261-262)
+    out0, lse0 = R.attention_f64(q, k[:, :, :0], v[:, :, :0])
+    assert np.all(out0 == 0) and np.all(np.isneginf(lse0))
+
+
+def test_masked_keys_equal_deleted_keys(rng):
+    q, k, v = _qkv(rng, B=1, H=2, Lq=5, Lk=10, D=8)
+    mask = np.array([[True, False, True, True, False, False, True, True, False, True]])
+    out, lse = R.attention_f64(q, k, v, mask)
+    keep = mask[0]
+    out2, lse2 = R.attention_f64(q, k[:, :, keep], v[:, :, keep])
+    assert np.allclose(out, out2, atol=1e-13) and np.allclose(lse, lse2, atol=1e-13)
+
+
+def test_fully_masked_rows_give_zero_and_neg_inf(rng):
+    q, k, v = _qkv(rng, B=2, H=1, Lq=3, Lk=4, D=8)
+    mask = np.array([[False] * 4, [True, False, True, False]])
+    out, lse = R.attention_f64(q, k, v, mask)
+    assert np.all(out[0] == 0) and np.all(np.isneginf(lse[0]))
+    assert np.all(np.isfinite(lse[1]))
+    # PyTorch's SDPA also returns zeros for such rows (the reference's backend)
+    ref = F.scaled_dot_product_attention(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+                                         attn_mask=torch.from_numpy(mask)[:, None, None, :])
+    assert np.allclose(out, ref.numpy(), atol=1e-12)
+
+
+def test_gqa_equals_repeated_heads(rng):
+    q, k, v = _qkv(rng, B=1, H=4, Hk=2, Lq=5, Lk=7, D=8)
+    out, lse = R.attention_f64(q, k, v)
+    out2, lse2 = R.attention_f64(q, np.repeat(k, 2, axis=1), np.repeat(v, 2, axis=1))
+    assert np.array_equal(out, out2) and np.array_equal(lse, lse2)
+
+
+# ---------------------------------------------------------------------------
+# Backward (flash backward with recompute; torch/.../_attention.py:567-575)
+# ---------------------------------------------------------------------------
+
+
+def _torch_grads(q, k, v, do, mask=None, gqa=False):
+    tq, tk, tv = (torch.from_numpy(x).requires_grad_(True) for x in (q, k, v))
+    m = None if mask is None else torch.from_numpy(mask)[:, None, None, :]
+    o = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=m, enable_gqa=gqa)
+    o.backward(torch.from_numpy(do))
+    return tq.grad.numpy(), tk.grad.numpy(), tv.grad.numpy()
+
+
+def test_backward_matches_torch_autograd_float64(rng):
+    q, k, v = _qkv(rng)
+    mask = rng.random((2, 13)) > 0.4
+    mask[:, 3] = True
+    do = rng.standard_normal(q.shape)
+    out, lse = R.attention_f64(q, k, v, mask)
+    dq, dk, dv = R.attention_bwd_f64(do, q, k, v, out, lse, mask)
+    rq, rk, rv = _torch_grads(q, k, v, do, mask)
+    for a, b in ((dq, rq), (dk, rk), (dv, rv)):
+        assert np.abs(a - b).max() < 1e-11
+    # masked keys get exactly zero gradient
+    assert np.all(dk[:, :, :][~np.broadcast_to(mask[:, None, :], dk.shape[:3])] == 0)
+
+
+def test_backward_gqa_matches_torch_autograd(rng):
+    q, k, v = _qkv(rng, B=1, H=4, Hk=2, Lq=6, Lk=5, D=8)
+    do = rng.standard_normal(q.shape)
+    out, lse = R.attention_f64(q, k, v)
+    dq, dk, dv = R.attention_bwd_f64(do, q, k, v, out, lse)
+    rq, rk, rv = _torch_grads(q, k, v, do, gqa=True)
+    assert np.abs(dq - rq).max() < 1e-11 and np.abs(dk - rk).max() < 1e-11 and np.abs(dv - rv).max() < 1e-11
+
+
+def test_backward_finite_differences(rng):
+    q, k, v = _qkv(rng, B=1, H=1, Lq=3, Lk=4, D=4)
+    do = rng.standard_normal(q.shape)
+    out, lse = R.attention_f64(q, k, v)
+    dq, dk, dv = R.attention_bwd_f64(do, q, k, v, out, lse)
+    eps = 1e-6
+
+    def loss(q_, k_, v_):
+        return float((R.attention_f64(q_, k_, v_)[0] * do).sum())
+
+    for arr, grad, idx in ((q, dq, (0, 0, 1, 2)), (k, dk, (0, 0, 3, 0)), (v, dv, (0, 0, 2, 3))):
+        plus, minus = arr.copy(), arr.copy()
+        plus[idx] += eps
+        minus[idx] -= eps
+        args_p = [plus if a is arr else a for a in (q, k, v)]
+        args_m = [minus if a is arr else a for a in (q, k, v)]
+        fd = (loss(*args_p) - loss(*args_m)) / (2 * eps)
+        assert abs(fd - grad[idx]) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# Ring merge and loops (torch/.../_attention.py:138-223, 422-478, 514-646)
+# ---------------------------------------------------------------------------
+
+
+def test_chunked_merged_equals_unchunked(rng):
+    q, k, v = _qkv(rng, B=1, H=2, Lq=6, Lk=20, D=8)
+    mask = rng.random((1, 20)) > 0.3
+    mask[0, :5] = False  # first chunk fully masked for every row
+    mask[0, 7] = True
+    keys = [k[:, :, i:i + 5] for i in range(0, 20, 5)]
+    vals = [v[:, :, i:i + 5] for i in range(0, 20, 5)]
+    masks = [mask[:, i:i + 5] for i in range(0, 20, 5)]
+    out, lse = R.ring_forward_f64(q, keys, vals, masks)
+    ref_out, ref_lse = R.attention_f64(q, k, v, mask)
+    assert np.abs(out - ref_out).max() < 1e-13 and np.abs(lse - ref_lse).max() < 1e-13
+    do = rng.standard_normal(q.shape)
+    dq, dks, dvs = R.ring_backward_f64(do, q, keys, vals, out, lse, masks)
+    rq, rk, rv = R.attention_bwd_f64(do, q, k, v, ref_out, ref_lse, mask)
+    assert np.abs(dq - rq).max() < 1e-12
+    assert np.abs(np.concatenate(dks, 2) - rk).max() < 1e-12
+    assert np.abs(np.concatenate(dvs, 2) - rv).max() < 1e-12
+
+
+def test_merge_f32_matches_torch_formula_and_exact_merge(rng):
+    out = rng.standard_normal((2, 3, 4, 8)).astype(np.float32)
+    out_b = rng.standard_normal((2, 3, 4, 8)).astype(np.float32)
+    lse = (rng.standard_normal((2, 3, 4)) * 5).astype(np.float32)
+    lse_b = (rng.standard_normal((2, 3, 4)) * 5).astype(np.float32)
+    mo, ml = R.lse_merge_f32(out, lse, out_b, lse_b)
+    to, tl = T.merge(torch.from_numpy(out), torch.from_numpy(lse), torch.from_numpy(out_b), torch.from_numpy(lse_b))
+    assert np.allclose(mo, to.numpy(), atol=2e-6) and np.allclose(ml, tl.numpy(), atol=2e-6)
+    eo, el = R.lse_merge_f64(out, lse, out_b, lse_b)
+    assert np.allclose(mo, eo, atol=1e-5) and np.allclose(ml, el, atol=1e-5)
+
+
+def test_merge_neg_inf_is_identity(rng):
+    out = rng.standard_normal((3, 8)).astype(np.float32)
+    out_b = rng.standard_normal((3, 8)).astype(np.float32)
+    lse = np.array([-np.inf, 1.0, -np.inf], np.float32)
+    lse_b = np.array([2.0, -np.inf, -np.inf], np.float32)
+    mo, ml = R.lse_merge_f32(out, lse, out_b, lse_b)
+    assert np.array_equal(mo[0], out_b[0]) and ml[0] == 2.0
+    assert np.array_equal(mo[1], out[1]) and ml[1] == 1.0
+    assert np.array_equal(mo[2], out[2]) and np.isneginf(ml[2])
+    to, tl = T.merge(torch.from_numpy(out), torch.from_numpy(lse), torch.from_numpy(out_b), torch.from_numpy(lse_b))
+    assert np.array_equal(to.numpy(), mo) and np.array_equal(tl.numpy(), ml)
+
+
+def test_merge_is_associative_and_commutative(rng):
+    parts = [(rng.standard_normal((4, 8)), rng.standard_normal(4) * 3) for _ in range(3)]
+    (a, la), (b, lb), (c, lc) = parts
+    ab, lab = R.lse_merge_f64(a, la, b, lb)
+    left, lleft = R.lse_merge_f64(ab, lab, c, lc)
+    bc, lbc = R.lse_merge_f64(b, lb, c, lc)
+    right, lright = R.lse_merge_f64(a, la, bc, lbc)
+    assert np.allclose(left, right) and np.allclose(lleft, lright)
+    ba, lba = R.lse_merge_f64(b, lb, a, la)
+    assert np.allclose(ab, ba) and np.allclose(lab, lba)
+
+
+def test_torch_ring_restatement_matches_oracle(rng):
+    q = torch.randn(1, 2, 8, 16)
+    k = torch.randn(1, 2, 24, 16)
+    v = torch.randn(1, 2, 24, 16)
+    mask = torch.rand(1, 24) > 0.3
+    mask[0, 0] = True
+    keys = list(k.split(6, dim=2))
+    vals = list(v.split(6, dim=2))
+    masks = list(mask.split(6, dim=1))
+    out, lse = T.ring_forward(q, keys, vals, masks)
+    ref_out, ref_lse = R.attention_f64(q.numpy(), k.numpy(), v.numpy(), mask.numpy())
+    assert np.abs(out.numpy() - ref_out).max() < 1e-5 and np.abs(lse.numpy() - ref_lse).max() < 1e-5
+    do = torch.randn_like(q)
+    dq, dks, dvs = T.ring_backward(do, q, keys, vals, out, lse, masks)
+    rq, rk, rv = R.attention_bwd_f64(do.numpy(), q.numpy(), k.numpy(), v.numpy(), ref_out, ref_lse, mask.numpy())
+    assert np.abs(dq.numpy() - rq).max() < 1e-4
+    assert np.abs(torch.cat(dks, 2).numpy() - rk).max() < 1e-4
+    assert np.abs(torch.cat(dvs, 2).numpy() - rv).max() < 1e-4
+
+
+# ---------------------------------------------------------------------------
+# Shard rules (src/avgen/parallel/context.py) and FLOP convention
+# ---------------------------------------------------------------------------
+
+
+def test_shard_rules_follow_reference_tests():
+    # tests/test_parallel.py:122-148 of the reference
+    assert R.sharded_length(64, 8) == 8
+    with pytest.raises(ValueError, match="not divisible"):
+        R.sharded_length(65, 8)
+    toks = np.arange(16, dtype=np.float32).reshape(1, 16, 1)
+    seen = [toks[0, slice(*R.shard_bounds(16, 4, r)), 0].tolist() for r in range(4)]
+    assert seen[0] == [0.0, 1.0, 2.0, 3.0] and seen[3] == [12.0, 13.0, 14.0, 15.0]
+    t, c, m = R.pad_to_multiple(np.ones((1, 10, 2)), np.ones((1, 10, 3), np.float32), np.ones((1, 10), bool), 4)
+    assert t.shape[1] == 12 and m[0, 10:].tolist() == [False, False] and m[0, :10].all()
+    assert np.all(c[0, 10:] == 0) and np.all(t[0, 10:] == 0)
+    # c3 shard boundary falls mid-frame: 75,600 / 4 = 18,900 = 5.25 frames of 3,600
+    assert R.sharded_length(21 * 45 * 80, 4) == 18900
+
+
+def test_flop_convention_matches_baseline_table():
+    assert R.attention_flops(1, 4, 1024, 1024, 64, backward=False) == pytest.approx(1.07e9, rel=5e-3)
+    assert R.attention_flops(2, 20, 16384, 16384, 128) == pytest.approx(1.65e13, rel=5e-3)
+    assert R.attention_flops(1, 40, 18900, 75600, 128) == pytest.approx(8.78e13, rel=5e-3)
+    assert R.attention_flops(2, 40, 75600, 75600, 128, backward=False) == pytest.approx(2.34e14, rel=5e-3)
+
+
+def test_key_padding_mask_semantics():
+    # tests/test_gpu_distributed.py:135-145 of the reference, on the CPU
+    full = np.ones((2, 128), bool)
+    assert R.key_padding_mask(full) is None
+    ragged = full.copy()
+    ragged[0, -1] = False
+    m = R.key_padding_mask(ragged)
+    assert m is not None and m.shape == (2, 1, 1, 128)
+    assert R.key_padding_mask(ragged, assume_dense=True) is None
+    with pytest.raises(ValueError):
+        R.key_padding_mask(np.ones((2, 1, 128), bool))
+    with pytest.raises(TypeError):
+        R.key_padding_mask(np.ones((2, 128), np.int32))
