@@ -62,6 +62,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr, c_ptr, c_i64, c_i32,
          c_ptr, c_i64p, c_ptr],
     ),
+    "avattn_timing_begin": (ctypes.c_int, [c_i32]),
+    "avattn_timing_end": (ctypes.c_int, []),
+    "avattn_timing_read": (ctypes.c_int, [c_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]),
+    "avattn_timing_reset": (ctypes.c_int, []),
 }
 
 # Status codes (include/avattn.h).
@@ -129,3 +133,42 @@ def i64_array(values) -> ctypes.Array:
     """A C ``int64_t[]`` holding ``values``."""
     vals = [int(v) for v in values]
     return (ctypes.c_int64 * len(vals))(*vals)
+
+
+#: Kernel ids of the launch timer (include/avattn.h).
+KERNEL_IDS = {
+    "attn_fwd": 0,
+    "bwd_preprocess": 1,
+    "bwd_dkdv": 2,
+    "bwd_dq": 3,
+    "lse_merge": 4,
+    "rope_apply": 5,
+    "rope_tables": 6,
+}
+
+
+class LaunchTiming:
+    """Context manager: per-kernel HIP-event timing of this library's launches.
+
+    ``with LaunchTiming(4096) as t: ...; t.read("attn_fwd") -> (total_ms, launches)``.
+    Reading synchronizes on the recorded events.
+    """
+
+    def __init__(self, capacity: int = 4096) -> None:
+        self.capacity = capacity
+
+    def __enter__(self) -> "LaunchTiming":
+        check(load().avattn_timing_begin(self.capacity), "avattn_timing_begin")
+        return self
+
+    def __exit__(self, *exc) -> None:
+        load().avattn_timing_end()
+
+    def read(self, kernel: str) -> tuple[float, int]:
+        ms = ctypes.c_double()
+        n = ctypes.c_int32()
+        check(load().avattn_timing_read(KERNEL_IDS[kernel], ctypes.byref(ms), ctypes.byref(n)), "avattn_timing_read")
+        return ms.value, n.value
+
+    def close(self) -> None:
+        load().avattn_timing_reset()

@@ -418,11 +418,13 @@ static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
   {
     constexpr int RPB = 256 / (D / 8);
     const int64_t rows = (int64_t)a.B * a.Hq * a.Lq;
+    LaunchTimer timer(kKidBwdPre, stream);
     hipLaunchKernelGGL(bwd_pre_kernel<D>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, stream, a);
   }
   {
     const int nkt = (a.Lk + 127) / 128;
     const dim3 grid(nkt * a.B * a.Hkv);
+    LaunchTimer timer(kKidBwdDkdv, stream);
     if (mask)
       hipLaunchKernelGGL((bwd_dkdv_kernel<D, true>), grid, dim3(256), 0, stream, a);
     else
@@ -431,6 +433,7 @@ static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
   {
     const int nqt = (a.Lq + 127) / 128;
     const dim3 grid(nqt * a.B * a.Hq);
+    LaunchTimer timer(kKidBwdDq, stream);
     if (mask)
       hipLaunchKernelGGL((bwd_dq_kernel<D, true>), grid, dim3(256), 0, stream, a);
     else

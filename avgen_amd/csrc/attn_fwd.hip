@@ -234,6 +234,7 @@ static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   const dim3 block(256);
   const bool mask = a.mask != nullptr;
   const bool rope = a.cos_q != nullptr;
+  LaunchTimer timer(kKidFwd, stream);
   if (mask && rope)
     hipLaunchKernelGGL((attn_fwd_kernel<D, true, true>), grid, block, 0, stream, a);
   else if (mask)

@@ -95,18 +95,25 @@ __device__ __forceinline__ uint32_t pack_halves(uint32_t a, uint32_t b, int hi) 
 // every product rounded separately (no FMA contraction), then rounded to
 // bf16.  Matches src/avgen/models/rope.py:332-338 bit for bit.
 __device__ __forceinline__ u32x4 rotate8(const u32x4& x, const f32x4& c, const f32x4& s, bool inverse) {
+  // Contraction off: with -ffp-contract=fast the compiler would fuse a
+  // product with the following add/sub into one FMA (one rounding instead of
+  // two).  HIP's __fmul_rn/__fadd_rn are plain operators defined in a header
+  // compiled with contraction on, so the operators are written out here,
+  // inside the pragma's scope.
+#pragma clang fp contract(off)
   u32x4 r;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
     const float e = __uint_as_float(x[p] << 16);
     const float o = __uint_as_float(x[p] & 0xffff0000u);
+    const float ec = e * c[p], os = o * s[p], es = e * s[p], oc = o * c[p];
     float a, b;
     if (!inverse) {
-      a = __fsub_rn(__fmul_rn(e, c[p]), __fmul_rn(o, s[p]));
-      b = __fadd_rn(__fmul_rn(e, s[p]), __fmul_rn(o, c[p]));
+      a = ec - os;
+      b = es + oc;
     } else {
-      a = __fadd_rn(__fmul_rn(e, c[p]), __fmul_rn(o, s[p]));
-      b = __fsub_rn(__fmul_rn(o, c[p]), __fmul_rn(e, s[p]));
+      a = ec + os;
+      b = oc - es;
     }
     r[p] = pack_bf16x2(a, b);
   }

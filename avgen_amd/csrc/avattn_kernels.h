@@ -57,6 +57,30 @@ struct BwdArgs {
   float* lse2;   // lse * log2(e); +inf for rows with lse == -inf
 };
 
+// Kernel ids of the opt-in launch timer (avattn_timing_* in include/avattn.h).
+enum KernelId : int {
+  kKidFwd = 0,
+  kKidBwdPre = 1,
+  kKidBwdDkdv = 2,
+  kKidBwdDq = 3,
+  kKidMerge = 4,
+  kKidRopeApply = 5,
+  kKidRopeTables = 6,
+};
+
+// Records HIP events around one launch on `stream` while timing is enabled.
+class LaunchTimer {
+ public:
+  LaunchTimer(int kernel_id, hipStream_t stream);
+  ~LaunchTimer();
+  LaunchTimer(const LaunchTimer&) = delete;
+  LaunchTimer& operator=(const LaunchTimer&) = delete;
+
+ private:
+  int slot_;
+  hipStream_t stream_;
+};
+
 hipError_t launch_fwd(const FwdArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_empty(bf16* o, int64_t osb, int64_t osh, int64_t osl, int B, int H, int L, int D, float* lse,
                         hipStream_t stream);

@@ -65,6 +65,7 @@ static void launch_merge_d(float* out, float* lse, const void* ob, const float* 
                            hipStream_t stream) {
   constexpr int RPB = 256 / (D / 8);
   const dim3 grid((unsigned)((rows + RPB - 1) / RPB));
+  LaunchTimer timer(kKidMerge, stream);
   if (bf)
     hipLaunchKernelGGL((lse_merge_kernel<D, true>), grid, dim3(256), 0, stream, out, lse, ob, lb, rows);
   else

@@ -94,6 +94,7 @@ hipError_t launch_rope_tables(const float* coords, int64_t csb, int64_t csr, int
   a.sin_out = sin_out;
   const int64_t n = (int64_t)B * L * P;
   if (n == 0) return hipSuccess;
+  LaunchTimer timer(kKidRopeTables, stream);
   hipLaunchKernelGGL(rope_tables_kernel, dim3(grid_for(n)), dim3(256), 0, stream, a);
   return hipGetLastError();
 }
@@ -103,6 +104,7 @@ hipError_t launch_rope_apply(const bf16* x, int64_t xsb, int64_t xsh, int64_t xs
                              int64_t osb, int64_t osh, int64_t osl, hipStream_t stream) {
   const int64_t n = (int64_t)B * H * L * (D / 8);
   if (n == 0) return hipSuccess;
+  LaunchTimer timer(kKidRopeApply, stream);
   hipLaunchKernelGGL(rope_apply_kernel, dim3(grid_for(n)), dim3(256), 0, stream, x, xsb, xsh, xsl, B, H, L, D,
                      cos_tab, sin_tab, tsb, inverse ? 1 : 0, out, osb, osh, osl);
   return hipGetLastError();

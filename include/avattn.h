@@ -177,6 +177,22 @@ int avattn_rope_apply(const void* x, const int64_t* x_strides,
                       void* out, const int64_t* out_strides,
                       avattn_stream_t stream);
 
+/*
+ * Launch timing (diagnostics; no counterpart in the reference, whose kernels
+ * are PyTorch's).  While enabled, every kernel launch of this library
+ * records a pair of HIP events on its launch stream; avattn_timing_read sums
+ * the elapsed times of one kernel kind (it synchronizes on the recorded
+ * events).  Kernel ids: 0 forward, 1 backward preprocess, 2 backward dK/dV,
+ * 3 backward dQ, 4 LSE merge, 5 rotary apply, 6 rotary tables.
+ * avattn_timing_begin creates `capacity` event pairs (call it outside any
+ * timed or captured region); launches beyond capacity are not recorded and
+ * make avattn_timing_read return AVATTN_ERR_WORKSPACE.
+ */
+int avattn_timing_begin(int32_t capacity);
+int avattn_timing_end(void);
+int avattn_timing_read(int32_t kernel_id, double* total_ms, int32_t* launches);
+int avattn_timing_reset(void);
+
 #ifdef __cplusplus
 }
 #endif
