@@ -4,10 +4,14 @@
 //   1. preprocess: delta = rowsum(dout * out) and lse2 = lse * log2(e) per
 //      query row (the `D` term of dS = P * (dP - D));
 //   2. dK/dV: one workgroup per 128 keys (32 per wave, kept in registers as
-//      MFMA operands); loops over every query tile of every query head that
-//      reads this KV head;
-//   3. dQ: one workgroup per 128 query rows (32 per wave); loops over 32-key
+//      MFMA operands); loops over 64-row query tiles of every query head
+//      that reads this KV head;
+//   3. dQ: one workgroup per 128 query rows (32 per wave); loops over 64-key
 //      tiles.
+// Tiles live in LDS row-major only; the transposed operands (Q^T, dO^T,
+// K^T) come from ds_read_b64_tr_b16 reads of the same tiles.  Each step
+// works on two independent 32-row halves so the MFMA chains of one half
+// overlap the softmax-gradient VALU work of the other.
 // With out/lse the merged result over all KV chunks, the outputs are one
 // chunk's contributions, which is how the ring backward calls the op
 // (torch/.../_context_parallel/_attention.py:567-575).
@@ -52,26 +56,23 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 // 2. dK / dV
 // ---------------------------------------------------------------------------
 // Per wave: 32 keys (lane % 32 owns key column k0w + lane % 32).  For each
-// 32-row query tile:
-//   S  = Q K^T    A = Q rows (LDS, row-major)     B = K^T (registers)
-//   dP = dO V^T   A = dO rows (LDS, row-major)    B = V^T (registers)
+// 32-row half of a 64-row query tile:
+//   S  = Q K^T    A = Q rows (LDS)             B = K^T (registers)
+//   dP = dO V^T   A = dO rows (LDS)            B = V^T (registers)
 //   P  = exp2(S*c - lse2[q]),  dS = P * (dP - delta[q])        (fp32)
-//   dV^T += dO^T P   A = dO^T (LDS, transposed)   B = P  (C layout reused)
-//   dK^T += Q^T dS   A = Q^T  (LDS, transposed)   B = dS (C layout reused)
-// The C layout of S puts query 8*(r/4) + 4*hh + r%4 in register r, so the
-// 16-row k-step k2 of P uses registers 8*k2 + e for slot (hh, e) <-> query
-// 16*k2 + 8*(e/4) + 4*hh + e%4 — the A reads below fetch the same queries.
+//   dV^T += dO^T P   A = dO^T (LDS, tr read)   B = P  (C layout reused)
+//   dK^T += Q^T dS   A = Q^T  (LDS, tr read)   B = dS (C layout reused)
+// The C layout of S puts query 8*(r/4) + 4*hh + r%4 in register r; the
+// 16-row k-step k2 uses registers 8*k2 + e for slot (hh, e) <-> query
+// 16*k2 + 8*(e/4) + 4*hh + e%4, which is the order tr_operand reads.
 template <int D, bool MASK>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
-  constexpr int BK = 128, BQ = 32, NT = 256;
+  constexpr int BK = 128, BQ = 64, NT = 256;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int RS = D + 8;
-  using QTile = TransTile<BQ, D, NT / 2>;
-  constexpr int TS = QTile::kStride;
+  using Tile = RowTile<BQ, D, NT>;
   __shared__ __attribute__((aligned(16))) bf16 sq[2][BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sqt[2][D * TS];
   __shared__ __attribute__((aligned(16))) bf16 sdo[2][BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sdot[2][D * TS];
   __shared__ __attribute__((aligned(16))) float slse[2][BQ];
   __shared__ __attribute__((aligned(16))) float sdel[2][BQ];
 
@@ -117,21 +118,16 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
 
   const int nqt = (a.Lq + BQ - 1) / BQ;
   const int niter = nqt * group;
-  // Threads [0, 128) stage Q, threads [128, 256) stage dO; both orientations.
-  const bool stage_q = tid < NT / 2;
-  const int stid = stage_q ? tid : tid - NT / 2;
-  QTile reg;
+  Tile qreg, oreg;
   float stat_reg = 0.f;
 
   auto load_tile = [&](int it) {
     const int hq = hk * group + it / nqt;
     const int q0 = (it % nqt) * BQ;
     const int rows = min(BQ, a.Lq - q0);
-    if (stage_q)
-      reg.load(a.q + b * a.qsb + hq * a.qsh + (int64_t)q0 * a.qsl, a.qsl, rows, stid);
-    else
-      reg.load(a.dout + b * a.dosb + hq * a.dosh + (int64_t)q0 * a.dosl, a.dosl, rows, stid);
-    // Row statistics: threads [0, 32) lse2, [32, 64) delta.
+    qreg.load(a.q + b * a.qsb + hq * a.qsh + (int64_t)q0 * a.qsl, a.qsl, rows, tid);
+    oreg.load(a.dout + b * a.dosb + hq * a.dosh + (int64_t)q0 * a.dosl, a.dosl, rows, tid);
+    // Row statistics: threads [0, 64) lse2, [64, 128) delta.
     if (tid < 2 * BQ) {
       const int i = tid % BQ;
       const int64_t row = ((int64_t)(b * a.Hq + hq)) * a.Lq + q0 + i;
@@ -142,13 +138,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
     }
   };
   auto store_tile = [&](int buf) {
-    if (stage_q) {
-      reg.template store_rowmajor<RS>(sq[buf], stid);
-      reg.store(sqt[buf], stid);
-    } else {
-      reg.template store_rowmajor<RS>(sdo[buf], stid);
-      reg.store(sdot[buf], stid);
-    }
+    qreg.store(sq[buf], tid);
+    oreg.store(sdo[buf], tid);
     if (tid < BQ)
       slse[buf][tid] = stat_reg;
     else if (tid < 2 * BQ)
@@ -163,53 +154,65 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
   for (int it = 0; it < niter; ++it) {
     const int buf = it & 1;
     if (it + 1 < niter) load_tile(it + 1);
+    const bf16* tq = sq[buf];
+    const bf16* tdo = sdo[buf];
 
-    f32x16 s = zero16(), dp = zero16();
+    f32x16 s[2], dp[2];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&sq[buf][l32 * RS + 16 * ks + 8 * hh]);
-      const bf16x8 da = *reinterpret_cast<const bf16x8*>(&sdo[buf][l32 * RS + 16 * ks + 8 * hh]);
-      s = mfma32(qa, kf[ks], s);
-      dp = mfma32(da, vf[ks], dp);
+    for (int sub = 0; sub < 2; ++sub) {
+      s[sub] = zero16();
+      dp[sub] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = (sub * 32 + l32) * RS + 16 * ks + 8 * hh;
+        const bf16x8 qa = *reinterpret_cast<const bf16x8*>(tq + off);
+        const bf16x8 da = *reinterpret_cast<const bf16x8*>(tdo + off);
+        s[sub] = mfma32(qa, kf[ks], s[sub]);
+        dp[sub] = mfma32(da, vf[ks], dp[sub]);
+      }
     }
 
-    bf16x8 pb[2], dsb[2];
+    bf16x8 pb[2][2], dsb[2][2];
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      u32x4 up, ud;
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        // registers 8*k2 + 4*half + [0,4) hold queries 16*k2 + 8*half + 4*hh + [0,4)
-        const int g = 2 * k2 + half;
-        const f32x4 l2 = *reinterpret_cast<const f32x4*>(&slse[buf][8 * g + 4 * hh]);
-        const f32x4 dl = *reinterpret_cast<const f32x4*>(&sdel[buf][8 * g + 4 * hh]);
-        float p[4], ds[4];
+      for (int k2 = 0; k2 < 2; ++k2) {
+        u32x4 up, ud;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pr = kvalid ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + r], c, -l2[r])) : 0.f;
-          p[r] = pr;
-          ds[r] = pr * (dp[4 * g + r] - dl[r]);
+        for (int half = 0; half < 2; ++half) {
+          // registers 8*k2 + 4*half + [0,4) hold queries
+          // 32*sub + 16*k2 + 8*half + 4*hh + [0,4)
+          const int g = 2 * k2 + half;
+          const f32x4 l2 = *reinterpret_cast<const f32x4*>(&slse[buf][sub * 32 + 8 * g + 4 * hh]);
+          const f32x4 dl = *reinterpret_cast<const f32x4*>(&sdel[buf][sub * 32 + 8 * g + 4 * hh]);
+          float p[4], ds[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pr = kvalid ? __builtin_amdgcn_exp2f(fmaf(s[sub][4 * g + r], c, -l2[r])) : 0.f;
+            p[r] = pr;
+            ds[r] = pr * (dp[sub][4 * g + r] - dl[r]);
+          }
+          up[2 * half] = pack_bf16x2(p[0], p[1]);
+          up[2 * half + 1] = pack_bf16x2(p[2], p[3]);
+          ud[2 * half] = pack_bf16x2(ds[0], ds[1]);
+          ud[2 * half + 1] = pack_bf16x2(ds[2], ds[3]);
         }
-        up[2 * half] = pack_bf16x2(p[0], p[1]);
-        up[2 * half + 1] = pack_bf16x2(p[2], p[3]);
-        ud[2 * half] = pack_bf16x2(ds[0], ds[1]);
-        ud[2 * half + 1] = pack_bf16x2(ds[2], ds[3]);
+        pb[sub][k2] = bits_to_bf16x8(up);
+        dsb[sub][k2] = bits_to_bf16x8(ud);
       }
-      pb[k2] = bits_to_bf16x8(up);
-      dsb[k2] = bits_to_bf16x8(ud);
-    }
 
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16* dr = &sdot[buf][(dt * 32 + l32) * TS + 16 * k2 + 4 * hh];
-        const bf16* qr = &sqt[buf][(dt * 32 + l32) * TS + 16 * k2 + 4 * hh];
-        const bf16x8 da = cat4(*reinterpret_cast<const u32x2*>(dr), *reinterpret_cast<const u32x2*>(dr + 8));
-        const bf16x8 qa = cat4(*reinterpret_cast<const u32x2*>(qr), *reinterpret_cast<const u32x2*>(qr + 8));
-        dv[dt] = mfma32(da, pb[k2], dv[dt]);
-        dk[dt] = mfma32(qa, dsb[k2], dk[dt]);
-      }
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const int r0 = sub * 32 + 16 * k2;
+          const bf16x8 da = tr_operand(tdo, RS, r0, dt * 32, lane);
+          const bf16x8 qa = tr_operand(tq, RS, r0, dt * 32, lane);
+          dv[dt] = mfma32(da, pb[sub][k2], dv[dt]);
+          dk[dt] = mfma32(qa, dsb[sub][k2], dk[dt]);
+        }
 
     if (it + 1 < niter) store_tile(buf ^ 1);
     __syncthreads();
@@ -237,23 +240,18 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
 // 3. dQ
 // ---------------------------------------------------------------------------
 // Per wave: 32 query rows (lane % 32 owns query column q0w + lane % 32).  For
-// each 32-key tile:
-//   S^T  = K Q^T    A = K rows (LDS)      B = Q^T (registers)
-//   dP^T = V dO^T   A = V rows (LDS)      B = dO^T (registers)
-//   dS^T = P^T * (dP^T - delta[q])        (fp32, key bias masks P^T)
-//   dQ^T += K^T dS^T   A = K^T (LDS, transposed)   B = dS^T (C layout reused)
+// each 32-key half of a 64-key tile:
+//   S^T  = K Q^T    A = K rows (LDS)          B = Q^T (registers)
+//   dP^T = V dO^T   A = V rows (LDS)          B = dO^T (registers)
+//   dS^T = P^T * (dP^T - delta[q])            (fp32, key bias masks P^T)
+//   dQ^T += K^T dS^T   A = K^T (LDS, tr read)  B = dS^T (C layout reused)
 template <int D, bool MASK>
-__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
-  constexpr int BM = 128, BN = 32, NT = 256;
+__global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdArgs a) {
+  constexpr int BM = 128, BN = 64, NT = 256;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int RS = D + 8;
-  // Threads [0, 128) stage K (row-major and transposed), threads [128, 256)
-  // stage V (row-major); both use the same 4-row unit so one register tile
-  // serves either role.
-  using Tile = TransTile<BN, D, NT / 2>;
-  constexpr int TS = Tile::kStride;
+  using Tile = RowTile<BN, D, NT>;
   __shared__ __attribute__((aligned(16))) bf16 sk[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16 skt[2][D * TS];
   __shared__ __attribute__((aligned(16))) bf16 sv[2][BN * RS];
   __shared__ __attribute__((aligned(16))) float sbias[2][BN];
   __shared__ int sfull[2];
@@ -296,18 +294,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
   const bf16* vbase = a.v + b * a.vsb + hk * a.vsh;
   const uint8_t* mbase = MASK ? a.mask + b * a.msb : nullptr;
 
-  const bool stage_k = tid < NT / 2;
-  const int stid = stage_k ? tid : tid - NT / 2;
-  Tile reg;
+  Tile kreg, vreg;
   float bias_reg = 0.f;
 
   auto load_tile = [&](int t) {
     const int k0 = t * BN;
     const int rows = min(BN, a.Lk - k0);
-    if (stage_k)
-      reg.load(kbase + (int64_t)k0 * a.ksl, a.ksl, rows, stid);
-    else
-      reg.load(vbase + (int64_t)k0 * a.vsl, a.vsl, rows, stid);
+    kreg.load(kbase + (int64_t)k0 * a.ksl, a.ksl, rows, tid);
+    vreg.load(vbase + (int64_t)k0 * a.vsl, a.vsl, rows, tid);
     if (tid < BN) {
       bool valid = tid < rows;
       if (MASK && valid) valid = mbase[k0 + tid] != 0;
@@ -315,15 +309,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
     }
   };
   auto store_tile = [&](int buf) {
-    if (stage_k) {
-      reg.template store_rowmajor<RS>(sk[buf], stid);
-      reg.store(skt[buf], stid);
-    } else {
-      reg.template store_rowmajor<RS>(sv[buf], stid);
-    }
-    if (tid < 64) {
-      if (tid < BN) sbias[buf][tid] = bias_reg;
-      const unsigned long long ball = __ballot(tid >= BN || bias_reg == 0.f);
+    kreg.store(sk[buf], tid);
+    vreg.store(sv[buf], tid);
+    if (tid < BN) {
+      sbias[buf][tid] = bias_reg;
+      const unsigned long long ball = __ballot(bias_reg == 0.f);
       if (tid == 0) sfull[buf] = (ball == ~0ull) ? 1 : 0;
     }
   };
@@ -341,44 +331,57 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
   for (int t = 0; t < nkt; ++t) {
     const int buf = t & 1;
     if (t + 1 < nkt) load_tile(t + 1);
+    const bf16* tk = sk[buf];
+    const bf16* tv = sv[buf];
 
-    f32x16 s = zero16(), dp = zero16();
+    f32x16 s[2], dp[2];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&sk[buf][l32 * RS + 16 * ks + 8 * hh]);
-      const bf16x8 va = *reinterpret_cast<const bf16x8*>(&sv[buf][l32 * RS + 16 * ks + 8 * hh]);
-      s = mfma32(ka, qf[ks], s);
-      dp = mfma32(va, df[ks], dp);
+    for (int sub = 0; sub < 2; ++sub) {
+      s[sub] = zero16();
+      dp[sub] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = (sub * 32 + l32) * RS + 16 * ks + 8 * hh;
+        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tk + off);
+        const bf16x8 va = *reinterpret_cast<const bf16x8*>(tv + off);
+        s[sub] = mfma32(ka, qf[ks], s[sub]);
+        dp[sub] = mfma32(va, df[ks], dp[sub]);
+      }
     }
     if (!sfull[buf]) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(&sbias[buf][8 * g + 4 * hh]);
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s[4 * g + r] += bb[r];
-      }
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(&sbias[buf][sub * 32 + 8 * g + 4 * hh]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[sub][4 * g + r] += bb[r];
+        }
     }
-    bf16x8 dsb[2];
+    bf16x8 dsb[2][2];
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      u32x4 u;
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const int r = 8 * k2 + 2 * e2;
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[r], c, -lse2));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[r + 1], c, -lse2));
-        u[e2] = pack_bf16x2(p0 * (dp[r] - delta), p1 * (dp[r + 1] - delta));
+      for (int k2 = 0; k2 < 2; ++k2) {
+        u32x4 u;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int r = 8 * k2 + 2 * e2;
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][r], c, -lse2));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][r + 1], c, -lse2));
+          u[e2] = pack_bf16x2(p0 * (dp[sub][r] - delta), p1 * (dp[sub][r + 1] - delta));
+        }
+        dsb[sub][k2] = bits_to_bf16x8(u);
       }
-      dsb[k2] = bits_to_bf16x8(u);
-    }
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const bf16* kr = &skt[buf][(dt * 32 + l32) * TS + 16 * k2 + 4 * hh];
-        const bf16x8 ka = cat4(*reinterpret_cast<const u32x2*>(kr), *reinterpret_cast<const u32x2*>(kr + 8));
-        dq[dt] = mfma32(ka, dsb[k2], dq[dt]);
-      }
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const bf16x8 ka = tr_operand(tk, RS, sub * 32 + 16 * k2, dt * 32, lane);
+          dq[dt] = mfma32(ka, dsb[sub][k2], dq[dt]);
+        }
 
     if (t + 1 < nkt) store_tile(buf ^ 1);
     __syncthreads();

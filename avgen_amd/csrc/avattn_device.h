@@ -133,6 +133,36 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 }
 
 // ---------------------------------------------------------------------------
+// Transposed MFMA operand from a row-major LDS tile (ds_read_b64_tr_b16).
+// ---------------------------------------------------------------------------
+// ds_read_b64_tr_b16, per group of 16 lanes: lane i of the group receives
+// element i%4 of the 8-byte chunks addressed by the group's lanes i/4 + 4j,
+// j = 0..3.  So if lane s addresses row r0 + s/4, column c0 + 4*(s%4), lane i
+// receives rows r0..r0+3 of column c0 + i: four consecutive rows of one
+// column, i.e. an MFMA operand along the row dimension.
+//
+// tr_operand returns the 32x32x16 A (or B) operand X^T[m][k] for m = column
+// c0 + lane%32 and k slot (hh, e) <-> row r0 + 8*(e/4) + 4*hh + e%4 of a
+// row-major bf16 tile X with row stride `stride` elements — the same k-slot
+// order as the C layout of a 32x32 MFMA output, so the result pairs with a
+// B (A) operand built from such an output.
+__device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int stride, int r0, int c0, int lane) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const int g = lane >> 4, s = lane & 15;
+  const int row = r0 + 4 * (g >> 1) + (s >> 2);
+  const int col = c0 + 16 * (g & 1) + 4 * (s & 3);
+  const bf16* p = tile + row * stride + col;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p + 8 * stride));
+  u32x4 u;
+  u[0] = __builtin_bit_cast(u32x2, lo)[0];
+  u[1] = __builtin_bit_cast(u32x2, lo)[1];
+  u[2] = __builtin_bit_cast(u32x2, hi)[0];
+  u[3] = __builtin_bit_cast(u32x2, hi)[1];
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// ---------------------------------------------------------------------------
 // Tile staging helpers: global (row-major, head_dim contiguous) -> registers
 // -> LDS.  The register step lets a kernel issue the global loads of tile
 // t+1 before computing on tile t.
