@@ -69,10 +69,9 @@ template <int D, bool MASK>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
   constexpr int BK = 128, BQ = 64, NT = 256;
   constexpr int KS = D / 16, DT = D / 32;
-  constexpr int RS = D + 8;
   using Tile = RowTile<BQ, D, NT>;
-  __shared__ __attribute__((aligned(16))) bf16 sq[2][BQ * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sdo[2][BQ * RS];
+  __shared__ __attribute__((aligned(16))) bf16 sq[2][Tile::kElems];
+  __shared__ __attribute__((aligned(16))) bf16 sdo[2][Tile::kElems];
   __shared__ __attribute__((aligned(16))) float slse[2][BQ];
   __shared__ __attribute__((aligned(16))) float sdel[2][BQ];
 
@@ -164,9 +163,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
       dp[sub] = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int off = (sub * 32 + l32) * RS + 16 * ks + 8 * hh;
-        const bf16x8 qa = *reinterpret_cast<const bf16x8*>(tq + off);
-        const bf16x8 da = *reinterpret_cast<const bf16x8*>(tdo + off);
+        const bf16x8 qa = row_operand<D>(tq, sub * 32 + l32, 16 * ks + 8 * hh);
+        const bf16x8 da = row_operand<D>(tdo, sub * 32 + l32, 16 * ks + 8 * hh);
         s[sub] = mfma32(qa, kf[ks], s[sub]);
         dp[sub] = mfma32(da, vf[ks], dp[sub]);
       }
@@ -208,8 +206,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const int r0 = sub * 32 + 16 * k2;
-          const bf16x8 da = tr_operand(tdo, RS, r0, dt * 32, lane);
-          const bf16x8 qa = tr_operand(tq, RS, r0, dt * 32, lane);
+          const bf16x8 da = tr_operand<D>(tdo, r0, dt * 32, lane);
+          const bf16x8 qa = tr_operand<D>(tq, r0, dt * 32, lane);
           dv[dt] = mfma32(da, pb[sub][k2], dv[dt]);
           dk[dt] = mfma32(qa, dsb[sub][k2], dk[dt]);
         }
@@ -245,14 +243,17 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
 //   dP^T = V dO^T   A = V rows (LDS)          B = dO^T (registers)
 //   dS^T = P^T * (dP^T - delta[q])            (fp32, key bias masks P^T)
 //   dQ^T += K^T dS^T   A = K^T (LDS, tr read)  B = dS^T (C layout reused)
+#ifndef AVATTN_DQ_BN
+#define AVATTN_DQ_BN 32  // keys per dQ step: 32 or 64 (two 32-key halves)
+#endif
+
 template <int D, bool MASK>
-__global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdArgs a) {
-  constexpr int BM = 128, BN = 64, NT = 256;
+__global__ __launch_bounds__(256, AVATTN_DQ_BN == 64 ? 1 : 2) void bwd_dq_kernel(BwdArgs a) {
+  constexpr int BM = 128, BN = AVATTN_DQ_BN, NT = 256, NSUB = BN / 32;
   constexpr int KS = D / 16, DT = D / 32;
-  constexpr int RS = D + 8;
   using Tile = RowTile<BN, D, NT>;
-  __shared__ __attribute__((aligned(16))) bf16 sk[2][BN * RS];
-  __shared__ __attribute__((aligned(16))) bf16 sv[2][BN * RS];
+  __shared__ __attribute__((aligned(16))) bf16 sk[2][Tile::kElems];
+  __shared__ __attribute__((aligned(16))) bf16 sv[2][Tile::kElems];
   __shared__ __attribute__((aligned(16))) float sbias[2][BN];
   __shared__ int sfull[2];
 
@@ -311,9 +312,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdArgs a) {
   auto store_tile = [&](int buf) {
     kreg.store(sk[buf], tid);
     vreg.store(sv[buf], tid);
-    if (tid < BN) {
-      sbias[buf][tid] = bias_reg;
-      const unsigned long long ball = __ballot(bias_reg == 0.f);
+    if (tid < 64) {
+      if (tid < BN) sbias[buf][tid] = bias_reg;
+      const unsigned long long ball = __ballot(tid >= BN || bias_reg == 0.f);
       if (tid == 0) sfull[buf] = (ball == ~0ull) ? 1 : 0;
     }
   };
@@ -334,23 +335,22 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdArgs a) {
     const bf16* tk = sk[buf];
     const bf16* tv = sv[buf];
 
-    f32x16 s[2], dp[2];
+    f32x16 s[NSUB], dp[NSUB];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
+    for (int sub = 0; sub < NSUB; ++sub) {
       s[sub] = zero16();
       dp[sub] = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int off = (sub * 32 + l32) * RS + 16 * ks + 8 * hh;
-        const bf16x8 ka = *reinterpret_cast<const bf16x8*>(tk + off);
-        const bf16x8 va = *reinterpret_cast<const bf16x8*>(tv + off);
+        const bf16x8 ka = row_operand<D>(tk, sub * 32 + l32, 16 * ks + 8 * hh);
+        const bf16x8 va = row_operand<D>(tv, sub * 32 + l32, 16 * ks + 8 * hh);
         s[sub] = mfma32(ka, qf[ks], s[sub]);
         dp[sub] = mfma32(va, df[ks], dp[sub]);
       }
     }
     if (!sfull[buf]) {
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
+      for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 bb = *reinterpret_cast<const f32x4*>(&sbias[buf][sub * 32 + 8 * g + 4 * hh]);
@@ -358,9 +358,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdArgs a) {
           for (int r = 0; r < 4; ++r) s[sub][4 * g + r] += bb[r];
         }
     }
-    bf16x8 dsb[2][2];
+    bf16x8 dsb[NSUB][2];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         u32x4 u;
@@ -374,12 +374,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_kernel(BwdArgs a) {
         dsb[sub][k2] = bits_to_bf16x8(u);
       }
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int sub = 0; sub < NSUB; ++sub)
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const bf16x8 ka = tr_operand(tk, RS, sub * 32 + 16 * k2, dt * 32, lane);
+          const bf16x8 ka = tr_operand<D>(tk, sub * 32 + 16 * k2, dt * 32, lane);
           dq[dt] = mfma32(ka, dsb[sub][k2], dq[dt]);
         }
 

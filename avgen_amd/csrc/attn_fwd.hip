@@ -1,6 +1,7 @@
 // Flash-style attention forward for gfx950: one workgroup = 128 query rows of
 // one (batch, head); four waves own 32 rows each; K/V stream through LDS in
-// 64-key tiles, double-buffered.
+// 64-key row-major tiles, double-buffered (V^T operands come from LDS
+// transpose reads).
 //
 // Per wave and tile the scores are computed transposed, S^T = K Q^T, so that
 // each lane owns one query column (query = lane % 32) and holds 32 of that
@@ -16,15 +17,21 @@
 
 namespace avattn {
 
-template <int D, bool MASK, bool ROPE>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
-  constexpr int BM = 128, BN = 64, NT = 256;
+#ifndef AVATTN_FWD_QH
+#define AVATTN_FWD_QH 1  // 32-row query halves per wave (1 or 2)
+#endif
+
+// QH = query halves per wave: each wave owns 32*QH query rows and reuses every
+// K/V operand it reads from LDS for all of them (QH = 2 halves the LDS reads
+// per MFMA and gives the scheduler two independent softmax/MFMA chains).
+template <int D, bool MASK, bool ROPE, int QH>
+__global__ __launch_bounds__(256, QH == 1 ? 2 : 1) void attn_fwd_kernel(FwdArgs a) {
+  constexpr int BM = 128 * QH, BN = 64, NT = 256;
   constexpr int KS = D / 16;  // 16-channel k-steps of q k^T
   constexpr int DT = D / 32;  // 32-channel row tiles of O^T
-  using KTile = RowTile<BN, D, NT>;
-  using VTile = TransTile<BN, D, NT>;
-  __shared__ __attribute__((aligned(16))) bf16 sk[2][BN * KTile::kStride];
-  __shared__ __attribute__((aligned(16))) bf16 svt[2][D * VTile::kStride];
+  using Tile = RowTile<BN, D, NT>;
+  __shared__ __attribute__((aligned(16))) bf16 sk[2][Tile::kElems];
+  __shared__ __attribute__((aligned(16))) bf16 sv[2][Tile::kElems];
   __shared__ __attribute__((aligned(16))) float sbias[2][BN];
   __shared__ int sfull[2];
 
@@ -40,27 +47,33 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   const int b = bh / a.Hq, h = bh % a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
 
-  const int qrow = qt * BM + wave * 32 + l32;
-  const bool qvalid = qrow < a.Lq;
+  int qrow[QH];
+  bool qvalid[QH];
+#pragma unroll
+  for (int qh = 0; qh < QH; ++qh) {
+    qrow[qh] = qt * BM + (wave * QH + qh) * 32 + l32;
+    qvalid[qh] = qrow[qh] < a.Lq;
+  }
 
   // Q fragments: B operand of S^T = K Q^T; lane holds row qrow, channels
   // 16*ks + 8*hh + [0, 8).
-  bf16x8 qf[KS];
-  {
-    const bf16* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)qrow * a.qsl + 8 * hh;
+  bf16x8 qf[QH][KS];
+#pragma unroll
+  for (int qh = 0; qh < QH; ++qh) {
+    const bf16* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)qrow[qh] * a.qsl + 8 * hh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 x = {0u, 0u, 0u, 0u};
-      if (qvalid) {
+      if (qvalid[qh]) {
         x = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
         if constexpr (ROPE) {
-          const int64_t t = b * a.rsb + (int64_t)qrow * (D / 2) + 8 * ks + 4 * hh;
+          const int64_t t = b * a.rsb + (int64_t)qrow[qh] * (D / 2) + 8 * ks + 4 * hh;
           const f32x4 c = *reinterpret_cast<const f32x4*>(a.cos_q + t);
           const f32x4 s = *reinterpret_cast<const f32x4*>(a.sin_q + t);
           x = rotate8(x, c, s, false);
         }
       }
-      qf[ks] = bits_to_bf16x8(x);
+      qf[qh][ks] = bits_to_bf16x8(x);
     }
   }
 
@@ -68,8 +81,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   const bf16* vbase = a.v + b * a.vsb + hk * a.vsh;
   const uint8_t* mbase = MASK ? a.mask + b * a.msb : nullptr;
 
-  KTile kreg;
-  VTile vreg;
+  Tile kreg, vreg;
   float bias_reg = 0.f;
 
   auto load_tile = [&](int t) {
@@ -85,7 +97,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   };
   auto store_tile = [&](int buf) {
     kreg.store(sk[buf], tid);
-    vreg.store(svt[buf], tid);
+    vreg.store(sv[buf], tid);
     if (tid < BN) {
       sbias[buf][tid] = bias_reg;
       const unsigned long long ball = __ballot(bias_reg == 0.f);
@@ -94,11 +106,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   };
 
   const float c = a.scale_log2;
-  float m_run = kNegInf;  // running max of raw scores for this lane's query
-  float l_run = 0.f;      // this lane's share of the running row sum
-  f32x16 acc[DT];
+  // Lazy rescaling: the reference max m_run only moves when a tile's max
+  // exceeds it by more than 8 in log2 units, so probabilities stay <= 2^8
+  // (exact in fp32/bf16 range) and the O rescale is rare after the first
+  // tile.  The result is the same softmax; only roundings differ.
+  const float tau = 8.f / c;
+  float m_run[QH], l_run[QH][2];
+  f32x16 acc[QH][DT];
 #pragma unroll
-  for (int i = 0; i < DT; ++i) acc[i] = zero16();
+  for (int qh = 0; qh < QH; ++qh) {
+    m_run[qh] = kNegInf;  // reference max of raw scores for this lane's query
+    l_run[qh][0] = l_run[qh][1] = 0.f;  // this lane's share of the row sum
+#pragma unroll
+    for (int i = 0; i < DT; ++i) acc[qh][i] = zero16();
+  }
 
   const int nkt = (a.Lk + BN - 1) / BN;
   load_tile(0);
@@ -109,105 +130,110 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
     const int buf = t & 1;
     if (t + 1 < nkt) load_tile(t + 1);
     const bf16* kl = sk[buf];
-    const bf16* vl = svt[buf];
+    const bf16* vl = sv[buf];
+    const bool full = sfull[buf] != 0;
 
-    // S^T for the two 32-key halves: s[sub][r] is the score of key
-    // 32*sub + 8*(r/4) + 4*hh + r%4 against this lane's query.
-    f32x16 s[2];
+    // S^T for the two 32-key halves: s[qh][sub][r] is the score of key
+    // 32*sub + 8*(r/4) + 4*hh + r%4 against this lane's query of half qh.
+    f32x16 s[QH][2];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
-      s[sub] = zero16();
+#pragma unroll
+      for (int qh = 0; qh < QH; ++qh) s[qh][sub] = zero16();
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 kf =
-            *reinterpret_cast<const bf16x8*>(kl + (sub * 32 + l32) * KTile::kStride + 16 * ks + 8 * hh);
-        s[sub] = mfma32(kf, qf[ks], s[sub]);
+        const bf16x8 kf = row_operand<D>(kl, sub * 32 + l32, 16 * ks + 8 * hh);
+#pragma unroll
+        for (int qh = 0; qh < QH; ++qh) s[qh][sub] = mfma32(kf, qf[qh][ks], s[qh][sub]);
       }
     }
-    if (!sfull[buf]) {
+
+    bf16x8 pf[QH][2][2];
+#pragma unroll
+    for (int qh = 0; qh < QH; ++qh) {
+      if (!full) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 bb = *reinterpret_cast<const f32x4*>(&sbias[buf][sub * 32 + 8 * g + 4 * hh]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[qh][sub][4 * g + r] += bb[r];
+          }
+      }
+      float mx = kNegInf;
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 bb = *reinterpret_cast<const f32x4*>(&sbias[buf][sub * 32 + 8 * g + 4 * hh]);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qh][sub][r]);
+      mx = halves_max(mx);
+      if (mx > m_run[qh] + tau) {
+        // New reference max (both lanes of a query agree: mx is shared).
+        const float alpha = __builtin_amdgcn_exp2f((m_run[qh] - mx) * c);
+        l_run[qh][0] *= alpha;
+        l_run[qh][1] *= alpha;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s[sub][4 * g + r] += bb[r];
-        }
-    }
-
-    float mx = kNegInf;
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[sub][r]);
-    mx = halves_max(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == kNegInf) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
-    const float mc = m_use * c;
-
-    float rs = 0.f;
-    bf16x8 pf[2][2];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        u32x4 u;
-#pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const int r = 8 * k2 + 2 * e2;
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][r], c, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][r + 1], c, -mc));
-          rs += p0 + p1;
-          u[e2] = pack_bf16x2(p0, p1);
-        }
-        pf[sub][k2] = bits_to_bf16x8(u);
+          for (int r = 0; r < 16; ++r) acc[qh][dt][r] *= alpha;
+        m_run[qh] = mx;
       }
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
-    if (alpha != 1.f) {
+      const float mc = (m_run[qh] == kNegInf) ? 0.f : m_run[qh] * c;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
+      for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+        for (int k2 = 0; k2 < 2; ++k2) {
+          u32x4 u;
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int r = 8 * k2 + 2 * e2;
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qh][sub][r], c, -mc));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qh][sub][r + 1], c, -mc));
+            l_run[qh][e2 & 1] += p0 + p1;
+            u[e2] = pack_bf16x2(p0, p1);
+          }
+          pf[qh][sub][k2] = bits_to_bf16x8(u);
+        }
     }
 
-    // O^T += V^T P^T.  B operand slot (hh, e) of pf[sub][k2] is key
-    // 32*sub + 16*k2 + 8*(e/4) + 4*hh + e%4; the A operand reads the same keys
-    // of channel row d from the transposed V tile.
+    // O^T += V^T P^T.  B operand slot (hh, e) of pf[qh][sub][k2] is key
+    // 32*sub + 16*k2 + 8*(e/4) + 4*hh + e%4; tr_operand reads V^T in that
+    // key order from the row-major V tile.
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-          const bf16* vr = vl + (dt * 32 + l32) * VTile::kStride + sub * 32 + 16 * k2 + 4 * hh;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vr);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vr + 8);
-          acc[dt] = mfma32(cat4(lo, hi), pf[sub][k2], acc[dt]);
+          const bf16x8 va = tr_operand<D>(vl, sub * 32 + 16 * k2, dt * 32, lane);
+#pragma unroll
+          for (int qh = 0; qh < QH; ++qh) acc[qh][dt] = mfma32(va, pf[qh][sub][k2], acc[qh][dt]);
         }
 
     if (t + 1 < nkt) store_tile(buf ^ 1);
     __syncthreads();
   }
 
-  const float l_tot = halves_sum(l_run);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  if (qvalid) {
-    if (hh == 0) {
-      const float lse = l_tot > 0.f ? fmaf(m_run, a.scale, logf(l_tot)) : kNegInf;
-      a.lse[(int64_t)bh * a.Lq + qrow] = lse;
-    }
-    bf16* op = a.o + b * a.osb + h * a.osh + (int64_t)qrow * a.osl;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 w;
-        w[0] = pack_bf16x2(acc[dt][4 * g] * inv, acc[dt][4 * g + 1] * inv);
-        w[1] = pack_bf16x2(acc[dt][4 * g + 2] * inv, acc[dt][4 * g + 3] * inv);
-        *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
+  for (int qh = 0; qh < QH; ++qh) {
+    const float l_tot = halves_sum(l_run[qh][0] + l_run[qh][1]);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    if (qvalid[qh]) {
+      if (hh == 0) {
+        const float lse = l_tot > 0.f ? fmaf(m_run[qh], a.scale, logf(l_tot)) : kNegInf;
+        a.lse[(int64_t)bh * a.Lq + qrow[qh]] = lse;
       }
+      bf16* op = a.o + b * a.osb + h * a.osh + (int64_t)qrow[qh] * a.osl;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          u32x2 w;
+          w[0] = pack_bf16x2(acc[qh][dt][4 * g] * inv, acc[qh][dt][4 * g + 1] * inv);
+          w[1] = pack_bf16x2(acc[qh][dt][4 * g + 2] * inv, acc[qh][dt][4 * g + 3] * inv);
+          *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
+        }
+    }
   }
 }
 
@@ -229,20 +255,21 @@ __global__ void attn_empty_kernel(bf16* o, int64_t osb, int64_t osh, int64_t osl
 
 template <int D>
 static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
-  const int nqt = (a.Lq + 127) / 128;
+  constexpr int QH = AVATTN_FWD_QH;
+  const int nqt = (a.Lq + 128 * QH - 1) / (128 * QH);
   const dim3 grid(nqt * a.B * a.Hq);
   const dim3 block(256);
   const bool mask = a.mask != nullptr;
   const bool rope = a.cos_q != nullptr;
   LaunchTimer timer(kKidFwd, stream);
   if (mask && rope)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, true, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, true, true, QH>), grid, block, 0, stream, a);
   else if (mask)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, true, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, true, false, QH>), grid, block, 0, stream, a);
   else if (rope)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false, true, QH>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false, false, QH>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -133,6 +133,29 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 }
 
 // ---------------------------------------------------------------------------
+// LDS tile layout
+// ---------------------------------------------------------------------------
+// Row-major ROWS x D bf16 tile.  For D == 128 rows are 256 bytes with no
+// padding and the 16-byte chunk c of row r sits at chunk position c ^ f(r),
+// f(r) = 4*(r%4) + (r/4)%4.  Then sixteen lanes reading one chunk of 16
+// consecutive rows (ds_read_b128) and the 32 lanes of a transpose read (4
+// rows x 64 contiguous bytes, see tr_operand) each touch all 64 banks
+// exactly once.  Other head dims pad rows to D + 8 elements.
+template <int D>
+struct TileLayout {
+  static constexpr int kRowElems = (D == 128) ? 128 : D + 8;
+  // Element offset of (row, col); col must be a multiple of 4.
+  static __device__ __forceinline__ int off(int row, int col) {
+    if constexpr (D == 128) {
+      const int f = ((row & 3) << 2) | ((row >> 2) & 3);
+      return row * 128 + (((col >> 3) ^ f) << 3) + (col & 7);
+    } else {
+      return row * (D + 8) + col;
+    }
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Transposed MFMA operand from a row-major LDS tile (ds_read_b64_tr_b16).
 // ---------------------------------------------------------------------------
 // ds_read_b64_tr_b16, per group of 16 lanes: lane i of the group receives
@@ -143,17 +166,19 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 //
 // tr_operand returns the 32x32x16 A (or B) operand X^T[m][k] for m = column
 // c0 + lane%32 and k slot (hh, e) <-> row r0 + 8*(e/4) + 4*hh + e%4 of a
-// row-major bf16 tile X with row stride `stride` elements — the same k-slot
-// order as the C layout of a 32x32 MFMA output, so the result pairs with a
-// B (A) operand built from such an output.
-__device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int stride, int r0, int c0, int lane) {
+// row-major TileLayout<D> tile X — the same k-slot order as the C layout of
+// a 32x32 MFMA output, so the result pairs with a B (A) operand built from
+// such an output.
+template <int D>
+__device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int r0, int c0, int lane) {
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   const int g = lane >> 4, s = lane & 15;
   const int row = r0 + 4 * (g >> 1) + (s >> 2);
   const int col = c0 + 16 * (g & 1) + 4 * (s & 3);
-  const bf16* p = tile + row * stride + col;
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p + 8 * stride));
+  const bf16* plo = tile + TileLayout<D>::off(row, col);
+  const bf16* phi = tile + TileLayout<D>::off(row + 8, col);
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(plo));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(phi));
   u32x4 u;
   u[0] = __builtin_bit_cast(u32x2, lo)[0];
   u[1] = __builtin_bit_cast(u32x2, lo)[1];
@@ -162,116 +187,54 @@ __device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int stride, int r
   return __builtin_bit_cast(bf16x8, u);
 }
 
+// Row operand (8 consecutive channels of one row) from a TileLayout<D> tile.
+template <int D>
+__device__ __forceinline__ bf16x8 row_operand(const bf16* tile, int row, int col) {
+  return *reinterpret_cast<const bf16x8*>(tile + TileLayout<D>::off(row, col));
+}
+
 // ---------------------------------------------------------------------------
-// Tile staging helpers: global (row-major, head_dim contiguous) -> registers
-// -> LDS.  The register step lets a kernel issue the global loads of tile
-// t+1 before computing on tile t.
+// Tile staging: global (row-major, head_dim contiguous) -> registers -> LDS.
+// The register step lets a kernel issue the global loads of tile t+1 before
+// computing on tile t.
 // ---------------------------------------------------------------------------
 
-// Row-major tile ROWS x D staged by NT threads: each 16-byte chunk (8
-// channels) goes to lds[row * (D + 8) + col].  The +8 pad makes rows 4 banks
-// apart so eight lanes reading the same column of consecutive rows with
-// ds_read_b128 hit distinct banks.
+// ROWS x D tile staged by NT threads as 16-byte chunks into TileLayout<D>.
+// Loads are unconditional (rows past the end re-read the last valid row) so
+// the compiler emits one uninterrupted batch of global loads; the rows past
+// the end become zeros when stored, by which time the data has arrived.
 template <int ROWS, int D, int NT>
 struct RowTile {
-  static constexpr int kStride = D + 8;
+  static constexpr int kElems = ROWS * TileLayout<D>::kRowElems;  // LDS size
   static constexpr int kChunks = ROWS * D / 8;
   static constexpr int kPer = (kChunks + NT - 1) / NT;
   u32x4 reg[kPer];
+  int rows_valid_;
 
+  // rows_valid >= 1.
   __device__ __forceinline__ void load(const bf16* base, int64_t row_stride, int rows_valid, int tid) {
+    rows_valid_ = rows_valid;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = tid + i * NT;
-      const int row = c / (D / 8);
-      const int col = (c % (D / 8)) * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (c < kChunks && row < rows_valid)
-        v = *reinterpret_cast<const u32x4*>(base + (int64_t)row * row_stride + col);
-      reg[i] = v;
+      if (kChunks % NT == 0 || c < kChunks) {
+        const int row = min(c / (D / 8), rows_valid - 1);
+        reg[i] = *reinterpret_cast<const u32x4*>(base + (int64_t)row * row_stride + (c % (D / 8)) * 8);
+      }
     }
   }
   __device__ __forceinline__ void store(bf16* lds, int tid) const {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = tid + i * NT;
-      if (c < kChunks) {
+      if (kChunks % NT == 0 || c < kChunks) {
         const int row = c / (D / 8);
         const int col = (c % (D / 8)) * 8;
-        *reinterpret_cast<u32x4*>(lds + row * kStride + col) = reg[i];
-      }
-    }
-  }
-};
-
-// Transposed tile: global rows x D -> lds_t[d * (ROWS + 4) + row].  A unit of
-// work is 4 rows x 8 channels (four 16-byte loads); the thread transposes it
-// in registers and writes eight 8-byte runs (4 consecutive rows of one
-// channel).  Units are numbered so that the 16 lanes of one write pass cover
-// 16 consecutive row groups of a single channel row: a contiguous,
-// conflict-free 128-byte LDS span for ROWS = 64.  Readers fetch 4 consecutive
-// rows of one channel per 8-byte read; the ROWS+4 pad puts consecutive
-// channel rows 2 banks apart.
-template <int ROWS, int D, int NT>
-struct TransTile {
-  static constexpr int kStride = ROWS + 4;
-  static constexpr int kRowGroups = ROWS / 4;
-  static constexpr int kUnits = kRowGroups * (D / 8);
-  static constexpr int kPer = (kUnits + NT - 1) / NT;
-  u32x4 reg[kPer][4];
-
-  __device__ __forceinline__ void load(const bf16* base, int64_t row_stride, int rows_valid, int tid) {
+        const bool in = row < rows_valid_;
+        u32x4 v;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = tid + i * NT;
-      const int rg = u % kRowGroups;
-      const int dg = u / kRowGroups;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = rg * 4 + r;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (u < kUnits && row < rows_valid)
-          v = *reinterpret_cast<const u32x4*>(base + (int64_t)row * row_stride + dg * 8);
-        reg[i][r] = v;
-      }
-    }
-  }
-  // Also write the row-major copy of the same data (used by kernels that
-  // need both orientations of one tile).
-  template <int RSTRIDE>
-  __device__ __forceinline__ void store_rowmajor(bf16* lds, int tid) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = tid + i * NT;
-      if (u < kUnits) {
-        const int rg = u % kRowGroups;
-        const int dg = u / kRowGroups;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          *reinterpret_cast<u32x4*>(lds + (rg * 4 + r) * RSTRIDE + dg * 8) = reg[i][r];
-      }
-    }
-  }
-  __device__ __forceinline__ void store(bf16* lds_t, int tid) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int u = tid + i * NT;
-      if (u < kUnits) {
-        const int rg = u % kRowGroups;
-        const int dg = u / kRowGroups;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          // channel pair (2w, 2w+1) of the 8 channels, 4 rows each.
-          const uint32_t a0 = reg[i][0][w], a1 = reg[i][1][w], a2 = reg[i][2][w], a3 = reg[i][3][w];
-          u32x2 lo, hi;
-          lo[0] = pack_halves(a0, a1, 0);
-          lo[1] = pack_halves(a2, a3, 0);
-          hi[0] = pack_halves(a0, a1, 1);
-          hi[1] = pack_halves(a2, a3, 1);
-          const int d = dg * 8 + 2 * w;
-          *reinterpret_cast<u32x2*>(lds_t + d * kStride + rg * 4) = lo;
-          *reinterpret_cast<u32x2*>(lds_t + (d + 1) * kStride + rg * 4) = hi;
-        }
+        for (int w = 0; w < 4; ++w) v[w] = in ? reg[i][w] : 0u;
+        *reinterpret_cast<u32x4*>(lds + TileLayout<D>::off(row, col)) = v;
       }
     }
   }
