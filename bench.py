@@ -212,6 +212,70 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
+CALIBRATION_BYTES = 1 << 30  # float32 elements read and written by torch.neg
+
+
+def pmc_calibration(device) -> None:
+    """A copy-like kernel of known size for scaling the PMC byte counters:
+    torch.neg over 1 GiB of float32 reads 1 GiB and writes 1 GiB."""
+    src = torch.ones(CALIBRATION_BYTES // 4, device=device, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def ingest_pmc(fetch_csv: str, write_csv: str, kernel: str, workload: str) -> dict:
+    """Per-launch HBM bytes of `kernel` from two rocprofv3 --pmc runs.
+
+    FETCH_SIZE and WRITE_SIZE are read in KiB per dispatch; each is scaled by
+    the ratio of the calibration kernel's known bytes (CALIBRATION_BYTES read
+    and written by torch.neg) to what the same counter reported for it.
+    Writes profiles/traffic_<kernel>_<workload>.json and returns it.
+    """
+    import csv
+
+    symbol = {"attn_fwd": "attn_fwd_kernel", "bwd_dkdv": "bwd_dkdv_kernel", "bwd_dq": "bwd_dq_kernel"}[kernel]
+
+    def read(path: str, counter: str) -> tuple[float, float, int]:
+        kern, cal = [], []
+        with open(path) as fh:
+            for row in csv.DictReader(fh):
+                if row["Counter_Name"] != counter:
+                    continue
+                name = row["Kernel_Name"]
+                if symbol in name:
+                    kern.append(float(row["Counter_Value"]))
+                elif "neg_kernel" in name:
+                    cal.append(float(row["Counter_Value"]))
+        if not kern or not cal:
+            raise SystemExit(f"{path}: no {counter} rows for {symbol} and the calibration kernel")
+        return sum(kern) / len(kern), sum(cal) / len(cal), len(kern)
+
+    fk, fc, n = read(fetch_csv, "FETCH_SIZE")
+    wk, wc, _ = read(write_csv, "WRITE_SIZE")
+    f_scale = CALIBRATION_BYTES / (fc * 1024.0)
+    w_scale = CALIBRATION_BYTES / (wc * 1024.0)
+    result = {
+        "kernel": kernel,
+        "workload": workload,
+        "dispatches": n,
+        "fetch_kib_raw": fk,
+        "write_kib_raw": wk,
+        "calibration": {"bytes": CALIBRATION_BYTES, "fetch_kib_raw": fc, "write_kib_raw": wc,
+                        "fetch_scale": f_scale, "write_scale": w_scale},
+        "fetch_bytes_per_launch": fk * 1024.0 * f_scale,
+        "write_bytes_per_launch": wk * 1024.0 * w_scale,
+        "bytes_per_launch": fk * 1024.0 * f_scale + wk * 1024.0 * w_scale,
+        "command": (f"rocprofv3 --pmc FETCH_SIZE -d <dir> -o pmc --output-format csv -- python3 bench.py --config "
+                    f"{workload} --steps 1 --warmup 1 --no-cpu-baseline --pmc-calibration; same with WRITE_SIZE; "
+                    f"then python bench.py --ingest-pmc <fetch.csv> <write.csv> --kernel {kernel} --config {workload}"),
+    }
+    out = ROOT / "profiles" / f"traffic_{kernel}_{workload}.json"
+    out.write_text(json.dumps(result, indent=1) + "\n")
+    return result
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -220,7 +284,16 @@ def main() -> int:
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="also run the known-size calibration kernel (for rocprofv3 --pmc byte counters)")
+    ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn two rocprofv3 --pmc CSVs into profiles/traffic_<kernel>_<config>.json and exit")
+    ap.add_argument("--kernel", default="bwd_dkdv", choices=sorted(KERNEL_UNITS))
     args = ap.parse_args()
+
+    if args.ingest_pmc:
+        print(json.dumps(ingest_pmc(args.ingest_pmc[0], args.ingest_pmc[1], args.kernel, args.config)))
+        return 0
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the ring is emulated on one "
@@ -255,6 +328,9 @@ def main() -> int:
         torch.cuda.synchronize()
         t1 = time.perf_counter()
     log(f"[bench] timed {args.steps} steps in {t1 - t0:.3f}s")
+    if args.pmc_calibration:
+        pmc_calibration(dev)
+        log("[bench] calibration kernel done")
     per_kernel = {}
     for name in ("attn_fwd", "bwd_dkdv", "bwd_dq", "bwd_preprocess", "lse_merge", "rope_apply"):
         ms, n = timing.read(name)
