@@ -76,6 +76,12 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None) -> Path:
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
+    # A kernel whose host-side launch stub was not emitted links fine but
+    # fails at load time; refuse such a library here.
+    nm = subprocess.run(["nm", "-D", "--undefined-only", str(tmp)], capture_output=True, text=True)
+    missing = [line.split()[-1] for line in nm.stdout.splitlines() if "__device_stub__" in line]
+    if missing:
+        raise RuntimeError(f"link produced undefined kernel stubs (compiler host-pass issue): {missing[:4]}")
     os.replace(tmp, LIB)
     return LIB
 

@@ -135,23 +135,25 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 // ---------------------------------------------------------------------------
 // LDS tile layout
 // ---------------------------------------------------------------------------
-// Row-major ROWS x D bf16 tile.  For D == 128 rows are 256 bytes with no
-// padding and the 16-byte chunk c of row r sits at chunk position c ^ f(r),
-// f(r) = 4*(r%4) + (r/4)%4.  Then sixteen lanes reading one chunk of 16
-// consecutive rows (ds_read_b128) and the 32 lanes of a transpose read (4
-// rows x 64 contiguous bytes, see tr_operand) each touch all 64 banks
-// exactly once.  Other head dims pad rows to D + 8 elements.
+// Row-major ROWS x D bf16 tile with unpadded rows whose 16-byte chunks are
+// XOR-swizzled: chunk c of row r sits at chunk slot c ^ f(r).
+//   D == 128 (256-byte rows): f(r) = 4*(r%4) + (r/4)%4
+//   D == 64  (128-byte rows): f(r) = 4*((r/2)%2) + (r/4)%4
+// With these, sixteen lanes reading one chunk of 16 consecutive rows
+// (ds_read_b128) and the 32 lanes of a transpose read (4 rows x 64
+// contiguous bytes, see tr_operand) each touch all 64 banks exactly once,
+// and a 1 KB block of consecutive rows can be filled by one direct
+// global->LDS wave load (stage_direct).
 template <int D>
 struct TileLayout {
-  static constexpr int kRowElems = (D == 128) ? 128 : D + 8;
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static constexpr int kRowElems = D;
+  static __device__ __forceinline__ int swz(int row) {
+    return D == 128 ? (((row & 3) << 2) | ((row >> 2) & 3)) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+  }
   // Element offset of (row, col); col must be a multiple of 4.
   static __device__ __forceinline__ int off(int row, int col) {
-    if constexpr (D == 128) {
-      const int f = ((row & 3) << 2) | ((row >> 2) & 3);
-      return row * 128 + (((col >> 3) ^ f) << 3) + (col & 7);
-    } else {
-      return row * (D + 8) + col;
-    }
+    return row * D + (((col >> 3) ^ swz(row)) << 3) + (col & 7);
   }
 };
 
@@ -239,5 +241,75 @@ struct RowTile {
     }
   }
 };
+
+// 16 bytes per lane from global memory straight into LDS at
+// lds_block + 16*lane (global_load_lds_dwordx4; lds_block is wave-uniform).
+__device__ __forceinline__ void direct_load16(const bf16* src, bf16* lds_block) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
+}
+
+// Direct global->LDS staging of a ROWS x D tile into TileLayout<D> with
+// global_load_lds_dwordx4.  One wave instruction moves 1 KB: lane j's 16
+// bytes land at LDS block base + 16*j, i.e. row row0 + j/(D/8), chunk slot
+// j%(D/8); the lane therefore loads the logical chunk the swizzle maps to
+// that slot.  Rows at or past rows_valid (>= 1) re-read row rows_valid-1:
+// callers never use those rows unmasked.  The NW waves of a workgroup split
+// the tile's instructions; completion is tracked by vmcnt (callers wait with
+// vmcnt(0) and a barrier before reading).
+template <int ROWS, int D, int NW>
+__device__ __forceinline__ void stage_direct(bf16* lds, const bf16* g, int64_t row_stride, int rows_valid, int wave,
+                                             int lane) {
+  constexpr int kCpr = D / 8;       // 16-byte chunks per row
+  constexpr int kRpi = 64 / kCpr;   // rows per wave instruction
+  constexpr int kNi = ROWS / kRpi;  // instructions per tile
+  static_assert(kNi % NW == 0, "tile must split evenly over the waves");
+#pragma unroll
+  for (int i = 0; i < kNi / NW; ++i) {
+    const int row0 = (wave * (kNi / NW) + i) * kRpi;
+    const int row = row0 + lane / kCpr;
+    const int chunk = (lane % kCpr) ^ TileLayout<D>::swz(row);
+    const int srow = min(row, rows_valid - 1);
+    direct_load16(g + (int64_t)srow * row_stride + chunk * 8, lds + row0 * D);
+  }
+}
+
+// stage_direct with the per-lane source offsets precomputed (they depend only
+// on the lane, the wave and the row stride): for full tiles each load is a
+// uniform tile base plus a 32-bit lane offset, with no per-tile address math.
+template <int ROWS, int D, int NW>
+struct DirectStager {
+  static constexpr int kCpr = D / 8;
+  static constexpr int kRpi = 64 / kCpr;
+  static constexpr int kNi = ROWS / kRpi;
+  static constexpr int kPer = kNi / NW;
+  static_assert(kNi % NW == 0, "tile must split evenly over the waves");
+  int off[kPer];  // element offset of this lane's source chunk, per instruction
+  int lds_row0[kPer];
+
+  __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int row0 = (wave * kPer + i) * kRpi;
+      const int row = row0 + lane / kCpr;
+      off[i] = (int)(row * row_stride) + ((lane % kCpr) ^ TileLayout<D>::swz(row)) * 8;
+      lds_row0[i] = row0;
+    }
+  }
+  // rows_valid in [1, ROWS]; `g` points at the tile's first row.
+  __device__ __forceinline__ void stage(bf16* lds, const bf16* g, int64_t row_stride, int rows_valid, int wave,
+                                        int lane) const {
+    if (rows_valid >= ROWS) {
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        direct_load16(g + off[i], lds + lds_row0[i] * D);
+    } else {
+      stage_direct<ROWS, D, NW>(lds, g, row_stride, rows_valid, wave, lane);
+    }
+  }
+};
+
+// Wait for this wave's outstanding global loads (including direct-to-LDS
+// ones); a following barrier makes every wave's tile visible.
+__device__ __forceinline__ void wait_vmem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 }  // namespace avattn
