@@ -35,9 +35,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_f32,
          c_ptr, c_i64p,
          c_ptr,
+         c_ptr, c_size,
          c_ptr],
     ),
-    "avattn_bwd_workspace_size": (c_size, [c_i32, c_i32, c_i32]),
+    "avattn_fwd_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32]),
+    "avattn_bwd_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "avattn_bwd": (
         ctypes.c_int,
         [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
@@ -144,6 +146,7 @@ KERNEL_IDS = {
     "lse_merge": 4,
     "rope_apply": 5,
     "rope_tables": 6,
+    "transpose": 7,
 }
 
 

@@ -1,17 +1,21 @@
 // Flash-style attention forward for gfx950: one workgroup = 128 query rows of
-// one (batch, head); four waves own 32 rows each; K/V stream through LDS in
-// 64-key row-major tiles, double-buffered (V^T operands come from LDS
-// transpose reads).
+// one (batch, head); four waves own 32 rows each; K streams through LDS in
+// 64-key row-major tiles and V in 64-key head_dim-major tiles (from the
+// padded copies made by prep.hip), double-buffered.
 //
 // Per wave and tile the scores are computed transposed, S^T = K Q^T, so that
 // each lane owns one query column (query = lane % 32) and holds 32 of that
 // query's 64 scores: the row max and row sum are in-lane plus one exchange
-// with the partner lane (lane ^ 32).  The probabilities, in the MFMA C
-// layout, are exactly the B operand of O^T += V^T P^T, so P never leaves
-// registers.  Q stays in registers for the whole kernel (optionally rotated
-// on load, src/avgen/models/rope.py:332-338).  Softmax runs in the exp2
-// domain on raw scores with a running max; the LSE is natural-log
+// with the partner lane (lane ^ 32).  Lane l reads K row perm23(l % 32) of
+// each 32-key half, so the probabilities in the MFMA C layout are exactly the
+// B operand of O^T += V^T P^T with eight consecutive keys per k slot group,
+// and the matching V^T operand is one 16-byte LDS read.  P never leaves
+// registers.  Q stays in registers for the whole kernel (optionally rotated on
+// load, src/avgen/models/rope.py:332-338).  Softmax runs in the exp2 domain on
+// raw scores with a running max; the LSE is natural-log
 // (aten::_scaled_dot_product_flash_attention's logsumexp output).
+#include <type_traits>
+
 #include "avattn_device.h"
 #include "avattn_kernels.h"
 
@@ -21,24 +25,30 @@ namespace avattn {
 //
 // Per tile the waves issue both 32-key halves' QK^T MFMAs, then run each
 // half's softmax on the VALU while the other half's MFMAs (QK^T of half 1,
-// then PV of half 0) execute.  K and V are double-buffered in LDS: right
-// after the barrier that opens iteration t, tile t+1 is loaded straight from
-// global memory into buffer (t+1)%2 (tile t-1 was fully consumed before that
-// barrier) and lands before the next one.  One barrier per tile.
-template <int D, bool MASK, bool ROPE>
+// then PV of half 0) execute.  K rows and V^T come from padded copies and are
+// double-buffered in LDS: right after the barrier that opens iteration t,
+// tile t+1 is loaded straight from global memory into the other buffer (tile
+// t-1 was fully consumed before that barrier) and lands before the next one.
+// The loop body is branch-free apart from the masked-tile bias, and unrolled
+// over the two buffers so LDS addresses are per-lane bases plus immediates.
+template <int D, bool ROPE>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   constexpr int BM = 128, BN = 64, NW = 4;
   constexpr int KS = D / 16;  // 16-channel k-steps of q k^T
   constexpr int DT = D / 32;  // 32-channel row tiles of O^T
   constexpr int TE = BN * D;  // tile elements
-  __shared__ __attribute__((aligned(16))) bf16 sk[2][TE];
-  __shared__ __attribute__((aligned(16))) bf16 sv[2][TE];
-  __shared__ __attribute__((aligned(16))) float sbias[2][BN];
-  __shared__ int sfull[2];
+  // Each buffer of the double-buffered tiles is its own LDS object: the
+  // compiler then knows that the direct global->LDS loads into one buffer do
+  // not alias the LDS reads of the other, and does not wait for the next
+  // tile's loads before reading the current one.
+  __shared__ __attribute__((aligned(16))) bf16 sk0[TE], sk1[TE];    // K rows: TileLayout<D>
+  __shared__ __attribute__((aligned(16))) bf16 svt0[TE], svt1[TE];  // V^T rows (channel-major): TileLayout<BN>
+  __shared__ __attribute__((aligned(16))) float sb0[BN], sb1[BN];   // key bias
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
+  const int prow = perm23(l32);  // K row this lane supplies to S^T = K Q^T
 
   const int nqt = (a.Lq + BM - 1) / BM;
   const int total = nqt * a.B * a.Hq;
@@ -51,36 +61,33 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   const int qrow = qt * BM + wave * 32 + l32;
   const bool qvalid = qrow < a.Lq;
 
-  const bf16* kbase = a.k + b * a.ksb + hk * a.ksh;
-  const bf16* vbase = a.v + b * a.vsb + hk * a.vsh;
-  const uint8_t* mbase = MASK ? a.mask + b * a.msb : nullptr;
-  const int nkt = (a.Lk + BN - 1) / BN;
+  const int64_t bhk = (int64_t)(b * a.Hkv + hk);
+  const bf16* krbase = a.kr + bhk * a.Lkp * D;
+  const bf16* vtbase = a.vt + bhk * D * a.Lkp;
+  const float* kbias = a.kbias + (int64_t)b * a.Lkp;
+  const int* kfull = a.kfull + (int64_t)b * (a.Lkp / 32);
+  const int nkt = a.Lkp / BN;
 
-  DirectStager<BN, D, NW> kst, vst;
-  kst.init(a.ksl, wave, lane);
-  vst.init(a.vsl, wave, lane);
-  // Key bias of tile t (0 or -inf) into sbias[t & 1]; wave 0 only.
-  float bias_reg = 0.f;
-  auto load_bias = [&](int t) {
-    if (wave == 0) {
-      const int key = t * BN + lane;
-      bool valid = key < a.Lk;
-      if (MASK && valid) valid = mbase[key] != 0;
-      bias_reg = valid ? 0.f : kNegInf;
-    }
-  };
-  auto store_bias = [&](int t) {
-    if (wave == 0) {
-      sbias[t & 1][lane] = bias_reg;
-      const unsigned long long ball = __ballot(bias_reg == 0.f);
-      if (lane == 0) sfull[t & 1] = (ball == ~0ull) ? 1 : 0;
-    }
+  DirectStager<BN, D, NW> kst;  // 64 K rows of D channels (row stride D)
+  DirectStager<D, BN, NW> vst;  // D V^T rows of 64 keys (row stride Lkp)
+  kst.init(D, wave, lane);
+  vst.init(a.Lkp, wave, lane);
+  // Stages tile t into one buffer and loads its two 32-key "all attended"
+  // flags into registers (consumed one iteration later, after the wait that
+  // covers the tile: a flag load issued mid-iteration would otherwise make
+  // its use wait for every tile load issued before it).
+  int full_next0 = 1, full_next1 = 1;
+  auto stage = [&](int t, bf16* lk, bf16* lvt, float* lb) {
+    const int k0 = t * BN;
+    full_next0 = kfull[2 * t];
+    full_next1 = kfull[2 * t + 1];
+    kst.stage_full(lk, krbase + (int64_t)k0 * D, wave);
+    vst.stage_full(lvt, vtbase + k0, wave);
+    direct_load4(kbias + k0 + lane, lb);
   };
 
   // Prologue loads, then Q (rotated on load) while they fly.
-  kst.stage(sk[0], kbase, a.ksl, min(BN, a.Lk), wave, lane);
-  vst.stage(sv[0], vbase, a.vsl, min(BN, a.Lk), wave, lane);
-  load_bias(0);
+  stage(0, sk0, svt0, sb0);
 
   // Q fragments: B operand of S^T = K Q^T; lane holds row qrow, channels
   // 16*ks + 8*hh + [0, 8).
@@ -103,14 +110,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
     }
   }
 
-  // S^T of one 32-key half of a tile: s[r] is the score of key
-  // 32*half + 8*(r/4) + 4*hh + r%4 against this lane's query.
-  auto scores = [&](const bf16* kl, int half) {
-    f32x16 s = zero16();
+  // Loop-invariant per-lane LDS element offsets.
+  int ko[KS];  // K row perm23(l32), chunk 16*ks + 8*hh
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) s = mfma32(row_operand<D>(kl, half * 32 + l32, 16 * ks + 8 * hh), qf[ks], s);
-    return s;
-  };
+  for (int ks = 0; ks < KS; ++ks) ko[ks] = TileLayout<D>::off(prow, 16 * ks + 8 * hh);
+  int vo[4];  // V^T row l32 (+32*dt), key chunk 16*j + 8*hh (j = 2*half + k2)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) vo[j] = TileLayout<BN>::off(l32, 16 * j + 8 * hh);
 
   const float c = a.scale_log2;
   // Lazy rescaling: the reference max m_run only moves when a half-tile's
@@ -124,36 +130,39 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = zero16();
 
-  wait_vmem();
-  store_bias(0);
-
-  for (int t = 0; t < nkt; ++t) {
-    const int buf = t & 1;
+  auto body = [&](int t, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
     wait_vmem();
-    __syncthreads();  // K(t), V(t), bias(t) visible; tile t-1 fully consumed everywhere
-    if (t + 1 < nkt) {
-      const int k1 = (t + 1) * BN;
-      kst.stage(sk[buf ^ 1], kbase + (int64_t)k1 * a.ksl, a.ksl, min(BN, a.Lk - k1), wave, lane);
-      vst.stage(sv[buf ^ 1], vbase + (int64_t)k1 * a.vsl, a.vsl, min(BN, a.Lk - k1), wave, lane);
-      load_bias(t + 1);
-    }
-    const bf16* kl = sk[buf];
-    const bf16* vl = sv[buf];
-    const bool full = sfull[buf] != 0;
+    __syncthreads();  // tile t visible in `buf`; tile t-1 fully consumed everywhere
+    const int full[2] = {__builtin_amdgcn_readfirstlane(full_next0), __builtin_amdgcn_readfirstlane(full_next1)};
+    // the last iteration re-stages a tile nobody reads
+    if constexpr (buf == 0)
+      stage(min(t + 1, nkt - 1), sk1, svt1, sb1);
+    else
+      stage(min(t + 1, nkt - 1), sk0, svt0, sb0);
+    const bf16* kl = buf == 0 ? sk0 : sk1;
+    const bf16* vl = buf == 0 ? svt0 : svt1;
+    const float* bl = buf == 0 ? sb0 : sb1;
 
-    // Both halves' QK^T MFMAs are issued up front; the softmax of half 0
-    // then runs on the VALU while half 1's MFMAs execute, and the softmax of
-    // half 1 while half 0's PV MFMAs execute.
+    // S^T of both 32-key halves: sh[half][8*k2 + e] is the score of key
+    // 32*half + 16*k2 + 8*hh + e against this lane's query.
     f32x16 sh[2];
-    sh[0] = scores(kl, 0);
-    sh[1] = scores(kl, 1);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      bf16x8 ka[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const bf16x8*>(kl + hf * 32 * D + ko[ks]);
+      sh[hf] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sh[hf] = mfma32(ka[ks], qf[ks], sh[hf]);
+    }
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       f32x16& s_cur = sh[hf];
-      if (!full) {
+      if (!full[hf]) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 bb = *reinterpret_cast<const f32x4*>(&sbias[buf][hf * 32 + 8 * g + 4 * hh]);
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(bl + hf * 32 + 16 * (g >> 1) + 8 * hh + 4 * (g & 1));
 #pragma unroll
           for (int r = 0; r < 4; ++r) s_cur[4 * g + r] += bb[r];
         }
@@ -194,16 +203,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
       }
 
       // O^T += V^T P^T.  B operand slot (hh, e) of pf[k2] is key
-      // 32*hf + 16*k2 + 8*(e/4) + 4*hh + e%4; tr_operand reads V^T in that
-      // key order from the row-major V tile.
+      // 32*hf + 16*k2 + 8*hh + e: one 16-byte chunk of a V^T row.
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          acc[dt] = mfma32(tr_operand<D>(vl, hf * 32 + 16 * k2, dt * 32, lane), pf[k2], acc[dt]);
+          acc[dt] = mfma32(*reinterpret_cast<const bf16x8*>(vl + dt * 32 * BN + vo[2 * hf + k2]), pf[k2], acc[dt]);
     }
+  };
 
-    if (t + 1 < nkt) store_bias(t + 1);
+  for (int t = 0; t < nkt; t += 2) {
+    body(t, std::integral_constant<int, 0>());
+    if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());
   }
 
   const float l_tot = halves_sum(l_run0 + l_run1);
@@ -244,20 +255,21 @@ __global__ void attn_empty_kernel(bf16* o, int64_t osb, int64_t osh, int64_t osl
 
 template <int D>
 static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
+  {
+    LaunchTimer timer(kKidTranspose, stream);
+    hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
+    if (e == hipSuccess) e = launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream);
+    if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, nullptr, a.vt, stream);
+    if (e != hipSuccess) return e;
+  }
   const int nqt = (a.Lq + 127) / 128;
   const dim3 grid(nqt * a.B * a.Hq);
   const dim3 block(256);
-  const bool mask = a.mask != nullptr;
-  const bool rope = a.cos_q != nullptr;
   LaunchTimer timer(kKidFwd, stream);
-  if (mask && rope)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, true, true>), grid, block, 0, stream, a);
-  else if (mask)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, true, false>), grid, block, 0, stream, a);
-  else if (rope)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false, true>), grid, block, 0, stream, a);
+  if (a.cos_q != nullptr)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, true>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

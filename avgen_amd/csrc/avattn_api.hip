@@ -33,6 +33,59 @@ int check_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32
 
 int launch_status(hipError_t e) { return e == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH; }
 
+size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Key bias (B, Lkp) floats plus a 64-float tail pad (tile loads read 64
+// biases from a 32-key tile start), and per-32-key-tile flags (B, Lkp/32).
+size_t kbias_bytes(int32_t B, size_t Lkp) { return round256(((size_t)B * Lkp + 64) * sizeof(float)); }
+size_t kfull_bytes(int32_t B, size_t Lkp) { return round256((size_t)B * (Lkp / 32) * sizeof(int)); }
+
+// Forward workspace: [k rows | v^T | key bias | key tile flags], each region
+// 256-byte aligned.
+struct FwdWorkspace {
+  size_t kr, vt, kbias, kfull, total;
+};
+
+FwdWorkspace fwd_workspace(int32_t B, int32_t Hkv, int32_t Lk, int32_t D) {
+  FwdWorkspace w{};
+  const size_t Lkp = transpose_padded_len(Lk);
+  const size_t kcopy = round256((size_t)B * Hkv * D * Lkp * sizeof(bf16));
+  w.kr = 0;
+  w.vt = w.kr + kcopy;
+  w.kbias = w.vt + kcopy;
+  w.kfull = w.kbias + kbias_bytes(B, Lkp);
+  w.total = w.kfull + kfull_bytes(B, Lkp);
+  return w;
+}
+
+// Backward workspace: [lse2 | ndelta | q rows | dout rows | q^T | dout^T |
+// k rows | v rows | k^T | key bias | key tile flags], each region 256-byte
+// aligned.
+struct BwdWorkspace {
+  size_t lse2, ndelta, qr, dor, qt, dot, kr, vr, kt, kbias, kfull, total;
+};
+
+BwdWorkspace bwd_workspace(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32_t D) {
+  BwdWorkspace w{};
+  const size_t Lqp = transpose_padded_len(Lq), Lkp = transpose_padded_len(Lk);
+  const size_t stats = round256((size_t)B * Hq * Lqp * sizeof(float));
+  const size_t qcopy = round256((size_t)B * Hq * D * Lqp * sizeof(bf16));
+  const size_t kcopy = round256((size_t)B * Hkv * D * Lkp * sizeof(bf16));
+  w.lse2 = 0;
+  w.ndelta = w.lse2 + stats;
+  w.qr = w.ndelta + stats;
+  w.dor = w.qr + qcopy;
+  w.qt = w.dor + qcopy;
+  w.dot = w.qt + qcopy;
+  w.kr = w.dot + qcopy;
+  w.vr = w.kr + kcopy;
+  w.kt = w.vr + kcopy;
+  w.kbias = w.kt + kcopy;
+  w.kfull = w.kbias + kbias_bytes(B, Lkp);
+  w.total = w.kfull + kfull_bytes(B, Lkp);
+  return w;
+}
+
 }  // namespace
 
 extern "C" {
@@ -47,7 +100,9 @@ const char* avattn_strerror(int status) {
     case AVATTN_ERR_LAYOUT:
       return "misaligned tensor: pointers must be 16-byte aligned, head_dim contiguous and "
              "batch/head/seq strides multiples of 8 elements";
-    case AVATTN_ERR_WORKSPACE: return "workspace missing or smaller than avattn_bwd_workspace_size()";
+    case AVATTN_ERR_WORKSPACE:
+      return "workspace missing, misaligned or smaller than avattn_fwd_workspace_size() / "
+             "avattn_bwd_workspace_size()";
     case AVATTN_ERR_LAUNCH: return "HIP kernel launch failed";
     case AVATTN_ERR_TOO_LARGE: return "problem size exceeds the 32-bit grid/index range";
     case AVATTN_ERR_ARGUMENT: return "invalid argument";
@@ -55,13 +110,14 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 1; }
+int avattn_abi_version(void) { return 2; }
 
 int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_strides, const int64_t* k_strides,
                const int64_t* v_strides, int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
                int32_t len_k, int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
                const float* rope_cos_q, const float* rope_sin_q, int64_t rope_batch_stride, float scale, void* out,
-               const int64_t* out_strides, float* lse, avattn_stream_t stream) {
+               const int64_t* out_strides, float* lse, void* workspace, size_t workspace_bytes,
+               avattn_stream_t stream) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (st != AVATTN_OK) return st;
   if (!q_strides || !k_strides || !v_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
@@ -81,6 +137,8 @@ int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_str
   if (rope_cos_q && (!aligned16(rope_cos_q) || !aligned16(rope_sin_q) || rope_batch_stride % 4 != 0))
     return AVATTN_ERR_LAYOUT;
   if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
+  const size_t need = avattn_fwd_workspace_size(batch, heads_kv, len_k, head_dim);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
   FwdArgs a;
   a.q = static_cast<const bf16*>(q);
@@ -100,12 +158,25 @@ int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_str
   a.o = static_cast<bf16*>(out);
   a.osb = out_strides[0]; a.osh = out_strides[1]; a.osl = out_strides[2];
   a.lse = lse;
+  const FwdWorkspace wl = fwd_workspace(batch, heads_kv, len_k, head_dim);
+  char* ws = static_cast<char*>(workspace);
+  a.kr = reinterpret_cast<bf16*>(ws + wl.kr);
+  a.vt = reinterpret_cast<bf16*>(ws + wl.vt);
+  a.kbias = reinterpret_cast<float*>(ws + wl.kbias);
+  a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
+  a.Lkp = transpose_padded_len(len_k);
   return launch_status(launch_fwd(a, head_dim, s));
 }
 
-size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q) {
-  if (batch <= 0 || heads_q <= 0 || len_q <= 0) return 0;
-  return (size_t)2 * (size_t)batch * (size_t)heads_q * (size_t)len_q * sizeof(float);
+size_t avattn_fwd_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k, int32_t head_dim) {
+  if (batch <= 0 || heads_kv <= 0 || len_k <= 0 || head_dim <= 0) return 0;
+  return fwd_workspace(batch, heads_kv, len_k, head_dim).total;
+}
+
+size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
+                                 int32_t head_dim) {
+  if (batch <= 0 || heads_q <= 0 || heads_kv <= 0 || len_q <= 0 || len_k <= 0 || head_dim <= 0) return 0;
+  return bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim).total;
 }
 
 int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out, const float* lse,
@@ -149,8 +220,8 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
       !strides_ok(out_strides))
     return AVATTN_ERR_LAYOUT;
   if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
-  const size_t need = avattn_bwd_workspace_size(batch, heads_q, len_q);
-  if (!workspace || workspace_bytes < need || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
+  const BwdWorkspace wl = bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (!workspace || workspace_bytes < wl.total || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
   BwdArgs a;
   a.dout = static_cast<const bf16*>(dout);
@@ -175,9 +246,20 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   a.dksb = dk_strides[0]; a.dksh = dk_strides[1]; a.dksl = dk_strides[2];
   a.dv = static_cast<bf16*>(dv);
   a.dvsb = dv_strides[0]; a.dvsh = dv_strides[1]; a.dvsl = dv_strides[2];
-  const int64_t rows = (int64_t)batch * heads_q * len_q;
-  a.delta = static_cast<float*>(workspace);
-  a.lse2 = static_cast<float*>(workspace) + rows;
+  char* ws = static_cast<char*>(workspace);
+  a.lse2 = reinterpret_cast<float*>(ws + wl.lse2);
+  a.ndelta = reinterpret_cast<float*>(ws + wl.ndelta);
+  a.qr = reinterpret_cast<bf16*>(ws + wl.qr);
+  a.dor = reinterpret_cast<bf16*>(ws + wl.dor);
+  a.qt = reinterpret_cast<bf16*>(ws + wl.qt);
+  a.dot = reinterpret_cast<bf16*>(ws + wl.dot);
+  a.kr = reinterpret_cast<bf16*>(ws + wl.kr);
+  a.vr = reinterpret_cast<bf16*>(ws + wl.vr);
+  a.kt = reinterpret_cast<bf16*>(ws + wl.kt);
+  a.kbias = reinterpret_cast<float*>(ws + wl.kbias);
+  a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
+  a.Lqp = transpose_padded_len(len_q);
+  a.Lkp = transpose_padded_len(len_k);
   return launch_status(launch_bwd(a, head_dim, s));
 }
 

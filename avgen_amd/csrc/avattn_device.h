@@ -135,131 +135,71 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 // ---------------------------------------------------------------------------
 // LDS tile layout
 // ---------------------------------------------------------------------------
-// Row-major ROWS x D bf16 tile with unpadded rows whose 16-byte chunks are
-// XOR-swizzled: chunk c of row r sits at chunk slot c ^ f(r).
-//   D == 128 (256-byte rows): f(r) = 4*(r%4) + (r/4)%4
-//   D == 64  (128-byte rows): f(r) = 4*((r/2)%2) + (r/4)%4
-// With these, sixteen lanes reading one chunk of 16 consecutive rows
-// (ds_read_b128) and the 32 lanes of a transpose read (4 rows x 64
-// contiguous bytes, see tr_operand) each touch all 64 banks exactly once,
-// and a 1 KB block of consecutive rows can be filled by one direct
-// global->LDS wave load (stage_direct).
-template <int D>
+// Row-major tile of RL-element (2*RL-byte) bf16 rows, unpadded, whose
+// 16-byte chunks are XOR-swizzled: chunk c of row r sits at chunk slot
+// c ^ f(r).
+//   RL == 128 (256-byte rows): f(r) = 4*(r%4) + (r/4)%4
+//   RL == 64  (128-byte rows): f(r) = 4*((r/2)%2) + (r/4)%4
+//   RL == 32  ( 64-byte rows): f(r) = (r/4)%4
+// With these, sixteen lanes reading one chunk each of 16 distinct rows in an
+// aligned group of 16 (ds_read_b128) touch all 64 banks exactly once, and a
+// 1 KB block of consecutive rows can be filled by one direct global->LDS
+// wave load (stage_direct).  Row-major sequence tiles use RL = head_dim;
+// head_dim-major ("transposed") tiles use RL = the tile's sequence length.
+template <int RL>
 struct TileLayout {
-  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  static constexpr int kRowElems = D;
+  static_assert(RL == 32 || RL == 64 || RL == 128, "row length 32, 64 or 128 elements");
+  static constexpr int kRowElems = RL;
   static __device__ __forceinline__ int swz(int row) {
-    return D == 128 ? (((row & 3) << 2) | ((row >> 2) & 3)) : ((((row >> 1) & 1) << 2) | ((row >> 2) & 3));
+    if constexpr (RL == 128) return ((row & 3) << 2) | ((row >> 2) & 3);
+    if constexpr (RL == 64) return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
+    return (row >> 2) & 3;
   }
   // Element offset of (row, col); col must be a multiple of 4.
   static __device__ __forceinline__ int off(int row, int col) {
-    return row * D + (((col >> 3) ^ swz(row)) << 3) + (col & 7);
+    return row * RL + (((col >> 3) ^ swz(row)) << 3) + (col & 7);
   }
 };
 
-// ---------------------------------------------------------------------------
-// Transposed MFMA operand from a row-major LDS tile (ds_read_b64_tr_b16).
-// ---------------------------------------------------------------------------
-// ds_read_b64_tr_b16, per group of 16 lanes: lane i of the group receives
-// element i%4 of the 8-byte chunks addressed by the group's lanes i/4 + 4j,
-// j = 0..3.  So if lane s addresses row r0 + s/4, column c0 + 4*(s%4), lane i
-// receives rows r0..r0+3 of column c0 + i: four consecutive rows of one
-// column, i.e. an MFMA operand along the row dimension.
-//
-// tr_operand returns the 32x32x16 A (or B) operand X^T[m][k] for m = column
-// c0 + lane%32 and k slot (hh, e) <-> row r0 + 8*(e/4) + 4*hh + e%4 of a
-// row-major TileLayout<D> tile X — the same k-slot order as the C layout of
-// a 32x32 MFMA output, so the result pairs with a B (A) operand built from
-// such an output.
-template <int D>
-__device__ __forceinline__ bf16x8 tr_operand(const bf16* tile, int r0, int c0, int lane) {
-  typedef short s16x4 __attribute__((ext_vector_type(4)));
-  const int g = lane >> 4, s = lane & 15;
-  const int row = r0 + 4 * (g >> 1) + (s >> 2);
-  const int col = c0 + 16 * (g & 1) + 4 * (s & 3);
-  const bf16* plo = tile + TileLayout<D>::off(row, col);
-  const bf16* phi = tile + TileLayout<D>::off(row + 8, col);
-  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(plo));
-  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(phi));
-  u32x4 u;
-  u[0] = __builtin_bit_cast(u32x2, lo)[0];
-  u[1] = __builtin_bit_cast(u32x2, lo)[1];
-  u[2] = __builtin_bit_cast(u32x2, hi)[0];
-  u[3] = __builtin_bit_cast(u32x2, hi)[1];
-  return __builtin_bit_cast(bf16x8, u);
-}
+// Row index permutation that swaps bits 2 and 3 (an involution on 0..15 in
+// every aligned group of 16).  When lane l supplies row perm23(l % 32) of a
+// 32-row MFMA operand, the C-layout registers 8*k2 + e of lane l hold rows
+// 16*k2 + 8*(l/32) + e, e = 0..7: eight *consecutive* rows per 16-row k-step,
+// which is exactly the k order of an A (or B) operand read as one 16-byte
+// chunk from a transposed (sequence-contiguous) tile.
+__device__ __forceinline__ int perm23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
-// Row operand (8 consecutive channels of one row) from a TileLayout<D> tile.
-template <int D>
+// 8 consecutive elements (one 16-byte chunk) of one row of a TileLayout<RL>
+// tile: an MFMA operand whose k index runs along the row.
+template <int RL>
 __device__ __forceinline__ bf16x8 row_operand(const bf16* tile, int row, int col) {
-  return *reinterpret_cast<const bf16x8*>(tile + TileLayout<D>::off(row, col));
+  return *reinterpret_cast<const bf16x8*>(tile + TileLayout<RL>::off(row, col));
 }
-
-// ---------------------------------------------------------------------------
-// Tile staging: global (row-major, head_dim contiguous) -> registers -> LDS.
-// The register step lets a kernel issue the global loads of tile t+1 before
-// computing on tile t.
-// ---------------------------------------------------------------------------
-
-// ROWS x D tile staged by NT threads as 16-byte chunks into TileLayout<D>.
-// Loads are unconditional (rows past the end re-read the last valid row) so
-// the compiler emits one uninterrupted batch of global loads; the rows past
-// the end become zeros when stored, by which time the data has arrived.
-template <int ROWS, int D, int NT>
-struct RowTile {
-  static constexpr int kElems = ROWS * TileLayout<D>::kRowElems;  // LDS size
-  static constexpr int kChunks = ROWS * D / 8;
-  static constexpr int kPer = (kChunks + NT - 1) / NT;
-  u32x4 reg[kPer];
-  int rows_valid_;
-
-  // rows_valid >= 1.
-  __device__ __forceinline__ void load(const bf16* base, int64_t row_stride, int rows_valid, int tid) {
-    rows_valid_ = rows_valid;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = tid + i * NT;
-      if (kChunks % NT == 0 || c < kChunks) {
-        const int row = min(c / (D / 8), rows_valid - 1);
-        reg[i] = *reinterpret_cast<const u32x4*>(base + (int64_t)row * row_stride + (c % (D / 8)) * 8);
-      }
-    }
-  }
-  __device__ __forceinline__ void store(bf16* lds, int tid) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int c = tid + i * NT;
-      if (kChunks % NT == 0 || c < kChunks) {
-        const int row = c / (D / 8);
-        const int col = (c % (D / 8)) * 8;
-        const bool in = row < rows_valid_;
-        u32x4 v;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) v[w] = in ? reg[i][w] : 0u;
-        *reinterpret_cast<u32x4*>(lds + TileLayout<D>::off(row, col)) = v;
-      }
-    }
-  }
-};
 
 // 16 bytes per lane from global memory straight into LDS at
 // lds_block + 16*lane (global_load_lds_dwordx4; lds_block is wave-uniform).
-__device__ __forceinline__ void direct_load16(const bf16* src, bf16* lds_block) {
+__device__ __forceinline__ void direct_load16(const void* src, void* lds_block) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
 }
 
-// Direct global->LDS staging of a ROWS x D tile into TileLayout<D> with
+// 4 bytes per lane from global memory straight into LDS at lds_block + 4*lane.
+__device__ __forceinline__ void direct_load4(const void* src, void* lds_block) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_block, 4, 0, 0);
+}
+
+// Direct global->LDS staging of a ROWS x RL tile (global rows of RL
+// contiguous bf16 at `row_stride` elements) into TileLayout<RL> with
 // global_load_lds_dwordx4.  One wave instruction moves 1 KB: lane j's 16
-// bytes land at LDS block base + 16*j, i.e. row row0 + j/(D/8), chunk slot
-// j%(D/8); the lane therefore loads the logical chunk the swizzle maps to
+// bytes land at LDS block base + 16*j, i.e. row row0 + j/(RL/8), chunk slot
+// j%(RL/8); the lane therefore loads the logical chunk the swizzle maps to
 // that slot.  Rows at or past rows_valid (>= 1) re-read row rows_valid-1:
 // callers never use those rows unmasked.  The NW waves of a workgroup split
 // the tile's instructions; completion is tracked by vmcnt (callers wait with
 // vmcnt(0) and a barrier before reading).
-template <int ROWS, int D, int NW>
+template <int ROWS, int RL, int NW>
 __device__ __forceinline__ void stage_direct(bf16* lds, const bf16* g, int64_t row_stride, int rows_valid, int wave,
                                              int lane) {
-  constexpr int kCpr = D / 8;       // 16-byte chunks per row
+  constexpr int kCpr = RL / 8;      // 16-byte chunks per row
   constexpr int kRpi = 64 / kCpr;   // rows per wave instruction
   constexpr int kNi = ROWS / kRpi;  // instructions per tile
   static_assert(kNi % NW == 0, "tile must split evenly over the waves");
@@ -267,44 +207,46 @@ __device__ __forceinline__ void stage_direct(bf16* lds, const bf16* g, int64_t r
   for (int i = 0; i < kNi / NW; ++i) {
     const int row0 = (wave * (kNi / NW) + i) * kRpi;
     const int row = row0 + lane / kCpr;
-    const int chunk = (lane % kCpr) ^ TileLayout<D>::swz(row);
+    const int chunk = (lane % kCpr) ^ TileLayout<RL>::swz(row);
     const int srow = min(row, rows_valid - 1);
-    direct_load16(g + (int64_t)srow * row_stride + chunk * 8, lds + row0 * D);
+    direct_load16(g + (int64_t)srow * row_stride + chunk * 8, lds + row0 * RL);
   }
 }
 
 // stage_direct with the per-lane source offsets precomputed (they depend only
 // on the lane, the wave and the row stride): for full tiles each load is a
 // uniform tile base plus a 32-bit lane offset, with no per-tile address math.
-template <int ROWS, int D, int NW>
+// The row stride times ROWS must fit in 31 bits.
+template <int ROWS, int RL, int NW>
 struct DirectStager {
-  static constexpr int kCpr = D / 8;
+  static constexpr int kCpr = RL / 8;
   static constexpr int kRpi = 64 / kCpr;
   static constexpr int kNi = ROWS / kRpi;
   static constexpr int kPer = kNi / NW;
   static_assert(kNi % NW == 0, "tile must split evenly over the waves");
   int off[kPer];  // element offset of this lane's source chunk, per instruction
-  int lds_row0[kPer];
 
   __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int row0 = (wave * kPer + i) * kRpi;
       const int row = row0 + lane / kCpr;
-      off[i] = (int)(row * row_stride) + ((lane % kCpr) ^ TileLayout<D>::swz(row)) * 8;
-      lds_row0[i] = row0;
+      off[i] = (int)(row * row_stride) + ((lane % kCpr) ^ TileLayout<RL>::swz(row)) * 8;
     }
   }
-  // rows_valid in [1, ROWS]; `g` points at the tile's first row.
+  __device__ __forceinline__ static int lds_row0(int i, int wave) { return (wave * kPer + i) * kRpi; }
+  // Every row valid; `g` points at the tile's first row.
+  __device__ __forceinline__ void stage_full(bf16* lds, const bf16* g, int wave) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) direct_load16(g + off[i], lds + lds_row0(i, wave) * RL);
+  }
+  // rows_valid in [1, ROWS].
   __device__ __forceinline__ void stage(bf16* lds, const bf16* g, int64_t row_stride, int rows_valid, int wave,
                                         int lane) const {
-    if (rows_valid >= ROWS) {
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-        direct_load16(g + off[i], lds + lds_row0[i] * D);
-    } else {
-      stage_direct<ROWS, D, NW>(lds, g, row_stride, rows_valid, wave, lane);
-    }
+    if (rows_valid >= ROWS)
+      stage_full(lds, g, wave);
+    else
+      stage_direct<ROWS, RL, NW>(lds, g, row_stride, rows_valid, wave, lane);
   }
 };
 

@@ -27,6 +27,14 @@ struct FwdArgs {
   bf16* o;
   int64_t osb, osh, osl;
   float* lse;
+  // Padded copies (transpose.hip), written by the launcher: k rows, element
+  // (b, h, j, d) at ((b*Hkv + h)*Lkp + j)*D + d; v head_dim-major, element
+  // (b, h, d, j) at ((b*Hkv + h)*D + d)*Lkp + j.
+  bf16* kr;
+  bf16* vt;
+  float* kbias;  // (B, Lkp): 0 attended / -inf
+  int* kfull;    // (B, Lkp/32): 1 if every key of the 32-key tile is attended
+  int Lkp;
 };
 
 struct BwdArgs {
@@ -52,9 +60,23 @@ struct BwdArgs {
   int64_t dksb, dksh, dksl;
   bf16* dv;
   int64_t dvsb, dvsh, dvsl;
-  // Workspace: per query row (b, hq, i) at index (b*Hq + hq)*Lq + i.
-  float* delta;  // rowsum(dout * out)
-  float* lse2;   // lse * log2(e); +inf for rows with lse == -inf
+  // Workspace (written by the launcher's first kernels).
+  // Per query row (b, hq, i) at index (b*Hq + hq)*Lqp + i, i < Lqp:
+  float* ndelta;  // -rowsum(dout * out); 0 for padded rows
+  float* lse2;    // lse * log2(e); +inf for rows with lse == -inf and padded rows
+  // Padded copies (transpose.hip) with H/Lp = Hq/Lqp (q, dout) or Hkv/Lkp
+  // (k, v): row copies (*r) hold element (b, h, j, d) at ((b*H + h)*Lp + j)*D
+  // + d, head_dim-major copies (*t) at ((b*H + h)*D + d)*Lp + j.
+  bf16* qr;
+  bf16* dor;
+  bf16* qt;
+  bf16* dot;
+  bf16* kr;
+  bf16* vr;
+  bf16* kt;
+  float* kbias;  // (B, Lkp): 0 attended / -inf
+  int* kfull;    // (B, Lkp/32): 1 if every key of the 32-key tile is attended
+  int Lqp, Lkp;
 };
 
 // Kernel ids of the opt-in launch timer (avattn_timing_* in include/avattn.h).
@@ -66,6 +88,7 @@ enum KernelId : int {
   kKidMerge = 4,
   kKidRopeApply = 5,
   kKidRopeTables = 6,
+  kKidTranspose = 7,
 };
 
 // Records HIP events around one launch on `stream` while timing is enabled.
@@ -80,6 +103,20 @@ class LaunchTimer {
   int slot_;
   hipStream_t stream_;
 };
+
+// Sequence length of a head_dim-major copy (transpose.hip): padded to whole
+// 64-row tiles.
+inline int transpose_padded_len(int L) { return (L + 63) / 64 * 64; }
+
+// Padded key bias (B, Lkp) floats (0 attended / -inf) and per-32-key-tile
+// "all attended" flags (B, Lkp/32); mask may be null (only the tail is masked).
+hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, float* kbias, int* kfull,
+                           hipStream_t stream);
+
+// x (B, H, L, D) strided -> xr (B*H, Lp, D) and/or xt (B*H, D, Lp), contiguous,
+// zero padded to Lp = transpose_padded_len(L); either output may be null.
+hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
+                              bf16* xr, bf16* xt, hipStream_t stream);
 
 hipError_t launch_fwd(const FwdArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_empty(bf16* o, int64_t osb, int64_t osh, int64_t osl, int B, int H, int L, int D, float* lse,

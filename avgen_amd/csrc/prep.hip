@@ -1,0 +1,114 @@
+// Operand preparation for the attention kernels: padded copies of the
+// sequence tensors and the padded key bias.
+//
+// The attention kernels stream sequence tiles through LDS with direct
+// global->LDS loads.  Two kinds of copy of a (B, H, L, D) strided tensor are
+// made here, once per call, each padded with zeros to Lp = L rounded up to a
+// whole 64-row tile (transpose_padded_len), so that every tile load is a
+// full, branch-free load with loop-invariant per-lane offsets and padded
+// positions hold finite values:
+//   rows: xr[((b*H + h)*Lp + i)*D + d] = x[b, h, i, d]      (row-major)
+//   cols: xt[((b*H + h)*D + d)*Lp + i] = x[b, h, i, d]      (head_dim-major)
+// The head_dim-major copy serves the products that contract over the
+// sequence (O += P V, dV += P^T dO, dK += dS^T Q, dQ += dS K): their MFMA
+// operand then has its k index along a contiguous row and is one 16-byte LDS
+// read, instead of transpose reads, which run at a fraction of the rate on
+// gfx950.  Each copy is HBM-bound: one read of x, one write per copy.
+#include "avattn_device.h"
+#include "avattn_kernels.h"
+
+namespace avattn {
+
+// One workgroup copies 64 sequence rows x D channels of one (b, h).
+template <int D>
+__global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict__ x, int64_t sb, int64_t sh,
+                                                          int64_t sl, int H, int L, int Lp, bf16* __restrict__ xr,
+                                                          bf16* __restrict__ xt) {
+  constexpr int S = 64;       // sequence rows per workgroup
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  constexpr int LD = D + 2;   // LDS row pitch in bf16 (odd word count: column reads spread over banks)
+  __shared__ bf16 tile[S * LD];
+  const int tid = threadIdx.x;
+  const int ntiles = Lp / S;
+  const int s0 = (blockIdx.x % ntiles) * S;
+  const int bh = blockIdx.x / ntiles;
+  const int b = bh / H, h = bh % H;
+  const bf16* src = x + b * sb + h * sh;
+
+  // Load 64 rows (zeros past L) as 16-byte chunks; write the row-major copy
+  // and scatter into the pitched tile for the head_dim-major one.
+#pragma unroll
+  for (int i = 0; i < S * CPR / 256; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / CPR, ch = c % CPR;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (s0 + row < L) v = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + row) * sl + ch * 8);
+    if (xr) *reinterpret_cast<u32x4*>(xr + ((int64_t)bh * Lp + s0 + row) * D + ch * 8) = v;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(tile + row * LD + ch * 8);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) dst[w] = v[w];
+  }
+  if (!xt) return;
+  __syncthreads();
+
+  // Each thread writes 16-byte chunks of head_dim-major rows: 8 consecutive
+  // sequence positions of one channel.
+  bf16* dst = xt + (int64_t)bh * D * Lp + s0;
+#pragma unroll
+  for (int i = 0; i < D * (S / 8) / 256; ++i) {
+    const int c = tid + i * 256;
+    const int d = c / (S / 8), j = c % (S / 8);
+    u32x4 v;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint16_t lo = __builtin_bit_cast(uint16_t, tile[(8 * j + 2 * w) * LD + d]);
+      const uint16_t hi = __builtin_bit_cast(uint16_t, tile[(8 * j + 2 * w + 1) * LD + d]);
+      v[w] = (uint32_t)lo | ((uint32_t)hi << 16);
+    }
+    *reinterpret_cast<u32x4*>(dst + (int64_t)d * Lp + 8 * j) = v;
+  }
+}
+
+// Key bias and tile flags: kbias[b*Lkp + j] = 0 if key j < Lk is attended
+// (mask nonzero, or no mask) else -inf, for j < Lkp; kfull[b*(Lkp/32) + t] = 1
+// if all 32 keys of tile t are attended.  One thread per 32-key tile.
+__global__ __launch_bounds__(256) void key_prep_kernel(const uint8_t* __restrict__ mask, int64_t msb, int B, int Lk,
+                                                       int Lkp, float* __restrict__ kbias, int* __restrict__ kfull) {
+  const int tiles = Lkp / 32;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)B * tiles) return;
+  const int b = (int)(t / tiles), j0 = (int)(t % tiles) * 32;
+  int all = 1;
+  for (int j = j0; j < j0 + 32; ++j) {
+    const bool valid = j < Lk && (mask == nullptr || mask[b * msb + j] != 0);
+    kbias[(int64_t)b * Lkp + j] = valid ? 0.f : kNegInf;
+    all &= valid ? 1 : 0;
+  }
+  kfull[t] = all;
+}
+
+hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, float* kbias, int* kfull,
+                           hipStream_t stream) {
+  const int Lkp = transpose_padded_len(Lk);
+  const int64_t n = (int64_t)B * (Lkp / 32);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(key_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, mask, msb, B, Lk, Lkp,
+                     kbias, kfull);
+  return hipGetLastError();
+}
+
+hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
+                              bf16* xr, bf16* xt, hipStream_t stream) {
+  const int Lp = transpose_padded_len(L);
+  if ((int64_t)B * H == 0 || Lp == 0 || (!xr && !xt)) return hipSuccess;
+  const int64_t blocks = (int64_t)(Lp / 64) * B * H;
+  if (blocks > 2147483647) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks);
+  if (D == 128)
+    hipLaunchKernelGGL(prep_copies_kernel<128>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt);
+  else
+    hipLaunchKernelGGL(prep_copies_kernel<64>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt);
+  return hipGetLastError();
+}
+
+}  // namespace avattn

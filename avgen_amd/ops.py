@@ -55,6 +55,12 @@ def _strides3(t: torch.Tensor) -> ctypes.Array:
     return _lib.i64_array(t.stride()[:3])
 
 
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """Caller-owned scratch for one C-ABI call (torch's caching allocator; the
+    library itself never allocates).  Never empty, so its pointer is valid."""
+    return torch.empty(max(int(nbytes), 256), device=device, dtype=torch.uint8)
+
+
 def _require_gpu(name: str, *tensors: Optional[torch.Tensor]) -> None:
     for t in tensors:
         if t is not None and t.device.type != "cuda":
@@ -147,6 +153,7 @@ def _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale):
     out = _kernel_ready(out)
     lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32)
     lib = _lib.load()
+    ws = _workspace(lib.avattn_fwd_workspace_size(B, Hkv, Lk, D), q.device)
     st = lib.avattn_fwd(
         _ptr(q), _ptr(k), _ptr(v), _strides3(q), _strides3(k), _strides3(v),
         B, Hq, Hkv, Lq, Lk, D,
@@ -154,6 +161,7 @@ def _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale):
         _ptr(rope_cos), _ptr(rope_sin), rsb,
         float(scale),
         _ptr(out), _strides3(out), _ptr(lse),
+        _ptr(ws), ws.numel(),
         _stream(q.device),
     )
     _lib.check(st, name)
@@ -179,8 +187,7 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale):
     dk = _kernel_ready(torch.empty_like(k))
     dv = _kernel_ready(torch.empty_like(v))
     lib = _lib.load()
-    ws_bytes = lib.avattn_bwd_workspace_size(B, Hq, Lq)
-    ws = torch.empty(max(ws_bytes // 4, 4), device=q.device, dtype=torch.float32)
+    ws = _workspace(lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D), q.device)
     st = lib.avattn_bwd(
         _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
         _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
@@ -188,7 +195,7 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale):
         _ptr(mask), msb,
         float(scale),
         _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
-        _ptr(ws), ws.numel() * 4,
+        _ptr(ws), ws.numel(),
         _stream(q.device),
     )
     _lib.check(st, name)

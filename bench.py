@@ -332,7 +332,7 @@ def main() -> int:
         pmc_calibration(dev)
         log("[bench] calibration kernel done")
     per_kernel = {}
-    for name in ("attn_fwd", "bwd_dkdv", "bwd_dq", "bwd_preprocess", "lse_merge", "rope_apply"):
+    for name in ("attn_fwd", "bwd_dkdv", "bwd_dq", "bwd_preprocess", "lse_merge", "rope_apply", "transpose"):
         ms, n = timing.read(name)
         per_kernel[name] = {"total_ms": ms, "launches": n, "avg_ms": ms / n if n else 0.0}
     timing.close()

@@ -76,6 +76,8 @@ int avattn_abi_version(void);
  * b * rope_batch_stride + i * (head_dim/2) + p.
  * A zero len_q or len_k writes zeros to out (and -inf to lse) without a
  * compute launch (src/avgen/models/attention.py:261-262).
+ * workspace must hold avattn_fwd_workspace_size() bytes (16-byte aligned);
+ * it is scratch for this call only (padded copies of k and v, key bias).
  */
 int avattn_fwd(const void* q, const void* k, const void* v,
                const int64_t* q_strides, const int64_t* k_strides,
@@ -88,13 +90,25 @@ int avattn_fwd(const void* q, const void* k, const void* v,
                float scale,
                void* out, const int64_t* out_strides,
                float* lse,
+               void* workspace, size_t workspace_bytes,
                avattn_stream_t stream);
 
 /*
- * Workspace bytes avattn_bwd needs for these sizes (per-row softmax
- * statistics: 2 floats per query row).
+ * Workspace bytes avattn_fwd needs for these sizes: a row-major copy of k and
+ * a head_dim-major copy of v, sequences padded to a multiple of 64, plus the
+ * padded per-key bias and per-32-key flags (0 when there is nothing to do).
  */
-size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q);
+size_t avattn_fwd_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k, int32_t head_dim);
+
+/*
+ * Workspace bytes avattn_bwd needs for these sizes: two floats per query row
+ * (softmax statistics), row-major and head_dim-major copies of q and dout,
+ * row-major copies of k and v and a head_dim-major copy of k (sequences
+ * padded to multiples of 64), plus the padded per-key bias and per-32-key
+ * flags (0 when there is nothing to do).
+ */
+size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                 int32_t len_q, int32_t len_k, int32_t head_dim);
 
 /*
  * Backward of avattn_fwd with recomputation of the probabilities from
@@ -183,7 +197,8 @@ int avattn_rope_apply(const void* x, const int64_t* x_strides,
  * records a pair of HIP events on its launch stream; avattn_timing_read sums
  * the elapsed times of one kernel kind (it synchronizes on the recorded
  * events).  Kernel ids: 0 forward, 1 backward preprocess, 2 backward dK/dV,
- * 3 backward dQ, 4 LSE merge, 5 rotary apply, 6 rotary tables.
+ * 3 backward dQ, 4 LSE merge, 5 rotary apply, 6 rotary tables,
+ * 7 head_dim-major copies (forward and backward operand preparation).
  * avattn_timing_begin creates `capacity` event pairs (call it outside any
  * timed or captured region); launches beyond capacity are not recorded and
  * make avattn_timing_read return AVATTN_ERR_WORKSPACE.

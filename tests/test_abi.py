@@ -51,26 +51,53 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 1
+    assert lib.avattn_abi_version() == 2
     for code in range(0, 10):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
 
 
+def _round256(x: int) -> int:
+    return (x + 255) // 256 * 256
+
+
+def _pad64(n: int) -> int:
+    return (n + 63) // 64 * 64
+
+
+def _key_regions(B: int, lkp: int) -> int:
+    # key bias (B, Lkp) floats + a 64-float tail pad, then (B, Lkp/32) int flags
+    return _round256((B * lkp + 64) * 4) + _round256(B * (lkp // 32) * 4)
+
+
 def test_workspace_size(lib):
-    assert lib.avattn_bwd_workspace_size(2, 40, 18900) == 2 * 2 * 40 * 18900 * 4
-    assert lib.avattn_bwd_workspace_size(0, 40, 10) == 0
+    # Sequences pad to whole 64-row tiles: 18900 -> 18944; every region starts
+    # on a 256-byte boundary.
+    lp = _pad64(18900)
+    assert lp == 18944
+    copy = 2 * 40 * 128 * lp * 2  # one bf16 copy of a (2, 40, 18900, 128) tensor
+    stats = 2 * 40 * lp * 4
+    # backward: lse2 + ndelta, q/dout row + head_dim-major copies, k/v rows + k^T
+    assert lib.avattn_bwd_workspace_size(2, 40, 40, 18900, 18900, 128) == 2 * stats + 7 * copy + _key_regions(2, lp)
+    # GQA: k/v copies have heads_kv heads (len_k 70 pads to 128, len_q 10 to 64).
+    got = lib.avattn_bwd_workspace_size(1, 4, 2, 10, 70, 64)
+    assert got == 2 * (4 * 64 * 4) + 4 * (4 * 64 * 64 * 2) + 3 * (2 * 64 * 128 * 2) + _key_regions(1, 128)
+    assert lib.avattn_bwd_workspace_size(1, 1, 1, 1, 1, 64) == 2 * 256 + 7 * 64 * 64 * 2 + _key_regions(1, 64)
+    assert lib.avattn_bwd_workspace_size(0, 40, 40, 10, 10, 128) == 0
+    # forward: k rows + v^T copies of (B, Hkv, Lk, D), key bias/flags
+    assert lib.avattn_fwd_workspace_size(2, 8, 18900, 128) == 2 * (2 * 8 * 128 * lp * 2) + _key_regions(2, lp)
+    assert lib.avattn_fwd_workspace_size(1, 1, 0, 128) == 0
 
 
 def _fwd(lib, **over):
     s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
     args = dict(q=16, k=16, v=16, qs=s, ks=s, vs=s, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
-                cos=None, sin=None, rsb=0, scale=0.125, out=16, os=s, lse=16, stream=None)
+                cos=None, sin=None, rsb=0, scale=0.125, out=16, os=s, lse=16, ws=256, wsb=1 << 20, stream=None)
     args.update(over)
     return lib.avattn_fwd(args["q"], args["k"], args["v"], args["qs"], args["ks"], args["vs"], args["B"],
                           args["Hq"], args["Hkv"], args["Lq"], args["Lk"], args["D"], args["mask"], args["msb"],
                           args["cos"], args["sin"], args["rsb"], args["scale"], args["out"], args["os"],
-                          args["lse"], args["stream"])
+                          args["lse"], args["ws"], args["wsb"], args["stream"])
 
 
 @cpu_only
@@ -89,6 +116,9 @@ def test_fwd_validation_paths(lib):
     assert _fwd(lib, k=None) == _lib.ERR_NULL_POINTER
     assert _fwd(lib, mask=16, msb=2) == _lib.ERR_ARGUMENT
     assert _fwd(lib, B=1, Hq=1 << 30, Hkv=1, Lq=1 << 20) == _lib.ERR_TOO_LARGE
+    assert _fwd(lib, ws=None) == _lib.ERR_WORKSPACE
+    assert _fwd(lib, wsb=100) == _lib.ERR_WORKSPACE  # needs more than 2 * (2*128*64*2) bytes
+    assert _fwd(lib, ws=8) == _lib.ERR_WORKSPACE
     # empty problems succeed without any launch
     assert _fwd(lib, Lq=0) == _lib.OK
     assert _fwd(lib, B=0) == _lib.OK
