@@ -65,42 +65,52 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // 2. dK / dV
 // ---------------------------------------------------------------------------
-// Per wave: 32 keys (lane % 32 owns key column k0w + lane % 32).  For each
-// 32-row half `sub` of a 64-row query tile (lane l supplies query row
-// 32*sub + perm23(l % 32) to the first two products):
-//   S  = Q K^T    A = Q rows (LDS)              B = K^T (registers)
-//   dP = dO V^T   A = dO rows (LDS)             B = V^T (registers)
-//   P  = exp2(S*c - lse2[q]),  dS = P * (dP + ndelta[q])        (fp32)
-//   dV^T += dO^T P   A = dO^T (LDS, head_dim-major)   B = P  (C layout reused)
-//   dK^T += Q^T dS   A = Q^T  (LDS, head_dim-major)   B = dS (C layout reused)
+// One workgroup = 128 keys and 8 waves in two roles; waves w and w+4 own the
+// same 32 keys (lane % 32 owns key column kt*128 + 32*(w%4) + lane % 32) and
+// run on the same SIMD.  For each 32-row half `sub` of a 64-row query tile
+// (lane l supplies query row 32*sub + perm23(l % 32) to the first products):
+//   P waves (w < 4):   S  = Q K^T      A = Q rows (LDS)   B = K^T (registers)
+//                      P  = exp2(S*c - lse2[q])   -> bf16, handed to the partner
+//                      dV^T += dO^T P  A = dO^T (LDS, head_dim-major), B = P
+//   dS waves (w >= 4): dP = dO V^T     A = dO rows (LDS)  B = V^T (registers)
+//                      dS = P * (dP + ndelta[q])  (P from the partner)
+//                      dK^T += Q^T dS  A = Q^T (LDS, head_dim-major), B = dS
 // C-layout register 8*k2 + e of lane l holds query 32*sub + 16*k2 + 8*(l/32)
-// + e, so the A operands of the last two products and the row statistics are
-// 16-byte / 32-byte LDS reads.  Keys that are masked (or past the end) are
+// + e, so the A operands of the last products and the row statistics are
+// 16-byte LDS reads, and P travels between the partners as each lane's own
+// registers (one 16-byte LDS write and read per 16 rows).
+//
+// Two barriers per tile: T (tile staged) and X (P written).  Between T and X
+// each SIMD runs the P wave's QK^T MFMAs and softmax beside the dS wave's
+// dO V^T MFMAs; between X and the next T the P wave's dV MFMAs beside the dS
+// wave's dS arithmetic and dK MFMAs, so one wave's VALU work always has the
+// other's MFMAs to hide behind.  Keys that are masked (or past the end) are
 // not special-cased in the loop: each key's dK/dV column depends only on that
 // key, and those columns are written as zeros (or not at all) at the end.
-//
-// Tiles come from the padded copies (every load full, per-lane offsets loop
-// invariant); the loop body is branch-free and unrolled over the two LDS
-// buffers so that every LDS address is a per-lane base plus an immediate.
-// Order inside one tile: S/dP of half 0; S/dP of half 1 (the softmax of half
-// 0 fills the VALU meanwhile); dV/dK of half 0 (softmax of half 1); dV/dK of
-// half 1.
 template <int D, bool MASK>
-__global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
-  constexpr int BK = 128, BQ = 64, NW = 4;
+__global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
+  constexpr int BK = 128, BQ = 64, NW = 8;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BQ * D;
-  // Each buffer of the double-buffered tiles is its own LDS object, so the
-  // compiler knows the next tile's direct loads do not alias this tile's reads.
-  __shared__ __attribute__((aligned(16))) bf16 sq0[TE], sq1[TE];      // Q rows: TileLayout<D>
-  __shared__ __attribute__((aligned(16))) bf16 sdo0[TE], sdo1[TE];    // dO rows: TileLayout<D>
-  __shared__ __attribute__((aligned(16))) bf16 sqt0[TE], sqt1[TE];    // Q^T: D rows of BQ, TileLayout<BQ>
-  __shared__ __attribute__((aligned(16))) bf16 sdot0[TE], sdot1[TE];  // dO^T: TileLayout<BQ>
-  __shared__ __attribute__((aligned(16))) float slse0[BQ], slse1[BQ];
-  __shared__ __attribute__((aligned(16))) float sndl0[BQ], sndl1[BQ];
+  // One LDS object per buffer of the double-buffered stage: the compiler then
+  // knows the next tile's direct loads (into one object) do not alias this
+  // tile's reads (of the other), and tracks them with precise waits.
+  struct Stage {
+    bf16 q[TE];     // Q rows: TileLayout<D>
+    bf16 dout[TE];  // dO rows: TileLayout<D>
+    bf16 qt[TE];    // Q^T: D rows of BQ, TileLayout<BQ>
+    bf16 dot[TE];   // dO^T: TileLayout<BQ>
+    float lse2[BQ];
+    float ndl[BQ];
+  };
+  __shared__ __attribute__((aligned(16))) Stage st0, st1;
+  // P hand-over: 1 KB per (key group, sub, k2), lane-major.
+  __shared__ __attribute__((aligned(16))) u32x4 sxp[4 * 2 * 2 * 64];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int role = wave >> 2, kw = wave & 3;
   const int l32 = lane & 31, hh = lane >> 5;
   const int prow = perm23(l32);
 
@@ -112,31 +122,25 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int group = a.Hq / a.Hkv;
 
-  const int key = kt * BK + wave * 32 + l32;
+  const int key = kt * BK + kw * 32 + l32;
 
-  // K/V of this lane's key (zeros past the end).
-  bf16x8 kf[KS], vf[KS];
+  // This wave's B operand: K (P waves) or V (dS waves) of the lane's key,
+  // zeros past the end.
+  bf16x8 kv[KS];
   {
     const bool in = key < a.Lk;
-    const int64_t kr = ((int64_t)bhk * a.Lkp + key) * D + 8 * hh;
+    const bf16* src = (role == 0 ? a.kr : a.vr) + ((int64_t)bhk * a.Lkp + key) * D + 8 * hh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      u32x4 x = {0u, 0u, 0u, 0u}, y = {0u, 0u, 0u, 0u};
-      if (in) {
-        x = *reinterpret_cast<const u32x4*>(a.kr + kr + 16 * ks);
-        y = *reinterpret_cast<const u32x4*>(a.vr + kr + 16 * ks);
-      }
-      kf[ks] = bits_to_bf16x8(x);
-      vf[ks] = bits_to_bf16x8(y);
+      u32x4 x = {0u, 0u, 0u, 0u};
+      if (in) x = *reinterpret_cast<const u32x4*>(src + 16 * ks);
+      kv[ks] = bits_to_bf16x8(x);
     }
   }
 
-  f32x16 dk[DT], dv[DT];
+  f32x16 acc[DT];  // dV^T (P waves) or dK^T (dS waves)
 #pragma unroll
-  for (int i = 0; i < DT; ++i) {
-    dk[i] = zero16();
-    dv[i] = zero16();
-  }
+  for (int i = 0; i < DT; ++i) acc[i] = zero16();
 
   // Loop-invariant per-lane LDS element offsets.
   int ro[KS];  // row tiles: chunk (16*ks + 8*hh) of row perm23(l32)
@@ -145,135 +149,193 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
   int to[4];  // head_dim-major tiles: chunk (32*sub + 16*k2 + 8*hh) of row l32 (+32*dt rows)
 #pragma unroll
   for (int j = 0; j < 4; ++j) to[j] = TileLayout<BQ>::off(l32, 16 * j + 8 * hh);
+  u32x4* xp = sxp + kw * 4 * 64 + lane;  // + 64*(2*sub + k2)
 
   const int nqt = a.Lqp / BQ;
   const int niter = nqt * group;
-  DirectStager<BQ, D, NW> rst;  // 64 rows of D channels (row stride D)
-  DirectStager<D, BQ, NW> tst;  // D rows of 64 queries (row stride Lqp)
+  // Buffers over the query heads of this KV head's group (b, hk*group ..).
+  const int64_t bq0 = (int64_t)(b * a.Hq + hk * group);
+  const uint32_t qbytes = (uint32_t)group * a.Lqp * D * 2;
+  const u32x4 rq = make_rsrc(a.qr + bq0 * a.Lqp * D, qbytes);
+  const u32x4 rdo = make_rsrc(a.dor + bq0 * a.Lqp * D, qbytes);
+  const u32x4 rqt = make_rsrc(a.qt + bq0 * D * a.Lqp, qbytes);
+  const u32x4 rdot = make_rsrc(a.dot + bq0 * D * a.Lqp, qbytes);
+  const u32x4 rl2 = make_rsrc(a.lse2 + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
+  const u32x4 rnd = make_rsrc(a.ndelta + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
+  TileStager<BQ, D, NW> rst;  // 64 rows of D channels (row stride D)
+  TileStager<D, BQ, NW> tst;  // D rows of 64 queries (row stride Lqp)
   rst.init(D, wave, lane);
   tst.init(a.Lqp, wave, lane);
 
   auto stage = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    const int hq = hk * group + it / nqt;
-    const int q0 = (it % nqt) * BQ;
-    const int64_t bq = (int64_t)(b * a.Hq + hq);
-    const int64_t rb = (bq * a.Lqp + q0) * D;
-    rst.stage_full(buf == 0 ? sq0 : sq1, a.qr + rb, wave);
-    rst.stage_full(buf == 0 ? sdo0 : sdo1, a.dor + rb, wave);
-    const int64_t tb = bq * D * a.Lqp + q0;
-    tst.stage_full(buf == 0 ? sqt0 : sqt1, a.qt + tb, wave);
-    tst.stage_full(buf == 0 ? sdot0 : sdot1, a.dot + tb, wave);
-    const int64_t sr = bq * a.Lqp + q0 + lane;
-    direct_load4(a.lse2 + sr, buf == 0 ? slse0 : slse1);
-    direct_load4(a.ndelta + sr, buf == 0 ? sndl0 : sndl1);
+    const uint32_t g = (uint32_t)(it / nqt);  // query head within the group
+    const uint32_t q0 = (uint32_t)(it % nqt) * BQ;
+    const uint32_t row0 = g * a.Lqp + q0;  // first row of the tile in the group's copies
+    Stage& sg = buf == 0 ? st0 : st1;
+    rst.stage(sg.q, rq, row0 * D * 2);
+    rst.stage(sg.dout, rdo, row0 * D * 2);
+    const uint32_t tcol = (g * D * a.Lqp + q0) * 2;
+    tst.stage(sg.qt, rqt, tcol);
+    tst.stage(sg.dot, rdot, tcol);
+    // Every wave loads both (identical bytes): no branch in the loop body.
+    dma4(rl2, lds_addr(sg.lse2), lane * 4, row0 * 4);
+    dma4(rnd, lds_addr(sg.ndl), lane * 4, row0 * 4);
   };
 
   const float c = a.scale_log2;
 
-  // P and dS of one 32-row half from its S/dP accumulators.
-  auto softmax = [&](const f32x16& s, const f32x16& dp, const float* ll, const float* lnd, bf16x8* pb,
-                     bf16x8* dsb) {
-#pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      const f32x4 l2a = *reinterpret_cast<const f32x4*>(ll + 16 * k2 + 8 * hh);
-      const f32x4 l2b = *reinterpret_cast<const f32x4*>(ll + 16 * k2 + 8 * hh + 4);
-      const f32x4 nda = *reinterpret_cast<const f32x4*>(lnd + 16 * k2 + 8 * hh);
-      const f32x4 ndb = *reinterpret_cast<const f32x4*>(lnd + 16 * k2 + 8 * hh + 4);
-      u32x4 up, ud;
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) {
-        const int e = 2 * e2;
-        const float l0 = e < 4 ? l2a[e] : l2b[e - 4], l1 = e < 4 ? l2a[e + 1] : l2b[e - 3];
-        const float n0 = e < 4 ? nda[e] : ndb[e - 4], n1 = e < 4 ? nda[e + 1] : ndb[e - 3];
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s[8 * k2 + e], c, -l0));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s[8 * k2 + e + 1], c, -l1));
-        up[e2] = pack_bf16x2(p0, p1);
-        ud[e2] = pack_bf16x2(p0 * (dp[8 * k2 + e] + n0), p1 * (dp[8 * k2 + e + 1] + n1));
-      }
-      pb[k2] = bits_to_bf16x8(up);
-      dsb[k2] = bits_to_bf16x8(ud);
-    }
-  };
-
-  auto body = [&](int it, auto bufc) {
+  auto body_p = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     wait_vmem();
-    __syncthreads();  // tile `it` visible in `buf`; tile it-1 fully consumed everywhere
-    // the last iteration re-stages a tile nobody reads
-    stage(min(it + 1, niter - 1), std::integral_constant<int, buf ^ 1>());
-    const bf16* tq = buf == 0 ? sq0 : sq1;
-    const bf16* tdo = buf == 0 ? sdo0 : sdo1;
-    const bf16* tqt = buf == 0 ? sqt0 : sqt1;
-    const bf16* tdot = buf == 0 ? sdot0 : sdot1;
-    const float* tl = buf == 0 ? slse0 : slse1;
-    const float* tn = buf == 0 ? sndl0 : sndl1;
+    barrier_lds();  // T: tile `it` visible in `buf`; tile it-1 fully consumed everywhere
+    stage(min(it + 1, niter - 1), std::integral_constant<int, buf ^ 1>());  // last: re-stages an unread tile
+    const Stage& sg = buf == 0 ? st0 : st1;
+    const bf16* tq = sg.q;
+    const bf16* tdot = sg.dot;
+    const float* tl = sg.lse2;
 
-    bf16x8 qa[KS], da[KS];
-    f32x16 s0 = zero16(), dp0 = zero16(), s1 = zero16(), dp1 = zero16();
+    f32x16 s[2];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qa[ks] = *reinterpret_cast<const bf16x8*>(tq + ro[ks]);
-      da[ks] = *reinterpret_cast<const bf16x8*>(tdo + ro[ks]);
+    for (int sub = 0; sub < 2; ++sub) {
+      bf16x8 qa[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qa[ks] = *reinterpret_cast<const bf16x8*>(tq + sub * 32 * D + ro[ks]);
+      s[sub] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s[sub] = mfma32(qa[ks], kv[ks], s[sub]);
     }
+    // Keep four operand reads in flight ahead of the QK^T MFMAs.
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s0 = mfma32(qa[ks], kf[ks], s0);
-      dp0 = mfma32(da[ks], vf[ks], dp0);
+    for (int i = 0; i < 2 * KS - 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
     }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+    bf16x8 pb[2][2];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qa[ks] = *reinterpret_cast<const bf16x8*>(tq + 32 * D + ro[ks]);
-      da[ks] = *reinterpret_cast<const bf16x8*>(tdo + 32 * D + ro[ks]);
-    }
+    for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      s1 = mfma32(qa[ks], kf[ks], s1);
-      dp1 = mfma32(da[ks], vf[ks], dp1);
-    }
-    bf16x8 pb[2], dsb[2];
-    softmax(s0, dp0, tl, tn, pb, dsb);
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const f32x4 la = *reinterpret_cast<const f32x4*>(tl + 32 * sub + 16 * k2 + 8 * hh);
+        const f32x4 lb = *reinterpret_cast<const f32x4*>(tl + 32 * sub + 16 * k2 + 8 * hh + 4);
+        u32x4 up;
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        dv[dt] = mfma32(*reinterpret_cast<const bf16x8*>(tdot + dt * 32 * BQ + to[k2]), pb[k2], dv[dt]);
-        dk[dt] = mfma32(*reinterpret_cast<const bf16x8*>(tqt + dt * 32 * BQ + to[k2]), dsb[k2], dk[dt]);
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int e = 2 * e2;
+          const float l0 = e < 4 ? la[e] : lb[e - 4], l1 = e < 4 ? la[e + 1] : lb[e - 3];
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e], c, -l0));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e + 1], c, -l1));
+          up[e2] = pack_bf16x2(p0, p1);
+        }
+        xp[64 * (2 * sub + k2)] = up;
+        pb[sub][k2] = bits_to_bf16x8(up);
       }
-    softmax(s1, dp1, tl + 32, tn + 32, pb, dsb);
+    barrier_lds();  // X: P handed over
+    // dV^T += dO^T P over the 16 (sub, k2, dt) steps, with the dO^T operand
+    // reads software-pipelined four steps ahead.
+    constexpr int NJ = 4 * DT;
+    auto dot_op = [&](int j) {
+      const int sk = j / DT, dt = j % DT;  // sk = 2*sub + k2
+      return *reinterpret_cast<const bf16x8*>(tdot + dt * 32 * BQ + to[sk]);
+    };
+    // (sched_barrier pins this order: the scheduler would otherwise sink
+    // each read next to its MFMA.)
+    bf16x8 opq[4];
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
+    for (int j = 0; j < 4; ++j) opq[j] = dot_op(j);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        dv[dt] = mfma32(*reinterpret_cast<const bf16x8*>(tdot + dt * 32 * BQ + to[2 + k2]), pb[k2], dv[dt]);
-        dk[dt] = mfma32(*reinterpret_cast<const bf16x8*>(tqt + dt * 32 * BQ + to[2 + k2]), dsb[k2], dk[dt]);
+    for (int j = 0; j < NJ; ++j) {
+      const bf16x8 op = opq[j % 4];
+      if (j + 4 < NJ) opq[j % 4] = dot_op(j + 4);
+      const int sk = j / DT, dt = j % DT;
+      acc[dt] = mfma32(op, pb[sk >> 1][sk & 1], acc[dt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  auto body_ds = [&](int it, auto bufc) {
+    constexpr int buf = decltype(bufc)::value;
+    wait_vmem();
+    barrier_lds();  // T
+    stage(min(it + 1, niter - 1), std::integral_constant<int, buf ^ 1>());
+    const Stage& sg = buf == 0 ? st0 : st1;
+    const bf16* tdo = sg.dout;
+    const bf16* tqt = sg.qt;
+    const float* tn = sg.ndl;
+
+    f32x16 dp[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      bf16x8 da[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) da[ks] = *reinterpret_cast<const bf16x8*>(tdo + sub * 32 * D + ro[ks]);
+      dp[sub] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) dp[sub] = mfma32(da[ks], kv[ks], dp[sub]);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 2 * KS - 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+    barrier_lds();  // X: partner's P available
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2) {
+        const u32x4 up = xp[64 * (2 * sub + k2)];
+        const f32x4 na = *reinterpret_cast<const f32x4*>(tn + 32 * sub + 16 * k2 + 8 * hh);
+        const f32x4 nb = *reinterpret_cast<const f32x4*>(tn + 32 * sub + 16 * k2 + 8 * hh + 4);
+        u32x4 ud;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int e = 2 * e2;
+          const float n0 = e < 4 ? na[e] : nb[e - 4], n1 = e < 4 ? na[e + 1] : nb[e - 3];
+          const float p0 = __uint_as_float(up[e2] << 16), p1 = __uint_as_float(up[e2] & 0xffff0000u);
+          ud[e2] = pack_bf16x2(p0 * (dp[sub][8 * k2 + e] + n0), p1 * (dp[sub][8 * k2 + e + 1] + n1));
+        }
+        const bf16x8 dsb = bits_to_bf16x8(ud);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          acc[dt] = mfma32(*reinterpret_cast<const bf16x8*>(tqt + dt * 32 * BQ + to[2 * sub + k2]), dsb, acc[dt]);
       }
   };
 
+  retire_prologue_loads();
   stage(0, std::integral_constant<int, 0>());
-  for (int it = 0; it < niter; it += 2) {
-    body(it, std::integral_constant<int, 0>());
-    if (it + 1 < niter) body(it + 1, std::integral_constant<int, 1>());
+  if (role == 0) {
+    for (int it = 0; it < niter; it += 2) {
+      body_p(it, std::integral_constant<int, 0>());
+      if (it + 1 < niter) body_p(it + 1, std::integral_constant<int, 1>());
+    }
+  } else {
+    for (int it = 0; it < niter; it += 2) {
+      body_ds(it, std::integral_constant<int, 0>());
+      if (it + 1 < niter) body_ds(it + 1, std::integral_constant<int, 1>());
+    }
   }
 
   if (key < a.Lk) {
     bool kvalid = true;
     if (MASK) kvalid = a.mask[b * a.msb + key] != 0;
-    bf16* kp = a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl;
-    bf16* vp = a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl;
+    const float sc = role == 0 ? 1.f : a.scale;
+    bf16* op = role == 0 ? a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl
+                         : a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        u32x2 wk = {0u, 0u}, wv = {0u, 0u};
+        u32x2 w = {0u, 0u};
         if (kvalid) {
-          wk[0] = pack_bf16x2(dk[dt][4 * g] * a.scale, dk[dt][4 * g + 1] * a.scale);
-          wk[1] = pack_bf16x2(dk[dt][4 * g + 2] * a.scale, dk[dt][4 * g + 3] * a.scale);
-          wv[0] = pack_bf16x2(dv[dt][4 * g], dv[dt][4 * g + 1]);
-          wv[1] = pack_bf16x2(dv[dt][4 * g + 2], dv[dt][4 * g + 3]);
+          w[0] = pack_bf16x2(acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc);
+          w[1] = pack_bf16x2(acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc);
         }
-        *reinterpret_cast<u32x2*>(kp + dt * 32 + 8 * g + 4 * hh) = wk;
-        *reinterpret_cast<u32x2*>(vp + dt * 32 + 8 * g + 4 * hh) = wv;
+        *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
       }
   }
 }
@@ -281,28 +343,39 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // 3. dQ
 // ---------------------------------------------------------------------------
-// Per wave: 32 query rows (lane % 32 owns query column q0w + lane % 32).  For
-// each 32-key tile (lane l supplies key row perm23(l % 32) to the first two
-// products):
+// One workgroup = 256 query rows of one (batch, head): 8 waves x 32 rows
+// (lane % 32 owns query column q0w + lane % 32), 1 workgroup per CU, so each
+// K/V tile is staged once for 256 rows.  For each 32-key tile (lane l supplies
+// key row perm23(l % 32) to the first two products):
 //   S^T  = K Q^T    A = K rows (LDS)          B = Q^T (registers)
 //   dP^T = V dO^T   A = V rows (LDS)          B = dO^T (registers)
 //   dS^T = P^T * (dP^T + ndelta[q])           (fp32, key bias masks P^T)
 //   dQ^T += K^T dS^T   A = K^T (LDS, head_dim-major)  B = dS^T (C layout reused)
-// Tiles come from the padded copies; the body is unrolled over the two LDS
-// buffers and branch-free apart from the masked-tile bias.
+// Tiles come from the padded copies through three LDS stages: tile t+2 is
+// loaded while tile t is computed, so each load has two tiles' time to land.
+// The body is unrolled over the three stages and branch-free apart from the
+// masked-tile bias.
+#ifndef AVATTN_DQ_WAVES
+#define AVATTN_DQ_WAVES 8
+#endif
 template <int D>
-__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
-  constexpr int BM = 128, BN = 32, NW = 4;
+__global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd_dq_kernel(BwdArgs a) {
+  constexpr int NW = AVATTN_DQ_WAVES, BM = 32 * NW, BN = 32;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BN * D;
-  // One LDS object per buffer (see bwd_dkdv_kernel).
-  __shared__ __attribute__((aligned(16))) bf16 sk0[TE], sk1[TE];    // K rows: TileLayout<D>
-  __shared__ __attribute__((aligned(16))) bf16 sv0[TE], sv1[TE];    // V rows: TileLayout<D>
-  __shared__ __attribute__((aligned(16))) bf16 skt0[TE], skt1[TE];  // K^T: D rows of BN keys, TileLayout<BN>
-  __shared__ __attribute__((aligned(16))) float sb0[64], sb1[64];   // key bias (this tile and the next)
+  // One LDS object per stage (see bwd_dkdv_kernel).
+  struct Stage {
+    bf16 k[TE];      // K rows: TileLayout<D>
+    bf16 v[TE];      // V rows: TileLayout<D>
+    bf16 kt[TE];     // K^T: D rows of BN keys, TileLayout<BN>
+    float bias[64];  // key bias (this tile and the next)
+    int flags[64];   // "all attended" flag of this tile (and the next 63)
+  };
+  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
   const int prow = perm23(l32);
 
@@ -337,30 +410,33 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
   }
 
   const int64_t bhk = (int64_t)(b * a.Hkv + hk);
-  const bf16* krbase = a.kr + bhk * a.Lkp * D;
-  const bf16* vrbase = a.vr + bhk * a.Lkp * D;
-  const bf16* ktbase = a.kt + bhk * D * a.Lkp;
-  const float* kbias = a.kbias + (int64_t)b * a.Lkp;
-  const int* kfull = a.kfull + (int64_t)b * (a.Lkp / 32);
+  const uint32_t slice = (uint32_t)a.Lkp * D * 2;
+  const u32x4 rk = make_rsrc(a.kr + bhk * a.Lkp * D, slice);
+  const u32x4 rv = make_rsrc(a.vr + bhk * a.Lkp * D, slice);
+  const u32x4 rkt = make_rsrc(a.kt + bhk * D * a.Lkp, slice);
+  // Biases and flags: both arrays are padded by 64 entries, so the 64 read
+  // from a tile start stay inside them.
+  const u32x4 rb = make_rsrc(a.kbias + (int64_t)b * a.Lkp, (uint32_t)(a.Lkp + 64) * 4);
+  const u32x4 rf = make_rsrc(a.kfull + (int64_t)b * (a.Lkp / 32), (uint32_t)(a.Lkp / 32 + 64) * 4);
 
-  DirectStager<BN, D, NW> rst;   // 32 rows of D channels (row stride D)
-  DirectStager<D, BN, NW> ktst;  // D rows of 32 keys (row stride Lkp)
+  using RowStager = TileStager<BN, D, NW>;  // 32 rows of D channels (row stride D)
+  using ColStager = TileStager<D, BN, NW>;  // D rows of 32 keys (row stride Lkp)
+  RowStager rst;
+  ColStager ktst;
   rst.init(D, wave, lane);
   ktst.init(a.Lkp, wave, lane);
-  // Stages tile t and loads its "all attended" flag into a register that is
-  // consumed one iteration later (after the wait that covers the tile).
-  int full_next = 1;
+  // Vector-memory loads one stage issues per wave: K, V, K^T, bias, flags.
+  constexpr int kStageLoads = 2 * RowStager::kPer + ColStager::kPer + 2;
+
   auto stage = [&](int t, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    const int k0 = t * BN;
-    full_next = kfull[t];
-    rst.stage_full(buf == 0 ? sk0 : sk1, krbase + (int64_t)k0 * D, wave);
-    rst.stage_full(buf == 0 ? sv0 : sv1, vrbase + (int64_t)k0 * D, wave);
-    ktst.stage_full(buf == 0 ? skt0 : skt1, ktbase + k0, wave);
-    // 64 biases (this tile and the next; the array is padded to whole
-    // 64-key tiles, so k0 + 63 < Lkp for every even tile and the read for an
-    // odd last tile stays inside the next batch row or the 64-float pad).
-    direct_load4(kbias + k0 + lane, buf == 0 ? sb0 : sb1);
+    Stage& sg = buf == 0 ? st0 : (buf == 1 ? st1 : st2);
+    const uint32_t k0 = (uint32_t)t * BN;
+    rst.stage(sg.k, rk, k0 * D * 2);
+    rst.stage(sg.v, rv, k0 * D * 2);
+    ktst.stage(sg.kt, rkt, k0 * 2);
+    dma4(rb, lds_addr(sg.bias), lane * 4, k0 * 4);
+    dma4(rf, lds_addr(sg.flags), lane * 4, (uint32_t)t * 4);
   };
 
   int ko[KS];  // K/V row perm23(l32), chunk 16*ks + 8*hh
@@ -379,27 +455,46 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
 
   auto body = [&](int t, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    wait_vmem();
-    __syncthreads();  // tile t visible in `buf`; tile t-1 fully consumed everywhere
-    const int full = __builtin_amdgcn_readfirstlane(full_next);
-    stage(min(t + 1, nkt - 1), std::integral_constant<int, buf ^ 1>());
-    const bf16* tk = buf == 0 ? sk0 : sk1;
-    const bf16* tv = buf == 0 ? sv0 : sv1;
-    const bf16* tkt = buf == 0 ? skt0 : skt1;
-    const float* tb = buf == 0 ? sb0 : sb1;
+    wait_vmem_n<kStageLoads>();  // tile t landed (tile t+1 may still be in flight)
+    barrier_lds();               // ... for every wave; tile t-1's stage is free
+    // Tile t+2 into the stage tile t-1 used (the last iterations re-stage a
+    // tile nobody reads, keeping the per-iteration load count fixed).
+    stage(min(t + 2, nkt - 1), std::integral_constant<int, (buf + 2) % 3>());
+    const Stage& sg = buf == 0 ? st0 : (buf == 1 ? st1 : st2);
+    const int full = __builtin_amdgcn_readfirstlane(sg.flags[0]);
+    const bf16* tk = sg.k;
+    const bf16* tv = sg.v;
+    const bf16* tkt = sg.kt;
+    const float* tb = sg.bias;
 
-    bf16x8 ka[KS], va[KS];
+    // S^T and dP^T: operand reads run four k-steps ahead of the MFMAs
+    // (sched_barrier pins the order; the scheduler would otherwise sink each
+    // read next to its MFMA and expose the LDS latency).
+    auto krow = [&](int ks) { return *reinterpret_cast<const bf16x8*>(tk + ko[ks]); };
+    auto vrow = [&](int ks) { return *reinterpret_cast<const bf16x8*>(tv + ko[ks]); };
+    bf16x8 ka[4], va[4];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      ka[ks] = *reinterpret_cast<const bf16x8*>(tk + ko[ks]);
-      va[ks] = *reinterpret_cast<const bf16x8*>(tv + ko[ks]);
+    for (int j = 0; j < 4; ++j) {
+      ka[j] = krow(j);
+      va[j] = vrow(j);
     }
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 s = zero16(), dp = zero16();
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      s = mfma32(ka[ks], qf[ks], s);
-      dp = mfma32(va[ks], df[ks], dp);
+      s = mfma32(ka[ks & 3], qf[ks], s);
+      dp = mfma32(va[ks & 3], df[ks], dp);
+      if (ks + 4 < KS) {
+        ka[ks & 3] = krow(ks + 4);
+        va[ks & 3] = vrow(ks + 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // dQ operands (K^T) are read now, while the softmax below runs.
+    bf16x8 kta[2 * DT];
+#pragma unroll
+    for (int j = 0; j < 2 * DT; ++j) kta[j] = *reinterpret_cast<const bf16x8*>(tkt + (j % DT) * 32 * BN + to[j / DT]);
+    __builtin_amdgcn_sched_barrier(0);
     // registers 8*k2 + e hold key 16*k2 + 8*hh + e
     if (!full) {
 #pragma unroll
@@ -423,16 +518,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(BwdArgs a) {
       dsb[k2] = bits_to_bf16x8(u);
     }
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        dq[dt] = mfma32(*reinterpret_cast<const bf16x8*>(tkt + dt * 32 * BN + to[k2]), dsb[k2], dq[dt]);
+    for (int j = 0; j < 2 * DT; ++j) dq[j % DT] = mfma32(kta[j], dsb[j / DT], dq[j % DT]);
   };
 
+  retire_prologue_loads();
   stage(0, std::integral_constant<int, 0>());
-  for (int t = 0; t < nkt; t += 2) {
+  stage(min(1, nkt - 1), std::integral_constant<int, 1>());
+  for (int t = 0; t < nkt; t += 3) {
     body(t, std::integral_constant<int, 0>());
     if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());
+    if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 2>());
   }
 
   if (qvalid) {
@@ -485,17 +580,18 @@ static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
   {
     const int nkt = (a.Lk + 127) / 128;
     const dim3 grid(nkt * a.B * a.Hkv);
-    LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup per CU (LDS-bound occupancy)
+    LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup (8 waves) per CU: LDS-bound occupancy
     if (mask)
-      hipLaunchKernelGGL((bwd_dkdv_kernel<D, true>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<D, true>), grid, dim3(512), 0, stream, a);
     else
-      hipLaunchKernelGGL((bwd_dkdv_kernel<D, false>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<D, false>), grid, dim3(512), 0, stream, a);
   }
   {
-    const int nqt = (a.Lq + 127) / 128;
+    constexpr int BM = 32 * AVATTN_DQ_WAVES;
+    const int nqt = (a.Lq + BM - 1) / BM;
     const dim3 grid(nqt * a.B * a.Hq);
     LaunchTimer timer(kKidBwdDq, stream);
-    hipLaunchKernelGGL(bwd_dq_kernel<D>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(bwd_dq_kernel<D>, grid, dim3(64 * AVATTN_DQ_WAVES), 0, stream, a);
   }
   return hipGetLastError();
 }

@@ -37,13 +37,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   constexpr int KS = D / 16;  // 16-channel k-steps of q k^T
   constexpr int DT = D / 32;  // 32-channel row tiles of O^T
   constexpr int TE = BN * D;  // tile elements
-  // Each buffer of the double-buffered tiles is its own LDS object: the
-  // compiler then knows that the direct global->LDS loads into one buffer do
-  // not alias the LDS reads of the other, and does not wait for the next
-  // tile's loads before reading the current one.
-  __shared__ __attribute__((aligned(16))) bf16 sk0[TE], sk1[TE];    // K rows: TileLayout<D>
-  __shared__ __attribute__((aligned(16))) bf16 svt0[TE], svt1[TE];  // V^T rows (channel-major): TileLayout<BN>
-  __shared__ __attribute__((aligned(16))) float sb0[BN], sb1[BN];   // key bias
+  // One LDS object per buffer of the double-buffered stage: the compiler then
+  // knows that the direct global->LDS loads into one buffer do not alias the
+  // LDS reads of the other, and does not wait for the next tile's loads
+  // before reading the current one.
+  struct Stage {
+    bf16 k[TE];       // K rows: TileLayout<D>
+    bf16 vt[TE];      // V^T rows (channel-major): TileLayout<BN>
+    float bias[BN];   // key bias
+    int flags[64];    // "all attended" flags of the tile's two 32-key halves (and beyond)
+  };
+  __shared__ __attribute__((aligned(16))) Stage st0, st1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -62,32 +66,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   const bool qvalid = qrow < a.Lq;
 
   const int64_t bhk = (int64_t)(b * a.Hkv + hk);
-  const bf16* krbase = a.kr + bhk * a.Lkp * D;
-  const bf16* vtbase = a.vt + bhk * D * a.Lkp;
-  const float* kbias = a.kbias + (int64_t)b * a.Lkp;
-  const int* kfull = a.kfull + (int64_t)b * (a.Lkp / 32);
+  const uint32_t slice = (uint32_t)a.Lkp * D * 2;  // bytes of one (b, h) slice of a copy
+  const u32x4 rk = make_rsrc(a.kr + bhk * a.Lkp * D, slice);
+  const u32x4 rv = make_rsrc(a.vt + bhk * D * a.Lkp, slice);
+  const u32x4 rb = make_rsrc(a.kbias + (int64_t)b * a.Lkp, (uint32_t)(a.Lkp + 64) * 4);
+  // Flags are padded by 64 entries: the 64 read from a tile start stay inside.
+  const u32x4 rf = make_rsrc(a.kfull + (int64_t)b * (a.Lkp / 32), (uint32_t)(a.Lkp / 32 + 64) * 4);
   const int nkt = a.Lkp / BN;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  DirectStager<BN, D, NW> kst;  // 64 K rows of D channels (row stride D)
-  DirectStager<D, BN, NW> vst;  // D V^T rows of 64 keys (row stride Lkp)
-  kst.init(D, wave, lane);
-  vst.init(a.Lkp, wave, lane);
-  // Stages tile t into one buffer and loads its two 32-key "all attended"
-  // flags into registers (consumed one iteration later, after the wait that
-  // covers the tile: a flag load issued mid-iteration would otherwise make
-  // its use wait for every tile load issued before it).
-  int full_next0 = 1, full_next1 = 1;
-  auto stage = [&](int t, bf16* lk, bf16* lvt, float* lb) {
-    const int k0 = t * BN;
-    full_next0 = kfull[2 * t];
-    full_next1 = kfull[2 * t + 1];
-    kst.stage_full(lk, krbase + (int64_t)k0 * D, wave);
-    vst.stage_full(lvt, vtbase + k0, wave);
-    direct_load4(kbias + k0 + lane, lb);
+  TileStager<BN, D, NW> kst;  // 64 K rows of D channels (row stride D)
+  TileStager<D, BN, NW> vst;  // D V^T rows of 64 keys (row stride Lkp)
+  kst.init(D, wave_u, lane);
+  vst.init(a.Lkp, wave_u, lane);
+  auto stage = [&](int t, Stage& sg) {
+    const uint32_t k0 = (uint32_t)t * BN;
+    kst.stage(sg.k, rk, k0 * D * 2);
+    vst.stage(sg.vt, rv, k0 * 2);
+    dma4(rb, lds_addr(sg.bias), lane * 4, k0 * 4);
+    dma4(rf, lds_addr(sg.flags), lane * 4, (uint32_t)t * 8);
   };
 
   // Prologue loads, then Q (rotated on load) while they fly.
-  stage(0, sk0, svt0, sb0);
+  stage(0, st0);
 
   // Q fragments: B operand of S^T = K Q^T; lane holds row qrow, channels
   // 16*ks + 8*hh + [0, 8).
@@ -133,16 +134,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   auto body = [&](int t, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     wait_vmem();
-    __syncthreads();  // tile t visible in `buf`; tile t-1 fully consumed everywhere
-    const int full[2] = {__builtin_amdgcn_readfirstlane(full_next0), __builtin_amdgcn_readfirstlane(full_next1)};
+    barrier_lds();  // tile t visible in `buf`; tile t-1 fully consumed everywhere
     // the last iteration re-stages a tile nobody reads
-    if constexpr (buf == 0)
-      stage(min(t + 1, nkt - 1), sk1, svt1, sb1);
-    else
-      stage(min(t + 1, nkt - 1), sk0, svt0, sb0);
-    const bf16* kl = buf == 0 ? sk0 : sk1;
-    const bf16* vl = buf == 0 ? svt0 : svt1;
-    const float* bl = buf == 0 ? sb0 : sb1;
+    stage(min(t + 1, nkt - 1), buf == 0 ? st1 : st0);
+    const Stage& sg = buf == 0 ? st0 : st1;
+    const int full[2] = {__builtin_amdgcn_readfirstlane(sg.flags[0]), __builtin_amdgcn_readfirstlane(sg.flags[1])};
+    const bf16* kl = sg.k;
+    const bf16* vl = sg.vt;
+    const float* bl = sg.bias;
 
     // S^T of both 32-key halves: sh[half][8*k2 + e] is the score of key
     // 32*half + 16*k2 + 8*hh + e against this lane's query.
@@ -212,6 +211,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
     }
   };
 
+  retire_prologue_loads();
   for (int t = 0; t < nkt; t += 2) {
     body(t, std::integral_constant<int, 0>());
     if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());

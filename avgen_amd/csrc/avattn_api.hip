@@ -35,10 +35,10 @@ int launch_status(hipError_t e) { return e == hipSuccess ? AVATTN_OK : AVATTN_ER
 
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
-// Key bias (B, Lkp) floats plus a 64-float tail pad (tile loads read 64
-// biases from a 32-key tile start), and per-32-key-tile flags (B, Lkp/32).
+// Key bias (B, Lkp) floats and per-32-key-tile flags (B, Lkp/32) ints, each
+// with a 64-entry tail pad (tile loads read 64 entries from a tile start).
 size_t kbias_bytes(int32_t B, size_t Lkp) { return round256(((size_t)B * Lkp + 64) * sizeof(float)); }
-size_t kfull_bytes(int32_t B, size_t Lkp) { return round256((size_t)B * (Lkp / 32) * sizeof(int)); }
+size_t kfull_bytes(int32_t B, size_t Lkp) { return round256(((size_t)B * (Lkp / 32) + 64) * sizeof(int)); }
 
 // Forward workspace: [k rows | v^T | key bias | key tile flags], each region
 // 256-byte aligned.

@@ -176,82 +176,129 @@ __device__ __forceinline__ bf16x8 row_operand(const bf16* tile, int row, int col
   return *reinterpret_cast<const bf16x8*>(tile + TileLayout<RL>::off(row, col));
 }
 
-// 16 bytes per lane from global memory straight into LDS at
-// lds_block + 16*lane (global_load_lds_dwordx4; lds_block is wave-uniform).
-__device__ __forceinline__ void direct_load16(const void* src, void* lds_block) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_block, 16, 0, 0);
+// ---------------------------------------------------------------------------
+// Direct global->LDS tile loads (buffer_load_dword{,x4} ... lds).
+// ---------------------------------------------------------------------------
+// Issued through inline assembly on purpose: the kernels order these loads
+// themselves (a counted vmcnt wait, then a workgroup barrier, before a stage
+// is read; a barrier before a stage is refilled).  Seen as compiler builtins
+// they are LDS writes whose aliasing with later LDS reads the compiler can
+// only track for a few buffers at a time, and it then inserts vmcnt waits
+// that also wait for tiles loaded ahead.  Addressing: a raw buffer resource
+// (scalar base + byte range), a 32-bit per-lane byte offset and a scalar byte
+// offset; M0 holds the LDS destination of lane 0 (lane j writes +4*j or
+// +16*j bytes).
+
+// Raw buffer over [base, base + bytes): descriptor words for the gfx9 family
+// (32-bit data format in word 3, no swizzle, stride 0), in scalar registers.
+__device__ __forceinline__ u32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;
+  return r;
 }
 
-// 4 bytes per lane from global memory straight into LDS at lds_block + 4*lane.
-__device__ __forceinline__ void direct_load4(const void* src, void* lds_block) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_block, 4, 0, 0);
+// Byte address of an LDS location (the value M0 takes).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p);
 }
 
-// Direct global->LDS staging of a ROWS x RL tile (global rows of RL
-// contiguous bf16 at `row_stride` elements) into TileLayout<RL> with
-// global_load_lds_dwordx4.  One wave instruction moves 1 KB: lane j's 16
-// bytes land at LDS block base + 16*j, i.e. row row0 + j/(RL/8), chunk slot
-// j%(RL/8); the lane therefore loads the logical chunk the swizzle maps to
-// that slot.  Rows at or past rows_valid (>= 1) re-read row rows_valid-1:
-// callers never use those rows unmasked.  The NW waves of a workgroup split
-// the tile's instructions; completion is tracked by vmcnt (callers wait with
-// vmcnt(0) and a barrier before reading).
+// 16 bytes per lane from base + voff + soff into LDS at lds + 16*lane.
+__device__ __forceinline__ void dma16(const u32x4& r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  __asm__ volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(lds),
+      "v"(voff), "s"(r), "s"(soff)
+      : "memory", "m0");
+}
+
+// 4 bytes per lane into LDS at lds + 4*lane.
+__device__ __forceinline__ void dma4(const u32x4& r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  __asm__ volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %1, %2, %3 offen lds" ::"s"(lds),
+      "v"(voff), "s"(r), "s"(soff)
+      : "memory", "m0");
+}
+
+// Full ROWS x RL tile (rows of RL contiguous bf16, `row_stride` elements
+// apart in the source) into TileLayout<RL> with dma16.  One wave instruction
+// moves 1 KB: lane j's 16 bytes land at LDS block base + 16*j, i.e. row
+// row0 + j/(RL/8), chunk slot j%(RL/8), so the lane loads the logical chunk
+// the swizzle maps to that slot.  The NW waves of a workgroup split the
+// tile's instructions; the per-lane byte offsets depend only on the lane, the
+// wave and the row stride, so they are computed once.
 template <int ROWS, int RL, int NW>
-__device__ __forceinline__ void stage_direct(bf16* lds, const bf16* g, int64_t row_stride, int rows_valid, int wave,
-                                             int lane) {
-  constexpr int kCpr = RL / 8;      // 16-byte chunks per row
-  constexpr int kRpi = 64 / kCpr;   // rows per wave instruction
-  constexpr int kNi = ROWS / kRpi;  // instructions per tile
-  static_assert(kNi % NW == 0, "tile must split evenly over the waves");
-#pragma unroll
-  for (int i = 0; i < kNi / NW; ++i) {
-    const int row0 = (wave * (kNi / NW) + i) * kRpi;
-    const int row = row0 + lane / kCpr;
-    const int chunk = (lane % kCpr) ^ TileLayout<RL>::swz(row);
-    const int srow = min(row, rows_valid - 1);
-    direct_load16(g + (int64_t)srow * row_stride + chunk * 8, lds + row0 * RL);
-  }
-}
-
-// stage_direct with the per-lane source offsets precomputed (they depend only
-// on the lane, the wave and the row stride): for full tiles each load is a
-// uniform tile base plus a 32-bit lane offset, with no per-tile address math.
-// The row stride times ROWS must fit in 31 bits.
-template <int ROWS, int RL, int NW>
-struct DirectStager {
-  static constexpr int kCpr = RL / 8;
-  static constexpr int kRpi = 64 / kCpr;
-  static constexpr int kNi = ROWS / kRpi;
-  static constexpr int kPer = kNi / NW;
-  static_assert(kNi % NW == 0, "tile must split evenly over the waves");
-  int off[kPer];  // element offset of this lane's source chunk, per instruction
+struct TileStager {
+  static constexpr int kCpr = RL / 8;      // 16-byte chunks per row
+  static constexpr int kRpi = 64 / kCpr;   // rows per wave instruction
+  static constexpr int kNi = ROWS / kRpi;  // instructions per tile
+  // Instructions per wave.  With fewer instructions than waves, wave w
+  // repeats instruction w % kNi (the same bytes to the same place), so every
+  // wave issues the same number of loads and can wait on a fixed count.
+  static constexpr int kPer = kNi >= NW ? kNi / NW : 1;
+  static_assert(kNi % NW == 0 || NW % kNi == 0, "tile must split evenly over the waves");
+  uint32_t off[kPer];  // byte offset of this lane's source chunk, per instruction
+  uint32_t lds0;       // byte offset of this wave's first LDS block in the tile
 
   __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
+    const int first = (wave * kPer) % kNi;
+    lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(first * kRpi * RL * 2));
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int row0 = (wave * kPer + i) * kRpi;
-      const int row = row0 + lane / kCpr;
-      off[i] = (int)(row * row_stride) + ((lane % kCpr) ^ TileLayout<RL>::swz(row)) * 8;
+      const int row = (first + i) * kRpi + lane / kCpr;
+      off[i] = (uint32_t)((row * row_stride + ((lane % kCpr) ^ TileLayout<RL>::swz(row)) * 8) * 2);
     }
   }
-  __device__ __forceinline__ static int lds_row0(int i, int wave) { return (wave * kPer + i) * kRpi; }
-  // Every row valid; `g` points at the tile's first row.
-  __device__ __forceinline__ void stage_full(bf16* lds, const bf16* g, int wave) const {
+  // `soff`: byte offset of the tile's first row in the buffer.
+  __device__ __forceinline__ void stage(bf16* lds, const u32x4& r, uint32_t soff) const {
+    const uint32_t base = lds_addr(lds) + lds0;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) direct_load16(g + off[i], lds + lds_row0(i, wave) * RL);
-  }
-  // rows_valid in [1, ROWS].
-  __device__ __forceinline__ void stage(bf16* lds, const bf16* g, int64_t row_stride, int rows_valid, int wave,
-                                        int lane) const {
-    if (rows_valid >= ROWS)
-      stage_full(lds, g, wave);
-    else
-      stage_direct<ROWS, RL, NW>(lds, g, row_stride, rows_valid, wave, lane);
+    for (int i = 0; i < kPer; ++i) dma16(r, base + i * kRpi * RL * 2, off[i], soff);
   }
 };
+
+// Retire every outstanding memory operation of this wave, as an instruction
+// the compiler's wait-count bookkeeping sees: a loop that issues its tile
+// loads as inline assembly calls this first, so no compiler-inserted wait for
+// a prologue load lands inside the loop (where, counting the loop's own tile
+// loads too, it would wait for tiles loaded ahead).
+__device__ __forceinline__ void retire_prologue_loads() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Wait until at most N of this wave's vector-memory loads are outstanding
+// (loads complete in issue order, so every load issued before the last N has
+// landed).
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
 
 // Wait for this wave's outstanding global loads (including direct-to-LDS
 // ones); a following barrier makes every wave's tile visible.
 __device__ __forceinline__ void wait_vmem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Workgroup barrier that orders this wave's LDS writes before every wave's
+// later LDS reads, without waiting for outstanding global loads (unlike
+// __syncthreads, whose release fence also waits for the next tile's direct
+// global->LDS loads still in flight).
+__device__ __forceinline__ void barrier_lds() {
+  __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+// Instruction-class masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedValu = 0x002;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kSchedDsWrite = 0x200;
+constexpr int kSchedVmem = 0x010;
+constexpr int kSchedSalu = 0x004;
 
 }  // namespace avattn

@@ -66,8 +66,8 @@ def _pad64(n: int) -> int:
 
 
 def _key_regions(B: int, lkp: int) -> int:
-    # key bias (B, Lkp) floats + a 64-float tail pad, then (B, Lkp/32) int flags
-    return _round256((B * lkp + 64) * 4) + _round256(B * (lkp // 32) * 4)
+    # key bias (B, Lkp) floats and (B, Lkp/32) int flags, each + a 64-entry tail pad
+    return _round256((B * lkp + 64) * 4) + _round256((B * (lkp // 32) + 64) * 4)
 
 
 def test_workspace_size(lib):
