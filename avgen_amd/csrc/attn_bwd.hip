@@ -92,18 +92,22 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   constexpr int BK = 128, BQ = 64, NW = 8;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BQ * D;
-  // One LDS object per buffer of the double-buffered stage: the compiler then
-  // knows the next tile's direct loads (into one object) do not alias this
-  // tile's reads (of the other), and tracks them with precise waits.
-  struct Stage {
+  // Two double-buffered halves of a tile: the rows (read before the P
+  // hand-over) and the head_dim-major columns (read after it).  Each half is
+  // refilled as soon as the phase that reads it is over, so the row tiles are
+  // loaded two tiles ahead and the column tiles one and a half.
+  struct RowStage {
     bf16 q[TE];     // Q rows: TileLayout<D>
     bf16 dout[TE];  // dO rows: TileLayout<D>
-    bf16 qt[TE];    // Q^T: D rows of BQ, TileLayout<BQ>
-    bf16 dot[TE];   // dO^T: TileLayout<BQ>
     float lse2[BQ];
+  };
+  struct ColStage {
+    bf16 qt[TE];   // Q^T: D rows of BQ, TileLayout<BQ>
+    bf16 dot[TE];  // dO^T: TileLayout<BQ>
     float ndl[BQ];
   };
-  __shared__ __attribute__((aligned(16))) Stage st0, st1;
+  __shared__ __attribute__((aligned(16))) RowStage rs0, rs1;
+  __shared__ __attribute__((aligned(16))) ColStage cs0, cs1;
   // P hand-over: 1 KB per (key group, sub, k2), lane-major.
   __shared__ __attribute__((aligned(16))) u32x4 sxp[4 * 2 * 2 * 64];
 
@@ -167,81 +171,129 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   rst.init(D, wave, lane);
   tst.init(a.Lqp, wave, lane);
 
-  auto stage = [&](int it, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    const uint32_t g = (uint32_t)(it / nqt);  // query head within the group
-    const uint32_t q0 = (uint32_t)(it % nqt) * BQ;
-    const uint32_t row0 = g * a.Lqp + q0;  // first row of the tile in the group's copies
-    Stage& sg = buf == 0 ? st0 : st1;
-    rst.stage(sg.q, rq, row0 * D * 2);
-    rst.stage(sg.dout, rdo, row0 * D * 2);
-    const uint32_t tcol = (g * D * a.Lqp + q0) * 2;
-    tst.stage(sg.qt, rqt, tcol);
-    tst.stage(sg.dot, rdot, tcol);
-    // Every wave loads both (identical bytes): no branch in the loop body.
-    dma4(rl2, lds_addr(sg.lse2), lane * 4, row0 * 4);
-    dma4(rnd, lds_addr(sg.ndl), lane * 4, row0 * 4);
+  // Each half of a tile = kHalfOps loads per wave, issued one at a time so
+  // they can be spread between MFMAs (a burst of them at the start of a
+  // phase would hold up the wave's instruction stream).
+  constexpr int kRowOps = TileStager<BQ, D, NW>::kPer, kColOps = TileStager<D, BQ, NW>::kPer;
+  static_assert(kRowOps == kColOps, "row and column halves issue the same number of loads");
+  constexpr int kHalfOps = 2 * kRowOps + 1;
+  auto tile_rows = [&](int it) {  // first row of tile `it` in the group's copies
+    return (uint32_t)(it / nqt) * a.Lqp + (uint32_t)(it % nqt) * BQ;
   };
+  auto tile_cols = [&](int it) {  // byte offset of tile `it` in the head_dim-major copies
+    return ((uint32_t)(it / nqt) * D * a.Lqp + (uint32_t)(it % nqt) * BQ) * 2;
+  };
+  auto row_op = [&](int it, auto bufc, int i) {
+    RowStage& rsg = decltype(bufc)::value == 0 ? rs0 : rs1;
+    const uint32_t row0 = tile_rows(it);
+    if (i < kRowOps)
+      rst.stage_one(rsg.q, rq, row0 * D * 2, i);
+    else if (i < 2 * kRowOps)
+      rst.stage_one(rsg.dout, rdo, row0 * D * 2, i - kRowOps);
+    else
+      dma4(rl2, lds_addr(rsg.lse2), lane * 4, row0 * 4);  // every wave loads the stats: no branch
+  };
+  auto col_op = [&](int it, auto bufc, int i) {
+    ColStage& csg = decltype(bufc)::value == 0 ? cs0 : cs1;
+    if (i < kColOps)
+      tst.stage_one(csg.qt, rqt, tile_cols(it), i);
+    else if (i < 2 * kColOps)
+      tst.stage_one(csg.dot, rdot, tile_cols(it), i - kColOps);
+    else
+      dma4(rnd, lds_addr(csg.ndl), lane * 4, tile_rows(it) * 4);
+  };
+  // Loads issued per wave between two consecutive waits: one row half and one
+  // column half.  Waiting until at most that many are outstanding retires the
+  // older half the coming phase reads.
+  constexpr int kInFlight = 2 * kHalfOps;
+  // Slots of a 2*KS-slot phase that issue the kHalfOps loads.
+  auto load_slot = [](int j, int nslots) { return j % 3 == 1 && j / 3 < kHalfOps && j < nslots; };
 
   const float c = a.scale_log2;
 
+  // The loop bodies below are explicitly software-pipelined: each "slot" is
+  // one MFMA plus the LDS read it needs four slots later, at most one load of
+  // the next tile, and a share of the VALU work; sched_barrier(0) pins the
+  // slot order (the scheduler would otherwise sink each read next to its
+  // MFMA and bunch the loads and the VALU work).
   auto body_p = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    wait_vmem();
-    barrier_lds();  // T: tile `it` visible in `buf`; tile it-1 fully consumed everywhere
-    stage(min(it + 1, niter - 1), std::integral_constant<int, buf ^ 1>());  // last: re-stages an unread tile
-    const Stage& sg = buf == 0 ? st0 : st1;
-    const bf16* tq = sg.q;
-    const bf16* tdot = sg.dot;
-    const float* tl = sg.lse2;
+    using NextBuf = std::integral_constant<int, buf ^ 1>;
+    wait_vmem_n<kInFlight>();  // this tile's rows landed (for this wave)
+    barrier_lds();             // T: ... for every wave; the other column half is free
+    // The wave whose phase ends in VALU-dependent work gets issue priority:
+    // P waves between T and X (softmax after QK^T), dS waves after X.
+    __builtin_amdgcn_s_setprio(2);
+    const RowStage& rsg = buf == 0 ? rs0 : rs1;
+    const ColStage& csg = buf == 0 ? cs0 : cs1;
+    const int itc = min(it + 1, niter - 1);  // column half loaded now (the last tiles re-load)
+    const int itr = min(it + 2, niter - 1);  // row half loaded after X
 
-    f32x16 s[2];
+    constexpr int NS = 2 * KS;  // QK^T MFMAs: (sub, ks)
+    auto qop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.q + (j / KS) * 32 * D + ro[j % KS]); };
+    bf16x8 qa[4];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      bf16x8 qa[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qa[ks] = *reinterpret_cast<const bf16x8*>(tq + sub * 32 * D + ro[ks]);
-      s[sub] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s[sub] = mfma32(qa[ks], kv[ks], s[sub]);
-    }
-    // Keep four operand reads in flight ahead of the QK^T MFMAs.
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
-#pragma unroll
-    for (int i = 0; i < 2 * KS - 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-    bf16x8 pb[2][2];
+    for (int j = 0; j < 4; ++j) qa[j] = qop(j);
+    // lse2 of this lane's 16 rows per sub: 8 consecutive rows per k2.
+    f32x4 l2[2][2][2];
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub)
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const f32x4 la = *reinterpret_cast<const f32x4*>(tl + 32 * sub + 16 * k2 + 8 * hh);
-        const f32x4 lb = *reinterpret_cast<const f32x4*>(tl + 32 * sub + 16 * k2 + 8 * hh + 4);
-        u32x4 up;
+      for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const int e = 2 * e2;
-          const float l0 = e < 4 ? la[e] : lb[e - 4], l1 = e < 4 ? la[e + 1] : lb[e - 3];
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e], c, -l0));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e + 1], c, -l1));
-          up[e2] = pack_bf16x2(p0, p1);
-        }
-        xp[64 * (2 * sub + k2)] = up;
-        pb[sub][k2] = bits_to_bf16x8(up);
+        for (int hf = 0; hf < 2; ++hf)
+          l2[sub][k2][hf] = *reinterpret_cast<const f32x4*>(rsg.lse2 + 32 * sub + 16 * k2 + 8 * hh + 4 * hf);
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x16 s[2] = {zero16(), zero16()};
+    bf16x8 pb[2][2];
+    u32x4 up[2][2];
+    // Softmax step (sub, k2, e2): two probabilities, packed; the last step
+    // of a (sub, k2) hands its 16 bytes to the partner wave.
+    auto smx = [&](int sub, int k2, int e2) {
+      const int e = 2 * e2;
+      const f32x4& lv = l2[sub][k2][e >> 2];
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e], c, -lv[e & 3]));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e + 1], c, -lv[(e & 3) + 1]));
+      up[sub][k2][e2] = pack_bf16x2(p0, p1);
+      if (e2 == 3) {
+        xp[64 * (2 * sub + k2)] = up[sub][k2];
+        pb[sub][k2] = bits_to_bf16x8(up[sub][k2]);
       }
-    barrier_lds();  // X: P handed over
-    // dV^T += dO^T P over the 16 (sub, k2, dt) steps, with the dO^T operand
-    // reads software-pipelined four steps ahead.
+    };
+    // Softmax steps of sub 0 (8 of them) go into the slots after S(sub 0) is
+    // complete (two slots of MFMA latency after its last MFMA).
+    constexpr int kLo = KS + 2 < NS ? KS + 2 : NS;
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int sub = j / KS, ks = j % KS;
+      s[sub] = mfma32(qa[j & 3], kv[ks], s[sub]);
+      if (j + 4 < NS) qa[j & 3] = qop(j + 4);
+      if (load_slot(j, NS)) col_op(itc, NextBuf(), j / 3);
+      if (j >= kLo) {
+        const int n = NS - kLo;
+        for (int st = (j - kLo) * 8 / n; st < (j - kLo + 1) * 8 / n; ++st) smx(0, st >> 2, st & 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = (NS + 1) / 3; i < kHalfOps; ++i) col_op(itc, NextBuf(), i);
+    if (kLo >= NS) {
+#pragma unroll
+      for (int st = 0; st < 8; ++st) smx(0, st >> 2, st & 3);
+    }
+#pragma unroll
+    for (int st = 0; st < 8; ++st) smx(1, st >> 2, st & 3);
+    wait_vmem_n<kInFlight>();  // this tile's columns landed (for this wave)
+    barrier_lds();             // X: P handed over, columns visible; this row half is free
+    __builtin_amdgcn_s_setprio(0);
+
+    // dV^T += dO^T P over the (sub, k2, dt) steps, reads four steps ahead.
     constexpr int NJ = 4 * DT;
     auto dot_op = [&](int j) {
       const int sk = j / DT, dt = j % DT;  // sk = 2*sub + k2
-      return *reinterpret_cast<const bf16x8*>(tdot + dt * 32 * BQ + to[sk]);
+      return *reinterpret_cast<const bf16x8*>(csg.dot + dt * 32 * BQ + to[sk]);
     };
-    // (sched_barrier pins this order: the scheduler would otherwise sink
-    // each read next to its MFMA.)
     bf16x8 opq[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) opq[j] = dot_op(j);
@@ -252,62 +304,104 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (j + 4 < NJ) opq[j % 4] = dot_op(j + 4);
       const int sk = j / DT, dt = j % DT;
       acc[dt] = mfma32(op, pb[sk >> 1][sk & 1], acc[dt]);
+      if (load_slot(j, NJ)) row_op(itr, bufc, j / 3);
       __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int i = (NJ + 1) / 3; i < kHalfOps; ++i) row_op(itr, bufc, i);
   };
 
   auto body_ds = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    wait_vmem();
+    using NextBuf = std::integral_constant<int, buf ^ 1>;
+    wait_vmem_n<kInFlight>();
     barrier_lds();  // T
-    stage(min(it + 1, niter - 1), std::integral_constant<int, buf ^ 1>());
-    const Stage& sg = buf == 0 ? st0 : st1;
-    const bf16* tdo = sg.dout;
-    const bf16* tqt = sg.qt;
-    const float* tn = sg.ndl;
+    __builtin_amdgcn_s_setprio(0);
+    const RowStage& rsg = buf == 0 ? rs0 : rs1;
+    const ColStage& csg = buf == 0 ? cs0 : cs1;
+    const int itc = min(it + 1, niter - 1);
+    const int itr = min(it + 2, niter - 1);
 
-    f32x16 dp[2];
+    constexpr int NS = 2 * KS;  // dO V^T MFMAs: (sub, ks)
+    auto dop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.dout + (j / KS) * 32 * D + ro[j % KS]); };
+    bf16x8 da[4];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      bf16x8 da[KS];
+    for (int j = 0; j < 4; ++j) da[j] = dop(j);
+    __builtin_amdgcn_sched_barrier(0);
+    f32x16 dp[2] = {zero16(), zero16()};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) da[ks] = *reinterpret_cast<const bf16x8*>(tdo + sub * 32 * D + ro[ks]);
-      dp[sub] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) dp[sub] = mfma32(da[ks], kv[ks], dp[sub]);
+    for (int j = 0; j < NS; ++j) {
+      const int sub = j / KS, ks = j % KS;
+      dp[sub] = mfma32(da[j & 3], kv[ks], dp[sub]);
+      if (j + 4 < NS) da[j & 3] = dop(j + 4);
+      if (load_slot(j, NS)) col_op(itc, NextBuf(), j / 3);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
 #pragma unroll
-    for (int i = 0; i < 2 * KS - 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    for (int i = (NS + 1) / 3; i < kHalfOps; ++i) col_op(itc, NextBuf(), i);
+    wait_vmem_n<kInFlight>();
+    barrier_lds();  // X: partner's P available, columns visible
+    __builtin_amdgcn_s_setprio(2);
+
+    // dS for group g = 2*sub + k2 (4 steps of two elements) interleaved with
+    // the dK^T MFMAs of group g-1; every LDS read is issued up front or four
+    // MFMAs ahead.
+    u32x4 pv[4];
+    f32x4 nd[4][2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      pv[g] = xp[64 * g];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+        nd[g][hf] = *reinterpret_cast<const f32x4*>(csg.ndl + 32 * (g >> 1) + 16 * (g & 1) + 8 * hh + 4 * hf);
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
-    barrier_lds();  // X: partner's P available
+    constexpr int NJ = 4 * DT;
+    auto qt_op = [&](int j) {
+      const int g = j / DT, dt = j % DT;
+      return *reinterpret_cast<const bf16x8*>(csg.qt + dt * 32 * BQ + to[g]);
+    };
+    bf16x8 opq[4];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+    for (int j = 0; j < 4; ++j) opq[j] = qt_op(j);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 ud[4];
+    auto dstep = [&](int g, int e2) {
+      const int sub = g >> 1, k2 = g & 1, e = 2 * e2;
+      const f32x4& nv = nd[g][e >> 2];
+      const float p0 = __uint_as_float(pv[g][e2] << 16), p1 = __uint_as_float(pv[g][e2] & 0xffff0000u);
+      ud[g][e2] = pack_bf16x2(p0 * (dp[sub][8 * k2 + e] + nv[e & 3]), p1 * (dp[sub][8 * k2 + e + 1] + nv[(e & 3) + 1]));
+    };
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2) {
-        const u32x4 up = xp[64 * (2 * sub + k2)];
-        const f32x4 na = *reinterpret_cast<const f32x4*>(tn + 32 * sub + 16 * k2 + 8 * hh);
-        const f32x4 nb = *reinterpret_cast<const f32x4*>(tn + 32 * sub + 16 * k2 + 8 * hh + 4);
-        u32x4 ud;
+    for (int e2 = 0; e2 < 4; ++e2) dstep(0, e2);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int e2 = 0; e2 < 4; ++e2) {
-          const int e = 2 * e2;
-          const float n0 = e < 4 ? na[e] : nb[e - 4], n1 = e < 4 ? na[e + 1] : nb[e - 3];
-          const float p0 = __uint_as_float(up[e2] << 16), p1 = __uint_as_float(up[e2] & 0xffff0000u);
-          ud[e2] = pack_bf16x2(p0 * (dp[sub][8 * k2 + e] + n0), p1 * (dp[sub][8 * k2 + e + 1] + n1));
-        }
-        const bf16x8 dsb = bits_to_bf16x8(ud);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          acc[dt] = mfma32(*reinterpret_cast<const bf16x8*>(tqt + dt * 32 * BQ + to[2 * sub + k2]), dsb, acc[dt]);
+    for (int j = 0; j < NJ; ++j) {
+      const int g = j / DT, dt = j % DT;
+      const bf16x8 op = opq[j % 4];
+      if (j + 4 < NJ) opq[j % 4] = qt_op(j + 4);
+      acc[dt] = mfma32(op, bits_to_bf16x8(ud[g]), acc[dt]);
+      if (g + 1 < 4) {
+        // the next group's 4 steps, spread over this group's DT MFMAs
+        for (int st = dt * 4 / DT; st < (dt + 1) * 4 / DT; ++st) dstep(g + 1, st);
       }
+      if (load_slot(j, NJ)) row_op(itr, bufc, j / 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int i = (NJ + 1) / 3; i < kHalfOps; ++i) row_op(itr, bufc, i);
   };
 
   retire_prologue_loads();
-  stage(0, std::integral_constant<int, 0>());
+  {
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+#pragma unroll
+    for (int i = 0; i < kHalfOps; ++i) row_op(0, B0(), i);
+#pragma unroll
+    for (int i = 0; i < kHalfOps; ++i) col_op(0, B0(), i);
+#pragma unroll
+    for (int i = 0; i < kHalfOps; ++i) row_op(min(1, niter - 1), B1(), i);
+  }
   if (role == 0) {
     for (int it = 0; it < niter; it += 2) {
       body_p(it, std::integral_constant<int, 0>());

@@ -21,36 +21,41 @@
 
 namespace avattn {
 
-// One workgroup = 128 query rows, 4 waves x 32 rows; K/V tiles of 64 keys.
-//
-// Per tile the waves issue both 32-key halves' QK^T MFMAs, then run each
-// half's softmax on the VALU while the other half's MFMAs (QK^T of half 1,
-// then PV of half 0) execute.  K rows and V^T come from padded copies and are
-// double-buffered in LDS: right after the barrier that opens iteration t,
-// tile t+1 is loaded straight from global memory into the other buffer (tile
-// t-1 was fully consumed before that barrier) and lands before the next one.
-// The loop body is branch-free apart from the masked-tile bias, and unrolled
-// over the two buffers so LDS addresses are per-lane bases plus immediates.
+// One workgroup = 256 query rows of one (batch, head), 8 waves x 32 rows, one
+// workgroup per CU; K/V tiles of 64 keys.  Waves 0-3 (group A) and 4-7
+// (group B) share the SIMDs pairwise and run the same per-tile work
+//   S = K Q^T (16 MFMAs), softmax (VALU), O^T += V^T P^T (16 MFMAs)
+// in a staggered order: group A does QK^T(t), softmax(t), PV(t) in iteration
+// t; group B is one tile behind and does softmax(t-1), PV(t-1), QK^T(t) (its
+// scores are carried in registers across the barrier).  Each group's softmax
+// thus runs while the other group's MFMAs keep the matrix pipe busy, and wave
+// priorities (s_setprio) give the MFMA phases first claim on issue.  K rows
+// and V^T come from padded copies through four LDS stages: tile t+2 is loaded
+// during iteration t (spread between MFMAs), tile t-1 stays resident for
+// group B.
 template <int D, bool ROPE>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
-  constexpr int BM = 128, BN = 64, NW = 4;
+__global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
+  constexpr int NW = 8, BM = 32 * NW, BN = 64;
   constexpr int KS = D / 16;  // 16-channel k-steps of q k^T
   constexpr int DT = D / 32;  // 32-channel row tiles of O^T
   constexpr int TE = BN * D;  // tile elements
-  // One LDS object per buffer of the double-buffered stage: the compiler then
-  // knows that the direct global->LDS loads into one buffer do not alias the
-  // LDS reads of the other, and does not wait for the next tile's loads
-  // before reading the current one.
+  // One LDS object per stage (the compiler never sees the tile loads, which
+  // are ordered by the explicit waits and barriers below).
   struct Stage {
-    bf16 k[TE];       // K rows: TileLayout<D>
-    bf16 vt[TE];      // V^T rows (channel-major): TileLayout<BN>
-    float bias[BN];   // key bias
-    int flags[64];    // "all attended" flags of the tile's two 32-key halves (and beyond)
+    bf16 k[TE];      // K rows: TileLayout<D>
+    bf16 vt[TE];     // V^T rows (channel-major): TileLayout<BN>
+    float bias[BN];  // key bias
+    int flags[64];   // "all attended" flags of the tile's two 32-key halves (and beyond)
   };
-  __shared__ __attribute__((aligned(16))) Stage st0, st1;
+  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
+  auto stage_ref = [&](auto bufc) __attribute__((always_inline)) -> Stage& {
+    constexpr int buf = decltype(bufc)::value;
+    return buf == 0 ? st0 : (buf == 1 ? st1 : (buf == 2 ? st2 : st3));
+  };
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
   const int prow = perm23(l32);  // K row this lane supplies to S^T = K Q^T
 
@@ -73,22 +78,26 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
   // Flags are padded by 64 entries: the 64 read from a tile start stay inside.
   const u32x4 rf = make_rsrc(a.kfull + (int64_t)b * (a.Lkp / 32), (uint32_t)(a.Lkp / 32 + 64) * 4);
   const int nkt = a.Lkp / BN;
-  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
 
-  TileStager<BN, D, NW> kst;  // 64 K rows of D channels (row stride D)
-  TileStager<D, BN, NW> vst;  // D V^T rows of 64 keys (row stride Lkp)
-  kst.init(D, wave_u, lane);
-  vst.init(a.Lkp, wave_u, lane);
-  auto stage = [&](int t, Stage& sg) {
+  using KSt = TileStager<BN, D, NW>;  // 64 K rows of D channels (row stride D)
+  using VSt = TileStager<D, BN, NW>;  // D V^T rows of 64 keys (row stride Lkp)
+  KSt kst;
+  VSt vst;
+  kst.init(D, wave, lane);
+  vst.init(a.Lkp, wave, lane);
+  constexpr int kStageOps = KSt::kPer + VSt::kPer + 2;  // loads per wave per tile
+  auto stage_op = [&](int t, auto bufc, int i) __attribute__((always_inline)) {
+    Stage& sg = stage_ref(bufc);
     const uint32_t k0 = (uint32_t)t * BN;
-    kst.stage(sg.k, rk, k0 * D * 2);
-    vst.stage(sg.vt, rv, k0 * 2);
-    dma4(rb, lds_addr(sg.bias), lane * 4, k0 * 4);
-    dma4(rf, lds_addr(sg.flags), lane * 4, (uint32_t)t * 8);
+    if (i < KSt::kPer)
+      kst.stage_one(sg.k, rk, k0 * D * 2, i);
+    else if (i < KSt::kPer + VSt::kPer)
+      vst.stage_one(sg.vt, rv, k0 * 2, i - KSt::kPer);
+    else if (i == kStageOps - 2)
+      dma4(rb, lds_addr(sg.bias), lane * 4, k0 * 4);
+    else
+      dma4(rf, lds_addr(sg.flags), lane * 4, (uint32_t)t * 8);
   };
-
-  // Prologue loads, then Q (rotated on load) while they fly.
-  stage(0, st0);
 
   // Q fragments: B operand of S^T = K Q^T; lane holds row qrow, channels
   // 16*ks + 8*hh + [0, 8).
@@ -131,37 +140,37 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int i = 0; i < DT; ++i) acc[i] = zero16();
 
-  auto body = [&](int t, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    wait_vmem();
-    barrier_lds();  // tile t visible in `buf`; tile t-1 fully consumed everywhere
-    // the last iteration re-stages a tile nobody reads
-    stage(min(t + 1, nkt - 1), buf == 0 ? st1 : st0);
-    const Stage& sg = buf == 0 ? st0 : st1;
-    const int full[2] = {__builtin_amdgcn_readfirstlane(sg.flags[0]), __builtin_amdgcn_readfirstlane(sg.flags[1])};
-    const bf16* kl = sg.k;
-    const bf16* vl = sg.vt;
-    const float* bl = sg.bias;
-
-    // S^T of both 32-key halves: sh[half][8*k2 + e] is the score of key
-    // 32*half + 16*k2 + 8*hh + e against this lane's query.
-    f32x16 sh[2];
+  // The 2*KS QK^T MFMAs of a tile: sh[half][8*k2 + e] is the score of key
+  // 32*half + 16*k2 + 8*hh + e against this lane's query.  K operand reads
+  // run four MFMAs ahead; `slot(j)` runs extra work after MFMA j.
+  // sched_barrier(0) pins the order (the scheduler would otherwise sink each
+  // read next to its MFMA).
+  auto scores = [&](const Stage& sg, f32x16* sh, auto&& slot) __attribute__((always_inline)) {
+    constexpr int NS = 2 * KS;
+    auto kop = [&](int j) __attribute__((always_inline)) { return *reinterpret_cast<const bf16x8*>(sg.k + (j / KS) * 32 * D + ko[j % KS]); };
+    bf16x8 ka[4];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      bf16x8 ka[KS];
+    for (int j = 0; j < 4; ++j) ka[j] = kop(j);
+    sh[0] = zero16();
+    sh[1] = zero16();
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) ka[ks] = *reinterpret_cast<const bf16x8*>(kl + hf * 32 * D + ko[ks]);
-      sh[hf] = zero16();
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) sh[hf] = mfma32(ka[ks], qf[ks], sh[hf]);
+    for (int j = 0; j < NS; ++j) {
+      sh[j / KS] = mfma32(ka[j & 3], qf[j % KS], sh[j / KS]);
+      if (j + 4 < NS) ka[j & 3] = kop(j + 4);
+      slot(j);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  // Softmax of one tile's scores (both halves) into the bf16 PV operands.
+  auto softmax = [&](const Stage& sg, f32x16* sh, bf16x8 (*pf)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       f32x16& s_cur = sh[hf];
-      if (!full[hf]) {
+      if (!__builtin_amdgcn_readfirstlane(sg.flags[hf])) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 bb = *reinterpret_cast<const f32x4*>(bl + hf * 32 + 16 * (g >> 1) + 8 * hh + 4 * (g & 1));
+          const f32x4 bb = *reinterpret_cast<const f32x4*>(sg.bias + hf * 32 + 16 * (g >> 1) + 8 * hh + 4 * (g & 1));
 #pragma unroll
           for (int r = 0; r < 4; ++r) s_cur[4 * g + r] += bb[r];
         }
@@ -182,8 +191,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
         m_run = mx;
       }
       const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
-
-      bf16x8 pf[2];
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         u32x4 u;
@@ -198,24 +205,115 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(FwdArgs a) {
             l_run0 += p0 + p1;
           u[e2] = pack_bf16x2(p0, p1);
         }
-        pf[k2] = bits_to_bf16x8(u);
+        pf[hf][k2] = bits_to_bf16x8(u);
       }
-
-      // O^T += V^T P^T.  B operand slot (hh, e) of pf[k2] is key
-      // 32*hf + 16*k2 + 8*hh + e: one 16-byte chunk of a V^T row.
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-          acc[dt] = mfma32(*reinterpret_cast<const bf16x8*>(vl + dt * 32 * BN + vo[2 * hf + k2]), pf[k2], acc[dt]);
     }
+  };
+  // O^T += V^T P^T over the (half, k2, dt) steps; B operand slot (hh, e) of
+  // pf[hf][k2] is key 32*hf + 16*k2 + 8*hh + e: one 16-byte chunk of a V^T
+  // row.  Reads four MFMAs ahead; `slot(j)` runs extra work after MFMA j.
+  auto pv = [&](const Stage& sg, bf16x8 (*pf)[2], auto&& slot) __attribute__((always_inline)) {
+    constexpr int NJ = 4 * DT;
+    auto vop = [&](int j) __attribute__((always_inline)) {
+      const int sk = j / DT, dt = j % DT;
+      return *reinterpret_cast<const bf16x8*>(sg.vt + dt * 32 * BN + vo[sk]);
+    };
+    bf16x8 va[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) va[j] = vop(j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int sk = j / DT, dt = j % DT;
+      acc[dt] = mfma32(va[j & 3], pf[sk >> 1][sk & 1], acc[dt]);
+      if (j + 4 < NJ) va[j & 3] = vop(j + 4);
+      slot(j);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto no_slot = [](int) __attribute__((always_inline)) {};
+
+  // Top of iteration t: tile t has landed (its loads were issued two
+  // iterations ago; only tile t+1's may still be in flight) for every wave;
+  // the stage tile t-2 used is free for tile t+2.
+  auto top = [&]() __attribute__((always_inline)) {
+    wait_vmem_n<kStageOps>();
+    barrier_lds();
+  };
+  auto loads_in = [&](int t, auto nextc) __attribute__((always_inline)) {  // tile t's loads, one after each of the first MFMAs
+    return [&, t, nextc](int j) __attribute__((always_inline)) {
+      if (j < kStageOps) stage_op(t, nextc, j);
+    };
   };
 
   retire_prologue_loads();
-  for (int t = 0; t < nkt; t += 2) {
-    body(t, std::integral_constant<int, 0>());
-    if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());
+  {
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+#pragma unroll
+    for (int i = 0; i < kStageOps; ++i) stage_op(0, B0(), i);
+#pragma unroll
+    for (int i = 0; i < kStageOps; ++i) stage_op(min(1, nkt - 1), B1(), i);
   }
+
+  f32x16 sh[2];
+  bf16x8 pf[2][2];
+  if (wave < NW / 2) {
+    // Group A: QK^T(t), softmax(t), PV(t).
+    auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      using Next2 = std::integral_constant<int, (buf + 2) % 4>;
+      top();
+      const Stage& sg = stage_ref(bufc);
+      __builtin_amdgcn_s_setprio(2);
+      scores(sg, sh, loads_in(min(t + 2, nkt - 1), Next2()));
+      __builtin_amdgcn_s_setprio(0);
+      softmax(sg, sh, pf);
+      __builtin_amdgcn_s_setprio(2);
+      pv(sg, pf, no_slot);
+    };
+    for (int t = 0; t < nkt; t += 4) {
+      body(t, std::integral_constant<int, 0>());
+      if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());
+      if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 2>());
+      if (t + 3 < nkt) body(t + 3, std::integral_constant<int, 3>());
+    }
+  } else {
+    // Group B: softmax(t-1), PV(t-1), QK^T(t); the scores of tile t are
+    // carried to the next iteration.
+    auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      using Prev = std::integral_constant<int, (buf + 3) % 4>;
+      using Next2 = std::integral_constant<int, (buf + 2) % 4>;
+      top();
+      const Stage& sp = stage_ref(Prev());
+      __builtin_amdgcn_s_setprio(0);
+      softmax(sp, sh, pf);
+      __builtin_amdgcn_s_setprio(2);
+      pv(sp, pf, loads_in(min(t + 2, nkt - 1), Next2()));
+      scores(stage_ref(bufc), sh, no_slot);
+    };
+    {
+      // Iteration 0: only QK^T(0).
+      using B0 = std::integral_constant<int, 0>;
+      top();
+      scores(stage_ref(B0()), sh, loads_in(min(2, nkt - 1), std::integral_constant<int, 2>()));
+    }
+    for (int t = 1; t < nkt; t += 4) {
+      body(t, std::integral_constant<int, 1>());
+      if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 2>());
+      if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 3>());
+      if (t + 3 < nkt) body(t + 3, std::integral_constant<int, 0>());
+    }
+    // Tail: softmax and PV of the last tile (its stage is not refilled).
+    const int bl = (nkt - 1) % 4;
+    const Stage& sl = bl == 0 ? st0 : (bl == 1 ? st1 : (bl == 2 ? st2 : st3));
+    __builtin_amdgcn_s_setprio(0);
+    softmax(sl, sh, pf);
+    pv(sl, pf, no_slot);
+  }
+  __builtin_amdgcn_s_setprio(0);
+  wait_vmem();  // the last (re-staged) tile loads
 
   const float l_tot = halves_sum(l_run0 + l_run1);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -262,9 +360,9 @@ static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
     if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, nullptr, a.vt, stream);
     if (e != hipSuccess) return e;
   }
-  const int nqt = (a.Lq + 127) / 128;
+  const int nqt = (a.Lq + 255) / 256;
   const dim3 grid(nqt * a.B * a.Hq);
-  const dim3 block(256);
+  const dim3 block(512);
   LaunchTimer timer(kKidFwd, stream);
   if (a.cos_q != nullptr)
     hipLaunchKernelGGL((attn_fwd_kernel<D, true>), grid, block, 0, stream, a);

@@ -257,9 +257,13 @@ struct TileStager {
   }
   // `soff`: byte offset of the tile's first row in the buffer.
   __device__ __forceinline__ void stage(bf16* lds, const u32x4& r, uint32_t soff) const {
-    const uint32_t base = lds_addr(lds) + lds0;
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) dma16(r, base + i * kRpi * RL * 2, off[i], soff);
+    for (int i = 0; i < kPer; ++i) stage_one(lds, r, soff, i);
+  }
+  // Instruction i of stage() alone (i < kPer), for spreading a tile's loads
+  // between other work.
+  __device__ __forceinline__ void stage_one(bf16* lds, const u32x4& r, uint32_t soff, int i) const {
+    dma16(r, lds_addr(lds) + lds0 + i * kRpi * RL * 2, off[i], soff);
   }
 };
 
