@@ -3,8 +3,8 @@
 //   1. preprocess: per query row, lse2 = lse * log2(e) and
 //      ndelta = -rowsum(dout * out) (the `D` term of dS = P * (dP - D)), in
 //      arrays padded to whole 64-row tiles (+inf / 0 past the end so padded
-//      rows get P = 0); plus head_dim-major copies of q, dout and k
-//      (transpose.hip);
+//      rows get P = 0); plus the padded row-major and head_dim-major operand
+//      copies (prep.hip);
 //   2. dK/dV: one workgroup per 128 keys (32 per wave, kept in registers as
 //      MFMA operands); loops over 64-row query tiles of every query head
 //      that reads this KV head;

@@ -1,7 +1,6 @@
-// Flash-style attention forward for gfx950: one workgroup = 128 query rows of
-// one (batch, head); four waves own 32 rows each; K streams through LDS in
-// 64-key row-major tiles and V in 64-key head_dim-major tiles (from the
-// padded copies made by prep.hip), double-buffered.
+// Flash-style attention forward for gfx950.  K streams through LDS in 64-key
+// row-major tiles and V in 64-key head_dim-major tiles, both from the padded
+// copies made by prep.hip.
 //
 // Per wave and tile the scores are computed transposed, S^T = K Q^T, so that
 // each lane owns one query column (query = lane % 32) and holds 32 of that

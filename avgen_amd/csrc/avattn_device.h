@@ -144,19 +144,19 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
 // With these, sixteen lanes reading one chunk each of 16 distinct rows in an
 // aligned group of 16 (ds_read_b128) touch all 64 banks exactly once, and a
 // 1 KB block of consecutive rows can be filled by one direct global->LDS
-// wave load (stage_direct).  Row-major sequence tiles use RL = head_dim;
+// wave load (TileStager).  Row-major sequence tiles use RL = head_dim;
 // head_dim-major ("transposed") tiles use RL = the tile's sequence length.
 template <int RL>
 struct TileLayout {
   static_assert(RL == 32 || RL == 64 || RL == 128, "row length 32, 64 or 128 elements");
   static constexpr int kRowElems = RL;
-  static __device__ __forceinline__ int swz(int row) {
+  static __host__ __device__ __forceinline__ int swz(int row) {
     if constexpr (RL == 128) return ((row & 3) << 2) | ((row >> 2) & 3);
     if constexpr (RL == 64) return (((row >> 1) & 1) << 2) | ((row >> 2) & 3);
     return (row >> 2) & 3;
   }
   // Element offset of (row, col); col must be a multiple of 4.
-  static __device__ __forceinline__ int off(int row, int col) {
+  static __host__ __device__ __forceinline__ int off(int row, int col) {
     return row * RL + (((col >> 3) ^ swz(row)) << 3) + (col & 7);
   }
 };
@@ -167,7 +167,7 @@ struct TileLayout {
 // 16*k2 + 8*(l/32) + e, e = 0..7: eight *consecutive* rows per 16-row k-step,
 // which is exactly the k order of an A (or B) operand read as one 16-byte
 // chunk from a transposed (sequence-contiguous) tile.
-__device__ __forceinline__ int perm23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
+__host__ __device__ __forceinline__ int perm23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
 // 8 consecutive elements (one 16-byte chunk) of one row of a TileLayout<RL>
 // tile: an MFMA operand whose k index runs along the row.
@@ -246,14 +246,24 @@ struct TileStager {
   uint32_t off[kPer];  // byte offset of this lane's source chunk, per instruction
   uint32_t lds0;       // byte offset of this wave's first LDS block in the tile
 
+  // First instruction of wave `wave` (instructions first .. first+kPer-1).
+  static __host__ __device__ __forceinline__ int first_instr(int wave) { return (wave * kPer) % kNi; }
+  // Tile row whose chunk lane `lane` moves in instruction `instr`.
+  static __host__ __device__ __forceinline__ int row_of(int instr, int lane) {
+    return instr * kRpi + lane / kCpr;
+  }
+  // Byte offset (from the tile's first source row) of the 16-byte source chunk
+  // lane `lane` moves in instruction `instr`: the logical chunk stored at
+  // physical slot lane % kCpr of its row.
+  static __host__ __device__ __forceinline__ uint32_t src_offset(int instr, int lane, int64_t row_stride) {
+    const int row = row_of(instr, lane);
+    return (uint32_t)((row * row_stride + ((lane % kCpr) ^ TileLayout<RL>::swz(row)) * 8) * 2);
+  }
   __device__ __forceinline__ void init(int64_t row_stride, int wave, int lane) {
-    const int first = (wave * kPer) % kNi;
+    const int first = first_instr(wave);
     lds0 = __builtin_amdgcn_readfirstlane((uint32_t)(first * kRpi * RL * 2));
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int row = (first + i) * kRpi + lane / kCpr;
-      off[i] = (uint32_t)((row * row_stride + ((lane % kCpr) ^ TileLayout<RL>::swz(row)) * 8) * 2);
-    }
+    for (int i = 0; i < kPer; ++i) off[i] = src_offset(first + i, lane, row_stride);
   }
   // `soff`: byte offset of the tile's first row in the buffer.
   __device__ __forceinline__ void stage(bf16* lds, const u32x4& r, uint32_t soff) const {

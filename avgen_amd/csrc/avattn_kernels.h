@@ -27,7 +27,7 @@ struct FwdArgs {
   bf16* o;
   int64_t osb, osh, osl;
   float* lse;
-  // Padded copies (transpose.hip), written by the launcher: k rows, element
+  // Padded copies (prep.hip), written by the launcher: k rows, element
   // (b, h, j, d) at ((b*Hkv + h)*Lkp + j)*D + d; v head_dim-major, element
   // (b, h, d, j) at ((b*Hkv + h)*D + d)*Lkp + j.
   bf16* kr;
@@ -64,7 +64,7 @@ struct BwdArgs {
   // Per query row (b, hq, i) at index (b*Hq + hq)*Lqp + i, i < Lqp:
   float* ndelta;  // -rowsum(dout * out); 0 for padded rows
   float* lse2;    // lse * log2(e); +inf for rows with lse == -inf and padded rows
-  // Padded copies (transpose.hip) with H/Lp = Hq/Lqp (q, dout) or Hkv/Lkp
+  // Padded copies (prep.hip) with H/Lp = Hq/Lqp (q, dout) or Hkv/Lkp
   // (k, v): row copies (*r) hold element (b, h, j, d) at ((b*H + h)*Lp + j)*D
   // + d, head_dim-major copies (*t) at ((b*H + h)*D + d)*Lp + j.
   bf16* qr;
@@ -104,7 +104,7 @@ class LaunchTimer {
   hipStream_t stream_;
 };
 
-// Sequence length of a head_dim-major copy (transpose.hip): padded to whole
+// Sequence length of a head_dim-major copy (prep.hip): padded to whole
 // 64-row tiles.
 inline int transpose_padded_len(int L) { return (L + 63) / 64 * 64; }
 
