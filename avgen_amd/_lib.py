@@ -39,6 +39,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr],
     ),
     "avattn_fwd_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32]),
+    "avattn_fwd_fp8": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr,
+         c_f32,
+         c_ptr, c_i64p,
+         c_ptr,
+         c_ptr, c_size,
+         c_ptr],
+    ),
+    "avattn_fwd_fp8_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32]),
+    "avattn_fp8_absmax_scales": (ctypes.c_int, [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr]),
     "avattn_bwd_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "avattn_bwd": (
         ctypes.c_int,
@@ -147,6 +161,8 @@ KERNEL_IDS = {
     "rope_apply": 5,
     "rope_tables": 6,
     "transpose": 7,
+    "attn_fwd_fp8": 8,
+    "fp8_absmax": 9,
 }
 
 

@@ -33,6 +33,7 @@ __all__ = [
     "BACKEND",
     "attention",
     "attention_backends",
+    "attention_fp8",
     "device_arch",
     "key_padding_mask",
     "rotary_attention",
@@ -195,4 +196,37 @@ def rotary_attention(
     k_rot = ops.rope_apply(key, kt.cos, kt.sin, False)
     mask = _as_key_mask(attn_mask, query.shape[0], query.shape[-2], key.shape[-2])
     out, _ = ops.flash_fwd(query, k_rot, value, mask, tables.cos, tables.sin, ops.default_scale(query.shape[-1]))
+    return out
+
+
+def attention_fp8(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    attn_mask: torch.Tensor | None = None,
+    enable_gqa: bool = False,
+    q_scale: torch.Tensor | None = None,
+    k_scale: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """:func:`attention` with q k^T on fp8 (OCP e4m3) operands: the
+    sampling-time variant (forward only; no reference counterpart, whose
+    attention is bf16 throughout).
+
+    ``q_scale`` / ``k_scale`` are per-head dequantization scales, fp32
+    ``(heads,)`` / ``(kv_heads,)`` on the GPU; each defaults to the head's
+    absmax / 448 (:func:`avgen_amd.ops.fp8_absmax_scales`), computed on the
+    GPU for this call.  Scores are ``(e4m3(q/q_scale) . e4m3(k/k_scale)) *
+    q_scale * k_scale / sqrt(head_dim)``; P, V and the output accumulation
+    are those of :func:`attention`.  Other arguments as for :func:`attention`.
+    """
+    if query.shape[-2] == 0 or key.shape[-2] == 0:
+        return torch.zeros_like(query)
+    _validate(query, key, value, 0.0, False, enable_gqa)
+    mask = _as_key_mask(attn_mask, query.shape[0], query.shape[-2], key.shape[-2])
+    if q_scale is None:
+        q_scale = ops.fp8_absmax_scales(query)
+    if k_scale is None:
+        k_scale = ops.fp8_absmax_scales(key)
+    out, _ = ops.flash_fwd_fp8(query, key, value, mask, q_scale, k_scale, ops.default_scale(query.shape[-1]))
     return out

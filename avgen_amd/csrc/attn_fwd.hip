@@ -32,17 +32,26 @@ namespace avattn {
 // and V^T come from padded copies through four LDS stages: tile t+2 is loaded
 // during iteration t (spread between MFMAs), tile t-1 stays resident for
 // group B.
-template <int D, bool ROPE>
+//
+// FP8: q k^T on e4m3 operands (v_mfma_f32_32x32x64_f8f6f4, twice the bf16
+// rate): q is quantized on load with its head's scale, K comes from the e4m3
+// copy (fp8.hip), and the per-head scales fold into the softmax constant and
+// the LSE.  P, V and O^T += V^T P^T stay bf16 / fp32 as above.
+template <int D, bool ROPE, bool FP8>
 __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
+  static_assert(!(ROPE && FP8), "the fp8 variant takes rotated q");
   constexpr int NW = 8, BM = 32 * NW, BN = 64;
-  constexpr int KS = D / 16;  // 16-channel k-steps of q k^T
+  // k-steps of q k^T: 16 bf16 channels (32x32x16 bf16) or 64 fp8 channels
+  // (32x32x64 e4m3) per MFMA.
+  constexpr int KS = FP8 ? D / 64 : D / 16;
+  constexpr int KRL = FP8 ? D / 2 : D;  // K tile row in 2-byte units (an fp8 row is D bytes)
   constexpr int DT = D / 32;  // 32-channel row tiles of O^T
   constexpr int TE = BN * D;  // tile elements
   // One LDS object per stage (the compiler never sees the tile loads, which
   // are ordered by the explicit waits and barriers below).
   struct Stage {
-    bf16 k[TE];      // K rows: TileLayout<D>
-    bf16 vt[TE];     // V^T rows (channel-major): TileLayout<BN>
+    bf16 k[BN * KRL];  // K rows: TileLayout<KRL> (bf16, or e4m3 byte pairs)
+    bf16 vt[TE];       // V^T rows (channel-major): TileLayout<BN>
     float bias[BN];  // key bias
     int flags[64];   // "all attended" flags of the tile's two 32-key halves (and beyond)
   };
@@ -71,25 +80,26 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
 
   const int64_t bhk = (int64_t)(b * a.Hkv + hk);
   const uint32_t slice = (uint32_t)a.Lkp * D * 2;  // bytes of one (b, h) slice of a copy
-  const u32x4 rk = make_rsrc(a.kr + bhk * a.Lkp * D, slice);
+  const bf16* kcopy = FP8 ? reinterpret_cast<const bf16*>(a.k8) : a.kr;
+  const u32x4 rk = make_rsrc(kcopy + bhk * a.Lkp * KRL, (uint32_t)a.Lkp * KRL * 2);
   const u32x4 rv = make_rsrc(a.vt + bhk * D * a.Lkp, slice);
   const u32x4 rb = make_rsrc(a.kbias + (int64_t)b * a.Lkp, (uint32_t)(a.Lkp + 64) * 4);
   // Flags are padded by 64 entries: the 64 read from a tile start stay inside.
   const u32x4 rf = make_rsrc(a.kfull + (int64_t)b * (a.Lkp / 32), (uint32_t)(a.Lkp / 32 + 64) * 4);
   const int nkt = a.Lkp / BN;
 
-  using KSt = TileStager<BN, D, NW>;  // 64 K rows of D channels (row stride D)
+  using KSt = TileStager<BN, KRL, NW>;  // 64 K rows of D channels
   using VSt = TileStager<D, BN, NW>;  // D V^T rows of 64 keys (row stride Lkp)
   KSt kst;
   VSt vst;
-  kst.init(D, wave, lane);
+  kst.init(KRL, wave, lane);
   vst.init(a.Lkp, wave, lane);
   constexpr int kStageOps = KSt::kPer + VSt::kPer + 2;  // loads per wave per tile
   auto stage_op = [&](int t, auto bufc, int i) __attribute__((always_inline)) {
     Stage& sg = stage_ref(bufc);
     const uint32_t k0 = (uint32_t)t * BN;
     if (i < KSt::kPer)
-      kst.stage_one(sg.k, rk, k0 * D * 2, i);
+      kst.stage_one(sg.k, rk, k0 * KRL * 2, i);
     else if (i < KSt::kPer + VSt::kPer)
       vst.stage_one(sg.vt, rv, k0 * 2, i - KSt::kPer);
     else if (i == kStageOps - 2)
@@ -99,9 +109,34 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   };
 
   // Q fragments: B operand of S^T = K Q^T; lane holds row qrow, channels
-  // 16*ks + 8*hh + [0, 8).
-  bf16x8 qf[KS];
-  {
+  // 16*ks + 8*hh + [0, 8) (bf16), or 64*ks + 32*hh + [0, 32) (e4m3 bytes in
+  // channel order, the same order the K operand reads).
+  using QFrag = std::conditional_t<FP8, i32x8, bf16x8>;
+  QFrag qf[KS];
+  float c = a.scale_log2, sc = a.scale;  // softmax constants on raw q.k
+  if constexpr (FP8) {
+    const float qs = a.q_scale[h];
+    const float qk = qs * a.k_scale[hk];
+    c *= qk;
+    sc *= qk;
+    const float qinv = 1.f / qs;
+    const bf16* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)qrow * a.qsl + 32 * hh;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      i32x8 x = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (qvalid) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(qp + 64 * ks + 8 * q4);
+          x[2 * q4] = (int)pack_fp8x4(bf16_lo(w[0]) * qinv, bf16_hi(w[0]) * qinv, bf16_lo(w[1]) * qinv,
+                                      bf16_hi(w[1]) * qinv);
+          x[2 * q4 + 1] = (int)pack_fp8x4(bf16_lo(w[2]) * qinv, bf16_hi(w[2]) * qinv, bf16_lo(w[3]) * qinv,
+                                          bf16_hi(w[3]) * qinv);
+        }
+      }
+      qf[ks] = x;
+    }
+  } else {
     const bf16* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)qrow * a.qsl + 8 * hh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -120,14 +155,18 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   }
 
   // Loop-invariant per-lane LDS element offsets.
-  int ko[KS];  // K row perm23(l32), chunk 16*ks + 8*hh
+  constexpr int KC = FP8 ? 2 : 1;  // 16-byte chunks per K operand
+  int ko[KS * KC];  // K row perm23(l32): chunk 16*ks + 8*hh, or chunks 32*ks + 16*hh + {0, 8} (fp8)
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) ko[ks] = TileLayout<D>::off(prow, 16 * ks + 8 * hh);
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int cc = 0; cc < KC; ++cc)
+      ko[KC * ks + cc] = FP8 ? TileLayout<KRL>::off(prow, 32 * ks + 16 * hh + 8 * cc)
+                             : TileLayout<KRL>::off(prow, 16 * ks + 8 * hh);
   int vo[4];  // V^T row l32 (+32*dt), key chunk 16*j + 8*hh (j = 2*half + k2)
 #pragma unroll
   for (int j = 0; j < 4; ++j) vo[j] = TileLayout<BN>::off(l32, 16 * j + 8 * hh);
 
-  const float c = a.scale_log2;
   // Lazy rescaling: the reference max m_run only moves when a half-tile's
   // max exceeds it by more than 8 in log2 units, so probabilities stay
   // <= 2^8 (exact in fp32/bf16 range) and the O rescale is rare after the
@@ -146,17 +185,30 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   // read next to its MFMA).
   auto scores = [&](const Stage& sg, f32x16* sh, auto&& slot) __attribute__((always_inline)) {
     constexpr int NS = 2 * KS;
-    auto kop = [&](int j) __attribute__((always_inline)) { return *reinterpret_cast<const bf16x8*>(sg.k + (j / KS) * 32 * D + ko[j % KS]); };
-    bf16x8 ka[4];
+    constexpr int R = NS < 4 ? NS : 4;  // operand reads in flight
+    auto kop = [&](int j) __attribute__((always_inline)) {
+      const bf16* base = sg.k + (j / KS) * 32 * KRL;
+      if constexpr (FP8) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(base + ko[2 * (j % KS)]);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(base + ko[2 * (j % KS) + 1]);
+        return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+      } else {
+        return *reinterpret_cast<const bf16x8*>(base + ko[j % KS]);
+      }
+    };
+    QFrag ka[R];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ka[j] = kop(j);
+    for (int j = 0; j < R; ++j) ka[j] = kop(j);
     sh[0] = zero16();
     sh[1] = zero16();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
-      sh[j / KS] = mfma32(ka[j & 3], qf[j % KS], sh[j / KS]);
-      if (j + 4 < NS) ka[j & 3] = kop(j + 4);
+      if constexpr (FP8)
+        sh[j / KS] = mfma32_fp8(ka[j % R], qf[j % KS], sh[j / KS]);
+      else
+        sh[j / KS] = mfma32(ka[j % R], qf[j % KS], sh[j / KS]);
+      if (j + R < NS) ka[j % R] = kop(j + R);
       slot(j);
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -244,6 +296,12 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
       if (j < kStageOps) stage_op(t, nextc, j);
     };
   };
+  // Every wave issues exactly kStageOps loads per iteration (the counted
+  // waits rely on it): the loop a group hands its loads to has that many
+  // MFMA slots.  The fp8 q k^T has too few (4 per tile), so there the loads
+  // ride on PV.
+  static_assert(kStageOps <= 4 * DT, "tile loads must fit the PV slots");
+  static_assert(FP8 || kStageOps <= 2 * KS, "tile loads must fit the q k^T slots");
 
   retire_prologue_loads();
   {
@@ -265,11 +323,17 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
       top();
       const Stage& sg = stage_ref(bufc);
       __builtin_amdgcn_s_setprio(2);
-      scores(sg, sh, loads_in(min(t + 2, nkt - 1), Next2()));
+      if constexpr (FP8)
+        scores(sg, sh, no_slot);
+      else
+        scores(sg, sh, loads_in(min(t + 2, nkt - 1), Next2()));
       __builtin_amdgcn_s_setprio(0);
       softmax(sg, sh, pf);
       __builtin_amdgcn_s_setprio(2);
-      pv(sg, pf, no_slot);
+      if constexpr (FP8)
+        pv(sg, pf, loads_in(min(t + 2, nkt - 1), Next2()));
+      else
+        pv(sg, pf, no_slot);
     };
     for (int t = 0; t < nkt; t += 4) {
       body(t, std::integral_constant<int, 0>());
@@ -295,8 +359,15 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
     {
       // Iteration 0: only QK^T(0).
       using B0 = std::integral_constant<int, 0>;
+      using B2 = std::integral_constant<int, 2>;
       top();
-      scores(stage_ref(B0()), sh, loads_in(min(2, nkt - 1), std::integral_constant<int, 2>()));
+      if constexpr (FP8) {
+        scores(stage_ref(B0()), sh, no_slot);
+#pragma unroll
+        for (int i = 0; i < kStageOps; ++i) stage_op(min(2, nkt - 1), B2(), i);
+      } else {
+        scores(stage_ref(B0()), sh, loads_in(min(2, nkt - 1), B2()));
+      }
     }
     for (int t = 1; t < nkt; t += 4) {
       body(t, std::integral_constant<int, 1>());
@@ -318,7 +389,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (qvalid) {
     if (hh == 0) {
-      const float lse = l_tot > 0.f ? fmaf(m_run, a.scale, logf(l_tot)) : kNegInf;
+      const float lse = l_tot > 0.f ? fmaf(m_run, sc, logf(l_tot)) : kNegInf;
       a.lse[(int64_t)bh * a.Lq + qrow] = lse;
     }
     bf16* op = a.o + b * a.osb + h * a.osh + (int64_t)qrow * a.osl;
@@ -352,21 +423,26 @@ __global__ void attn_empty_kernel(bf16* o, int64_t osb, int64_t osh, int64_t osl
 
 template <int D>
 static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
+  const bool fp8 = a.k8 != nullptr;
   {
     LaunchTimer timer(kKidTranspose, stream);
     hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
-    if (e == hipSuccess) e = launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream);
+    if (e == hipSuccess)
+      e = fp8 ? launch_quantize_rows(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.k_scale, a.k8, stream)
+              : launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream);
     if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, nullptr, a.vt, stream);
     if (e != hipSuccess) return e;
   }
   const int nqt = (a.Lq + 255) / 256;
   const dim3 grid(nqt * a.B * a.Hq);
   const dim3 block(512);
-  LaunchTimer timer(kKidFwd, stream);
-  if (a.cos_q != nullptr)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, true>), grid, block, 0, stream, a);
+  LaunchTimer timer(fp8 ? kKidFwdFp8 : kKidFwd, stream);
+  if (fp8)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false, true>), grid, block, 0, stream, a);
+  else if (a.cos_q != nullptr)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, true, false>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

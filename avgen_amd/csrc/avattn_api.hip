@@ -46,12 +46,14 @@ struct FwdWorkspace {
   size_t kr, vt, kbias, kfull, total;
 };
 
-FwdWorkspace fwd_workspace(int32_t B, int32_t Hkv, int32_t Lk, int32_t D) {
+// The fp8 forward has the e4m3 k rows (one byte per element) in place of
+// the bf16 ones.
+FwdWorkspace fwd_workspace(int32_t B, int32_t Hkv, int32_t Lk, int32_t D, bool fp8 = false) {
   FwdWorkspace w{};
   const size_t Lkp = transpose_padded_len(Lk);
   const size_t kcopy = round256((size_t)B * Hkv * D * Lkp * sizeof(bf16));
   w.kr = 0;
-  w.vt = w.kr + kcopy;
+  w.vt = w.kr + (fp8 ? round256((size_t)B * Hkv * D * Lkp) : kcopy);
   w.kbias = w.vt + kcopy;
   w.kfull = w.kbias + kbias_bytes(B, Lkp);
   w.total = w.kfull + kfull_bytes(B, Lkp);
@@ -110,14 +112,19 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 2; }
+int avattn_abi_version(void) { return 3; }
 
-int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_strides, const int64_t* k_strides,
-               const int64_t* v_strides, int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
-               int32_t len_k, int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
-               const float* rope_cos_q, const float* rope_sin_q, int64_t rope_batch_stride, float scale, void* out,
-               const int64_t* out_strides, float* lse, void* workspace, size_t workspace_bytes,
-               avattn_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// avattn_fwd and avattn_fwd_fp8 (q_scale/k_scale non-null selects fp8).
+int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strides, const int64_t* k_strides,
+             const int64_t* v_strides, int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
+             int32_t len_k, int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+             const float* rope_cos_q, const float* rope_sin_q, int64_t rope_batch_stride, bool fp8,
+             const float* q_scale, const float* k_scale, float scale, void* out, const int64_t* out_strides,
+             float* lse, void* workspace, size_t workspace_bytes, avattn_stream_t stream) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (st != AVATTN_OK) return st;
   if (!q_strides || !k_strides || !v_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
@@ -137,8 +144,11 @@ int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_str
   if (rope_cos_q && (!aligned16(rope_cos_q) || !aligned16(rope_sin_q) || rope_batch_stride % 4 != 0))
     return AVATTN_ERR_LAYOUT;
   if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
-  const size_t need = avattn_fwd_workspace_size(batch, heads_kv, len_k, head_dim);
-  if (!workspace || workspace_bytes < need || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
+  if (fp8 && (!q_scale || !k_scale)) return AVATTN_ERR_NULL_POINTER;
+  if (fp8 && ((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(k_scale)) & 3u))
+    return AVATTN_ERR_LAYOUT;
+  const FwdWorkspace wl = fwd_workspace(batch, heads_kv, len_k, head_dim, fp8);
+  if (!workspace || workspace_bytes < wl.total || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
   FwdArgs a;
   a.q = static_cast<const bf16*>(q);
@@ -158,14 +168,63 @@ int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_str
   a.o = static_cast<bf16*>(out);
   a.osb = out_strides[0]; a.osh = out_strides[1]; a.osl = out_strides[2];
   a.lse = lse;
-  const FwdWorkspace wl = fwd_workspace(batch, heads_kv, len_k, head_dim);
   char* ws = static_cast<char*>(workspace);
-  a.kr = reinterpret_cast<bf16*>(ws + wl.kr);
+  a.kr = fp8 ? nullptr : reinterpret_cast<bf16*>(ws + wl.kr);
+  a.k8 = fp8 ? reinterpret_cast<uint8_t*>(ws + wl.kr) : nullptr;
+  a.q_scale = fp8 ? q_scale : nullptr;
+  a.k_scale = fp8 ? k_scale : nullptr;
   a.vt = reinterpret_cast<bf16*>(ws + wl.vt);
   a.kbias = reinterpret_cast<float*>(ws + wl.kbias);
   a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
   a.Lkp = transpose_padded_len(len_k);
   return launch_status(launch_fwd(a, head_dim, s));
+}
+
+}  // namespace
+
+extern "C" {
+
+int avattn_fwd(const void* q, const void* k, const void* v, const int64_t* q_strides, const int64_t* k_strides,
+               const int64_t* v_strides, int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
+               int32_t len_k, int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+               const float* rope_cos_q, const float* rope_sin_q, int64_t rope_batch_stride, float scale, void* out,
+               const int64_t* out_strides, float* lse, void* workspace, size_t workspace_bytes,
+               avattn_stream_t stream) {
+  return fwd_impl(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
+                  key_mask, key_mask_batch_stride, rope_cos_q, rope_sin_q, rope_batch_stride, false, nullptr,
+                  nullptr, scale, out, out_strides, lse, workspace, workspace_bytes, stream);
+}
+
+int avattn_fwd_fp8(const void* q, const void* k, const void* v, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
+                   int32_t len_k, int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                   const float* q_scale, const float* k_scale, float scale, void* out, const int64_t* out_strides,
+                   float* lse, void* workspace, size_t workspace_bytes, avattn_stream_t stream) {
+  return fwd_impl(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
+                  key_mask, key_mask_batch_stride, nullptr, nullptr, 0, true, q_scale, k_scale, scale, out,
+                  out_strides, lse, workspace, workspace_bytes, stream);
+}
+
+size_t avattn_fwd_fp8_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k, int32_t head_dim) {
+  if (batch <= 0 || heads_kv <= 0 || len_k <= 0 || head_dim <= 0) return 0;
+  return fwd_workspace(batch, heads_kv, len_k, head_dim, true).total;
+}
+
+int avattn_fp8_absmax_scales(const void* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,
+                             int32_t head_dim, float* scale_out, avattn_stream_t stream) {
+  if (batch < 0 || heads < 0 || len < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return AVATTN_ERR_HEAD_DIM;
+  if (!x_strides) return AVATTN_ERR_NULL_POINTER;
+  if (heads == 0) return AVATTN_OK;
+  if (heads > 65535) return AVATTN_ERR_TOO_LARGE;
+  if ((int64_t)batch * len * (head_dim / 8) > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
+  if (!scale_out || ((int64_t)batch * len > 0 && !x)) return AVATTN_ERR_NULL_POINTER;
+  if ((reinterpret_cast<uintptr_t>(scale_out) & 3u) != 0) return AVATTN_ERR_LAYOUT;
+  if ((int64_t)batch * len > 0 && (!aligned16(x) || !strides_ok(x_strides))) return AVATTN_ERR_LAYOUT;
+  return launch_status(launch_absmax_scales(static_cast<const bf16*>(x), x_strides[0], x_strides[1], x_strides[2],
+                                            batch, heads, len, head_dim, scale_out,
+                                            reinterpret_cast<uint32_t*>(scale_out),
+                                            reinterpret_cast<hipStream_t>(stream)));
 }
 
 size_t avattn_fwd_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k, int32_t head_dim) {

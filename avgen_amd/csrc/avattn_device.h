@@ -25,6 +25,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));  // 32 fp8 values
 
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kPosInf = __builtin_huge_valf();
@@ -34,6 +35,31 @@ constexpr float kLn2 = 0.6931471805599453f;
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
+
+// 32x32x64 product of e4m3 (OCP fp8) operands: lane l supplies row (A) or
+// column (B) l % 32 as 32 bytes; A and B use the same byte -> k mapping, so a
+// lane's bytes j of A and B meet in the sum whatever that mapping is.  With
+// zero scale operands the compiler selects the unscaled
+// v_mfma_f32_32x32x64_f8f6f4 (format 0 = e4m3 for both operands), which
+// computes the plain product (checked on the GPU against the layout-free sum
+// of per-lane byte products).
+__device__ __forceinline__ f32x16 mfma32_fp8(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// Four fp32 values -> four e4m3 bytes (byte i = value i), round to nearest
+// even, no saturation (|x| < 464 stays finite; the callers scale into
+// [-448, 448]); v_cvt_pk_fp8_f32 matches torch's float8_e4m3fn cast bit for
+// bit, subnormals included.
+__device__ __forceinline__ uint32_t pack_fp8x4(float x0, float x1, float x2, float x3) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(x2, x3, w, true);
+  return (uint32_t)w;
+}
+
+// The two bf16 halves of a 32-bit word as fp32 (exact).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;

@@ -35,6 +35,12 @@ struct FwdArgs {
   float* kbias;  // (B, Lkp): 0 attended / -inf
   int* kfull;    // (B, Lkp/32): 1 if every key of the 32-key tile is attended
   int Lkp;
+  // fp8 variant only (null otherwise): per-head dequantization scales (q8 =
+  // e4m3(q / q_scale[h]), k8 likewise) and the e4m3 row-major k copy, element
+  // (b, h, j, d) at byte ((b*Hkv + h)*Lkp + j)*D + d.
+  const float* q_scale;
+  const float* k_scale;
+  uint8_t* k8;
 };
 
 struct BwdArgs {
@@ -89,6 +95,8 @@ enum KernelId : int {
   kKidRopeApply = 5,
   kKidRopeTables = 6,
   kKidTranspose = 7,
+  kKidFwdFp8 = 8,
+  kKidAbsmax = 9,
 };
 
 // Records HIP events around one launch on `stream` while timing is enabled.
@@ -118,6 +126,18 @@ hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, floa
 hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
                               bf16* xr, bf16* xt, hipStream_t stream);
 
+// Per-head e4m3 scales of x (B, H, L, D) strided: scale[h] = max|x[:, h]| / 448
+// (1 for an all-zero head).  `bits` (H words) holds the running maxima; it
+// may alias `scale`.
+hipError_t launch_absmax_scales(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
+                                float* scale, uint32_t* bits, hipStream_t stream);
+
+// x (B, H, L, D) strided -> e4m3 row-major copy (B*H, Lp, D) bytes of
+// x * (1 / scale[h]), zero padded to Lp = transpose_padded_len(L).
+hipError_t launch_quantize_rows(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
+                                const float* scale, uint8_t* out, hipStream_t stream);
+
+// Forward; the fp8 q k^T variant when a.k8 is set (a.q_scale, a.k_scale too).
 hipError_t launch_fwd(const FwdArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_empty(bf16* o, int64_t osb, int64_t osh, int64_t osl, int B, int H, int L, int D, float* lse,
                         hipStream_t stream);

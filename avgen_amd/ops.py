@@ -14,6 +14,9 @@ Ops (namespace ``avgen_amd``):
   the ring backward step (torch/.../_context_parallel/_attention.py:567-575).
 * ``rope_apply(x, cos, sin, inverse) -> x_rot`` — src/avgen/models/rope.py
   :297-338, differentiable.
+* ``flash_fwd_fp8(q, k, v, key_mask, q_scale, k_scale, scale) -> (out, lse)``
+  — forward with q k^T on e4m3 operands and per-head scales (no reference
+  counterpart; the sampling-time fp8 variant of ``flash_fwd``), forward only.
 """
 
 from __future__ import annotations
@@ -29,6 +32,8 @@ from . import _lib
 __all__ = [
     "flash_fwd",
     "flash_bwd",
+    "flash_fwd_fp8",
+    "fp8_absmax_scales",
     "lse_merge_",
     "rope_apply",
     "rope_tables",
@@ -168,6 +173,38 @@ def _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale):
     return out, lse
 
 
+def _fwd_fp8_impl(q, k, v, key_mask, q_scale, k_scale, scale):
+    name = "avgen_amd.flash_fwd_fp8"
+    _check_qkv(name, q, k, v)
+    _require_gpu(name, q, k, v, key_mask, q_scale, k_scale)
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    for label, t, n in (("q_scale", q_scale, Hq), ("k_scale", k_scale, Hkv)):
+        if t.dtype is not torch.float32:
+            raise TypeError(f"{name}: {label} must be float32; got {t.dtype}")
+        if t.shape != (n,):
+            raise ValueError(f"{name}: {label} must have one entry per head ({n},); got {tuple(t.shape)}")
+    q_scale, k_scale = q_scale.contiguous(), k_scale.contiguous()
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    out = _kernel_ready(torch.empty_like(q, memory_format=torch.preserve_format))
+    lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws = _workspace(lib.avattn_fwd_fp8_workspace_size(B, Hkv, Lk, D), q.device)
+    st = lib.avattn_fwd_fp8(
+        _ptr(q), _ptr(k), _ptr(v), _strides3(q), _strides3(k), _strides3(v),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        _ptr(q_scale), _ptr(k_scale),
+        float(scale),
+        _ptr(out), _strides3(out), _ptr(lse),
+        _ptr(ws), ws.numel(),
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return out, lse
+
+
 def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale):
     name = "avgen_amd.flash_bwd"
     _check_qkv(name, q, k, v)
@@ -276,6 +313,25 @@ def _(x, cos, sin, inverse):
     return x.new_empty(x.shape)
 
 
+@torch.library.custom_op("avgen_amd::flash_fwd_fp8", mutates_args=())
+def flash_fwd_fp8(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    key_mask: Optional[torch.Tensor],
+    q_scale: torch.Tensor,
+    k_scale: torch.Tensor,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Forward with e4m3 q k^T: ``(out, lse)``; not differentiable."""
+    return _fwd_fp8_impl(q, k, v, key_mask, q_scale, k_scale, scale)
+
+
+@flash_fwd_fp8.register_fake
+def _(q, k, v, key_mask, q_scale, k_scale, scale):
+    return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
+
+
 def _fwd_setup(ctx, inputs, output):
     q, k, v, key_mask, rope_cos, rope_sin, scale = inputs
     out, lse = output
@@ -315,6 +371,25 @@ torch.library.register_autograd("avgen_amd::rope_apply", _rope_backward, setup_c
 # ---------------------------------------------------------------------------
 # Non-differentiable helpers
 # ---------------------------------------------------------------------------
+
+
+def fp8_absmax_scales(x: torch.Tensor) -> torch.Tensor:
+    """Per-head e4m3 scales of ``x (batch, heads, seq, head_dim)`` bf16:
+    ``max|x[:, h]| / 448`` in fp32 (1 for an all-zero head), shape ``(heads,)``."""
+    name = "avgen_amd.fp8_absmax_scales"
+    if x.ndim != 4:
+        raise ValueError(f"{name}: input must be (batch, heads, seq, head_dim); got {tuple(x.shape)}")
+    if x.dtype is not torch.bfloat16:
+        raise TypeError(f"{name}: input must be bfloat16; got {x.dtype}")
+    if x.shape[-1] not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{name}: head_dim {x.shape[-1]} not supported (supported: {SUPPORTED_HEAD_DIMS})")
+    _require_gpu(name, x)
+    B, H, L, D = x.shape
+    x = _kernel_ready(x)
+    out = torch.empty((H,), device=x.device, dtype=torch.float32)
+    st = _lib.load().avattn_fp8_absmax_scales(_ptr(x), _strides3(x), B, H, L, D, _ptr(out), _stream(x.device))
+    _lib.check(st, name)
+    return out
 
 
 def lse_merge_(out_acc: torch.Tensor, lse_acc: torch.Tensor, out_blk: torch.Tensor, lse_blk: torch.Tensor) -> None:

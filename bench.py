@@ -52,6 +52,9 @@ CONFIGS = {
                     "21x45x80 latent), 40 heads x d128, RoPE + ring fwd (merge) + ring bwd"),
     "c4": dict(B=2, H=40, Lq=76112, L=76112, D=128, cp=1, grid=(21, 45, 80), text=512,
                desc="c4 joint text+video: (2,40,76112,128), 512 text slots with key-padding mask"),
+    "c5": dict(B=2, H=40, Lq=75600, L=75600, D=128, cp=1, grid=(21, 45, 80), text=0,
+               desc="c5 sampling with CFG batch: (2,40,75600,128) forward only, bf16 and fp8 (e4m3) q k^T "
+                    "with per-head absmax scales, repeated calls"),
 }
 
 
@@ -276,6 +279,74 @@ def ingest_pmc(fetch_csv: str, write_csv: str, kernel: str, workload: str) -> di
     return result
 
 
+def bench_c5(cfg: dict, steps: int, warmup: int) -> dict:
+    """Sampling-time forward (BASELINE config c5): `steps` repeated calls of
+    the bf16 forward and of the fp8 q k^T forward (per-head absmax scales
+    computed in each call) over the same rotated q/k and v; reports both
+    rates (4*B*H*L^2*D FLOP per call) and the fp8 output's error against the
+    bf16 output."""
+    import avgen_amd
+    from avgen_amd import _lib
+
+    dev = torch.device("cuda", 0)
+    x = make_inputs(cfg, dev)
+    with torch.no_grad():
+        q = avgen_amd.rope.apply_rotary(x["q"], x["tables_q"])
+        k = avgen_amd.rope.apply_rotary(x["k"], x["tables_k"])
+        v = x["v"]
+        torch.cuda.synchronize()
+        log("[bench] c5 inputs ready (rotated q, k)")
+        att, att8 = avgen_amd.attention.attention, avgen_amd.attention.attention_fp8
+        for _ in range(warmup):
+            att(q, k, v)
+            att8(q, k, v)
+        torch.cuda.synchronize()
+        log("[bench] c5 warmup done")
+        res = {}
+        for name, fn in (("bf16", att), ("fp8", att8)):
+            with _lib.LaunchTiming(16 * steps + 16) as timing:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    out = fn(q, k, v)
+                torch.cuda.synchronize()
+                t1 = time.perf_counter()
+                kern = "attn_fwd_fp8" if name == "fp8" else "attn_fwd"
+                kms, kn = timing.read(kern)
+            timing.close()
+            res[name] = {"ms_per_call": (t1 - t0) * 1e3 / steps, "kernel": kern,
+                         "kernel_avg_ms": kms / kn if kn else None, "out": out}
+            log(f"[bench] c5 {name}: {res[name]['ms_per_call']:.2f} ms per call")
+        err = (res["fp8"]["out"].float() - res["bf16"]["out"].float()).abs().max().item()
+        ref_mag = res["bf16"]["out"].float().abs().max().item()
+    flops = 4.0 * cfg["B"] * cfg["H"] * cfg["Lq"] * cfg["L"] * cfg["D"]
+    r16, r8 = res["bf16"], res["fp8"]
+    return {
+        "metric": "attention fwd TFLOP/s (c5 sampling: B=2, 75.6k tokens, 40h x d128), fp8 (e4m3) q k^T",
+        "value": round(flops / (r8["ms_per_call"] / 1e3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(r8["ms_per_call"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8 e4m3 q k^T, bf16 P V",
+        "data": "synthetic (seeded N(0,1)/sqrt(2) q/k/v, rotated by the 3D RoPE of an 8-fps 2x2-patch grid)",
+        "config": {"workload": cfg["desc"], "name": "c5", "batch": cfg["B"], "heads": cfg["H"],
+                   "head_dim": cfg["D"], "len_q": cfg["Lq"], "len_k": cfg["L"]},
+        "pct_of_peak_bf16": round(100.0 * flops / (r8["ms_per_call"] / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        "bf16": {"tflops": round(flops / (r16["ms_per_call"] / 1e3) / 1e12, 2),
+                 "ms_per_call": round(r16["ms_per_call"], 3), "kernel_avg_ms": r16["kernel_avg_ms"]},
+        "fp8": {"tflops": round(flops / (r8["ms_per_call"] / 1e3) / 1e12, 2),
+                "ms_per_call": round(r8["ms_per_call"], 3), "kernel_avg_ms": r8["kernel_avg_ms"]},
+        "fp8_vs_bf16_out_max_abs": err,
+        "bf16_out_max_abs": ref_mag,
+        "flops_per_call": flops,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -309,6 +380,10 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.config == "c5":
+        log(f"[bench] config c5: {cfg['desc']}")
+        print(json.dumps(bench_c5(cfg, args.steps, args.warmup)), flush=True)
+        return 0
     log(f"[bench] config {args.config}: {cfg['desc']}")
     x = make_inputs(cfg, dev)
     torch.cuda.synchronize()

@@ -30,6 +30,11 @@
  *   avattn_rope_tables  src/avgen/models/rope.py:218-294 (build_rotary_tables)
  *   avattn_rope_apply   src/avgen/models/rope.py:297-338 (apply_rotary) and
  *                       its autograd backward
+ *   avattn_fwd_fp8,     no counterpart in the reference (its attention is
+ *   avattn_fp8_absmax_scales   bf16 SDPA only): the fp8 (e4m3) q k^T forward
+ *                       of the sampling-time CFG configuration, a drop-in for
+ *                       attention() (src/avgen/models/attention.py:227-273)
+ *                       where fp8 scores are acceptable
  */
 #ifndef AVATTN_H
 #define AVATTN_H
@@ -109,6 +114,47 @@ size_t avattn_fwd_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k,
  */
 size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
                                  int32_t len_q, int32_t len_k, int32_t head_dim);
+
+/*
+ * Forward with q k^T on fp8 (OCP e4m3) operands: per-head dequantization
+ * scales q_scale[heads_q], k_scale[heads_kv] (device float32, e.g. from
+ * avattn_fp8_absmax_scales); q8 = e4m3(q * (1/q_scale[h])) and k8 likewise
+ * (fp32 multiply by the correctly rounded reciprocal, round to nearest even,
+ * no saturation: |q / q_scale| must stay below 464), scores =
+ * (q8 . k8) * q_scale[h] * k_scale[hk] * scale.  P, V and the output
+ * accumulation are as in avattn_fwd (bf16 P, fp32 accumulate), and so are
+ * the arguments, masks, GQA, lse and zero-length behaviour; there is no RoPE
+ * argument (pass rotated q and k).  workspace must hold
+ * avattn_fwd_fp8_workspace_size() bytes (an e4m3 copy of k, a head_dim-major
+ * copy of v, key bias and flags).  Forward only (no backward).
+ */
+int avattn_fwd_fp8(const void* q, const void* k, const void* v,
+                   const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides,
+                   int32_t batch, int32_t heads_q, int32_t heads_kv,
+                   int32_t len_q, int32_t len_k, int32_t head_dim,
+                   const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                   const float* q_scale, const float* k_scale,
+                   float scale,
+                   void* out, const int64_t* out_strides,
+                   float* lse,
+                   void* workspace, size_t workspace_bytes,
+                   avattn_stream_t stream);
+
+/* Workspace bytes avattn_fwd_fp8 needs (0 when there is nothing to do). */
+size_t avattn_fwd_fp8_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k, int32_t head_dim);
+
+/*
+ * Per-head e4m3 scales of x (batch, heads, len, head_dim) bf16 (strides as
+ * for q): scale_out[h] = max |x[:, h, :, :]| / 448 over every batch, position
+ * and channel of head h, in fp32 (correctly rounded division), or 1 for an
+ * all-zero head; x must be finite.  scale_out: device float32[heads], also
+ * used as the scratch of the running maxima (no workspace).
+ */
+int avattn_fp8_absmax_scales(const void* x, const int64_t* x_strides,
+                             int32_t batch, int32_t heads, int32_t len,
+                             int32_t head_dim, float* scale_out,
+                             avattn_stream_t stream);
 
 /*
  * Backward of avattn_fwd with recomputation of the probabilities from
@@ -198,7 +244,8 @@ int avattn_rope_apply(const void* x, const int64_t* x_strides,
  * the elapsed times of one kernel kind (it synchronizes on the recorded
  * events).  Kernel ids: 0 forward, 1 backward preprocess, 2 backward dK/dV,
  * 3 backward dQ, 4 LSE merge, 5 rotary apply, 6 rotary tables,
- * 7 head_dim-major copies (forward and backward operand preparation).
+ * 7 operand copies (forward and backward operand preparation, including the
+ * fp8 forward's e4m3 k copy), 8 fp8 forward, 9 fp8 absmax scales.
  * avattn_timing_begin creates `capacity` event pairs (call it outside any
  * timed or captured region); launches beyond capacity are not recorded and
  * make avattn_timing_read return AVATTN_ERR_WORKSPACE.

@@ -196,6 +196,66 @@ def attention_f64(
     return out, lse
 
 
+# ---------------------------------------------------------------------------
+# fp8 (e4m3) q k^T variant.  The reference has no fp8 path (its attention is
+# bf16 SDPA, src/avgen/models/attention.py:265-273); this is the sampling-time
+# configuration's definition: per-head absmax scales, OCP e4m3 operands,
+# scores dequantized by the two scales, everything else as attention_f64.
+# ---------------------------------------------------------------------------
+
+E4M3_MAX = 448.0
+
+
+def e4m3_round(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest OCP FP8 E4M3 value (ties to even),
+    returned as float32.
+
+    E4M3: exponent bias 7, 3 mantissa bits, normal values down to 2**-6,
+    subnormals in steps of 2**-9, largest finite 448, no infinities (a value
+    that rounds above 448 — |x| > 464 — is NaN, as is NaN).  Signed zeros
+    keep their sign.
+    """
+    f = np.asarray(x, dtype=np.float32).astype(np.float64)
+    a = np.abs(f)
+    _, ex = np.frexp(a)  # a = m * 2**ex, 0.5 <= m < 1
+    e = np.maximum(ex - 1, -6)  # exponent of the binade, clamped at the subnormal range
+    step = np.ldexp(1.0, e - 3)  # spacing of 3-bit mantissas in that binade
+    with np.errstate(invalid="ignore"):
+        r = np.round(a / step) * step  # np.round: half to even
+        r = np.where((r > E4M3_MAX) | np.isnan(f), np.nan, r)
+    return np.copysign(r, f).astype(np.float32)
+
+
+def fp8_absmax_scale(x: np.ndarray) -> np.ndarray:
+    """Per-head scales of ``x (B, H, L, D)``: float32(max |x[:, h]|) / 448 in
+    float32 (correctly rounded), 1 for an all-zero head."""
+    m = np.abs(np.asarray(x, np.float32)).max(axis=(0, 2, 3)) if x.size else np.zeros(x.shape[1], np.float32)
+    m = m.astype(np.float32)
+    return np.where(m > 0, m / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
+
+
+def fp8_quantize(x: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """e4m3(x * (1/scale[h])) per head, the product and reciprocal in float32
+    (each correctly rounded); returns the e4m3 values as float32."""
+    inv = (np.float32(1.0) / np.asarray(scale, np.float32)).astype(np.float32)
+    return e4m3_round(np.asarray(x, np.float32) * inv[None, :, None, None])
+
+
+def attention_fp8_f64(
+    q: np.ndarray, k: np.ndarray, v: np.ndarray, q_scale: np.ndarray, k_scale: np.ndarray,
+    key_mask: np.ndarray | None = None, scale: float | None = None,
+) -> tuple[np.ndarray, np.ndarray]:
+    """attention_f64 with scores ``(q8 . k8) * q_scale[h] * k_scale[hk] * scale``,
+    ``q8 = fp8_quantize(q, q_scale)``, ``k8 = fp8_quantize(k, k_scale)``.
+
+    The dequantized operands ``q8 * q_scale`` are exact in float64 (4 + 24
+    significant bits), so this is attention_f64 on them.
+    """
+    qd = fp8_quantize(q, q_scale).astype(np.float64) * np.asarray(q_scale, np.float64)[None, :, None, None]
+    kd = fp8_quantize(k, k_scale).astype(np.float64) * np.asarray(k_scale, np.float64)[None, :, None, None]
+    return attention_f64(qd, kd, v, key_mask, scale)
+
+
 def attention_bwd_f64(
     dout: np.ndarray, q: np.ndarray, k: np.ndarray, v: np.ndarray, out: np.ndarray, lse: np.ndarray,
     key_mask: np.ndarray | None = None, scale: float | None = None,

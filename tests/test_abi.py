@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 2
+    assert lib.avattn_abi_version() == 3
     for code in range(0, 10):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
@@ -87,6 +87,12 @@ def test_workspace_size(lib):
     # forward: k rows + v^T copies of (B, Hkv, Lk, D), key bias/flags
     assert lib.avattn_fwd_workspace_size(2, 8, 18900, 128) == 2 * (2 * 8 * 128 * lp * 2) + _key_regions(2, lp)
     assert lib.avattn_fwd_workspace_size(1, 1, 0, 128) == 0
+    # fp8 forward: the k copy is e4m3 (one byte per element)
+    assert lib.avattn_fwd_fp8_workspace_size(2, 8, 18900, 128) == (
+        2 * 8 * 128 * lp + 2 * 8 * 128 * lp * 2 + _key_regions(2, lp))
+    assert lib.avattn_fwd_fp8_workspace_size(1, 1, 70, 64) == (
+        _round256(128 * 64) + 128 * 64 * 2 + _key_regions(1, 128))
+    assert lib.avattn_fwd_fp8_workspace_size(1, 1, 0, 128) == 0
 
 
 def _fwd(lib, **over):
@@ -161,3 +167,43 @@ def test_merge_and_rope_validation_paths(lib):
                                   16, 16, None) == _lib.ERR_ARGUMENT
     assert lib.avattn_rope_tables(16, 3, 3, 1, 4, 2, cast(f), cast(ax), cast(z), cast(f3), cast(z), cast(f3),
                                   16, 16, None) == _lib.ERR_HEAD_DIM
+
+
+def _fwd_fp8(lib, **over):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+    args = dict(q=16, k=16, v=16, qs=s, ks=s, vs=s, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
+                qsc=16, ksc=16, scale=0.125, out=16, os=s, lse=16, ws=256, wsb=1 << 20, stream=None)
+    args.update(over)
+    return lib.avattn_fwd_fp8(args["q"], args["k"], args["v"], args["qs"], args["ks"], args["vs"], args["B"],
+                              args["Hq"], args["Hkv"], args["Lq"], args["Lk"], args["D"], args["mask"], args["msb"],
+                              args["qsc"], args["ksc"], args["scale"], args["out"], args["os"], args["lse"],
+                              args["ws"], args["wsb"], args["stream"])
+
+
+@cpu_only
+def test_fwd_fp8_validation_paths(lib):
+    assert _fwd_fp8(lib, D=96) == _lib.ERR_HEAD_DIM
+    assert _fwd_fp8(lib, Hq=3, Hkv=2) == _lib.ERR_GQA
+    assert _fwd_fp8(lib, scale=-1.0) == _lib.ERR_ARGUMENT
+    assert _fwd_fp8(lib, qsc=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_fp8(lib, ksc=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_fp8(lib, qsc=18) == _lib.ERR_LAYOUT
+    assert _fwd_fp8(lib, q=8) == _lib.ERR_LAYOUT
+    assert _fwd_fp8(lib, ws=None) == _lib.ERR_WORKSPACE
+    assert _fwd_fp8(lib, wsb=1000) == _lib.ERR_WORKSPACE
+    assert _fwd_fp8(lib, Lq=0) == _lib.OK
+
+
+@cpu_only
+def test_fp8_absmax_validation_paths(lib):
+    s = _lib.i64_array([1 << 17, 1 << 17, 128])
+    f = lib.avattn_fp8_absmax_scales
+    assert f(16, s, 1, 2, 4, 96, 16, None) == _lib.ERR_HEAD_DIM
+    assert f(16, s, -1, 2, 4, 128, 16, None) == _lib.ERR_BAD_SHAPE
+    assert f(16, None, 1, 2, 4, 128, 16, None) == _lib.ERR_NULL_POINTER
+    assert f(16, s, 1, 2, 4, 128, None, None) == _lib.ERR_NULL_POINTER
+    assert f(None, s, 1, 2, 4, 128, 16, None) == _lib.ERR_NULL_POINTER
+    assert f(8, s, 1, 2, 4, 128, 16, None) == _lib.ERR_LAYOUT
+    assert f(16, s, 1, 2, 4, 128, 18, None) == _lib.ERR_LAYOUT
+    assert f(16, s, 1, 1 << 17, 4, 128, 16, None) == _lib.ERR_TOO_LARGE
+    assert f(16, s, 1, 0, 4, 128, 16, None) == _lib.OK

@@ -1,0 +1,144 @@
+"""GPU parity of the fp8 (e4m3) q k^T forward and its per-head scales
+(through the C ABI) against the CPU oracle.
+
+The oracle quantizes exactly as the kernels do (oracle/reference.py
+fp8_quantize: fp32 product with the correctly rounded reciprocal, e4m3
+round-to-nearest-even), so the bar is the bf16 forward's: output max-abs
+<= 2e-2 and LSE <= 1e-3 against float64 attention on the dequantized
+operands, masks bit-exact.  The per-head scales are bit-exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = 2e-2
+LSE_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def amd():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    import avgen_amd
+
+    return avgen_amd
+
+
+def _randn(shape, seed, scale=2 ** -0.5):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_absmax_scales_bit_exact(amd, D):
+    B, H, L = 2, 5, 333
+    x = _randn((B, L, H, D), 40, scale=3.0).transpose(1, 2)  # strided (B, H, L, D) view
+    x[:, 3] = 0  # all-zero head -> 1
+    x[1, 1, 17, 5] = -1000.0
+    print(f"absmax D={D}", flush=True)
+    s = amd.ops.fp8_absmax_scales(x.cuda())
+    ref = R.fp8_absmax_scale(_np(x))
+    assert s.dtype is torch.float32 and s.shape == (H,)
+    assert np.array_equal(s.cpu().numpy(), ref)
+    assert s[3].item() == 1.0 and s[1].item() == np.float32(1000.0) / np.float32(448.0)
+
+
+FP8_CASES = [
+    # B, Hq, Hkv, Lq, Lk, D
+    (1, 2, 2, 128, 128, 128),
+    (2, 3, 3, 200, 333, 128),
+    (1, 4, 4, 1024, 1024, 64),
+    (1, 4, 2, 130, 257, 128),
+    (2, 2, 1, 65, 64, 64),
+    (1, 1, 1, 1, 1, 128),
+    (1, 2, 2, 300, 5, 128),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D", FP8_CASES)
+@pytest.mark.parametrize("masked", [False, True])
+def test_fp8_forward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
+    q = _randn((B, Hq, Lq, D), 0)
+    k = _randn((B, Hkv, Lk, D), 1)
+    v = _randn((B, Hkv, Lk, D), 2)
+    mask = None
+    if masked:
+        g = torch.Generator()
+        g.manual_seed(4)
+        lengths = torch.randint(1, Lk + 1, (B,), generator=g)
+        mask = torch.arange(Lk)[None, :] < lengths[:, None]
+        if B > 1:
+            mask[0] = False  # fully masked batch row
+    qs, ks = R.fp8_absmax_scale(_np(q)), R.fp8_absmax_scale(_np(k))
+    print(f"fp8 fwd case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked}", flush=True)
+    out, lse = amd.ops.flash_fwd_fp8(q.cuda(), k.cuda(), v.cuda(), None if mask is None else mask.cuda(),
+                                     torch.from_numpy(qs).cuda(), torch.from_numpy(ks).cuda(), D ** -0.5)
+    ro, rl = R.attention_fp8_f64(_np(q), _np(k), _np(v), qs, ks, None if mask is None else mask.numpy())
+    o = out.float().cpu().numpy().astype(np.float64)
+    l = lse.cpu().numpy().astype(np.float64)
+    assert np.isfinite(o).all()
+    assert np.abs(o - ro).max() <= OUT_TOL
+    fin = np.isfinite(rl)
+    assert np.array_equal(np.isneginf(l), ~fin)
+    assert np.abs(l[fin] - rl[fin]).max(initial=0.0) <= LSE_TOL
+    if masked and B > 1:
+        assert np.all(o[0] == 0)
+
+
+def test_fp8_masked_keys_bit_exact(amd):
+    B, H, Lq, Lk, D = 2, 2, 96, 200, 128
+    q, k, v = _randn((B, H, Lq, D), 30), _randn((B, H, Lk, D), 31), _randn((B, H, Lk, D), 32)
+    m = torch.ones(B, Lk, dtype=torch.bool)
+    m[0, 120:] = False
+    m[1, 7:40] = False
+    qs = amd.ops.fp8_absmax_scales(q.cuda())
+    ks = amd.ops.fp8_absmax_scales(k.cuda())
+    out, lse = amd.ops.flash_fwd_fp8(q.cuda(), k.cuda(), v.cuda(), m.cuda(), qs, ks, D ** -0.5)
+    k2, v2 = k.clone(), v.clone()
+    garbage = _randn((B, H, Lk, D), 33, scale=0.1)  # inside the range the scales cover
+    sel = (~m)[:, None, :, None].expand_as(k2)
+    k2[sel] = garbage[sel]
+    v2[sel] = garbage[sel] * 100
+    # same scales: masked keys contribute exactly nothing
+    out2, lse2 = amd.ops.flash_fwd_fp8(q.cuda(), k2.cuda(), v2.cuda(), m.cuda(), qs, ks, D ** -0.5)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+
+
+def test_attention_fp8_dropin_and_error_vs_bf16(amd):
+    """Default (absmax) scales; the fp8 output stays close to the bf16 one."""
+    B, H, L, D = 2, 4, 1000, 128
+    q, k, v = _randn((B, H, L, D), 50), _randn((B, H, L, D), 51), _randn((B, H, L, D), 52)
+    out8 = amd.attention.attention_fp8(q.cuda(), k.cuda(), v.cuda())
+    qs, ks = R.fp8_absmax_scale(_np(q)), R.fp8_absmax_scale(_np(k))
+    ro, _ = R.attention_fp8_f64(_np(q), _np(k), _np(v), qs, ks)
+    assert np.abs(out8.float().cpu().numpy() - ro).max() <= OUT_TOL
+    out16 = amd.attention.attention(q.cuda(), k.cuda(), v.cuda())
+    err = (out8.float() - out16.float()).abs().max().item()
+    print(f"fp8 vs bf16 output max-abs {err:.3e}", flush=True)
+    assert err <= 5e-2
+    # zero-length sequences short-circuit like attention()
+    k0 = _randn((B, H, 0, D), 53).cuda()
+    assert torch.all(amd.attention.attention_fp8(q.cuda(), k0, k0) == 0)
+
+
+def test_fp8_argument_errors(amd):
+    q = _randn((1, 2, 64, 128), 60).cuda()
+    s = torch.ones(2, device="cuda")
+    with pytest.raises(ValueError):
+        amd.ops.flash_fwd_fp8(q, q, q, None, torch.ones(3, device="cuda"), s, 0.1)
+    with pytest.raises(TypeError):
+        amd.ops.flash_fwd_fp8(q, q, q, None, s.double(), s, 0.1)
+    with pytest.raises(TypeError):
+        amd.ops.fp8_absmax_scales(q.float())

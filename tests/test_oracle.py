@@ -429,3 +429,96 @@ def test_key_padding_mask_semantics():
         R.key_padding_mask(np.ones((2, 1, 128), bool))
     with pytest.raises(TypeError):
         R.key_padding_mask(np.ones((2, 128), np.int32))
+
+
+# ---------------------------------------------------------------------------
+# fp8 (e4m3) q k^T variant
+# ---------------------------------------------------------------------------
+
+
+def _e4m3_finite_values() -> torch.Tensor:
+    vals = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float()
+    return torch.sort(vals[torch.isfinite(vals)].unique()).values
+
+
+def test_e4m3_round_matches_torch_cast(rng):
+    """Bit for bit against torch's float8_e4m3fn cast: every finite value, every
+    midpoint (ties), points just off the midpoints, subnormals, random values
+    over many binades, the overflow edge."""
+    fin = _e4m3_finite_values()
+    assert fin.numel() == 253  # 254 finite codes, +0 and -0 equal
+    mids = (fin[1:] + fin[:-1]) / 2
+    off = (mids[:, None] * torch.tensor([1 - 2**-20, 1 + 2**-20])).flatten()
+    rand = torch.from_numpy(rng.standard_normal(20000).astype(np.float32)) * torch.from_numpy(
+        np.exp2(rng.integers(-14, 9, 20000)).astype(np.float32))
+    edge = torch.tensor([448.0, 463.99, 464.0, 464.01, 465.0, 1e30, float("inf"), -0.0, 0.0, 2.0**-10,
+                         3 * 2.0**-10, 2.0**-9 * 0.5000001, float("nan")])
+    x = torch.cat([fin, -fin, mids, -mids, off, rand, edge])
+    ref = x.to(torch.float8_e4m3fn).float().numpy()
+    got = R.e4m3_round(x.numpy())
+    same = (got == ref) | (np.isnan(got) & np.isnan(ref))
+    assert same.all(), x.numpy()[~same][:10]
+    assert np.array_equal(np.signbit(got[~np.isnan(got)]), np.signbit(ref[~np.isnan(ref)]))
+
+
+def test_e4m3_round_closed_forms():
+    """Values fixed by the format definition (bias 7, 3 mantissa bits)."""
+    r = lambda v: float(R.e4m3_round(np.array([v], np.float32))[0])
+    assert r(448.0) == 448.0 and r(-448.0) == -448.0
+    assert r(2.0**-9) == 2.0**-9  # smallest subnormal
+    assert r(2.0**-6) == 2.0**-6  # smallest normal
+    assert r(2.0**-10) == 0.0  # tie between 0 and 2**-9 -> even (0)
+    assert r(3 * 2.0**-10) == 2.0**-8  # tie between 1 and 2 steps -> even (2)
+    assert r(1.0625) == 1.0 and r(1.1875) == 1.25  # ties in [1, 2): steps of 1/8
+    assert r(240.0) == 240.0 and r(232.0) == 224.0  # [128, 256): steps of 16, tie -> even
+    assert math.isnan(r(465.0)) and r(464.0) == 448.0
+    # every representable value is a fixed point
+    fin = _e4m3_finite_values().numpy()
+    assert np.array_equal(R.e4m3_round(fin), fin)
+
+
+def test_fp8_absmax_scale_and_quantize(rng):
+    x = rng.standard_normal((2, 3, 17, 8)).astype(np.float32)
+    x[:, 1] = 0.0  # all-zero head -> scale 1
+    x[1, 2, 5, 3] = -7.5  # head 2's absmax, negative, in batch 1
+    x[:, 2] = np.clip(x[:, 2], -7.0, 7.0)
+    x[1, 2, 5, 3] = -7.5
+    s = R.fp8_absmax_scale(x)
+    assert s.dtype == np.float32 and s.shape == (3,)
+    assert s[1] == np.float32(1.0)
+    assert s[2] == np.float32(7.5) / np.float32(448.0)
+    assert s[0] == np.float32(np.abs(x[:, 0]).max()) / np.float32(448.0)
+    q8 = R.fp8_quantize(x, s)
+    # the absmax element lands exactly on -448; everything stays finite and in range
+    assert q8[1, 2, 5, 3] == -448.0
+    assert np.isfinite(q8).all() and np.abs(q8).max() <= 448.0
+    # quantized values are e4m3 values within half a step of x / scale
+    y = x * (np.float32(1) / s)[None, :, None, None]
+    assert np.array_equal(R.e4m3_round(q8), q8)
+    assert (np.abs(q8 - y) <= np.maximum(np.abs(y) * 2.0**-4, 2.0**-10) + 1e-12).all()
+
+
+def test_attention_fp8_reduces_to_bf16_attention(rng):
+    """With e4m3-representable q, k and unit scales the fp8 variant is plain
+    attention; scaling q (or k) and its scale by the same power of two gives
+    plain attention of the scaled operands (quantization commutes with powers
+    of two in range)."""
+    fin = _e4m3_finite_values().numpy()
+    small = fin[(np.abs(fin) <= 2.0) & (np.abs(fin) >= 2.0**-3)]
+    q = rng.choice(small, size=(1, 2, 9, 16)).astype(np.float32)
+    k = rng.choice(small, size=(1, 1, 11, 16)).astype(np.float32)
+    v = rng.standard_normal((1, 1, 11, 16)).astype(np.float32)
+    mask = np.ones((1, 11), bool)
+    mask[0, 3] = False
+    one_q, one_k = np.ones(2, np.float32), np.ones(1, np.float32)
+    o8, l8 = R.attention_fp8_f64(q, k, v, one_q, one_k, mask)
+    o, l = R.attention_f64(q, k, v, mask)
+    assert np.array_equal(o8, o) and np.array_equal(l8, l)
+    # q * 8 with scale 8 quantizes to the same e4m3 values and dequantizes to q * 8
+    o8b, l8b = R.attention_fp8_f64(q * 8, k / 4, v, one_q * 8, one_k / 4, mask)
+    ob, lb = R.attention_f64(q * 8, k / 4, v, mask)
+    assert np.array_equal(o8b, ob) and np.array_equal(l8b, lb)
+    # and a non-representable q is rounded: the result moves off plain attention
+    o8c, _ = R.attention_fp8_f64(q * 1.03, k, v, one_q, one_k, mask)
+    oc, _ = R.attention_f64(q * 1.03, k, v, mask)
+    assert not np.allclose(o8c, oc, rtol=0, atol=1e-9)
