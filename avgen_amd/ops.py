@@ -205,7 +205,21 @@ def _fwd_fp8_impl(q, k, v, key_mask, q_scale, k_scale, scale):
     return out, lse
 
 
-def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale):
+def _out_or_new(t: Optional[torch.Tensor], like: torch.Tensor, name: str, label: str) -> torch.Tensor:
+    """A caller-provided output (any kernel-ready strides, e.g. a slice of a
+    larger tensor) or a new one shaped like ``like``."""
+    if t is None:
+        return _kernel_ready(torch.empty_like(like))
+    if t.shape != like.shape or t.dtype is not torch.bfloat16 or t.device != like.device:
+        raise ValueError(f"{name}: {label} must be bf16 {tuple(like.shape)} on {like.device}")
+    if _kernel_ready(t) is not t:
+        raise ValueError(f"{name}: {label} needs a contiguous head_dim and 16-byte aligned rows")
+    return t
+
+
+def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=None):
+    """Backward launch; ``dq``/``dk``/``dv`` may be preallocated outputs
+    (written in place, e.g. slices of a full-sequence gradient)."""
     name = "avgen_amd.flash_bwd"
     _check_qkv(name, q, k, v)
     _require_gpu(name, dout, q, k, v, out, lse, key_mask)
@@ -220,9 +234,9 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale):
     dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
     lse = lse.contiguous()
     mask, msb = _normalise_mask(name, key_mask, B, Lk)
-    dq = _kernel_ready(torch.empty_like(q))
-    dk = _kernel_ready(torch.empty_like(k))
-    dv = _kernel_ready(torch.empty_like(v))
+    dq = _out_or_new(dq, q, name, "dq")
+    dk = _out_or_new(dk, k, name, "dk")
+    dv = _out_or_new(dv, v, name, "dv")
     lib = _lib.load()
     ws = _workspace(lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D), q.device)
     st = lib.avattn_bwd(

@@ -189,16 +189,36 @@ def ring_attention_backward(
     cast once; each chunk's dk/dv is that chunk's gradient (on a real ring it
     travels back to the chunk's owner)."""
     masks = _chunk_masks(key_masks, len(keys))
-    dq_acc = torch.zeros(query.shape, dtype=torch.float32, device=query.device)
+    dq_acc = None
     dks, dvs = [], []
     for k, v, m in zip(keys, values, masks):
         dq_i, dk_i, dv_i = flash_attention_backward_op(
             grad_out, query, k, v, out, lse, scale=scale, attn_mask=m
         )
-        dq_acc += dq_i
+        dq_acc = dq_i.float() if dq_acc is None else dq_acc.add_(dq_i)
         dks.append(dk_i)
         dvs.append(dv_i)
     return dq_acc.to(query.dtype), dks, dvs
+
+
+def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, scale):
+    """The emulated ring's backward writing each chunk's dk/dv straight into
+    its slice of the full-sequence gradients (one chunk, one contribution, so
+    no accumulation or concatenation is needed); dq accumulates in fp32 as
+    in :func:`ring_attention_backward`."""
+    L = key.shape[2]
+    D = query.shape[-1]
+    scale = ops.default_scale(D) if scale is None else float(scale)
+    dk = torch.empty(key.shape, dtype=key.dtype, device=key.device)
+    dv = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    dq_acc = None
+    for r in range(cp):
+        a, b = shard_bounds(L, cp, r)
+        m = None if key_mask is None else key_mask[:, a:b]
+        dq_i, _, _ = ops._bwd_impl(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse, m, scale,
+                                   dk=dk[:, :, a:b], dv=dv[:, :, a:b])
+        dq_acc = dq_i.float() if dq_acc is None else dq_acc.add_(dq_i)
+    return dq_acc.to(query.dtype), dk, dv
 
 
 class _RingAttention(torch.autograd.Function):
@@ -219,15 +239,9 @@ class _RingAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out, _grad_lse):
         query, key, value, out, lse, key_mask = ctx.saved_tensors
-        L = key.shape[2]
-        bounds = [shard_bounds(L, ctx.cp, r) for r in range(ctx.cp)]
-        keys = [key[:, :, a:b] for a, b in bounds]
-        values = [value[:, :, a:b] for a, b in bounds]
-        masks = None if key_mask is None else [key_mask[:, a:b] for a, b in bounds]
-        dq, dks, dvs = ring_attention_backward(
-            grad_out.contiguous(), query, keys, values, out, lse, key_masks=masks, scale=ctx.scale
-        )
-        return dq, torch.cat(dks, dim=2), torch.cat(dvs, dim=2), None, None, None
+        dq, dk, dv = _ring_backward_into(grad_out.contiguous(), query, key, value, out, lse, key_mask, ctx.cp,
+                                         ctx.scale)
+        return dq, dk, dv, None, None, None
 
 
 def ring_attention(

@@ -290,10 +290,10 @@ def test_lse_merge_kernel_matches_oracle(amd):
     assert np.allclose(lg[fin], rl[fin], atol=2e-6, rtol=0)
 
 
-@pytest.mark.parametrize("masked", [False, True])
-def test_emulated_ring_matches_unchunked(amd, masked):
+@pytest.mark.parametrize("masked,Hkv", [(False, 3), (True, 3), (False, 1)])
+def test_emulated_ring_matches_unchunked(amd, masked, Hkv):
     B, H, Lq, L, D, cp = 1, 3, 256, 1024, 128, 4
-    q, k, v = _randn((B, H, Lq, D), 90), _randn((B, H, L, D), 91), _randn((B, H, L, D), 92)
+    q, k, v = _randn((B, H, Lq, D), 90), _randn((B, Hkv, L, D), 91), _randn((B, Hkv, L, D), 92)
     do = _randn((B, H, Lq, D), 93)
     m = None
     if masked:
