@@ -100,11 +100,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     bf16 q[TE];     // Q rows: TileLayout<D>
     bf16 dout[TE];  // dO rows: TileLayout<D>
     float lse2[BQ];
+    float ndl[BQ];  // ndelta: the dP accumulators start from it
   };
   struct ColStage {
     bf16 qt[TE];   // Q^T: D rows of BQ, TileLayout<BQ>
     bf16 dot[TE];  // dO^T: TileLayout<BQ>
-    float ndl[BQ];
   };
   __shared__ __attribute__((aligned(16))) RowStage rs0, rs1;
   __shared__ __attribute__((aligned(16))) ColStage cs0, cs1;
@@ -171,12 +171,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   rst.init(D, wave, lane);
   tst.init(a.Lqp, wave, lane);
 
-  // Each half of a tile = kHalfOps loads per wave, issued one at a time so
-  // they can be spread between MFMAs (a burst of them at the start of a
-  // phase would hold up the wave's instruction stream).
+  // The row half of a tile is kRowHalf loads per wave and the column half
+  // kColHalf, issued one at a time so they can be spread between MFMAs (a
+  // burst of them at the start of a phase would hold up the wave's
+  // instruction stream).
   constexpr int kRowOps = TileStager<BQ, D, NW>::kPer, kColOps = TileStager<D, BQ, NW>::kPer;
-  static_assert(kRowOps == kColOps, "row and column halves issue the same number of loads");
-  constexpr int kHalfOps = 2 * kRowOps + 1;
+  constexpr int kRowHalf = 2 * kRowOps + 2, kColHalf = 2 * kColOps;
   auto tile_rows = [&](int it) {  // first row of tile `it` in the group's copies
     return (uint32_t)(it / nqt) * a.Lqp + (uint32_t)(it % nqt) * BQ;
   };
@@ -190,24 +190,25 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       rst.stage_one(rsg.q, rq, row0 * D * 2, i);
     else if (i < 2 * kRowOps)
       rst.stage_one(rsg.dout, rdo, row0 * D * 2, i - kRowOps);
-    else
+    else if (i == 2 * kRowOps)
       dma4(rl2, lds_addr(rsg.lse2), lane * 4, row0 * 4);  // every wave loads the stats: no branch
+    else
+      dma4(rnd, lds_addr(rsg.ndl), lane * 4, row0 * 4);
   };
   auto col_op = [&](int it, auto bufc, int i) {
     ColStage& csg = decltype(bufc)::value == 0 ? cs0 : cs1;
     if (i < kColOps)
       tst.stage_one(csg.qt, rqt, tile_cols(it), i);
-    else if (i < 2 * kColOps)
-      tst.stage_one(csg.dot, rdot, tile_cols(it), i - kColOps);
     else
-      dma4(rnd, lds_addr(csg.ndl), lane * 4, tile_rows(it) * 4);
+      tst.stage_one(csg.dot, rdot, tile_cols(it), i - kColOps);
   };
   // Loads issued per wave between two consecutive waits: one row half and one
   // column half.  Waiting until at most that many are outstanding retires the
   // older half the coming phase reads.
-  constexpr int kInFlight = 2 * kHalfOps;
-  // Slots of a 2*KS-slot phase that issue the kHalfOps loads.
-  auto load_slot = [](int j, int nslots) { return j % 3 == 1 && j / 3 < kHalfOps && j < nslots; };
+  constexpr int kInFlight = kRowHalf + kColHalf;
+  // Slots of a phase that issue its `count` loads (one in every third slot;
+  // the rest follow the phase's loop).
+  auto load_slot = [](int j, int nslots, int count) { return j % 3 == 1 && j / 3 < count && j < nslots; };
 
   const float c = a.scale_log2;
 
@@ -269,7 +270,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int sub = j / KS, ks = j % KS;
       s[sub] = mfma32(qa[j & 3], kv[ks], s[sub]);
       if (j + 4 < NS) qa[j & 3] = qop(j + 4);
-      if (load_slot(j, NS)) col_op(itc, NextBuf(), j / 3);
+      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), j / 3);
       if (j >= kLo) {
         const int n = NS - kLo;
         for (int st = (j - kLo) * 8 / n; st < (j - kLo + 1) * 8 / n; ++st) smx(0, st >> 2, st & 3);
@@ -277,7 +278,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NS + 1) / 3; i < kHalfOps; ++i) col_op(itc, NextBuf(), i);
+    for (int i = (NS + 1) / 3; i < kColHalf; ++i) col_op(itc, NextBuf(), i);
     if (kLo >= NS) {
 #pragma unroll
       for (int st = 0; st < 8; ++st) smx(0, st >> 2, st & 3);
@@ -304,11 +305,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (j + 4 < NJ) opq[j % 4] = dot_op(j + 4);
       const int sk = j / DT, dt = j % DT;
       acc[dt] = mfma32(op, pb[sk >> 1][sk & 1], acc[dt]);
-      if (load_slot(j, NJ)) row_op(itr, bufc, j / 3);
+      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, j / 3);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NJ + 1) / 3; i < kHalfOps; ++i) row_op(itr, bufc, i);
+    for (int i = (NJ + 1) / 3; i < kRowHalf; ++i) row_op(itr, bufc, i);
   };
 
   auto body_ds = [&](int it, auto bufc) {
@@ -327,18 +328,30 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     bf16x8 da[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) da[j] = dop(j);
+    // dP starts at ndelta of its row (registers 8*k2 + e: row 32*sub + 16*k2
+    // + 8*hh + e), so the MFMAs deliver dP + ndelta directly.
+    f32x16 dp[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const f32x4 n4 = *reinterpret_cast<const f32x4*>(rsg.ndl + 32 * sub + 16 * k2 + 8 * hh + 4 * hf);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dp[sub][8 * k2 + 4 * hf + r] = n4[r];
+        }
     __builtin_amdgcn_sched_barrier(0);
-    f32x16 dp[2] = {zero16(), zero16()};
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int sub = j / KS, ks = j % KS;
       dp[sub] = mfma32(da[j & 3], kv[ks], dp[sub]);
       if (j + 4 < NS) da[j & 3] = dop(j + 4);
-      if (load_slot(j, NS)) col_op(itc, NextBuf(), j / 3);
+      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), j / 3);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NS + 1) / 3; i < kHalfOps; ++i) col_op(itc, NextBuf(), i);
+    for (int i = (NS + 1) / 3; i < kColHalf; ++i) col_op(itc, NextBuf(), i);
     wait_vmem_n<kInFlight>();
     barrier_lds();  // X: partner's P available, columns visible
     __builtin_amdgcn_s_setprio(2);
@@ -347,14 +360,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     // the dK^T MFMAs of group g-1; every LDS read is issued up front or four
     // MFMAs ahead.
     u32x4 pv[4];
-    f32x4 nd[4][2];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      pv[g] = xp[64 * g];
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-        nd[g][hf] = *reinterpret_cast<const f32x4*>(csg.ndl + 32 * (g >> 1) + 16 * (g & 1) + 8 * hh + 4 * hf);
-    }
+    for (int g = 0; g < 4; ++g) pv[g] = xp[64 * g];
     constexpr int NJ = 4 * DT;
     auto qt_op = [&](int j) {
       const int g = j / DT, dt = j % DT;
@@ -367,9 +374,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     u32x4 ud[4];
     auto dstep = [&](int g, int e2) {
       const int sub = g >> 1, k2 = g & 1, e = 2 * e2;
-      const f32x4& nv = nd[g][e >> 2];
       const float p0 = __uint_as_float(pv[g][e2] << 16), p1 = __uint_as_float(pv[g][e2] & 0xffff0000u);
-      ud[g][e2] = pack_bf16x2(p0 * (dp[sub][8 * k2 + e] + nv[e & 3]), p1 * (dp[sub][8 * k2 + e + 1] + nv[(e & 3) + 1]));
+      ud[g][e2] = pack_bf16x2(p0 * dp[sub][8 * k2 + e], p1 * dp[sub][8 * k2 + e + 1]);
     };
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) dstep(0, e2);
@@ -384,11 +390,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
         // the next group's 4 steps, spread over this group's DT MFMAs
         for (int st = dt * 4 / DT; st < (dt + 1) * 4 / DT; ++st) dstep(g + 1, st);
       }
-      if (load_slot(j, NJ)) row_op(itr, bufc, j / 3);
+      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, j / 3);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NJ + 1) / 3; i < kHalfOps; ++i) row_op(itr, bufc, i);
+    for (int i = (NJ + 1) / 3; i < kRowHalf; ++i) row_op(itr, bufc, i);
   };
 
   retire_prologue_loads();
@@ -396,11 +402,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
 #pragma unroll
-    for (int i = 0; i < kHalfOps; ++i) row_op(0, B0(), i);
+    for (int i = 0; i < kRowHalf; ++i) row_op(0, B0(), i);
 #pragma unroll
-    for (int i = 0; i < kHalfOps; ++i) col_op(0, B0(), i);
+    for (int i = 0; i < kColHalf; ++i) col_op(0, B0(), i);
 #pragma unroll
-    for (int i = 0; i < kHalfOps; ++i) row_op(min(1, niter - 1), B1(), i);
+    for (int i = 0; i < kRowHalf; ++i) row_op(min(1, niter - 1), B1(), i);
   }
   if (role == 0) {
     for (int it = 0; it < niter; it += 2) {
@@ -573,7 +579,9 @@ __global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd
       va[j] = vrow(j);
     }
     __builtin_amdgcn_sched_barrier(0);
-    f32x16 s = zero16(), dp = zero16();
+    // dP^T starts at ndelta (one value per query column, i.e. per lane), so
+    // the MFMAs deliver dP^T + ndelta directly.
+    f32x16 s = zero16(), dp = splat16(ndelta);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       s = mfma32(ka[ks & 3], qf[ks], s);
@@ -607,7 +615,7 @@ __global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd
         const int r = 8 * k2 + 2 * e2;
         const float p0 = __builtin_amdgcn_exp2f(fmaf(s[r], c, -lse2));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(s[r + 1], c, -lse2));
-        u[e2] = pack_bf16x2(p0 * (dp[r] + ndelta), p1 * (dp[r + 1] + ndelta));
+        u[e2] = pack_bf16x2(p0 * dp[r], p1 * dp[r + 1]);
       }
       dsb[k2] = bits_to_bf16x8(u);
     }

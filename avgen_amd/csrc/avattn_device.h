@@ -68,6 +68,13 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+__device__ __forceinline__ f32x16 splat16(float x) {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = x;
+  return z;
+}
+
 // Combine a value with the one held by the lane 32 positions away.
 // v_permlane32_swap exchanges the upper 32 lanes of its first operand with the
 // lower 32 lanes of its second; with both operands equal, every lane ends up
