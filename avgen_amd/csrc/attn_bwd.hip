@@ -451,16 +451,17 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
 //   dP^T = V dO^T   A = V rows (LDS)          B = dO^T (registers)
 //   dS^T = P^T * (dP^T + ndelta[q])           (fp32, key bias masks P^T)
 //   dQ^T += K^T dS^T   A = K^T (LDS, head_dim-major)  B = dS^T (C layout reused)
-// Tiles come from the padded copies through three LDS stages: tile t+2 is
-// loaded while tile t is computed, so each load has two tiles' time to land.
-// The body is unrolled over the three stages and branch-free apart from the
-// masked-tile bias.
-#ifndef AVATTN_DQ_WAVES
-#define AVATTN_DQ_WAVES 8
-#endif
+// Ping-pong: waves 0-3 (group A) and 4-7 (group B) share the SIMDs pairwise.
+// Group A runs S/dP(t), dS(t), dQ(t) in iteration t; group B is one tile
+// behind and runs dS(t-1), dQ(t-1), S/dP(t), carrying S^T/dP^T across the
+// barrier.  So while one wave of a SIMD computes dS (VALU), the other issues
+// MFMAs, and the per-tile barrier no longer lines both up on the same phase.
+// Tiles come from the padded copies through four LDS stages: tile t+2 is
+// loaded during iteration t (spread between MFMAs) and tile t-1 stays
+// resident for group B.
 template <int D>
-__global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd_dq_kernel(BwdArgs a) {
-  constexpr int NW = AVATTN_DQ_WAVES, BM = 32 * NW, BN = 32;
+__global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
+  constexpr int NW = 8, BM = 32 * NW, BN = 32;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BN * D;
   // One LDS object per stage (see bwd_dkdv_kernel).
@@ -471,7 +472,11 @@ __global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd
     float bias[64];  // key bias (this tile and the next)
     int flags[64];   // "all attended" flag of this tile (and the next 63)
   };
-  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2;
+  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
+  auto stage_ref = [&](auto bufc) __attribute__((always_inline)) -> Stage& {
+    constexpr int buf = decltype(bufc)::value;
+    return buf == 0 ? st0 : (buf == 1 ? st1 : (buf == 2 ? st2 : st3));
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -527,16 +532,19 @@ __global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd
   ktst.init(a.Lkp, wave, lane);
   // Vector-memory loads one stage issues per wave: K, V, K^T, bias, flags.
   constexpr int kStageLoads = 2 * RowStager::kPer + ColStager::kPer + 2;
-
-  auto stage = [&](int t, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    Stage& sg = buf == 0 ? st0 : (buf == 1 ? st1 : st2);
+  auto stage_op = [&](int t, auto bufc, int i) __attribute__((always_inline)) {
+    Stage& sg = stage_ref(bufc);
     const uint32_t k0 = (uint32_t)t * BN;
-    rst.stage(sg.k, rk, k0 * D * 2);
-    rst.stage(sg.v, rv, k0 * D * 2);
-    ktst.stage(sg.kt, rkt, k0 * 2);
-    dma4(rb, lds_addr(sg.bias), lane * 4, k0 * 4);
-    dma4(rf, lds_addr(sg.flags), lane * 4, (uint32_t)t * 4);
+    if (i < RowStager::kPer)
+      rst.stage_one(sg.k, rk, k0 * D * 2, i);
+    else if (i < 2 * RowStager::kPer)
+      rst.stage_one(sg.v, rv, k0 * D * 2, i - RowStager::kPer);
+    else if (i < 2 * RowStager::kPer + ColStager::kPer)
+      ktst.stage_one(sg.kt, rkt, k0 * 2, i - 2 * RowStager::kPer);
+    else if (i == kStageLoads - 2)
+      dma4(rb, lds_addr(sg.bias), lane * 4, k0 * 4);
+    else
+      dma4(rf, lds_addr(sg.flags), lane * 4, (uint32_t)t * 4);
   };
 
   int ko[KS];  // K/V row perm23(l32), chunk 16*ks + 8*hh
@@ -553,60 +561,46 @@ __global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd
   const float c = a.scale_log2;
   const int nkt = (a.Lk + BN - 1) / BN;
 
-  auto body = [&](int t, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    wait_vmem_n<kStageLoads>();  // tile t landed (tile t+1 may still be in flight)
-    barrier_lds();               // ... for every wave; tile t-1's stage is free
-    // Tile t+2 into the stage tile t-1 used (the last iterations re-stage a
-    // tile nobody reads, keeping the per-iteration load count fixed).
-    stage(min(t + 2, nkt - 1), std::integral_constant<int, (buf + 2) % 3>());
-    const Stage& sg = buf == 0 ? st0 : (buf == 1 ? st1 : st2);
-    const int full = __builtin_amdgcn_readfirstlane(sg.flags[0]);
-    const bf16* tk = sg.k;
-    const bf16* tv = sg.v;
-    const bf16* tkt = sg.kt;
-    const float* tb = sg.bias;
-
-    // S^T and dP^T: operand reads run four k-steps ahead of the MFMAs
-    // (sched_barrier pins the order; the scheduler would otherwise sink each
-    // read next to its MFMA and expose the LDS latency).
-    auto krow = [&](int ks) { return *reinterpret_cast<const bf16x8*>(tk + ko[ks]); };
-    auto vrow = [&](int ks) { return *reinterpret_cast<const bf16x8*>(tv + ko[ks]); };
-    bf16x8 ka[4], va[4];
+  // S^T and dP^T of one tile (2*KS MFMAs, the two chains alternating); dP^T
+  // starts at ndelta (one value per query column, i.e. per lane), so the MFMAs
+  // deliver dP^T + ndelta directly.  Operand reads run two k-steps (four
+  // MFMAs) ahead; `slot(j)` runs extra work after MFMA j; sched_barrier(0)
+  // pins the order.
+  auto sdp = [&](const Stage& sg, f32x16& s, f32x16& dp, auto&& slot) __attribute__((always_inline)) {
+    auto krow = [&](int ks) __attribute__((always_inline)) { return *reinterpret_cast<const bf16x8*>(sg.k + opaque(ko[ks])); };
+    auto vrow = [&](int ks) __attribute__((always_inline)) { return *reinterpret_cast<const bf16x8*>(sg.v + opaque(ko[ks])); };
+    bf16x8 ka[2], va[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       ka[j] = krow(j);
       va[j] = vrow(j);
     }
+    s = zero16();
+    dp = splat16(ndelta);
     __builtin_amdgcn_sched_barrier(0);
-    // dP^T starts at ndelta (one value per query column, i.e. per lane), so
-    // the MFMAs deliver dP^T + ndelta directly.
-    f32x16 s = zero16(), dp = splat16(ndelta);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      s = mfma32(ka[ks & 3], qf[ks], s);
-      dp = mfma32(va[ks & 3], df[ks], dp);
-      if (ks + 4 < KS) {
-        ka[ks & 3] = krow(ks + 4);
-        va[ks & 3] = vrow(ks + 4);
-      }
+      s = mfma32(ka[ks & 1], qf[ks], s);
+      if (ks + 2 < KS) ka[ks & 1] = krow(ks + 2);
+      slot(2 * ks);
+      __builtin_amdgcn_sched_barrier(0);
+      dp = mfma32(va[ks & 1], df[ks], dp);
+      if (ks + 2 < KS) va[ks & 1] = vrow(ks + 2);
+      slot(2 * ks + 1);
       __builtin_amdgcn_sched_barrier(0);
     }
-    // dQ operands (K^T) are read now, while the softmax below runs.
-    bf16x8 kta[2 * DT];
-#pragma unroll
-    for (int j = 0; j < 2 * DT; ++j) kta[j] = *reinterpret_cast<const bf16x8*>(tkt + (j % DT) * 32 * BN + to[j / DT]);
-    __builtin_amdgcn_sched_barrier(0);
-    // registers 8*k2 + e hold key 16*k2 + 8*hh + e
-    if (!full) {
+  };
+  // dS^T of one tile (its S^T, dP^T and stage) as the bf16 B operands of dQ;
+  // registers 8*k2 + e hold key 16*k2 + 8*hh + e.
+  auto dsm = [&](const Stage& sg, f32x16& s, const f32x16& dp, bf16x8* dsb) __attribute__((always_inline)) {
+    if (!__builtin_amdgcn_readfirstlane(sg.flags[0])) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const f32x4 bb = *reinterpret_cast<const f32x4*>(tb + 16 * (g >> 1) + 8 * hh + 4 * (g & 1));
+        const f32x4 bb = *reinterpret_cast<const f32x4*>(sg.bias + 16 * (g >> 1) + 8 * hh + 4 * (g & 1));
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[4 * g + r] += bb[r];
       }
     }
-    bf16x8 dsb[2];
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
       u32x4 u;
@@ -619,18 +613,110 @@ __global__ __launch_bounds__(64 * AVATTN_DQ_WAVES, 8 / AVATTN_DQ_WAVES) void bwd
       }
       dsb[k2] = bits_to_bf16x8(u);
     }
+  };
+  // dQ^T += K^T dS^T (2*DT MFMAs).  The first four K^T operands are read
+  // before dsm runs (their latency hides behind it), the rest four MFMAs
+  // ahead.
+  auto kt_op = [&](const Stage& sg, int j) __attribute__((always_inline)) {
+    return *reinterpret_cast<const bf16x8*>(sg.kt + (j % DT) * 32 * BN + opaque(to[j / DT]));
+  };
+  auto kt_read = [&](const Stage& sg, bf16x8* kta) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2 * DT; ++j) dq[j % DT] = mfma32(kta[j], dsb[j / DT], dq[j % DT]);
+    for (int j = 0; j < 4; ++j) kta[j] = kt_op(sg, j);
+  };
+  auto dqm = [&](const Stage& sg, bf16x8* kta, const bf16x8* dsb) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 2 * DT; ++j) {
+      dq[j % DT] = mfma32(kta[j & 3], dsb[j / DT], dq[j % DT]);
+      if (j + 4 < 2 * DT) kta[j & 3] = kt_op(sg, j + 4);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  static_assert(kStageLoads <= 2 * KS, "tile loads must fit the S/dP slots");
+  auto loads_in = [&](int t, auto nextc) __attribute__((always_inline)) {  // tile t's loads, one after each of the first MFMAs
+    return [&, t, nextc](int j) __attribute__((always_inline)) {
+      if (j < kStageLoads) stage_op(t, nextc, j);
+    };
+  };
+  // Top of iteration t: tile t landed (only tile t+1's loads may still be in
+  // flight) for every wave; the stage tile t-2 used is free for tile t+2.
+  auto top = [&]() __attribute__((always_inline)) {
+    wait_vmem_n<kStageLoads>();
+    barrier_lds();
   };
 
   retire_prologue_loads();
-  stage(0, std::integral_constant<int, 0>());
-  stage(min(1, nkt - 1), std::integral_constant<int, 1>());
-  for (int t = 0; t < nkt; t += 3) {
-    body(t, std::integral_constant<int, 0>());
-    if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());
-    if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 2>());
+  {
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+#pragma unroll
+    for (int i = 0; i < kStageLoads; ++i) stage_op(0, B0(), i);
+#pragma unroll
+    for (int i = 0; i < kStageLoads; ++i) stage_op(min(1, nkt - 1), B1(), i);
   }
+
+  f32x16 s, dp;
+  bf16x8 kta[4], dsb[2];
+  if (wave < NW / 2) {
+    // Group A: S/dP(t), dS(t), dQ(t).
+    auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      using Next2 = std::integral_constant<int, (buf + 2) % 4>;
+      top();
+      const Stage& sg = stage_ref(bufc);
+      __builtin_amdgcn_s_setprio(2);
+      sdp(sg, s, dp, loads_in(min(t + 2, nkt - 1), Next2()));
+      kt_read(sg, kta);
+      __builtin_amdgcn_s_setprio(0);
+      dsm(sg, s, dp, dsb);
+      __builtin_amdgcn_s_setprio(2);
+      dqm(sg, kta, dsb);
+    };
+    for (int t = 0; t < nkt; t += 4) {
+      body(t, std::integral_constant<int, 0>());
+      if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());
+      if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 2>());
+      if (t + 3 < nkt) body(t + 3, std::integral_constant<int, 3>());
+    }
+  } else {
+    // Group B: dS(t-1), dQ(t-1), S/dP(t); S^T/dP^T of tile t are carried to
+    // the next iteration.
+    auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
+      constexpr int buf = decltype(bufc)::value;
+      using Prev = std::integral_constant<int, (buf + 3) % 4>;
+      using Next2 = std::integral_constant<int, (buf + 2) % 4>;
+      top();
+      const Stage& sp = stage_ref(Prev());
+      kt_read(sp, kta);
+      __builtin_amdgcn_s_setprio(0);
+      dsm(sp, s, dp, dsb);
+      __builtin_amdgcn_s_setprio(2);
+      dqm(sp, kta, dsb);
+      sdp(stage_ref(bufc), s, dp, loads_in(min(t + 2, nkt - 1), Next2()));
+    };
+    {
+      // Iteration 0: only S/dP(0).
+      top();
+      sdp(stage_ref(std::integral_constant<int, 0>()), s, dp,
+          loads_in(min(2, nkt - 1), std::integral_constant<int, 2>()));
+    }
+    for (int t = 1; t < nkt; t += 4) {
+      body(t, std::integral_constant<int, 1>());
+      if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 2>());
+      if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 3>());
+      if (t + 3 < nkt) body(t + 3, std::integral_constant<int, 0>());
+    }
+    // Tail: dS and dQ of the last tile (its stage is not refilled).
+    const int bl = (nkt - 1) % 4;
+    const Stage& sl = bl == 0 ? st0 : (bl == 1 ? st1 : (bl == 2 ? st2 : st3));
+    kt_read(sl, kta);
+    __builtin_amdgcn_s_setprio(0);
+    dsm(sl, s, dp, dsb);
+    dqm(sl, kta, dsb);
+  }
+  __builtin_amdgcn_s_setprio(0);
+  wait_vmem();  // the last (re-staged) tile loads
 
   if (qvalid) {
     bf16* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)qrow * a.dqsl;
@@ -689,11 +775,11 @@ static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
       hipLaunchKernelGGL((bwd_dkdv_kernel<D, false>), grid, dim3(512), 0, stream, a);
   }
   {
-    constexpr int BM = 32 * AVATTN_DQ_WAVES;
+    constexpr int BM = 256;  // 8 waves x 32 query rows
     const int nqt = (a.Lq + BM - 1) / BM;
     const dim3 grid(nqt * a.B * a.Hq);
     LaunchTimer timer(kKidBwdDq, stream);
-    hipLaunchKernelGGL(bwd_dq_kernel<D>, grid, dim3(64 * AVATTN_DQ_WAVES), 0, stream, a);
+    hipLaunchKernelGGL(bwd_dq_kernel<D>, grid, dim3(512), 0, stream, a);
   }
   return hipGetLastError();
 }

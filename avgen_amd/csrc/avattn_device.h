@@ -68,6 +68,15 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// The same value, opaque to the optimizer at this point of the program: an
+// LDS offset passed through it is added to a stage's base where it is used
+// (folded into the instruction's offset field when that fits) instead of
+// being hoisted out of the loop as one extra register per stage.
+__device__ __forceinline__ int opaque(int x) {
+  __asm__ volatile("" : "+v"(x));
+  return x;
+}
+
 __device__ __forceinline__ f32x16 splat16(float x) {
   f32x16 z;
 #pragma unroll
