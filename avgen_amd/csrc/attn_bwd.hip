@@ -547,12 +547,30 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
       dma4(rf, lds_addr(sg.flags), lane * 4, (uint32_t)t * 4);
   };
 
-  int ko[KS];  // K/V row perm23(l32), chunk 16*ks + 8*hh
+  // Per-lane LDS byte offsets inside a tile.  Each iteration passes them
+  // through opaque() once (Off), so every read of that iteration adds its
+  // stage's base as an instruction immediate instead of the compiler keeping
+  // one hoisted copy of every offset per stage in registers.
+  struct Off {
+    int k[KS];  // K/V row perm23(l32), chunk 16*ks + 8*hh
+    int t[2];   // K^T row l32, key chunk 16*k2 + 8*hh (+32*dt rows)
+  };
+  Off off0;
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) ko[ks] = TileLayout<D>::off(prow, 16 * ks + 8 * hh);
-  int to[2];  // K^T row l32 (+32*dt), key chunk 16*k2 + 8*hh
+  for (int ks = 0; ks < KS; ++ks) off0.k[ks] = 2 * TileLayout<D>::off(prow, 16 * ks + 8 * hh);
 #pragma unroll
-  for (int k2 = 0; k2 < 2; ++k2) to[k2] = TileLayout<BN>::off(l32, 16 * k2 + 8 * hh);
+  for (int k2 = 0; k2 < 2; ++k2) off0.t[k2] = 2 * TileLayout<BN>::off(l32, 16 * k2 + 8 * hh);
+  auto fresh = [&]() __attribute__((always_inline)) {
+    Off o;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) o.k[ks] = opaque(off0.k[ks]);
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) o.t[k2] = opaque(off0.t[k2]);
+    return o;
+  };
+  auto lds16 = [](const void* base, int byte_off) __attribute__((always_inline)) {
+    return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const char*>(base) + byte_off);
+  };
 
   f32x16 dq[DT];
 #pragma unroll
@@ -566,9 +584,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
   // deliver dP^T + ndelta directly.  Operand reads run two k-steps (four
   // MFMAs) ahead; `slot(j)` runs extra work after MFMA j; sched_barrier(0)
   // pins the order.
-  auto sdp = [&](const Stage& sg, f32x16& s, f32x16& dp, auto&& slot) __attribute__((always_inline)) {
-    auto krow = [&](int ks) __attribute__((always_inline)) { return *reinterpret_cast<const bf16x8*>(sg.k + opaque(ko[ks])); };
-    auto vrow = [&](int ks) __attribute__((always_inline)) { return *reinterpret_cast<const bf16x8*>(sg.v + opaque(ko[ks])); };
+  auto sdp = [&](const Stage& sg, const Off& o, f32x16& s, f32x16& dp, auto&& slot) __attribute__((always_inline)) {
+    auto krow = [&](int ks) __attribute__((always_inline)) { return lds16(sg.k, o.k[ks]); };
+    auto vrow = [&](int ks) __attribute__((always_inline)) { return lds16(sg.v, o.k[ks]); };
     bf16x8 ka[2], va[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -592,7 +610,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
   };
   // dS^T of one tile (its S^T, dP^T and stage) as the bf16 B operands of dQ;
   // registers 8*k2 + e hold key 16*k2 + 8*hh + e.
-  auto dsm = [&](const Stage& sg, f32x16& s, const f32x16& dp, bf16x8* dsb) __attribute__((always_inline)) {
+  auto dsm = [&](const Stage& sg, f32x16& s, const f32x16& dp, bf16x8* dsb, auto&& slot) __attribute__((always_inline)) {
     if (!__builtin_amdgcn_readfirstlane(sg.flags[0])) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -610,6 +628,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
         const float p0 = __builtin_amdgcn_exp2f(fmaf(s[r], c, -lse2));
         const float p1 = __builtin_amdgcn_exp2f(fmaf(s[r + 1], c, -lse2));
         u[e2] = pack_bf16x2(p0 * dp[r], p1 * dp[r + 1]);
+        slot(4 * k2 + e2);
       }
       dsb[k2] = bits_to_bf16x8(u);
     }
@@ -617,23 +636,29 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
   // dQ^T += K^T dS^T (2*DT MFMAs).  The first four K^T operands are read
   // before dsm runs (their latency hides behind it), the rest four MFMAs
   // ahead.
-  auto kt_op = [&](const Stage& sg, int j) __attribute__((always_inline)) {
-    return *reinterpret_cast<const bf16x8*>(sg.kt + (j % DT) * 32 * BN + opaque(to[j / DT]));
+  auto kt_op = [&](const Stage& sg, const Off& o, int j) __attribute__((always_inline)) {
+    return lds16(sg.kt + (j % DT) * 32 * BN, o.t[j / DT]);
   };
-  auto kt_read = [&](const Stage& sg, bf16x8* kta) __attribute__((always_inline)) {
+  auto kt_read = [&](const Stage& sg, const Off& o, bf16x8* kta) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kta[j] = kt_op(sg, j);
+    for (int j = 0; j < 4; ++j) kta[j] = kt_op(sg, o, j);
   };
-  auto dqm = [&](const Stage& sg, bf16x8* kta, const bf16x8* dsb) __attribute__((always_inline)) {
+  auto dqm = [&](const Stage& sg, const Off& o, bf16x8* kta, const bf16x8* dsb, auto&& slot) __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < 2 * DT; ++j) {
       dq[j % DT] = mfma32(kta[j & 3], dsb[j / DT], dq[j % DT]);
-      if (j + 4 < 2 * DT) kta[j & 3] = kt_op(sg, j + 4);
+      if (j + 4 < 2 * DT) kta[j & 3] = kt_op(sg, o, j + 4);
+      slot(j);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  static_assert(kStageLoads <= 2 * KS, "tile loads must fit the S/dP slots");
+  // Where a tile's loads are issued: between the dQ MFMAs when they fit there
+  // (measured ~1% faster than between the S/dP MFMAs), else between the S/dP
+  // MFMAs (0); 2 would spread them over the dS VALU steps (measured slower).
+  constexpr int kLoadsAt = kStageLoads <= 2 * DT ? 1 : 0;
+  static_assert(kStageLoads <= 2 * KS && kStageLoads <= 8, "tile loads must fit the slots");
+  auto no_slot = [](int) __attribute__((always_inline)) {};
   auto loads_in = [&](int t, auto nextc) __attribute__((always_inline)) {  // tile t's loads, one after each of the first MFMAs
     return [&, t, nextc](int j) __attribute__((always_inline)) {
       if (j < kStageLoads) stage_op(t, nextc, j);
@@ -665,13 +690,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
       using Next2 = std::integral_constant<int, (buf + 2) % 4>;
       top();
       const Stage& sg = stage_ref(bufc);
+      const Off o = fresh();
+      auto ld = loads_in(min(t + 2, nkt - 1), Next2());
       __builtin_amdgcn_s_setprio(2);
-      sdp(sg, s, dp, loads_in(min(t + 2, nkt - 1), Next2()));
-      kt_read(sg, kta);
+      if constexpr (kLoadsAt == 0) sdp(sg, o, s, dp, ld); else sdp(sg, o, s, dp, no_slot);
+      kt_read(sg, o, kta);
       __builtin_amdgcn_s_setprio(0);
-      dsm(sg, s, dp, dsb);
+      if constexpr (kLoadsAt == 2) dsm(sg, s, dp, dsb, ld); else dsm(sg, s, dp, dsb, no_slot);
       __builtin_amdgcn_s_setprio(2);
-      dqm(sg, kta, dsb);
+      if constexpr (kLoadsAt == 1) dqm(sg, o, kta, dsb, ld); else dqm(sg, o, kta, dsb, no_slot);
     };
     for (int t = 0; t < nkt; t += 4) {
       body(t, std::integral_constant<int, 0>());
@@ -688,18 +715,27 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
       using Next2 = std::integral_constant<int, (buf + 2) % 4>;
       top();
       const Stage& sp = stage_ref(Prev());
-      kt_read(sp, kta);
+      const Off o = fresh();
+      auto ld = loads_in(min(t + 2, nkt - 1), Next2());
+      kt_read(sp, o, kta);
       __builtin_amdgcn_s_setprio(0);
-      dsm(sp, s, dp, dsb);
+      if constexpr (kLoadsAt == 2) dsm(sp, s, dp, dsb, ld); else dsm(sp, s, dp, dsb, no_slot);
       __builtin_amdgcn_s_setprio(2);
-      dqm(sp, kta, dsb);
-      sdp(stage_ref(bufc), s, dp, loads_in(min(t + 2, nkt - 1), Next2()));
+      if constexpr (kLoadsAt == 1) dqm(sp, o, kta, dsb, ld); else dqm(sp, o, kta, dsb, no_slot);
+      if constexpr (kLoadsAt == 0) sdp(stage_ref(bufc), o, s, dp, ld); else sdp(stage_ref(bufc), o, s, dp, no_slot);
     };
     {
       // Iteration 0: only S/dP(0).
+      using B2 = std::integral_constant<int, 2>;
       top();
-      sdp(stage_ref(std::integral_constant<int, 0>()), s, dp,
-          loads_in(min(2, nkt - 1), std::integral_constant<int, 2>()));
+      const Off o = fresh();
+      if constexpr (kLoadsAt == 0) {
+        sdp(stage_ref(std::integral_constant<int, 0>()), o, s, dp, loads_in(min(2, nkt - 1), B2()));
+      } else {
+        sdp(stage_ref(std::integral_constant<int, 0>()), o, s, dp, no_slot);
+#pragma unroll
+        for (int i = 0; i < kStageLoads; ++i) stage_op(min(2, nkt - 1), B2(), i);
+      }
     }
     for (int t = 1; t < nkt; t += 4) {
       body(t, std::integral_constant<int, 1>());
@@ -710,10 +746,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
     // Tail: dS and dQ of the last tile (its stage is not refilled).
     const int bl = (nkt - 1) % 4;
     const Stage& sl = bl == 0 ? st0 : (bl == 1 ? st1 : (bl == 2 ? st2 : st3));
-    kt_read(sl, kta);
+    const Off o = fresh();
+    kt_read(sl, o, kta);
     __builtin_amdgcn_s_setprio(0);
-    dsm(sl, s, dp, dsb);
-    dqm(sl, kta, dsb);
+    dsm(sl, s, dp, dsb, no_slot);
+    dqm(sl, o, kta, dsb, no_slot);
   }
   __builtin_amdgcn_s_setprio(0);
   wait_vmem();  // the last (re-staged) tile loads
