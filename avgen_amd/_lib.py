@@ -63,6 +63,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_f32,
          c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
          c_ptr, c_size,
+         ctypes.c_uint32,
          c_ptr],
     ),
     "avattn_lse_merge": (ctypes.c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i32, c_i32, c_ptr]),
@@ -95,6 +96,10 @@ ERR_WORKSPACE = 6
 ERR_LAUNCH = 7
 ERR_TOO_LARGE = 8
 ERR_ARGUMENT = 9
+
+# avattn_bwd flags (include/avattn.h).
+BWD_REUSE_QUERY_SIDE = 1
+BWD_DQ_ACCUMULATE_F32 = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

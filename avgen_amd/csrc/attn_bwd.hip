@@ -755,7 +755,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
   __builtin_amdgcn_s_setprio(0);
   wait_vmem();  // the last (re-staged) tile loads
 
-  if (qvalid) {
+  if (qvalid && a.dq_acc) {
+    // fp32 accumulation: dq_acc += this chunk's dq (each element owned by
+    // exactly one lane, so a plain load-add-store).
+    float* op = a.dq_acc + b * a.dqsb + h * a.dqsh + (int64_t)qrow * a.dqsl;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4* p = reinterpret_cast<f32x4*>(op + dt * 32 + 8 * g + 4 * hh);
+        f32x4 w = *p;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[r] += dq[dt][4 * g + r] * a.scale;
+        *p = w;
+      }
+  } else if (qvalid) {
     bf16* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)qrow * a.dqsl;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -788,15 +802,18 @@ static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
   const bool mask = a.mask != nullptr;
   {
     LaunchTimer timer(kKidTranspose, stream);
-    hipError_t e = launch_prep_copies(a.q, a.qsb, a.qsh, a.qsl, a.B, a.Hq, a.Lq, D, a.qr, a.qt, stream);
-    if (e == hipSuccess)
-      e = launch_prep_copies(a.dout, a.dosb, a.dosh, a.dosl, a.B, a.Hq, a.Lq, D, a.dor, a.dot, stream);
+    hipError_t e = hipSuccess;
+    if (!a.reuse_q) {
+      e = launch_prep_copies(a.q, a.qsb, a.qsh, a.qsl, a.B, a.Hq, a.Lq, D, a.qr, a.qt, stream);
+      if (e == hipSuccess)
+        e = launch_prep_copies(a.dout, a.dosb, a.dosh, a.dosl, a.B, a.Hq, a.Lq, D, a.dor, a.dot, stream);
+    }
     if (e == hipSuccess) e = launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, a.kt, stream);
     if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, a.vr, nullptr, stream);
     if (e == hipSuccess) e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
     if (e != hipSuccess) return e;
   }
-  {
+  if (!a.reuse_q) {
     constexpr int RPB = 256 / (D / 8);
     const int64_t rows = (int64_t)a.B * a.Hq * a.Lqp;
     LaunchTimer timer(kKidBwdPre, stream);

@@ -15,8 +15,10 @@ constexpr int64_t kMaxI32 = 2147483647;
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Row starts must stay 16-byte aligned: every stride a multiple of 8 bf16.
+// Row starts must stay 16-byte aligned: every stride a multiple of 8 bf16
+// (or 4 floats for an fp32 tensor).
 bool strides_ok(const int64_t* s) { return s && s[0] % 8 == 0 && s[1] % 8 == 0 && s[2] % 8 == 0; }
+bool strides_ok_f32(const int64_t* s) { return s && s[0] % 4 == 0 && s[1] % 4 == 0 && s[2] % 4 == 0; }
 
 int check_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32_t D) {
   if (B < 0 || Hq < 0 || Hkv < 0 || Lq < 0 || Lk < 0) return AVATTN_ERR_BAD_SHAPE;
@@ -112,7 +114,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 3; }
+int avattn_abi_version(void) { return 4; }
 
 }  // extern "C"
 
@@ -244,8 +246,10 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
                int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
                int64_t key_mask_batch_stride, float scale, void* dq, const int64_t* dq_strides, void* dk,
                const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
-               size_t workspace_bytes, avattn_stream_t stream) {
+               size_t workspace_bytes, uint32_t flags, avattn_stream_t stream) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32)) return AVATTN_ERR_ARGUMENT;
+  const bool dq_f32 = (flags & AVATTN_BWD_DQ_ACCUMULATE_F32) != 0;
   if (st != AVATTN_OK) return st;
   if (!dout_strides || !q_strides || !k_strides || !v_strides || !out_strides || !dq_strides || !dk_strides ||
       !dv_strides)
@@ -254,7 +258,7 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   if ((int64_t)batch * heads_q == 0) return AVATTN_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool have_q = len_q > 0, have_k = len_k > 0;
-  if (have_q && (!dq || !aligned16(dq) || !strides_ok(dq_strides)))
+  if (have_q && (!dq || !aligned16(dq) || !(dq_f32 ? strides_ok_f32(dq_strides) : strides_ok(dq_strides))))
     return !dq ? AVATTN_ERR_NULL_POINTER : AVATTN_ERR_LAYOUT;
   if (have_k && (!dk || !dv)) return AVATTN_ERR_NULL_POINTER;
   if (have_k && (!aligned16(dk) || !aligned16(dv) || !strides_ok(dk_strides) || !strides_ok(dv_strides)))
@@ -262,7 +266,7 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   if (!have_q || !have_k) {
     // Empty attention: every gradient is zero.
     hipError_t e = hipSuccess;
-    if (have_q)
+    if (have_q && !dq_f32)  // an fp32 accumulator gets nothing added
       e = launch_zero_rows(static_cast<bf16*>(dq), dq_strides[0], dq_strides[1], dq_strides[2], batch, heads_q, len_q,
                            head_dim, s);
     if (e == hipSuccess && have_k)
@@ -299,7 +303,9 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   a.msb = key_mask_batch_stride;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;
-  a.dq = static_cast<bf16*>(dq);
+  a.dq = dq_f32 ? nullptr : static_cast<bf16*>(dq);
+  a.dq_acc = dq_f32 ? static_cast<float*>(dq) : nullptr;
+  a.reuse_q = (flags & AVATTN_BWD_REUSE_QUERY_SIDE) != 0;
   a.dqsb = dq_strides[0]; a.dqsh = dq_strides[1]; a.dqsl = dq_strides[2];
   a.dk = static_cast<bf16*>(dk);
   a.dksb = dk_strides[0]; a.dksh = dk_strides[1]; a.dksl = dk_strides[2];

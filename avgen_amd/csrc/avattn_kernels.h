@@ -83,6 +83,12 @@ struct BwdArgs {
   float* kbias;  // (B, Lkp): 0 attended / -inf
   int* kfull;    // (B, Lkp/32): 1 if every key of the 32-key tile is attended
   int Lqp, Lkp;
+  // dq as an fp32 accumulator (dq_acc += this chunk's dq; dq is then null),
+  // strides dqsb/dqsh/dqsl in floats.
+  float* dq_acc;
+  // The query-side preparation (q/dout copies, lse2, ndelta) is already in
+  // the workspace: skip it.
+  bool reuse_q;
 };
 
 // Kernel ids of the opt-in launch timer (avattn_timing_* in include/avattn.h).

@@ -217,9 +217,18 @@ def _out_or_new(t: Optional[torch.Tensor], like: torch.Tensor, name: str, label:
     return t
 
 
-def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=None):
+def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=None, *,
+              workspace=None, reuse_query_side=False, dq_accumulate=None):
     """Backward launch; ``dq``/``dk``/``dv`` may be preallocated outputs
-    (written in place, e.g. slices of a full-sequence gradient)."""
+    (written in place, e.g. slices of a full-sequence gradient).
+
+    Ring-step options (one query shard against consecutive KV chunks):
+    ``workspace`` is a caller-kept workspace of at least the size this call
+    needs; ``reuse_query_side`` asserts that it already holds the query-side
+    preparation of a previous call with the same dout/q/out/lse/scale;
+    ``dq_accumulate`` is an fp32 tensor shaped like q that this chunk's dq is
+    added to (returned in dq's place).
+    """
     name = "avgen_amd.flash_bwd"
     _check_qkv(name, q, k, v)
     _require_gpu(name, dout, q, k, v, out, lse, key_mask)
@@ -234,11 +243,31 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
     dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
     lse = lse.contiguous()
     mask, msb = _normalise_mask(name, key_mask, B, Lk)
-    dq = _out_or_new(dq, q, name, "dq")
+    flags = 0
+    if dq_accumulate is not None:
+        if dq_accumulate.shape != q.shape or dq_accumulate.dtype is not torch.float32:
+            raise ValueError(f"{name}: dq accumulator must be float32 {tuple(q.shape)}")
+        if dq_accumulate.stride(-1) != 1 or dq_accumulate.data_ptr() % 16 or any(
+                st % 4 for st in dq_accumulate.stride()[:3]):
+            raise ValueError(f"{name}: dq accumulator needs a contiguous head_dim and 16-byte aligned rows")
+        dq = dq_accumulate
+        flags |= _lib.BWD_DQ_ACCUMULATE_F32
+    else:
+        dq = _out_or_new(dq, q, name, "dq")
     dk = _out_or_new(dk, k, name, "dk")
     dv = _out_or_new(dv, v, name, "dv")
     lib = _lib.load()
-    ws = _workspace(lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D), q.device)
+    need = lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D)
+    if workspace is None:
+        if reuse_query_side:
+            raise ValueError(f"{name}: reuse_query_side needs the caller's workspace")
+        ws = _workspace(need, q.device)
+    else:
+        if workspace.dtype is not torch.uint8 or workspace.numel() < need or workspace.device != q.device:
+            raise ValueError(f"{name}: workspace must be uint8 with at least {need} bytes on {q.device}")
+        ws = workspace
+    if reuse_query_side:
+        flags |= _lib.BWD_REUSE_QUERY_SIDE
     st = lib.avattn_bwd(
         _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
         _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
@@ -247,6 +276,7 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
         float(scale),
         _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
         _ptr(ws), ws.numel(),
+        flags,
         _stream(q.device),
     )
     _lib.check(st, name)

@@ -202,22 +202,31 @@ def ring_attention_backward(
 
 
 def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, scale):
-    """The emulated ring's backward writing each chunk's dk/dv straight into
-    its slice of the full-sequence gradients (one chunk, one contribution, so
-    no accumulation or concatenation is needed); dq accumulates in fp32 as
-    in :func:`ring_attention_backward`."""
+    """The emulated ring's backward.  Each chunk's dk/dv goes straight into its
+    slice of the full-sequence gradients (one chunk, one contribution, so no
+    accumulation or concatenation is needed); dq accumulates in fp32 as in
+    the torch ring (torch/.../_attention.py:505-506, 623, 636), inside the
+    kernel; the query-side preparation (copies of q and dout, softmax
+    statistics) is made for the first chunk and reused for the others."""
     L = key.shape[2]
     D = query.shape[-1]
     scale = ops.default_scale(D) if scale is None else float(scale)
     dk = torch.empty(key.shape, dtype=key.dtype, device=key.device)
     dv = torch.empty(value.shape, dtype=value.dtype, device=value.device)
-    dq_acc = None
+    dq_acc = torch.zeros(query.shape, dtype=torch.float32, device=query.device)
+    from . import _lib
+
+    B, Hq, Lq, _ = query.shape
+    Hkv = key.shape[1]
+    need = max(_lib.load().avattn_bwd_workspace_size(B, Hq, Hkv, Lq, b - a, D)
+               for a, b in (shard_bounds(L, cp, r) for r in range(cp)))
+    ws = ops._workspace(need, query.device)
     for r in range(cp):
         a, b = shard_bounds(L, cp, r)
         m = None if key_mask is None else key_mask[:, a:b]
-        dq_i, _, _ = ops._bwd_impl(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse, m, scale,
-                                   dk=dk[:, :, a:b], dv=dv[:, :, a:b])
-        dq_acc = dq_i.float() if dq_acc is None else dq_acc.add_(dq_i)
+        ops._bwd_impl(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse, m, scale,
+                      dk=dk[:, :, a:b], dv=dv[:, :, a:b], workspace=ws, reuse_query_side=r > 0,
+                      dq_accumulate=dq_acc)
     return dq_acc.to(query.dtype), dk, dv
 
 

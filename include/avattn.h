@@ -164,9 +164,25 @@ int avattn_fp8_absmax_scales(const void* x, const int64_t* x_strides,
  * *merged* output and LSE of all KV chunks, in which case dq/dk/dv are this
  * chunk's contributions.  dk/dv of a masked key are exactly 0.  With
  * heads_kv < heads_q, dk/dv sum over the query heads of each group.
- * workspace must hold avattn_bwd_workspace_size() bytes; it is scratch for
- * this call only.
+ * workspace must hold avattn_bwd_workspace_size() bytes; its query-side part
+ * (statistics and the q/dout copies, at offsets that depend only on batch,
+ * heads_q, len_q and head_dim) may be kept between calls, everything else is
+ * scratch for this call.
+ * flags (bitwise or, 0 = neither):
+ *   AVATTN_BWD_REUSE_QUERY_SIDE  the workspace already holds the query-side
+ *       preparation of a previous avattn_bwd call with the same dout, q, out,
+ *       lse, scale, batch, heads_q, len_q and head_dim (e.g. the previous KV
+ *       chunk of one ring step); it is not recomputed.  The caller asserts
+ *       this; stale contents give wrong gradients.
+ *   AVATTN_BWD_DQ_ACCUMULATE_F32 dq is float32 (strides in float elements,
+ *       multiples of 4, 16-byte aligned) and this chunk's dq is added to it
+ *       in fp32 (before any rounding) instead of being written as bf16: the
+ *       fp32 dq sum over KV chunks of the ring backward
+ *       (torch/.../_context_parallel/_attention.py:505-506, 623, 636) without a
+ *       separate add per chunk.
  */
+#define AVATTN_BWD_REUSE_QUERY_SIDE  1u
+#define AVATTN_BWD_DQ_ACCUMULATE_F32 2u
 int avattn_bwd(const void* dout, const void* q, const void* k, const void* v,
                const void* out, const float* lse,
                const int64_t* dout_strides, const int64_t* q_strides,
@@ -180,6 +196,7 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v,
                void* dk, const int64_t* dk_strides,
                void* dv, const int64_t* dv_strides,
                void* workspace, size_t workspace_bytes,
+               uint32_t flags,
                avattn_stream_t stream);
 
 /*

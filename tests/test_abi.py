@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 3
+    assert lib.avattn_abi_version() == 4
     for code in range(0, 10):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
@@ -134,8 +134,18 @@ def test_fwd_validation_paths(lib):
 def test_bwd_validation_paths(lib):
     s = _lib.i64_array([1 << 17, 1 << 17, 128])
     base = [16, 16, 16, 16, 16, 16, s, s, s, s, s, 1, 2, 2, 4, 4, 128, None, 0, 0.125,
-            16, s, 16, s, 16, s, 16, 8, None]
+            16, s, 16, s, 16, s, 16, 8, 0, None]
     assert lib.avattn_bwd(*base) == _lib.ERR_WORKSPACE  # 8 bytes < 2*1*2*4*4
+    bad = list(base)
+    bad[28] = 4  # unknown flag
+    assert lib.avattn_bwd(*bad) == _lib.ERR_ARGUMENT
+    # fp32 dq accumulator: strides in floats, multiples of 4 (not 8)
+    bad = list(base)
+    bad[28] = _lib.BWD_DQ_ACCUMULATE_F32
+    bad[21] = _lib.i64_array([1 << 16, 1 << 16, 132])
+    assert lib.avattn_bwd(*bad) == _lib.ERR_WORKSPACE  # layout accepted, reaches the workspace check
+    bad[21] = _lib.i64_array([1 << 16, 1 << 16, 130])
+    assert lib.avattn_bwd(*bad) == _lib.ERR_LAYOUT
     bad = list(base)
     bad[16] = 80
     assert lib.avattn_bwd(*bad) == _lib.ERR_HEAD_DIM

@@ -312,6 +312,31 @@ def test_emulated_ring_matches_unchunked(amd, masked, Hkv):
         assert np.abs(_f64(got) - ref).max() <= GRAD_REL_TOL * np.abs(ref).max()
 
 
+def test_bwd_query_side_reuse_and_dq_accumulation(amd):
+    """avattn_bwd flags: the query-side preparation kept in the workspace gives
+    bit-identical dk/dv, and the fp32 dq accumulator equals the sum of the
+    per-chunk dq up to their bf16 rounding (it adds unrounded values)."""
+    B, H, Lq, Lc, D = 1, 2, 200, 150, 128
+    q, do = _randn((B, H, Lq, D), 70).cuda(), _randn((B, H, Lq, D), 71).cuda()
+    ks = [_randn((B, H, Lc, D), 72 + i).cuda() for i in range(2)]
+    vs = [_randn((B, H, Lc, D), 74 + i).cuda() for i in range(2)]
+    kf, vf = torch.cat(ks, 2), torch.cat(vs, 2)
+    out, lse = amd.ops.flash_fwd(q, kf, vf, None, None, None, D ** -0.5)
+    ref = [amd.ops.flash_bwd(do, q, k, v, out, lse, None, D ** -0.5) for k, v in zip(ks, vs)]
+    lib = amd._lib.load()
+    ws = amd.ops._workspace(lib.avattn_bwd_workspace_size(B, H, H, Lq, Lc, D), q.device)
+    acc = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
+    for i, (k, v) in enumerate(zip(ks, vs)):
+        _, dk, dv = amd.ops._bwd_impl(do, q, k, v, out, lse, None, D ** -0.5, workspace=ws,
+                                      reuse_query_side=i > 0, dq_accumulate=acc)
+        assert torch.equal(dk, ref[i][1]) and torch.equal(dv, ref[i][2])
+    summed = ref[0][0].float() + ref[1][0].float()
+    assert (acc - summed).abs().max().item() <= 8e-3 * summed.abs().max().item()
+    rq, _, _ = R.attention_bwd_f64(_f64(do), _f64(q), _f64(kf), _f64(vf), _f64(out),
+                                   lse.cpu().numpy().astype(np.float64))
+    assert np.abs(acc.cpu().numpy() - rq).max() <= GRAD_REL_TOL * np.abs(rq).max()
+
+
 def test_ring_step_signatures_drop_into_torch_loop(amd):
     # Call the local-step ops exactly as torch's ring does
     # (torch/.../_attention.py:468-475 and 567-575).
