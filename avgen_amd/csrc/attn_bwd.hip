@@ -206,9 +206,18 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // column half.  Waiting until at most that many are outstanding retires the
   // older half the coming phase reads.
   constexpr int kInFlight = kRowHalf + kColHalf;
-  // Slots of a phase that issue its `count` loads (one in every third slot;
-  // the rest follow the phase's loop).
-  auto load_slot = [](int j, int nslots, int count) { return j % 3 == 1 && j / 3 < count && j < nslots; };
+  // Slots of a phase that issue its `count` loads: every second slot from
+  // slot kLoad0 on (the start of a phase is left to its operand and
+  // statistics reads); the rest follow the phase's loop.  Load i goes in slot
+  // kLoad0 + 2*i.
+  constexpr int kLoad0 = 6;
+  auto load_slot = [](int j, int nslots, int count) {
+    return j >= kLoad0 && (j - kLoad0) % 2 == 0 && (j - kLoad0) / 2 < count && j < nslots;
+  };
+  auto loads_in_loop = [](int nslots) { return nslots > kLoad0 ? (nslots - kLoad0 + 1) / 2 : 0; };
+  // Operand reads in flight ahead of the MFMAs (three measured faster than
+  // four or six: fewer LDS requests queued at once).
+  constexpr int kRA = 3;
 
   const float c = a.scale_log2;
 
@@ -232,18 +241,17 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
 
     constexpr int NS = 2 * KS;  // QK^T MFMAs: (sub, ks)
     auto qop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.q + (j / KS) * 32 * D + ro[j % KS]); };
-    bf16x8 qa[4];
+    bf16x8 qa[kRA];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) qa[j] = qop(j);
-    // lse2 of this lane's 16 rows per sub: 8 consecutive rows per k2.
+    for (int j = 0; j < kRA; ++j) qa[j] = qop(j);
+    // lse2 of this lane's 16 rows per sub (8 consecutive rows per k2), read
+    // one f32x4 per slot from slot 1 on (the softmax needs them only later;
+    // reading them up front delays the first MFMAs' operands).
     f32x4 l2[2][2][2];
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-          l2[sub][k2][hf] = *reinterpret_cast<const f32x4*>(rsg.lse2 + 32 * sub + 16 * k2 + 8 * hh + 4 * hf);
+    auto l2_read = [&](int q8) {
+      l2[q8 >> 2][(q8 >> 1) & 1][q8 & 1] =
+          *reinterpret_cast<const f32x4*>(rsg.lse2 + 32 * (q8 >> 2) + 16 * ((q8 >> 1) & 1) + 8 * hh + 4 * (q8 & 1));
+    };
     __builtin_amdgcn_sched_barrier(0);
 
     f32x16 s[2] = {zero16(), zero16()};
@@ -268,9 +276,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int sub = j / KS, ks = j % KS;
-      s[sub] = mfma32(qa[j & 3], kv[ks], s[sub]);
-      if (j + 4 < NS) qa[j & 3] = qop(j + 4);
-      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), j / 3);
+      s[sub] = mfma32(qa[j % kRA], kv[ks], s[sub]);
+      if (j + kRA < NS) qa[j % kRA] = qop(j + kRA);
+      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / 2);
+      if (j >= 1 && j <= 8) l2_read(j - 1);
       if (j >= kLo) {
         const int n = NS - kLo;
         for (int st = (j - kLo) * 8 / n; st < (j - kLo + 1) * 8 / n; ++st) smx(0, st >> 2, st & 3);
@@ -278,7 +287,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NS + 1) / 3; i < kColHalf; ++i) col_op(itc, NextBuf(), i);
+    for (int i = loads_in_loop(NS); i < kColHalf; ++i) col_op(itc, NextBuf(), i);
+#pragma unroll
+    for (int q8 = NS - 1; q8 < 8; ++q8) l2_read(q8);  // what the loop had no slot for
     if (kLo >= NS) {
 #pragma unroll
       for (int st = 0; st < 8; ++st) smx(0, st >> 2, st & 3);
@@ -295,21 +306,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int sk = j / DT, dt = j % DT;  // sk = 2*sub + k2
       return *reinterpret_cast<const bf16x8*>(csg.dot + dt * 32 * BQ + to[sk]);
     };
-    bf16x8 opq[4];
+    bf16x8 opq[kRA];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) opq[j] = dot_op(j);
+    for (int j = 0; j < kRA; ++j) opq[j] = dot_op(j);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
-      const bf16x8 op = opq[j % 4];
-      if (j + 4 < NJ) opq[j % 4] = dot_op(j + 4);
+      const bf16x8 op = opq[j % kRA];
+      if (j + kRA < NJ) opq[j % kRA] = dot_op(j + kRA);
       const int sk = j / DT, dt = j % DT;
       acc[dt] = mfma32(op, pb[sk >> 1][sk & 1], acc[dt]);
-      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, j / 3);
+      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / 2);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NJ + 1) / 3; i < kRowHalf; ++i) row_op(itr, bufc, i);
+    for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, bufc, i);
   };
 
   auto body_ds = [&](int it, auto bufc) {
@@ -325,33 +336,33 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
 
     constexpr int NS = 2 * KS;  // dO V^T MFMAs: (sub, ks)
     auto dop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.dout + (j / KS) * 32 * D + ro[j % KS]); };
-    bf16x8 da[4];
+    bf16x8 da[kRA];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) da[j] = dop(j);
+    for (int j = 0; j < kRA; ++j) da[j] = dop(j);
     // dP starts at ndelta of its row (registers 8*k2 + e: row 32*sub + 16*k2
-    // + 8*hh + e), so the MFMAs deliver dP + ndelta directly.
+    // + 8*hh + e), so the MFMAs deliver dP + ndelta directly.  Sub 0's values
+    // are read now, sub 1's in the first slots (its MFMAs start at slot KS).
     f32x16 dp[2];
+    auto nd_read = [&](int sub, int q4) {
+      const int k2 = q4 >> 1, hf = q4 & 1;
+      const f32x4 n4 = *reinterpret_cast<const f32x4*>(rsg.ndl + 32 * sub + 16 * k2 + 8 * hh + 4 * hf);
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
+      for (int r = 0; r < 4; ++r) dp[sub][8 * k2 + 4 * hf + r] = n4[r];
+    };
 #pragma unroll
-      for (int k2 = 0; k2 < 2; ++k2)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const f32x4 n4 = *reinterpret_cast<const f32x4*>(rsg.ndl + 32 * sub + 16 * k2 + 8 * hh + 4 * hf);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dp[sub][8 * k2 + 4 * hf + r] = n4[r];
-        }
+    for (int q4 = 0; q4 < 4; ++q4) nd_read(0, q4);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       const int sub = j / KS, ks = j % KS;
-      dp[sub] = mfma32(da[j & 3], kv[ks], dp[sub]);
-      if (j + 4 < NS) da[j & 3] = dop(j + 4);
-      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), j / 3);
+      dp[sub] = mfma32(da[j % kRA], kv[ks], dp[sub]);
+      if (j + kRA < NS) da[j % kRA] = dop(j + kRA);
+      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / 2);
+      if (j < 4) nd_read(1, j);  // KS >= 4: before sub 1's first MFMA
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NS + 1) / 3; i < kColHalf; ++i) col_op(itc, NextBuf(), i);
+    for (int i = loads_in_loop(NS); i < kColHalf; ++i) col_op(itc, NextBuf(), i);
     wait_vmem_n<kInFlight>();
     barrier_lds();  // X: partner's P available, columns visible
     __builtin_amdgcn_s_setprio(2);
@@ -367,9 +378,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int g = j / DT, dt = j % DT;
       return *reinterpret_cast<const bf16x8*>(csg.qt + dt * 32 * BQ + to[g]);
     };
-    bf16x8 opq[4];
+    bf16x8 opq[kRA];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) opq[j] = qt_op(j);
+    for (int j = 0; j < kRA; ++j) opq[j] = qt_op(j);
     __builtin_amdgcn_sched_barrier(0);
     u32x4 ud[4];
     auto dstep = [&](int g, int e2) {
@@ -383,18 +394,18 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int g = j / DT, dt = j % DT;
-      const bf16x8 op = opq[j % 4];
-      if (j + 4 < NJ) opq[j % 4] = qt_op(j + 4);
+      const bf16x8 op = opq[j % kRA];
+      if (j + kRA < NJ) opq[j % kRA] = qt_op(j + kRA);
       acc[dt] = mfma32(op, bits_to_bf16x8(ud[g]), acc[dt]);
       if (g + 1 < 4) {
         // the next group's 4 steps, spread over this group's DT MFMAs
         for (int st = dt * 4 / DT; st < (dt + 1) * 4 / DT; ++st) dstep(g + 1, st);
       }
-      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, j / 3);
+      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / 2);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = (NJ + 1) / 3; i < kRowHalf; ++i) row_op(itr, bufc, i);
+    for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, bufc, i);
   };
 
   retire_prologue_loads();
