@@ -172,6 +172,30 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   // <= 2^8 (exact in fp32/bf16 range) and the O rescale is rare after the
   // first tiles.  The result is the same softmax; only roundings differ.
   const float tau = 8.f / c;
+  // Score bound (bf16 path): |s| <= |q_row| * max_k |k| (Cauchy-Schwarz; the
+  // fp32 accumulation error is far below the 1/1024 margin).  Once
+  // (bound - m_run) * c <= kBoundTau for every row of the wave, no later
+  // score can make a probability exceed 2^kBoundTau (far inside fp32/bf16
+  // range, and O, l stay finite), so the wave stops tracking row maxima:
+  // m_run is then final and the per-tile max and rescale test are skipped.
+  constexpr float kBoundTau = 32.f;
+  float bound = kPosInf;
+  if constexpr (!FP8) {
+    if (a.kmax2 != nullptr) {
+      float qn2 = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = (float)qf[ks][e];
+          qn2 = fmaf(x, x, qn2);
+        }
+      qn2 = halves_sum(qn2);
+      const float km2 = __uint_as_float(a.kmax2[bhk]);
+      bound = sqrtf(qn2) * sqrtf(km2) * (1.f + 1.f / 1024.f);
+    }
+  }
+  int bounded = 0;  // wave-uniform
   float m_run = kNegInf;             // reference max of raw scores for this lane's query
   float l_run0 = 0.f, l_run1 = 0.f;  // this lane's share of the row sum
   f32x16 acc[DT];
@@ -226,20 +250,23 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
           for (int r = 0; r < 4; ++r) s_cur[4 * g + r] += bb[r];
         }
       }
-      float mx = kNegInf;
+      if (!bounded) {
+        float mx = kNegInf;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[r]);
-      mx = halves_max(mx);
-      if (mx > m_run + tau) {
-        // New reference max (both lanes of a query agree: mx is shared).
-        const float alpha = __builtin_amdgcn_exp2f((m_run - mx) * c);
-        l_run0 *= alpha;
-        l_run1 *= alpha;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[r]);
+        mx = halves_max(mx);
+        if (mx > m_run + tau) {
+          // New reference max (both lanes of a query agree: mx is shared).
+          const float alpha = __builtin_amdgcn_exp2f((m_run - mx) * c);
+          l_run0 *= alpha;
+          l_run1 *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+          for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-        m_run = mx;
+            for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+          m_run = mx;
+        }
+        if constexpr (!FP8) bounded = __all((bound - m_run) * c <= kBoundTau);
       }
       const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
 #pragma unroll
@@ -441,10 +468,10 @@ static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   const bool fp8 = a.k8 != nullptr;
   {
     LaunchTimer timer(kKidTranspose, stream);
-    hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
+    hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream, a.kmax2, a.B * a.Hkv);
     if (e == hipSuccess)
       e = fp8 ? launch_quantize_rows(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.k_scale, a.k8, stream)
-              : launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream);
+              : launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream, a.kmax2);
     if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, nullptr, a.vt, stream);
     if (e != hipSuccess) return e;
   }

@@ -42,10 +42,10 @@ size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 size_t kbias_bytes(int32_t B, size_t Lkp) { return round256(((size_t)B * Lkp + 64) * sizeof(float)); }
 size_t kfull_bytes(int32_t B, size_t Lkp) { return round256(((size_t)B * (Lkp / 32) + 64) * sizeof(int)); }
 
-// Forward workspace: [k rows | v^T | key bias | key tile flags], each region
-// 256-byte aligned.
+// Forward workspace: [k rows | v^T | key bias | key tile flags | max squared
+// k row norm per (b, kv head)], each region 256-byte aligned.
 struct FwdWorkspace {
-  size_t kr, vt, kbias, kfull, total;
+  size_t kr, vt, kbias, kfull, kmax2, total;
 };
 
 // The fp8 forward has the e4m3 k rows (one byte per element) in place of
@@ -58,7 +58,8 @@ FwdWorkspace fwd_workspace(int32_t B, int32_t Hkv, int32_t Lk, int32_t D, bool f
   w.vt = w.kr + (fp8 ? round256((size_t)B * Hkv * D * Lkp) : kcopy);
   w.kbias = w.vt + kcopy;
   w.kfull = w.kbias + kbias_bytes(B, Lkp);
-  w.total = w.kfull + kfull_bytes(B, Lkp);
+  w.kmax2 = w.kfull + kfull_bytes(B, Lkp);
+  w.total = w.kmax2 + round256((size_t)B * Hkv * sizeof(uint32_t));
   return w;
 }
 
@@ -178,6 +179,7 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
   a.vt = reinterpret_cast<bf16*>(ws + wl.vt);
   a.kbias = reinterpret_cast<float*>(ws + wl.kbias);
   a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
+  a.kmax2 = fp8 ? nullptr : reinterpret_cast<uint32_t*>(ws + wl.kmax2);
   a.Lkp = transpose_padded_len(len_k);
   return launch_status(launch_fwd(a, head_dim, s));
 }

@@ -41,6 +41,10 @@ struct FwdArgs {
   const float* q_scale;
   const float* k_scale;
   uint8_t* k8;
+  // bf16 path: largest squared row norm of k per (b, kv head), float bits
+  // (written by the k copy): bounds every score of a query row by
+  // |q_row| * sqrt(kmax2).
+  uint32_t* kmax2;
 };
 
 struct BwdArgs {
@@ -125,12 +129,14 @@ inline int transpose_padded_len(int L) { return (L + 63) / 64 * 64; }
 // Padded key bias (B, Lkp) floats (0 attended / -inf) and per-32-key-tile
 // "all attended" flags (B, Lkp/32); mask may be null (only the tail is masked).
 hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, float* kbias, int* kfull,
-                           hipStream_t stream);
+                           hipStream_t stream, uint32_t* clear = nullptr, int nclear = 0);
 
 // x (B, H, L, D) strided -> xr (B*H, Lp, D) and/or xt (B*H, D, Lp), contiguous,
 // zero padded to Lp = transpose_padded_len(L); either output may be null.
+// With rowmax2 set (B*H words, zeroed beforehand), also the largest squared
+// row norm of each (b, h) slice as float bits.
 hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
-                              bf16* xr, bf16* xt, hipStream_t stream);
+                              bf16* xr, bf16* xt, hipStream_t stream, uint32_t* rowmax2 = nullptr);
 
 // Per-head e4m3 scales of x (B, H, L, D) strided: scale[h] = max|x[:, h]| / 448
 // (1 for an all-zero head).  `bits` (H words) holds the running maxima; it

@@ -19,11 +19,13 @@
 
 namespace avattn {
 
-// One workgroup copies 64 sequence rows x D channels of one (b, h).
+// One workgroup copies 64 sequence rows x D channels of one (b, h).  With
+// rowmax2 set, it also folds the largest squared row norm of its rows into
+// rowmax2[b*H + h] (float bits, unsigned atomic max; cleared beforehand).
 template <int D>
 __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict__ x, int64_t sb, int64_t sh,
                                                           int64_t sl, int H, int L, int Lp, bf16* __restrict__ xr,
-                                                          bf16* __restrict__ xt) {
+                                                          bf16* __restrict__ xt, uint32_t* __restrict__ rowmax2) {
   constexpr int S = 64;       // sequence rows per workgroup
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   constexpr int LD = D + 2;   // LDS row pitch in bf16 (odd word count: column reads spread over banks)
@@ -37,6 +39,7 @@ __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict
 
   // Load 64 rows (zeros past L) as 16-byte chunks; write the row-major copy
   // and scatter into the pitched tile for the head_dim-major one.
+  float nmax = 0.f;  // largest squared row norm seen by this thread's rows
 #pragma unroll
   for (int i = 0; i < S * CPR / 256; ++i) {
     const int c = tid + i * 256;
@@ -47,6 +50,20 @@ __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict
     uint32_t* dst = reinterpret_cast<uint32_t*>(tile + row * LD + ch * 8);
 #pragma unroll
     for (int w = 0; w < 4; ++w) dst[w] = v[w];
+    if (rowmax2) {
+      // A row's CPR chunks sit in CPR consecutive lanes: sum their squares.
+      float n = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) n = fmaf(bf16_lo(v[w]), bf16_lo(v[w]), fmaf(bf16_hi(v[w]), bf16_hi(v[w]), n));
+#pragma unroll
+      for (int off = 1; off < CPR; off <<= 1) n += __shfl_xor(n, off);
+      nmax = fmaxf(nmax, n);
+    }
+  }
+  if (rowmax2) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) nmax = fmaxf(nmax, __shfl_xor(nmax, off));
+    if ((tid & 63) == 0) atomicMax(rowmax2 + bh, __float_as_uint(nmax));
   }
   if (!xt) return;
   __syncthreads();
@@ -71,11 +88,14 @@ __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict
 
 // Key bias and tile flags: kbias[b*Lkp + j] = 0 if key j < Lk is attended
 // (mask nonzero, or no mask) else -inf, for j < Lkp; kfull[b*(Lkp/32) + t] = 1
-// if all 32 keys of tile t are attended.  One thread per 32-key tile.
+// if all 32 keys of tile t are attended.  One thread per 32-key tile.  The
+// threads also zero the nclear words of `clear` (grid-stride).
 __global__ __launch_bounds__(256) void key_prep_kernel(const uint8_t* __restrict__ mask, int64_t msb, int B, int Lk,
-                                                       int Lkp, float* __restrict__ kbias, int* __restrict__ kfull) {
+                                                       int Lkp, float* __restrict__ kbias, int* __restrict__ kfull,
+                                                       uint32_t* __restrict__ clear, int nclear) {
   const int tiles = Lkp / 32;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t i = t; i < nclear; i += (int64_t)gridDim.x * blockDim.x) clear[i] = 0u;
   if (t >= (int64_t)B * tiles) return;
   const int b = (int)(t / tiles), j0 = (int)(t % tiles) * 32;
   int all = 1;
@@ -88,26 +108,26 @@ __global__ __launch_bounds__(256) void key_prep_kernel(const uint8_t* __restrict
 }
 
 hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, float* kbias, int* kfull,
-                           hipStream_t stream) {
+                           hipStream_t stream, uint32_t* clear, int nclear) {
   const int Lkp = transpose_padded_len(Lk);
   const int64_t n = (int64_t)B * (Lkp / 32);
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(key_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, mask, msb, B, Lk, Lkp,
-                     kbias, kfull);
+                     kbias, kfull, clear, clear ? nclear : 0);
   return hipGetLastError();
 }
 
 hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
-                              bf16* xr, bf16* xt, hipStream_t stream) {
+                              bf16* xr, bf16* xt, hipStream_t stream, uint32_t* rowmax2) {
   const int Lp = transpose_padded_len(L);
   if ((int64_t)B * H == 0 || Lp == 0 || (!xr && !xt)) return hipSuccess;
   const int64_t blocks = (int64_t)(Lp / 64) * B * H;
   if (blocks > 2147483647) return hipErrorInvalidValue;
   const dim3 grid((unsigned)blocks);
   if (D == 128)
-    hipLaunchKernelGGL(prep_copies_kernel<128>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt);
+    hipLaunchKernelGGL(prep_copies_kernel<128>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt, rowmax2);
   else
-    hipLaunchKernelGGL(prep_copies_kernel<64>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt);
+    hipLaunchKernelGGL(prep_copies_kernel<64>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt, rowmax2);
   return hipGetLastError();
 }
 

@@ -93,6 +93,27 @@ def test_forward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
         assert np.all(o[0] == 0)
 
 
+def test_forward_score_bound_paths(amd):
+    """The forward stops tracking row maxima once |q_row| * max|k| certifies
+    that no later score can grow a probability past 2^32; rows whose bound is
+    loose (large-norm queries nearly orthogonal to every key) keep the exact
+    path, and a late dominant key must still move the reference max.  Both
+    regimes in one launch match float64."""
+    B, H, Lq, Lk, D = 1, 2, 300, 700, 128
+    q = _randn((B, H, Lq, D), 80).float()
+    k = _randn((B, H, Lk, D), 81).float()
+    v = _randn((B, H, Lk, D), 82)
+    q[:, :, 40:72] = 0.0
+    q[:, :, 40:72, 0] = 60.0  # huge norm, scores ~ 60 * k[..., 0]: loose bound
+    k[:, :, :, 0] *= 0.05
+    k[:, :, 650] *= 6.0  # a late key that dominates its rows
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), None, None, None, D ** -0.5)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v))
+    assert np.abs(_f64(out) - ro).max() <= OUT_TOL
+    assert np.abs(lse.cpu().numpy() - rl).max() <= LSE_TOL
+
+
 def test_attention_dropin_matches_torch_restatement(amd):
     q, k, v = _randn((1, 4, 256, 128), 10), _randn((1, 4, 384, 128), 11), _randn((1, 4, 384, 128), 12)
     out = amd.attention.attention(q.cuda(), k.cuda(), v.cuda())
