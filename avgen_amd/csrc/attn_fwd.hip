@@ -191,7 +191,13 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
           qn2 = fmaf(x, x, qn2);
         }
       qn2 = halves_sum(qn2);
-      const float km2 = __uint_as_float(a.kmax2[bhk]);
+      // Largest squared k row norm of the head: a wave maximum over its tiles.
+      const int ntk = a.Lkp / 64;
+      const uint32_t* km = a.kmax2 + bhk * ntk;
+      float km2 = 0.f;
+      for (int i = lane; i < ntk; i += 64) km2 = fmaxf(km2, __uint_as_float(km[i]));
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) km2 = fmaxf(km2, __shfl_xor(km2, off));
       bound = sqrtf(qn2) * sqrtf(km2) * (1.f + 1.f / 1024.f);
     }
   }
@@ -468,7 +474,7 @@ static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   const bool fp8 = a.k8 != nullptr;
   {
     LaunchTimer timer(kKidTranspose, stream);
-    hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream, a.kmax2, a.B * a.Hkv);
+    hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
     if (e == hipSuccess)
       e = fp8 ? launch_quantize_rows(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.k_scale, a.k8, stream)
               : launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream, a.kmax2);

@@ -43,7 +43,7 @@ size_t kbias_bytes(int32_t B, size_t Lkp) { return round256(((size_t)B * Lkp + 6
 size_t kfull_bytes(int32_t B, size_t Lkp) { return round256(((size_t)B * (Lkp / 32) + 64) * sizeof(int)); }
 
 // Forward workspace: [k rows | v^T | key bias | key tile flags | max squared
-// k row norm per (b, kv head)], each region 256-byte aligned.
+// k row norm per (b, kv head, 64-key tile)], each region 256-byte aligned.
 struct FwdWorkspace {
   size_t kr, vt, kbias, kfull, kmax2, total;
 };
@@ -59,7 +59,7 @@ FwdWorkspace fwd_workspace(int32_t B, int32_t Hkv, int32_t Lk, int32_t D, bool f
   w.kbias = w.vt + kcopy;
   w.kfull = w.kbias + kbias_bytes(B, Lkp);
   w.kmax2 = w.kfull + kfull_bytes(B, Lkp);
-  w.total = w.kmax2 + round256((size_t)B * Hkv * sizeof(uint32_t));
+  w.total = w.kmax2 + round256((size_t)B * Hkv * (Lkp / 64) * sizeof(uint32_t));
   return w;
 }
 

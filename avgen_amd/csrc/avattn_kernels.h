@@ -41,9 +41,10 @@ struct FwdArgs {
   const float* q_scale;
   const float* k_scale;
   uint8_t* k8;
-  // bf16 path: largest squared row norm of k per (b, kv head), float bits
-  // (written by the k copy): bounds every score of a query row by
-  // |q_row| * sqrt(kmax2).
+  // bf16 path: largest squared row norm of k per 64-key tile, (b, kv head,
+  // tile) at ((b*Hkv + h)*(Lkp/64) + tile), float bits (written by the k
+  // copy): the largest over a head bounds every score of a query row by
+  // |q_row| * sqrt(max).
   uint32_t* kmax2;
 };
 
@@ -129,12 +130,12 @@ inline int transpose_padded_len(int L) { return (L + 63) / 64 * 64; }
 // Padded key bias (B, Lkp) floats (0 attended / -inf) and per-32-key-tile
 // "all attended" flags (B, Lkp/32); mask may be null (only the tail is masked).
 hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, float* kbias, int* kfull,
-                           hipStream_t stream, uint32_t* clear = nullptr, int nclear = 0);
+                           hipStream_t stream);
 
 // x (B, H, L, D) strided -> xr (B*H, Lp, D) and/or xt (B*H, D, Lp), contiguous,
 // zero padded to Lp = transpose_padded_len(L); either output may be null.
-// With rowmax2 set (B*H words, zeroed beforehand), also the largest squared
-// row norm of each (b, h) slice as float bits.
+// With rowmax2 set (B*H*(Lp/64) words), also the largest squared row norm of
+// each 64-row tile of each (b, h) slice, as float bits.
 hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
                               bf16* xr, bf16* xt, hipStream_t stream, uint32_t* rowmax2 = nullptr);
 

@@ -20,8 +20,9 @@
 namespace avattn {
 
 // One workgroup copies 64 sequence rows x D channels of one (b, h).  With
-// rowmax2 set, it also folds the largest squared row norm of its rows into
-// rowmax2[b*H + h] (float bits, unsigned atomic max; cleared beforehand).
+// rowmax2 set, it also writes the largest squared norm of its (valid) rows to
+// rowmax2[(b*H + h)*(Lp/64) + tile] as float bits (one plain store per
+// workgroup; an atomic per wave into one word per head serialised badly).
 template <int D>
 __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict__ x, int64_t sb, int64_t sh,
                                                           int64_t sl, int H, int L, int Lp, bf16* __restrict__ xr,
@@ -61,9 +62,12 @@ __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict
     }
   }
   if (rowmax2) {
+    __shared__ float wmax[4];
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) nmax = fmaxf(nmax, __shfl_xor(nmax, off));
-    if ((tid & 63) == 0) atomicMax(rowmax2 + bh, __float_as_uint(nmax));
+    if ((tid & 63) == 0) wmax[tid >> 6] = nmax;
+    __syncthreads();
+    if (tid == 0) rowmax2[blockIdx.x] = __float_as_uint(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
   }
   if (!xt) return;
   __syncthreads();
@@ -88,14 +92,11 @@ __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict
 
 // Key bias and tile flags: kbias[b*Lkp + j] = 0 if key j < Lk is attended
 // (mask nonzero, or no mask) else -inf, for j < Lkp; kfull[b*(Lkp/32) + t] = 1
-// if all 32 keys of tile t are attended.  One thread per 32-key tile.  The
-// threads also zero the nclear words of `clear` (grid-stride).
+// if all 32 keys of tile t are attended.  One thread per 32-key tile.
 __global__ __launch_bounds__(256) void key_prep_kernel(const uint8_t* __restrict__ mask, int64_t msb, int B, int Lk,
-                                                       int Lkp, float* __restrict__ kbias, int* __restrict__ kfull,
-                                                       uint32_t* __restrict__ clear, int nclear) {
+                                                       int Lkp, float* __restrict__ kbias, int* __restrict__ kfull) {
   const int tiles = Lkp / 32;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (int64_t i = t; i < nclear; i += (int64_t)gridDim.x * blockDim.x) clear[i] = 0u;
   if (t >= (int64_t)B * tiles) return;
   const int b = (int)(t / tiles), j0 = (int)(t % tiles) * 32;
   int all = 1;
@@ -108,12 +109,12 @@ __global__ __launch_bounds__(256) void key_prep_kernel(const uint8_t* __restrict
 }
 
 hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, float* kbias, int* kfull,
-                           hipStream_t stream, uint32_t* clear, int nclear) {
+                           hipStream_t stream) {
   const int Lkp = transpose_padded_len(Lk);
   const int64_t n = (int64_t)B * (Lkp / 32);
   if (n == 0) return hipSuccess;
   hipLaunchKernelGGL(key_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, mask, msb, B, Lk, Lkp,
-                     kbias, kfull, clear, clear ? nclear : 0);
+                     kbias, kfull);
   return hipGetLastError();
 }
 

@@ -85,13 +85,13 @@ def test_workspace_size(lib):
     assert lib.avattn_bwd_workspace_size(1, 1, 1, 1, 1, 64) == 2 * 256 + 7 * 64 * 64 * 2 + _key_regions(1, 64)
     assert lib.avattn_bwd_workspace_size(0, 40, 40, 10, 10, 128) == 0
     # forward: k rows + v^T copies of (B, Hkv, Lk, D), key bias/flags, one
-    # max squared k row norm per (b, kv head)
+    # max squared k row norm per (b, kv head, 64-key tile)
     assert lib.avattn_fwd_workspace_size(2, 8, 18900, 128) == (
-        2 * (2 * 8 * 128 * lp * 2) + _key_regions(2, lp) + _round256(2 * 8 * 4))
+        2 * (2 * 8 * 128 * lp * 2) + _key_regions(2, lp) + _round256(2 * 8 * (lp // 64) * 4))
     assert lib.avattn_fwd_workspace_size(1, 1, 0, 128) == 0
     # fp8 forward: the k copy is e4m3 (one byte per element)
     assert lib.avattn_fwd_fp8_workspace_size(2, 8, 18900, 128) == (
-        2 * 8 * 128 * lp + 2 * 8 * 128 * lp * 2 + _key_regions(2, lp) + _round256(2 * 8 * 4))
+        2 * 8 * 128 * lp + 2 * 8 * 128 * lp * 2 + _key_regions(2, lp) + _round256(2 * 8 * (lp // 64) * 4))
     assert lib.avattn_fwd_fp8_workspace_size(1, 1, 70, 64) == (
         _round256(128 * 64) + 128 * 64 * 2 + _key_regions(1, 128) + 256)
     assert lib.avattn_fwd_fp8_workspace_size(1, 1, 0, 128) == 0
