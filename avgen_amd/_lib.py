@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "avattn_fwd_fp8_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32]),
     "avattn_fp8_absmax_scales": (ctypes.c_int, [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr]),
     "avattn_bwd_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "avattn_bwd_staged_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "avattn_bwd": (
         ctypes.c_int,
         [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
@@ -100,6 +101,7 @@ ERR_ARGUMENT = 9
 # avattn_bwd flags (include/avattn.h).
 BWD_REUSE_QUERY_SIDE = 1
 BWD_DQ_ACCUMULATE_F32 = 2
+BWD_STAGE_DS = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -168,6 +170,7 @@ KERNEL_IDS = {
     "transpose": 7,
     "attn_fwd_fp8": 8,
     "fp8_absmax": 9,
+    "bwd_dq_ds": 10,
 }
 
 

@@ -87,7 +87,8 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 // other's MFMAs to hide behind.  Keys that are masked (or past the end) are
 // not special-cased in the loop: each key's dK/dV column depends only on that
 // key, and those columns are written as zeros (or not at all) at the end.
-template <int D, bool MASK>
+// With STAGE the dS waves also store their dS tiles (BwdArgs::ds).
+template <int D, bool MASK, bool STAGE>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   constexpr int BK = 128, BQ = 64, NW = 8;
   constexpr int KS = D / 16, DT = D / 32;
@@ -119,14 +120,16 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   const int prow = perm23(l32);
 
   const int nkt = (a.Lk + BK - 1) / BK;
-  const int total = nkt * a.B * a.Hkv;
+  const int total = nkt * a.nkv;
   const int bid = xcd_remap(blockIdx.x, total);
   const int kt = bid % nkt;
-  const int bhk = bid / nkt;
+  const int bhk = a.kv0 + bid / nkt;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int group = a.Hq / a.Hkv;
 
   const int key = kt * BK + kw * 32 + l32;
+  bool kvalid = key < a.Lk;
+  if (MASK && kvalid) kvalid = a.mask[b * a.msb + key] != 0;
 
   // This wave's B operand: K (P waves) or V (dS waves) of the lane's key,
   // zeros past the end.
@@ -166,16 +169,22 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   const u32x4 rdot = make_rsrc(a.dot + bq0 * D * a.Lqp, qbytes);
   const u32x4 rl2 = make_rsrc(a.lse2 + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
   const u32x4 rnd = make_rsrc(a.ndelta + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
-  TileStager<BQ, D, NW> rst;  // 64 rows of D channels (row stride D)
-  TileStager<D, BQ, NW> tst;  // D rows of 64 queries (row stride Lqp)
-  rst.init(D, wave, lane);
-  tst.init(a.Lqp, wave, lane);
+  // With STAGE only the P waves load tiles, so the dS waves' vector-memory
+  // counter holds nothing but their dS stores, which no wait depends on (a
+  // load issued behind a store only counts as done once the store has been
+  // written).  Otherwise all eight waves share the loads.
+  constexpr int NWL = STAGE ? 4 : NW;
+  const bool loader = !STAGE || role == 0;
+  TileStager<BQ, D, NWL> rst;  // 64 rows of D channels (row stride D)
+  TileStager<D, BQ, NWL> tst;  // D rows of 64 queries (row stride Lqp)
+  rst.init(D, STAGE ? kw : wave, lane);
+  tst.init(a.Lqp, STAGE ? kw : wave, lane);
 
   // The row half of a tile is kRowHalf loads per wave and the column half
   // kColHalf, issued one at a time so they can be spread between MFMAs (a
   // burst of them at the start of a phase would hold up the wave's
   // instruction stream).
-  constexpr int kRowOps = TileStager<BQ, D, NW>::kPer, kColOps = TileStager<D, BQ, NW>::kPer;
+  constexpr int kRowOps = TileStager<BQ, D, NWL>::kPer, kColOps = TileStager<D, BQ, NWL>::kPer;
   constexpr int kRowHalf = 2 * kRowOps + 2, kColHalf = 2 * kColOps;
   auto tile_rows = [&](int it) {  // first row of tile `it` in the group's copies
     return (uint32_t)(it / nqt) * a.Lqp + (uint32_t)(it % nqt) * BQ;
@@ -210,14 +219,24 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // slot kLoad0 on (the start of a phase is left to its operand and
   // statistics reads); the rest follow the phase's loop.  Load i goes in slot
   // kLoad0 + 2*i.
-  constexpr int kLoad0 = 6;
+  // With STAGE the P waves issue twice as many loads: every slot from 4 on.
+  constexpr int kLoad0 = STAGE ? 4 : 6, kLoadStep = STAGE ? 1 : 2;
   auto load_slot = [](int j, int nslots, int count) {
-    return j >= kLoad0 && (j - kLoad0) % 2 == 0 && (j - kLoad0) / 2 < count && j < nslots;
+    return j >= kLoad0 && (j - kLoad0) % kLoadStep == 0 && (j - kLoad0) / kLoadStep < count && j < nslots;
   };
-  auto loads_in_loop = [](int nslots) { return nslots > kLoad0 ? (nslots - kLoad0 + 1) / 2 : 0; };
+  auto loads_in_loop = [](int nslots) {
+    return nslots > kLoad0 ? (nslots - kLoad0 + kLoadStep - 1) / kLoadStep : 0;
+  };
   // Operand reads in flight ahead of the MFMAs (three measured faster than
   // four or six: fewer LDS requests queued at once).
   constexpr int kRA = 3;
+
+  // dS staging (STAGE): per tile each dS wave stores its 32 keys x 64 rows
+  // of dS as four 16-byte stores per lane (group g = 2*sub + k2: the lane's
+  // key, its 8 consecutive rows), each instruction 1 KB contiguous in unit
+  // `sub`, in the first slot of each group's dK^T MFMAs.
+  const uint32_t ds_keep = kvalid ? 0xffffffffu : 0u;  // dS of masked / past-the-end keys is stored as 0
+  const uint32_t ds_voff = (uint32_t)((kw * 32 + l32) * 32 + 16 * hh);
 
   const float c = a.scale_log2;
 
@@ -278,7 +297,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int sub = j / KS, ks = j % KS;
       s[sub] = mfma32(qa[j % kRA], kv[ks], s[sub]);
       if (j + kRA < NS) qa[j % kRA] = qop(j + kRA);
-      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / 2);
+      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / kLoadStep);
       if (j >= 1 && j <= 8) l2_read(j - 1);
       if (j >= kLo) {
         const int n = NS - kLo;
@@ -316,7 +335,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (j + kRA < NJ) opq[j % kRA] = dot_op(j + kRA);
       const int sk = j / DT, dt = j % DT;
       acc[dt] = mfma32(op, pb[sk >> 1][sk & 1], acc[dt]);
-      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / 2);
+      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / kLoadStep);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
@@ -326,13 +345,27 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   auto body_ds = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
     using NextBuf = std::integral_constant<int, buf ^ 1>;
-    wait_vmem_n<kInFlight>();
+    // With STAGE the dS waves load nothing: the barriers alone order them
+    // after the P waves' counted waits.
+    auto wait_loads = [&]() {
+      if constexpr (!STAGE) wait_vmem_n<kInFlight>();
+    };
+    wait_loads();
     barrier_lds();  // T
     __builtin_amdgcn_s_setprio(0);
     const RowStage& rsg = buf == 0 ? rs0 : rs1;
     const ColStage& csg = buf == 0 ? cs0 : cs1;
     const int itc = min(it + 1, niter - 1);
     const int itr = min(it + 2, niter - 1);
+    // This tile's two dS units (query groups 2*(it % nqt) and +1).
+    u32x4 rds = {0u, 0u, 0u, 0u};
+    uint32_t ds_unit1 = 0;
+    if constexpr (STAGE) {
+      const int64_t bq = (int64_t)(bhk - a.kv0) * group + it / nqt;
+      const int64_t unit = (bq * (2 * nqt) + 2 * (it % nqt)) * nkt + kt;
+      rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, (uint32_t)(nkt + 1) * 8192);
+      ds_unit1 = (uint32_t)nkt * 8192;
+    }
 
     constexpr int NS = 2 * KS;  // dO V^T MFMAs: (sub, ks)
     auto dop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.dout + (j / KS) * 32 * D + ro[j % KS]); };
@@ -357,13 +390,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int sub = j / KS, ks = j % KS;
       dp[sub] = mfma32(da[j % kRA], kv[ks], dp[sub]);
       if (j + kRA < NS) da[j % kRA] = dop(j + kRA);
-      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / 2);
+      if (!STAGE && load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / kLoadStep);
       if (j < 4) nd_read(1, j);  // KS >= 4: before sub 1's first MFMA
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (!STAGE) {
 #pragma unroll
-    for (int i = loads_in_loop(NS); i < kColHalf; ++i) col_op(itc, NextBuf(), i);
-    wait_vmem_n<kInFlight>();
+      for (int i = loads_in_loop(NS); i < kColHalf; ++i) col_op(itc, NextBuf(), i);
+    }
+    wait_loads();
     barrier_lds();  // X: partner's P available, columns visible
     __builtin_amdgcn_s_setprio(2);
 
@@ -388,6 +423,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const float p0 = __uint_as_float(pv[g][e2] << 16), p1 = __uint_as_float(pv[g][e2] & 0xffff0000u);
       ud[g][e2] = pack_bf16x2(p0 * dp[sub][8 * k2 + e], p1 * dp[sub][8 * k2 + e + 1]);
     };
+    // Group g's dS: rows 16*k2 + 8*hh .. +7 of unit `sub`, at ((k2*128 +
+    // key)*16 + 8*hh) bf16 into the unit.
+    auto ds_store = [&](int g) {
+      const int sub = g >> 1, k2 = g & 1;
+      const u32x4 w = {ud[g][0] & ds_keep, ud[g][1] & ds_keep, ud[g][2] & ds_keep, ud[g][3] & ds_keep};
+      store_b128_nt(rds, ds_voff, (sub ? ds_unit1 : 0u) + (uint32_t)k2 * 4096, w);
+    };
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) dstep(0, e2);
     __builtin_amdgcn_sched_barrier(0);
@@ -401,15 +443,20 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
         // the next group's 4 steps, spread over this group's DT MFMAs
         for (int st = dt * 4 / DT; st < (dt + 1) * 4 / DT; ++st) dstep(g + 1, st);
       }
-      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / 2);
+      if constexpr (STAGE) {
+        if (dt == 0) ds_store(g);
+      }
+      if (!STAGE && load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / kLoadStep);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (!STAGE) {
 #pragma unroll
-    for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, bufc, i);
+      for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, bufc, i);
+    }
   };
 
   retire_prologue_loads();
-  {
+  if (loader) {
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
 #pragma unroll
@@ -432,8 +479,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   }
 
   if (key < a.Lk) {
-    bool kvalid = true;
-    if (MASK) kvalid = a.mask[b * a.msb + key] != 0;
     const float sc = role == 0 ? 1.f : a.scale;
     bf16* op = role == 0 ? a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl
                          : a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl;
@@ -794,6 +839,143 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 3'. dQ from staged dS
+// ---------------------------------------------------------------------------
+// dQ^T[d, q] = scale * sum_key K^T[d, key] dS^T[key, q], a plain product
+// (the S and dP recomputation of bwd_dq_kernel is replaced by reading the dS
+// the dK/dV kernel stored).  One workgroup = 256 query rows of one (batch,
+// head) of the pass: wave w owns query group 8*qb + w (32 rows, lane % 32 one
+// row) and all D channels (DT accumulators).  64-key stages through three LDS
+// buffers: K^T (D rows of 64 keys, TileLayout<64>, shared) and each wave's
+// own 4 KB of dS, the stage's keys of its unit copied as stored
+// ([k2][64 keys][16 rows]); the B operand (8 consecutive keys of one row per
+// lane) comes from two transposed reads per 16-key step.  The kernel streams
+// dS from HBM once; K^T comes from L2 (the query groups of one head run on
+// one XCD).
+template <int D>
+__global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
+  constexpr int NW = 8, BK = 64, DT = D / 32;
+  struct Stage {
+    bf16 kt[D * BK];             // K^T: D rows of BK keys, TileLayout<BK>
+    bf16 ds[NW][2 * BK * 16];    // per wave: [k2][BK keys][16 rows]
+  };
+  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2;
+  auto stage_ref = [&](auto bufc) __attribute__((always_inline)) -> Stage& {
+    constexpr int buf = decltype(bufc)::value;
+    return buf == 0 ? st0 : (buf == 1 ? st1 : st2);
+  };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hh = lane >> 5;
+
+  const int group = a.Hq / a.Hkv;
+  const int nqg = a.Lqp / 32;
+  const int nqb = (nqg + NW - 1) / NW;
+  const int total = nqb * a.nkv * group;
+  const int bid = xcd_remap(blockIdx.x, total);
+  const int qb = bid % nqb;
+  const int bq_rel = bid / nqb;             // (b, hq) within the pass
+  const int bq = a.kv0 * group + bq_rel;    // b*Hq + hq
+  const int b = bq / a.Hq, h = bq % a.Hq;
+  const int hk = h / group;
+  const int qg = qb * NW + wave;
+  const int qgl = min(qg, nqg - 1);  // groups past the end re-read the last one and write nothing
+  const int qrow = qg * 32 + l32;
+  const bool qvalid = qrow < a.Lq;
+  const int nkt = (a.Lk + 127) / 128;
+  const int nst = a.Lkp / BK;
+
+  const u32x4 rkt = make_rsrc(a.kt + (int64_t)(b * a.Hkv + hk) * D * a.Lkp, (uint32_t)a.Lkp * D * 2);
+  const u32x4 rds =
+      make_rsrc(reinterpret_cast<const char*>(a.ds) + ((int64_t)bq_rel * nqg + qgl) * nkt * 8192, (uint32_t)nkt * 8192);
+  using KtStager = TileStager<D, BK, NW>;
+  KtStager ktst;
+  ktst.init(a.Lkp, wave, lane);
+  constexpr int kDsOps = 4;  // 4 KB per wave and stage
+  constexpr int kStageLoads = KtStager::kPer + kDsOps;
+  // Stage s = keys [64 s, 64 s + 64): in unit s / 2 (bytes (s/2)*8192 on),
+  // the 2 KB at (64*(s%2))*32 of each k2 half (k2 at 4096 bytes).
+  auto stage_load = [&](int s, auto bufc) __attribute__((always_inline)) {
+    Stage& sg = stage_ref(bufc);
+#pragma unroll
+    for (int i = 0; i < KtStager::kPer; ++i) ktst.stage_one(sg.kt, rkt, (uint32_t)s * BK * 2, i);
+    const uint32_t soff = (uint32_t)(s >> 1) * 8192 + (uint32_t)(s & 1) * 2048;
+#pragma unroll
+    for (int i = 0; i < kDsOps; ++i)
+      dma16_nt(rds, lds_addr(&sg.ds[wave][512 * i]), lane * 16 + (i & 1) * 1024 + (i >> 1) * 4096, soff);
+  };
+  // Transposed B-operand reads: in 16-lane group G (k2 = G % 2, hh = G / 2),
+  // lane i reads rows 16*k2 + 4*(i%4) .. +3 of key 16*ks + 8*hh + i/4 (+4 for
+  // the second read) and receives keys +0..3 (+4..7) of row 16*k2 + i.
+  const int tr_g = lane >> 4, tr_i = lane & 15;
+  const int tr_off = ((tr_g & 1) * BK + 8 * (tr_g >> 1) + (tr_i >> 2)) * 16 + 4 * (tr_i & 3);
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) acc[i] = zero16();
+
+  auto compute = [&](const Stage& sg) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const bf16* src = sg.ds[wave] + tr_off + ks * 16 * 16;
+      const bf16x4 lo = lds_read_tr16(src), hi = lds_read_tr16(src + 4 * 16);
+      const bf16x8 bop = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        acc[dt] = mfma32(row_operand<BK>(sg.kt, 32 * dt + l32, 16 * ks + 8 * hh), bop, acc[dt]);
+    }
+  };
+
+  retire_prologue_loads();
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  stage_load(0, S0());
+  stage_load(min(1, nst - 1), S1());
+  // Iteration s: stage s is waited for, stage s + 2 (clamped: the last stage
+  // is re-loaded, same bytes) goes into the buffer stage s - 1 used.
+  auto body = [&](int s, auto bufc, auto nextc) __attribute__((always_inline)) {
+    wait_vmem_n<kStageLoads>();
+    barrier_lds();
+    stage_load(min(s + 2, nst - 1), nextc);
+    compute(stage_ref(bufc));
+  };
+  for (int s = 0; s < nst; s += 3) {
+    body(s, S0(), S2());
+    if (s + 1 < nst) body(s + 1, S1(), S0());
+    if (s + 2 < nst) body(s + 2, S2(), S1());
+  }
+  wait_vmem();  // the last (re-staged) loads
+
+  if (qvalid && a.dq_acc) {
+    float* op = a.dq_acc + b * a.dqsb + h * a.dqsh + (int64_t)qrow * a.dqsl;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4* p = reinterpret_cast<f32x4*>(op + dt * 32 + 8 * g + 4 * hh);
+        f32x4 w = *p;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) w[r] += acc[dt][4 * g + r] * a.scale;
+        *p = w;
+      }
+  } else if (qvalid) {
+    bf16* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)qrow * a.dqsl;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        u32x2 w;
+        w[0] = pack_bf16x2(acc[dt][4 * g] * a.scale, acc[dt][4 * g + 1] * a.scale);
+        w[1] = pack_bf16x2(acc[dt][4 * g + 2] * a.scale, acc[dt][4 * g + 3] * a.scale);
+        *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
+      }
+  }
+}
+
 // Zero-fill rows of a strided (B, H, L, D) bf16 tensor (gradients of an empty
 // attention).
 __global__ void zero_rows_kernel(bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D) {
@@ -809,7 +991,7 @@ __global__ void zero_rows_kernel(bf16* x, int64_t sb, int64_t sh, int64_t sl, in
 }
 
 template <int D>
-static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
+static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t stream) {
   const bool mask = a.mask != nullptr;
   {
     LaunchTimer timer(kKidTranspose, stream);
@@ -830,16 +1012,38 @@ static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
     LaunchTimer timer(kKidBwdPre, stream);
     hipLaunchKernelGGL(bwd_pre_kernel<D>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, stream, a);
   }
-  {
-    const int nkt = (a.Lk + 127) / 128;
-    const dim3 grid(nkt * a.B * a.Hkv);
-    LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup (8 waves) per CU: LDS-bound occupancy
-    if (mask)
-      hipLaunchKernelGGL((bwd_dkdv_kernel<D, true>), grid, dim3(512), 0, stream, a);
-    else
-      hipLaunchKernelGGL((bwd_dkdv_kernel<D, false>), grid, dim3(512), 0, stream, a);
+  // dK/dV (and, with staged dS, dQ) per pass over (b, kv head) pairs.
+  const int nkv_all = a.B * a.Hkv;
+  const int step = a.ds ? kv_per_pass : nkv_all;
+  const int nkt = (a.Lk + 127) / 128;
+  const int group = a.Hq / a.Hkv;
+  for (int kv0 = 0; kv0 < nkv_all; kv0 += step) {
+    BwdArgs p = a;
+    p.kv0 = kv0;
+    p.nkv = min(step, nkv_all - kv0);
+    {
+      const dim3 grid(nkt * p.nkv);
+      LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup (8 waves) per CU: LDS-bound occupancy
+      if (mask) {
+        if (p.ds)
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true>), grid, dim3(512), 0, stream, p);
+        else
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, false>), grid, dim3(512), 0, stream, p);
+      } else {
+        if (p.ds)
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true>), grid, dim3(512), 0, stream, p);
+        else
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false>), grid, dim3(512), 0, stream, p);
+      }
+    }
+    if (p.ds) {
+      const int nqb = (p.Lqp / 32 + 7) / 8;  // 256 query rows per workgroup
+      const dim3 grid(nqb * p.nkv * group);
+      LaunchTimer timer(kKidBwdDqDs, stream);
+      hipLaunchKernelGGL(bwd_dq_ds_kernel<D>, grid, dim3(512), 0, stream, p);
+    }
   }
-  {
+  if (!a.ds) {
     constexpr int BM = 256;  // 8 waves x 32 query rows
     const int nqt = (a.Lq + BM - 1) / BM;
     const dim3 grid(nqt * a.B * a.Hq);
@@ -849,8 +1053,8 @@ static hipError_t launch_bwd_d(const BwdArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_bwd(const BwdArgs& a, int head_dim, hipStream_t stream) {
-  return head_dim == 128 ? launch_bwd_d<128>(a, stream) : launch_bwd_d<64>(a, stream);
+hipError_t launch_bwd(const BwdArgs& a, int head_dim, int kv_per_pass, hipStream_t stream) {
+  return head_dim == 128 ? launch_bwd_d<128>(a, kv_per_pass, stream) : launch_bwd_d<64>(a, kv_per_pass, stream);
 }
 
 hipError_t launch_zero_rows(bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,

@@ -91,6 +91,9 @@ BwdWorkspace bwd_workspace(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32
   return w;
 }
 
+// The staged dS region starts on a 4 KB boundary after the base workspace.
+size_t staged_ds_offset(const BwdWorkspace& w) { return (w.total + 4095) / 4096 * 4096; }
+
 }  // namespace
 
 extern "C" {
@@ -115,7 +118,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 4; }
+int avattn_abi_version(void) { return 5; }
 
 }  // extern "C"
 
@@ -242,6 +245,17 @@ size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_k
   return bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim).total;
 }
 
+size_t avattn_bwd_staged_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
+                                        int32_t len_k, int32_t head_dim, int32_t kv_pairs_per_pass) {
+  if (batch <= 0 || heads_q <= 0 || heads_kv <= 0 || len_q <= 0 || len_k <= 0 || head_dim <= 0 ||
+      kv_pairs_per_pass <= 0 || heads_q % heads_kv != 0)
+    return 0;
+  const BwdWorkspace wl = bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  const int64_t pairs = (int64_t)batch * heads_kv;
+  const int64_t n = kv_pairs_per_pass < pairs ? kv_pairs_per_pass : pairs;
+  return staged_ds_offset(wl) + (size_t)n * ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k);
+}
+
 int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out, const float* lse,
                const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
                const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
@@ -250,7 +264,8 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
                const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
                size_t workspace_bytes, uint32_t flags, avattn_stream_t stream) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
-  if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32)) return AVATTN_ERR_ARGUMENT;
+  if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32 | AVATTN_BWD_STAGE_DS))
+    return AVATTN_ERR_ARGUMENT;
   const bool dq_f32 = (flags & AVATTN_BWD_DQ_ACCUMULATE_F32) != 0;
   if (st != AVATTN_OK) return st;
   if (!dout_strides || !q_strides || !k_strides || !v_strides || !out_strides || !dq_strides || !dk_strides ||
@@ -327,7 +342,19 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
   a.Lqp = transpose_padded_len(len_q);
   a.Lkp = transpose_padded_len(len_k);
-  return launch_status(launch_bwd(a, head_dim, s));
+  a.kv0 = 0;
+  a.nkv = batch * heads_kv;
+  a.ds = nullptr;
+  int kv_per_pass = 0;
+  if (flags & AVATTN_BWD_STAGE_DS) {
+    const size_t off = staged_ds_offset(wl);
+    const size_t per = ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k);
+    if (workspace_bytes < off + per) return AVATTN_ERR_WORKSPACE;
+    const size_t fit = (workspace_bytes - off) / per;
+    kv_per_pass = (int)(fit < (size_t)a.nkv ? fit : (size_t)a.nkv);
+    a.ds = reinterpret_cast<bf16*>(ws + off);
+  }
+  return launch_status(launch_bwd(a, head_dim, kv_per_pass, s));
 }
 
 int avattn_lse_merge(float* out_acc, float* lse_acc, const void* out_blk, const float* lse_blk, int64_t n_rows,

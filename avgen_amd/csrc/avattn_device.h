@@ -319,6 +319,34 @@ struct TileStager {
   }
 };
 
+// 16 bytes per lane at byte base + voff + soff of a raw buffer, non-temporal
+// (streamed past the caches, so a large write does not evict the reader's
+// cached tiles).  Inline assembly like the loads above: the caller counts
+// these stores in its vmcnt waits.
+__device__ __forceinline__ void store_b128_nt(const u32x4& r, uint32_t voff, uint32_t soff, const u32x4& data) {
+  __asm__ volatile("buffer_store_dwordx4 %0, %1, %2, %3 offen nt" ::"v"(data), "v"(voff), "s"(r), "s"(soff)
+                   : "memory");
+}
+
+// dma16 with a non-temporal load (data read once).
+__device__ __forceinline__ void dma16_nt(const u32x4& r, uint32_t lds, uint32_t voff, uint32_t soff) {
+  __asm__ volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, %3 offen nt lds" ::"s"(lds),
+      "v"(voff), "s"(r), "s"(soff)
+      : "memory", "m0");
+}
+
+// Four bf16 of a transposed LDS read (ds_read_b64_tr_b16): in each group of
+// 16 lanes, lane i supplies the address of 4 consecutive elements, the
+// piece (i % 4) of "row" i / 4 of a 4 x 16 block, and lane j receives
+// element j of rows 0..3 (checked on the GPU).
+__device__ __forceinline__ bf16x4 lds_read_tr16(const bf16* p) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(const_cast<bf16*>(p)));
+}
+
 // Retire every outstanding memory operation of this wave, as an instruction
 // the compiler's wait-count bookkeeping sees: a loop that issues its tile
 // loads as inline assembly calls this first, so no compiler-inserted wait for

@@ -94,7 +94,27 @@ struct BwdArgs {
   // The query-side preparation (q/dout copies, lse2, ndelta) is already in
   // the workspace: skip it.
   bool reuse_q;
+  // Pass over the flattened (b, kv head) pairs kv0 .. kv0 + nkv - 1 (b*Hkv +
+  // hk); the whole problem unless dS is staged in several passes.
+  int kv0, nkv;
+  // Staged dS (null: the dQ kernel recomputes S and dP from q, k, v, dout).
+  // The dK/dV kernel stores dS = P * (dP - delta) in bf16 for every query
+  // head of its pass (masked keys and keys past the end as 0) and the dQ
+  // kernel contracts it with K^T.  Unit (bq, qg, kt), bq = b*Hq + hq -
+  // kv0*group, qg = 32-row query group (Lqp/32 of them), kt = 128-key block
+  // (ceil(Lk/128) of them), is 8 KB at byte ((bq*(Lqp/32) + qg)*nkt + kt) *
+  // 8192, ordered [k2 (2)][128 keys][16 rows]: row 16*k2 + r of key j at
+  // bf16 (k2*128 + j)*16 + r, so a dS wave stores 8 consecutive rows of its
+  // key as 16 bytes (1 KB per instruction) and the dQ kernel reads 8
+  // consecutive keys of a row with two transposed LDS reads.
+  bf16* ds;
 };
+
+// Bytes of staged dS per (b, kv head) pair.
+inline size_t ds_bytes_per_kv(int group, int Lq, int Lk) {
+  const size_t Lqp = (size_t)(Lq + 63) / 64 * 64;
+  return (size_t)group * (Lqp / 32) * (size_t)((Lk + 127) / 128) * 8192;
+}
 
 // Kernel ids of the opt-in launch timer (avattn_timing_* in include/avattn.h).
 enum KernelId : int {
@@ -108,6 +128,7 @@ enum KernelId : int {
   kKidTranspose = 7,
   kKidFwdFp8 = 8,
   kKidAbsmax = 9,
+  kKidBwdDqDs = 10,
 };
 
 // Records HIP events around one launch on `stream` while timing is enabled.
@@ -154,7 +175,9 @@ hipError_t launch_quantize_rows(const bf16* x, int64_t sb, int64_t sh, int64_t s
 hipError_t launch_fwd(const FwdArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_empty(bf16* o, int64_t osb, int64_t osh, int64_t osl, int B, int H, int L, int D, float* lse,
                         hipStream_t stream);
-hipError_t launch_bwd(const BwdArgs& a, int head_dim, hipStream_t stream);
+// Backward.  With a.ds set, the (b, kv head) pairs go in passes of
+// kv_per_pass, each staging its dS in a.ds (ds_bytes_per_kv bytes per pair).
+hipError_t launch_bwd(const BwdArgs& a, int head_dim, int kv_per_pass, hipStream_t stream);
 hipError_t launch_zero_rows(bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
                             hipStream_t stream);
 hipError_t launch_lse_merge(float* out_acc, float* lse_acc, const void* out_blk, const float* lse_blk, int64_t rows,

@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from typing import Optional
 
 import torch
@@ -217,8 +218,46 @@ def _out_or_new(t: Optional[torch.Tensor], like: torch.Tensor, name: str, label:
     return t
 
 
+# Staged dS (the dK/dV kernel stores dS and dQ is one product with k): the
+# device memory it may take, default min(48 GiB, half the free memory);
+# AVGEN_AMD_DS_BUDGET_GB overrides it, 0 turns staging off.
+_DS_BUDGET_CAP = 48 << 30
+
+
+def _ds_budget(device: torch.device) -> int:
+    env = os.environ.get("AVGEN_AMD_DS_BUDGET_GB")
+    if env is not None:
+        return int(float(env) * (1 << 30))
+    free, _ = torch.cuda.mem_get_info(device)
+    return min(_DS_BUDGET_CAP, free // 2)
+
+
+def ds_bytes_per_pair(group, Lq, Lk):
+    """Bytes of staged dS per (batch, kv head) pair: bf16 per (query head of
+    the group, query row padded to 64, key padded to 128)."""
+    return group * ((Lq + 63) // 64 * 64) * ((Lk + 127) // 128 * 128) * 2
+
+
+def bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None):
+    """(bytes, staged) for one backward call: the workspace to allocate and
+    whether dS is staged (``stage_ds`` None: when the staged dS of at least
+    one (batch, kv head) pair fits the budget; True: at least one pair
+    whatever the budget; False: never)."""
+    lib = _lib.load()
+    base = lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D)
+    if stage_ds is False or base == 0:
+        return base, False
+    per = ds_bytes_per_pair(Hq // Hkv, Lq, Lk)
+    pairs = min(B * Hkv, _ds_budget(device) // max(per, 1))
+    if pairs == 0:
+        if not stage_ds:
+            return base, False
+        pairs = 1
+    return lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(pairs)), True
+
+
 def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=None, *,
-              workspace=None, reuse_query_side=False, dq_accumulate=None):
+              workspace=None, reuse_query_side=False, dq_accumulate=None, stage_ds=None):
     """Backward launch; ``dq``/``dk``/``dv`` may be preallocated outputs
     (written in place, e.g. slices of a full-sequence gradient).
 
@@ -227,7 +266,9 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
     needs; ``reuse_query_side`` asserts that it already holds the query-side
     preparation of a previous call with the same dout/q/out/lse/scale;
     ``dq_accumulate`` is an fp32 tensor shaped like q that this chunk's dq is
-    added to (returned in dq's place).
+    added to (returned in dq's place).  ``stage_ds``: see bwd_workspace_plan;
+    with a caller workspace, dS is staged when it is large enough for one
+    (batch, kv head) pair (and ``stage_ds`` is not False).
     """
     name = "avgen_amd.flash_bwd"
     _check_qkv(name, q, k, v)
@@ -261,11 +302,18 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
     if workspace is None:
         if reuse_query_side:
             raise ValueError(f"{name}: reuse_query_side needs the caller's workspace")
-        ws = _workspace(need, q.device)
+        nbytes, staged = bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds)
+        ws = _workspace(nbytes, q.device)
     else:
         if workspace.dtype is not torch.uint8 or workspace.numel() < need or workspace.device != q.device:
             raise ValueError(f"{name}: workspace must be uint8 with at least {need} bytes on {q.device}")
         ws = workspace
+        one = lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, 1)
+        staged = stage_ds is not False and one > 0 and ws.numel() >= one
+        if stage_ds and not staged:
+            raise ValueError(f"{name}: staging dS needs a workspace of at least {one} bytes")
+    if staged:
+        flags |= _lib.BWD_STAGE_DS
     if reuse_query_side:
         flags |= _lib.BWD_REUSE_QUERY_SIDE
     st = lib.avattn_bwd(

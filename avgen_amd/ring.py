@@ -218,7 +218,7 @@ def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, sca
 
     B, Hq, Lq, _ = query.shape
     Hkv = key.shape[1]
-    need = max(_lib.load().avattn_bwd_workspace_size(B, Hq, Hkv, Lq, b - a, D)
+    need = max(ops.bwd_workspace_plan(B, Hq, Hkv, Lq, b - a, D, query.device)[0]
                for a, b in (shard_bounds(L, cp, r) for r in range(cp)))
     ws = ops._workspace(need, query.device)
     for r in range(cp):

@@ -40,8 +40,9 @@ PEAK_HBM_GBS = 8000.0
 # Algorithmic MFMA work each kernel performs under the FLOP convention, in
 # units of 2*B*H*Lq*Lk*D (one Lq x Lk x D product): the forward does QK^T and
 # PV (2); the dK/dV kernel does dP, dV and dK (3; its S recompute is not
-# counted); the dQ kernel does dQ (1; its S and dP recomputes are not counted).
-KERNEL_UNITS = {"attn_fwd": 2, "bwd_dkdv": 3, "bwd_dq": 1}
+# counted); the dQ kernel does dQ (1; its S and dP recomputes are not
+# counted), and so does the dQ-from-staged-dS kernel (1).
+KERNEL_UNITS = {"attn_fwd": 2, "bwd_dkdv": 3, "bwd_dq": 1, "bwd_dq_ds": 1}
 
 CONFIGS = {
     # name: (B, H, Lq_shard, L_total, D, cp, grid(F,H,W), text_slots)
@@ -130,10 +131,12 @@ def flops_per_step(cfg: dict, x: dict) -> tuple[float, float]:
     return 12.0 * H * Lq * valid * D, dense
 
 
-def kernel_flops_per_launch(cfg: dict, x: dict, kernel: str) -> float:
-    """Algorithmic FLOPs of one launch of `kernel` (one KV chunk)."""
-    B, H, Lq, L, D, cp = cfg["B"], cfg["H"], cfg["Lq"], cfg["L"], cfg["D"], cfg["cp"]
-    keys = L // cp if x["mask"] is None else float(x["mask"].sum().item()) / B / cp
+def kernel_flops_per_step(cfg: dict, x: dict, kernel: str) -> float:
+    """Algorithmic FLOPs `kernel` performs in one step (all its launches: one
+    per KV chunk, or one per pass of (batch, kv head) pairs when dS is staged
+    in passes)."""
+    B, H, Lq, L, D = cfg["B"], cfg["H"], cfg["Lq"], cfg["L"], cfg["D"]
+    keys = L if x["mask"] is None else float(x["mask"].sum().item()) / B
     return KERNEL_UNITS[kernel] * 2.0 * B * H * Lq * keys * D
 
 
@@ -238,7 +241,8 @@ def ingest_pmc(fetch_csv: str, write_csv: str, kernel: str, workload: str) -> di
     """
     import csv
 
-    symbol = {"attn_fwd": "attn_fwd_kernel", "bwd_dkdv": "bwd_dkdv_kernel", "bwd_dq": "bwd_dq_kernel"}[kernel]
+    symbol = {"attn_fwd": "attn_fwd_kernel", "bwd_dkdv": "bwd_dkdv_kernel", "bwd_dq": "bwd_dq_kernel",
+              "bwd_dq_ds": "bwd_dq_ds_kernel"}[kernel]
 
     def read(path: str, counter: str) -> tuple[float, float, int]:
         kern, cal = [], []
@@ -407,7 +411,8 @@ def main() -> int:
         pmc_calibration(dev)
         log("[bench] calibration kernel done")
     per_kernel = {}
-    for name in ("attn_fwd", "bwd_dkdv", "bwd_dq", "bwd_preprocess", "lse_merge", "rope_apply", "transpose"):
+    for name in ("attn_fwd", "bwd_dkdv", "bwd_dq", "bwd_dq_ds", "bwd_preprocess", "lse_merge", "rope_apply",
+                 "transpose"):
         ms, n = timing.read(name)
         per_kernel[name] = {"total_ms": ms, "launches": n, "avg_ms": ms / n if n else 0.0}
     timing.close()
@@ -417,9 +422,11 @@ def main() -> int:
     value = flops / (ms_per_step / 1e3) / 1e12
     dominant = max(KERNEL_UNITS, key=lambda k: per_kernel[k]["total_ms"])
     dk = per_kernel[dominant]
-    achieved = kernel_flops_per_launch(cfg, x, dominant) / (dk["avg_ms"] / 1e3) / 1e12
+    # Per-launch work / average launch time, taken as totals over the timed
+    # steps (the same ratio; launches of one kernel may differ in size).
+    achieved = kernel_flops_per_step(cfg, x, dominant) * args.steps / (dk["total_ms"] / 1e3) / 1e12
     kernel_rates = {
-        k: round(kernel_flops_per_launch(cfg, x, k) / (per_kernel[k]["avg_ms"] / 1e3) / 1e12, 1)
+        k: round(kernel_flops_per_step(cfg, x, k) * args.steps / (per_kernel[k]["total_ms"] / 1e3) / 1e12, 1)
         for k in KERNEL_UNITS if per_kernel[k]["launches"]
     }
 

@@ -116,6 +116,19 @@ size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_k
                                  int32_t len_q, int32_t len_k, int32_t head_dim);
 
 /*
+ * Workspace bytes avattn_bwd needs with AVATTN_BWD_STAGE_DS when
+ * kv_pairs_per_pass (batch, kv head) pairs are done per pass: the
+ * avattn_bwd_workspace_size() part, rounded up to 4 KB, plus the staged dS of
+ * that many pairs, 2 bytes per (query head of the pair, query row, key) with
+ * rows padded to 64 and keys to 128 (capped at batch*heads_kv pairs; 0 for
+ * empty or invalid sizes).  No counterpart in the reference (torch's flash
+ * backward keeps dS on chip and sums dQ with atomics).
+ */
+size_t avattn_bwd_staged_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                        int32_t len_q, int32_t len_k, int32_t head_dim,
+                                        int32_t kv_pairs_per_pass);
+
+/*
  * Forward with q k^T on fp8 (OCP e4m3) operands: per-head dequantization
  * scales q_scale[heads_q], k_scale[heads_kv] (device float32, e.g. from
  * avattn_fp8_absmax_scales); q8 = e4m3(q * (1/q_scale[h])) and k8 likewise
@@ -180,9 +193,17 @@ int avattn_fp8_absmax_scales(const void* x, const int64_t* x_strides,
  *       fp32 dq sum over KV chunks of the ring backward
  *       (torch/.../_context_parallel/_attention.py:505-506, 623, 636) without a
  *       separate add per chunk.
+ *   AVATTN_BWD_STAGE_DS           the dK/dV kernel stores dS in the workspace
+ *       and dq is one product of dS with k, instead of a second kernel that
+ *       recomputes the scores and dP (two of its three products).  The
+ *       workspace must hold avattn_bwd_staged_workspace_size() bytes for at
+ *       least one pair per pass; the pairs go in passes of as many as fit.
+ *       Same results to rounding (dq sums dS rounded to bf16, as the
+ *       recomputing kernel does).
  */
 #define AVATTN_BWD_REUSE_QUERY_SIDE  1u
 #define AVATTN_BWD_DQ_ACCUMULATE_F32 2u
+#define AVATTN_BWD_STAGE_DS          4u
 int avattn_bwd(const void* dout, const void* q, const void* k, const void* v,
                const void* out, const float* lse,
                const int64_t* dout_strides, const int64_t* q_strides,

@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 4
+    assert lib.avattn_abi_version() == 5
     for code in range(0, 10):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
@@ -97,6 +97,26 @@ def test_workspace_size(lib):
     assert lib.avattn_fwd_fp8_workspace_size(1, 1, 0, 128) == 0
 
 
+def test_staged_workspace_size(lib):
+    # base workspace rounded up to 4 KB, then 8 KB per (query head, 32-row
+    # group of the 64-padded rows, 128-key block) for each pair of a pass
+    def r4k(x):
+        return (x + 4095) // 4096 * 4096
+
+    base = lib.avattn_bwd_workspace_size(2, 40, 40, 18900, 18900, 128)
+    per = (18944 // 32) * ((18900 + 127) // 128) * 8192
+    assert per == 18944 * 18944 * 2
+    assert lib.avattn_bwd_staged_workspace_size(2, 40, 40, 18900, 18900, 128, 1) == r4k(base) + per
+    assert lib.avattn_bwd_staged_workspace_size(2, 40, 40, 18900, 18900, 128, 8) == r4k(base) + 8 * per
+    assert lib.avattn_bwd_staged_workspace_size(2, 40, 40, 18900, 18900, 128, 1000) == r4k(base) + 80 * per
+    # GQA: every query head of the pair's group (2 here); len_q 10 -> 64 rows, len_k 70 -> one block
+    base = lib.avattn_bwd_workspace_size(1, 4, 2, 10, 70, 64)
+    assert lib.avattn_bwd_staged_workspace_size(1, 4, 2, 10, 70, 64, 2) == r4k(base) + 2 * (2 * 2 * 1 * 8192)
+    assert lib.avattn_bwd_staged_workspace_size(1, 4, 2, 10, 70, 64, 0) == 0
+    assert lib.avattn_bwd_staged_workspace_size(0, 4, 2, 10, 70, 64, 1) == 0
+    assert lib.avattn_bwd_staged_workspace_size(1, 4, 2, 0, 70, 64, 1) == 0
+
+
 def _fwd(lib, **over):
     s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
     args = dict(q=16, k=16, v=16, qs=s, ks=s, vs=s, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
@@ -139,8 +159,16 @@ def test_bwd_validation_paths(lib):
             16, s, 16, s, 16, s, 16, 8, 0, None]
     assert lib.avattn_bwd(*base) == _lib.ERR_WORKSPACE  # 8 bytes < 2*1*2*4*4
     bad = list(base)
-    bad[28] = 4  # unknown flag
+    bad[28] = 8  # unknown flag
     assert lib.avattn_bwd(*bad) == _lib.ERR_ARGUMENT
+    # staged dS needs the base workspace (4 KB aligned) plus one pair's dS
+    bad = list(base)
+    bad[28] = _lib.BWD_STAGE_DS
+    need = lib.avattn_bwd_workspace_size(1, 2, 2, 4, 4, 128)
+    bad[27] = need
+    assert lib.avattn_bwd(*bad) == _lib.ERR_WORKSPACE
+    bad[27] = lib.avattn_bwd_staged_workspace_size(1, 2, 2, 4, 4, 128, 1) - 1
+    assert lib.avattn_bwd(*bad) == _lib.ERR_WORKSPACE
     # fp32 dq accumulator: strides in floats, multiples of 4 (not 8)
     bad = list(base)
     bad[28] = _lib.BWD_DQ_ACCUMULATE_F32

@@ -181,14 +181,18 @@ BWD_CASES = [
 
 
 @pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,masked", BWD_CASES)
-def test_backward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
+@pytest.mark.parametrize("staged", [True, False])
+def test_backward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked, staged):
+    """Both dQ paths: staged dS (dK/dV kernel stores dS, dQ = dS K) and the
+    kernel that recomputes S and dP."""
     q, k, v = _randn((B, Hq, Lq, D), 40), _randn((B, Hkv, Lk, D), 41), _randn((B, Hkv, Lk, D), 42)
     do = _randn((B, Hq, Lq, D), 43)
     m = _key_mask(B, Lk, 6, empty_rows=(1,) if B > 1 else ()) if masked else None
-    print(f"bwd case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked}", flush=True)
+    print(f"bwd case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked} staged={staged}", flush=True)
     mc = None if m is None else m.cuda()
     out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), mc, None, None, D ** -0.5)
-    dq, dk, dv = amd.ops.flash_bwd(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, mc, D ** -0.5)
+    dq, dk, dv = amd.ops._bwd_impl(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, mc, D ** -0.5,
+                                   stage_ds=staged)
     mn = None if m is None else m.numpy()
     ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), mn)
     rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, mn)
@@ -333,10 +337,12 @@ def test_emulated_ring_matches_unchunked(amd, masked, Hkv):
         assert np.abs(_f64(got) - ref).max() <= GRAD_REL_TOL * np.abs(ref).max()
 
 
-def test_bwd_query_side_reuse_and_dq_accumulation(amd):
+@pytest.mark.parametrize("staged", [False, True])
+def test_bwd_query_side_reuse_and_dq_accumulation(amd, staged):
     """avattn_bwd flags: the query-side preparation kept in the workspace gives
     bit-identical dk/dv, and the fp32 dq accumulator equals the sum of the
-    per-chunk dq up to their bf16 rounding (it adds unrounded values)."""
+    per-chunk dq up to their bf16 rounding (it adds unrounded values); with
+    and without staged dS."""
     B, H, Lq, Lc, D = 1, 2, 200, 150, 128
     q, do = _randn((B, H, Lq, D), 70).cuda(), _randn((B, H, Lq, D), 71).cuda()
     ks = [_randn((B, H, Lc, D), 72 + i).cuda() for i in range(2)]
@@ -345,17 +351,44 @@ def test_bwd_query_side_reuse_and_dq_accumulation(amd):
     out, lse = amd.ops.flash_fwd(q, kf, vf, None, None, None, D ** -0.5)
     ref = [amd.ops.flash_bwd(do, q, k, v, out, lse, None, D ** -0.5) for k, v in zip(ks, vs)]
     lib = amd._lib.load()
-    ws = amd.ops._workspace(lib.avattn_bwd_workspace_size(B, H, H, Lq, Lc, D), q.device)
+    size = (lib.avattn_bwd_staged_workspace_size(B, H, H, Lq, Lc, D, B * H) if staged
+            else lib.avattn_bwd_workspace_size(B, H, H, Lq, Lc, D))
+    ws = amd.ops._workspace(size, q.device)
     acc = torch.zeros(q.shape, dtype=torch.float32, device=q.device)
     for i, (k, v) in enumerate(zip(ks, vs)):
         _, dk, dv = amd.ops._bwd_impl(do, q, k, v, out, lse, None, D ** -0.5, workspace=ws,
-                                      reuse_query_side=i > 0, dq_accumulate=acc)
+                                      reuse_query_side=i > 0, dq_accumulate=acc, stage_ds=staged)
         assert torch.equal(dk, ref[i][1]) and torch.equal(dv, ref[i][2])
     summed = ref[0][0].float() + ref[1][0].float()
     assert (acc - summed).abs().max().item() <= 8e-3 * summed.abs().max().item()
     rq, _, _ = R.attention_bwd_f64(_f64(do), _f64(q), _f64(kf), _f64(vf), _f64(out),
                                    lse.cpu().numpy().astype(np.float64))
     assert np.abs(acc.cpu().numpy() - rq).max() <= GRAD_REL_TOL * np.abs(rq).max()
+
+
+def test_staged_ds_in_passes_matches_recompute(amd, monkeypatch):
+    """A dS budget of two (batch, kv head) pairs: the backward runs in three
+    passes; dk/dv are bit-identical to the recomputing path (same dK/dV
+    kernel arithmetic) and dq agrees to rounding; masked keys stay exact."""
+    B, Hq, Hkv, Lq, Lk, D = 2, 6, 3, 200, 333, 128
+    q, k, v = _randn((B, Hq, Lq, D), 80).cuda(), _randn((B, Hkv, Lk, D), 81).cuda(), _randn((B, Hkv, Lk, D), 82).cuda()
+    do = _randn((B, Hq, Lq, D), 83).cuda()
+    m = _key_mask(B, Lk, 7).cuda()
+    per = amd.ops.ds_bytes_per_pair(Hq // Hkv, Lq, Lk)
+    out, lse = amd.ops.flash_fwd(q, k, v, m, None, None, D ** -0.5)
+    ref = amd.ops._bwd_impl(do, q, k, v, out, lse, m, D ** -0.5, stage_ds=False)
+    monkeypatch.setenv("AVGEN_AMD_DS_BUDGET_GB", repr(2.5 * per / (1 << 30)))
+    nbytes, staged = amd.ops.bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, q.device)
+    lib = amd._lib.load()
+    assert staged and nbytes == lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, 2)
+    print(f"staged passes: {per} bytes per pair, workspace {nbytes}", flush=True)
+    got = amd.ops._bwd_impl(do, q, k, v, out, lse, m, D ** -0.5)
+    assert torch.equal(got[1], ref[1]) and torch.equal(got[2], ref[2])
+    err = (got[0].float() - ref[0].float()).abs().max().item()
+    assert err <= 1e-2 * ref[0].float().abs().max().item(), err
+    rq, _, _ = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), _f64(out),
+                                   lse.cpu().numpy().astype(np.float64), m.cpu().numpy())
+    assert np.abs(_f64(got[0]) - rq).max() <= GRAD_REL_TOL * np.abs(rq).max()
 
 
 def test_ring_step_signatures_drop_into_torch_loop(amd):
