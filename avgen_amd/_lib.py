@@ -55,6 +55,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "avattn_fp8_absmax_scales": (ctypes.c_int, [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr]),
     "avattn_bwd_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "avattn_bwd_staged_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "avattn_bwd_dq_staged": (
+        ctypes.c_int,
+        [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, ctypes.c_float, c_ptr, c_i64p, c_ptr, c_size, ctypes.c_uint32,
+         c_ptr],
+    ),
     "avattn_bwd": (
         ctypes.c_int,
         [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
@@ -102,6 +107,7 @@ ERR_ARGUMENT = 9
 BWD_REUSE_QUERY_SIDE = 1
 BWD_DQ_ACCUMULATE_F32 = 2
 BWD_STAGE_DS = 4
+BWD_DEFER_DQ = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -1036,7 +1036,7 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
           hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false>), grid, dim3(512), 0, stream, p);
       }
     }
-    if (p.ds) {
+    if (p.ds && !p.defer_dq) {
       const int nqb = (p.Lqp / 32 + 7) / 8;  // 256 query rows per workgroup
       const dim3 grid(nqb * p.nkv * group);
       LaunchTimer timer(kKidBwdDqDs, stream);
@@ -1055,6 +1055,18 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
 
 hipError_t launch_bwd(const BwdArgs& a, int head_dim, int kv_per_pass, hipStream_t stream) {
   return head_dim == 128 ? launch_bwd_d<128>(a, kv_per_pass, stream) : launch_bwd_d<64>(a, kv_per_pass, stream);
+}
+
+hipError_t launch_bwd_dq_staged(const BwdArgs& a, int head_dim, hipStream_t stream) {
+  const int group = a.Hq / a.Hkv;
+  const int nqb = (a.Lqp / 32 + 7) / 8;
+  const dim3 grid(nqb * a.nkv * group);
+  LaunchTimer timer(kKidBwdDqDs, stream);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(bwd_dq_ds_kernel<128>, grid, dim3(512), 0, stream, a);
+  else
+    hipLaunchKernelGGL(bwd_dq_ds_kernel<64>, grid, dim3(512), 0, stream, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_zero_rows(bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,

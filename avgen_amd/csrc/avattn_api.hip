@@ -264,8 +264,11 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
                const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
                size_t workspace_bytes, uint32_t flags, avattn_stream_t stream) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
-  if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32 | AVATTN_BWD_STAGE_DS))
+  if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32 | AVATTN_BWD_STAGE_DS |
+                AVATTN_BWD_DEFER_DQ))
     return AVATTN_ERR_ARGUMENT;
+  const bool defer = (flags & AVATTN_BWD_DEFER_DQ) != 0;
+  if (defer && !(flags & AVATTN_BWD_STAGE_DS)) return AVATTN_ERR_ARGUMENT;
   const bool dq_f32 = (flags & AVATTN_BWD_DQ_ACCUMULATE_F32) != 0;
   if (st != AVATTN_OK) return st;
   if (!dout_strides || !q_strides || !k_strides || !v_strides || !out_strides || !dq_strides || !dk_strides ||
@@ -275,7 +278,8 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   if ((int64_t)batch * heads_q == 0) return AVATTN_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool have_q = len_q > 0, have_k = len_k > 0;
-  if (have_q && (!dq || !aligned16(dq) || !(dq_f32 ? strides_ok_f32(dq_strides) : strides_ok(dq_strides))))
+  if (have_q && !defer &&
+      (!dq || !aligned16(dq) || !(dq_f32 ? strides_ok_f32(dq_strides) : strides_ok(dq_strides))))
     return !dq ? AVATTN_ERR_NULL_POINTER : AVATTN_ERR_LAYOUT;
   if (have_k && (!dk || !dv)) return AVATTN_ERR_NULL_POINTER;
   if (have_k && (!aligned16(dk) || !aligned16(dv) || !strides_ok(dk_strides) || !strides_ok(dv_strides)))
@@ -283,7 +287,7 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   if (!have_q || !have_k) {
     // Empty attention: every gradient is zero.
     hipError_t e = hipSuccess;
-    if (have_q && !dq_f32)  // an fp32 accumulator gets nothing added
+    if (have_q && !dq_f32 && !defer)  // an fp32 accumulator gets nothing added; a deferred dq is zeroed later
       e = launch_zero_rows(static_cast<bf16*>(dq), dq_strides[0], dq_strides[1], dq_strides[2], batch, heads_q, len_q,
                            head_dim, s);
     if (e == hipSuccess && have_k)
@@ -345,16 +349,57 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   a.kv0 = 0;
   a.nkv = batch * heads_kv;
   a.ds = nullptr;
+  a.defer_dq = defer;
   int kv_per_pass = 0;
   if (flags & AVATTN_BWD_STAGE_DS) {
     const size_t off = staged_ds_offset(wl);
     const size_t per = ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k);
-    if (workspace_bytes < off + per) return AVATTN_ERR_WORKSPACE;
+    // A deferred dq needs every pair's dS at once.
+    const size_t need = off + (defer ? (size_t)a.nkv * per : per);
+    if (workspace_bytes < need) return AVATTN_ERR_WORKSPACE;
     const size_t fit = (workspace_bytes - off) / per;
     kv_per_pass = (int)(fit < (size_t)a.nkv ? fit : (size_t)a.nkv);
     a.ds = reinterpret_cast<bf16*>(ws + off);
   }
   return launch_status(launch_bwd(a, head_dim, kv_per_pass, s));
+}
+
+int avattn_bwd_dq_staged(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
+                         int32_t head_dim, float scale, void* dq, const int64_t* dq_strides, void* workspace,
+                         size_t workspace_bytes, uint32_t flags, avattn_stream_t stream) {
+  int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  if (flags & ~AVATTN_BWD_DQ_ACCUMULATE_F32) return AVATTN_ERR_ARGUMENT;
+  const bool dq_f32 = (flags & AVATTN_BWD_DQ_ACCUMULATE_F32) != 0;
+  if (!(scale > 0.f) || !isfinite(scale)) return AVATTN_ERR_ARGUMENT;
+  if ((int64_t)batch * heads_q == 0 || len_q == 0) return AVATTN_OK;
+  if (!dq || !dq_strides) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(dq) || !(dq_f32 ? strides_ok_f32(dq_strides) : strides_ok(dq_strides))) return AVATTN_ERR_LAYOUT;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (len_k == 0) {
+    if (dq_f32) return AVATTN_OK;
+    return launch_status(launch_zero_rows(static_cast<bf16*>(dq), dq_strides[0], dq_strides[1], dq_strides[2], batch,
+                                          heads_q, len_q, head_dim, s));
+  }
+  const BwdWorkspace wl = bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  const size_t off = staged_ds_offset(wl);
+  const size_t all = (size_t)batch * heads_kv * ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k);
+  if (!workspace || !aligned16(workspace) || workspace_bytes < off + all) return AVATTN_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  BwdArgs a{};
+  a.B = batch; a.Hq = heads_q; a.Hkv = heads_kv; a.Lq = len_q; a.Lk = len_k;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.dq = dq_f32 ? nullptr : static_cast<bf16*>(dq);
+  a.dq_acc = dq_f32 ? static_cast<float*>(dq) : nullptr;
+  a.dqsb = dq_strides[0]; a.dqsh = dq_strides[1]; a.dqsl = dq_strides[2];
+  a.kt = reinterpret_cast<bf16*>(ws + wl.kt);
+  a.Lqp = transpose_padded_len(len_q);
+  a.Lkp = transpose_padded_len(len_k);
+  a.kv0 = 0;
+  a.nkv = batch * heads_kv;
+  a.ds = reinterpret_cast<bf16*>(ws + off);
+  return launch_status(launch_bwd_dq_staged(a, head_dim, s));
 }
 
 int avattn_lse_merge(float* out_acc, float* lse_acc, const void* out_blk, const float* lse_blk, int64_t n_rows,

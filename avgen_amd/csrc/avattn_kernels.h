@@ -108,6 +108,9 @@ struct BwdArgs {
   // key as 16 bytes (1 KB per instruction) and the dQ kernel reads 8
   // consecutive keys of a row with two transposed LDS reads.
   bf16* ds;
+  // With ds: leave dq to launch_bwd_dq_staged (a later call on the same
+  // workspace, possibly on another stream).
+  bool defer_dq;
 };
 
 // Bytes of staged dS per (b, kv head) pair.
@@ -178,6 +181,9 @@ hipError_t launch_empty(bf16* o, int64_t osb, int64_t osh, int64_t osl, int B, i
 // Backward.  With a.ds set, the (b, kv head) pairs go in passes of
 // kv_per_pass, each staging its dS in a.ds (ds_bytes_per_kv bytes per pair).
 hipError_t launch_bwd(const BwdArgs& a, int head_dim, int kv_per_pass, hipStream_t stream);
+// dQ from the dS and K^T copy a deferred launch_bwd left in the workspace
+// (every (b, kv head) pair in one pass).
+hipError_t launch_bwd_dq_staged(const BwdArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_zero_rows(bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
                             hipStream_t stream);
 hipError_t launch_lse_merge(float* out_acc, float* lse_acc, const void* out_blk, const float* lse_blk, int64_t rows,

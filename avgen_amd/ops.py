@@ -219,9 +219,9 @@ def _out_or_new(t: Optional[torch.Tensor], like: torch.Tensor, name: str, label:
 
 
 # Staged dS (the dK/dV kernel stores dS and dQ is one product with k): the
-# device memory it may take, default min(48 GiB, half the free memory);
+# device memory it may take, default min(96 GiB, half the free memory);
 # AVGEN_AMD_DS_BUDGET_GB overrides it, 0 turns staging off.
-_DS_BUDGET_CAP = 48 << 30
+_DS_BUDGET_CAP = 96 << 30
 
 
 def _ds_budget(device: torch.device) -> int:
@@ -257,7 +257,7 @@ def bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None):
 
 
 def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=None, *,
-              workspace=None, reuse_query_side=False, dq_accumulate=None, stage_ds=None):
+              workspace=None, reuse_query_side=False, dq_accumulate=None, stage_ds=None, defer_dq=False):
     """Backward launch; ``dq``/``dk``/``dv`` may be preallocated outputs
     (written in place, e.g. slices of a full-sequence gradient).
 
@@ -268,7 +268,9 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
     ``dq_accumulate`` is an fp32 tensor shaped like q that this chunk's dq is
     added to (returned in dq's place).  ``stage_ds``: see bwd_workspace_plan;
     with a caller workspace, dS is staged when it is large enough for one
-    (batch, kv head) pair (and ``stage_ds`` is not False).
+    (batch, kv head) pair (and ``stage_ds`` is not False).  ``defer_dq``: stage
+    every pair's dS in the caller's workspace and compute dk/dv only (dq is
+    returned as None); _bwd_dq_staged_impl on that workspace computes dq.
     """
     name = "avgen_amd.flash_bwd"
     _check_qkv(name, q, k, v)
@@ -285,7 +287,12 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
     lse = lse.contiguous()
     mask, msb = _normalise_mask(name, key_mask, B, Lk)
     flags = 0
-    if dq_accumulate is not None:
+    if defer_dq:
+        if workspace is None or stage_ds is False:
+            raise ValueError(f"{name}: a deferred dq needs staged dS in the caller's workspace")
+        flags |= _lib.BWD_DEFER_DQ
+        dq = None
+    elif dq_accumulate is not None:
         if dq_accumulate.shape != q.shape or dq_accumulate.dtype is not torch.float32:
             raise ValueError(f"{name}: dq accumulator must be float32 {tuple(q.shape)}")
         if dq_accumulate.stride(-1) != 1 or dq_accumulate.data_ptr() % 16 or any(
@@ -322,13 +329,35 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
         B, Hq, Hkv, Lq, Lk, D,
         _ptr(mask), msb,
         float(scale),
-        _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
+        _ptr(dq), _strides3(dq if dq is not None else q), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
         _ptr(ws), ws.numel(),
         flags,
         _stream(q.device),
     )
     _lib.check(st, name)
     return dq, dk, dv
+
+
+def _bwd_dq_staged_impl(q, Hkv, Lk, scale, workspace, dq=None, dq_accumulate=None):
+    """dq of a backward run with ``defer_dq`` on ``workspace`` (same q shape,
+    kv heads and key length), on the current stream: written to ``dq`` (new
+    if None) or added in fp32 to ``dq_accumulate`` (returned)."""
+    name = "avgen_amd.flash_bwd"
+    B, Hq, Lq, D = q.shape
+    flags = 0
+    if dq_accumulate is not None:
+        if dq_accumulate.shape != q.shape or dq_accumulate.dtype is not torch.float32:
+            raise ValueError(f"{name}: dq accumulator must be float32 {tuple(q.shape)}")
+        dq = dq_accumulate
+        flags |= _lib.BWD_DQ_ACCUMULATE_F32
+    else:
+        dq = _out_or_new(dq, q, name, "dq")
+    _require_gpu(name, dq, workspace)
+    st = _lib.load().avattn_bwd_dq_staged(
+        B, Hq, Hkv, Lq, Lk, D, float(scale), _ptr(dq), _strides3(dq), _ptr(workspace), workspace.numel(), flags,
+        _stream(q.device))
+    _lib.check(st, name)
+    return dq
 
 
 def _rope_apply_impl(x, cos, sin, inverse):

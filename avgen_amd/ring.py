@@ -201,13 +201,20 @@ def ring_attention_backward(
     return dq_acc.to(query.dtype), dks, dvs
 
 
-def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, scale):
+def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, scale, overlap=False):
     """The emulated ring's backward.  Each chunk's dk/dv goes straight into its
     slice of the full-sequence gradients (one chunk, one contribution, so no
     accumulation or concatenation is needed); dq accumulates in fp32 as in
     the torch ring (torch/.../_attention.py:505-506, 623, 636), inside the
     kernel; the query-side preparation (copies of q and dout, softmax
-    statistics) is made for the first chunk and reused for the others."""
+    statistics) is made once per workspace and reused for the other chunks.
+
+    With ``overlap`` chunk r's dq (a memory-bound product of the staged dS
+    with k) runs on a side stream while chunk r+1's dk/dv (compute-bound) run
+    on the current one; two workspaces alternate, each reused only once its
+    dq has finished.  Off by default: on one MI355X at the c3 ring shape the
+    concurrent kernels slowed each other (both power- and HBM-limited) and
+    the step took 3% longer than running them in turn."""
     L = key.shape[2]
     D = query.shape[-1]
     scale = ops.default_scale(D) if scale is None else float(scale)
@@ -216,17 +223,42 @@ def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, sca
     dq_acc = torch.zeros(query.shape, dtype=torch.float32, device=query.device)
     from . import _lib
 
+    lib = _lib.load()
     B, Hq, Lq, _ = query.shape
     Hkv = key.shape[1]
-    need = max(ops.bwd_workspace_plan(B, Hq, Hkv, Lq, b - a, D, query.device)[0]
-               for a, b in (shard_bounds(L, cp, r) for r in range(cp)))
-    ws = ops._workspace(need, query.device)
-    for r in range(cp):
-        a, b = shard_bounds(L, cp, r)
-        m = None if key_mask is None else key_mask[:, a:b]
-        ops._bwd_impl(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse, m, scale,
-                      dk=dk[:, :, a:b], dv=dv[:, :, a:b], workspace=ws, reuse_query_side=r > 0,
-                      dq_accumulate=dq_acc)
+    bounds = [shard_bounds(L, cp, r) for r in range(cp)]
+    masks = [None if key_mask is None else key_mask[:, a:b] for a, b in bounds]
+    full = max(lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, b - a, D, B * Hkv) for a, b in bounds)
+    if overlap and not (cp > 1 and full > 0):
+        overlap = False
+    if overlap:
+        dev = query.device
+        ws = [ops._workspace(full, dev) for _ in range(2)]
+        main = torch.cuda.current_stream(dev)
+        side = torch.cuda.Stream(dev)
+        done = [None, None]
+        for r, (a, b) in enumerate(bounds):
+            w = r % 2
+            if done[w] is not None:
+                main.wait_event(done[w])  # chunk r-2's dq has read this workspace
+            ops._bwd_impl(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse, masks[r], scale,
+                          dk=dk[:, :, a:b], dv=dv[:, :, a:b], workspace=ws[w], reuse_query_side=r >= 2,
+                          stage_ds=True, defer_dq=True)
+            ready = torch.cuda.Event()
+            ready.record(main)
+            side.wait_event(ready)
+            with torch.cuda.stream(side):
+                ops._bwd_dq_staged_impl(query, Hkv, b - a, scale, ws[w], dq_accumulate=dq_acc)
+                done[w] = torch.cuda.Event()
+                done[w].record(side)
+        main.wait_stream(side)
+    else:
+        need = max(ops.bwd_workspace_plan(B, Hq, Hkv, Lq, b - a, D, query.device)[0] for a, b in bounds)
+        ws = ops._workspace(need, query.device)
+        for r, (a, b) in enumerate(bounds):
+            ops._bwd_impl(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse, masks[r], scale,
+                          dk=dk[:, :, a:b], dv=dv[:, :, a:b], workspace=ws, reuse_query_side=r > 0,
+                          dq_accumulate=dq_acc)
     return dq_acc.to(query.dtype), dk, dv
 
 

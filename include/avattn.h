@@ -200,10 +200,15 @@ int avattn_fp8_absmax_scales(const void* x, const int64_t* x_strides,
  *       least one pair per pass; the pairs go in passes of as many as fit.
  *       Same results to rounding (dq sums dS rounded to bf16, as the
  *       recomputing kernel does).
+ *   AVATTN_BWD_DEFER_DQ           with AVATTN_BWD_STAGE_DS and a workspace
+ *       holding every pair's dS: compute dk and dv only (dq / dq_strides are
+ *       not used); avattn_bwd_dq_staged on the same workspace then computes
+ *       dq, e.g. on another stream while the next KV chunk's dk/dv run.
  */
 #define AVATTN_BWD_REUSE_QUERY_SIDE  1u
 #define AVATTN_BWD_DQ_ACCUMULATE_F32 2u
 #define AVATTN_BWD_STAGE_DS          4u
+#define AVATTN_BWD_DEFER_DQ          8u
 int avattn_bwd(const void* dout, const void* q, const void* k, const void* v,
                const void* out, const float* lse,
                const int64_t* dout_strides, const int64_t* q_strides,
@@ -219,6 +224,21 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v,
                void* workspace, size_t workspace_bytes,
                uint32_t flags,
                avattn_stream_t stream);
+
+/*
+ * dq of a backward that avattn_bwd ran with AVATTN_BWD_STAGE_DS |
+ * AVATTN_BWD_DEFER_DQ on this workspace and these sizes: dq = scale * dS k
+ * from the staged dS and the copy of k in the workspace (the workspace must
+ * not be reused in between; order this call after that one, e.g. by an
+ * event when it runs on another stream).  flags: 0 (dq bf16, written) or
+ * AVATTN_BWD_DQ_ACCUMULATE_F32 (dq fp32, added to), as for avattn_bwd.  No
+ * counterpart in the reference (its flash backward returns dq with dk/dv).
+ */
+int avattn_bwd_dq_staged(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                         int32_t len_q, int32_t len_k, int32_t head_dim,
+                         float scale, void* dq, const int64_t* dq_strides,
+                         void* workspace, size_t workspace_bytes,
+                         uint32_t flags, avattn_stream_t stream);
 
 /*
  * Online-softmax merge of one chunk's (out_blk, lse_blk) into the running

@@ -169,6 +169,23 @@ def test_bwd_validation_paths(lib):
     assert lib.avattn_bwd(*bad) == _lib.ERR_WORKSPACE
     bad[27] = lib.avattn_bwd_staged_workspace_size(1, 2, 2, 4, 4, 128, 1) - 1
     assert lib.avattn_bwd(*bad) == _lib.ERR_WORKSPACE
+    # a deferred dq needs staging, and every pair's dS at once (2 pairs here)
+    bad[28] = _lib.BWD_DEFER_DQ
+    assert lib.avattn_bwd(*bad) == _lib.ERR_ARGUMENT
+    bad[28] = _lib.BWD_STAGE_DS | _lib.BWD_DEFER_DQ
+    bad[27] = lib.avattn_bwd_staged_workspace_size(1, 2, 2, 4, 4, 128, 1)
+    assert lib.avattn_bwd(*bad) == _lib.ERR_WORKSPACE
+    bad[20] = None  # dq is not used by a deferred backward: still fails on the workspace, not the pointer
+    assert lib.avattn_bwd(*bad) == _lib.ERR_WORKSPACE
+    # avattn_bwd_dq_staged: flags, pointers, workspace
+    dq_s = _lib.i64_array([1 << 17, 1 << 17, 128])
+    full = lib.avattn_bwd_staged_workspace_size(1, 2, 2, 4, 4, 128, 2)
+    assert lib.avattn_bwd_dq_staged(1, 2, 2, 4, 4, 128, 0.125, 16, dq_s, 256, full, 1, None) == _lib.ERR_ARGUMENT
+    assert lib.avattn_bwd_dq_staged(1, 2, 2, 4, 4, 128, 0.125, None, dq_s, 256, full, 0, None) == _lib.ERR_NULL_POINTER
+    assert lib.avattn_bwd_dq_staged(1, 2, 2, 4, 4, 128, 0.125, 16, dq_s, 256, full - 1, 0, None) == _lib.ERR_WORKSPACE
+    assert lib.avattn_bwd_dq_staged(1, 2, 2, 4, 4, 128, 0.0, 16, dq_s, 256, full, 0, None) == _lib.ERR_ARGUMENT
+    assert lib.avattn_bwd_dq_staged(1, 3, 2, 4, 4, 128, 0.125, 16, dq_s, 256, full, 0, None) == _lib.ERR_GQA
+    assert lib.avattn_bwd_dq_staged(1, 2, 2, 0, 4, 128, 0.125, None, dq_s, None, 0, 0, None) == _lib.OK
     # fp32 dq accumulator: strides in floats, multiples of 4 (not 8)
     bad = list(base)
     bad[28] = _lib.BWD_DQ_ACCUMULATE_F32

@@ -391,6 +391,28 @@ def test_staged_ds_in_passes_matches_recompute(amd, monkeypatch):
     assert np.abs(_f64(got[0]) - rq).max() <= GRAD_REL_TOL * np.abs(rq).max()
 
 
+@pytest.mark.parametrize("masked", [False, True])
+def test_ring_backward_overlapped_dq_is_identical(amd, masked):
+    """The ring backward with each chunk's dq on a side stream (two
+    alternating workspaces, deferred dq) gives the same bits as the
+    sequential staged backward."""
+    B, Hq, Hkv, Lq, L, D, cp = 2, 4, 2, 200, 700, 128, 4
+    q = _randn((B, Hq, Lq, D), 90).cuda()
+    k, v = _randn((B, Hkv, L, D), 91).cuda(), _randn((B, Hkv, L, D), 92).cuda()
+    do = _randn((B, Hq, Lq, D), 93).cuda()
+    m = _key_mask(B, L, 8).cuda() if masked else None
+    out, lse = amd.ring.ring_attention(q, k, v, cp=cp, key_mask=m)
+    seq = amd.ring._ring_backward_into(do, q, k, v, out, lse, m, cp, None, overlap=False)
+    ovl = amd.ring._ring_backward_into(do, q, k, v, out, lse, m, cp, None, overlap=True)
+    torch.cuda.synchronize()
+    for a_, b_ in zip(seq, ovl):
+        assert torch.equal(a_, b_)
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), _f64(out),
+                                     lse.cpu().numpy().astype(np.float64), None if m is None else m.cpu().numpy())
+    for got, ref in zip(ovl, (rq, rk, rv)):
+        assert np.abs(_f64(got) - ref).max() <= GRAD_REL_TOL * np.abs(ref).max()
+
+
 def test_ring_step_signatures_drop_into_torch_loop(amd):
     # Call the local-step ops exactly as torch's ring does
     # (torch/.../_attention.py:468-475 and 567-575).
