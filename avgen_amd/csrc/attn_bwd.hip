@@ -853,18 +853,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
 // lane) comes from two transposed reads per 16-key step.  The kernel streams
 // dS from HBM once; K^T comes from L2 (the query groups of one head run on
 // one XCD).
-template <int D>
+template <int D, int BK, int NSTG>
 __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
-  constexpr int NW = 8, BK = 64, DT = D / 32;
+  constexpr int NW = 8, DT = D / 32;
+  static_assert(BK == 32 || BK == 64, "stage of 32 or 64 keys");
   struct Stage {
     bf16 kt[D * BK];             // K^T: D rows of BK keys, TileLayout<BK>
     bf16 ds[NW][2 * BK * 16];    // per wave: [k2][BK keys][16 rows]
   };
-  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2;
-  auto stage_ref = [&](auto bufc) __attribute__((always_inline)) -> Stage& {
-    constexpr int buf = decltype(bufc)::value;
-    return buf == 0 ? st0 : (buf == 1 ? st1 : st2);
-  };
+  __shared__ __attribute__((aligned(16))) Stage st[NSTG];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -894,18 +891,18 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   using KtStager = TileStager<D, BK, NW>;
   KtStager ktst;
   ktst.init(a.Lkp, wave, lane);
-  constexpr int kDsOps = 4;  // 4 KB per wave and stage
+  constexpr int kPerK2 = BK / 32;            // 1 KB loads per k2 half and stage
+  constexpr int kDsOps = 2 * kPerK2;         // this wave's 32 rows x BK keys
   constexpr int kStageLoads = KtStager::kPer + kDsOps;
-  // Stage s = keys [64 s, 64 s + 64): in unit s / 2 (bytes (s/2)*8192 on),
-  // the 2 KB at (64*(s%2))*32 of each k2 half (k2 at 4096 bytes).
-  auto stage_load = [&](int s, auto bufc) __attribute__((always_inline)) {
-    Stage& sg = stage_ref(bufc);
+  // Stage s = keys [BK s, BK s + BK): in unit BK*s/128, the BK*32 bytes at
+  // (BK*s % 128)*32 of each k2 half (k2 at 4096 bytes).
+  auto stage_load = [&](int s, Stage& sg) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < KtStager::kPer; ++i) ktst.stage_one(sg.kt, rkt, (uint32_t)s * BK * 2, i);
-    const uint32_t soff = (uint32_t)(s >> 1) * 8192 + (uint32_t)(s & 1) * 2048;
+    const uint32_t soff = (uint32_t)(s * BK / 128) * 8192 + (uint32_t)((s * BK) % 128) * 32;
 #pragma unroll
     for (int i = 0; i < kDsOps; ++i)
-      dma16_nt(rds, lds_addr(&sg.ds[wave][512 * i]), lane * 16 + (i & 1) * 1024 + (i >> 1) * 4096, soff);
+      dma16_nt(rds, lds_addr(&sg.ds[wave][512 * i]), lane * 16 + (i % kPerK2) * 1024 + (i / kPerK2) * 4096, soff);
   };
   // Transposed B-operand reads: in 16-lane group G (k2 = G % 2, hh = G / 2),
   // lane i reads rows 16*k2 + 4*(i%4) .. +3 of key 16*ks + 8*hh + i/4 (+4 for
@@ -930,23 +927,19 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   };
 
   retire_prologue_loads();
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
-  stage_load(0, S0());
-  stage_load(min(1, nst - 1), S1());
-  // Iteration s: stage s is waited for, stage s + 2 (clamped: the last stage
-  // is re-loaded, same bytes) goes into the buffer stage s - 1 used.
-  auto body = [&](int s, auto bufc, auto nextc) __attribute__((always_inline)) {
-    wait_vmem_n<kStageLoads>();
+#pragma unroll
+  for (int p = 0; p < NSTG - 1; ++p) stage_load(min(p, nst - 1), st[p]);
+  // Iteration s: stage s is waited for (NSTG - 2 later stages may still be
+  // in flight), then stage s + NSTG - 1 (clamped: the last stage is
+  // re-loaded, same bytes) goes into the buffer stage s - 1 used.
+  int cur = 0;
+  for (int s = 0; s < nst; ++s) {
+    wait_vmem_n<(NSTG - 2) * kStageLoads>();
     barrier_lds();
-    stage_load(min(s + 2, nst - 1), nextc);
-    compute(stage_ref(bufc));
-  };
-  for (int s = 0; s < nst; s += 3) {
-    body(s, S0(), S2());
-    if (s + 1 < nst) body(s + 1, S1(), S0());
-    if (s + 2 < nst) body(s + 2, S2(), S1());
+    const int nxt = cur == 0 ? NSTG - 1 : cur - 1;
+    stage_load(min(s + NSTG - 1, nst - 1), st[nxt]);
+    compute(st[cur]);
+    cur = cur == NSTG - 1 ? 0 : cur + 1;
   }
   wait_vmem();  // the last (re-staged) loads
 
@@ -988,6 +981,17 @@ __global__ void zero_rows_kernel(bf16* x, int64_t sb, int64_t sh, int64_t sl, in
     const int b = (int)(row / ((int64_t)L * H));
     *reinterpret_cast<u32x4*>(x + b * sb + h * sh + (int64_t)i * sl + 8 * c) = u32x4{0u, 0u, 0u, 0u};
   }
+}
+
+template <int D>
+static void launch_dq_ds_d(const BwdArgs& a, hipStream_t stream) {
+  const int group = a.Hq / a.Hkv;
+  const int nqb = (a.Lqp / 32 + 7) / 8;  // 256 query rows per workgroup
+  const dim3 grid(nqb * a.nkv * group);
+  LaunchTimer timer(kKidBwdDqDs, stream);
+  // 64-key stages, three buffers: measured faster than 32-key stages with
+  // four or six buffers (4.75 vs 4.9-5.4 ms per c3 chunk).
+  hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3>), grid, dim3(512), 0, stream, a);
 }
 
 template <int D>
@@ -1036,12 +1040,7 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
           hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false>), grid, dim3(512), 0, stream, p);
       }
     }
-    if (p.ds && !p.defer_dq) {
-      const int nqb = (p.Lqp / 32 + 7) / 8;  // 256 query rows per workgroup
-      const dim3 grid(nqb * p.nkv * group);
-      LaunchTimer timer(kKidBwdDqDs, stream);
-      hipLaunchKernelGGL(bwd_dq_ds_kernel<D>, grid, dim3(512), 0, stream, p);
-    }
+    if (p.ds && !p.defer_dq) launch_dq_ds_d<D>(p, stream);
   }
   if (!a.ds) {
     constexpr int BM = 256;  // 8 waves x 32 query rows
@@ -1058,14 +1057,10 @@ hipError_t launch_bwd(const BwdArgs& a, int head_dim, int kv_per_pass, hipStream
 }
 
 hipError_t launch_bwd_dq_staged(const BwdArgs& a, int head_dim, hipStream_t stream) {
-  const int group = a.Hq / a.Hkv;
-  const int nqb = (a.Lqp / 32 + 7) / 8;
-  const dim3 grid(nqb * a.nkv * group);
-  LaunchTimer timer(kKidBwdDqDs, stream);
   if (head_dim == 128)
-    hipLaunchKernelGGL(bwd_dq_ds_kernel<128>, grid, dim3(512), 0, stream, a);
+    launch_dq_ds_d<128>(a, stream);
   else
-    hipLaunchKernelGGL(bwd_dq_ds_kernel<64>, grid, dim3(512), 0, stream, a);
+    launch_dq_ds_d<64>(a, stream);
   return hipGetLastError();
 }
 

@@ -218,6 +218,23 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
+def dq_ds_roofline(cfg: dict, timing: dict, steps: int, workload: str):
+    """HBM roofline of the dQ-from-staged-dS kernel (memory-bound): its
+    algorithmic bytes per step — each staged dS byte read once (2 bytes per
+    query row padded to 64 x key padded to 128, per chunk), the fp32 dq
+    accumulator read and written, k^T read — over its total time."""
+    if not timing["launches"]:
+        return None
+    B, H, Lq, L, D, cp = cfg["B"], cfg["H"], cfg["Lq"], cfg["L"], cfg["D"], cfg["cp"]
+    lc = L // cp
+    lqp = (Lq + 63) // 64 * 64
+    per_chunk = B * H * lqp * ((lc + 127) // 128 * 128) * 2 + 2 * B * H * Lq * D * 4 + B * H * lc * D * 2
+    achieved = per_chunk * cp * steps / (timing["total_ms"] / 1e3) / 1e9
+    return {"kernel": "bwd_dq_ds", "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": load_traffic("bwd_dq_ds", workload)}
+
+
 CALIBRATION_BYTES = 1 << 30  # float32 elements read and written by torch.neg
 
 
@@ -469,6 +486,7 @@ def main() -> int:
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": load_traffic(dominant, args.config),
         },
+        "roofline_hbm": dq_ds_roofline(cfg, per_kernel["bwd_dq_ds"], args.steps, args.config),
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
