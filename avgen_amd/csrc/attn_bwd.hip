@@ -236,7 +236,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // key, its 8 consecutive rows), each instruction 1 KB contiguous in unit
   // `sub`, in the first slot of each group's dK^T MFMAs.
   const uint32_t ds_keep = kvalid ? 0xffffffffu : 0u;  // dS of masked / past-the-end keys is stored as 0
-  const uint32_t ds_voff = (uint32_t)((kw * 32 + l32) * 32 + 16 * hh);
+  const uint32_t ds_voff = DsUnit::store_offset(kw * 32 + l32, lane, 0, 0, 0);
 
   const float c = a.scale_log2;
 
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     auto ds_store = [&](int g) {
       const int sub = g >> 1, k2 = g & 1;
       const u32x4 w = {ud[g][0] & ds_keep, ud[g][1] & ds_keep, ud[g][2] & ds_keep, ud[g][3] & ds_keep};
-      store_b128_nt(rds, ds_voff, (sub ? ds_unit1 : 0u) + (uint32_t)k2 * 4096, w);
+      store_b128_nt(rds, ds_voff, (sub ? ds_unit1 : 0u) + (uint32_t)k2 * 4096, w);  // = DsUnit::store_offset
     };
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) dstep(0, e2);
@@ -899,16 +899,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   auto stage_load = [&](int s, Stage& sg) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < KtStager::kPer; ++i) ktst.stage_one(sg.kt, rkt, (uint32_t)s * BK * 2, i);
-    const uint32_t soff = (uint32_t)(s * BK / 128) * 8192 + (uint32_t)((s * BK) % 128) * 32;
+    const uint32_t soff = DsUnit::stage_src<BK>(s, 0, 0);
 #pragma unroll
     for (int i = 0; i < kDsOps; ++i)
-      dma16_nt(rds, lds_addr(&sg.ds[wave][512 * i]), lane * 16 + (i % kPerK2) * 1024 + (i / kPerK2) * 4096, soff);
+      dma16_nt(rds, lds_addr(&sg.ds[wave][512 * i]), DsUnit::stage_src<BK>(0, i, lane), soff);
   };
   // Transposed B-operand reads: in 16-lane group G (k2 = G % 2, hh = G / 2),
   // lane i reads rows 16*k2 + 4*(i%4) .. +3 of key 16*ks + 8*hh + i/4 (+4 for
   // the second read) and receives keys +0..3 (+4..7) of row 16*k2 + i.
-  const int tr_g = lane >> 4, tr_i = lane & 15;
-  const int tr_off = ((tr_g & 1) * BK + 8 * (tr_g >> 1) + (tr_i >> 2)) * 16 + 4 * (tr_i & 3);
+  const int tr_off = DsUnit::tr_elem<BK>(lane, 0, 0);
 
   f32x16 acc[DT];
 #pragma unroll

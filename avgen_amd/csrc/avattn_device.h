@@ -219,6 +219,43 @@ __device__ __forceinline__ bf16x8 row_operand(const bf16* tile, int row, int col
 }
 
 // ---------------------------------------------------------------------------
+// Staged dS units (backward with the dS stored to HBM)
+// ---------------------------------------------------------------------------
+// A unit is the bf16 dS of 32 query rows x 128 keys, 8 KB ordered
+// [k2 (2)][128 keys][16 rows]: row 16*k2 + r of key j at element
+// (k2*128 + j)*16 + r.  The units of one (query head, 32-row group) follow
+// each other for the 128-key blocks kt = 0, 1, ...; the two units of a
+// 64-row tile are nkt*8192 bytes apart.
+struct DsUnit {
+  // Writer (a dS wave of the dK/dV kernel; its lane owns key j of the block,
+  // j = 32*kw + lane % 32): the 16 bytes of rows 16*k2 + 8*(lane/32) .. +7
+  // of the tile's half `sub` go to this byte offset from the tile's first
+  // unit.
+  static __host__ __device__ __forceinline__ uint32_t store_offset(int j, int lane, int sub, int k2, int nkt) {
+    return (uint32_t)(sub ? nkt * 8192 : 0) + (uint32_t)k2 * 4096 + (uint32_t)j * 32 + 16 * (lane >> 5);
+  }
+  // Reader (the dQ kernel; a wave owns one 32-row group): stage s holds keys
+  // [BK*s, BK*s + BK); its 1 KB load i (of BK/16) brings lane `lane`'s 16
+  // bytes from this byte offset of the group's units to LDS byte 1024*i +
+  // 16*lane, so the stage sits in LDS as [k2][BK keys][16 rows].
+  template <int BK>
+  static __host__ __device__ __forceinline__ uint32_t stage_src(int s, int i, int lane) {
+    constexpr int per_k2 = BK / 32;
+    return (uint32_t)(s * BK / 128) * 8192 + (uint32_t)((s * BK) % 128) * 32 + (uint32_t)lane * 16 +
+           (uint32_t)(i % per_k2) * 1024 + (uint32_t)(i / per_k2) * 4096;
+  }
+  // Element offset (in the wave's [k2][BK][16] stage) that lane `lane`
+  // passes to the transposed read `half` (0, 1) of 16-key step ks: in its
+  // 16-lane group G (k2 = G % 2, key half G / 2) lane i points at rows
+  // 16*k2 + 4*(i%4) .. +3 of key 16*ks + 8*(G/2) + 4*half + i/4.
+  template <int BK>
+  static __host__ __device__ __forceinline__ int tr_elem(int lane, int ks, int half) {
+    const int g = lane >> 4, i = lane & 15;
+    return ((g & 1) * BK + 8 * (g >> 1) + (i >> 2)) * 16 + 4 * (i & 3) + ks * 256 + half * 64;
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Direct global->LDS tile loads (buffer_load_dword{,x4} ... lds).
 // ---------------------------------------------------------------------------
 // Issued through inline assembly on purpose: the kernels order these loads

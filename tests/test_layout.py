@@ -15,7 +15,11 @@ of 32 or 64 sequence positions, head_dim 64 and 128, 8 waves):
   perm23 order) touches 16 distinct 16-byte bank groups of a 64-bank x
   4-byte LDS, i.e. is bank-conflict free;
 * perm23 is an involution that maps 8 consecutive C-layout rows of each
-  16-row k-step to one aligned 8-row chunk.
+  16-row k-step to one aligned 8-row chunk;
+* staged dS (``DsUnit``): the dK/dV kernel's stores cover every element of
+  a unit once and stay in it, and the dQ kernel's stage loads plus
+  transposed reads hand every lane the (row, key) pairs of its B operand,
+  for 64- and 32-key stages.
 """
 
 import shutil
@@ -89,7 +93,70 @@ void check_tile() {
       }
 }
 
+// Staged dS: the dK/dV kernel's 16-byte stores and the dQ kernel's 1 KB
+// stage loads plus transposed reads (ds_read_b64_tr_b16: in each 16-lane
+// group, lane j receives element j % 4 of the 4 elements lane 4*r + j/4
+// points at, r = 0..3, as checked on the GPU) deliver every lane the
+// (row, key) pairs of its MFMA B operand.
+template <int BK>
+void check_ds(int nkt) {
+  // One query group's units for nkt key blocks, written as the dK/dV waves
+  // of sub 0 write them (the sub-1 half goes to the next group's units).
+  const int unit_elems = 4096;
+  std::vector<int> row_of(nkt * unit_elems, -1), key_of(nkt * unit_elems, -1);
+  for (int kt = 0; kt < nkt; ++kt)
+    for (int kw = 0; kw < 4; ++kw)
+      for (int lane = 0; lane < 64; ++lane)
+        for (int sub = 0; sub < 2; ++sub)
+          for (int k2 = 0; k2 < 2; ++k2) {
+            const int j = 32 * kw + (lane & 31);
+            const uint32_t off = DsUnit::store_offset(j, lane, sub, k2, nkt);
+            CHECK(off % 16 == 0 && off + 16 <= (uint32_t)(nkt + 1) * 8192, "store offset %u out of range\n", off);
+            CHECK((int)(off / (nkt * 8192)) == sub && off % (nkt * 8192) < 8192, "store leaves its unit\n");
+            if (sub) continue;
+            for (int e = 0; e < 8; ++e) {
+              const int el = kt * unit_elems + (int)(off / 2) + e;
+              CHECK(row_of[el] < 0, "element %d stored twice\n", el);
+              row_of[el] = 16 * k2 + 8 * (lane >> 5) + e;
+              key_of[el] = 128 * kt + j;
+            }
+          }
+  for (int el = 0; el < nkt * unit_elems; ++el) CHECK(row_of[el] >= 0, "element %d never stored\n", el);
+  constexpr int per_stage = 2 * BK * 16;  // bf16 elements of one wave's stage
+  for (int s = 0; s < nkt * 128 / BK; ++s) {
+    std::vector<int> lrow(per_stage, -1), lkey(per_stage, -1);
+    for (int i = 0; i < BK / 16; ++i)
+      for (int lane = 0; lane < 64; ++lane) {
+        const uint32_t src = DsUnit::stage_src<BK>(s, i, lane);
+        CHECK(src == DsUnit::stage_src<BK>(s, 0, 0) + DsUnit::stage_src<BK>(0, i, lane), "stage offset not separable\n");
+        CHECK(src % 16 == 0 && src + 16 <= (uint32_t)nkt * 8192, "stage source %u out of range\n", src);
+        for (int e = 0; e < 8; ++e) {
+          const int d = (1024 * i + 16 * lane) / 2 + e;
+          CHECK(d < per_stage && lrow[d] < 0, "stage element %d written twice\n", d);
+          lrow[d] = row_of[src / 2 + e];
+          lkey[d] = key_of[src / 2 + e];
+        }
+      }
+    for (int ks = 0; ks < BK / 16; ++ks)
+      for (int half = 0; half < 2; ++half)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int g = lane >> 4, j = lane & 15;
+          for (int r = 0; r < 4; ++r) {
+            const int src_lane = 16 * g + 4 * r + j / 4;
+            const int el = DsUnit::tr_elem<BK>(src_lane, ks, half) + j % 4;
+            CHECK(el >= 0 && el < per_stage, "tr read out of the stage\n");
+            const int want_key = BK * s + 16 * ks + 8 * (lane >> 5) + 4 * half + r;
+            CHECK(lrow[el] == (lane & 31) && lkey[el] == want_key,
+                  "BK %d stage %d ks %d half %d lane %d r %d: row %d key %d, want %d %d\n", BK, s, ks, half, lane,
+                  r, lrow[el], lkey[el], lane & 31, want_key);
+          }
+        }
+  }
+}
+
 int main() {
+  check_ds<64>(3);
+  check_ds<32>(2);
   check_tile<64, 128, 8>();  // forward K tile; dK/dV Q, dO row tiles (d128)
   check_tile<128, 64, 8>();  // forward V^T tile; dK/dV Q^T, dO^T tiles (d128)
   check_tile<32, 128, 8>();  // dQ K, V row tiles (d128)
