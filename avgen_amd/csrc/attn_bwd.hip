@@ -7,13 +7,18 @@
 //      copies (prep.hip);
 //   2. dK/dV: one workgroup per 128 keys (32 per wave, kept in registers as
 //      MFMA operands); loops over 64-row query tiles of every query head
-//      that reads this KV head;
-//   3. dQ: one workgroup per 128 query rows (32 per wave); loops over 32-key
-//      tiles.
-// Every MFMA operand read from LDS is one 16-byte chunk of a tile row: the
-// products contracting over the sequence read head_dim-major tiles of the
-// copies, and the rows feeding the first product are read in perm23 order so
-// that their C layout lines up with those chunks.
+//      that reads this KV head; with staged dS it also stores dS (bf16) to
+//      the workspace;
+//   3. dQ, either
+//      3'. from the staged dS: dQ = scale * dS K, one product, one workgroup
+//          per 256 query rows streaming the dS once (bwd_dq_ds_kernel), or
+//      3''. recomputing S and dP: one workgroup per 256 query rows (32 per
+//          wave), 32-key tiles (bwd_dq_kernel).
+// Every MFMA operand read from LDS is one 16-byte chunk of a tile row (or,
+// for the staged dS, two transposed reads): the products contracting over
+// the sequence read head_dim-major tiles of the copies, and the rows feeding
+// the first product are read in perm23 order so that their C layout lines up
+// with those chunks.
 // With out/lse the merged result over all KV chunks, the outputs are one
 // chunk's contributions, which is how the ring backward calls the op
 // (torch/.../_context_parallel/_attention.py:567-575).
