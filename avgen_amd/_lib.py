@@ -38,6 +38,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr, c_size,
          c_ptr],
     ),
+    "avattn_fwd_windowed": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p, c_ptr,
+         c_ptr, c_size,
+         c_ptr],
+    ),
     "avattn_fwd_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32]),
     "avattn_fwd_fp8": (
         ctypes.c_int,
@@ -66,6 +77,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_i64p, c_i64p, c_i64p, c_i64p, c_i64p,
          c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
          c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
+         c_ptr, c_size,
+         ctypes.c_uint32,
+         c_ptr],
+    ),
+    "avattn_bwd_windowed": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_i64p, c_i64p, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
          c_f32,
          c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
          c_ptr, c_size,

@@ -14,8 +14,16 @@ bf16 tensors on a ROCm GPU, head_dim 64 or 128, ``dropout_p == 0``,
 ``is_causal == False`` (video DiT attention is bidirectional), and masks
 that are key-padding masks — boolean, broadcastable as ``(batch, 1, 1,
 keys)`` — which is what :func:`key_padding_mask` and CrossAttention build
-(src/avgen/models/layers.py:651-657).  Query-dependent dense masks
-(src/avgen/models/blocks.py:54-104) are not supported by this kernel.
+(src/avgen/models/layers.py:651-657).
+
+Query-dependent masks are not taken as dense ``(queries, keys)`` tensors —
+those are what makes the reference run out of memory — but as per-row key
+windows ``[lo, hi)`` that the kernels skip tiles by:
+:func:`temporal_neighbour_attention` for the audio-video fusion mask
+(src/avgen/models/blocks.py:54-104, built at src/avgen/models/dit.py:931-942)
+and :func:`varlen_attention` for packed sequences (the ``cu_seqlens`` of
+src/avgen/data/packing.py:163-200); :func:`windowed_attention` takes the
+windows directly.
 """
 
 from __future__ import annotations
@@ -38,6 +46,11 @@ __all__ = [
     "key_padding_mask",
     "rotary_attention",
     "sdpa_context",
+    "packed_windows",
+    "temporal_neighbour_attention",
+    "temporal_neighbour_windows",
+    "varlen_attention",
+    "windowed_attention",
 ]
 
 #: The single backend this package provides.
@@ -230,3 +243,221 @@ def attention_fp8(
         k_scale = ops.fp8_absmax_scales(key)
     out, _ = ops.flash_fwd_fp8(query, key, value, mask, q_scale, k_scale, ops.default_scale(query.shape[-1]))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Per-row key windows
+# ---------------------------------------------------------------------------
+
+
+def windowed_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    window_lo: torch.Tensor,
+    window_hi: torch.Tensor,
+    *,
+    attn_mask: torch.Tensor | None = None,
+    enable_gqa: bool = False,
+) -> torch.Tensor:
+    """:func:`attention` where query row ``i`` attends only to keys
+    ``window_lo[.., i] <= j < window_hi[.., i]`` (and the key-padding
+    ``attn_mask``).
+
+    ``window_lo``/``window_hi`` are int32 ``(batch, queries)`` or
+    ``(queries,)`` on the query's device, shared by all heads.  A row whose
+    window holds no attended key returns zeros.  The backward requires both
+    bounds to be non-decreasing in the row (true of every window built here)
+    and raises otherwise.
+    """
+    if query.shape[-2] == 0 or key.shape[-2] == 0:
+        return torch.zeros_like(query)
+    _validate(query, key, value, 0.0, False, enable_gqa)
+    mask = _as_key_mask(attn_mask, query.shape[0], query.shape[-2], key.shape[-2])
+    out, _ = ops.flash_fwd_windowed(
+        query, key, value, window_lo, window_hi, mask, ops.default_scale(query.shape[-1])
+    )
+    return out
+
+
+def _leading_count(pred, n: int, shape, device) -> torch.Tensor:
+    """Per row, the number of leading ``j`` in ``0..n-1`` with ``pred(j)`` true,
+    for a predicate that is true then false along ``j`` (binary lifting over
+    the powers of two; ``pred`` takes an int64 index tensor of ``shape``)."""
+    pos = torch.zeros(shape, dtype=torch.int64, device=device)
+    step = 1 << max(n.bit_length() - 1, 0)
+    while step >= 1:
+        cand = pos + step
+        ok = cand <= n
+        idx = torch.where(ok, cand - 1, torch.zeros_like(cand))
+        pos = torch.where(ok & pred(idx), cand, pos)
+        step >>= 1
+    return pos
+
+
+def temporal_neighbour_windows(
+    query_seconds: torch.Tensor, key_seconds: torch.Tensor, *, window_seconds: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Key windows of the temporal neighbour mask (src/avgen/models/blocks.py
+    :97-98): for ``key_seconds`` non-decreasing along each batch row, the
+    keys with ``|tq - tk| <= window_seconds`` form one range ``[lo, hi)``.
+
+    The bounds come from a binary search that evaluates the reference's own
+    predicate (``tq - tk`` in the coordinates' dtype, compared with the
+    Python float), so the windows select exactly the keys the dense mask
+    does, ties and rounding included.  For non-decreasing ``query_seconds``
+    both bounds are non-decreasing in the row.  Returns int32 ``(batch,
+    queries)`` ``(lo, hi)`` on the coordinates' device.
+    """
+    if query_seconds.ndim != 2 or key_seconds.ndim != 2 or query_seconds.shape[0] != key_seconds.shape[0]:
+        raise ValueError(
+            f"query_seconds/key_seconds must be (batch, queries)/(batch, keys); got "
+            f"{tuple(query_seconds.shape)} and {tuple(key_seconds.shape)}"
+        )
+    B, Lq = query_seconds.shape
+    Lk = key_seconds.shape[1]
+    tq = query_seconds
+
+    def delta(j):
+        return tq - torch.gather(key_seconds, 1, j)
+
+    # (tq - tk) decreases along sorted keys: "delta > w" holds on a prefix (the
+    # keys before the window), "-delta <= w" on a prefix too (up to its end).
+    lo = _leading_count(lambda j: ~(delta(j) <= window_seconds), Lk, (B, Lq), tq.device)
+    hi = _leading_count(lambda j: (-delta(j)) <= window_seconds, Lk, (B, Lq), tq.device)
+    hi = torch.maximum(hi, lo)
+    return lo.to(torch.int32), hi.to(torch.int32)
+
+
+def _is_sorted_rows(t: torch.Tensor) -> torch.Tensor:
+    return (t[:, 1:] >= t[:, :-1]).all() if t.shape[1] > 1 else torch.ones((), dtype=torch.bool, device=t.device)
+
+
+def temporal_neighbour_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    query_seconds: torch.Tensor,
+    key_seconds: torch.Tensor,
+    *,
+    window_seconds: float,
+    key_mask: torch.Tensor | None = None,
+    enable_gqa: bool = False,
+) -> torch.Tensor:
+    """``attention(query, key, value, attn_mask=temporal_neighbour_mask(
+    query_seconds, key_seconds, window_seconds=..., key_mask=key_mask))``
+    without the dense ``(batch, 1, queries, keys)`` mask
+    (src/avgen/models/blocks.py:54-104; the fusion call at
+    src/avgen/models/dit.py:931-942).
+
+    Same semantics as the reference composition: a query attends to the valid
+    keys within ``window_seconds`` of it; ``window_seconds <= 0`` is plain
+    key-padding attention; a query with no admissible key attends to every
+    key, masked ones included (:101-103).  Coordinates are ``(batch, tokens)``
+    seconds.  Tokens in non-decreasing time order (how video and audio
+    streams are laid out) go straight to the windowed kernel; otherwise the
+    rows are permuted into time order first (attention is invariant under a
+    permutation of the keys and equivariant under one of the queries).
+    """
+    if query.shape[-2] == 0 or key.shape[-2] == 0:
+        return torch.zeros_like(query)
+    _validate(query, key, value, 0.0, False, enable_gqa)
+    B, Lq, Lk = query.shape[0], query.shape[-2], key.shape[-2]
+    if tuple(query_seconds.shape) != (B, Lq) or tuple(key_seconds.shape) != (B, Lk):
+        raise ValueError(
+            f"query_seconds must be {(B, Lq)} and key_seconds {(B, Lk)}; got "
+            f"{tuple(query_seconds.shape)} and {tuple(key_seconds.shape)}"
+        )
+    if key_mask is not None and tuple(key_mask.shape) != (B, Lk):
+        raise ValueError(f"key_mask must be (batch, keys)={(B, Lk)}; got {tuple(key_mask.shape)}")
+    scale = ops.default_scale(query.shape[-1])
+    if window_seconds <= 0.0:
+        mask = None if key_mask is None else key_mask.to(device=query.device, dtype=torch.bool)
+        return ops.flash_fwd(query, key, value, mask, None, None, scale)[0]
+
+    dev = query.device
+    tq = query_seconds.to(dev)
+    tk = key_seconds.to(dev)
+    km = None if key_mask is None else key_mask.to(device=dev, dtype=torch.bool)
+    sorted_q, sorted_k = (bool(x) for x in torch.stack([_is_sorted_rows(tq), _is_sorted_rows(tk)]).tolist())
+    perm_q = None
+    if not sorted_k:
+        order = torch.sort(tk, dim=1, stable=True).indices
+        tk = torch.gather(tk, 1, order)
+        km = None if km is None else torch.gather(km, 1, order)
+        idx = order[:, None, :, None]
+        key = torch.gather(key, 2, idx.expand(-1, key.shape[1], -1, key.shape[3]))
+        value = torch.gather(value, 2, idx.expand(-1, value.shape[1], -1, value.shape[3]))
+    if not sorted_q:
+        perm_q = torch.sort(tq, dim=1, stable=True).indices
+        tq = torch.gather(tq, 1, perm_q)
+        query = torch.gather(query, 2, perm_q[:, None, :, None].expand(-1, query.shape[1], -1, query.shape[3]))
+
+    lo, hi = temporal_neighbour_windows(tq, tk, window_seconds=window_seconds)
+    out, _ = ops.flash_fwd_windowed(query, key, value, lo, hi, km, scale)
+
+    # Rows with no admissible key: every key, unmasked (the reference's
+    # ``mask | ~mask.any(-1)``).
+    if km is None:
+        fallback = hi == lo
+    else:
+        pre = torch.nn.functional.pad(km.to(torch.int32).cumsum(1), (1, 0))
+        fallback = (torch.gather(pre, 1, hi.long()) - torch.gather(pre, 1, lo.long())) == 0
+    rows = fallback.nonzero()
+    if rows.shape[0] > 0:
+        out = out.clone()
+        for b in rows[:, 0].unique().tolist():
+            r = rows[rows[:, 0] == b, 1]
+            qb = query[b:b + 1].index_select(2, r)
+            ob, _ = ops.flash_fwd(qb, key[b:b + 1], value[b:b + 1], None, None, None, scale)
+            out[b, :, r] = ob[0]
+    if perm_q is not None:
+        inv = torch.argsort(perm_q, dim=1)
+        out = torch.gather(out, 2, inv[:, None, :, None].expand(-1, out.shape[1], -1, out.shape[3]))
+    return out
+
+
+def packed_windows(cu_seqlens: torch.Tensor, length: int, *, device=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Key windows of a packed sequence's block-diagonal mask
+    (src/avgen/data/packing.py:181-200): row ``i`` of segment ``s`` attends
+    keys ``[cu[s], cu[s+1])``; rows past ``cu[-1]`` (padding) get the empty
+    window ``[cu[-1], cu[-1])`` and no window reaches a padding key.  Returns
+    int32 ``(length,)`` ``(lo, hi)``, both non-decreasing."""
+    cu = cu_seqlens.to(device=device if device is not None else cu_seqlens.device, dtype=torch.int64)
+    if cu.ndim != 1 or cu.numel() < 1:
+        raise ValueError(f"cu_seqlens must be a non-empty 1-D tensor; got {tuple(cu_seqlens.shape)}")
+    i = torch.arange(length, device=cu.device)
+    seg = torch.searchsorted(cu[1:].contiguous(), i, right=True)
+    ext = torch.cat([cu, cu[-1:]])
+    return ext[seg].to(torch.int32), ext[seg + 1].to(torch.int32)
+
+
+def varlen_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    *,
+    enable_gqa: bool = False,
+) -> torch.Tensor:
+    """Attention over packed variable-length sequences: what
+    ``attention(q, k, v, attn_mask=layout.attention_mask())`` computes
+    (src/avgen/data/packing.py:181-200), from ``layout.cu_seqlens``
+    (:163-179) instead of the ``(capacity, capacity)`` mask.
+
+    ``query``/``key``/``value`` share the packed length; every batch row uses
+    the same ``cu_seqlens`` (int32 ``(segments + 1,)``, on any device).
+    Tokens attend within their own segment only; padding rows (past
+    ``cu_seqlens[-1]``) attend to nothing and return zeros.
+    """
+    if query.shape[-2] != key.shape[-2]:
+        raise ValueError("varlen_attention: query and key must share the packed length")
+    if query.shape[-2] == 0:
+        return torch.zeros_like(query)
+    if int(cu_seqlens[-1]) > query.shape[-2]:
+        raise ValueError(
+            f"varlen_attention: cu_seqlens ends at {int(cu_seqlens[-1])}, past the packed length "
+            f"{query.shape[-2]}"
+        )
+    lo, hi = packed_windows(cu_seqlens, query.shape[-2], device=query.device)
+    return windowed_attention(query, key, value, lo, hi, enable_gqa=enable_gqa)

@@ -92,9 +92,14 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 // other's MFMAs to hide behind.  Keys that are masked (or past the end) are
 // not special-cased in the loop: each key's dK/dV column depends only on that
 // key, and those columns are written as zeros (or not at all) at the end.
-// With STAGE the dS waves also store their dS tiles (BwdArgs::ds).
-template <int D, bool MASK, bool STAGE>
+// With STAGE the dS waves also store their dS tiles (BwdArgs::ds).  With WIN
+// (key windows non-decreasing in the row, BwdArgs::wlo/whi; staged dS only)
+// the workgroup visits only the 64-row tiles whose rows' window union meets
+// its keys, and the P waves set the scores outside a row's window to -inf
+// in tiles not inside every window (so P and dS are 0 there).
+template <int D, bool MASK, bool STAGE, bool WIN>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
+  static_assert(!WIN || STAGE, "windows with staged dS only");
   constexpr int BK = 128, BQ = 64, NW = 8;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BQ * D;
@@ -107,6 +112,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     bf16 dout[TE];  // dO rows: TileLayout<D>
     float lse2[BQ];
     float ndl[BQ];  // ndelta: the dP accumulators start from it
+    int wlo[WIN ? BQ : 4];  // key windows of the tile's rows (WIN)
+    int whi[WIN ? BQ : 4];
   };
   struct ColStage {
     bf16 qt[TE];   // Q^T: D rows of BQ, TileLayout<BQ>
@@ -164,7 +171,49 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   u32x4* xp = sxp + kw * 4 * 64 + lane;  // + 64*(2*sub + k2)
 
   const int nqt = a.Lqp / BQ;
-  const int niter = nqt * group;
+  // Query tiles visited: tq0 .. tq0 + ntq - 1 of every query head of the
+  // group (all of them without windows).  With monotone windows, tile T
+  // meets this block's keys [k0, k1) iff lo(first row of T) < k1 and
+  // hi(last row of T) > k0; both conditions hold on a prefix / suffix of the
+  // tiles, so their counts give the range.
+  int tq0 = 0, ntq = nqt;
+  if constexpr (WIN) {
+    __shared__ int cred[NW][2];
+    const int k0 = kt * BK, k1 = min(k0 + BK, a.Lk);
+    const int* lo = a.wlo + b * a.wsb;
+    const int* hi = a.whi + b * a.wsb;
+    const int nvt = (a.Lq + BQ - 1) / BQ;  // tiles holding valid rows
+    int c_lo = 0, c_hi = 0;
+    for (int T = tid; T < nvt; T += NW * 64) {
+      const int f = T * BQ, l = min(f + BQ - 1, a.Lq - 1);
+      const int lof = min(max(lo[f], 0), a.Lk);
+      const int lol = min(max(lo[l], 0), a.Lk);
+      const int hil = min(max(hi[l], lol), a.Lk);
+      c_hi += lof < k1;
+      c_lo += hil <= k0;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      c_lo += __shfl_xor(c_lo, off);
+      c_hi += __shfl_xor(c_hi, off);
+    }
+    if (lane == 0) {
+      cred[wave][0] = c_lo;
+      cred[wave][1] = c_hi;
+    }
+    __syncthreads();
+    int s_lo = 0, s_hi = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      s_lo += cred[w][0];
+      s_hi += cred[w][1];
+    }
+    tq0 = __builtin_amdgcn_readfirstlane(s_lo);
+    ntq = __builtin_amdgcn_readfirstlane(max(s_hi - s_lo, 0));
+  }
+  const int niter = ntq * group;
+  auto tile_head = [&](int it) { return it / ntq; };     // query head within the group
+  auto tile_idx = [&](int it) { return tq0 + it % ntq; };  // 64-row tile of that head
   // Buffers over the query heads of this KV head's group (b, hk*group ..).
   const int64_t bq0 = (int64_t)(b * a.Hq + hk * group);
   const uint32_t qbytes = (uint32_t)group * a.Lqp * D * 2;
@@ -190,13 +239,19 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // burst of them at the start of a phase would hold up the wave's
   // instruction stream).
   constexpr int kRowOps = TileStager<BQ, D, NWL>::kPer, kColOps = TileStager<D, BQ, NWL>::kPer;
-  constexpr int kRowHalf = 2 * kRowOps + 2, kColHalf = 2 * kColOps;
+  constexpr int kRowHalf = 2 * kRowOps + 2 + (WIN ? 2 : 0), kColHalf = 2 * kColOps;
   auto tile_rows = [&](int it) {  // first row of tile `it` in the group's copies
-    return (uint32_t)(it / nqt) * a.Lqp + (uint32_t)(it % nqt) * BQ;
+    return (uint32_t)tile_head(it) * a.Lqp + (uint32_t)tile_idx(it) * BQ;
   };
   auto tile_cols = [&](int it) {  // byte offset of tile `it` in the head_dim-major copies
-    return ((uint32_t)(it / nqt) * D * a.Lqp + (uint32_t)(it % nqt) * BQ) * 2;
+    return ((uint32_t)tile_head(it) * D * a.Lqp + (uint32_t)tile_idx(it) * BQ) * 2;
   };
+  // Window arrays of this batch (WIN); rows past Lq read as 0 (empty).
+  u32x4 rwl = {0u, 0u, 0u, 0u}, rwh = {0u, 0u, 0u, 0u};
+  if constexpr (WIN) {
+    rwl = make_rsrc(a.wlo + b * a.wsb, (uint32_t)a.Lq * 4);
+    rwh = make_rsrc(a.whi + b * a.wsb, (uint32_t)a.Lq * 4);
+  }
   auto row_op = [&](int it, auto bufc, int i) {
     RowStage& rsg = decltype(bufc)::value == 0 ? rs0 : rs1;
     const uint32_t row0 = tile_rows(it);
@@ -206,8 +261,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       rst.stage_one(rsg.dout, rdo, row0 * D * 2, i - kRowOps);
     else if (i == 2 * kRowOps)
       dma4(rl2, lds_addr(rsg.lse2), lane * 4, row0 * 4);  // every wave loads the stats: no branch
-    else
+    else if (i == 2 * kRowOps + 1)
       dma4(rnd, lds_addr(rsg.ndl), lane * 4, row0 * 4);
+    else if (i == 2 * kRowOps + 2)
+      dma4(rwl, lds_addr(rsg.wlo), lane * 4, (uint32_t)tile_idx(it) * BQ * 4);
+    else
+      dma4(rwh, lds_addr(rsg.whi), lane * 4, (uint32_t)tile_idx(it) * BQ * 4);
   };
   auto col_op = [&](int it, auto bufc, int i) {
     ColStage& csg = decltype(bufc)::value == 0 ? cs0 : cs1;
@@ -283,11 +342,31 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     u32x4 up[2][2];
     // Softmax step (sub, k2, e2): two probabilities, packed; the last step
     // of a (sub, k2) hands its 16 bytes to the partner wave.
+    // WIN: a tile not inside every row's window for all 32 keys of this
+    // wave (rows' windows are monotone: the last valid row has the largest
+    // lo, the first the smallest hi) masks scores per (row, key).
+    bool edge = false;
+    if constexpr (WIN) {
+      const int last = min(BQ - 1, a.Lq - 1 - tile_idx(it) * BQ);
+      const int kk0 = kt * BK + kw * 32;
+      edge = __builtin_amdgcn_readfirstlane(rsg.wlo[last]) > kk0 ||
+             __builtin_amdgcn_readfirstlane(rsg.whi[0]) < kk0 + 32;
+    }
     auto smx = [&](int sub, int k2, int e2) {
       const int e = 2 * e2;
       const f32x4& lv = l2[sub][k2][e >> 2];
-      const float p0 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e], c, -lv[e & 3]));
-      const float p1 = __builtin_amdgcn_exp2f(fmaf(s[sub][8 * k2 + e + 1], c, -lv[(e & 3) + 1]));
+      float s0 = s[sub][8 * k2 + e], s1 = s[sub][8 * k2 + e + 1];
+      if constexpr (WIN) {
+        if (edge) {
+          // rows 32*sub + 16*k2 + 8*hh + e (+1) of the tile, this lane's key
+          const int r0 = 32 * sub + 16 * k2 + 8 * hh + e;
+          const int lo0 = rsg.wlo[r0], lo1 = rsg.wlo[r0 + 1], hi0 = rsg.whi[r0], hi1 = rsg.whi[r0 + 1];
+          if (key < lo0 || key >= hi0) s0 = kNegInf;
+          if (key < lo1 || key >= hi1) s1 = kNegInf;
+        }
+      }
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(s0, c, -lv[e & 3]));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(s1, c, -lv[(e & 3) + 1]));
       up[sub][k2][e2] = pack_bf16x2(p0, p1);
       if (e2 == 3) {
         xp[64 * (2 * sub + k2)] = up[sub][k2];
@@ -362,12 +441,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     const ColStage& csg = buf == 0 ? cs0 : cs1;
     const int itc = min(it + 1, niter - 1);
     const int itr = min(it + 2, niter - 1);
-    // This tile's two dS units (query groups 2*(it % nqt) and +1).
+    // This tile's two dS units (query groups 2*tile_idx(it) and +1).
     u32x4 rds = {0u, 0u, 0u, 0u};
     uint32_t ds_unit1 = 0;
     if constexpr (STAGE) {
-      const int64_t bq = (int64_t)(bhk - a.kv0) * group + it / nqt;
-      const int64_t unit = (bq * (2 * nqt) + 2 * (it % nqt)) * nkt + kt;
+      const int64_t bq = (int64_t)(bhk - a.kv0) * group + tile_head(it);
+      const int64_t unit = (bq * (2 * nqt) + 2 * tile_idx(it)) * nkt + kt;
       rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, (uint32_t)(nkt + 1) * 8192);
       ds_unit1 = (uint32_t)nkt * 8192;
     }
@@ -461,7 +540,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   };
 
   retire_prologue_loads();
-  if (loader) {
+  if (loader && niter > 0) {  // niter is 0 when no window meets this block's keys
     using B0 = std::integral_constant<int, 0>;
     using B1 = std::integral_constant<int, 1>;
 #pragma unroll
@@ -858,7 +937,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
 // lane) comes from two transposed reads per 16-key step.  The kernel streams
 // dS from HBM once; K^T comes from L2 (the query groups of one head run on
 // one XCD).
-template <int D, int BK, int NSTG>
+// WIN: only the stages that meet the union of the workgroup's rows' key
+// windows are staged, and a wave multiplies only those that meet its own
+// 32 rows' windows (the dK/dV kernel wrote the dS of exactly those: a
+// group's window union lies inside its 64-row tile's).
+template <int D, int BK, int NSTG, bool WIN>
 __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   constexpr int NW = 8, DT = D / 32;
   static_assert(BK == 32 || BK == 64, "stage of 32 or 64 keys");
@@ -888,7 +971,32 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   const int qrow = qg * 32 + l32;
   const bool qvalid = qrow < a.Lq;
   const int nkt = (a.Lk + 127) / 128;
-  const int nst = a.Lkp / BK;
+  int s0 = 0, s1 = a.Lkp / BK;  // stages of the workgroup
+  int w0 = s0, w1 = s1;         // stages this wave multiplies
+  if constexpr (WIN) {
+    // Monotone windows: a row range's key union is [lo(first), hi(last)).
+    const int* lo = a.wlo + b * a.wsb;
+    const int* hi = a.whi + b * a.wsb;
+    auto range = [&](int r0, int r1, int& st0, int& st1) {  // rows [r0, r1)
+      r1 = min(r1, a.Lq);
+      st0 = st1 = 0;
+      if (r1 > r0) {
+        const int l = min(max(lo[r0], 0), a.Lk);
+        const int lol = min(max(lo[r1 - 1], 0), a.Lk);
+        const int h = min(max(hi[r1 - 1], lol), a.Lk);
+        if (h > l) {
+          st0 = l / BK;
+          st1 = (h + BK - 1) / BK;
+        }
+      }
+    };
+    range(qb * NW * 32, qb * NW * 32 + NW * 32, s0, s1);
+    range(qg * 32, qg * 32 + 32, w0, w1);
+    s0 = __builtin_amdgcn_readfirstlane(s0);
+    s1 = __builtin_amdgcn_readfirstlane(s1);
+    w0 = __builtin_amdgcn_readfirstlane(w0);
+    w1 = __builtin_amdgcn_readfirstlane(w1);
+  }
 
   const u32x4 rkt = make_rsrc(a.kt + (int64_t)(b * a.Hkv + hk) * D * a.Lkp, (uint32_t)a.Lkp * D * 2);
   const u32x4 rds =
@@ -931,19 +1039,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   };
 
   retire_prologue_loads();
+  if (s1 > s0) {  // same for every wave of the workgroup
 #pragma unroll
-  for (int p = 0; p < NSTG - 1; ++p) stage_load(min(p, nst - 1), st[p]);
-  // Iteration s: stage s is waited for (NSTG - 2 later stages may still be
-  // in flight), then stage s + NSTG - 1 (clamped: the last stage is
-  // re-loaded, same bytes) goes into the buffer stage s - 1 used.
-  int cur = 0;
-  for (int s = 0; s < nst; ++s) {
-    wait_vmem_n<(NSTG - 2) * kStageLoads>();
-    barrier_lds();
-    const int nxt = cur == 0 ? NSTG - 1 : cur - 1;
-    stage_load(min(s + NSTG - 1, nst - 1), st[nxt]);
-    compute(st[cur]);
-    cur = cur == NSTG - 1 ? 0 : cur + 1;
+    for (int p = 0; p < NSTG - 1; ++p) stage_load(min(s0 + p, s1 - 1), st[p]);
+    // Iteration s: stage s is waited for (NSTG - 2 later stages may still be
+    // in flight), then stage s + NSTG - 1 (clamped: the last stage is
+    // re-loaded, same bytes) goes into the buffer stage s - 1 used.
+    int cur = 0;
+    for (int s = s0; s < s1; ++s) {
+      wait_vmem_n<(NSTG - 2) * kStageLoads>();
+      barrier_lds();
+      const int nxt = cur == 0 ? NSTG - 1 : cur - 1;
+      stage_load(min(s + NSTG - 1, s1 - 1), st[nxt]);
+      if (!WIN || (s >= w0 && s < w1)) compute(st[cur]);
+      cur = cur == NSTG - 1 ? 0 : cur + 1;
+    }
   }
   wait_vmem();  // the last (re-staged) loads
 
@@ -995,7 +1105,10 @@ static void launch_dq_ds_d(const BwdArgs& a, hipStream_t stream) {
   LaunchTimer timer(kKidBwdDqDs, stream);
   // 64-key stages, three buffers: measured faster than 32-key stages with
   // four or six buffers (4.75 vs 4.9-5.4 ms per c3 chunk).
-  hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3>), grid, dim3(512), 0, stream, a);
+  if (a.wlo)
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, true>), grid, dim3(512), 0, stream, a);
+  else
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, false>), grid, dim3(512), 0, stream, a);
 }
 
 template <int D>
@@ -1032,16 +1145,21 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
     {
       const dim3 grid(nkt * p.nkv);
       LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup (8 waves) per CU: LDS-bound occupancy
-      if (mask) {
-        if (p.ds)
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true>), grid, dim3(512), 0, stream, p);
+      if (p.wlo) {  // windows (staged dS only)
+        if (mask)
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true, true>), grid, dim3(512), 0, stream, p);
         else
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, false>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true, true>), grid, dim3(512), 0, stream, p);
+      } else if (mask) {
+        if (p.ds)
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true, false>), grid, dim3(512), 0, stream, p);
+        else
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, false, false>), grid, dim3(512), 0, stream, p);
       } else {
         if (p.ds)
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true, false>), grid, dim3(512), 0, stream, p);
         else
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false, false>), grid, dim3(512), 0, stream, p);
       }
     }
     if (p.ds && !p.defer_dq) launch_dq_ds_d<D>(p, stream);

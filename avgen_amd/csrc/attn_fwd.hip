@@ -37,9 +37,15 @@ namespace avattn {
 // rate): q is quantized on load with its head's scale, K comes from the e4m3
 // copy (fp8.hip), and the per-head scales fold into the softmax constant and
 // the LSE.  P, V and O^T += V^T P^T stay bf16 / fp32 as above.
-template <int D, bool ROPE, bool FP8>
+//
+// WIN: per-query-row key windows [wlo, whi) (FwdArgs::wlo/whi).  The
+// workgroup visits only the tiles that meet the union of its rows' windows,
+// and a tile half that is not inside every window of the wave masks each
+// score outside its row's window to -inf (before the key bias and softmax).
+template <int D, bool ROPE, bool FP8, bool WIN>
 __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   static_assert(!(ROPE && FP8), "the fp8 variant takes rotated q");
+  static_assert(!(WIN && FP8), "windows on the bf16 path only");
   constexpr int NW = 8, BM = 32 * NW, BN = 64;
   // k-steps of q k^T: 16 bf16 channels (32x32x16 bf16) or 64 fp8 channels
   // (32x32x64 e4m3) per MFMA.
@@ -78,6 +84,53 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   const int qrow = qt * BM + wave * 32 + l32;
   const bool qvalid = qrow < a.Lq;
 
+  // Key windows: this lane's row's [wlo, whi) (every key for a row past the
+  // end); the wave's largest lo and smallest hi (a tile half inside both is
+  // inside every row's window); the workgroup's tile range [t0, t0 + ntile).
+  int wlo = 0, whi = a.Lkp, wlo_max = 0, whi_min = a.Lkp;
+  int t0 = 0;
+  int ntile = a.Lkp / BN;
+  if constexpr (WIN) {
+    __shared__ int wred[NW][2];
+    int rlo = 0x7fffffff, rhi = -1;  // range contribution (none for empty or past-the-end rows)
+    int mlo = -1, mhi = 0x7fffffff;  // interior test contribution
+    if (qvalid) {
+      // Clamped into 0 <= lo <= hi <= Lk, so any values stay in bounds.
+      wlo = min(max(a.wlo[b * a.wsb + qrow], 0), a.Lk);
+      whi = min(max(a.whi[b * a.wsb + qrow], wlo), a.Lk);
+      mlo = wlo;
+      mhi = whi;
+      if (wlo < whi) {
+        rlo = wlo;
+        rhi = whi;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      rlo = min(rlo, __shfl_xor(rlo, off));
+      rhi = max(rhi, __shfl_xor(rhi, off));
+      mlo = max(mlo, __shfl_xor(mlo, off));
+      mhi = min(mhi, __shfl_xor(mhi, off));
+    }
+    wlo_max = __builtin_amdgcn_readfirstlane(mlo);
+    whi_min = __builtin_amdgcn_readfirstlane(mhi);
+    if (lane == 0) {
+      wred[wave][0] = rlo;
+      wred[wave][1] = rhi;
+    }
+    __syncthreads();
+    int glo = 0x7fffffff, ghi = -1;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      glo = min(glo, wred[w][0]);
+      ghi = max(ghi, wred[w][1]);
+    }
+    glo = __builtin_amdgcn_readfirstlane(glo);
+    ghi = __builtin_amdgcn_readfirstlane(ghi);
+    t0 = ghi > glo ? glo / BN : 0;
+    ntile = ghi > glo ? (ghi + BN - 1) / BN - t0 : 0;
+  }
+
   const int64_t bhk = (int64_t)(b * a.Hkv + hk);
   const uint32_t slice = (uint32_t)a.Lkp * D * 2;  // bytes of one (b, h) slice of a copy
   const bf16* kcopy = FP8 ? reinterpret_cast<const bf16*>(a.k8) : a.kr;
@@ -86,7 +139,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   const u32x4 rb = make_rsrc(a.kbias + (int64_t)b * a.Lkp, (uint32_t)(a.Lkp + 64) * 4);
   // Flags are padded by 64 entries: the 64 read from a tile start stay inside.
   const u32x4 rf = make_rsrc(a.kfull + (int64_t)b * (a.Lkp / 32), (uint32_t)(a.Lkp / 32 + 64) * 4);
-  const int nkt = a.Lkp / BN;
+  const int tend = t0 + ntile;  // tiles t0 .. tend-1 (all of them without windows)
 
   using KSt = TileStager<BN, KRL, NW>;  // 64 K rows of D channels
   using VSt = TileStager<D, BN, NW>;  // D V^T rows of 64 keys (row stride Lkp)
@@ -244,10 +297,21 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
     }
   };
   // Softmax of one tile's scores (both halves) into the bf16 PV operands.
-  auto softmax = [&](const Stage& sg, f32x16* sh, bf16x8 (*pf)[2]) __attribute__((always_inline)) {
+  auto softmax = [&](const Stage& sg, f32x16* sh, bf16x8 (*pf)[2], int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       f32x16& s_cur = sh[hf];
+      if constexpr (WIN) {
+        // Register 8*k2 + e holds key 64*t + 32*hf + 16*k2 + 8*hh + e.
+        const int kh = BN * t + 32 * hf;
+        if (kh < wlo_max || kh + 32 > whi_min) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kh + 16 * (r >> 3) + 8 * hh + (r & 7);
+            if (key < wlo || key >= whi) s_cur[r] = kNegInf;
+          }
+        }
+      }
       if (!__builtin_amdgcn_readfirstlane(sg.flags[hf])) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
@@ -345,90 +409,95 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   };
 
   retire_prologue_loads();
-  {
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
-#pragma unroll
-    for (int i = 0; i < kStageOps; ++i) stage_op(0, B0(), i);
-#pragma unroll
-    for (int i = 0; i < kStageOps; ++i) stage_op(min(1, nkt - 1), B1(), i);
-  }
-
-  f32x16 sh[2];
-  bf16x8 pf[2][2];
-  if (wave < NW / 2) {
-    // Group A: QK^T(t), softmax(t), PV(t).
-    auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
-      constexpr int buf = decltype(bufc)::value;
-      using Next2 = std::integral_constant<int, (buf + 2) % 4>;
-      top();
-      const Stage& sg = stage_ref(bufc);
-      __builtin_amdgcn_s_setprio(2);
-      const int tl = min(t + 2, nkt - 1);
-      if constexpr (FP8) {
-        scores(sg, sh, no_slot);
-      } else {
-        scores(sg, sh, loads_in(tl, Next2()));
-        loads_after(tl, Next2(), 2 * KS);
-      }
-      __builtin_amdgcn_s_setprio(0);
-      softmax(sg, sh, pf);
-      __builtin_amdgcn_s_setprio(2);
-      if constexpr (FP8) {
-        pv(sg, pf, loads_in(tl, Next2()));
-        loads_after(tl, Next2(), 4 * DT);
-      } else {
-        pv(sg, pf, no_slot);
-      }
-    };
-    for (int t = 0; t < nkt; t += 4) {
-      body(t, std::integral_constant<int, 0>());
-      if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 1>());
-      if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 2>());
-      if (t + 3 < nkt) body(t + 3, std::integral_constant<int, 3>());
-    }
-  } else {
-    // Group B: softmax(t-1), PV(t-1), QK^T(t); the scores of tile t are
-    // carried to the next iteration.
-    auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
-      constexpr int buf = decltype(bufc)::value;
-      using Prev = std::integral_constant<int, (buf + 3) % 4>;
-      using Next2 = std::integral_constant<int, (buf + 2) % 4>;
-      top();
-      const Stage& sp = stage_ref(Prev());
-      __builtin_amdgcn_s_setprio(0);
-      softmax(sp, sh, pf);
-      __builtin_amdgcn_s_setprio(2);
-      pv(sp, pf, loads_in(min(t + 2, nkt - 1), Next2()));
-      loads_after(min(t + 2, nkt - 1), Next2(), 4 * DT);
-      scores(stage_ref(bufc), sh, no_slot);
-    };
+  // ntile is the same for every wave of the workgroup (0: every row's window
+  // is empty, nothing to visit).
+  if (ntile > 0) {
     {
-      // Iteration 0: only QK^T(0).
       using B0 = std::integral_constant<int, 0>;
-      using B2 = std::integral_constant<int, 2>;
-      top();
-      if constexpr (FP8) {
-        scores(stage_ref(B0()), sh, no_slot);
+      using B1 = std::integral_constant<int, 1>;
 #pragma unroll
-        for (int i = 0; i < kStageOps; ++i) stage_op(min(2, nkt - 1), B2(), i);
-      } else {
-        scores(stage_ref(B0()), sh, loads_in(min(2, nkt - 1), B2()));
-        loads_after(min(2, nkt - 1), B2(), 2 * KS);
+      for (int i = 0; i < kStageOps; ++i) stage_op(t0, B0(), i);
+#pragma unroll
+      for (int i = 0; i < kStageOps; ++i) stage_op(min(t0 + 1, tend - 1), B1(), i);
+    }
+
+    f32x16 sh[2];
+    bf16x8 pf[2][2];
+    // Tile t0 + i uses stage i % 4.
+    if (wave < NW / 2) {
+      // Group A: QK^T(t), softmax(t), PV(t).
+      auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        using Next2 = std::integral_constant<int, (buf + 2) % 4>;
+        top();
+        const Stage& sg = stage_ref(bufc);
+        __builtin_amdgcn_s_setprio(2);
+        const int tl = min(t + 2, tend - 1);
+        if constexpr (FP8) {
+          scores(sg, sh, no_slot);
+        } else {
+          scores(sg, sh, loads_in(tl, Next2()));
+          loads_after(tl, Next2(), 2 * KS);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        softmax(sg, sh, pf, t);
+        __builtin_amdgcn_s_setprio(2);
+        if constexpr (FP8) {
+          pv(sg, pf, loads_in(tl, Next2()));
+          loads_after(tl, Next2(), 4 * DT);
+        } else {
+          pv(sg, pf, no_slot);
+        }
+      };
+      for (int t = t0; t < tend; t += 4) {
+        body(t, std::integral_constant<int, 0>());
+        if (t + 1 < tend) body(t + 1, std::integral_constant<int, 1>());
+        if (t + 2 < tend) body(t + 2, std::integral_constant<int, 2>());
+        if (t + 3 < tend) body(t + 3, std::integral_constant<int, 3>());
       }
+    } else {
+      // Group B: softmax(t-1), PV(t-1), QK^T(t); the scores of tile t are
+      // carried to the next iteration.
+      auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
+        constexpr int buf = decltype(bufc)::value;
+        using Prev = std::integral_constant<int, (buf + 3) % 4>;
+        using Next2 = std::integral_constant<int, (buf + 2) % 4>;
+        top();
+        const Stage& sp = stage_ref(Prev());
+        __builtin_amdgcn_s_setprio(0);
+        softmax(sp, sh, pf, t - 1);
+        __builtin_amdgcn_s_setprio(2);
+        pv(sp, pf, loads_in(min(t + 2, tend - 1), Next2()));
+        loads_after(min(t + 2, tend - 1), Next2(), 4 * DT);
+        scores(stage_ref(bufc), sh, no_slot);
+      };
+      {
+        // Iteration 0: only QK^T(t0).
+        using B0 = std::integral_constant<int, 0>;
+        using B2 = std::integral_constant<int, 2>;
+        top();
+        if constexpr (FP8) {
+          scores(stage_ref(B0()), sh, no_slot);
+#pragma unroll
+          for (int i = 0; i < kStageOps; ++i) stage_op(min(t0 + 2, tend - 1), B2(), i);
+        } else {
+          scores(stage_ref(B0()), sh, loads_in(min(t0 + 2, tend - 1), B2()));
+          loads_after(min(t0 + 2, tend - 1), B2(), 2 * KS);
+        }
+      }
+      for (int t = t0 + 1; t < tend; t += 4) {
+        body(t, std::integral_constant<int, 1>());
+        if (t + 1 < tend) body(t + 1, std::integral_constant<int, 2>());
+        if (t + 2 < tend) body(t + 2, std::integral_constant<int, 3>());
+        if (t + 3 < tend) body(t + 3, std::integral_constant<int, 0>());
+      }
+      // Tail: softmax and PV of the last tile (its stage is not refilled).
+      const int bl = (ntile - 1) % 4;
+      const Stage& sl = bl == 0 ? st0 : (bl == 1 ? st1 : (bl == 2 ? st2 : st3));
+      __builtin_amdgcn_s_setprio(0);
+      softmax(sl, sh, pf, tend - 1);
+      pv(sl, pf, no_slot);
     }
-    for (int t = 1; t < nkt; t += 4) {
-      body(t, std::integral_constant<int, 1>());
-      if (t + 1 < nkt) body(t + 1, std::integral_constant<int, 2>());
-      if (t + 2 < nkt) body(t + 2, std::integral_constant<int, 3>());
-      if (t + 3 < nkt) body(t + 3, std::integral_constant<int, 0>());
-    }
-    // Tail: softmax and PV of the last tile (its stage is not refilled).
-    const int bl = (nkt - 1) % 4;
-    const Stage& sl = bl == 0 ? st0 : (bl == 1 ? st1 : (bl == 2 ? st2 : st3));
-    __builtin_amdgcn_s_setprio(0);
-    softmax(sl, sh, pf);
-    pv(sl, pf, no_slot);
   }
   __builtin_amdgcn_s_setprio(0);
   wait_vmem();  // the last (re-staged) tile loads
@@ -486,11 +555,13 @@ static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
   const dim3 block(512);
   LaunchTimer timer(fp8 ? kKidFwdFp8 : kKidFwd, stream);
   if (fp8)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false, true, false>), grid, block, 0, stream, a);
+  else if (a.wlo != nullptr)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false, false, true>), grid, block, 0, stream, a);
   else if (a.cos_q != nullptr)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, true, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, true, false, false>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false, false, false>), grid, block, 0, stream, a);
   return hipGetLastError();
 }
 

@@ -91,6 +91,17 @@ BwdWorkspace bwd_workspace(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32
   return w;
 }
 
+// Key windows: both arrays or neither, 4-byte aligned, batch stride 0
+// (shared) or >= len_q; not with the fused RoPE or fp8 variants.
+int check_windows(const int32_t* lo, const int32_t* hi, int64_t batch_stride, int32_t len_q, bool excluded) {
+  if (!lo && !hi) return AVATTN_OK;
+  if (!lo || !hi) return AVATTN_ERR_NULL_POINTER;
+  if (excluded) return AVATTN_ERR_ARGUMENT;
+  if (((reinterpret_cast<uintptr_t>(lo) | reinterpret_cast<uintptr_t>(hi)) & 3u) != 0) return AVATTN_ERR_LAYOUT;
+  if (batch_stride != 0 && batch_stride < len_q) return AVATTN_ERR_ARGUMENT;
+  return AVATTN_OK;
+}
+
 // The staged dS region starts on a 4 KB boundary after the base workspace.
 size_t staged_ds_offset(const BwdWorkspace& w) { return (w.total + 4095) / 4096 * 4096; }
 
@@ -118,7 +129,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 5; }
+int avattn_abi_version(void) { return 6; }
 
 }  // extern "C"
 
@@ -130,7 +141,8 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
              int32_t len_k, int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
              const float* rope_cos_q, const float* rope_sin_q, int64_t rope_batch_stride, bool fp8,
              const float* q_scale, const float* k_scale, float scale, void* out, const int64_t* out_strides,
-             float* lse, void* workspace, size_t workspace_bytes, avattn_stream_t stream) {
+             float* lse, void* workspace, size_t workspace_bytes, avattn_stream_t stream,
+             const int32_t* window_lo = nullptr, const int32_t* window_hi = nullptr, int64_t window_batch_stride = 0) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (st != AVATTN_OK) return st;
   if (!q_strides || !k_strides || !v_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
@@ -153,6 +165,8 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
   if (fp8 && (!q_scale || !k_scale)) return AVATTN_ERR_NULL_POINTER;
   if (fp8 && ((reinterpret_cast<uintptr_t>(q_scale) | reinterpret_cast<uintptr_t>(k_scale)) & 3u))
     return AVATTN_ERR_LAYOUT;
+  st = check_windows(window_lo, window_hi, window_batch_stride, len_q, fp8 || rope_cos_q != nullptr);
+  if (st != AVATTN_OK) return st;
   const FwdWorkspace wl = fwd_workspace(batch, heads_kv, len_k, head_dim, fp8);
   if (!workspace || workspace_bytes < wl.total || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
@@ -184,6 +198,9 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
   a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
   a.kmax2 = fp8 ? nullptr : reinterpret_cast<uint32_t*>(ws + wl.kmax2);
   a.Lkp = transpose_padded_len(len_k);
+  a.wlo = window_lo;
+  a.whi = window_hi;
+  a.wsb = window_batch_stride;
   return launch_status(launch_fwd(a, head_dim, s));
 }
 
@@ -210,6 +227,18 @@ int avattn_fwd_fp8(const void* q, const void* k, const void* v, const int64_t* q
   return fwd_impl(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
                   key_mask, key_mask_batch_stride, nullptr, nullptr, 0, true, q_scale, k_scale, scale, out,
                   out_strides, lse, workspace, workspace_bytes, stream);
+}
+
+int avattn_fwd_windowed(const void* q, const void* k, const void* v, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
+                        int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                        int64_t key_mask_batch_stride, const int32_t* window_lo, const int32_t* window_hi,
+                        int64_t window_batch_stride, float scale, void* out, const int64_t* out_strides, float* lse,
+                        void* workspace, size_t workspace_bytes, avattn_stream_t stream) {
+  if (!window_lo || !window_hi) return AVATTN_ERR_NULL_POINTER;
+  return fwd_impl(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
+                  key_mask, key_mask_batch_stride, nullptr, nullptr, 0, false, nullptr, nullptr, scale, out,
+                  out_strides, lse, workspace, workspace_bytes, stream, window_lo, window_hi, window_batch_stride);
 }
 
 size_t avattn_fwd_fp8_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k, int32_t head_dim) {
@@ -256,13 +285,14 @@ size_t avattn_bwd_staged_workspace_size(int32_t batch, int32_t heads_q, int32_t 
   return staged_ds_offset(wl) + (size_t)n * ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k);
 }
 
-int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out, const float* lse,
-               const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
-               const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
-               int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
-               int64_t key_mask_batch_stride, float scale, void* dq, const int64_t* dq_strides, void* dk,
-               const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
-               size_t workspace_bytes, uint32_t flags, avattn_stream_t stream) {
+static int bwd_impl(const void* dout, const void* q, const void* k, const void* v, const void* out, const float* lse,
+                    const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
+                    const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
+                    int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                    int64_t key_mask_batch_stride, float scale, void* dq, const int64_t* dq_strides, void* dk,
+                    const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
+                    size_t workspace_bytes, uint32_t flags, avattn_stream_t stream, const int32_t* window_lo,
+                    const int32_t* window_hi, int64_t window_batch_stride) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32 | AVATTN_BWD_STAGE_DS |
                 AVATTN_BWD_DEFER_DQ))
@@ -304,6 +334,10 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
       !strides_ok(out_strides))
     return AVATTN_ERR_LAYOUT;
   if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
+  st = check_windows(window_lo, window_hi, window_batch_stride, len_q, false);
+  if (st != AVATTN_OK) return st;
+  // Windows run on the staged-dS path only, and dq is not deferred.
+  if (window_lo && (!(flags & AVATTN_BWD_STAGE_DS) || (flags & AVATTN_BWD_DEFER_DQ))) return AVATTN_ERR_ARGUMENT;
   const BwdWorkspace wl = bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (!workspace || workspace_bytes < wl.total || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
@@ -350,6 +384,9 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
   a.nkv = batch * heads_kv;
   a.ds = nullptr;
   a.defer_dq = defer;
+  a.wlo = window_lo;
+  a.whi = window_hi;
+  a.wsb = window_batch_stride;
   int kv_per_pass = 0;
   if (flags & AVATTN_BWD_STAGE_DS) {
     const size_t off = staged_ds_offset(wl);
@@ -362,6 +399,34 @@ int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, co
     a.ds = reinterpret_cast<bf16*>(ws + off);
   }
   return launch_status(launch_bwd(a, head_dim, kv_per_pass, s));
+}
+
+int avattn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out, const float* lse,
+               const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
+               const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
+               int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+               int64_t key_mask_batch_stride, float scale, void* dq, const int64_t* dq_strides, void* dk,
+               const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
+               size_t workspace_bytes, uint32_t flags, avattn_stream_t stream) {
+  return bwd_impl(dout, q, k, v, out, lse, dout_strides, q_strides, k_strides, v_strides, out_strides, batch, heads_q,
+                  heads_kv, len_q, len_k, head_dim, key_mask, key_mask_batch_stride, scale, dq, dq_strides, dk,
+                  dk_strides, dv, dv_strides, workspace, workspace_bytes, flags, stream, nullptr, nullptr, 0);
+}
+
+int avattn_bwd_windowed(const void* dout, const void* q, const void* k, const void* v, const void* out,
+                        const float* lse, const int64_t* dout_strides, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                        int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
+                        int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                        const int32_t* window_lo, const int32_t* window_hi, int64_t window_batch_stride, float scale,
+                        void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                        const int64_t* dv_strides, void* workspace, size_t workspace_bytes, uint32_t flags,
+                        avattn_stream_t stream) {
+  if (!window_lo || !window_hi) return AVATTN_ERR_NULL_POINTER;
+  return bwd_impl(dout, q, k, v, out, lse, dout_strides, q_strides, k_strides, v_strides, out_strides, batch, heads_q,
+                  heads_kv, len_q, len_k, head_dim, key_mask, key_mask_batch_stride, scale, dq, dq_strides, dk,
+                  dk_strides, dv, dv_strides, workspace, workspace_bytes, flags, stream, window_lo, window_hi,
+                  window_batch_stride);
 }
 
 int avattn_bwd_dq_staged(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,

@@ -46,6 +46,11 @@ struct FwdArgs {
   // copy): the largest over a head bounds every score of a query row by
   // |q_row| * sqrt(max).
   uint32_t* kmax2;
+  // Key windows (null: every key): query row i of batch b attends to keys
+  // [wlo[b*wsb + i], whi[b*wsb + i]) (and the key mask), shared by all heads.
+  const int* wlo;
+  const int* whi;
+  int64_t wsb;
 };
 
 struct BwdArgs {
@@ -111,6 +116,11 @@ struct BwdArgs {
   // With ds: leave dq to launch_bwd_dq_staged (a later call on the same
   // workspace, possibly on another stream).
   bool defer_dq;
+  // Key windows as in FwdArgs (null: every key); non-decreasing in the row
+  // (lo and hi), staged dS only.
+  const int* wlo;
+  const int* whi;
+  int64_t wsb;
 };
 
 // Bytes of staged dS per (b, kv head) pair.

@@ -17,6 +17,12 @@ Ops (namespace ``avgen_amd``):
 * ``flash_fwd_fp8(q, k, v, key_mask, q_scale, k_scale, scale) -> (out, lse)``
   — forward with q k^T on e4m3 operands and per-head scales (no reference
   counterpart; the sampling-time fp8 variant of ``flash_fwd``), forward only.
+* ``flash_fwd_windowed(q, k, v, window_lo, window_hi, key_mask, scale)`` /
+  ``flash_bwd_windowed(...)`` — every query row i attends only keys
+  [window_lo[i], window_hi[i]) (int32, per batch or shared): the temporal
+  neighbour mask (src/avgen/models/blocks.py:54-104) and the block-diagonal
+  mask of packed variable-length sequences (src/avgen/data/packing.py:185-200)
+  as row ranges instead of an (L, L) boolean tensor; differentiable.
 """
 
 from __future__ import annotations
@@ -34,6 +40,8 @@ __all__ = [
     "flash_fwd",
     "flash_bwd",
     "flash_fwd_fp8",
+    "flash_fwd_windowed",
+    "flash_bwd_windowed",
     "fp8_absmax_scales",
     "lse_merge_",
     "rope_apply",
@@ -172,6 +180,85 @@ def _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale):
     )
     _lib.check(st, name)
     return out, lse
+
+
+def _check_windows(name, lo, hi, B, Lq):
+    """Key windows: int32 (B, Lq) or (Lq,) device tensors -> (lo, hi, batch stride)."""
+    if lo is None or hi is None:
+        raise ValueError(f"{name}: pass both window_lo and window_hi")
+    for label, t in (("window_lo", lo), ("window_hi", hi)):
+        if t.dtype is not torch.int32:
+            raise TypeError(f"{name}: {label} must be int32; got {t.dtype}")
+        if t.shape not in ((B, Lq), (Lq,), (1, Lq)):
+            raise ValueError(f"{name}: {label} must be (batch, queries) or (queries,); got {tuple(t.shape)}")
+    if lo.shape != hi.shape:
+        raise ValueError(f"{name}: window_lo and window_hi shapes differ")
+    lo, hi = lo.contiguous(), hi.contiguous()
+    wsb = Lq if lo.ndim == 2 and lo.shape[0] == B and B > 1 else 0
+    return lo, hi, wsb
+
+
+def _fwd_windowed_impl(q, k, v, window_lo, window_hi, key_mask, scale):
+    name = "avgen_amd.flash_fwd_windowed"
+    _check_qkv(name, q, k, v)
+    _require_gpu(name, q, k, v, key_mask, window_lo, window_hi)
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    lo, hi, wsb = _check_windows(name, window_lo, window_hi, B, Lq)
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    out = _kernel_ready(torch.empty_like(q, memory_format=torch.preserve_format))
+    lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws = _workspace(lib.avattn_fwd_workspace_size(B, Hkv, Lk, D), q.device)
+    st = lib.avattn_fwd_windowed(
+        _ptr(q), _ptr(k), _ptr(v), _strides3(q), _strides3(k), _strides3(v),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        _ptr(lo), _ptr(hi), wsb,
+        float(scale),
+        _ptr(out), _strides3(out), _ptr(lse),
+        _ptr(ws), ws.numel(),
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return out, lse
+
+
+def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale):
+    """Backward of _fwd_windowed_impl (windows non-decreasing in the row;
+    always with staged dS, in passes if one pass does not fit the budget)."""
+    name = "avgen_amd.flash_bwd_windowed"
+    _check_qkv(name, q, k, v)
+    _require_gpu(name, dout, q, k, v, out, lse, key_mask, window_lo, window_hi)
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    lo, hi, wsb = _check_windows(name, window_lo, window_hi, B, Lq)
+    if Lq > 1 and bool(((lo[..., 1:] < lo[..., :-1]) | (hi[..., 1:] < hi[..., :-1])).any()):
+        raise ValueError(f"{name}: the backward needs window_lo and window_hi non-decreasing along the queries")
+    dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
+    lse = lse.contiguous()
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    dq = _out_or_new(None, q, name, "dq")
+    dk = _out_or_new(None, k, name, "dk")
+    dv = _out_or_new(None, v, name, "dv")
+    lib = _lib.load()
+    nbytes, _ = bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds=True)
+    ws = _workspace(nbytes, q.device)
+    st = lib.avattn_bwd_windowed(
+        _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+        _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        _ptr(lo), _ptr(hi), wsb,
+        float(scale),
+        _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
+        _ptr(ws), ws.numel(),
+        _lib.BWD_STAGE_DS,
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return dq, dk, dv
 
 
 def _fwd_fp8_impl(q, k, v, key_mask, q_scale, k_scale, scale):
@@ -451,6 +538,66 @@ def flash_fwd_fp8(
 @flash_fwd_fp8.register_fake
 def _(q, k, v, key_mask, q_scale, k_scale, scale):
     return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
+
+
+@torch.library.custom_op("avgen_amd::flash_fwd_windowed", mutates_args=())
+def flash_fwd_windowed(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    window_lo: torch.Tensor,
+    window_hi: torch.Tensor,
+    key_mask: Optional[torch.Tensor],
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Forward where query row i attends keys [window_lo[i], window_hi[i]) only."""
+    return _fwd_windowed_impl(q, k, v, window_lo, window_hi, key_mask, scale)
+
+
+@flash_fwd_windowed.register_fake
+def _(q, k, v, window_lo, window_hi, key_mask, scale):
+    return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
+
+
+@torch.library.custom_op("avgen_amd::flash_bwd_windowed", mutates_args=())
+def flash_bwd_windowed(
+    dout: torch.Tensor,
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    window_lo: torch.Tensor,
+    window_hi: torch.Tensor,
+    key_mask: Optional[torch.Tensor],
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of ``flash_fwd_windowed`` (windows non-decreasing in the row)."""
+    return _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale)
+
+
+@flash_bwd_windowed.register_fake
+def _(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _fwd_windowed_setup(ctx, inputs, output):
+    q, k, v, window_lo, window_hi, key_mask, scale = inputs
+    out, lse = output
+    ctx.scale = scale
+    ctx.save_for_backward(q, k, v, out, lse, window_lo, window_hi, key_mask)
+    ctx.mark_non_differentiable(lse)
+
+
+def _fwd_windowed_backward(ctx, dout, _dlse):
+    q, k, v, out, lse, window_lo, window_hi, key_mask = ctx.saved_tensors
+    dq, dk, dv = flash_bwd_windowed(dout.contiguous(), q, k, v, out, lse, window_lo, window_hi, key_mask, ctx.scale)
+    return dq, dk, dv, None, None, None, None
+
+
+torch.library.register_autograd(
+    "avgen_amd::flash_fwd_windowed", _fwd_windowed_backward, setup_context=_fwd_windowed_setup
+)
 
 
 def _fwd_setup(ctx, inputs, output):

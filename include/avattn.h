@@ -241,6 +241,55 @@ int avattn_bwd_dq_staged(int32_t batch, int32_t heads_q, int32_t heads_kv,
                          uint32_t flags, avattn_stream_t stream);
 
 /*
+ * Attention with per-query-row key windows: row i of batch b attends to the
+ * keys j with window_lo[b*wsb + i] <= j < window_hi[b*wsb + i] (and, if
+ * given, key_mask[b, j]), the same for every head; wsb = window_batch_stride
+ * (0: one window array for every batch).  int32 device arrays of len_q
+ * entries per batch, values clamped into 0 <= lo <= hi <= len_k; a row with
+ * an empty window gets out = 0 and lse = -inf.  The forward visits only the
+ * 64-key tiles that meet its rows' windows.  The backward (staged dS only:
+ * flags must include AVATTN_BWD_STAGE_DS and not AVATTN_BWD_DEFER_DQ)
+ * requires lo and hi non-decreasing in the row (sorted time coordinates,
+ * packed sequences); it then visits only the query and key tiles that meet.
+ * Every other argument, the workspace sizes and the error codes are those of
+ * avattn_fwd / avattn_bwd (no RoPE argument: pass rotated q and k).
+ * Replaces the dense (B, 1, Lq, Lk) masks of
+ * src/avgen/models/blocks.py:54-104 (temporal_neighbour_mask, with sorted
+ * time coordinates) and src/avgen/data/packing.py:185-200 (the block-diagonal
+ * attention_mask of a packed layout; windows from cu_seqlens, :164-183).
+ */
+int avattn_fwd_windowed(const void* q, const void* k, const void* v,
+                        const int64_t* q_strides, const int64_t* k_strides,
+                        const int64_t* v_strides,
+                        int32_t batch, int32_t heads_q, int32_t heads_kv,
+                        int32_t len_q, int32_t len_k, int32_t head_dim,
+                        const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                        const int32_t* window_lo, const int32_t* window_hi,
+                        int64_t window_batch_stride,
+                        float scale,
+                        void* out, const int64_t* out_strides,
+                        float* lse,
+                        void* workspace, size_t workspace_bytes,
+                        avattn_stream_t stream);
+int avattn_bwd_windowed(const void* dout, const void* q, const void* k, const void* v,
+                        const void* out, const float* lse,
+                        const int64_t* dout_strides, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides,
+                        const int64_t* out_strides,
+                        int32_t batch, int32_t heads_q, int32_t heads_kv,
+                        int32_t len_q, int32_t len_k, int32_t head_dim,
+                        const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                        const int32_t* window_lo, const int32_t* window_hi,
+                        int64_t window_batch_stride,
+                        float scale,
+                        void* dq, const int64_t* dq_strides,
+                        void* dk, const int64_t* dk_strides,
+                        void* dv, const int64_t* dv_strides,
+                        void* workspace, size_t workspace_bytes,
+                        uint32_t flags,
+                        avattn_stream_t stream);
+
+/*
  * Online-softmax merge of one chunk's (out_blk, lse_blk) into the running
  * (out_acc, lse_acc), in place, in fp32:
  *   out_acc <- out_acc - sigmoid(lse_blk - lse_acc) * (out_acc - out_blk)

@@ -12,7 +12,9 @@ Modules:
   (src/avgen/models/attention.py -> torch SDPA), the flash backward, the
   ring merge and the ring forward/backward loops
   (torch/distributed/tensor/experimental/_context_parallel/_attention.py),
-  contiguous sharding (src/avgen/parallel/context.py) and the FLOP
+  contiguous sharding (src/avgen/parallel/context.py), the query-dependent
+  masks (temporal neighbourhoods, src/avgen/models/blocks.py:54-104; packed
+  sequences, src/avgen/data/packing.py:136-200) and the FLOP
   convention (src/avgen/simulate/compute.py).  Attention math is float64;
   the RoPE rotation mirrors the reference's float32 elementwise chain bit for
   bit and rounds to bf16.

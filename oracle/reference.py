@@ -162,14 +162,29 @@ def _expand_kv(k: np.ndarray, hq: int) -> np.ndarray:
     return np.repeat(k, hq // hk, axis=1) if hk != hq else k
 
 
+def _dense_mask(key_mask, attn_mask):
+    """Combined ``(B|1, 1, Lq|1, Lk)`` bool mask (True = attend), or None."""
+    m = None
+    if key_mask is not None:
+        m = np.asarray(key_mask, bool)[:, None, None, :]
+    if attn_mask is not None:
+        a = np.asarray(attn_mask, bool)
+        a = a[:, None] if a.ndim == 3 else a
+        m = a if m is None else (m & a)
+    return m
+
+
 def attention_f64(
     q: np.ndarray, k: np.ndarray, v: np.ndarray, key_mask: np.ndarray | None = None,
-    scale: float | None = None,
+    scale: float | None = None, attn_mask: np.ndarray | None = None,
 ) -> tuple[np.ndarray, np.ndarray]:
     """Softmax attention in float64 (the math of F.scaled_dot_product_attention
     called at src/avgen/models/attention.py:265-273, default scale 1/sqrt(D)).
 
-    key_mask: ``(B|1, Lk)`` bool, True = attend.  Returns ``(out, lse)``:
+    key_mask: ``(B|1, Lk)`` bool, True = attend; attn_mask: a dense
+    ``(B|1, [1,] Lq, Lk)`` bool mask (the query-dependent masks of
+    :func:`temporal_neighbour_mask` and :func:`packed_attention_mask`), and-ed
+    with key_mask.  Returns ``(out, lse)``:
     ``out (B, H, Lq, D)``, ``lse (B, H, Lq)`` natural log.  A row with no
     valid key gives out = 0 (what F.scaled_dot_product_attention returns) and
     lse = -inf.  Zero-length keys give zeros (src/avgen/models/attention.py
@@ -183,8 +198,8 @@ def attention_f64(
         return np.zeros_like(q), np.full((B, H, Lq), -np.inf)
     scale = 1.0 / math.sqrt(D) if scale is None else scale
     s = np.einsum("bhqd,bhkd->bhqk", q, k) * scale
-    if key_mask is not None:
-        m = np.asarray(key_mask, bool)[:, None, None, :]
+    m = _dense_mask(key_mask, attn_mask)
+    if m is not None:
         s = np.where(m, s, -np.inf)
     mx = s.max(axis=-1, keepdims=True)
     safe = np.where(np.isfinite(mx), mx, 0.0)
@@ -194,6 +209,62 @@ def attention_f64(
         out = np.where(l > 0, np.einsum("bhqk,bhkd->bhqd", p, v) / np.where(l > 0, l, 1.0), 0.0)
         lse = np.where(l[..., 0] > 0, np.log(np.where(l[..., 0] > 0, l[..., 0], 1.0)) + safe[..., 0], -np.inf)
     return out, lse
+
+
+# ---------------------------------------------------------------------------
+# Query-dependent masks: temporal neighbourhoods (src/avgen/models/blocks.py)
+# and packed variable-length sequences (src/avgen/data/packing.py)
+# ---------------------------------------------------------------------------
+
+
+def temporal_neighbour_mask(
+    query_seconds: np.ndarray, key_seconds: np.ndarray, window_seconds: float,
+    key_mask: np.ndarray | None = None,
+) -> np.ndarray | None:
+    """src/avgen/models/blocks.py:54-104: ``(B, 1, Lq, Lk)`` bool, True where
+    ``|tq - tk| <= window_seconds`` and the key is valid; a query row with no
+    admissible key attends to every key (the key mask included, :101-103).
+    ``window_seconds <= 0``: None when every key is valid (or no mask), else
+    the key mask as ``(B, 1, 1, Lk)`` (:92-95)."""
+    if window_seconds <= 0.0:
+        if key_mask is None or bool(np.asarray(key_mask, bool).all()):
+            return None
+        return np.asarray(key_mask, bool)[:, None, None, :]
+    tq = np.asarray(query_seconds)
+    tk = np.asarray(key_seconds)
+    m = np.abs(tq[:, :, None] - tk[:, None, :]) <= window_seconds
+    if key_mask is not None:
+        m = m & np.asarray(key_mask, bool)[:, None, :]
+    m = m | ~m.any(axis=-1, keepdims=True)
+    return m[:, None]
+
+
+PADDING_SEGMENT = -1
+
+
+def packed_segment_ids(lengths: Sequence[int], capacity: int) -> np.ndarray:
+    """src/avgen/data/packing.py:136-158: ``(capacity,)`` int32 segment index of
+    each position, PADDING_SEGMENT past the last segment."""
+    ids = np.full(capacity, PADDING_SEGMENT, np.int32)
+    start = 0
+    for seg, n in enumerate(lengths):
+        ids[start:start + n] = seg
+        start += n
+    return ids
+
+
+def packed_cu_seqlens(lengths: Sequence[int]) -> np.ndarray:
+    """src/avgen/data/packing.py:163-179: ``(segments + 1,)`` int32 bounds."""
+    return np.concatenate([[0], np.cumsum(np.asarray(lengths, np.int64))]).astype(np.int32)
+
+
+def packed_attention_mask(lengths: Sequence[int], capacity: int) -> np.ndarray:
+    """src/avgen/data/packing.py:181-200: ``(capacity, capacity)`` bool,
+    True where row and column lie in the same segment; padding positions
+    attend to nothing and are attended to by nothing."""
+    ids = packed_segment_ids(lengths, capacity)
+    valid = ids != PADDING_SEGMENT
+    return (ids[:, None] == ids[None, :]) & valid[:, None] & valid[None, :]
 
 
 # ---------------------------------------------------------------------------
@@ -258,7 +329,7 @@ def attention_fp8_f64(
 
 def attention_bwd_f64(
     dout: np.ndarray, q: np.ndarray, k: np.ndarray, v: np.ndarray, out: np.ndarray, lse: np.ndarray,
-    key_mask: np.ndarray | None = None, scale: float | None = None,
+    key_mask: np.ndarray | None = None, scale: float | None = None, attn_mask: np.ndarray | None = None,
 ) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Flash-attention backward in float64 given (possibly merged) ``out``/``lse``
     (what the ring backward hands the op, torch/.../_attention.py:567-575):
@@ -277,8 +348,9 @@ def attention_bwd_f64(
     s = np.einsum("bhqd,bhkd->bhqk", q, kk) * scale
     lse_b = np.where(np.isfinite(lse), lse, np.inf)[..., None]
     p = np.exp(s - lse_b)
-    if key_mask is not None:
-        p = np.where(np.asarray(key_mask, bool)[:, None, None, :], p, 0.0)
+    m = _dense_mask(key_mask, attn_mask)
+    if m is not None:
+        p = np.where(m, p, 0.0)
     dv = np.einsum("bhqk,bhqd->bhkd", p, do)
     dp = np.einsum("bhqd,bhkd->bhqk", do, vv)
     dr = (do * o).sum(-1, keepdims=True)

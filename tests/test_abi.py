@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 5
+    assert lib.avattn_abi_version() == 6
     for code in range(0, 10):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
@@ -150,6 +150,42 @@ def test_fwd_validation_paths(lib):
     # empty problems succeed without any launch
     assert _fwd(lib, Lq=0) == _lib.OK
     assert _fwd(lib, B=0) == _lib.OK
+
+
+def _fwd_windowed(lib, lo=32, hi=32, wb=0, **over):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+    a = dict(q=16, k=16, v=16, qs=s, ks=s, vs=s, B=2, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
+             scale=0.125, out=16, os=s, lse=16, ws=256, wsb=1 << 20, stream=None)
+    a.update(over)
+    return lib.avattn_fwd_windowed(a["q"], a["k"], a["v"], a["qs"], a["ks"], a["vs"], a["B"], a["Hq"], a["Hkv"],
+                                   a["Lq"], a["Lk"], a["D"], a["mask"], a["msb"], lo, hi, wb, a["scale"],
+                                   a["out"], a["os"], a["lse"], a["ws"], a["wsb"], a["stream"])
+
+
+@cpu_only
+def test_windowed_validation_paths(lib):
+    assert _fwd_windowed(lib, lo=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_windowed(lib, hi=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_windowed(lib, lo=34) == _lib.ERR_LAYOUT
+    assert _fwd_windowed(lib, wb=3) == _lib.ERR_ARGUMENT  # batch stride below len_q
+    assert _fwd_windowed(lib, wb=4, ws=8) == _lib.ERR_WORKSPACE  # valid windows reach the workspace check
+    assert _fwd_windowed(lib, wb=0, ws=8) == _lib.ERR_WORKSPACE
+    assert _fwd_windowed(lib, D=96) == _lib.ERR_HEAD_DIM
+    assert _fwd_windowed(lib, Lq=0) == _lib.OK
+    s = _lib.i64_array([1 << 17, 1 << 17, 128])
+    staged = lib.avattn_bwd_staged_workspace_size(1, 2, 2, 4, 4, 128, 2)
+
+    def bwd(lo, hi, wb, ws_bytes, flags):
+        return lib.avattn_bwd_windowed(16, 16, 16, 16, 16, 16, s, s, s, s, s, 1, 2, 2, 4, 4, 128, None, 0,
+                                       lo, hi, wb, 0.125, 16, s, 16, s, 16, s, 16, ws_bytes, flags, None)
+
+    assert bwd(None, 32, 0, staged, _lib.BWD_STAGE_DS) == _lib.ERR_NULL_POINTER
+    assert bwd(32, 32, 0, staged, 0) == _lib.ERR_ARGUMENT  # windows need staged dS
+    assert bwd(32, 32, 0, staged, _lib.BWD_STAGE_DS | _lib.BWD_DEFER_DQ) == _lib.ERR_ARGUMENT
+    assert bwd(32, 32, 2, staged, _lib.BWD_STAGE_DS) == _lib.ERR_ARGUMENT
+    assert bwd(34, 32, 0, staged, _lib.BWD_STAGE_DS) == _lib.ERR_LAYOUT
+    one_pair = lib.avattn_bwd_staged_workspace_size(1, 2, 2, 4, 4, 128, 1)
+    assert bwd(32, 32, 0, one_pair - 1, _lib.BWD_STAGE_DS) == _lib.ERR_WORKSPACE
 
 
 @cpu_only

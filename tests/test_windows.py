@@ -1,0 +1,107 @@
+"""Query-dependent masks as per-row key windows: the oracle's restatements
+of the reference masks pinned against the reference's own expectations and
+hand-worked cases, and the window builders (host logic, run here on CPU
+tensors) checked against those masks element by element."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from avgen_amd import attention as A
+from oracle import reference as R
+
+
+def _window_mask(lo, hi, Lk):
+    j = np.arange(Lk)
+    return (j >= np.asarray(lo)[..., None]) & (j < np.asarray(hi)[..., None])
+
+
+def test_packed_mask_matches_the_reference_test():
+    """tests/test_data.py:640-667 of the reference: segments of 3, 4 and 2
+    tokens in a capacity of 12."""
+    ids = R.packed_segment_ids([3, 4, 2], 12)
+    assert ids.tolist() == [0] * 3 + [1] * 4 + [2] * 2 + [R.PADDING_SEGMENT] * 3
+    assert R.packed_cu_seqlens([3, 4, 2]).tolist() == [0, 3, 7, 9]
+    mask = R.packed_attention_mask([3, 4, 2], 12)
+    assert mask.shape == (12, 12)
+    for row in range(12):
+        for col in range(12):
+            expected = ids[row] != R.PADDING_SEGMENT and ids[row] == ids[col]
+            assert bool(mask[row, col]) is bool(expected), (row, col)
+
+
+@pytest.mark.parametrize("lengths,capacity", [([3, 4, 2], 12), ([5], 5), ([1, 1, 1], 4), ([64, 200, 7, 129], 512)])
+def test_packed_windows_give_the_block_diagonal_mask(lengths, capacity):
+    cu = torch.tensor(R.packed_cu_seqlens(lengths))
+    lo, hi = A.packed_windows(cu, capacity)
+    assert lo.dtype is torch.int32 and hi.dtype is torch.int32
+    assert (lo[1:] >= lo[:-1]).all() and (hi[1:] >= hi[:-1]).all()
+    np.testing.assert_array_equal(_window_mask(lo.numpy(), hi.numpy(), capacity),
+                                  R.packed_attention_mask(lengths, capacity))
+
+
+def test_temporal_mask_hand_worked():
+    """|tq - tk| <= w with exactly representable times; the last query has no
+    key within the window and falls back to every key
+    (src/avgen/models/blocks.py:97-104)."""
+    tq = np.array([[0.0, 1.0, 2.0, 5.0]], np.float32)
+    tk = np.array([[0.0, 0.5, 1.5, 2.0, 2.6]], np.float32)
+    T, F = True, False
+    m = R.temporal_neighbour_mask(tq, tk, 0.5)
+    assert m.shape == (1, 1, 4, 5)
+    assert m[0, 0].tolist() == [[T, T, F, F, F], [F, T, T, F, F], [F, F, T, T, F], [T, T, T, T, T]]
+    km = np.array([[T, T, F, T, T]])
+    m = R.temporal_neighbour_mask(tq, tk, 0.5, km)
+    assert m[0, 0].tolist() == [[T, T, F, F, F], [F, T, F, F, F], [F, F, F, T, F], [T, T, T, T, T]]
+    # a window holding only masked keys also falls back to every key
+    km = np.array([[F, F, T, T, T]])
+    m = R.temporal_neighbour_mask(tq, tk, 0.5, km)
+    assert m[0, 0, 0].tolist() == [T, T, T, T, T]
+    # window <= 0: no mask, or the key mask alone (:92-95)
+    assert R.temporal_neighbour_mask(tq, tk, 0.0) is None
+    assert R.temporal_neighbour_mask(tq, tk, -1.0, np.ones((1, 5), bool)) is None
+    assert R.temporal_neighbour_mask(tq, tk, 0.0, km).shape == (1, 1, 1, 5)
+
+
+def _stream_times(n, rate, start=0.0, per_step=1):
+    steps = np.arange(n) // per_step
+    return (start + steps / rate).astype(np.float32)
+
+
+@pytest.mark.parametrize("window", [1 / 24, 0.25, 1.0, 1e-6, 30.0])
+def test_temporal_windows_select_the_reference_keys(window):
+    """Video times repeat per frame (many tokens share one time), audio runs at
+    another rate: the windows hold exactly the keys the dense mask holds,
+    boundary roundings included; rows with none are the fallback rows."""
+    tq = np.stack([_stream_times(600, 24.0, per_step=40), _stream_times(600, 24.0, 0.3, per_step=16)])
+    tk = np.stack([_stream_times(257, 43.07), _stream_times(257, 43.07, 0.01)])
+    lo, hi = A.temporal_neighbour_windows(torch.from_numpy(tq), torch.from_numpy(tk), window_seconds=window)
+    lo, hi = lo.numpy(), hi.numpy()
+    assert (np.diff(lo, axis=1) >= 0).all() and (np.diff(hi, axis=1) >= 0).all()
+    ref = R.temporal_neighbour_mask(tq, tk, window)[:, 0]
+    wm = _window_mask(lo, hi, tk.shape[1])
+    empty = hi == lo
+    np.testing.assert_array_equal(wm[~empty], ref[~empty])
+    assert ref[empty].all()  # fallback rows attend to everything
+
+
+def test_temporal_windows_at_rounding_boundaries():
+    """Differences that round onto the window edge: the bound search uses the
+    reference's own float32 predicate, so it agrees where tq - w would not."""
+    rng = np.random.default_rng(3)
+    tk = np.sort(rng.uniform(0, 2, (1, 4000)).astype(np.float32), axis=1)
+    w = 0.1
+    tq = np.sort((tk[:, rng.integers(0, 4000, 700)] + np.float32(w)).astype(np.float32), axis=1)
+    lo, hi = A.temporal_neighbour_windows(torch.from_numpy(tq), torch.from_numpy(tk), window_seconds=w)
+    ref = R.temporal_neighbour_mask(tq, tk, w)[:, 0]
+    wm = _window_mask(lo.numpy(), hi.numpy(), tk.shape[1])
+    np.testing.assert_array_equal(wm, ref)
+
+
+def test_window_builders_validate():
+    with pytest.raises(ValueError):
+        A.temporal_neighbour_windows(torch.zeros(3), torch.zeros(1, 3), window_seconds=1.0)
+    with pytest.raises(ValueError):
+        A.packed_windows(torch.zeros((2, 2), dtype=torch.int32), 4)
