@@ -177,6 +177,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // hi(last row of T) > k0; both conditions hold on a prefix / suffix of the
   // tiles, so their counts give the range.
   int tq0 = 0, ntq = nqt;
+  // WIN: tiles [w_ia, w_ib) hold only rows whose windows cover all 32 keys
+  // of this wave (hi(first row) >= kk0 + 32 and lo(last row) <= kk0; each
+  // condition holds on a suffix / prefix of the tiles); the others mask
+  // scores per (row, key).
+  int w_ia = 0, w_ib = 0;
   if constexpr (WIN) {
     __shared__ int cred[NW][2];
     const int k0 = kt * BK, k1 = min(k0 + BK, a.Lk);
@@ -210,6 +215,20 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     }
     tq0 = __builtin_amdgcn_readfirstlane(s_lo);
     ntq = __builtin_amdgcn_readfirstlane(max(s_hi - s_lo, 0));
+    const int kk0 = kt * BK + kw * 32;
+    int c_a = 0, c_b = 0;
+    for (int T = lane; T < nvt; T += 64) {
+      const int f = T * BQ, l = min(f + BQ - 1, a.Lq - 1);
+      c_a += hi[f] < kk0 + 32;
+      c_b += lo[l] <= kk0;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      c_a += __shfl_xor(c_a, off);
+      c_b += __shfl_xor(c_b, off);
+    }
+    w_ia = __builtin_amdgcn_readfirstlane(c_a);
+    w_ib = __builtin_amdgcn_readfirstlane(c_b);
   }
   const int niter = ntq * group;
   auto tile_head = [&](int it) { return it / ntq; };     // query head within the group
@@ -342,15 +361,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     u32x4 up[2][2];
     // Softmax step (sub, k2, e2): two probabilities, packed; the last step
     // of a (sub, k2) hands its 16 bytes to the partner wave.
-    // WIN: a tile not inside every row's window for all 32 keys of this
-    // wave (rows' windows are monotone: the last valid row has the largest
-    // lo, the first the smallest hi) masks scores per (row, key).
+    // WIN: a tile outside [w_ia, w_ib) masks scores per (row, key).
     bool edge = false;
     if constexpr (WIN) {
-      const int last = min(BQ - 1, a.Lq - 1 - tile_idx(it) * BQ);
-      const int kk0 = kt * BK + kw * 32;
-      edge = __builtin_amdgcn_readfirstlane(rsg.wlo[last]) > kk0 ||
-             __builtin_amdgcn_readfirstlane(rsg.whi[0]) < kk0 + 32;
+      const int T = tile_idx(it);
+      edge = T < w_ia || T >= w_ib;
     }
     auto smx = [&](int sub, int k2, int e2) {
       const int e = 2 * e2;

@@ -395,7 +395,10 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
     const size_t need = off + (defer ? (size_t)a.nkv * per : per);
     if (workspace_bytes < need) return AVATTN_ERR_WORKSPACE;
     const size_t fit = (workspace_bytes - off) / per;
-    kv_per_pass = (int)(fit < (size_t)a.nkv ? fit : (size_t)a.nkv);
+    // Passes of equal size (the fewest that fit): a short last pass would
+    // leave most of the chip idle for its whole launch.
+    const size_t npass = ((size_t)a.nkv + fit - 1) / fit;
+    kv_per_pass = (int)(((size_t)a.nkv + npass - 1) / npass);
     a.ds = reinterpret_cast<bf16*>(ws + off);
   }
   return launch_status(launch_bwd(a, head_dim, kv_per_pass, s));

@@ -340,6 +340,8 @@ def bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None):
         if not stage_ds:
             return base, False
         pairs = 1
+    npass = -(-(B * Hkv) // pairs)
+    pairs = -(-(B * Hkv) // npass)  # equal passes, as the library splits them
     return lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(pairs)), True
 
 

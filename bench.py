@@ -56,6 +56,16 @@ CONFIGS = {
     "c5": dict(B=2, H=40, Lq=75600, L=75600, D=128, cp=1, grid=(21, 45, 80), text=0,
                desc="c5 sampling with CFG batch: (2,40,75600,128) forward only, bf16 and fp8 (e4m3) q k^T "
                     "with per-head absmax scales, repeated calls"),
+    # Per-row key windows (block-sparse): the same 40h x d128 shape as c3's
+    # full sequence, fwd+bwd, FLOPs counted over admitted (query, key) pairs.
+    "varlen": dict(B=1, H=40, Lq=75600, L=75600, D=128, cp=1, grid=(21, 45, 80), text=0,
+                   segments=(28800, 21600, 14400, 9000),
+                   desc="varlen packed: 75,600-token capacity holding clips of 28,800/21,600/14,400/9,000 tokens "
+                        "(8/6/4/2.5 frames of 45x80) + 1,800 padding, (1,40,75600,128) fwd+bwd, windows from "
+                        "cu_seqlens"),
+    "window": dict(B=1, H=40, Lq=75600, L=75600, D=128, cp=1, grid=(21, 45, 80), text=0, window_seconds=0.25,
+                   desc="temporal window: (1,40,75600,128) self-attention fwd+bwd over the 21x45x80 latent at 8 fps, "
+                        "keys within 0.25 s of the query (+-2 frames), windows from temporal_neighbour_windows"),
 }
 
 
@@ -368,6 +378,87 @@ def bench_c5(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
+def bench_windowed(cfg: dict, name: str, steps: int, warmup: int) -> dict:
+    """fwd+bwd through the key-window kernels (`flash_fwd_windowed` and its
+    autograd backward) on the `varlen` or `window` workload.  The windows are
+    built once before the timed region, as the reference builds its dense
+    mask once per forward (src/avgen/models/dit.py:927-942)."""
+    import avgen_amd
+    from avgen_amd import _lib
+
+    B, H, L, D = cfg["B"], cfg["H"], cfg["L"], cfg["D"]
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    s = 1.0 / math.sqrt(2.0)
+    q = (torch.randn((B, H, L, D), generator=g, device=dev) * s).to(torch.bfloat16)
+    k = (torch.randn((B, H, L, D), generator=g, device=dev) * s).to(torch.bfloat16)
+    v = (torch.randn((B, H, L, D), generator=g, device=dev) * s).to(torch.bfloat16)
+    do = torch.randn((B, H, L, D), generator=g, device=dev).to(torch.bfloat16)
+    if name == "varlen":
+        cu = torch.tensor([0, *torch.tensor(cfg["segments"]).cumsum(0).tolist()], dtype=torch.int32)
+        lo, hi = avgen_amd.attention.packed_windows(cu, L, device=dev)
+    else:
+        t = video_coords(*cfg["grid"], batch=B, device=dev)[..., 0]
+        lo, hi = avgen_amd.attention.temporal_neighbour_windows(t, t, window_seconds=cfg["window_seconds"])
+    pairs = float((hi.long() - lo.long()).sum().item()) * (B if lo.ndim == 1 else 1)
+    scale = D ** -0.5
+
+    def one():
+        qq, kk, vv = (t.requires_grad_(True) for t in (q, k, v))
+        out, _ = avgen_amd.ops.flash_fwd_windowed(qq, kk, vv, lo, hi, None, scale)
+        out.backward(do)
+        q.grad = k.grad = v.grad = None
+
+    for i in range(warmup):
+        one()
+        torch.cuda.synchronize()
+        log(f"[bench] {name} warmup {i + 1}/{warmup} done")
+    with _lib.LaunchTiming(16 * steps + 16) as timing:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            one()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    log(f"[bench] {name}: timed {steps} steps in {t1 - t0:.3f}s")
+    per_kernel = {}
+    for kname in ("attn_fwd", "bwd_dkdv", "bwd_dq_ds", "bwd_preprocess", "transpose"):
+        ms, n = timing.read(kname)
+        per_kernel[kname] = {"total_ms": ms, "launches": n, "avg_ms": ms / n if n else 0.0}
+    timing.close()
+    ms_per_step = (t1 - t0) * 1e3 / steps
+    flops = 12.0 * H * D * pairs
+    rates = {kn: KERNEL_UNITS[kn] * 2.0 * H * D * pairs * steps / (per_kernel[kn]["total_ms"] / 1e3) / 1e12
+             for kn in ("attn_fwd", "bwd_dkdv", "bwd_dq_ds") if per_kernel[kn]["launches"]}
+    dominant = max(rates, key=lambda kn: per_kernel[kn]["total_ms"])
+    value = flops / (ms_per_step / 1e3) / 1e12
+    return {
+        "metric": f"windowed attention fwd+bwd TFLOP/s over admitted pairs ({name})",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)/sqrt(2) q/k/v, N(0,1) dO)",
+        "config": {"workload": cfg["desc"], "name": name, "batch": B, "heads": H, "head_dim": D, "len": L,
+                   "admitted_fraction": round(pairs / (B * float(L) * L), 4), "parallelism": "1 GPU"},
+        "pct_of_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        "flops_per_step": flops,
+        "kernels": {kn: {**kv, "algorithmic_tflops": round(rates[kn], 1) if kn in rates else None}
+                    for kn, kv in per_kernel.items()},
+        "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(rates[dominant], 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(rates[dominant] / PEAK_BF16_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -404,6 +495,10 @@ def main() -> int:
     if args.config == "c5":
         log(f"[bench] config c5: {cfg['desc']}")
         print(json.dumps(bench_c5(cfg, args.steps, args.warmup)), flush=True)
+        return 0
+    if args.config in ("varlen", "window"):
+        log(f"[bench] config {args.config}: {cfg['desc']}")
+        print(json.dumps(bench_windowed(cfg, args.config, args.steps, args.warmup)), flush=True)
         return 0
     log(f"[bench] config {args.config}: {cfg['desc']}")
     x = make_inputs(cfg, dev)
