@@ -12,7 +12,7 @@ interfaces:
 * :mod:`avgen_amd.ops` — the ``torch.library`` ops over the C ABI.
 """
 
-from . import attention, context, ops, ring, rope
+from . import attention, context, layers, ops, ring, rope
 from .attention import attention as attention_fn
 from .attention import key_padding_mask, rotary_attention
 from .ring import SDPAMerger, flash_attention_backward_op, flash_attention_op, ring_attention
@@ -30,6 +30,7 @@ __all__ = [
     "flash_attention_backward_op",
     "flash_attention_op",
     "key_padding_mask",
+    "layers",
     "ops",
     "ring",
     "ring_attention",

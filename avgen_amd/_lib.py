@@ -109,6 +109,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr, c_ptr, c_i64, c_i32,
          c_ptr, c_i64p, c_ptr],
     ),
+    "avattn_qk_norm_rope": (
+        ctypes.c_int,
+        [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_f32,
+         c_ptr, c_ptr, c_i64, c_ptr, c_i64p, c_ptr],
+    ),
+    "avattn_qk_norm_rope_bwd_workspace_size": (c_size, [c_i32]),
+    "avattn_qk_norm_rope_bwd": (
+        ctypes.c_int,
+        [c_ptr, c_i64p, c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_f32,
+         c_ptr, c_ptr, c_i64, c_ptr, c_i64p, c_ptr, c_ptr, c_size, c_ptr],
+    ),
     "avattn_timing_begin": (ctypes.c_int, [c_i32]),
     "avattn_timing_end": (ctypes.c_int, []),
     "avattn_timing_read": (ctypes.c_int, [c_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]),
@@ -201,6 +212,8 @@ KERNEL_IDS = {
     "attn_fwd_fp8": 8,
     "fp8_absmax": 9,
     "bwd_dq_ds": 10,
+    "qk_norm": 11,
+    "qk_norm_bwd": 12,
 }
 
 

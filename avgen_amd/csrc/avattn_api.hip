@@ -102,6 +102,36 @@ int check_windows(const int32_t* lo, const int32_t* hi, int64_t batch_stride, in
   return AVATTN_OK;
 }
 
+int check_qk_norm(const void* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,
+                  int32_t head_dim, const void* weight, float eps, const float* cos_tab, const float* sin_tab,
+                  int64_t table_batch_stride) {
+  if (batch < 0 || heads < 0 || len < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return AVATTN_ERR_HEAD_DIM;
+  if (!x_strides) return AVATTN_ERR_NULL_POINTER;
+  if (!(eps >= 0.f) || !isfinite(eps)) return AVATTN_ERR_ARGUMENT;
+  if (!cos_tab != !sin_tab) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * heads * len == 0) return AVATTN_OK;
+  if (!x) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(x) || !strides_ok(x_strides) || (weight && !aligned16(weight))) return AVATTN_ERR_LAYOUT;
+  if (cos_tab && (!aligned16(cos_tab) || !aligned16(sin_tab) || table_batch_stride % 4 != 0))
+    return AVATTN_ERR_LAYOUT;
+  if ((int64_t)batch * heads > kMaxI32 || len > kMaxI32) return AVATTN_ERR_TOO_LARGE;
+  return AVATTN_OK;
+}
+
+QkNormArgs qk_norm_args(const void* x, const int64_t* xs, int32_t batch, int32_t heads, int32_t len,
+                        const void* weight, float eps, const float* cos_tab, const float* sin_tab, int64_t tsb) {
+  QkNormArgs a{};
+  a.x = static_cast<const bf16*>(x);
+  a.xsb = xs[0]; a.xsh = xs[1]; a.xsl = xs[2];
+  a.B = batch; a.H = heads; a.L = len;
+  a.hfast = xs[1] < xs[2];
+  a.w = static_cast<const bf16*>(weight);
+  a.eps = eps;
+  a.ct = cos_tab; a.st = sin_tab; a.tsb = tsb;
+  return a;
+}
+
 // The staged dS region starts on a 4 KB boundary after the base workspace.
 size_t staged_ds_offset(const BwdWorkspace& w) { return (w.total + 4095) / 4096 * 4096; }
 
@@ -129,7 +159,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 6; }
+int avattn_abi_version(void) { return 7; }
 
 }  // extern "C"
 
@@ -515,6 +545,56 @@ int avattn_rope_apply(const void* x, const int64_t* x_strides, int32_t batch, in
                                          heads, len, head_dim, cos_tab, sin_tab, table_batch_stride, inverse != 0,
                                          static_cast<bf16*>(out), out_strides[0], out_strides[1], out_strides[2],
                                          reinterpret_cast<hipStream_t>(stream)));
+}
+
+size_t avattn_qk_norm_rope_bwd_workspace_size(int32_t head_dim) {
+  if (head_dim != 64 && head_dim != 128) return 0;
+  return qk_norm_bwd_workspace_bytes(head_dim);
+}
+
+int avattn_qk_norm_rope(const void* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,
+                        int32_t head_dim, const void* weight, float eps, const float* cos_tab, const float* sin_tab,
+                        int64_t table_batch_stride, void* out, const int64_t* out_strides, avattn_stream_t stream) {
+  int st = check_qk_norm(x, x_strides, batch, heads, len, head_dim, weight, eps, cos_tab, sin_tab,
+                         table_batch_stride);
+  if (st != AVATTN_OK) return st;
+  if (!out_strides) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * heads * len == 0) return AVATTN_OK;
+  if (!out) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(out) || !strides_ok(out_strides)) return AVATTN_ERR_LAYOUT;
+  QkNormArgs a = qk_norm_args(x, x_strides, batch, heads, len, weight, eps, cos_tab, sin_tab, table_batch_stride);
+  a.out = static_cast<bf16*>(out);
+  a.osb = out_strides[0]; a.osh = out_strides[1]; a.osl = out_strides[2];
+  return launch_status(launch_qk_norm(a, head_dim, reinterpret_cast<hipStream_t>(stream)));
+}
+
+int avattn_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, const void* dy, const int64_t* dy_strides,
+                            int32_t batch, int32_t heads, int32_t len, int32_t head_dim, const void* weight, float eps,
+                            const float* cos_tab, const float* sin_tab, int64_t table_batch_stride, void* dx,
+                            const int64_t* dx_strides, float* dweight, void* workspace, size_t workspace_bytes,
+                            avattn_stream_t stream) {
+  int st = check_qk_norm(x, x_strides, batch, heads, len, head_dim, weight, eps, cos_tab, sin_tab,
+                         table_batch_stride);
+  if (st != AVATTN_OK) return st;
+  if (!dy_strides || !dx_strides) return AVATTN_ERR_NULL_POINTER;
+  if (weight && !dweight) return AVATTN_ERR_NULL_POINTER;
+  if (weight && (!workspace || workspace_bytes < qk_norm_bwd_workspace_bytes(head_dim) || !aligned16(workspace)))
+    return AVATTN_ERR_WORKSPACE;
+  if ((int64_t)batch * heads * len == 0) {
+    if (!weight) return AVATTN_OK;
+    // No rows: the gain's gradient is zero (the reduction over no blocks).
+    return launch_status(launch_qk_norm_dw_zero(dweight, head_dim, reinterpret_cast<hipStream_t>(stream)));
+  }
+  if (!dy || !dx) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(dy) || !aligned16(dx) || !strides_ok(dy_strides) || !strides_ok(dx_strides))
+    return AVATTN_ERR_LAYOUT;
+  QkNormArgs a = qk_norm_args(x, x_strides, batch, heads, len, weight, eps, cos_tab, sin_tab, table_batch_stride);
+  a.dy = static_cast<const bf16*>(dy);
+  a.dsb = dy_strides[0]; a.dsh = dy_strides[1]; a.dsl = dy_strides[2];
+  a.dx = static_cast<bf16*>(dx);
+  a.xgb = dx_strides[0]; a.xgh = dx_strides[1]; a.xgl = dx_strides[2];
+  a.wpart = weight ? static_cast<float*>(workspace) : nullptr;
+  return launch_status(launch_qk_norm_bwd(a, head_dim, dweight, reinterpret_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

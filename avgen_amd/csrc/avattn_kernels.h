@@ -142,6 +142,8 @@ enum KernelId : int {
   kKidFwdFp8 = 8,
   kKidAbsmax = 9,
   kKidBwdDqDs = 10,
+  kKidQkNorm = 11,
+  kKidQkNormBwd = 12,
 };
 
 // Records HIP events around one launch on `stream` while timing is enabled.
@@ -194,6 +196,33 @@ hipError_t launch_bwd(const BwdArgs& a, int head_dim, int kv_per_pass, hipStream
 // dQ from the dS and K^T copy a deferred launch_bwd left in the workspace
 // (every (b, kv head) pair in one pass).
 hipError_t launch_bwd_dq_staged(const BwdArgs& a, int head_dim, hipStream_t stream);
+// Fused q/k RMSNorm + rotation (qk_norm.hip).  Rows (b, h, i) of x, dy,
+// out and dx at b*sb + h*sh + i*sl (elements), head_dim contiguous.
+struct QkNormArgs {
+  const bf16* x;
+  int64_t xsb, xsh, xsl;
+  int B, H, L;
+  bool hfast;        // visit rows head-fastest (set when the head stride is the smaller)
+  const bf16* w;     // (head_dim) gain, or null for none
+  float eps;
+  const float* ct;   // rotation tables (b, 0, i, pair) at b*tsb + i*head_dim/2 + pair; null: no rotation
+  const float* st;
+  int64_t tsb;
+  bf16* out;         // forward output
+  int64_t osb, osh, osl;
+  const bf16* dy;    // backward: gradient of the output
+  int64_t dsb, dsh, dsl;
+  bf16* dx;          // backward: gradient of x
+  int64_t xgb, xgh, xgl;
+  float* wpart;      // backward: per-block dW partials (qk_norm_bwd_workspace_bytes), null without a gain
+};
+size_t qk_norm_bwd_workspace_bytes(int head_dim);
+hipError_t launch_qk_norm(const QkNormArgs& a, int head_dim, hipStream_t stream);
+// Backward; with a.wpart also dw (head_dim floats) = the gain's gradient.
+hipError_t launch_qk_norm_bwd(const QkNormArgs& a, int head_dim, float* dw, hipStream_t stream);
+// dw[0 .. head_dim) = 0 (the gain gradient of an empty input).
+hipError_t launch_qk_norm_dw_zero(float* dw, int head_dim, hipStream_t stream);
+
 hipError_t launch_zero_rows(bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
                             hipStream_t stream);
 hipError_t launch_lse_merge(float* out_acc, float* lse_acc, const void* out_blk, const float* lse_blk, int64_t rows,

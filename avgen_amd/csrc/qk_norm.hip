@@ -1,0 +1,226 @@
+// Per-head RMSNorm of q or k rows fused with the interleaved-pair rotation:
+// the steps between the q/k projections and the attention kernel
+// (src/avgen/models/layers.py:530-536: q_norm/k_norm, then apply_rotary),
+// and their backward.
+//
+// Forward, per row of head_dim values (torch's F.rms_norm with a bf16 gain,
+// src/avgen/models/layers.py:106-118, then src/avgen/models/rope.py:297-338):
+//   rstd = 1/sqrt(mean(x^2) + eps)            (fp32)
+//   n    = bf16((x * rstd) * w)               (the norm's bf16 output)
+//   y    = bf16(rotate(n, cos, sin))          (fp32 rotation, as rotate8)
+// Backward, given dy:
+//   g    = bf16(rotate^T(dy))                 (the rotation's autograd grad)
+//   xh   = x * rstd,  wg = w * g
+//   dx   = bf16(rstd * (wg - xh * mean(wg * xh)))
+//   dw   = sum over rows of g * xh            (fp32, per-block partials then
+//                                              one reduction: deterministic)
+// One row is D/8 lanes holding 16 bytes each, so every access is a full
+// 128-bit load or store; rows are visited in memory order (head fastest for
+// a (batch, seq, head, dim) layout, seq fastest otherwise).  HBM-bound: one
+// read and one write of the rows (two reads in the backward).
+#include "avattn_device.h"
+#include "avattn_kernels.h"
+
+namespace avattn {
+
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormBwdBlocks = 1024;  // fixed grid of the backward: dW partials per block
+
+__device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    f[2 * p] = __uint_as_float(v[p] << 16);
+    f[2 * p + 1] = __uint_as_float(v[p] & 0xffff0000u);
+  }
+}
+
+// Row u -> element offset of its first value for strides (sb, sh, sl).
+struct RowMap {
+  int H, L;
+  bool hfast;
+  __device__ __forceinline__ void split(int64_t u, int& b, int& h, int& i) const {
+    if (hfast) {
+      h = (int)(u % H);
+      const int64_t r = u / H;
+      i = (int)(r % L);
+      b = (int)(r / L);
+    } else {
+      i = (int)(u % L);
+      const int64_t r = u / L;
+      h = (int)(r % H);
+      b = (int)(r / H);
+    }
+  }
+};
+
+// Sum over the R lanes of one row (consecutive lanes, R a power of two).
+template <int R>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+  for (int off = R / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+}  // namespace
+
+template <int D>
+__global__ __launch_bounds__(kNormThreads) void qk_norm_fwd_kernel(QkNormArgs a) {
+#pragma clang fp contract(off)
+  constexpr int R = D / 8;
+  constexpr int RPB = kNormThreads / R;
+  const int c = threadIdx.x % R;
+  float w[8];
+  if (a.w) {
+    unpack8(*reinterpret_cast<const u32x4*>(a.w + 8 * c), w);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = 1.f;
+  }
+  const RowMap map{a.H, a.L, a.hfast};
+  const int64_t nrows = (int64_t)a.B * a.H * a.L;
+  for (int64_t u = (int64_t)blockIdx.x * RPB + threadIdx.x / R; u < nrows; u += (int64_t)gridDim.x * RPB) {
+    int b, h, i;
+    map.split(u, b, h, i);
+    const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c);
+    float x[8];
+    unpack8(xv, x);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+    ss = row_sum<R>(ss);
+    const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
+    u32x4 n;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float t0 = x[2 * p] * rstd, t1 = x[2 * p + 1] * rstd;
+      n[p] = pack_bf16x2(t0 * w[2 * p], t1 * w[2 * p + 1]);
+    }
+    if (a.ct) {
+      const int64_t t = b * a.tsb + (int64_t)i * (D / 2) + 4 * c;
+      n = rotate8(n, *reinterpret_cast<const f32x4*>(a.ct + t), *reinterpret_cast<const f32x4*>(a.st + t), false);
+    }
+    *reinterpret_cast<u32x4*>(a.out + b * a.osb + h * a.osh + (int64_t)i * a.osl + 8 * c) = n;
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kNormThreads) void qk_norm_bwd_kernel(QkNormArgs a) {
+#pragma clang fp contract(off)
+  constexpr int R = D / 8;
+  constexpr int RPB = kNormThreads / R;
+  __shared__ float red[RPB][D];
+  const int c = threadIdx.x % R;
+  float w[8], dw[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dw[j] = 0.f;
+  if (a.w) {
+    unpack8(*reinterpret_cast<const u32x4*>(a.w + 8 * c), w);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w[j] = 1.f;
+  }
+  const RowMap map{a.H, a.L, a.hfast};
+  const int64_t nrows = (int64_t)a.B * a.H * a.L;
+  for (int64_t u = (int64_t)blockIdx.x * RPB + threadIdx.x / R; u < nrows; u += (int64_t)gridDim.x * RPB) {
+    int b, h, i;
+    map.split(u, b, h, i);
+    float x[8], g[8];
+    unpack8(*reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c), x);
+    u32x4 gv = *reinterpret_cast<const u32x4*>(a.dy + b * a.dsb + h * a.dsh + (int64_t)i * a.dsl + 8 * c);
+    if (a.ct) {
+      const int64_t t = b * a.tsb + (int64_t)i * (D / 2) + 4 * c;
+      gv = rotate8(gv, *reinterpret_cast<const f32x4*>(a.ct + t), *reinterpret_cast<const f32x4*>(a.st + t), true);
+    }
+    unpack8(gv, g);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+    ss = row_sum<R>(ss);
+    const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
+    float xh[8], wg[8], dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      xh[j] = x[j] * rstd;
+      wg[j] = w[j] * g[j];
+      dot += wg[j] * xh[j];
+      dw[j] += g[j] * xh[j];
+    }
+    const float m = row_sum<R>(dot) / (float)D;
+    u32x4 dx;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      dx[p] = pack_bf16x2(rstd * (wg[2 * p] - xh[2 * p] * m), rstd * (wg[2 * p + 1] - xh[2 * p + 1] * m));
+    *reinterpret_cast<u32x4*>(a.dx + b * a.xgb + h * a.xgh + (int64_t)i * a.xgl + 8 * c) = dx;
+  }
+  if (!a.wpart) return;  // uniform: no gain, no dW
+  const int rg = threadIdx.x / R;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) red[rg][8 * c + j] = dw[j];
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float s = 0.f;
+    for (int r = 0; r < RPB; ++r) s += red[r][threadIdx.x];
+    a.wpart[(int64_t)blockIdx.x * D + threadIdx.x] = s;
+  }
+}
+
+// dw[d] = sum over the backward's blocks of their partials (fixed order).
+__global__ __launch_bounds__(128) void qk_norm_dw_kernel(const float* __restrict__ part, int nblocks, int D,
+                                                         float* __restrict__ dw) {
+  const int d = threadIdx.x;
+  if (d >= D) return;
+  float s = 0.f;
+  for (int k = 0; k < nblocks; ++k) s += part[(int64_t)k * D + d];
+  dw[d] = s;
+}
+
+__global__ __launch_bounds__(128) void qk_norm_dw_zero_kernel(int D, float* __restrict__ dw) {
+  if ((int)threadIdx.x < D) dw[threadIdx.x] = 0.f;
+}
+
+hipError_t launch_qk_norm_dw_zero(float* dw, int D, hipStream_t stream) {
+  hipLaunchKernelGGL(qk_norm_dw_zero_kernel, dim3(1), dim3(128), 0, stream, D, dw);
+  return hipGetLastError();
+}
+
+size_t qk_norm_bwd_workspace_bytes(int D) { return (size_t)kNormBwdBlocks * D * sizeof(float); }
+
+static int norm_grid(int64_t rows, int D, int cap) {
+  const int64_t rpb = kNormThreads / (D / 8);
+  const int64_t blocks = (rows + rpb - 1) / rpb;
+  return (int)(blocks < 1 ? 1 : (blocks > cap ? cap : blocks));
+}
+
+hipError_t launch_qk_norm(const QkNormArgs& a, int D, hipStream_t stream) {
+  const int64_t rows = (int64_t)a.B * a.H * a.L;
+  if (rows == 0) return hipSuccess;
+  LaunchTimer timer(kKidQkNorm, stream);
+  const dim3 grid(norm_grid(rows, D, 16384)), block(kNormThreads);
+  if (D == 128)
+    hipLaunchKernelGGL(qk_norm_fwd_kernel<128>, grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL(qk_norm_fwd_kernel<64>, grid, block, 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_bwd(const QkNormArgs& a, int D, float* dw, hipStream_t stream) {
+  const int64_t rows = (int64_t)a.B * a.H * a.L;
+  if (rows == 0) return hipSuccess;
+  const int nb = norm_grid(rows, D, kNormBwdBlocks);
+  {
+    LaunchTimer timer(kKidQkNormBwd, stream);
+    if (D == 128)
+      hipLaunchKernelGGL(qk_norm_bwd_kernel<128>, dim3(nb), dim3(kNormThreads), 0, stream, a);
+    else
+      hipLaunchKernelGGL(qk_norm_bwd_kernel<64>, dim3(nb), dim3(kNormThreads), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (!a.wpart) return hipSuccess;
+  hipLaunchKernelGGL(qk_norm_dw_kernel, dim3(1), dim3(128), 0, stream, a.wpart, nb, D, dw);
+  return hipGetLastError();
+}
+
+}  // namespace avattn

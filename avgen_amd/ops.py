@@ -23,6 +23,9 @@ Ops (namespace ``avgen_amd``):
   neighbour mask (src/avgen/models/blocks.py:54-104) and the block-diagonal
   mask of packed variable-length sequences (src/avgen/data/packing.py:185-200)
   as row ranges instead of an (L, L) boolean tensor; differentiable.
+* ``qk_norm_rope(x, weight, eps, cos, sin)`` — per-head RMSNorm of q or k
+  with a bf16 gain, then the rotation (tables None: norm only), in one pass:
+  src/avgen/models/layers.py:530-536; differentiable in ``x`` and ``weight``.
 """
 
 from __future__ import annotations
@@ -46,6 +49,8 @@ __all__ = [
     "lse_merge_",
     "rope_apply",
     "rope_tables",
+    "qk_norm_rope",
+    "qk_norm_rope_bwd",
     "default_scale",
 ]
 
@@ -459,13 +464,70 @@ def _rope_apply_impl(x, cos, sin, inverse):
     cos, sin, tsb = _check_tables(name, cos, sin, B, L, D)
     _require_gpu(name, x, cos, sin)
     x = _kernel_ready(x)
-    out = torch.empty((B, H, L, D), device=x.device, dtype=x.dtype)
+    out = _kernel_ready(torch.empty_like(x, memory_format=torch.preserve_format))
     st = _lib.load().avattn_rope_apply(
         _ptr(x), _strides3(x), B, H, L, D, _ptr(cos), _ptr(sin), tsb, 1 if inverse else 0,
         _ptr(out), _strides3(out), _stream(x.device),
     )
     _lib.check(st, name)
     return out
+
+
+def _qk_norm_common(name, x, weight, eps, cos, sin):
+    if x.ndim != 4:
+        raise ValueError(f"{name}: input must be (batch, heads, length, head_dim); got {tuple(x.shape)}")
+    if x.dtype is not torch.bfloat16:
+        raise TypeError(f"{name}: input must be bfloat16; got {x.dtype}")
+    B, H, L, D = x.shape
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"{name}: head_dim {D} not supported (supported: {SUPPORTED_HEAD_DIMS})")
+    if weight is not None:
+        if weight.shape != (D,):
+            raise ValueError(f"{name}: weight must be ({D},); got {tuple(weight.shape)}")
+        weight = weight.to(torch.bfloat16).contiguous()
+    tsb = 0
+    if cos is not None or sin is not None:
+        if cos is None or sin is None:
+            raise ValueError(f"{name}: pass both rotation tables or neither")
+        cos, sin, tsb = _check_tables(name, cos, sin, B, L, D)
+    if not (eps >= 0.0 and math.isfinite(eps)):
+        raise ValueError(f"{name}: eps must be finite and >= 0; got {eps}")
+    _require_gpu(name, x, weight, cos, sin)
+    return _kernel_ready(x), weight, cos, sin, tsb
+
+
+def _qk_norm_rope_impl(x, weight, eps, cos, sin):
+    name = "avgen_amd.qk_norm_rope"
+    x, w, cos, sin, tsb = _qk_norm_common(name, x, weight, eps, cos, sin)
+    B, H, L, D = x.shape
+    out = _kernel_ready(torch.empty_like(x, memory_format=torch.preserve_format))
+    st = _lib.load().avattn_qk_norm_rope(
+        _ptr(x), _strides3(x), B, H, L, D, _ptr(w), float(eps), _ptr(cos), _ptr(sin), tsb,
+        _ptr(out), _strides3(out), _stream(x.device))
+    _lib.check(st, name)
+    return out
+
+
+def _qk_norm_rope_bwd_impl(dy, x, weight, eps, cos, sin):
+    name = "avgen_amd.qk_norm_rope_bwd"
+    x, w, cos, sin, tsb = _qk_norm_common(name, x, weight, eps, cos, sin)
+    B, H, L, D = x.shape
+    if dy.shape != x.shape or dy.dtype is not torch.bfloat16:
+        raise ValueError(f"{name}: dy must be bf16 {tuple(x.shape)}")
+    _require_gpu(name, dy)
+    dy = _kernel_ready(dy)
+    dx = _kernel_ready(torch.empty_like(x, memory_format=torch.preserve_format))
+    lib = _lib.load()
+    dw = ws = None
+    if w is not None:
+        dw = torch.empty(D, device=x.device, dtype=torch.float32)
+        ws = _workspace(lib.avattn_qk_norm_rope_bwd_workspace_size(D), x.device)
+    st = lib.avattn_qk_norm_rope_bwd(
+        _ptr(x), _strides3(x), _ptr(dy), _strides3(dy), B, H, L, D, _ptr(w), float(eps),
+        _ptr(cos), _ptr(sin), tsb, _ptr(dx), _strides3(dx), _ptr(dw), _ptr(ws), 0 if ws is None else ws.numel(),
+        _stream(x.device))
+    _lib.check(st, name)
+    return dx, dw
 
 
 # ---------------------------------------------------------------------------
@@ -600,6 +662,52 @@ def _fwd_windowed_backward(ctx, dout, _dlse):
 torch.library.register_autograd(
     "avgen_amd::flash_fwd_windowed", _fwd_windowed_backward, setup_context=_fwd_windowed_setup
 )
+
+
+@torch.library.custom_op("avgen_amd::qk_norm_rope", mutates_args=())
+def qk_norm_rope(
+    x: torch.Tensor, weight: Optional[torch.Tensor], eps: float, cos: Optional[torch.Tensor],
+    sin: Optional[torch.Tensor],
+) -> torch.Tensor:
+    """Per-head RMSNorm (gain ``weight`` cast to bf16) then the rotation; see module docstring."""
+    return _qk_norm_rope_impl(x, weight, eps, cos, sin)
+
+
+@qk_norm_rope.register_fake
+def _(x, weight, eps, cos, sin):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("avgen_amd::qk_norm_rope_bwd", mutates_args=())
+def qk_norm_rope_bwd(
+    dy: torch.Tensor, x: torch.Tensor, weight: Optional[torch.Tensor], eps: float, cos: Optional[torch.Tensor],
+    sin: Optional[torch.Tensor],
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(dx, dweight)`` of ``qk_norm_rope`` (``dweight`` fp32; zeros(0) without a gain)."""
+    dx, dw = _qk_norm_rope_bwd_impl(dy, x, weight, eps, cos, sin)
+    return dx, (dw if dw is not None else x.new_zeros(0, dtype=torch.float32))
+
+
+@qk_norm_rope_bwd.register_fake
+def _(dy, x, weight, eps, cos, sin):
+    return torch.empty_like(x), x.new_empty(0 if weight is None else x.shape[-1], dtype=torch.float32)
+
+
+def _qk_norm_setup(ctx, inputs, output):
+    x, weight, eps, cos, sin = inputs
+    ctx.eps = eps
+    ctx.has_weight = weight is not None
+    ctx.weight_dtype = None if weight is None else weight.dtype
+    ctx.save_for_backward(x, weight, cos, sin)
+
+
+def _qk_norm_backward(ctx, dy):
+    x, weight, cos, sin = ctx.saved_tensors
+    dx, dw = qk_norm_rope_bwd(dy.contiguous(), x, weight, ctx.eps, cos, sin)
+    return dx, (dw.to(ctx.weight_dtype) if ctx.has_weight else None), None, None, None
+
+
+torch.library.register_autograd("avgen_amd::qk_norm_rope", _qk_norm_backward, setup_context=_qk_norm_setup)
 
 
 def _fwd_setup(ctx, inputs, output):

@@ -66,6 +66,10 @@ CONFIGS = {
     "window": dict(B=1, H=40, Lq=75600, L=75600, D=128, cp=1, grid=(21, 45, 80), text=0, window_seconds=0.25,
                    desc="temporal window: (1,40,75600,128) self-attention fwd+bwd over the 21x45x80 latent at 8 fps, "
                         "keys within 0.25 s of the query (+-2 frames), windows from temporal_neighbour_windows"),
+    # Fused q/k RMSNorm + rotation over c3's full sequence (HBM-bound).
+    "qknorm": dict(B=1, H=40, Lq=75600, L=75600, D=128, cp=1, grid=(21, 45, 80), text=0,
+                   desc="qk norm + rotation: q_proj output (1,75600,40*128) viewed as heads, RMSNorm with a bf16 "
+                        "gain then 3D RoPE, forward and backward (dx, dweight)"),
 }
 
 
@@ -459,6 +463,74 @@ def bench_windowed(cfg: dict, name: str, steps: int, warmup: int) -> dict:
     }
 
 
+def bench_qknorm(cfg: dict, steps: int, warmup: int) -> dict:
+    """Fused RMSNorm + rotation of one q (or k) projection, forward and
+    backward, on c3's full sequence.  Algorithmic HBM bytes: forward reads x
+    and writes y (4 B per element) plus the cos/sin tables (4 B per (token,
+    dim)); backward reads x and dy and writes dx (6 B per element) plus the
+    tables; the dW partials (0.5 MB) are not counted."""
+    import avgen_amd
+    from avgen_amd import _lib
+
+    B, H, L, D = cfg["B"], cfg["H"], cfg["L"], cfg["D"]
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    xp = torch.randn((B, L, H * D), generator=g, device=dev).to(torch.bfloat16)
+    x = avgen_amd.layers.split_heads(xp, D).requires_grad_(True)
+    w = (torch.rand(D, generator=g, device=dev) + 0.5).requires_grad_(True)
+    dy = torch.randn((B, H, L, D), generator=g, device=dev).to(torch.bfloat16).transpose(1, 2).contiguous().transpose(1, 2)
+    tables = avgen_amd.rope.build_rotary_tables(video_coords(*cfg["grid"], batch=B, device=dev), head_dim=D)
+
+    def one():
+        y = avgen_amd.layers.qk_norm_rope(x, w, eps=1e-6, tables=tables)
+        y.backward(dy)
+        x.grad = w.grad = None
+
+    for _ in range(warmup):
+        one()
+    torch.cuda.synchronize()
+    with _lib.LaunchTiming(8 * steps + 8) as timing:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            one()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    fms, fn = timing.read("qk_norm")
+    bms, bn = timing.read("qk_norm_bwd")
+    timing.close()
+    n = float(B * H * L * D)
+    fwd_bytes = 4.0 * n + 4.0 * B * L * D
+    bwd_bytes = 6.0 * n + 4.0 * B * L * D
+    fwd_gbs = fwd_bytes * fn / (fms / 1e3) / 1e9
+    bwd_gbs = bwd_bytes * bn / (bms / 1e3) / 1e9
+    ms_per_step = (t1 - t0) * 1e3 / steps
+    value = (fwd_bytes + bwd_bytes) / (ms_per_step / 1e3) / 1e9
+    return {
+        "metric": "q/k RMSNorm + rotation fwd+bwd GB/s (algorithmic HBM bytes)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations and gradients, U[0.5,1.5) gain, 8-fps 2x2-patch coords)",
+        "config": {"workload": cfg["desc"], "name": "qknorm", "batch": B, "heads": H, "len": L, "head_dim": D,
+                   "parallelism": "1 GPU"},
+        "kernels": {"qk_norm": {"avg_ms": fms / max(fn, 1), "launches": fn, "gbs": round(fwd_gbs, 1)},
+                    "qk_norm_bwd": {"avg_ms": bms / max(bn, 1), "launches": bn, "gbs": round(bwd_gbs, 1)}},
+        "roofline": {"kernel": "qk_norm_bwd", "bound": "hbm", "achieved": round(bwd_gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(bwd_gbs / PEAK_HBM_GBS, 4), "traffic": None},
+        "roofline_fwd": {"kernel": "qk_norm", "bound": "hbm", "achieved": round(fwd_gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(fwd_gbs / PEAK_HBM_GBS, 4)},
+        "cpu_baseline": None,
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -495,6 +567,10 @@ def main() -> int:
     if args.config == "c5":
         log(f"[bench] config c5: {cfg['desc']}")
         print(json.dumps(bench_c5(cfg, args.steps, args.warmup)), flush=True)
+        return 0
+    if args.config == "qknorm":
+        log(f"[bench] config qknorm: {cfg['desc']}")
+        print(json.dumps(bench_qknorm(cfg, args.steps, args.warmup)), flush=True)
         return 0
     if args.config in ("varlen", "window"):
         log(f"[bench] config {args.config}: {cfg['desc']}")

@@ -35,6 +35,12 @@
  *                       of the sampling-time CFG configuration, a drop-in for
  *                       attention() (src/avgen/models/attention.py:227-273)
  *                       where fp8 scores are acceptable
+ *   avattn_fwd_windowed, src/avgen/models/blocks.py:54-104 (the dense
+ *   avattn_bwd_windowed  temporal_neighbour_mask fed to attention) and
+ *                       src/avgen/data/packing.py:181-200 (the packed
+ *                       block-diagonal mask) as per-row key windows
+ *   avattn_qk_norm_rope, src/avgen/models/layers.py:530-536 (q_norm/k_norm
+ *   avattn_qk_norm_rope_bwd  then apply_rotary) and their autograd backward
  */
 #ifndef AVATTN_H
 #define AVATTN_H
@@ -345,6 +351,48 @@ int avattn_rope_apply(const void* x, const int64_t* x_strides,
                       avattn_stream_t stream);
 
 /*
+ * Per-head RMSNorm of q or k rows fused with the rotation: replaces the
+ * q_norm / k_norm step and the apply_rotary call that follows it
+ * (src/avgen/models/layers.py:530-536; the norm is F.rms_norm with the gain
+ * cast to bf16, src/avgen/models/layers.py:106-118; the rotation
+ * src/avgen/models/rope.py:297-338).  Per row of head_dim values:
+ * rstd = 1/sqrt(mean(x^2) + eps); n = bf16((x*rstd)*weight) (fp32 math);
+ * out = bf16 rotation of n as in avattn_rope_apply (inverse 0), or out = n
+ * when cos_tab is NULL.  weight: bf16 (head_dim), NULL = no gain.
+ * x/out strides: 3 entries (batch, head, seq), head_dim contiguous; a
+ * (batch, seq, heads, head_dim) projection output passes as a strided view.
+ * head_dim 64 or 128.  Tables as for avattn_rope_apply.
+ */
+int avattn_qk_norm_rope(const void* x, const int64_t* x_strides,
+                        int32_t batch, int32_t heads, int32_t len,
+                        int32_t head_dim, const void* weight, float eps,
+                        const float* cos_tab, const float* sin_tab,
+                        int64_t table_batch_stride,
+                        void* out, const int64_t* out_strides,
+                        avattn_stream_t stream);
+
+/* Device workspace bytes avattn_qk_norm_rope_bwd needs (dW partials). */
+size_t avattn_qk_norm_rope_bwd_workspace_size(int32_t head_dim);
+
+/*
+ * Backward of avattn_qk_norm_rope given dy (the gradient of out):
+ * g = bf16 transposed rotation of dy (avattn_rope_apply, inverse 1), then the
+ * RMSNorm gradient dx = bf16(rstd*(w*g - xh*mean(w*g*xh))), xh = x*rstd,
+ * and, when weight is not NULL, dweight (head_dim floats, fp32) = sum over
+ * all rows of g*xh, reduced in a fixed order (deterministic).  dy/dx
+ * strides as x.  The workspace is used only with a weight.
+ */
+int avattn_qk_norm_rope_bwd(const void* x, const int64_t* x_strides,
+                            const void* dy, const int64_t* dy_strides,
+                            int32_t batch, int32_t heads, int32_t len,
+                            int32_t head_dim, const void* weight, float eps,
+                            const float* cos_tab, const float* sin_tab,
+                            int64_t table_batch_stride,
+                            void* dx, const int64_t* dx_strides,
+                            float* dweight, void* workspace,
+                            size_t workspace_bytes, avattn_stream_t stream);
+
+/*
  * Launch timing (diagnostics; no counterpart in the reference, whose kernels
  * are PyTorch's).  While enabled, every kernel launch of this library
  * records a pair of HIP events on its launch stream; avattn_timing_read sums
@@ -352,7 +400,8 @@ int avattn_rope_apply(const void* x, const int64_t* x_strides,
  * events).  Kernel ids: 0 forward, 1 backward preprocess, 2 backward dK/dV,
  * 3 backward dQ, 4 LSE merge, 5 rotary apply, 6 rotary tables,
  * 7 operand copies (forward and backward operand preparation, including the
- * fp8 forward's e4m3 k copy), 8 fp8 forward, 9 fp8 absmax scales.
+ * fp8 forward's e4m3 k copy), 8 fp8 forward, 9 fp8 absmax scales,
+ * 10 dQ from staged dS, 11 q/k norm + rotation, 12 its backward.
  * avattn_timing_begin creates `capacity` event pairs (call it outside any
  * timed or captured region); launches beyond capacity are not recorded and
  * make avattn_timing_read return AVATTN_ERR_WORKSPACE.

@@ -123,6 +123,43 @@ def apply_rotary_bf16(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, inverse: 
     return bf16_round(out)
 
 
+# ---------------------------------------------------------------------------
+# QK RMSNorm  (src/avgen/models/layers.py:70-118, 153-174, 530-531)
+# ---------------------------------------------------------------------------
+
+
+def rms_norm_bf16(x: np.ndarray, weight: np.ndarray | None, eps: float = 1e-6) -> np.ndarray:
+    """F.rms_norm over the last axis as FusedRMSNorm calls it on bf16
+    activations (src/avgen/models/layers.py:106-118: the gain cast to bf16):
+    float32 ``rstd = 1/sqrt(mean(x^2) + eps)``, ``(x * rstd) * w`` in float32,
+    rounded once to bf16.  ``x`` holds bf16 values as float32."""
+    x = np.asarray(x, np.float32)
+    D = x.shape[-1]
+    ms = (np.square(x, dtype=np.float32).sum(axis=-1, keepdims=True, dtype=np.float32) / np.float32(D)).astype(np.float32)
+    rstd = (np.float32(1.0) / np.sqrt(ms + np.float32(eps), dtype=np.float32)).astype(np.float32)
+    t = (x * rstd).astype(np.float32)
+    if weight is not None:
+        t = (t * bf16_round(np.asarray(weight, np.float32))).astype(np.float32)
+    return bf16_round(t)
+
+
+def rms_norm_bwd_f64(
+    x: np.ndarray, weight: np.ndarray | None, g: np.ndarray, eps: float = 1e-6
+) -> tuple[np.ndarray, np.ndarray | None]:
+    """Gradients of ``y = x * rstd(x) * w`` over the last axis in float64:
+    ``dx = rstd * (w*g - xh * mean(w*g*xh))``, ``xh = x*rstd``, and
+    ``dw = sum(g * xh)`` over every other axis (None without a gain)."""
+    x = np.asarray(x, np.float64)
+    g = np.asarray(g, np.float64)
+    w = np.ones(x.shape[-1]) if weight is None else bf16_round(np.asarray(weight, np.float32)).astype(np.float64)
+    rstd = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    xh = x * rstd
+    wg = w * g
+    dx = rstd * (wg - xh * np.mean(wg * xh, axis=-1, keepdims=True))
+    dw = None if weight is None else (g * xh).reshape(-1, x.shape[-1]).sum(0)
+    return dx, dw
+
+
 def video_coords(frames: int, height: int, width: int, fps: float = 8.0,
                  patch: tuple[int, int] = (2, 2), batch: int = 1) -> np.ndarray:
     """``(B, F*H*W, 3)`` float32 ``(seconds, row*patch_h, col*patch_w)``, token
