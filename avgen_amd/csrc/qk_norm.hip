@@ -166,14 +166,23 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_bwd_kernel(QkNormArgs a)
   }
 }
 
-// dw[d] = sum over the backward's blocks of their partials (fixed order).
-__global__ __launch_bounds__(128) void qk_norm_dw_kernel(const float* __restrict__ part, int nblocks, int D,
+// dw[d] = sum over the backward's blocks of their partials: one workgroup
+// per d, each thread a strided share of the partials, then a tree over the
+// threads (a fixed order, so the result is the same on every run).
+__global__ __launch_bounds__(256) void qk_norm_dw_kernel(const float* __restrict__ part, int nblocks, int D,
                                                          float* __restrict__ dw) {
-  const int d = threadIdx.x;
-  if (d >= D) return;
+  __shared__ float red[256];
+  const int d = blockIdx.x;
   float s = 0.f;
-  for (int k = 0; k < nblocks; ++k) s += part[(int64_t)k * D + d];
-  dw[d] = s;
+  for (int k = threadIdx.x; k < nblocks; k += 256) s += part[(int64_t)k * D + d];
+  red[threadIdx.x] = s;
+  __syncthreads();
+#pragma unroll
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) dw[d] = red[0];
 }
 
 __global__ __launch_bounds__(128) void qk_norm_dw_zero_kernel(int D, float* __restrict__ dw) {
@@ -219,7 +228,7 @@ hipError_t launch_qk_norm_bwd(const QkNormArgs& a, int D, float* dw, hipStream_t
     if (e != hipSuccess) return e;
   }
   if (!a.wpart) return hipSuccess;
-  hipLaunchKernelGGL(qk_norm_dw_kernel, dim3(1), dim3(128), 0, stream, a.wpart, nb, D, dw);
+  hipLaunchKernelGGL(qk_norm_dw_kernel, dim3(D), dim3(256), 0, stream, a.wpart, nb, D, dw);
   return hipGetLastError();
 }
 

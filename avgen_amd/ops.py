@@ -655,7 +655,7 @@ def _fwd_windowed_setup(ctx, inputs, output):
 
 def _fwd_windowed_backward(ctx, dout, _dlse):
     q, k, v, out, lse, window_lo, window_hi, key_mask = ctx.saved_tensors
-    dq, dk, dv = flash_bwd_windowed(dout.contiguous(), q, k, v, out, lse, window_lo, window_hi, key_mask, ctx.scale)
+    dq, dk, dv = flash_bwd_windowed(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, ctx.scale)
     return dq, dk, dv, None, None, None, None
 
 
@@ -703,7 +703,7 @@ def _qk_norm_setup(ctx, inputs, output):
 
 def _qk_norm_backward(ctx, dy):
     x, weight, cos, sin = ctx.saved_tensors
-    dx, dw = qk_norm_rope_bwd(dy.contiguous(), x, weight, ctx.eps, cos, sin)
+    dx, dw = qk_norm_rope_bwd(dy, x, weight, ctx.eps, cos, sin)
     return dx, (dw.to(ctx.weight_dtype) if ctx.has_weight else None), None, None, None
 
 
@@ -722,10 +722,10 @@ def _fwd_backward(ctx, dout, _dlse):
     q, k, v, out, lse, key_mask, rope_cos, rope_sin = ctx.saved_tensors
     if rope_cos is not None:
         q_rot = rope_apply(q, rope_cos, rope_sin, False)
-        dq_rot, dk, dv = flash_bwd(dout.contiguous(), q_rot, k, v, out, lse, key_mask, ctx.scale)
+        dq_rot, dk, dv = flash_bwd(dout, q_rot, k, v, out, lse, key_mask, ctx.scale)
         dq = rope_apply(dq_rot, rope_cos, rope_sin, True)
     else:
-        dq, dk, dv = flash_bwd(dout.contiguous(), q, k, v, out, lse, key_mask, ctx.scale)
+        dq, dk, dv = flash_bwd(dout, q, k, v, out, lse, key_mask, ctx.scale)
     return dq, dk, dv, None, None, None, None
 
 
@@ -740,7 +740,7 @@ def _rope_setup(ctx, inputs, output):
 
 def _rope_backward(ctx, grad):
     cos, sin = ctx.saved_tensors
-    return rope_apply(grad.contiguous(), cos, sin, not ctx.inverse), None, None, None
+    return rope_apply(grad, cos, sin, not ctx.inverse), None, None, None
 
 
 torch.library.register_autograd("avgen_amd::rope_apply", _rope_backward, setup_context=_rope_setup)

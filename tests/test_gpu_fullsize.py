@@ -198,3 +198,76 @@ def test_c2_block_with_fused_rope(amd):
     ou = amd.attention.attention(amd.rope.apply_rotary(qu, tables), k_rot, v)
     ou.backward(do)
     assert torch.equal(out, ou) and torch.equal(qg.grad, qu.grad)
+
+
+def _grads(amd_fn, q, k, v, do):
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+    out = amd_fn(q, k, v)
+    out.backward(do)
+    return out.detach(), q.grad, k.grad, v.grad
+
+
+def test_varlen_full_capacity_equals_per_segment_attention(amd):
+    """75,600-token capacity holding clips of 28,800/21,600/14,400/9,000
+    tokens and 1,800 padding, 40 heads x d128 (the bench's varlen workload):
+    packed attention equals attention over each clip on its own, forward and
+    all gradients; padding rows are zero and padding keys get zero dK/dV."""
+    H, D, L = 40, 128, 75600
+    seg = [28800, 21600, 14400, 9000]
+    cu = torch.tensor([0, 28800, 50400, 64800, 73800], dtype=torch.int32)
+    q, k, v = (_rand((1, H, L, D), s, 0.7) for s in (61, 62, 63))
+    do = _rand((1, H, L, D), 64, 1.0)
+    out, dq, dk, dv = _grads(lambda a, b, c: amd.attention.varlen_attention(a, b, c, cu), q, k, v, do)
+    print("varlen full size: packed pass done", flush=True)
+    for s0, n in zip(cu[:-1].tolist(), seg):
+        sl = slice(s0, s0 + n)
+        ro, rq, rk, rv = _grads(amd.attention.attention, q[:, :, sl], k[:, :, sl], v[:, :, sl], do[:, :, sl])
+        assert (out[:, :, sl].float() - ro.float()).abs().max().item() <= OUT_TOL
+        for got, ref in ((dq, rq), (dk, rk), (dv, rv)):
+            assert _max_rel(got[:, :, sl], ref) <= GRAD_REL_TOL
+        print(f"  segment [{s0}, {s0 + n}) ok", flush=True)
+    pad = slice(int(cu[-1]), L)
+    assert (out[:, :, pad] == 0).all() and (dq[:, :, pad] == 0).all()
+    assert (dk[:, :, pad] == 0).all() and (dv[:, :, pad] == 0).all()
+
+
+def test_temporal_window_full_latent_equals_frame_blocks(amd):
+    """The 21x45x80 latent at 8 fps (75,600 tokens, 40 heads x d128) with a
+    0.25 s temporal window: every query frame attends to the frames within
+    two of it, so each frame's output equals dense attention against that
+    block of frames (checked for the first, a middle and the last frames,
+    forward and dQ; dK/dV of the first frame's keys against the sum over the
+    query frames that see them)."""
+    H, D, F, T = 40, 128, 21, 3600
+    L = F * T
+    t = (torch.arange(L, device="cuda") // T).float() / 8.0
+    tq = t[None]
+    q, k, v = (_rand((1, H, L, D), s, 0.7) for s in (71, 72, 73))
+    do = _rand((1, H, L, D), 74, 1.0)
+
+    def windowed(a, b, c):
+        return amd.attention.temporal_neighbour_attention(a, b, c, tq, tq, window_seconds=0.25)
+
+    out, dq, dk, dv = _grads(windowed, q, k, v, do)
+    print("temporal full size: windowed pass done", flush=True)
+
+    def frames(f0, f1):
+        return slice(f0 * T, f1 * T)
+
+    for f in (0, 10, F - 1):
+        qs, ks = frames(f, f + 1), frames(max(f - 2, 0), min(f + 3, F))
+        ro, rq, _, _ = _grads(amd.attention.attention, q[:, :, qs], k[:, :, ks], v[:, :, ks], do[:, :, qs])
+        assert (out[:, :, qs].float() - ro.float()).abs().max().item() <= OUT_TOL
+        assert _max_rel(dq[:, :, qs], rq) <= GRAD_REL_TOL
+        print(f"  frame {f} ok", flush=True)
+    # keys of frame 0 are seen by query frames 0..2
+    ks = frames(0, 1)
+    gk = torch.zeros_like(dk[:, :, ks], dtype=torch.float32)
+    gv = torch.zeros_like(gk)
+    for f in range(3):
+        qs, kb = frames(f, f + 1), frames(max(f - 2, 0), min(f + 3, F))
+        _, _, rk, rv = _grads(amd.attention.attention, q[:, :, qs], k[:, :, kb], v[:, :, kb], do[:, :, qs])
+        gk += rk[:, :, :T].float()
+        gv += rv[:, :, :T].float()
+    assert _max_rel(dk[:, :, ks], gk) <= GRAD_REL_TOL
+    assert _max_rel(dv[:, :, ks], gv) <= GRAD_REL_TOL
