@@ -285,7 +285,9 @@ def _leading_count(pred, n: int, shape, device) -> torch.Tensor:
     for a predicate that is true then false along ``j`` (binary lifting over
     the powers of two; ``pred`` takes an int64 index tensor of ``shape``)."""
     pos = torch.zeros(shape, dtype=torch.int64, device=device)
-    step = 1 << max(n.bit_length() - 1, 0)
+    if n == 0:
+        return pos
+    step = 1 << (n.bit_length() - 1)
     while step >= 1:
         cand = pos + step
         ok = cand <= n

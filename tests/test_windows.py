@@ -100,6 +100,11 @@ def test_temporal_windows_at_rounding_boundaries():
     np.testing.assert_array_equal(wm, ref)
 
 
+def test_temporal_windows_without_keys_are_empty():
+    lo, hi = A.temporal_neighbour_windows(torch.zeros(2, 5), torch.zeros(2, 0), window_seconds=1.0)
+    assert lo.shape == (2, 5) and (lo == 0).all() and (hi == 0).all()
+
+
 def test_window_builders_validate():
     with pytest.raises(ValueError):
         A.temporal_neighbour_windows(torch.zeros(3), torch.zeros(1, 3), window_seconds=1.0)
