@@ -125,7 +125,6 @@ QkNormArgs qk_norm_args(const void* x, const int64_t* xs, int32_t batch, int32_t
   a.x = static_cast<const bf16*>(x);
   a.xsb = xs[0]; a.xsh = xs[1]; a.xsl = xs[2];
   a.B = batch; a.H = heads; a.L = len;
-  a.hfast = xs[1] < xs[2];
   a.w = static_cast<const bf16*>(weight);
   a.eps = eps;
   a.ct = cos_tab; a.st = sin_tab; a.tsb = tsb;

@@ -202,7 +202,6 @@ struct QkNormArgs {
   const bf16* x;
   int64_t xsb, xsh, xsl;
   int B, H, L;
-  bool hfast;        // visit rows head-fastest (set when the head stride is the smaller)
   const bf16* w;     // (head_dim) gain, or null for none
   float eps;
   const float* ct;   // rotation tables (b, 0, i, pair) at b*tsb + i*head_dim/2 + pair; null: no rotation

@@ -15,8 +15,8 @@
 //   dw   = sum over rows of g * xh            (fp32, per-block partials then
 //                                              one reduction: deterministic)
 // One row is D/8 lanes holding 16 bytes each, so every access is a full
-// 128-bit load or store; rows are visited in memory order (head fastest for
-// a (batch, seq, head, dim) layout, seq fastest otherwise).  HBM-bound: one
+// 128-bit load or store; a wave takes one token and its heads, so the
+// token's rotation tables are read once, not once per head.  HBM-bound: one
 // read and one write of the rows (two reads in the backward).
 #include "avattn_device.h"
 #include "avattn_kernels.h"
@@ -25,8 +25,8 @@ namespace avattn {
 
 namespace {
 
-constexpr int kNormThreads = 256;
-constexpr int kNormBwdBlocks = 1024;  // fixed grid of the backward: dW partials per block
+constexpr int kNormThreads = 64;      // one wave per token: D/8 lanes per head row, 64/(D/8) heads at a time
+constexpr int kNormBwdBlocks = 4096;  // fixed grid of the backward: dW partials per block
 
 __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 #pragma unroll
@@ -36,25 +36,6 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
   }
 }
 
-// Row u -> element offset of its first value for strides (sb, sh, sl).
-struct RowMap {
-  int H, L;
-  bool hfast;
-  __device__ __forceinline__ void split(int64_t u, int& b, int& h, int& i) const {
-    if (hfast) {
-      h = (int)(u % H);
-      const int64_t r = u / H;
-      i = (int)(r % L);
-      b = (int)(r / L);
-    } else {
-      i = (int)(u % L);
-      const int64_t r = u / L;
-      h = (int)(r % H);
-      b = (int)(r / H);
-    }
-  }
-};
-
 // Sum over the R lanes of one row (consecutive lanes, R a power of two).
 template <int R>
 __device__ __forceinline__ float row_sum(float v) {
@@ -63,45 +44,56 @@ __device__ __forceinline__ float row_sum(float v) {
   return v;
 }
 
+__device__ __forceinline__ void load_gain(const bf16* w, int c, float* out) {
+  if (w) {
+    unpack8(*reinterpret_cast<const u32x4*>(w + 8 * c), out);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = 1.f;
+  }
+}
+
 }  // namespace
 
+// Token-major: a wave takes token (b, i), loads this lane's 4 cos / 4 sin
+// values once, and normalises the token's rows head by head (64/(D/8)
+// heads per pass; for a (batch, seq, heads, dim) layout those rows are one
+// contiguous run).
 template <int D>
 __global__ __launch_bounds__(kNormThreads) void qk_norm_fwd_kernel(QkNormArgs a) {
 #pragma clang fp contract(off)
   constexpr int R = D / 8;
-  constexpr int RPB = kNormThreads / R;
-  const int c = threadIdx.x % R;
+  constexpr int HPW = kNormThreads / R;
+  const int c = threadIdx.x % R, hg = threadIdx.x / R;
   float w[8];
-  if (a.w) {
-    unpack8(*reinterpret_cast<const u32x4*>(a.w + 8 * c), w);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) w[j] = 1.f;
-  }
-  const RowMap map{a.H, a.L, a.hfast};
-  const int64_t nrows = (int64_t)a.B * a.H * a.L;
-  for (int64_t u = (int64_t)blockIdx.x * RPB + threadIdx.x / R; u < nrows; u += (int64_t)gridDim.x * RPB) {
-    int b, h, i;
-    map.split(u, b, h, i);
-    const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c);
-    float x[8];
-    unpack8(xv, x);
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
-    ss = row_sum<R>(ss);
-    const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
-    u32x4 n;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float t0 = x[2 * p] * rstd, t1 = x[2 * p + 1] * rstd;
-      n[p] = pack_bf16x2(t0 * w[2 * p], t1 * w[2 * p + 1]);
-    }
+  load_gain(a.w, c, w);
+  const int64_t ntok = (int64_t)a.B * a.L;
+  for (int64_t tok = blockIdx.x; tok < ntok; tok += gridDim.x) {
+    const int b = (int)(tok / a.L), i = (int)(tok % a.L);
+    f32x4 cs, sn;
     if (a.ct) {
       const int64_t t = b * a.tsb + (int64_t)i * (D / 2) + 4 * c;
-      n = rotate8(n, *reinterpret_cast<const f32x4*>(a.ct + t), *reinterpret_cast<const f32x4*>(a.st + t), false);
+      cs = *reinterpret_cast<const f32x4*>(a.ct + t);
+      sn = *reinterpret_cast<const f32x4*>(a.st + t);
     }
-    *reinterpret_cast<u32x4*>(a.out + b * a.osb + h * a.osh + (int64_t)i * a.osl + 8 * c) = n;
+    for (int h = hg; h < a.H; h += HPW) {  // uniform over the row's lanes
+      const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c);
+      float x[8];
+      unpack8(xv, x);
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+      ss = row_sum<R>(ss);
+      const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
+      u32x4 n;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float t0 = x[2 * p] * rstd, t1 = x[2 * p + 1] * rstd;
+        n[p] = pack_bf16x2(t0 * w[2 * p], t1 * w[2 * p + 1]);
+      }
+      if (a.ct) n = rotate8(n, cs, sn, false);
+      *reinterpret_cast<u32x4*>(a.out + b * a.osb + h * a.osh + (int64_t)i * a.osl + 8 * c) = n;
+    }
   }
 }
 
@@ -109,60 +101,57 @@ template <int D>
 __global__ __launch_bounds__(kNormThreads) void qk_norm_bwd_kernel(QkNormArgs a) {
 #pragma clang fp contract(off)
   constexpr int R = D / 8;
-  constexpr int RPB = kNormThreads / R;
-  __shared__ float red[RPB][D];
-  const int c = threadIdx.x % R;
+  constexpr int HPW = kNormThreads / R;
+  __shared__ float red[HPW][D];
+  const int c = threadIdx.x % R, hg = threadIdx.x / R;
   float w[8], dw[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) dw[j] = 0.f;
-  if (a.w) {
-    unpack8(*reinterpret_cast<const u32x4*>(a.w + 8 * c), w);
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) w[j] = 1.f;
-  }
-  const RowMap map{a.H, a.L, a.hfast};
-  const int64_t nrows = (int64_t)a.B * a.H * a.L;
-  for (int64_t u = (int64_t)blockIdx.x * RPB + threadIdx.x / R; u < nrows; u += (int64_t)gridDim.x * RPB) {
-    int b, h, i;
-    map.split(u, b, h, i);
-    float x[8], g[8];
-    unpack8(*reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c), x);
-    u32x4 gv = *reinterpret_cast<const u32x4*>(a.dy + b * a.dsb + h * a.dsh + (int64_t)i * a.dsl + 8 * c);
+  load_gain(a.w, c, w);
+  const int64_t ntok = (int64_t)a.B * a.L;
+  for (int64_t tok = blockIdx.x; tok < ntok; tok += gridDim.x) {
+    const int b = (int)(tok / a.L), i = (int)(tok % a.L);
+    f32x4 cs, sn;
     if (a.ct) {
       const int64_t t = b * a.tsb + (int64_t)i * (D / 2) + 4 * c;
-      gv = rotate8(gv, *reinterpret_cast<const f32x4*>(a.ct + t), *reinterpret_cast<const f32x4*>(a.st + t), true);
+      cs = *reinterpret_cast<const f32x4*>(a.ct + t);
+      sn = *reinterpret_cast<const f32x4*>(a.st + t);
     }
-    unpack8(gv, g);
-    float ss = 0.f;
+    for (int h = hg; h < a.H; h += HPW) {
+      float x[8], g[8];
+      unpack8(*reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c), x);
+      u32x4 gv = *reinterpret_cast<const u32x4*>(a.dy + b * a.dsb + h * a.dsh + (int64_t)i * a.dsl + 8 * c);
+      if (a.ct) gv = rotate8(gv, cs, sn, true);
+      unpack8(gv, g);
+      float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
-    ss = row_sum<R>(ss);
-    const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
-    float xh[8], wg[8], dot = 0.f;
+      for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
+      ss = row_sum<R>(ss);
+      const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
+      float xh[8], wg[8], dot = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      xh[j] = x[j] * rstd;
-      wg[j] = w[j] * g[j];
-      dot += wg[j] * xh[j];
-      dw[j] += g[j] * xh[j];
+      for (int j = 0; j < 8; ++j) {
+        xh[j] = x[j] * rstd;
+        wg[j] = w[j] * g[j];
+        dot += wg[j] * xh[j];
+        dw[j] += g[j] * xh[j];
+      }
+      const float m = row_sum<R>(dot) / (float)D;
+      u32x4 dx;
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        dx[p] = pack_bf16x2(rstd * (wg[2 * p] - xh[2 * p] * m), rstd * (wg[2 * p + 1] - xh[2 * p + 1] * m));
+      *reinterpret_cast<u32x4*>(a.dx + b * a.xgb + h * a.xgh + (int64_t)i * a.xgl + 8 * c) = dx;
     }
-    const float m = row_sum<R>(dot) / (float)D;
-    u32x4 dx;
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-      dx[p] = pack_bf16x2(rstd * (wg[2 * p] - xh[2 * p] * m), rstd * (wg[2 * p + 1] - xh[2 * p + 1] * m));
-    *reinterpret_cast<u32x4*>(a.dx + b * a.xgb + h * a.xgh + (int64_t)i * a.xgl + 8 * c) = dx;
   }
   if (!a.wpart) return;  // uniform: no gain, no dW
-  const int rg = threadIdx.x / R;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) red[rg][8 * c + j] = dw[j];
+  for (int j = 0; j < 8; ++j) red[hg][8 * c + j] = dw[j];
   __syncthreads();
-  if (threadIdx.x < D) {
+  for (int d = threadIdx.x; d < D; d += kNormThreads) {
     float s = 0.f;
-    for (int r = 0; r < RPB; ++r) s += red[r][threadIdx.x];
-    a.wpart[(int64_t)blockIdx.x * D + threadIdx.x] = s;
+    for (int r = 0; r < HPW; ++r) s += red[r][d];
+    a.wpart[(int64_t)blockIdx.x * D + d] = s;
   }
 }
 
@@ -196,17 +185,15 @@ hipError_t launch_qk_norm_dw_zero(float* dw, int D, hipStream_t stream) {
 
 size_t qk_norm_bwd_workspace_bytes(int D) { return (size_t)kNormBwdBlocks * D * sizeof(float); }
 
-static int norm_grid(int64_t rows, int D, int cap) {
-  const int64_t rpb = kNormThreads / (D / 8);
-  const int64_t blocks = (rows + rpb - 1) / rpb;
-  return (int)(blocks < 1 ? 1 : (blocks > cap ? cap : blocks));
+static int norm_grid(int64_t tokens, int cap) {
+  return (int)(tokens < 1 ? 1 : (tokens > cap ? cap : tokens));
 }
 
 hipError_t launch_qk_norm(const QkNormArgs& a, int D, hipStream_t stream) {
-  const int64_t rows = (int64_t)a.B * a.H * a.L;
-  if (rows == 0) return hipSuccess;
+  const int64_t tokens = (int64_t)a.B * a.L;
+  if (tokens == 0 || a.H == 0) return hipSuccess;
   LaunchTimer timer(kKidQkNorm, stream);
-  const dim3 grid(norm_grid(rows, D, 16384)), block(kNormThreads);
+  const dim3 grid(norm_grid(tokens, 1 << 20)), block(kNormThreads);
   if (D == 128)
     hipLaunchKernelGGL(qk_norm_fwd_kernel<128>, grid, block, 0, stream, a);
   else
@@ -215,9 +202,9 @@ hipError_t launch_qk_norm(const QkNormArgs& a, int D, hipStream_t stream) {
 }
 
 hipError_t launch_qk_norm_bwd(const QkNormArgs& a, int D, float* dw, hipStream_t stream) {
-  const int64_t rows = (int64_t)a.B * a.H * a.L;
-  if (rows == 0) return hipSuccess;
-  const int nb = norm_grid(rows, D, kNormBwdBlocks);
+  const int64_t tokens = (int64_t)a.B * a.L;
+  if (tokens == 0 || a.H == 0) return hipSuccess;
+  const int nb = norm_grid(tokens, kNormBwdBlocks);
   {
     LaunchTimer timer(kKidQkNormBwd, stream);
     if (D == 128)

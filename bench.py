@@ -468,7 +468,7 @@ def bench_qknorm(cfg: dict, steps: int, warmup: int) -> dict:
     backward, on c3's full sequence.  Algorithmic HBM bytes: forward reads x
     and writes y (4 B per element) plus the cos/sin tables (4 B per (token,
     dim)); backward reads x and dy and writes dx (6 B per element) plus the
-    tables; the dW partials (0.5 MB) are not counted."""
+    tables; the dW partials (2 MB) are not counted."""
     import avgen_amd
     from avgen_amd import _lib
 

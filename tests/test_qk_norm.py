@@ -94,7 +94,7 @@ def test_qk_norm_abi_validation():
     assert fwd(cos=16, sin=16, tsb=2) == _lib.ERR_LAYOUT
     assert fwd(os=_lib.i64_array([1 << 20, 128, 100])) == _lib.ERR_LAYOUT
     assert fwd(L=0) == _lib.OK
-    assert lib.avattn_qk_norm_rope_bwd_workspace_size(128) == 1024 * 128 * 4
+    assert lib.avattn_qk_norm_rope_bwd_workspace_size(128) == 4096 * 128 * 4
     assert lib.avattn_qk_norm_rope_bwd_workspace_size(96) == 0
 
     def bwd(ws=256, wsb=1 << 20, dw=16, w=16):
