@@ -83,6 +83,60 @@ def build() -> dict[str, dict[str, np.ndarray]]:
         "q_bits": R.bf16_bits(q), "k_bits": R.bf16_bits(k), "v_bits": R.bf16_bits(v),
         "out": o.astype(np.float32), "lse": lse, "merge01_out": mo, "merge01_lse": ml,
     }
+    # Packed variable-length sequences (segments 3/4/2 in 12, the reference's
+    # own test layout): block-diagonal mask and attention over it.
+    lengths, cap = [3, 4, 2], 12
+    pm = R.packed_attention_mask(lengths, cap)
+    q = _bf16(rng, (1, 2, cap, 64))
+    k = _bf16(rng, (1, 2, cap, 64))
+    v = _bf16(rng, (1, 2, cap, 64))
+    do = _bf16(rng, (1, 2, cap, 64))
+    o, lse = R.attention_f64(q, k, v, attn_mask=pm[None])
+    dq, dk, dv = R.attention_bwd_f64(do, q, k, v, o, lse, attn_mask=pm[None])
+    out["packed_attention"] = {
+        "lengths": np.array(lengths, np.int32), "capacity": np.int32(cap),
+        "segment_ids": R.packed_segment_ids(lengths, cap), "cu_seqlens": R.packed_cu_seqlens(lengths), "mask": pm,
+        "q_bits": R.bf16_bits(q), "k_bits": R.bf16_bits(k), "v_bits": R.bf16_bits(v), "do_bits": R.bf16_bits(do),
+        "out": o.astype(np.float32), "lse": lse, "dq": dq.astype(np.float32), "dk": dk.astype(np.float32),
+        "dv": dv.astype(np.float32),
+    }
+
+    # Temporal neighbour mask: video frames at 8 fps against audio tokens at
+    # 20 per second, window 0.1 s, a key mask, and queries past the audio
+    # (rows that fall back to every key).
+    tq = np.stack([np.repeat(np.arange(8, dtype=np.float32) / np.float32(8.0), 3)] * 2)
+    tk = np.stack([np.arange(12, dtype=np.float32) / np.float32(20.0)] * 2)
+    tk[1] += np.float32(0.05)
+    km = np.ones((2, 12), bool)
+    km[1, ::3] = False
+    tm = R.temporal_neighbour_mask(tq, tk, 0.1, km)
+    q = _bf16(rng, (2, 4, 24, 128))
+    k = _bf16(rng, (2, 2, 12, 128))
+    v = _bf16(rng, (2, 2, 12, 128))
+    o, lse = R.attention_f64(q, k, v, attn_mask=tm)
+    out["temporal_attention"] = {
+        "query_seconds": tq, "key_seconds": tk, "window_seconds": np.float64(0.1), "key_mask": km, "mask": tm,
+        "q_bits": R.bf16_bits(q), "k_bits": R.bf16_bits(k), "v_bits": R.bf16_bits(v),
+        "out": o.astype(np.float32), "lse": lse,
+    }
+
+    # QK RMSNorm + rotation on a (batch, seq, heads, dim) projection output.
+    c128, s128 = R.rotary_tables_f64(coords, 128)
+    c32, s32 = c128.astype(np.float32), s128.astype(np.float32)
+    L = coords.shape[1]
+    xp = _bf16(rng, (1, L, 3, 128), 3.0)
+    x = xp.transpose(0, 2, 1, 3)
+    w = R.bf16_round((rng.uniform(0.5, 1.5, 128)).astype(np.float32))
+    n = R.rms_norm_bf16(x, w, 1e-6)
+    y = R.apply_rotary_bf16(n, c32, s32)
+    dy = _bf16(rng, x.shape)
+    g = R.apply_rotary_bf16(dy, c32, s32, inverse=True)
+    dx, dw = R.rms_norm_bwd_f64(x, w, g, 1e-6)
+    out["qk_norm_rope_d128"] = {
+        "x_bits": R.bf16_bits(xp), "w_bits": R.bf16_bits(w), "cos": c32, "sin": s32, "eps": np.float64(1e-6),
+        "norm_bits": R.bf16_bits(n), "out_bits": R.bf16_bits(y), "dy_bits": R.bf16_bits(dy),
+        "dx": dx.astype(np.float32), "dw": dw,
+    }
     return out
 
 

@@ -12,7 +12,7 @@ import torch
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 NAMES = ["rope_tables_d12", "rope_tables_d128", "rope_tables_d128_ntk", "rope_apply_d64", "attn_d64", "attn_d128",
-         "ring_3chunks"]
+         "ring_3chunks", "packed_attention", "temporal_attention", "qk_norm_rope_d128"]
 
 
 def load(name: str) -> dict[str, np.ndarray]:
@@ -126,3 +126,51 @@ def test_gpu_ring_matches_golden(amd):
     amd.ops.lse_merge_(acc, acc_lse, b_out, b_lse)
     assert np.abs(acc.cpu().numpy() - o1.numpy()).max() <= 2e-2
     assert np.abs(acc_lse.cpu().numpy() - g["merge01_lse"]).max() <= 1e-3
+
+
+def test_packed_fixture_is_the_reference_layout():
+    """tests/test_data.py:640-667 of the reference: ids and cu_seqlens."""
+    g = load("packed_attention")
+    assert g["segment_ids"].tolist() == [0] * 3 + [1] * 4 + [2] * 2 + [-1] * 3
+    assert g["cu_seqlens"].tolist() == [0, 3, 7, 9]
+
+
+@pytest.mark.gpu
+def test_gpu_varlen_matches_golden(amd):
+    g = load("packed_attention")
+    q, k, v, do = (bits_to_bf16(g[f"{t}_bits"]).cuda().requires_grad_(t != "do") for t in ("q", "k", "v", "do"))
+    out = amd.attention.varlen_attention(q, k, v, torch.from_numpy(g["cu_seqlens"]))
+    assert np.abs(out.float().detach().cpu().numpy() - g["out"]).max() <= 2e-2
+    assert (out[:, :, 9:] == 0).all()
+    out.backward(do)
+    for t, key in ((q, "dq"), (k, "dk"), (v, "dv")):
+        ref = g[key]
+        assert np.abs(t.grad.float().cpu().numpy() - ref).max() <= 2e-2 * np.abs(ref).max(), key
+
+
+@pytest.mark.gpu
+def test_gpu_temporal_matches_golden(amd):
+    g = load("temporal_attention")
+    assert g["mask"][:, 0].all(axis=-1).any(), "the fixture has fallback rows"
+    q, k, v = (bits_to_bf16(g[f"{t}_bits"]).cuda() for t in "qkv")
+    out = amd.attention.temporal_neighbour_attention(
+        q, k, v, torch.from_numpy(g["query_seconds"]).cuda(), torch.from_numpy(g["key_seconds"]).cuda(),
+        window_seconds=float(g["window_seconds"]), key_mask=torch.from_numpy(g["key_mask"]).cuda(), enable_gqa=True)
+    assert np.abs(out.float().cpu().numpy() - g["out"]).max() <= 2e-2
+
+
+@pytest.mark.gpu
+def test_gpu_qk_norm_matches_golden(amd):
+    g = load("qk_norm_rope_d128")
+    xp = bits_to_bf16(g["x_bits"]).cuda()
+    x = amd.layers.split_heads(xp.flatten(2), 128).requires_grad_(True)
+    w = bits_to_bf16(g["w_bits"]).cuda()
+    cos, sin = torch.from_numpy(g["cos"]).cuda(), torch.from_numpy(g["sin"]).cuda()
+    y = amd.ops.qk_norm_rope(x, w, float(g["eps"]), cos, sin)
+    got = y.detach().float().cpu().numpy()
+    ref = bits_to_bf16(g["out_bits"]).float().numpy()
+    diff = np.abs(got - ref)
+    assert (diff <= np.abs(ref) * 2.0 ** -7 + 1e-6).all() and (diff > 0).mean() < 1e-3
+    dx, dw = amd.ops.qk_norm_rope_bwd(bits_to_bf16(g["dy_bits"]).cuda(), x.detach(), w, float(g["eps"]), cos, sin)
+    assert np.abs(dx.float().cpu().numpy() - g["dx"]).max() <= 2e-2 * np.abs(g["dx"]).max()
+    assert np.abs(dw.cpu().numpy() - g["dw"]).max() <= 1e-3 * np.abs(g["dw"]).max()

@@ -104,3 +104,35 @@ def test_qk_norm_abi_validation():
     assert bwd(dw=None) == _lib.ERR_NULL_POINTER
     assert bwd(ws=None) == _lib.ERR_WORKSPACE
     assert bwd(wsb=100) == _lib.ERR_WORKSPACE
+
+
+def test_self_attention_composition_oracle_matches_torch_cpu():
+    """src/avgen/models/layers.py:530-545 restated with torch CPU ops (split
+    heads, F.rms_norm with the bf16 gain, the reference's float32 rotation
+    chain, SDPA in float64, flatten) against the oracle's composition
+    (rms_norm_bf16 -> apply_rotary_bf16 -> attention_f64)."""
+    from oracle import torch_path as T
+
+    B, L, H, D = 1, 48, 2, 64
+    coords = torch.from_numpy(R.video_coords(2, 4, 6))
+    cos, sin = T.rotary_tables(coords, D)
+    qp, kp, vp = (_bf16((B, L, H * D), s) for s in (21, 22, 23))
+    wq = (torch.rand(D, generator=torch.Generator().manual_seed(24)) + 0.5).to(torch.bfloat16)
+    wk = (torch.rand(D, generator=torch.Generator().manual_seed(25)) + 0.5).to(torch.bfloat16)
+
+    def heads(t):
+        return t.unflatten(-1, (-1, D)).transpose(1, 2)
+
+    q = T.apply_rotary(F.rms_norm(heads(qp), (D,), wq, 1e-6), cos, sin)
+    k = T.apply_rotary(F.rms_norm(heads(kp), (D,), wk, 1e-6), cos, sin)
+    ref = F.scaled_dot_product_attention(q.double(), k.double(), heads(vp).double())
+    ref = ref.transpose(1, 2).flatten(2).numpy()
+
+    c, s = cos.numpy(), sin.numpy()
+    qn = R.apply_rotary_bf16(R.rms_norm_bf16(heads(qp).float().numpy(), wq.float().numpy()), c, s)
+    kn = R.apply_rotary_bf16(R.rms_norm_bf16(heads(kp).float().numpy(), wk.float().numpy()), c, s)
+    o, _ = R.attention_f64(qn, kn, heads(vp).float().numpy())
+    got = o.transpose(0, 2, 1, 3).reshape(B, L, H * D)
+    assert np.abs(got - ref).max() <= 1e-2
+    # exact where the normalised operands agree bit for bit
+    assert (qn == q.float().numpy()).mean() > 0.999 and (kn == k.float().numpy()).mean() > 0.999
