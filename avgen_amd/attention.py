@@ -29,6 +29,7 @@ windows directly.
 from __future__ import annotations
 
 from collections.abc import Sequence
+from dataclasses import dataclass
 from contextlib import AbstractContextManager, nullcontext
 from typing import Optional
 
@@ -47,7 +48,9 @@ __all__ = [
     "rotary_attention",
     "sdpa_context",
     "packed_windows",
+    "TemporalNeighbourhood",
     "temporal_neighbour_attention",
+    "temporal_neighbourhood",
     "temporal_neighbour_windows",
     "varlen_attention",
     "windowed_attention",
@@ -335,15 +338,97 @@ def _is_sorted_rows(t: torch.Tensor) -> torch.Tensor:
     return (t[:, 1:] >= t[:, :-1]).all() if t.shape[1] > 1 else torch.ones((), dtype=torch.bool, device=t.device)
 
 
-def temporal_neighbour_attention(
-    query: torch.Tensor,
-    key: torch.Tensor,
-    value: torch.Tensor,
+@dataclass(frozen=True)
+class TemporalNeighbourhood:
+    """The temporal neighbour mask of src/avgen/models/blocks.py:54-104 as
+    key windows, built once per forward (as the reference builds its dense
+    mask once, src/avgen/models/dit.py:927-942) and reused by every fusion
+    block without further host synchronisation.
+
+    ``lo``/``hi`` are int32 ``(batch, queries)`` over the time-sorted key
+    order; ``query_order``/``key_order`` (None when already sorted) permute
+    tokens into time order and ``query_inverse`` back; ``key_mask`` is the
+    key validity in sorted order; ``fallback`` lists, per batch row, the
+    (sorted) query rows with no admissible key, which attend to every key;
+    ``dense`` marks ``window_seconds <= 0`` (plain key-padding attention).
+    """
+
+    lo: torch.Tensor | None
+    hi: torch.Tensor | None
+    key_mask: torch.Tensor | None
+    query_order: torch.Tensor | None
+    query_inverse: torch.Tensor | None
+    key_order: torch.Tensor | None
+    fallback: tuple[tuple[int, torch.Tensor], ...]
+    dense: bool
+    len_q: int
+    len_k: int
+
+
+def temporal_neighbourhood(
     query_seconds: torch.Tensor,
     key_seconds: torch.Tensor,
     *,
     window_seconds: float,
     key_mask: torch.Tensor | None = None,
+) -> TemporalNeighbourhood:
+    """Build the :class:`TemporalNeighbourhood` of ``temporal_neighbour_mask(
+    query_seconds, key_seconds, window_seconds=..., key_mask=...)``
+    (src/avgen/models/blocks.py:54-104).  Two host synchronisations (the
+    sortedness test and the fallback rows), here once instead of per block."""
+    if query_seconds.ndim != 2 or key_seconds.ndim != 2 or query_seconds.shape[0] != key_seconds.shape[0]:
+        raise ValueError(
+            f"query_seconds/key_seconds must be (batch, queries)/(batch, keys); got "
+            f"{tuple(query_seconds.shape)} and {tuple(key_seconds.shape)}"
+        )
+    B, Lq = query_seconds.shape
+    Lk = key_seconds.shape[1]
+    dev = query_seconds.device
+    km = None if key_mask is None else key_mask.to(device=dev, dtype=torch.bool)
+    if km is not None and tuple(km.shape) != (B, Lk):
+        raise ValueError(f"key_mask must be (batch, keys)={(B, Lk)}; got {tuple(km.shape)}")
+    if window_seconds <= 0.0 or Lq == 0 or Lk == 0:
+        return TemporalNeighbourhood(None, None, km, None, None, None, (), True, Lq, Lk)
+    tq = query_seconds
+    tk = key_seconds.to(dev)
+    sorted_q, sorted_k = (bool(x) for x in torch.stack([_is_sorted_rows(tq), _is_sorted_rows(tk)]).tolist())
+    key_order = query_order = query_inverse = None
+    if not sorted_k:
+        key_order = torch.sort(tk, dim=1, stable=True).indices
+        tk = torch.gather(tk, 1, key_order)
+        km = None if km is None else torch.gather(km, 1, key_order)
+    if not sorted_q:
+        query_order = torch.sort(tq, dim=1, stable=True).indices
+        query_inverse = torch.argsort(query_order, dim=1)
+        tq = torch.gather(tq, 1, query_order)
+    lo, hi = temporal_neighbour_windows(tq, tk, window_seconds=window_seconds)
+    if km is None:
+        empty = hi == lo
+    else:
+        pre = torch.nn.functional.pad(km.to(torch.int32).cumsum(1), (1, 0))
+        empty = (torch.gather(pre, 1, hi.long()) - torch.gather(pre, 1, lo.long())) == 0
+    rows = empty.nonzero()
+    fallback = []
+    if rows.shape[0] > 0:
+        for b in rows[:, 0].unique().tolist():
+            fallback.append((b, rows[rows[:, 0] == b, 1]))
+    return TemporalNeighbourhood(lo, hi, km, query_order, query_inverse, key_order, tuple(fallback), False, Lq, Lk)
+
+
+def _gather_rows(x: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
+    return torch.gather(x, 2, order[:, None, :, None].expand(-1, x.shape[1], -1, x.shape[3]))
+
+
+def temporal_neighbour_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    query_seconds: torch.Tensor | None = None,
+    key_seconds: torch.Tensor | None = None,
+    *,
+    window_seconds: float | None = None,
+    key_mask: torch.Tensor | None = None,
+    neighbourhood: TemporalNeighbourhood | None = None,
     enable_gqa: bool = False,
 ) -> torch.Tensor:
     """``attention(query, key, value, attn_mask=temporal_neighbour_mask(
@@ -355,67 +440,48 @@ def temporal_neighbour_attention(
     Same semantics as the reference composition: a query attends to the valid
     keys within ``window_seconds`` of it; ``window_seconds <= 0`` is plain
     key-padding attention; a query with no admissible key attends to every
-    key, masked ones included (:101-103).  Coordinates are ``(batch, tokens)``
-    seconds.  Tokens in non-decreasing time order (how video and audio
-    streams are laid out) go straight to the windowed kernel; otherwise the
-    rows are permuted into time order first (attention is invariant under a
-    permutation of the keys and equivariant under one of the queries).
+    key, masked ones included (:101-103).  Pass either the coordinates
+    (``(batch, tokens)`` seconds) with ``window_seconds``/``key_mask``, or a
+    ``neighbourhood`` from :func:`temporal_neighbourhood` built once for
+    several calls (then this call does no host synchronisation).  Tokens out
+    of time order are permuted into it and back (attention is invariant
+    under a permutation of the keys and equivariant under one of the
+    queries).
     """
     if query.shape[-2] == 0 or key.shape[-2] == 0:
         return torch.zeros_like(query)
     _validate(query, key, value, 0.0, False, enable_gqa)
     B, Lq, Lk = query.shape[0], query.shape[-2], key.shape[-2]
-    if tuple(query_seconds.shape) != (B, Lq) or tuple(key_seconds.shape) != (B, Lk):
-        raise ValueError(
-            f"query_seconds must be {(B, Lq)} and key_seconds {(B, Lk)}; got "
-            f"{tuple(query_seconds.shape)} and {tuple(key_seconds.shape)}"
-        )
-    if key_mask is not None and tuple(key_mask.shape) != (B, Lk):
-        raise ValueError(f"key_mask must be (batch, keys)={(B, Lk)}; got {tuple(key_mask.shape)}")
+    nb = neighbourhood
+    if nb is None:
+        if query_seconds is None or key_seconds is None or window_seconds is None:
+            raise ValueError("pass query_seconds, key_seconds and window_seconds, or a neighbourhood")
+        if tuple(query_seconds.shape) != (B, Lq) or tuple(key_seconds.shape) != (B, Lk):
+            raise ValueError(
+                f"query_seconds must be {(B, Lq)} and key_seconds {(B, Lk)}; got "
+                f"{tuple(query_seconds.shape)} and {tuple(key_seconds.shape)}"
+            )
+        nb = temporal_neighbourhood(query_seconds.to(query.device), key_seconds.to(query.device),
+                                    window_seconds=window_seconds, key_mask=key_mask)
+    elif (nb.len_q, nb.len_k) != (Lq, Lk):
+        raise ValueError(f"neighbourhood was built for {(nb.len_q, nb.len_k)} tokens; got {(Lq, Lk)}")
     scale = ops.default_scale(query.shape[-1])
-    if window_seconds <= 0.0:
-        mask = None if key_mask is None else key_mask.to(device=query.device, dtype=torch.bool)
-        return ops.flash_fwd(query, key, value, mask, None, None, scale)[0]
-
-    dev = query.device
-    tq = query_seconds.to(dev)
-    tk = key_seconds.to(dev)
-    km = None if key_mask is None else key_mask.to(device=dev, dtype=torch.bool)
-    sorted_q, sorted_k = (bool(x) for x in torch.stack([_is_sorted_rows(tq), _is_sorted_rows(tk)]).tolist())
-    perm_q = None
-    if not sorted_k:
-        order = torch.sort(tk, dim=1, stable=True).indices
-        tk = torch.gather(tk, 1, order)
-        km = None if km is None else torch.gather(km, 1, order)
-        idx = order[:, None, :, None]
-        key = torch.gather(key, 2, idx.expand(-1, key.shape[1], -1, key.shape[3]))
-        value = torch.gather(value, 2, idx.expand(-1, value.shape[1], -1, value.shape[3]))
-    if not sorted_q:
-        perm_q = torch.sort(tq, dim=1, stable=True).indices
-        tq = torch.gather(tq, 1, perm_q)
-        query = torch.gather(query, 2, perm_q[:, None, :, None].expand(-1, query.shape[1], -1, query.shape[3]))
-
-    lo, hi = temporal_neighbour_windows(tq, tk, window_seconds=window_seconds)
-    out, _ = ops.flash_fwd_windowed(query, key, value, lo, hi, km, scale)
-
-    # Rows with no admissible key: every key, unmasked (the reference's
-    # ``mask | ~mask.any(-1)``).
-    if km is None:
-        fallback = hi == lo
-    else:
-        pre = torch.nn.functional.pad(km.to(torch.int32).cumsum(1), (1, 0))
-        fallback = (torch.gather(pre, 1, hi.long()) - torch.gather(pre, 1, lo.long())) == 0
-    rows = fallback.nonzero()
-    if rows.shape[0] > 0:
+    if nb.dense:
+        return ops.flash_fwd(query, key, value, nb.key_mask, None, None, scale)[0]
+    if nb.key_order is not None:
+        key = _gather_rows(key, nb.key_order)
+        value = _gather_rows(value, nb.key_order)
+    if nb.query_order is not None:
+        query = _gather_rows(query, nb.query_order)
+    out, _ = ops.flash_fwd_windowed(query, key, value, nb.lo, nb.hi, nb.key_mask, scale)
+    if nb.fallback:
         out = out.clone()
-        for b in rows[:, 0].unique().tolist():
-            r = rows[rows[:, 0] == b, 1]
+        for b, r in nb.fallback:
             qb = query[b:b + 1].index_select(2, r)
             ob, _ = ops.flash_fwd(qb, key[b:b + 1], value[b:b + 1], None, None, None, scale)
             out[b, :, r] = ob[0]
-    if perm_q is not None:
-        inv = torch.argsort(perm_q, dim=1)
-        out = torch.gather(out, 2, inv[:, None, :, None].expand(-1, out.shape[1], -1, out.shape[3]))
+    if nb.query_inverse is not None:
+        out = _gather_rows(out, nb.query_inverse)
     return out
 
 

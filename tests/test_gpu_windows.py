@@ -210,3 +210,28 @@ def test_temporal_neighbour_attention_matches_the_dense_mask(amd, order, masked)
     out.backward(do.cuda())
     rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, attn_mask=dense)
     _check_grads((q.grad, k.grad, v.grad), (rq, rk, rv))
+
+
+@pytest.mark.parametrize("order", ["sorted", "shuffled"])
+def test_neighbourhood_built_once_matches_per_call(amd, order):
+    """A TemporalNeighbourhood built once and reused (the reference builds its
+    fusion masks once per forward) gives the same bits as building it per
+    call, on two different q/k/v."""
+    B, H, D = 2, 2, 128
+    tq = np.stack([_times(480, 24.0, 48), _times(480, 24.0, 48, 0.05)])
+    tk = np.stack([_times(120, 43.0, 1), _times(120, 43.0, 1, 0.2)])
+    rng = np.random.default_rng(51)
+    km = rng.random((B, 120)) < 0.8
+    if order == "shuffled":
+        tq, tk = tq[:, rng.permutation(480)], tk[:, rng.permutation(120)]
+    tqc, tkc, kmc = (torch.from_numpy(a).cuda() for a in (tq, tk, km))
+    nb = amd.attention.temporal_neighbourhood(tqc, tkc, window_seconds=0.1, key_mask=kmc)
+    for seed in (1, 2):
+        q, k, v = _randn((B, H, 480, D), 10 * seed), _randn((B, H, 120, D), 10 * seed + 1), \
+            _randn((B, H, 120, D), 10 * seed + 2)
+        q, k, v = q.cuda(), k.cuda(), v.cuda()
+        a = amd.attention.temporal_neighbour_attention(q, k, v, neighbourhood=nb)
+        b = amd.attention.temporal_neighbour_attention(q, k, v, tqc, tkc, window_seconds=0.1, key_mask=kmc)
+        assert torch.equal(a, b)
+    ref, _ = R.attention_f64(_f64(q), _f64(k), _f64(v), attn_mask=R.temporal_neighbour_mask(tq, tk, 0.1, km))
+    assert np.abs(_f64(a) - ref).max() <= OUT_TOL

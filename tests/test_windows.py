@@ -110,3 +110,36 @@ def test_window_builders_validate():
         A.temporal_neighbour_windows(torch.zeros(3), torch.zeros(1, 3), window_seconds=1.0)
     with pytest.raises(ValueError):
         A.packed_windows(torch.zeros((2, 2), dtype=torch.int32), 4)
+
+
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_temporal_neighbourhood_reproduces_the_mask(shuffle):
+    """Host side of the build-once neighbourhood (CPU tensors): windows over
+    the time-sorted keys plus the fallback rows give back the reference mask
+    row by row, in the caller's token order."""
+    rng = np.random.default_rng(7)
+    tq = np.stack([_stream_times(90, 24.0, per_step=6), _stream_times(90, 24.0, 0.4, per_step=6)])
+    tk = np.stack([_stream_times(14, 20.0), _stream_times(14, 20.0, 0.1)])
+    km = rng.random((2, 14)) < 0.7
+    if shuffle:
+        tq = tq[:, rng.permutation(90)]
+        tk = tk[:, rng.permutation(14)]
+    nb = A.temporal_neighbourhood(torch.from_numpy(tq), torch.from_numpy(tk), window_seconds=0.1,
+                                  key_mask=torch.from_numpy(km))
+    assert (nb.query_order is not None) == shuffle and (nb.key_order is not None) == shuffle
+    ref = R.temporal_neighbour_mask(tq, tk, 0.1, km)[:, 0]
+    qo = np.arange(90)[None].repeat(2, 0) if nb.query_order is None else nb.query_order.numpy()
+    ko = np.arange(14)[None].repeat(2, 0) if nb.key_order is None else nb.key_order.numpy()
+    kms = np.take_along_axis(km, ko, 1)
+    win = _window_mask(nb.lo.numpy(), nb.hi.numpy(), 14) & kms[:, None, :]
+    fb = np.zeros((2, 90), bool)
+    for b, r in nb.fallback:
+        fb[b, r.numpy()] = True
+    assert fb.any(), "the case must have fallback rows"
+    for b in range(2):
+        for i in range(90):
+            row = ref[b, qo[b, i]][ko[b]]  # reference row in sorted key order
+            if fb[b, i]:
+                assert row.all()
+            else:
+                np.testing.assert_array_equal(win[b, i], row)
