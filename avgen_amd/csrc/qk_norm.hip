@@ -76,8 +76,13 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_fwd_kernel(QkNormArgs a)
       cs = *reinterpret_cast<const f32x4*>(a.ct + t);
       sn = *reinterpret_cast<const f32x4*>(a.st + t);
     }
+    // The next pass's row is loaded before this pass's arithmetic.
+    const bf16* xrow = a.x + b * a.xsb + (int64_t)i * a.xsl + 8 * c;
+    u32x4 xn{};
+    if (hg < a.H) xn = *reinterpret_cast<const u32x4*>(xrow + hg * a.xsh);
     for (int h = hg; h < a.H; h += HPW) {  // uniform over the row's lanes
-      const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c);
+      const u32x4 xv = xn;
+      if (h + HPW < a.H) xn = *reinterpret_cast<const u32x4*>(xrow + (h + HPW) * a.xsh);
       float x[8];
       unpack8(xv, x);
       float ss = 0.f;
@@ -117,10 +122,23 @@ __global__ __launch_bounds__(kNormThreads) void qk_norm_bwd_kernel(QkNormArgs a)
       cs = *reinterpret_cast<const f32x4*>(a.ct + t);
       sn = *reinterpret_cast<const f32x4*>(a.st + t);
     }
+    // The next pass's rows are loaded before this pass's arithmetic.
+    const bf16* xrow = a.x + b * a.xsb + (int64_t)i * a.xsl + 8 * c;
+    const bf16* grow = a.dy + b * a.dsb + (int64_t)i * a.dsl + 8 * c;
+    u32x4 xn{}, gn{};
+    if (hg < a.H) {
+      xn = *reinterpret_cast<const u32x4*>(xrow + hg * a.xsh);
+      gn = *reinterpret_cast<const u32x4*>(grow + hg * a.dsh);
+    }
     for (int h = hg; h < a.H; h += HPW) {
       float x[8], g[8];
-      unpack8(*reinterpret_cast<const u32x4*>(a.x + b * a.xsb + h * a.xsh + (int64_t)i * a.xsl + 8 * c), x);
-      u32x4 gv = *reinterpret_cast<const u32x4*>(a.dy + b * a.dsb + h * a.dsh + (int64_t)i * a.dsl + 8 * c);
+      const u32x4 xv = xn;
+      u32x4 gv = gn;
+      if (h + HPW < a.H) {
+        xn = *reinterpret_cast<const u32x4*>(xrow + (h + HPW) * a.xsh);
+        gn = *reinterpret_cast<const u32x4*>(grow + (h + HPW) * a.dsh);
+      }
+      unpack8(xv, x);
       if (a.ct) gv = rotate8(gv, cs, sn, true);
       unpack8(gv, g);
       float ss = 0.f;
