@@ -138,3 +138,27 @@ def test_self_attention_core_matches_oracle(amd, Hq, Hkv, masked):
     out.backward(_bf16((B, L, Hq * D), 16).cuda())
     for t in (qp, kp, vp, wq, wk):
         assert t.grad is not None and torch.isfinite(t.grad).all()
+
+
+@pytest.mark.parametrize("norm,rope", [(False, True), (False, False), (True, False)])
+def test_self_attention_core_variants(amd, norm, rope):
+    """qk_norm=False (no gains) and/or no rotary tables: the same composition
+    with those steps left out."""
+    B, H, D, grid = 1, 2, 64, (2, 4, 8)
+    L = grid[0] * grid[1] * grid[2]
+    qp, kp, vp = (_bf16((B, L, H * D), s).cuda() for s in (31, 32, 33))
+    w = (torch.rand(D, generator=torch.Generator().manual_seed(34)) + 0.5).cuda() if norm else None
+    tables = _tables(amd, B, grid, D) if rope else None
+    out = amd.layers.self_attention_core(qp, kp, vp, head_dim=D, q_norm_weight=w, k_norm_weight=w, rope=tables)
+
+    def prep(t):
+        x = _f(t).reshape(B, L, H, D).transpose(0, 2, 1, 3)
+        if norm:
+            x = R.rms_norm_bf16(x, _f(w), 1e-6)
+        if rope:
+            x = R.apply_rotary_bf16(x, _f(tables.cos), _f(tables.sin))
+        return x
+
+    ro, _ = R.attention_f64(prep(qp), prep(kp), _f(vp).reshape(B, L, H, D).transpose(0, 2, 1, 3))
+    ro = ro.transpose(0, 2, 1, 3).reshape(B, L, H * D)
+    assert np.abs(_f(out) - ro).max() <= 2e-2

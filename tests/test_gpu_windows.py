@@ -235,3 +235,21 @@ def test_neighbourhood_built_once_matches_per_call(amd, order):
         assert torch.equal(a, b)
     ref, _ = R.attention_f64(_f64(q), _f64(k), _f64(v), attn_mask=R.temporal_neighbour_mask(tq, tk, 0.1, km))
     assert np.abs(_f64(a) - ref).max() <= OUT_TOL
+
+
+def test_varlen_batch_of_packed_sequences(amd):
+    """Two packed rows sharing one layout (cu_seqlens applies to every batch
+    row), GQA, D=64."""
+    B, Hq, Hkv, D, cap = 2, 4, 2, 64, 300
+    lengths = [100, 57, 120]
+    q = _randn((B, Hq, cap, D), 81).cuda().requires_grad_(True)
+    k = _randn((B, Hkv, cap, D), 82).cuda().requires_grad_(True)
+    v = _randn((B, Hkv, cap, D), 83).cuda().requires_grad_(True)
+    do = _randn((B, Hq, cap, D), 84)
+    out = amd.attention.varlen_attention(q, k, v, torch.tensor(R.packed_cu_seqlens(lengths)), enable_gqa=True)
+    dense = R.packed_attention_mask(lengths, cap)[None]
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), attn_mask=dense)
+    assert np.abs(_f64(out) - ro).max() <= OUT_TOL
+    out.backward(do.cuda())
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, attn_mask=dense)
+    _check_grads((q.grad, k.grad, v.grad), (rq, rk, rv))
