@@ -473,7 +473,7 @@ def temporal_neighbour_attention(
         value = _gather_rows(value, nb.key_order)
     if nb.query_order is not None:
         query = _gather_rows(query, nb.query_order)
-    out, _ = ops.flash_fwd_windowed(query, key, value, nb.lo, nb.hi, nb.key_mask, scale)
+    out, _ = ops.flash_fwd_windowed(query, key, value, nb.lo, nb.hi, nb.key_mask, scale, True)
     if nb.fallback:
         out = out.clone()
         for b, r in nb.fallback:
@@ -527,5 +527,7 @@ def varlen_attention(
             f"varlen_attention: cu_seqlens ends at {int(cu_seqlens[-1])}, past the packed length "
             f"{query.shape[-2]}"
         )
+    _validate(query, key, value, 0.0, False, enable_gqa)
     lo, hi = packed_windows(cu_seqlens, query.shape[-2], device=query.device)
-    return windowed_attention(query, key, value, lo, hi, enable_gqa=enable_gqa)
+    out, _ = ops.flash_fwd_windowed(query, key, value, lo, hi, None, ops.default_scale(query.shape[-1]), True)
+    return out

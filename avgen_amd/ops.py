@@ -230,16 +230,18 @@ def _fwd_windowed_impl(q, k, v, window_lo, window_hi, key_mask, scale):
     return out, lse
 
 
-def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale):
-    """Backward of _fwd_windowed_impl (windows non-decreasing in the row;
-    always with staged dS, in passes if one pass does not fit the budget)."""
+def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale, check_monotone=True):
+    """Backward of _fwd_windowed_impl (windows non-decreasing in the row,
+    verified with one host synchronisation unless ``check_monotone`` is
+    False; always with staged dS, in passes if one pass does not fit the
+    budget)."""
     name = "avgen_amd.flash_bwd_windowed"
     _check_qkv(name, q, k, v)
     _require_gpu(name, dout, q, k, v, out, lse, key_mask, window_lo, window_hi)
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     lo, hi, wsb = _check_windows(name, window_lo, window_hi, B, Lq)
-    if Lq > 1 and bool(((lo[..., 1:] < lo[..., :-1]) | (hi[..., 1:] < hi[..., :-1])).any()):
+    if check_monotone and Lq > 1 and bool(((lo[..., 1:] < lo[..., :-1]) | (hi[..., 1:] < hi[..., :-1])).any()):
         raise ValueError(f"{name}: the backward needs window_lo and window_hi non-decreasing along the queries")
     dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
     lse = lse.contiguous()
@@ -613,13 +615,16 @@ def flash_fwd_windowed(
     window_hi: torch.Tensor,
     key_mask: Optional[torch.Tensor],
     scale: float,
+    monotone: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Forward where query row i attends keys [window_lo[i], window_hi[i]) only."""
+    """Forward where query row i attends keys [window_lo[i], window_hi[i]) only.
+    ``monotone``: the caller guarantees both bounds non-decreasing in the row
+    (its backward then skips the check and its host synchronisation)."""
     return _fwd_windowed_impl(q, k, v, window_lo, window_hi, key_mask, scale)
 
 
 @flash_fwd_windowed.register_fake
-def _(q, k, v, window_lo, window_hi, key_mask, scale):
+def _(q, k, v, window_lo, window_hi, key_mask, scale, monotone=False):
     return torch.empty_like(q), q.new_empty((q.shape[0], q.shape[1], q.shape[2]), dtype=torch.float32)
 
 
@@ -635,28 +640,33 @@ def flash_bwd_windowed(
     window_hi: torch.Tensor,
     key_mask: Optional[torch.Tensor],
     scale: float,
+    monotone: bool = False,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Backward of ``flash_fwd_windowed`` (windows non-decreasing in the row)."""
-    return _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale)
+    """Backward of ``flash_fwd_windowed`` (windows non-decreasing in the row;
+    checked unless ``monotone``)."""
+    return _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale,
+                              check_monotone=not monotone)
 
 
 @flash_bwd_windowed.register_fake
-def _(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale):
+def _(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale, monotone=False):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _fwd_windowed_setup(ctx, inputs, output):
-    q, k, v, window_lo, window_hi, key_mask, scale = inputs
+    q, k, v, window_lo, window_hi, key_mask, scale, monotone = inputs
     out, lse = output
     ctx.scale = scale
+    ctx.monotone = monotone
     ctx.save_for_backward(q, k, v, out, lse, window_lo, window_hi, key_mask)
     ctx.mark_non_differentiable(lse)
 
 
 def _fwd_windowed_backward(ctx, dout, _dlse):
     q, k, v, out, lse, window_lo, window_hi, key_mask = ctx.saved_tensors
-    dq, dk, dv = flash_bwd_windowed(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, ctx.scale)
-    return dq, dk, dv, None, None, None, None
+    dq, dk, dv = flash_bwd_windowed(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, ctx.scale,
+                                    ctx.monotone)
+    return dq, dk, dv, None, None, None, None, None
 
 
 torch.library.register_autograd(
