@@ -143,3 +143,31 @@ def test_temporal_neighbourhood_reproduces_the_mask(shuffle):
                 assert row.all()
             else:
                 np.testing.assert_array_equal(win[b, i], row)
+
+
+def test_oracle_dense_mask_attention_matches_torch_sdpa():
+    """attention_f64 / attention_bwd_f64 with a query-dependent boolean mask
+    against torch's float64 SDPA and autograd with the same mask (rows with
+    no admitted key excluded: SDPA returns NaN there, the oracle 0 / -inf)."""
+    import torch.nn.functional as F
+
+    rng = np.random.default_rng(11)
+    B, H, Lq, Lk, D = 2, 2, 19, 23, 16
+    q, k, v, do = (rng.standard_normal(s) for s in ((B, H, Lq, D), (B, H, Lk, D), (B, H, Lk, D), (B, H, Lq, D)))
+    m = rng.random((B, 1, Lq, Lk)) < 0.4
+    m[0, 0, 3] = False  # one row with no key
+    km = rng.random((B, Lk)) < 0.9
+    full = m & km[:, None, None, :]
+    o, lse = R.attention_f64(q, k, v, km, attn_mask=m)
+    tq, tk, tv = (torch.tensor(a, requires_grad=True) for a in (q, k, v))
+    ref = F.scaled_dot_product_attention(tq, tk, tv, attn_mask=torch.from_numpy(full))
+    ok = full.any(-1)[:, 0]  # (B, Lq)
+    np.testing.assert_allclose(o.transpose(0, 2, 1, 3)[ok], ref.detach().numpy().transpose(0, 2, 1, 3)[ok],
+                               rtol=1e-10, atol=1e-12)
+    assert (o[0, :, 3] == 0).all() and np.isneginf(lse[0, :, 3]).all()
+    g = np.where(ok[:, None, :, None], do, 0.0)
+    ref.backward(torch.from_numpy(np.where(ok[:, None, :, None], do, 0.0)))
+    dq, dk, dv = R.attention_bwd_f64(g, q, k, v, o, lse, km, attn_mask=m)
+    for got, want in ((dq, tq.grad), (dk, tk.grad), (dv, tv.grad)):
+        w = np.nan_to_num(want.numpy())
+        np.testing.assert_allclose(got, w, rtol=1e-9, atol=1e-11)
