@@ -133,8 +133,10 @@ class SDPAMerger:
         self._out_dtype = out.dtype
         self._lse_dtype = lse.dtype
         if self._out is None:
-            self._out = out.to(torch.float32, memory_format=torch.contiguous_format).clone()
-            self._lse = lse.to(torch.float32).contiguous().clone()
+            # One copy (a dtype change alone already copies; copy=True covers
+            # inputs that are fp32 and contiguous already).
+            self._out = out.to(torch.float32, memory_format=torch.contiguous_format, copy=True)
+            self._lse = lse.to(torch.float32, memory_format=torch.contiguous_format, copy=True)
             return
         ops.lse_merge_(self._out, self._lse, out, lse.to(torch.float32))
 
