@@ -96,6 +96,38 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.c_uint32,
          c_ptr],
     ),
+    "avattn_ring_fwd_step": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_ptr,
+         c_ptr, c_i64p,
+         ctypes.c_uint32,
+         c_ptr, c_size,
+         c_ptr],
+    ),
+    "avattn_ring_bwd_step": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_i64p, c_i64p, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
+         c_ptr, c_size,
+         ctypes.c_uint32,
+         c_ptr],
+    ),
+    "avattn_ring_dq_finish": (
+        ctypes.c_int,
+        [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_ptr, c_i64, c_ptr, c_i64p, c_ptr],
+    ),
     "avattn_lse_merge": (ctypes.c_int, [c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i32, c_i32, c_ptr]),
     "avattn_rope_tables": (
         ctypes.c_int,
@@ -143,6 +175,10 @@ BWD_REUSE_QUERY_SIDE = 1
 BWD_DQ_ACCUMULATE_F32 = 2
 BWD_STAGE_DS = 4
 BWD_DEFER_DQ = 8
+
+# avattn_ring_fwd_step flags (include/avattn.h).
+RING_FIRST = 1
+RING_LAST = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -214,6 +250,7 @@ KERNEL_IDS = {
     "bwd_dq_ds": 10,
     "qk_norm": 11,
     "qk_norm_bwd": 12,
+    "ring_dq_finish": 13,
 }
 
 

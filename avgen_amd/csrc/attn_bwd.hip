@@ -143,16 +143,26 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   bool kvalid = key < a.Lk;
   if (MASK && kvalid) kvalid = a.mask[b * a.msb + key] != 0;
 
-  // This wave's B operand: K (P waves) or V (dS waves) of the lane's key,
-  // zeros past the end.
+  // This wave's B operand: K (P waves, rotated when the backward carries the
+  // key's rotation) or V (dS waves) of the lane's key, read once from the
+  // caller's tensors; zeros past the end.
   bf16x8 kv[KS];
   {
     const bool in = key < a.Lk;
-    const bf16* src = (role == 0 ? a.kr : a.vr) + ((int64_t)bhk * a.Lkp + key) * D + 8 * hh;
+    const bf16* src = role == 0 ? a.k + b * a.ksb + hk * a.ksh + (int64_t)key * a.ksl + 8 * hh
+                                : a.v + b * a.vsb + hk * a.vsh + (int64_t)key * a.vsl + 8 * hh;
+    const bool rot = role == 0 && a.cos_k != nullptr;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 x = {0u, 0u, 0u, 0u};
-      if (in) x = *reinterpret_cast<const u32x4*>(src + 16 * ks);
+      if (in) {
+        x = *reinterpret_cast<const u32x4*>(src + 16 * ks);
+        if (rot) {
+          const int64_t t = b * a.rksb + (int64_t)key * (D / 2) + 8 * ks + 4 * hh;
+          x = rotate8(x, *reinterpret_cast<const f32x4*>(a.cos_k + t), *reinterpret_cast<const f32x4*>(a.sin_k + t),
+                      false);
+        }
+      }
       kv[ks] = bits_to_bf16x8(x);
     }
   }
@@ -581,6 +591,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     const float sc = role == 0 ? 1.f : a.scale;
     bf16* op = role == 0 ? a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl
                          : a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl;
+    // dk of an unrotated key: the rotated key's gradient rounded to bf16,
+    // then the transposed rotation (what the reference's autograd does
+    // through src/avgen/models/rope.py:332-338).
+    const bool rot = role == 1 && a.cos_k != nullptr;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -589,6 +603,13 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
         if (kvalid) {
           w[0] = pack_bf16x2(acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc);
           w[1] = pack_bf16x2(acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc);
+          if (rot) {
+            // channels dt*32 + 8g + 4hh .. +3: pairs (that)/2 and +1
+            const int64_t t = b * a.rksb + (int64_t)key * (D / 2) + 16 * dt + 4 * g + 2 * hh;
+            const f32x2 c2 = *reinterpret_cast<const f32x2*>(a.cos_k + t);
+            const f32x2 s2 = *reinterpret_cast<const f32x2*>(a.sin_k + t);
+            w = rotate4(w, c2[0], s2[0], c2[1], s2[1], true);
+          }
         }
         *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
       }
@@ -663,6 +684,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
       if (qvalid) {
         x = *reinterpret_cast<const u32x4*>(qp + 16 * ks);
         y = *reinterpret_cast<const u32x4*>(dp + 16 * ks);
+        if (a.cos_q) {
+          const int64_t t = b * a.rqsb + (int64_t)qrow * (D / 2) + 8 * ks + 4 * hh;
+          x = rotate8(x, *reinterpret_cast<const f32x4*>(a.cos_q + t), *reinterpret_cast<const f32x4*>(a.sin_q + t),
+                      false);
+        }
       }
       qf[ks] = bits_to_bf16x8(x);
       df[ks] = bits_to_bf16x8(y);
@@ -1133,12 +1159,20 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
     LaunchTimer timer(kKidTranspose, stream);
     hipError_t e = hipSuccess;
     if (!a.reuse_q) {
-      e = launch_prep_copies(a.q, a.qsb, a.qsh, a.qsl, a.B, a.Hq, a.Lq, D, a.qr, a.qt, stream);
+      e = launch_prep_copies(a.q, a.qsb, a.qsh, a.qsl, a.B, a.Hq, a.Lq, D, a.qr, a.qt, stream, nullptr, a.cos_q,
+                             a.sin_q, a.rqsb);
       if (e == hipSuccess)
         e = launch_prep_copies(a.dout, a.dosb, a.dosh, a.dosl, a.B, a.Hq, a.Lq, D, a.dor, a.dot, stream);
     }
-    if (e == hipSuccess) e = launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, a.kt, stream);
-    if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, a.vr, nullptr, stream);
+    // The dK/dV kernel reads its own key rows from k and v; the row-major
+    // copies serve only the recomputing dQ kernel (no staged dS), the
+    // head_dim-major k copy both dQ kernels.
+    const bool rows = a.ds == nullptr;
+    if (e == hipSuccess)
+      e = launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, rows ? a.kr : nullptr, a.kt, stream,
+                             nullptr, a.cos_k, a.sin_k, a.rksb);
+    if (e == hipSuccess && rows)
+      e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, a.vr, nullptr, stream);
     if (e == hipSuccess) e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
     if (e != hipSuccess) return e;
   }

@@ -502,23 +502,59 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   __builtin_amdgcn_s_setprio(0);
   wait_vmem();  // the last (re-staged) tile loads
 
+  // Three row states: l_tot > 0; l_tot == 0, no valid key (out 0 as SDPA
+  // returns, lse -inf); NaN, a NaN (or +inf) score reached the row (out and
+  // lse NaN, as the softmax of such a row gives).
   const float l_tot = halves_sum(l_run0 + l_run1);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float nan = __builtin_nanf("");
+  const float inv = l_tot > 0.f ? 1.f / l_tot : (l_tot == 0.f ? 0.f : nan);
+  const float lse = l_tot > 0.f ? fmaf(m_run, sc, logf(l_tot)) : (l_tot == 0.f ? kNegInf : nan);
   if (qvalid) {
-    if (hh == 0) {
-      const float lse = l_tot > 0.f ? fmaf(m_run, sc, logf(l_tot)) : kNegInf;
-      a.lse[(int64_t)bh * a.Lq + qrow] = lse;
-    }
     bf16* op = a.o + b * a.osb + h * a.osh + (int64_t)qrow * a.osl;
+    if (a.o_acc == nullptr) {
+      if (hh == 0) a.lse[(int64_t)bh * a.Lq + qrow] = lse;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        u32x2 w;
-        w[0] = pack_bf16x2(acc[dt][4 * g] * inv, acc[dt][4 * g + 1] * inv);
-        w[1] = pack_bf16x2(acc[dt][4 * g + 2] * inv, acc[dt][4 * g + 3] * inv);
-        *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
-      }
+        for (int g = 0; g < 4; ++g) {
+          u32x2 w;
+          w[0] = pack_bf16x2(acc[dt][4 * g] * inv, acc[dt][4 * g + 1] * inv);
+          w[1] = pack_bf16x2(acc[dt][4 * g + 2] * inv, acc[dt][4 * g + 3] * inv);
+          *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
+        }
+    } else {
+      // Ring step: merge this chunk's bf16-rounded output and lse into the
+      // fp32 accumulator, exactly as lse_merge_kernel would merge them
+      // (torch/.../_context_parallel/_attention.py:182-183).
+      const int64_t row = (int64_t)bh * a.Lq + qrow;
+      float* accp = a.o_acc + row * D;
+      int mode = 1;
+      float w = 1.f;
+      float nl = lse;
+      if (!a.acc_first) nl = lse_merge_coeffs(a.lse_acc[row], lse, mode, w);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ch = dt * 32 + 8 * g + 4 * hh;
+          const u32x2 ob = {pack_bf16x2(acc[dt][4 * g] * inv, acc[dt][4 * g + 1] * inv),
+                            pack_bf16x2(acc[dt][4 * g + 2] * inv, acc[dt][4 * g + 3] * inv)};
+          f32x4 m = {bf16_lo(ob[0]), bf16_hi(ob[0]), bf16_lo(ob[1]), bf16_hi(ob[1])};
+          if (mode != 1) {
+            const f32x4 prev = *reinterpret_cast<const f32x4*>(accp + ch);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) m[r] = lse_merge_elem(prev[r], m[r], mode, w);
+          }
+          *reinterpret_cast<f32x4*>(accp + ch) = m;
+          if (a.acc_final) {
+            const u32x2 fo = {pack_bf16x2(m[0], m[1]), pack_bf16x2(m[2], m[3])};
+            *reinterpret_cast<u32x2*>(op + ch) = fo;
+          }
+        }
+      // Both lanes of the row read lse_acc above (one wave, program order)
+      // before this write.
+      if (hh == 0) a.lse_acc[row] = nl;
+    }
   }
 }
 
@@ -546,7 +582,8 @@ static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
     hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
     if (e == hipSuccess)
       e = fp8 ? launch_quantize_rows(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.k_scale, a.k8, stream)
-              : launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream, a.kmax2);
+              : launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream, a.kmax2,
+                                   a.cos_k, a.sin_k, a.rksb);
     if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, nullptr, a.vt, stream);
     if (e != hipSuccess) return e;
   }

@@ -30,12 +30,40 @@ int check_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32
   const int64_t ktiles = ((int64_t)Lk + 127) / 128;
   if (qtiles * B * Hq > kMaxI32 || ktiles * B * Hkv > kMaxI32) return AVATTN_ERR_TOO_LARGE;
   if ((int64_t)B * Hq * Lq > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
+  // The kernels address one (batch, head) slice of a padded copy (and, in the
+  // backward, the query heads of one group) through 32-bit buffer ranges:
+  // group * Lqp * D and Lkp * D bf16 must stay below 2^32 bytes.
+  const int64_t Lqp = transpose_padded_len(Lq), Lkp = transpose_padded_len(Lk);
+  const int64_t lim = (int64_t)1 << 32;
+  if ((int64_t)(Hq / Hkv) * Lqp * D * 2 >= lim || Lkp * D * 2 >= lim) return AVATTN_ERR_TOO_LARGE;
   return AVATTN_OK;
 }
 
 int launch_status(hipError_t e) { return e == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH; }
 
 size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Fused ring-step extras (avattn_ring_fwd_step / avattn_ring_bwd_step).
+struct RingOpts {
+  const float* cos_q = nullptr;  // RoPE of the (unrotated) query shard
+  const float* sin_q = nullptr;
+  int64_t rqsb = 0;
+  const float* cos_k = nullptr;  // RoPE of the (unrotated) key chunk
+  const float* sin_k = nullptr;
+  int64_t rksb = 0;
+  float* o_acc = nullptr;  // forward: running fp32 merge
+  float* lse_acc = nullptr;
+  bool first = false, last = false;
+};
+
+// Rotation tables: both or neither, 16-byte aligned, batch stride a multiple
+// of 4 floats.
+int check_tables(const float* c, const float* s, int64_t batch_stride) {
+  if (!c && !s) return AVATTN_OK;
+  if (!c || !s) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(c) || !aligned16(s) || batch_stride % 4 != 0 || batch_stride < 0) return AVATTN_ERR_LAYOUT;
+  return AVATTN_OK;
+}
 
 // Key bias (B, Lkp) floats and per-32-key-tile flags (B, Lkp/32) ints, each
 // with a 64-entry tail pad (tile loads read 64 entries from a tile start).
@@ -158,7 +186,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 7; }
+int avattn_abi_version(void) { return 8; }
 
 }  // extern "C"
 
@@ -171,7 +199,8 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
              const float* rope_cos_q, const float* rope_sin_q, int64_t rope_batch_stride, bool fp8,
              const float* q_scale, const float* k_scale, float scale, void* out, const int64_t* out_strides,
              float* lse, void* workspace, size_t workspace_bytes, avattn_stream_t stream,
-             const int32_t* window_lo = nullptr, const int32_t* window_hi = nullptr, int64_t window_batch_stride = 0) {
+             const int32_t* window_lo = nullptr, const int32_t* window_hi = nullptr, int64_t window_batch_stride = 0,
+             const RingOpts* ring = nullptr) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (st != AVATTN_OK) return st;
   if (!q_strides || !k_strides || !v_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
@@ -199,7 +228,7 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
   const FwdWorkspace wl = fwd_workspace(batch, heads_kv, len_k, head_dim, fp8);
   if (!workspace || workspace_bytes < wl.total || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
-  FwdArgs a;
+  FwdArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k = static_cast<const bf16*>(k);
   a.v = static_cast<const bf16*>(v);
@@ -230,6 +259,15 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
   a.wlo = window_lo;
   a.whi = window_hi;
   a.wsb = window_batch_stride;
+  if (ring) {
+    a.cos_k = ring->cos_k;
+    a.sin_k = ring->sin_k;
+    a.rksb = ring->rksb;
+    a.o_acc = ring->o_acc;
+    a.lse_acc = ring->lse_acc;
+    a.acc_first = ring->first;
+    a.acc_final = ring->last;
+  }
   return launch_status(launch_fwd(a, head_dim, s));
 }
 
@@ -321,7 +359,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
                     int64_t key_mask_batch_stride, float scale, void* dq, const int64_t* dq_strides, void* dk,
                     const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
                     size_t workspace_bytes, uint32_t flags, avattn_stream_t stream, const int32_t* window_lo,
-                    const int32_t* window_hi, int64_t window_batch_stride) {
+                    const int32_t* window_hi, int64_t window_batch_stride, const RingOpts* ring = nullptr) {
   int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32 | AVATTN_BWD_STAGE_DS |
                 AVATTN_BWD_DEFER_DQ))
@@ -370,7 +408,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
   const BwdWorkspace wl = bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (!workspace || workspace_bytes < wl.total || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
-  BwdArgs a;
+  BwdArgs a{};
   a.dout = static_cast<const bf16*>(dout);
   a.q = static_cast<const bf16*>(q);
   a.k = static_cast<const bf16*>(k);
@@ -416,6 +454,14 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
   a.wlo = window_lo;
   a.whi = window_hi;
   a.wsb = window_batch_stride;
+  if (ring) {
+    a.cos_q = ring->cos_q;
+    a.sin_q = ring->sin_q;
+    a.rqsb = ring->rqsb;
+    a.cos_k = ring->cos_k;
+    a.sin_k = ring->sin_k;
+    a.rksb = ring->rksb;
+  }
   int kv_per_pass = 0;
   if (flags & AVATTN_BWD_STAGE_DS) {
     const size_t off = staged_ds_offset(wl);
@@ -594,6 +640,96 @@ int avattn_qk_norm_rope_bwd(const void* x, const int64_t* x_strides, const void*
   a.xgb = dx_strides[0]; a.xgh = dx_strides[1]; a.xgl = dx_strides[2];
   a.wpart = weight ? static_cast<float*>(workspace) : nullptr;
   return launch_status(launch_qk_norm_bwd(a, head_dim, dweight, reinterpret_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Fused ring steps
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int avattn_ring_fwd_step(const void* q, const void* k, const void* v, const int64_t* q_strides,
+                         const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
+                         int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                         int64_t key_mask_batch_stride, const float* rope_cos_q, const float* rope_sin_q,
+                         int64_t rope_q_batch_stride, const float* rope_cos_k, const float* rope_sin_k,
+                         int64_t rope_k_batch_stride, float scale, float* out_acc, float* lse_acc, void* out,
+                         const int64_t* out_strides, uint32_t flags, void* workspace, size_t workspace_bytes,
+                         avattn_stream_t stream) {
+  if (flags & ~(AVATTN_RING_FIRST | AVATTN_RING_LAST)) return AVATTN_ERR_ARGUMENT;
+  int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  if ((int64_t)batch * heads_q * len_q == 0) return AVATTN_OK;
+  if (len_k == 0) return AVATTN_ERR_BAD_SHAPE;  // a ring chunk holds at least one key
+  if (!out_acc || !lse_acc) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(out_acc) || (reinterpret_cast<uintptr_t>(lse_acc) & 3u)) return AVATTN_ERR_LAYOUT;
+  st = check_tables(rope_cos_q, rope_sin_q, rope_q_batch_stride);
+  if (st == AVATTN_OK) st = check_tables(rope_cos_k, rope_sin_k, rope_k_batch_stride);
+  if (st != AVATTN_OK) return st;
+  // Without AVATTN_RING_LAST the bf16 output is not written: out may be
+  // NULL; fwd_impl's layout checks then run on the accumulator instead.
+  const bool last = (flags & AVATTN_RING_LAST) != 0;
+  if (last && (!out || !out_strides)) return AVATTN_ERR_NULL_POINTER;
+  static const int64_t kNoStrides[3] = {0, 0, 0};
+  RingOpts ring;
+  ring.cos_k = rope_cos_k;
+  ring.sin_k = rope_sin_k;
+  ring.rksb = rope_k_batch_stride;
+  ring.o_acc = out_acc;
+  ring.lse_acc = lse_acc;
+  ring.first = (flags & AVATTN_RING_FIRST) != 0;
+  ring.last = last;
+  return fwd_impl(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
+                  key_mask, key_mask_batch_stride, rope_cos_q, rope_sin_q, rope_q_batch_stride, false, nullptr,
+                  nullptr, scale, last ? out : out_acc, last ? out_strides : kNoStrides, lse_acc, workspace,
+                  workspace_bytes, stream, nullptr, nullptr, 0, &ring);
+}
+
+int avattn_ring_bwd_step(const void* dout, const void* q, const void* k, const void* v, const void* out,
+                         const float* lse, const int64_t* dout_strides, const int64_t* q_strides,
+                         const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                         int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
+                         int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                         const float* rope_cos_q, const float* rope_sin_q, int64_t rope_q_batch_stride,
+                         const float* rope_cos_k, const float* rope_sin_k, int64_t rope_k_batch_stride, float scale,
+                         float* dq_acc, const int64_t* dq_acc_strides, void* dk, const int64_t* dk_strides, void* dv,
+                         const int64_t* dv_strides, void* workspace, size_t workspace_bytes, uint32_t flags,
+                         avattn_stream_t stream) {
+  if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_STAGE_DS)) return AVATTN_ERR_ARGUMENT;
+  int st = check_tables(rope_cos_q, rope_sin_q, rope_q_batch_stride);
+  if (st == AVATTN_OK) st = check_tables(rope_cos_k, rope_sin_k, rope_k_batch_stride);
+  if (st != AVATTN_OK) return st;
+  RingOpts ring;
+  ring.cos_q = rope_cos_q;
+  ring.sin_q = rope_sin_q;
+  ring.rqsb = rope_q_batch_stride;
+  ring.cos_k = rope_cos_k;
+  ring.sin_k = rope_sin_k;
+  ring.rksb = rope_k_batch_stride;
+  return bwd_impl(dout, q, k, v, out, lse, dout_strides, q_strides, k_strides, v_strides, out_strides, batch, heads_q,
+                  heads_kv, len_q, len_k, head_dim, key_mask, key_mask_batch_stride, scale, dq_acc, dq_acc_strides, dk,
+                  dk_strides, dv, dv_strides, workspace, workspace_bytes, flags | AVATTN_BWD_DQ_ACCUMULATE_F32,
+                  stream, nullptr, nullptr, 0, &ring);
+}
+
+int avattn_ring_dq_finish(const float* dq_acc, const int64_t* dq_acc_strides, int32_t batch, int32_t heads,
+                          int32_t len, int32_t head_dim, const float* rope_cos, const float* rope_sin,
+                          int64_t rope_batch_stride, void* dq, const int64_t* dq_strides, avattn_stream_t stream) {
+  if (batch < 0 || heads < 0 || len < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return AVATTN_ERR_HEAD_DIM;
+  if (!dq_acc_strides || !dq_strides) return AVATTN_ERR_NULL_POINTER;
+  int st = check_tables(rope_cos, rope_sin, rope_batch_stride);
+  if (st != AVATTN_OK) return st;
+  if ((int64_t)batch * heads * len == 0) return AVATTN_OK;
+  if (!dq_acc || !dq) return AVATTN_ERR_NULL_POINTER;
+  if (!aligned16(dq_acc) || !aligned16(dq) || !strides_ok_f32(dq_acc_strides) || !strides_ok(dq_strides))
+    return AVATTN_ERR_LAYOUT;
+  if ((int64_t)batch * heads * len > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
+  return launch_status(launch_dq_finish(dq_acc, dq_acc_strides[0], dq_acc_strides[1], dq_acc_strides[2], batch, heads,
+                                        len, head_dim, rope_cos, rope_sin, rope_batch_stride, static_cast<bf16*>(dq),
+                                        dq_strides[0], dq_strides[1], dq_strides[2],
+                                        reinterpret_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));  // 32 fp8 values
@@ -160,6 +161,63 @@ __device__ __forceinline__ u32x4 rotate8(const u32x4& x, const f32x4& c, const f
     r[p] = pack_bf16x2(a, b);
   }
   return r;
+}
+
+// Rotation of 2 interleaved pairs (4 consecutive channels) held as two bf16x2
+// words: the same arithmetic as rotate8, for the epilogues whose lanes own 4
+// consecutive channels of a row.
+__device__ __forceinline__ u32x2 rotate4(const u32x2& x, float c0, float s0, float c1, float s1, bool inverse) {
+#pragma clang fp contract(off)
+  u32x2 r;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float c = p ? c1 : c0, s = p ? s1 : s0;
+    const float e = __uint_as_float(x[p] << 16);
+    const float o = __uint_as_float(x[p] & 0xffff0000u);
+    const float ec = e * c, os = o * s, es = e * s, oc = o * c;
+    float a, b;
+    if (!inverse) {
+      a = ec - os;
+      b = es + oc;
+    } else {
+      a = ec + os;
+      b = oc - es;
+    }
+    r[p] = pack_bf16x2(a, b);
+  }
+  return r;
+}
+
+// One step of the ring merge (torch/.../_context_parallel/_attention.py
+// :182-183) for a row with accumulated LSE `la` and block LSE `lb`:
+//   out <- out - sigmoid(lb - la) * (out - out_b),  lse <- la - logsigmoid(la - lb)
+// with sigmoid = 1 / (1 + exp(-x)) and logsigmoid = min(x, 0) - log1p(exp(-|x|))
+// (PyTorch's closed forms).  A -inf LSE (a row with no valid key) is the
+// identity element: a -inf block keeps the accumulator (mode 0), a -inf
+// accumulator takes the block (mode 1).  Anything else, NaN included, goes
+// through the formula (mode 2), so a NaN on either side stays NaN.  Returns
+// the merged LSE; lse_merge_elem gives each merged output element.  Every
+// kernel that merges uses these two functions, so the separate merge kernel
+// and the forward's fused merge round identically.
+__device__ __forceinline__ float lse_merge_coeffs(float la, float lb, int& mode, float& w) {
+  if (lb == kNegInf) {
+    mode = 0;
+    w = 0.f;
+    return la;
+  }
+  if (la == kNegInf) {
+    mode = 1;
+    w = 1.f;
+    return lb;
+  }
+  mode = 2;
+  w = 1.f / (1.f + expf(-(lb - la)));
+  const float x = la - lb;
+  const float ls = fminf(x, 0.f) - log1pf(expf(-fabsf(x)));
+  return la - ls;
+}
+__device__ __forceinline__ float lse_merge_elem(float o, float ob, int mode, float w) {
+  return mode == 0 ? o : (mode == 1 ? ob : o - w * (o - ob));
 }
 
 // Map a linear block id so that consecutive *logical* ids land on the same

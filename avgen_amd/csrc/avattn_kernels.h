@@ -51,6 +51,21 @@ struct FwdArgs {
   const int* wlo;
   const int* whi;
   int64_t wsb;
+  // K rotation (null: k is used as given): the k copy rotates row j of batch
+  // b with the tables (b, 0, j, pair) at b*rksb + j*(D/2) + pair, as q is
+  // rotated on load with cos_q/sin_q.
+  const float* cos_k;
+  const float* sin_k;
+  int64_t rksb;
+  // Ring step (null o_acc: a plain forward writing o and lse): this chunk's
+  // (bf16-rounded output, lse) is merged into the running fp32 accumulator
+  // o_acc (B, Hq, Lq, D) contiguous and lse_acc (B, Hq, Lq) with the ring
+  // merge (lse_merge_coeffs); acc_first: the accumulator holds nothing yet
+  // and takes this chunk's result; acc_final: also write bf16(merged) to o.
+  float* o_acc;
+  float* lse_acc;
+  bool acc_first;
+  bool acc_final;
 };
 
 struct BwdArgs {
@@ -121,6 +136,19 @@ struct BwdArgs {
   const int* wlo;
   const int* whi;
   int64_t wsb;
+  // RoPE fused into the backward (null: q and k are used as given): q and k
+  // are the unrotated inputs; the query-side copies and the recomputing dQ
+  // kernel rotate q with cos_q/sin_q (b*rqsb + i*(D/2) + pair), the k copies
+  // and the dK/dV kernel's own key rows rotate k with cos_k/sin_k, and dk is
+  // written as the transposed rotation of the rotated key's gradient
+  // (rounded to bf16 first).  dq stays the rotated query's gradient (the
+  // ring finishes it once over all chunks, avattn_ring_dq_finish).
+  const float* cos_q;
+  const float* sin_q;
+  int64_t rqsb;
+  const float* cos_k;
+  const float* sin_k;
+  int64_t rksb;
 };
 
 // Bytes of staged dS per (b, kv head) pair.
@@ -144,6 +172,7 @@ enum KernelId : int {
   kKidBwdDqDs = 10,
   kKidQkNorm = 11,
   kKidQkNormBwd = 12,
+  kKidDqFinish = 13,
 };
 
 // Records HIP events around one launch on `stream` while timing is enabled.
@@ -172,8 +201,17 @@ hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, floa
 // zero padded to Lp = transpose_padded_len(L); either output may be null.
 // With rowmax2 set (B*H*(Lp/64) words), also the largest squared row norm of
 // each 64-row tile of each (b, h) slice, as float bits.
+// With cos/sin tables (b, 0, i, pair) at b*tsb + i*(D/2) + pair, rows are
+// rotated (rotate8) before they are copied.
 hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
-                              bf16* xr, bf16* xt, hipStream_t stream, uint32_t* rowmax2 = nullptr);
+                              bf16* xr, bf16* xt, hipStream_t stream, uint32_t* rowmax2 = nullptr,
+                              const float* cos_t = nullptr, const float* sin_t = nullptr, int64_t tsb = 0);
+
+// dq (bf16, strided) = transposed rotation of bf16(dq_acc) (fp32, strided);
+// a plain cast when cos_t is null.
+hipError_t launch_dq_finish(const float* acc, int64_t asb, int64_t ash, int64_t asl, int B, int H, int L, int D,
+                            const float* cos_t, const float* sin_t, int64_t tsb, bf16* dq, int64_t dsb, int64_t dsh,
+                            int64_t dsl, hipStream_t stream);
 
 // Per-head e4m3 scales of x (B, H, L, D) strided: scale[h] = max|x[:, h]| / 448
 // (1 for an all-zero head).  `bits` (H words) holds the running maxima; it

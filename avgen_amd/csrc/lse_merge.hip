@@ -5,7 +5,9 @@
 //   lse <- lse - logsigmoid(lse - lse_b)
 // sigmoid and logsigmoid use the same closed forms as PyTorch's elementwise
 // kernels: 1 / (1 + exp(-x)) and min(x, 0) - log1p(exp(-|x|)).
-// An LSE of -inf (a row with every key masked) is the identity element.
+// An LSE of -inf (a row with every key masked) is the identity element; a NaN
+// LSE (a row whose scores held a NaN) merges through the formula and stays
+// NaN (lse_merge_coeffs).
 #include "avattn_device.h"
 #include "avattn_kernels.h"
 
@@ -38,21 +40,11 @@ __global__ __launch_bounds__(256) void lse_merge_kernel(float* __restrict__ out,
     *reinterpret_cast<f32x4*>(&ob[0]) = *reinterpret_cast<const f32x4*>(bp);
     *reinterpret_cast<f32x4*>(&ob[4]) = *reinterpret_cast<const f32x4*>(bp + 4);
   }
-  float nl;
-  if (lb == kNegInf) {
-    nl = la;  // empty block: accumulator unchanged
-  } else if (la == kNegInf) {
-    nl = lb;  // empty accumulator: take the block
+  int mode;
+  float w;
+  const float nl = lse_merge_coeffs(la, lb, mode, w);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = ob[j];
-  } else {
-    const float w = 1.f / (1.f + expf(-(lb - la)));
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = o[j] - w * (o[j] - ob[j]);
-    const float x = la - lb;
-    const float ls = fminf(x, 0.f) - log1pf(expf(-fabsf(x)));
-    nl = la - ls;
-  }
+  for (int j = 0; j < 8; ++j) o[j] = lse_merge_elem(o[j], ob[j], mode, w);
   *reinterpret_cast<f32x4*>(op) = *reinterpret_cast<const f32x4*>(&o[0]);
   *reinterpret_cast<f32x4*>(op + 4) = *reinterpret_cast<const f32x4*>(&o[4]);
   // Every thread of the row has read lse[row] above (same wave, program

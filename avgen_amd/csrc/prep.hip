@@ -19,14 +19,18 @@
 
 namespace avattn {
 
-// One workgroup copies 64 sequence rows x D channels of one (b, h).  With
+// One workgroup copies 64 sequence rows x D channels of one (b, h), rotating
+// each row first when rotation tables are given (the copies then hold the
+// rotated rows src/avgen/models/rope.py:332-338 produces).  With
 // rowmax2 set, it also writes the largest squared norm of its (valid) rows to
 // rowmax2[(b*H + h)*(Lp/64) + tile] as float bits (one plain store per
 // workgroup; an atomic per wave into one word per head serialised badly).
 template <int D>
 __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict__ x, int64_t sb, int64_t sh,
                                                           int64_t sl, int H, int L, int Lp, bf16* __restrict__ xr,
-                                                          bf16* __restrict__ xt, uint32_t* __restrict__ rowmax2) {
+                                                          bf16* __restrict__ xt, uint32_t* __restrict__ rowmax2,
+                                                          const float* __restrict__ ct, const float* __restrict__ st,
+                                                          int64_t tsb) {
   constexpr int S = 64;       // sequence rows per workgroup
   constexpr int CPR = D / 8;  // 16-byte chunks per row
   constexpr int LD = D + 2;   // LDS row pitch in bf16 (odd word count: column reads spread over banks)
@@ -46,7 +50,14 @@ __global__ __launch_bounds__(256) void prep_copies_kernel(const bf16* __restrict
     const int c = tid + i * 256;
     const int row = c / CPR, ch = c % CPR;
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (s0 + row < L) v = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + row) * sl + ch * 8);
+    if (s0 + row < L) {
+      v = *reinterpret_cast<const u32x4*>(src + (int64_t)(s0 + row) * sl + ch * 8);
+      if (ct) {
+        // Channels 8*ch .. +7 are pairs 4*ch .. +3 of row s0 + row.
+        const int64_t t = b * tsb + (int64_t)(s0 + row) * (D / 2) + 4 * ch;
+        v = rotate8(v, *reinterpret_cast<const f32x4*>(ct + t), *reinterpret_cast<const f32x4*>(st + t), false);
+      }
+    }
     if (xr) *reinterpret_cast<u32x4*>(xr + ((int64_t)bh * Lp + s0 + row) * D + ch * 8) = v;
     uint32_t* dst = reinterpret_cast<uint32_t*>(tile + row * LD + ch * 8);
 #pragma unroll
@@ -119,16 +130,61 @@ hipError_t launch_key_prep(const uint8_t* mask, int64_t msb, int B, int Lk, floa
 }
 
 hipError_t launch_prep_copies(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
-                              bf16* xr, bf16* xt, hipStream_t stream, uint32_t* rowmax2) {
+                              bf16* xr, bf16* xt, hipStream_t stream, uint32_t* rowmax2, const float* cos_t,
+                              const float* sin_t, int64_t tsb) {
   const int Lp = transpose_padded_len(L);
   if ((int64_t)B * H == 0 || Lp == 0 || (!xr && !xt)) return hipSuccess;
   const int64_t blocks = (int64_t)(Lp / 64) * B * H;
   if (blocks > 2147483647) return hipErrorInvalidValue;
   const dim3 grid((unsigned)blocks);
   if (D == 128)
-    hipLaunchKernelGGL(prep_copies_kernel<128>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt, rowmax2);
+    hipLaunchKernelGGL(prep_copies_kernel<128>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt, rowmax2,
+                       cos_t, sin_t, tsb);
   else
-    hipLaunchKernelGGL(prep_copies_kernel<64>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt, rowmax2);
+    hipLaunchKernelGGL(prep_copies_kernel<64>, grid, dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp, xr, xt, rowmax2,
+                       cos_t, sin_t, tsb);
+  return hipGetLastError();
+}
+
+// dq = transposed rotation of bf16(acc): the ring's fp32 dq sum cast to the
+// input dtype (torch/.../_context_parallel/_attention.py:636) followed by the
+// rotation's backward (src/avgen/models/rope.py:332-338 through autograd),
+// in one pass.  One thread per 8 channels of a row.
+__global__ __launch_bounds__(256) void dq_finish_kernel(const float* __restrict__ acc, int64_t asb, int64_t ash,
+                                                        int64_t asl, int H, int L, int D, const float* __restrict__ ct,
+                                                        const float* __restrict__ st, int64_t tsb,
+                                                        bf16* __restrict__ dq, int64_t dsb, int64_t dsh, int64_t dsl,
+                                                        int64_t units) {
+  const int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= units) return;
+  const int cpr = D / 8;
+  const int c = (int)(u % cpr);
+  const int64_t row = u / cpr;
+  const int i = (int)(row % L);
+  const int h = (int)((row / L) % H);
+  const int b = (int)(row / ((int64_t)L * H));
+  const float* ap = acc + b * asb + h * ash + (int64_t)i * asl + 8 * c;
+  const f32x4 lo = *reinterpret_cast<const f32x4*>(ap);
+  const f32x4 hi = *reinterpret_cast<const f32x4*>(ap + 4);
+  u32x4 w = {pack_bf16x2(lo[0], lo[1]), pack_bf16x2(lo[2], lo[3]), pack_bf16x2(hi[0], hi[1]),
+             pack_bf16x2(hi[2], hi[3])};
+  if (ct) {
+    const int64_t t = b * tsb + (int64_t)i * (D / 2) + 4 * c;
+    w = rotate8(w, *reinterpret_cast<const f32x4*>(ct + t), *reinterpret_cast<const f32x4*>(st + t), true);
+  }
+  *reinterpret_cast<u32x4*>(dq + b * dsb + h * dsh + (int64_t)i * dsl + 8 * c) = w;
+}
+
+hipError_t launch_dq_finish(const float* acc, int64_t asb, int64_t ash, int64_t asl, int B, int H, int L, int D,
+                            const float* cos_t, const float* sin_t, int64_t tsb, bf16* dq, int64_t dsb, int64_t dsh,
+                            int64_t dsl, hipStream_t stream) {
+  const int64_t units = (int64_t)B * H * L * (D / 8);
+  if (units == 0) return hipSuccess;
+  const int64_t blocks = (units + 255) / 256;
+  if (blocks > 2147483647) return hipErrorInvalidValue;
+  LaunchTimer timer(kKidDqFinish, stream);
+  hipLaunchKernelGGL(dq_finish_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, acc, asb, ash, asl, H, L, D,
+                     cos_t, sin_t, tsb, dq, dsb, dsh, dsl, units);
   return hipGetLastError();
 }
 

@@ -52,6 +52,10 @@ __all__ = [
     "qk_norm_rope",
     "qk_norm_rope_bwd",
     "default_scale",
+    "ring_fwd_step_",
+    "ring_bwd_step",
+    "ring_dq_finish",
+    "set_ds_budget",
 ]
 
 SUPPORTED_HEAD_DIMS = (64, 128)
@@ -313,17 +317,37 @@ def _out_or_new(t: Optional[torch.Tensor], like: torch.Tensor, name: str, label:
 
 
 # Staged dS (the dK/dV kernel stores dS and dQ is one product with k): the
-# device memory it may take, default min(96 GiB, half the free memory);
-# AVGEN_AMD_DS_BUDGET_GB overrides it, 0 turns staging off.
+# device memory it may take.  Fixed per device (never read from the
+# allocator's current state, so the pass count of a given shape does not
+# change from call to call): set_ds_budget(), else AVGEN_AMD_DS_BUDGET_GB
+# (0 turns staging off), else min(96 GiB, a third of the device's memory),
+# decided at first use.
 _DS_BUDGET_CAP = 96 << 30
+_ds_budgets: dict[int, int] = {}
+
+
+def set_ds_budget(nbytes: Optional[int], device: Optional[torch.device] = None) -> None:
+    """Cap the staged-dS workspace of backward calls on ``device`` (default:
+    the current device) at ``nbytes`` (0: never stage; None: back to the
+    default)."""
+    idx = torch.device(device).index if device is not None else torch.cuda.current_device()
+    idx = torch.cuda.current_device() if idx is None else idx
+    if nbytes is None:
+        _ds_budgets.pop(idx, None)
+    else:
+        _ds_budgets[idx] = max(0, int(nbytes))
 
 
 def _ds_budget(device: torch.device) -> int:
-    env = os.environ.get("AVGEN_AMD_DS_BUDGET_GB")
-    if env is not None:
-        return int(float(env) * (1 << 30))
-    free, _ = torch.cuda.mem_get_info(device)
-    return min(_DS_BUDGET_CAP, free // 2)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _ds_budgets:
+        env = os.environ.get("AVGEN_AMD_DS_BUDGET_GB")
+        if env is not None:
+            _ds_budgets[idx] = int(float(env) * (1 << 30))
+        else:
+            total = torch.cuda.get_device_properties(idx).total_memory
+            _ds_budgets[idx] = min(_DS_BUDGET_CAP, total // 3)
+    return _ds_budgets[idx]
 
 
 def ds_bytes_per_pair(group, Lq, Lk):
@@ -454,6 +478,135 @@ def _bwd_dq_staged_impl(q, Hkv, Lk, scale, workspace, dq=None, dq_accumulate=Non
         _stream(q.device))
     _lib.check(st, name)
     return dq
+
+
+def _ring_tables(name, tables, batch, length, head_dim):
+    """(cos, sin, batch stride) of a RotaryTables (or None): shape (B|1, 1,
+    length, head_dim/2) float32 with contiguous rows of pairs, e.g. a slice
+    ``tables.slice(a, b)`` of full-sequence tables (no copy is made)."""
+    if tables is None:
+        return None, None, 0
+    cos, sin = tables.cos, tables.sin
+    if cos.ndim != 4 or cos.shape != sin.shape:
+        raise ValueError(f"{name}: rotary tables must be (batch, 1, length, pairs) and agree")
+    if cos.dtype is not torch.float32 or sin.dtype is not torch.float32:
+        raise TypeError(f"{name}: rotary tables must be float32")
+    if cos.shape[-1] * 2 != head_dim:
+        raise ValueError(f"{name}: head_dim {head_dim} does not match rotary tables built for head_dim "
+                         f"{2 * cos.shape[-1]}")
+    if cos.shape[-2] != length:
+        raise ValueError(f"{name}: sequence length {length} does not match rotary tables built for length "
+                         f"{cos.shape[-2]}")
+    if cos.shape[0] not in (1, batch) or cos.shape[1] != 1:
+        raise ValueError(f"{name}: rotary tables batch {cos.shape[0]} does not broadcast to {batch}")
+    pairs = cos.shape[-1]
+    out = []
+    for t in (cos, sin):
+        ok = t.stride(-1) == 1 and (t.shape[-2] <= 1 or t.stride(-2) == pairs) and t.data_ptr() % 16 == 0
+        ok = ok and (t.shape[0] == 1 or t.stride(0) % 4 == 0)
+        out.append(t if ok else t.contiguous())
+    cos, sin = out
+    if cos.stride(0) != sin.stride(0):
+        sin = sin.contiguous()
+        cos = cos.contiguous()
+    stride_b = 0 if cos.shape[0] == 1 else cos.stride(0)
+    _require_gpu(name, cos, sin)
+    return cos, sin, stride_b
+
+
+def ring_fwd_step_(q, k, v, key_mask, tables_q, tables_k, scale, out_acc, lse_acc, out, *, first: bool,
+                   last: bool) -> None:
+    """One fused ring forward step (``avattn_ring_fwd_step``): attention of the
+    UNROTATED query shard ``q`` against one UNROTATED KV chunk, rotated on the
+    fly with ``tables_q`` / ``tables_k`` (RotaryTables or None), merged into
+    the running fp32 ``out_acc`` / ``lse_acc`` (``first``: they take this
+    chunk's result); with ``last`` the merged output is also written to
+    ``out`` (bf16, q's shape).  Replaces apply_rotary + the ring's local op +
+    ``_SDPAMerger.step`` (torch/.../_context_parallel/_attention.py:182-183)."""
+    name = "avgen_amd.ring_fwd_step"
+    _check_qkv(name, q, k, v)
+    _require_gpu(name, q, k, v, key_mask, out_acc, lse_acc, out)
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if out_acc.shape != q.shape or out_acc.dtype is not torch.float32 or not out_acc.is_contiguous():
+        raise ValueError(f"{name}: out_acc must be contiguous float32 {tuple(q.shape)}")
+    if lse_acc.shape != (B, Hq, Lq) or lse_acc.dtype is not torch.float32 or not lse_acc.is_contiguous():
+        raise ValueError(f"{name}: lse_acc must be contiguous float32 {(B, Hq, Lq)}")
+    if last and (out is None or out.shape != q.shape or out.dtype is not torch.bfloat16
+                 or _kernel_ready(out) is not out):
+        raise ValueError(f"{name}: the last step needs a kernel-ready bf16 output shaped like the query")
+    q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    cq, sq, rqsb = _ring_tables(name, tables_q, B, Lq, D)
+    ck, sk, rksb = _ring_tables(name, tables_k, B, Lk, D)
+    flags = (_lib.RING_FIRST if first else 0) | (_lib.RING_LAST if last else 0)
+    lib = _lib.load()
+    ws = _workspace(lib.avattn_fwd_workspace_size(B, Hkv, Lk, D), q.device)
+    st = lib.avattn_ring_fwd_step(
+        _ptr(q), _ptr(k), _ptr(v), _strides3(q), _strides3(k), _strides3(v),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        _ptr(cq), _ptr(sq), rqsb, _ptr(ck), _ptr(sk), rksb,
+        float(scale),
+        _ptr(out_acc), _ptr(lse_acc),
+        _ptr(out) if last else None, _strides3(out) if last else None,
+        flags,
+        _ptr(ws), ws.numel(),
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+
+
+def ring_bwd_step(dout, q, k, v, out, lse, key_mask, tables_q, tables_k, scale, dq_acc, dk, dv, *, workspace,
+                  reuse_query_side: bool) -> None:
+    """One fused ring backward step (``avattn_ring_bwd_step``): adds this
+    chunk's gradient of the rotated query to the fp32 ``dq_acc`` and writes the
+    chunk's ``dk`` (of the unrotated keys) and ``dv`` in place.  ``workspace``
+    is a uint8 device tensor of at least the plain backward's size; dS is
+    staged when it holds at least one (batch, kv head) pair's dS."""
+    name = "avgen_amd.ring_bwd_step"
+    _check_qkv(name, q, k, v)
+    _require_gpu(name, dout, q, k, v, out, lse, key_mask, dq_acc, dk, dv, workspace)
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if dq_acc.shape != q.shape or dq_acc.dtype is not torch.float32:
+        raise ValueError(f"{name}: dq accumulator must be float32 {tuple(q.shape)}")
+    dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
+    lse = lse.contiguous()
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    cq, sq, rqsb = _ring_tables(name, tables_q, B, Lq, D)
+    ck, sk, rksb = _ring_tables(name, tables_k, B, Lk, D)
+    lib = _lib.load()
+    one = lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, 1)
+    flags = _lib.BWD_STAGE_DS if (one > 0 and workspace.numel() >= one) else 0
+    if reuse_query_side:
+        flags |= _lib.BWD_REUSE_QUERY_SIDE
+    st = lib.avattn_ring_bwd_step(
+        _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+        _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        _ptr(cq), _ptr(sq), rqsb, _ptr(ck), _ptr(sk), rksb,
+        float(scale),
+        _ptr(dq_acc), _strides3(dq_acc), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
+        _ptr(workspace), workspace.numel(),
+        flags,
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+
+
+def ring_dq_finish(dq_acc, tables_q, dq) -> None:
+    """``dq`` (bf16) = transposed rotation of ``bf16(dq_acc)``
+    (``avattn_ring_dq_finish``); a plain cast without tables."""
+    name = "avgen_amd.ring_dq_finish"
+    _require_gpu(name, dq_acc, dq)
+    B, H, L, D = dq_acc.shape
+    cq, sq, rqsb = _ring_tables(name, tables_q, B, L, D)
+    st = _lib.load().avattn_ring_dq_finish(
+        _ptr(dq_acc), _strides3(dq_acc), B, H, L, D, _ptr(cq), _ptr(sq), rqsb, _ptr(dq), _strides3(dq),
+        _stream(dq.device))
+    _lib.check(st, name)
 
 
 def _rope_apply_impl(x, cos, sin, inverse):

@@ -264,6 +264,81 @@ def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, sca
     return dq_acc.to(query.dtype), dk, dv
 
 
+def _chunk_tables(tables, a, b):
+    return None if tables is None else tables.slice(a, b)
+
+
+def _ring_forward_fused(query, key, value, key_mask, cp, scale, tables_q, tables_k):
+    """The emulated ring forward with RoPE and the merge fused into each
+    chunk's launch (``ops.ring_fwd_step_``): q and k are unrotated, each
+    chunk rotates its keys in its operand copy and the query shard on load,
+    and merges into one fp32 accumulator; the last chunk writes the bf16
+    output.  Same bits as apply_rotary + :func:`ring_attention_forward`."""
+    B, Hq, Lq, D = query.shape
+    L = key.shape[2]
+    if L == 0 or Lq == 0:
+        # No keys: zeros (src/avgen/models/attention.py:261-262), lse -inf.
+        return torch.zeros_like(query), torch.full((B, Hq, Lq), float("-inf"), device=query.device)
+    bounds = [shard_bounds(L, cp, r) for r in range(cp)]
+    acc = torch.empty(query.shape, dtype=torch.float32, device=query.device)
+    lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=query.device)
+    out = ops._kernel_ready(torch.empty_like(query, memory_format=torch.preserve_format))
+    for r, (a, b) in enumerate(bounds):
+        ops.ring_fwd_step_(query, key[:, :, a:b], value[:, :, a:b],
+                           None if key_mask is None else key_mask[:, a:b], tables_q,
+                           _chunk_tables(tables_k, a, b), scale, acc, lse, out,
+                           first=r == 0, last=r == cp - 1)
+    return out, lse
+
+
+def _ring_backward_fused(grad_out, query, key, value, out, lse, key_mask, cp, scale, tables_q, tables_k):
+    """The emulated ring backward with RoPE fused in (``ops.ring_bwd_step``):
+    each chunk's dk/dv land in their slice of the full-sequence gradients
+    (dk already of the unrotated keys), dq (of the rotated query) sums in fp32
+    across chunks and ``ops.ring_dq_finish`` casts and un-rotates it once.
+    Same bits as :func:`_ring_backward_into` followed by apply_rotary's
+    backward on dq and dk."""
+    L = key.shape[2]
+    B, Hq, Lq, D = query.shape
+    Hkv = key.shape[1]
+    dk = torch.empty(key.shape, dtype=key.dtype, device=key.device)
+    dv = torch.empty(value.shape, dtype=value.dtype, device=value.device)
+    dq = ops._kernel_ready(torch.empty_like(query, memory_format=torch.preserve_format))
+    if L == 0 or Lq == 0:
+        return dq.zero_(), dk.zero_(), dv.zero_()
+    dq_acc = torch.zeros(query.shape, dtype=torch.float32, device=query.device)
+    bounds = [shard_bounds(L, cp, r) for r in range(cp)]
+    need = max(ops.bwd_workspace_plan(B, Hq, Hkv, Lq, b - a, D, query.device)[0] for a, b in bounds)
+    ws = ops._workspace(need, query.device)
+    for r, (a, b) in enumerate(bounds):
+        ops.ring_bwd_step(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse,
+                          None if key_mask is None else key_mask[:, a:b], tables_q, _chunk_tables(tables_k, a, b),
+                          scale, dq_acc, dk[:, :, a:b], dv[:, :, a:b], workspace=ws, reuse_query_side=r > 0)
+    ops.ring_dq_finish(dq_acc, tables_q, dq)
+    return dq, dk, dv
+
+
+class _RingAttentionRope(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, query, key, value, key_mask, cp, scale, tables_q, tables_k):
+        s = ops.default_scale(query.shape[-1]) if scale is None else float(scale)
+        out, lse = _ring_forward_fused(query, key, value, key_mask, cp, s, tables_q, tables_k)
+        ctx.save_for_backward(query, key, value, out, lse, key_mask)
+        ctx.cp = cp
+        ctx.scale = s
+        ctx.tables = (tables_q, tables_k)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_out, _grad_lse):
+        query, key, value, out, lse, key_mask = ctx.saved_tensors
+        tables_q, tables_k = ctx.tables
+        dq, dk, dv = _ring_backward_fused(grad_out.contiguous(), query, key, value, out, lse, key_mask, ctx.cp,
+                                          ctx.scale, tables_q, tables_k)
+        return dq, dk, dv, None, None, None, None, None
+
+
 class _RingAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query, key, value, key_mask, cp, scale):
@@ -295,9 +370,24 @@ def ring_attention(
     cp: int,
     key_mask: Optional[torch.Tensor] = None,
     scale: Optional[float] = None,
+    tables_q=None,
+    tables_k=None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Differentiable emulated ring: ``key``/``value`` (full sequence) are split
     into ``cp`` contiguous chunks (ragged lengths raise, as
     src/avgen/parallel/context.py:74-79), the local ``query`` shard attends to
-    each in ring order, and results merge online.  Returns ``(out, lse)``."""
+    each in ring order, and results merge online.  Returns ``(out, lse)``.
+
+    With ``tables_q`` / ``tables_k`` (RotaryTables of the query shard's and
+    of the full key sequence's positions), ``query`` and ``key`` are the
+    UNROTATED tensors and the 3D RoPE of src/avgen/models/rope.py:297-338
+    (called at src/avgen/models/layers.py:535-536) is fused into the
+    kernels: no separate rotation or merge launches, the same bits as
+    ``ring_attention(apply_rotary(q, tables_q), apply_rotary(k, tables_k), v)``
+    and the same gradients with respect to the unrotated inputs."""
+    if (tables_q is None) != (tables_k is None):
+        raise ValueError("pass both tables_q and tables_k, or neither")
+    if tables_q is not None:
+        shard_bounds(key.shape[2], cp, 0)  # ragged lengths raise before any launch
+        return _RingAttentionRope.apply(query, key, value, key_mask, cp, scale, tables_q, tables_k)
     return _RingAttention.apply(query, key, value, key_mask, cp, scale)

@@ -124,13 +124,11 @@ def step(cfg: dict, x: dict) -> None:
     q = x["q"].requires_grad_(True)
     k = x["k"].requires_grad_(True)
     v = x["v"].requires_grad_(True)
-    q_rot = avgen_amd.rope.apply_rotary(q, x["tables_q"])
-    k_rot = avgen_amd.rope.apply_rotary(k, x["tables_k"])
-    if cfg["cp"] > 1:
-        out, _ = avgen_amd.ring.ring_attention(q_rot, k_rot, v, cp=cfg["cp"], key_mask=x["mask"])
-    else:
-        out = avgen_amd.attention.attention(q_rot, k_rot, v, attn_mask=None if x["mask"] is None
-                                            else x["mask"][:, None, None, :])
+    # RoPE fused into the ring's kernels (q rotated on load, k in its operand
+    # copy, dq/dk rotated back in the backward's epilogues); cp = 1 is the
+    # unchunked attention of the c2/c4 blocks.
+    out, _ = avgen_amd.ring.ring_attention(q, k, v, cp=cfg["cp"], key_mask=x["mask"], tables_q=x["tables_q"],
+                                           tables_k=x["tables_k"])
     out.backward(x["do"])
     q.grad = k.grad = v.grad = None
 
@@ -610,7 +608,7 @@ def main() -> int:
         log("[bench] calibration kernel done")
     per_kernel = {}
     for name in ("attn_fwd", "bwd_dkdv", "bwd_dq", "bwd_dq_ds", "bwd_preprocess", "lse_merge", "rope_apply",
-                 "transpose"):
+                 "transpose", "ring_dq_finish"):
         ms, n = timing.read(name)
         per_kernel[name] = {"total_ms": ms, "launches": n, "avg_ms": ms / n if n else 0.0}
     timing.close()

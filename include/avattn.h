@@ -312,6 +312,105 @@ int avattn_lse_merge(float* out_acc, float* lse_acc,
                      avattn_stream_t stream);
 
 /*
+ * One step of the non-causal ring forward with the rotation and the merge
+ * fused in: replaces, per KV chunk, apply_rotary on the query shard and on
+ * the chunk's keys (src/avgen/models/rope.py:297-338, called at
+ * src/avgen/models/layers.py:535-536), the ring's local attention op
+ * (torch/.../_context_parallel/_attention.py:468-474) and
+ * _SDPAMerger.step (:182-183; with convert_to_f32, :209-211), and on the last
+ * chunk _SDPAMerger.results() (:215-223).
+ * q and k are UNROTATED; rope_cos_q/rope_sin_q (tables of the query shard's
+ * positions) rotate q on load and rope_cos_k/rope_sin_k (tables of this
+ * chunk's positions) rotate k in its operand copy; either pair may be NULL
+ * (no rotation).  Tables as for avattn_fwd: element (b, 0, i, p) at
+ * b * batch_stride + i * (head_dim/2) + p.
+ * out_acc (float32, contiguous (batch, heads_q, len_q, head_dim)) and lse_acc
+ * (float32, contiguous (batch, heads_q, len_q)) hold the running merge:
+ * this chunk's output, rounded to bf16 as the ring's op returns it, and its
+ * LSE are merged into them in fp32 with the formula of avattn_lse_merge
+ * (bit-identical to a separate avattn_lse_merge call).  flags:
+ *   AVATTN_RING_FIRST  out_acc/lse_acc hold nothing yet (not read): they take
+ *                      this chunk's result.
+ *   AVATTN_RING_LAST   also write the merged output, cast to bf16, to out
+ *                      (out_strides as for avattn_fwd); without it out and
+ *                      out_strides are not used and may be NULL.
+ * After the last step lse_acc is the ring's LSE.  len_k must be positive.
+ * Every other argument, the workspace (avattn_fwd_workspace_size) and the
+ * error codes are those of avattn_fwd.
+ */
+#define AVATTN_RING_FIRST 1u
+#define AVATTN_RING_LAST  2u
+int avattn_ring_fwd_step(const void* q, const void* k, const void* v,
+                         const int64_t* q_strides, const int64_t* k_strides,
+                         const int64_t* v_strides,
+                         int32_t batch, int32_t heads_q, int32_t heads_kv,
+                         int32_t len_q, int32_t len_k, int32_t head_dim,
+                         const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                         const float* rope_cos_q, const float* rope_sin_q,
+                         int64_t rope_q_batch_stride,
+                         const float* rope_cos_k, const float* rope_sin_k,
+                         int64_t rope_k_batch_stride,
+                         float scale,
+                         float* out_acc, float* lse_acc,
+                         void* out, const int64_t* out_strides,
+                         uint32_t flags,
+                         void* workspace, size_t workspace_bytes,
+                         avattn_stream_t stream);
+
+/*
+ * One step of the non-causal ring backward with the rotation fused in:
+ * replaces, per KV chunk, the ring's local backward op
+ * (torch/.../_context_parallel/_attention.py:567-575) with its fp32 dq sum
+ * (:505-506, 623), and the rotation's backward for this chunk's keys
+ * (src/avgen/models/rope.py:332-338 through autograd).  q and k are
+ * UNROTATED with their tables as in avattn_ring_fwd_step; out/lse are the
+ * ring's merged output and LSE.  dq_acc (float32, strides in floats,
+ * multiples of 4) gets this chunk's gradient of the ROTATED query added in
+ * fp32; avattn_ring_dq_finish turns the sum into dq once all chunks are in.
+ * dk is the gradient of the unrotated keys: the rotated keys' gradient
+ * rounded to bf16, then the transposed rotation, rounded again (the
+ * reference's autograd order); dv as avattn_bwd.  flags: any of
+ * AVATTN_BWD_REUSE_QUERY_SIDE and AVATTN_BWD_STAGE_DS (the query-side copies
+ * kept in the workspace are the rotated ones); dq accumulation is implied.
+ * Every other argument, the workspace sizes and the error codes are those of
+ * avattn_bwd.
+ */
+int avattn_ring_bwd_step(const void* dout, const void* q, const void* k, const void* v,
+                         const void* out, const float* lse,
+                         const int64_t* dout_strides, const int64_t* q_strides,
+                         const int64_t* k_strides, const int64_t* v_strides,
+                         const int64_t* out_strides,
+                         int32_t batch, int32_t heads_q, int32_t heads_kv,
+                         int32_t len_q, int32_t len_k, int32_t head_dim,
+                         const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                         const float* rope_cos_q, const float* rope_sin_q,
+                         int64_t rope_q_batch_stride,
+                         const float* rope_cos_k, const float* rope_sin_k,
+                         int64_t rope_k_batch_stride,
+                         float scale,
+                         float* dq_acc, const int64_t* dq_acc_strides,
+                         void* dk, const int64_t* dk_strides,
+                         void* dv, const int64_t* dv_strides,
+                         void* workspace, size_t workspace_bytes,
+                         uint32_t flags,
+                         avattn_stream_t stream);
+
+/*
+ * The ring backward's last step for the query shard: dq (bf16) = transposed
+ * rotation of bf16(dq_acc), i.e. the fp32 dq sum cast to the input dtype
+ * (torch/.../_context_parallel/_attention.py:636) followed by the rotation's
+ * backward (src/avgen/models/rope.py:332-338 through autograd); a plain cast
+ * when rope_cos/rope_sin are NULL.  Strides: 3 entries (batch, head, seq),
+ * head_dim contiguous (floats for dq_acc, bf16 elements for dq).
+ */
+int avattn_ring_dq_finish(const float* dq_acc, const int64_t* dq_acc_strides,
+                          int32_t batch, int32_t heads, int32_t len, int32_t head_dim,
+                          const float* rope_cos, const float* rope_sin,
+                          int64_t rope_batch_stride,
+                          void* dq, const int64_t* dq_strides,
+                          avattn_stream_t stream);
+
+/*
  * Rotary tables from physical coordinates (src/avgen/models/rope.py:218-294).
  * coords: float32, element (b, i, a) at b*coords_batch_stride +
  * i*coords_row_stride + a.  inv_freq[p] and axis_of_pair[p] (0=time,
@@ -401,7 +500,8 @@ int avattn_qk_norm_rope_bwd(const void* x, const int64_t* x_strides,
  * 3 backward dQ, 4 LSE merge, 5 rotary apply, 6 rotary tables,
  * 7 operand copies (forward and backward operand preparation, including the
  * fp8 forward's e4m3 k copy), 8 fp8 forward, 9 fp8 absmax scales,
- * 10 dQ from staged dS, 11 q/k norm + rotation, 12 its backward.
+ * 10 dQ from staged dS, 11 q/k norm + rotation, 12 its backward,
+ * 13 the ring dq finish (avattn_ring_dq_finish).
  * avattn_timing_begin creates `capacity` event pairs (call it outside any
  * timed or captured region); launches beyond capacity are not recorded and
  * make avattn_timing_read return AVATTN_ERR_WORKSPACE.

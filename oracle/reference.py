@@ -174,6 +174,33 @@ def video_coords(frames: int, height: int, width: int, fps: float = 8.0,
     return np.broadcast_to(xyz, (batch,) + xyz.shape).copy()
 
 
+def temporal_coords(positions: np.ndarray, frames: int, height: int, width: int,
+                    patch: tuple[int, int, int] = (1, 2, 2), normalize_space: bool = False) -> np.ndarray:
+    """src/avgen/core/patchify.py:45-105 (build_temporal_coords) with an
+    explicit loop over tokens: token ``(f, r, c)`` of the post-patch grid
+    gets ``(mean of positions[b, f*pf:(f+1)*pf], r*ph, c*pw)`` (or ``r/(gh-1)``,
+    ``c/(gw-1)`` with ``normalize_space``), in float32, time -> row -> column
+    order.  ``positions`` is ``(B, frames)`` seconds before temporal patching."""
+    pos = np.asarray(positions, np.float32)
+    pf, ph, pw = patch
+    gf, gh, gw = frames // pf, height // ph, width // pw
+    out = np.empty((pos.shape[0], gf * gh * gw, 3), np.float32)
+    for b in range(pos.shape[0]):
+        i = 0
+        for f in range(gf):
+            t = np.float32(pos[b, f * pf:(f + 1) * pf].astype(np.float64).mean())
+            for r in range(gh):
+                for c in range(gw):
+                    if normalize_space:
+                        y = np.float32(r) / np.float32(max(gh - 1, 1))
+                        x = np.float32(c) / np.float32(max(gw - 1, 1))
+                    else:
+                        y, x = np.float32(r * ph), np.float32(c * pw)
+                    out[b, i] = (t, y, x)
+                    i += 1
+    return out
+
+
 # ---------------------------------------------------------------------------
 # Attention with key-padding mask and LSE  (src/avgen/models/attention.py)
 # ---------------------------------------------------------------------------
@@ -226,6 +253,12 @@ def attention_f64(
     valid key gives out = 0 (what F.scaled_dot_product_attention returns) and
     lse = -inf.  Zero-length keys give zeros (src/avgen/models/attention.py
     :261-262).
+
+    Non-finite inputs follow the math of SDPA's masked softmax: a mask is an
+    additive 0 / -inf bias (so a NaN score stays NaN even at a masked key,
+    as torch's math path computes it), and a row holding a NaN or a +inf
+    score gets out = NaN and lse = NaN (softmax(+inf, ...) is inf/inf).
+    Only a row whose every score is -inf counts as "no valid key".
     """
     q = np.asarray(q, np.float64)
     k = _expand_kv(np.asarray(k, np.float64), q.shape[1])
@@ -234,10 +267,13 @@ def attention_f64(
     if Lq == 0 or k.shape[2] == 0:
         return np.zeros_like(q), np.full((B, H, Lq), -np.inf)
     scale = 1.0 / math.sqrt(D) if scale is None else scale
-    s = np.einsum("bhqd,bhkd->bhqk", q, k) * scale
-    m = _dense_mask(key_mask, attn_mask)
-    if m is not None:
-        s = np.where(m, s, -np.inf)
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = np.einsum("bhqd,bhkd->bhqk", q, k) * scale
+        m = _dense_mask(key_mask, attn_mask)
+        if m is not None:
+            s = s + np.where(m, 0.0, -np.inf)
+    bad = (np.isnan(s) | np.isposinf(s)).any(axis=-1)  # (B, H, Lq)
+    s = np.where(bad[..., None], -np.inf, s)
     mx = s.max(axis=-1, keepdims=True)
     safe = np.where(np.isfinite(mx), mx, 0.0)
     p = np.exp(s - safe)
@@ -245,6 +281,8 @@ def attention_f64(
     with np.errstate(divide="ignore", invalid="ignore"):
         out = np.where(l > 0, np.einsum("bhqk,bhkd->bhqd", p, v) / np.where(l > 0, l, 1.0), 0.0)
         lse = np.where(l[..., 0] > 0, np.log(np.where(l[..., 0] > 0, l[..., 0], 1.0)) + safe[..., 0], -np.inf)
+    out = np.where(bad[..., None], np.nan, out)
+    lse = np.where(bad, np.nan, lse)
     return out, lse
 
 
@@ -443,8 +481,8 @@ def lse_merge_f64(out: np.ndarray, lse: np.ndarray, out_b: np.ndarray, lse_b: np
     ``exp(lse - L)`` and ``exp(lse_b - L)`` with ``L = logaddexp(lse, lse_b)``."""
     lse = np.asarray(lse, np.float64)
     lse_b = np.asarray(lse_b, np.float64)
-    L = np.logaddexp(lse, lse_b)
     with np.errstate(invalid="ignore"):
+        L = np.logaddexp(lse, lse_b)  # NaN in either stays NaN
         wa = np.where(np.isneginf(lse), 0.0, np.exp(lse - np.where(np.isneginf(L), 0.0, L)))
         wb = np.where(np.isneginf(lse_b), 0.0, np.exp(lse_b - np.where(np.isneginf(L), 0.0, L)))
     return wa[..., None] * np.asarray(out, np.float64) + wb[..., None] * np.asarray(out_b, np.float64), L

@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 7
+    assert lib.avattn_abi_version() == 8
     for code in range(0, 10):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
@@ -144,6 +144,12 @@ def test_fwd_validation_paths(lib):
     assert _fwd(lib, k=None) == _lib.ERR_NULL_POINTER
     assert _fwd(lib, mask=16, msb=2) == _lib.ERR_ARGUMENT
     assert _fwd(lib, B=1, Hq=1 << 30, Hkv=1, Lq=1 << 20) == _lib.ERR_TOO_LARGE
+    # 32-bit buffer ranges: one padded (b, head) slice of k (Lkp*D*2 bytes)
+    # and the query heads of one group in the backward (group*Lqp*D*2).
+    assert _fwd(lib, Lk=(1 << 24) - 64) == _lib.ERR_WORKSPACE  # 4 GiB - 16 KiB per slice: still addressable
+    assert _fwd(lib, Lk=1 << 24) == _lib.ERR_TOO_LARGE
+    assert _fwd(lib, Hq=40, Hkv=1, Lq=420_000) == _lib.ERR_TOO_LARGE  # MQA, 40 * 420k rows * 256 B >= 2^32
+    assert _fwd(lib, Hq=40, Hkv=1, Lq=400_000, ws=8) == _lib.ERR_WORKSPACE
     assert _fwd(lib, ws=None) == _lib.ERR_WORKSPACE
     assert _fwd(lib, wsb=100) == _lib.ERR_WORKSPACE  # needs more than 2 * (2*128*64*2) bytes
     assert _fwd(lib, ws=8) == _lib.ERR_WORKSPACE
@@ -260,6 +266,58 @@ def test_merge_and_rope_validation_paths(lib):
                                   16, 16, None) == _lib.ERR_ARGUMENT
     assert lib.avattn_rope_tables(16, 3, 3, 1, 4, 2, cast(f), cast(ax), cast(z), cast(f3), cast(z), cast(f3),
                                   16, 16, None) == _lib.ERR_HEAD_DIM
+
+
+def _ring_fwd(lib, **over):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+    a = dict(q=16, k=16, v=16, qs=s, ks=s, vs=s, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
+             cq=16, sq=16, rqb=0, ck=16, sk=16, rkb=0, scale=0.125, acc=16, lacc=16, out=16, os=s,
+             flags=_lib.RING_FIRST | _lib.RING_LAST, ws=256, wsb=1 << 20, stream=None)
+    a.update(over)
+    return lib.avattn_ring_fwd_step(a["q"], a["k"], a["v"], a["qs"], a["ks"], a["vs"], a["B"], a["Hq"], a["Hkv"],
+                                    a["Lq"], a["Lk"], a["D"], a["mask"], a["msb"], a["cq"], a["sq"], a["rqb"],
+                                    a["ck"], a["sk"], a["rkb"], a["scale"], a["acc"], a["lacc"], a["out"], a["os"],
+                                    a["flags"], a["ws"], a["wsb"], a["stream"])
+
+
+@cpu_only
+def test_ring_step_validation_paths(lib):
+    assert _ring_fwd(lib, ws=8) == _lib.ERR_WORKSPACE  # valid up to the workspace
+    assert _ring_fwd(lib, flags=4) == _lib.ERR_ARGUMENT
+    assert _ring_fwd(lib, Lk=0) == _lib.ERR_BAD_SHAPE  # a ring chunk holds keys
+    assert _ring_fwd(lib, Lq=0) == _lib.OK
+    assert _ring_fwd(lib, acc=None) == _lib.ERR_NULL_POINTER
+    assert _ring_fwd(lib, acc=8) == _lib.ERR_LAYOUT
+    assert _ring_fwd(lib, lacc=18) == _lib.ERR_LAYOUT
+    assert _ring_fwd(lib, sq=None) == _lib.ERR_NULL_POINTER
+    assert _ring_fwd(lib, ck=24) == _lib.ERR_LAYOUT
+    assert _ring_fwd(lib, rkb=2) == _lib.ERR_LAYOUT
+    assert _ring_fwd(lib, out=None) == _lib.ERR_NULL_POINTER  # the last step writes the output
+    assert _ring_fwd(lib, out=None, os=None, flags=_lib.RING_FIRST, ws=8) == _lib.ERR_WORKSPACE  # not needed
+    assert _ring_fwd(lib, cq=None, sq=None, ck=None, sk=None, ws=8) == _lib.ERR_WORKSPACE  # no rotation
+    s = _lib.i64_array([1 << 17, 1 << 17, 128])
+    fs = _lib.i64_array([1 << 17, 1 << 17, 132])  # fp32 accumulator strides: multiples of 4
+
+    def bwd(flags=0, ws_bytes=8, dq_s=fs, cq=16):
+        return lib.avattn_ring_bwd_step(16, 16, 16, 16, 16, 16, s, s, s, s, s, 1, 2, 2, 4, 4, 128, None, 0,
+                                        cq, 16, 0, 16, 16, 0, 0.125, 16, dq_s, 16, s, 16, s, 16, ws_bytes, flags,
+                                        None)
+
+    assert bwd() == _lib.ERR_WORKSPACE
+    assert bwd(flags=_lib.BWD_DEFER_DQ) == _lib.ERR_ARGUMENT  # dq always accumulates here
+    assert bwd(flags=_lib.BWD_DQ_ACCUMULATE_F32) == _lib.ERR_ARGUMENT
+    assert bwd(dq_s=_lib.i64_array([1 << 17, 1 << 17, 130])) == _lib.ERR_LAYOUT
+    assert bwd(cq=None) == _lib.ERR_NULL_POINTER
+    one = lib.avattn_bwd_staged_workspace_size(1, 2, 2, 4, 4, 128, 1)
+    assert bwd(flags=_lib.BWD_STAGE_DS, ws_bytes=one - 1) == _lib.ERR_WORKSPACE
+    f = lib.avattn_ring_dq_finish
+    assert f(16, fs, 1, 2, 4, 96, 16, 16, 0, 16, s, None) == _lib.ERR_HEAD_DIM
+    assert f(16, fs, -1, 2, 4, 128, 16, 16, 0, 16, s, None) == _lib.ERR_BAD_SHAPE
+    assert f(None, fs, 1, 2, 4, 128, 16, 16, 0, 16, s, None) == _lib.ERR_NULL_POINTER
+    assert f(16, fs, 1, 2, 4, 128, 16, None, 0, 16, s, None) == _lib.ERR_NULL_POINTER
+    assert f(16, _lib.i64_array([1 << 17, 1 << 17, 130]), 1, 2, 4, 128, 16, 16, 0, 16, s, None) == _lib.ERR_LAYOUT
+    assert f(16, fs, 1, 2, 4, 128, 16, 16, 0, 16, _lib.i64_array([1 << 17, 1 << 17, 132]), None) == _lib.ERR_LAYOUT
+    assert f(16, fs, 1, 0, 4, 128, 16, 16, 0, 16, s, None) == _lib.OK
 
 
 def _fwd_fp8(lib, **over):

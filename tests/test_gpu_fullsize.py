@@ -198,6 +198,75 @@ def test_c2_block_with_fused_rope(amd):
     ou = amd.attention.attention(amd.rope.apply_rotary(qu, tables), k_rot, v)
     ou.backward(do)
     assert torch.equal(out, ou) and torch.equal(qg.grad, qu.grad)
+    del qg, qu, ou
+    # Full backward with RoPE on both q and k fused in (the bench's c2 step:
+    # the ring path with one chunk): dq, dk, dv of the UNROTATED inputs for
+    # one head per batch against float32 (gradients of the rotated inputs
+    # from float32 products, rotated back by the transposed rotation in
+    # float32).
+    qf, kf, vf = (t.clone().requires_grad_(True) for t in (q, k, v))
+    of, lf = amd.ring.ring_attention(qf, kf, vf, cp=1, tables_q=tables, tables_k=tables)
+    of.backward(do)
+    torch.cuda.synchronize()
+    assert torch.equal(of, out)
+    cos, sin = tables.cos, tables.sin
+
+    def unrotate(g, b):  # transpose of the rotation, float32: (e*c + o*s, o*c - e*s)
+        c, s = cos[b if cos.shape[0] > 1 else 0, 0], sin[b if sin.shape[0] > 1 else 0, 0]
+        e, o = g[:, 0::2], g[:, 1::2]
+        r = torch.empty_like(g)
+        r[:, 0::2] = e * c + o * s
+        r[:, 1::2] = o * c - e * s
+        return r
+
+    for b in range(B):
+        h = 7 * b + 3
+        qh, kh, vh, doh = q_rot[b, h].float(), k_rot[b, h].float(), v[b, h].float(), do[b, h].float()
+        s = torch.mm(qh, kh.t().contiguous()) * scale
+        lse_ref = torch.logsumexp(s, dim=-1)
+        p = torch.exp(s - lse_ref[:, None])
+        del s
+        o_ref = torch.mm(p, vh)
+        ds = p * (torch.mm(doh, vh.t().contiguous()) - (doh * o_ref).sum(-1)[:, None])
+        rq = unrotate(torch.mm(ds, kh) * scale, b)
+        rk = unrotate(torch.mm(ds.t().contiguous(), qh) * scale, b)
+        rv = torch.mm(p.t().contiguous(), doh)
+        del p, ds
+        assert (lf[b, h] - lse_ref).abs().max().item() <= LSE_TOL
+        for name, got, ref in (("dq", qf.grad[b, h], rq), ("dk", kf.grad[b, h], rk), ("dv", vf.grad[b, h], rv)):
+            err = _max_rel(got, ref)
+            print(f"  c2 b={b} h={h} {name} rel err {err:.2e}", flush=True)
+            assert err <= GRAD_REL_TOL, name
+
+
+def test_c5_sampling_bf16_and_fp8_against_float32(amd):
+    """c5 CFG sampling (2, 40, 75600, 128), forward only: the bf16 forward and
+    the fp8 (e4m3, per-head absmax scales) q k^T forward against float32
+    attention of the same bf16 q/k/v for sampled query rows of four heads.
+    The bf16 path meets the bf16 bar (out <= 2e-2, LSE <= 1e-3).  The fp8
+    path's output meets the same out bar; its LSE carries the e4m3 rounding
+    of the scores (3 mantissa bits: ~2^-5 relative per operand), measured
+    at ~4.5e-3 here, so it is held to 1e-2 (sampling consumes only the
+    output)."""
+    B, H, L, D = 2, 40, 75600, 128
+    print(f"c5 sampling B={B} H={H} L={L} D={D}", flush=True)
+    scale = D ** -0.5
+    q, k, v = (_rand((B, H, L, D), s, 2 ** -0.5) for s in (40, 41, 42))
+    o16, l16 = amd.ops.flash_fwd(q, k, v, None, None, None, scale)
+    o8, l8 = amd.ops.flash_fwd_fp8(q, k, v, None, amd.ops.fp8_absmax_scales(q), amd.ops.fp8_absmax_scales(k), scale)
+    torch.cuda.synchronize()
+    rows = torch.arange(0, L, 149, device="cuda")[:512]
+    worst = {"bf16": [0.0, 0.0], "fp8": [0.0, 0.0]}
+    for b in range(B):
+        for h in (0, 13, 27, H - 1):
+            ro, rl = _ref_rows(q[b, h, rows], k[b, h], v[b, h], scale)
+            for name, o, l in (("bf16", o16, l16), ("fp8", o8, l8)):
+                eo = (o[b, h, rows].float() - ro).abs().max().item()
+                el = (l[b, h, rows] - rl).abs().max().item()
+                worst[name] = [max(worst[name][0], eo), max(worst[name][1], el)]
+    print(f"  c5 worst out/lse errors vs float32: {worst}", flush=True)
+    assert worst["bf16"][0] <= OUT_TOL and worst["bf16"][1] <= LSE_TOL
+    assert worst["fp8"][0] <= OUT_TOL and worst["fp8"][1] <= 1e-2
 
 
 def _grads(amd_fn, q, k, v, do):

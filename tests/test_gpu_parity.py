@@ -377,12 +377,15 @@ def test_staged_ds_in_passes_matches_recompute(amd, monkeypatch):
     per = amd.ops.ds_bytes_per_pair(Hq // Hkv, Lq, Lk)
     out, lse = amd.ops.flash_fwd(q, k, v, m, None, None, D ** -0.5)
     ref = amd.ops._bwd_impl(do, q, k, v, out, lse, m, D ** -0.5, stage_ds=False)
-    monkeypatch.setenv("AVGEN_AMD_DS_BUDGET_GB", repr(2.5 * per / (1 << 30)))
-    nbytes, staged = amd.ops.bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, q.device)
-    lib = amd._lib.load()
-    assert staged and nbytes == lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, 2)
-    print(f"staged passes: {per} bytes per pair, workspace {nbytes}", flush=True)
-    got = amd.ops._bwd_impl(do, q, k, v, out, lse, m, D ** -0.5)
+    amd.ops.set_ds_budget(int(2.5 * per), q.device)
+    try:
+        nbytes, staged = amd.ops.bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, q.device)
+        lib = amd._lib.load()
+        assert staged and nbytes == lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, 2)
+        print(f"staged passes: {per} bytes per pair, workspace {nbytes}", flush=True)
+        got = amd.ops._bwd_impl(do, q, k, v, out, lse, m, D ** -0.5)
+    finally:
+        amd.ops.set_ds_budget(None, q.device)
     assert torch.equal(got[1], ref[1]) and torch.equal(got[2], ref[2])
     err = (got[0].float() - ref[0].float()).abs().max().item()
     assert err <= 1e-2 * ref[0].float().abs().max().item(), err

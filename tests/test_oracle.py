@@ -357,6 +357,92 @@ def test_merge_neg_inf_is_identity(rng):
     assert np.array_equal(to.numpy(), mo) and np.array_equal(tl.numpy(), ml)
 
 
+def _sdpa_math(q, k, v, mask=None):
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    with sdpa_kernel([SDPBackend.MATH]):
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+
+
+def test_non_finite_scores_propagate_like_sdpa(rng):
+    """A NaN (or +inf) score makes its row NaN in out and lse, as torch's math
+    SDPA (out) and its CPU flash op (lse) give; a -inf score only drops its key;
+    a NaN at a masked key still poisons the row (the mask is an additive bias)."""
+    q, k, v = _qkv(rng, B=1, H=2, Lq=6, Lk=7, D=8)
+    cases = []
+    kn = k.copy()
+    kn[0, 1, 3, 2] = np.nan  # every row of head 1 sees a NaN score
+    cases.append(("nan key", q, kn, None))
+    ki = k.copy()
+    ki[0, 0, 4, 5] = np.inf  # +inf where q[.., 5] > 0, -inf (key dropped) where < 0
+    cases.append(("inf key", q, ki, None))
+    qn = q.copy()
+    qn[0, 0, 2, 0] = np.nan  # one query row
+    cases.append(("nan query row", qn, k, None))
+    mask = np.ones((1, 7), bool)
+    mask[0, 3] = False
+    cases.append(("nan at a masked key", q, kn, mask))
+    for name, qq, kk, m in cases:
+        out, lse = R.attention_f64(qq, kk, v, m)
+        tq, tk, tv = (torch.from_numpy(x) for x in (qq, kk, v))
+        tm = None if m is None else torch.from_numpy(m)[:, None, None, :]
+        ref = _sdpa_math(tq, tk, tv, tm).numpy()
+        assert np.array_equal(np.isnan(out), np.isnan(ref)), name
+        fin = ~np.isnan(ref)
+        assert np.abs(out[fin] - ref[fin]).max() < 1e-12, name
+        assert np.array_equal(np.isnan(lse), np.isnan(out).any(-1)), name
+        if name in ("nan key", "inf key"):
+            # torch's CPU flash op agrees on which rows have a NaN LSE and on
+            # the finite ones (its all-NaN-row case returns 0s, so it is not
+            # used for the query-row case).
+            _, tl = torch.ops.aten._scaled_dot_product_flash_attention_for_cpu(tq.float(), tk.float(), tv.float())[:2]
+            tl = tl.numpy()
+            assert np.array_equal(np.isnan(lse), np.isnan(tl)), name
+            assert np.abs(lse[~np.isnan(lse)] - tl[~np.isnan(tl)]).max() < 1e-5, name
+    out, lse = R.attention_f64(q, ki, v)
+    neg = q[0, 0, :, 5] < 0
+    assert neg.any() and (~neg).any()
+    assert np.isfinite(out[0, 0, neg]).all() and np.isnan(out[0, 0, ~neg]).all()
+    # a dropped (-inf) key equals deleting it
+    keep = [j for j in range(7) if j != 4]
+    ro, rl = R.attention_f64(q[:, :, neg], k[:, :, keep], v[:, :, keep])
+    assert np.abs(out[:, 0:1, neg] - ro[:, 0:1]).max() < 1e-12
+    # a row with no valid key is still zeros / -inf, not NaN
+    none = np.zeros((1, 7), bool)
+    out, lse = R.attention_f64(q, k, v, none)
+    assert (out == 0).all() and np.isneginf(lse).all()
+
+
+def test_merge_propagates_nan_but_not_neg_inf(rng):
+    """The merge treats only -inf as the identity: a NaN chunk LSE (or
+    accumulator) stays NaN, as the torch formula (:182-183) computes it, so a
+    ring cannot drop a chunk whose scores held a NaN."""
+    out = rng.standard_normal((3, 8)).astype(np.float32)
+    out_b = rng.standard_normal((3, 8)).astype(np.float32)
+    lse = np.array([1.0, np.nan, np.nan], np.float32)
+    lse_b = np.array([np.nan, 2.0, -np.inf], np.float32)
+    out_b[0] = np.nan
+    mo, ml = R.lse_merge_f32(out, lse, out_b, lse_b)
+    assert np.isnan(ml).all()
+    assert np.isnan(mo[0]).all() and np.isnan(mo[1]).all()
+    assert np.array_equal(mo[2], out[2])  # a -inf block keeps the (NaN-LSE) accumulator's values
+    to, tl = T.merge(torch.from_numpy(out), torch.from_numpy(lse), torch.from_numpy(out_b), torch.from_numpy(lse_b))
+    assert np.array_equal(np.isnan(to.numpy()), np.isnan(mo)) and np.isnan(tl.numpy()).all()
+    # a 4-chunk ring with a NaN in one key row of chunk 2 returns NaN rows,
+    # where dropping the chunk would have given a finite answer
+    q, k, v = _qkv(rng, B=1, H=1, Lq=5, Lk=16, D=8)
+    k[0, 0, 9] = np.nan
+    keys = [k[:, :, 4 * i:4 * i + 4] for i in range(4)]
+    values = [v[:, :, 4 * i:4 * i + 4] for i in range(4)]
+    ro, rl = R.ring_forward_f64(q, keys, values)
+    assert np.isnan(ro).all() and np.isnan(rl).all()
+    uo, _ = R.attention_f64(q, k, v)
+    assert np.isnan(uo).all()
+    to, tl = T.ring_forward(*(torch.from_numpy(x) for x in (q,)), [torch.from_numpy(x) for x in keys],
+                            [torch.from_numpy(x) for x in values])
+    assert torch.isnan(to).all() and torch.isnan(tl).all()
+
+
 def test_merge_is_associative_and_commutative(rng):
     parts = [(rng.standard_normal((4, 8)), rng.standard_normal(4) * 3) for _ in range(3)]
     (a, la), (b, lb), (c, lc) = parts
