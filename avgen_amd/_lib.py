@@ -38,6 +38,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr, c_size,
          c_ptr],
     ),
+    "avattn_fwd_noalloc": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p,
+         c_ptr,
+         c_ptr],
+    ),
     "avattn_fwd_windowed": (
         ctypes.c_int,
         [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
@@ -169,6 +180,10 @@ ERR_WORKSPACE = 6
 ERR_LAUNCH = 7
 ERR_TOO_LARGE = 8
 ERR_ARGUMENT = 9
+ERR_SCRATCH = 10
+
+#: Bytes of avattn_fwd_noalloc's fixed per-GPU scratch (AVATTN_FWD_NOALLOC_SCRATCH).
+FWD_NOALLOC_SCRATCH = 64 << 20
 
 # avattn_bwd flags (include/avattn.h).
 BWD_REUSE_QUERY_SIDE = 1

@@ -5,6 +5,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 #include "avattn_kernels.h"
 
 using namespace avattn;
@@ -182,11 +184,14 @@ const char* avattn_strerror(int status) {
     case AVATTN_ERR_LAUNCH: return "HIP kernel launch failed";
     case AVATTN_ERR_TOO_LARGE: return "problem size exceeds the 32-bit grid/index range";
     case AVATTN_ERR_ARGUMENT: return "invalid argument";
+    case AVATTN_ERR_SCRATCH:
+      return "problem needs more device scratch than avattn_fwd_noalloc's fixed array "
+             "(AVATTN_FWD_NOALLOC_SCRATCH = 64 MiB); use avattn_fwd with a workspace";
     default: return "unknown avattn status";
   }
 }
 
-int avattn_abi_version(void) { return 8; }
+int avattn_abi_version(void) { return 9; }
 
 }  // extern "C"
 
@@ -733,3 +738,68 @@ int avattn_ring_dq_finish(const float* dq_acc, const int64_t* dq_acc_strides, in
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward
+// ---------------------------------------------------------------------------
+// The forward's workspace (padded k/v copies, key bias and flags, k row-norm
+// maxima) lives in this array instead of a caller buffer.  Each GPU the
+// library runs on holds its own copy, at its own address, until the process
+// ends.  Nothing in it needs clearing between calls: every region the
+// kernels read is fully written by the same call first (the copies, bias and
+// flags of every padded key, one norm maximum per 64-key tile).  In host code
+// `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress, once per device.
+static __device__ __align__(256) unsigned char scratch[AVATTN_FWD_NOALLOC_SCRATCH];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 128;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device, with that device current).
+int scratch_on_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return AVATTN_ERR_LAUNCH;
+  if (dev >= kMaxScratchDevices) return AVATTN_ERR_ARGUMENT;
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess) return AVATTN_ERR_LAUNCH;
+    if (sdev != dev) return AVATTN_ERR_ARGUMENT;  // the array of another GPU
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) return AVATTN_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return AVATTN_OK;
+}
+
+}  // namespace
+
+extern "C" int avattn_fwd_noalloc(const void* q, const void* k, const void* v, const int64_t* q_strides,
+                                  const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
+                                  int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim,
+                                  const uint8_t* key_mask, int64_t key_mask_batch_stride, const float* rope_cos_q,
+                                  const float* rope_sin_q, int64_t rope_batch_stride, float scale, void* out,
+                                  const int64_t* out_strides, float* lse, avattn_stream_t stream) {
+  // Size checks first (no HIP call on a rejected problem); fwd_impl repeats
+  // the rest of the validation before it launches anything.
+  const int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  const size_t need = avattn_fwd_workspace_size(batch, heads_kv, len_k, head_dim);
+  if (need > AVATTN_FWD_NOALLOC_SCRATCH) return AVATTN_ERR_SCRATCH;
+  void* ws = nullptr;
+  if (need > 0 && (int64_t)batch * heads_q * len_q > 0) {
+    const int s = scratch_on_current_device(reinterpret_cast<hipStream_t>(stream), &ws);
+    if (s != AVATTN_OK) return s;
+  }
+  return fwd_impl(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
+                  key_mask, key_mask_batch_stride, rope_cos_q, rope_sin_q, rope_batch_stride, false, nullptr,
+                  nullptr, scale, out, out_strides, lse, ws, ws ? AVATTN_FWD_NOALLOC_SCRATCH : 0, stream);
+}

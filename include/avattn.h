@@ -66,6 +66,8 @@ typedef void* avattn_stream_t;
 #define AVATTN_ERR_LAUNCH           7  /* HIP reported an error at launch          */
 #define AVATTN_ERR_TOO_LARGE        8  /* a size exceeds the 32-bit index range    */
 #define AVATTN_ERR_ARGUMENT         9  /* other invalid argument                   */
+#define AVATTN_ERR_SCRATCH         10  /* avattn_fwd_noalloc: problem exceeds its  */
+                                       /* fixed device scratch                     */
 
 /* Human-readable text for a status code (static storage, never NULL). */
 const char* avattn_strerror(int status);
@@ -103,6 +105,35 @@ int avattn_fwd(const void* q, const void* k, const void* v,
                float* lse,
                void* workspace, size_t workspace_bytes,
                avattn_stream_t stream);
+
+/*
+ * avattn_fwd without a workspace argument and without any allocation: no
+ * counterpart in the reference; for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The operand copies and key statistics avattn_fwd keeps
+ * in its workspace go to a fixed device array of AVATTN_FWD_NOALLOC_SCRATCH
+ * bytes that the library holds on each GPU it runs on until the process
+ * ends; a problem whose avattn_fwd_workspace_size() exceeds it returns
+ * AVATTN_ERR_SCRATCH (nothing launched).  The caller still provides q, k, v,
+ * out and lse.  The stream must belong to the current device.  Calls that
+ * overlap on one GPU (concurrent streams, threads) share the array and race:
+ * order them.  The first call on a device looks the array up
+ * (hipGetSymbolAddress) and may return AVATTN_ERR_LAUNCH if that fails.
+ * Every other argument and result is that of avattn_fwd, bit for bit.
+ */
+#define AVATTN_FWD_NOALLOC_SCRATCH ((size_t)64 << 20)
+int avattn_fwd_noalloc(const void* q, const void* k, const void* v,
+                       const int64_t* q_strides, const int64_t* k_strides,
+                       const int64_t* v_strides,
+                       int32_t batch, int32_t heads_q, int32_t heads_kv,
+                       int32_t len_q, int32_t len_k, int32_t head_dim,
+                       const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                       const float* rope_cos_q, const float* rope_sin_q,
+                       int64_t rope_batch_stride,
+                       float scale,
+                       void* out, const int64_t* out_strides,
+                       float* lse,
+                       avattn_stream_t stream);
 
 /*
  * Workspace bytes avattn_fwd needs for these sizes: a row-major copy of k and

@@ -51,8 +51,8 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 8
-    for code in range(0, 10):
+    assert lib.avattn_abi_version() == 9
+    for code in range(0, 11):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
 
@@ -156,6 +156,27 @@ def test_fwd_validation_paths(lib):
     # empty problems succeed without any launch
     assert _fwd(lib, Lq=0) == _lib.OK
     assert _fwd(lib, B=0) == _lib.OK
+
+
+@cpu_only
+def test_fwd_noalloc_rejects_before_any_device_call(lib):
+    """Shape errors and problems beyond the fixed scratch return before the
+    library touches the device (no GPU here: a HIP call would fail)."""
+    s = _lib.i64_array([1 << 30, 1 << 20, 128])
+
+    def call(B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128):
+        return lib.avattn_fwd_noalloc(16, 16, 16, s, s, s, B, Hq, Hkv, Lq, Lk, D, None, 0, None, None, 0, 0.125,
+                                      16, s, 16, None)
+
+    assert call(D=96) == _lib.ERR_HEAD_DIM
+    assert call(Hq=3) == _lib.ERR_GQA
+    assert call(Lk=-1) == _lib.ERR_BAD_SHAPE
+    # k and v copies of (1, 2, 2^17, 128) bf16 are 128 MiB > 64 MiB
+    assert lib.avattn_fwd_workspace_size(1, 2, 1 << 17, 128) > _lib.FWD_NOALLOC_SCRATCH
+    assert call(Lk=1 << 17) == _lib.ERR_SCRATCH
+    assert lib.avattn_fwd_workspace_size(1, 2, 60000, 128) <= _lib.FWD_NOALLOC_SCRATCH
+    assert call(Lq=0) == _lib.OK
+    assert b"64 MiB" in lib.avattn_strerror(_lib.ERR_SCRATCH)
 
 
 def _fwd_windowed(lib, lo=32, hi=32, wb=0, **over):
