@@ -36,6 +36,8 @@ import torch
 ROOT = Path(__file__).resolve().parent
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (AMD spec)
 PEAK_HBM_GBS = 8000.0
+PEAK_FP8_TFLOPS = 5033.2  # MI355X dense fp8 MFMA (AMD spec)
+PEAK_MIXED_FP8_BF16_TFLOPS = 1.0 / (0.5 / PEAK_FP8_TFLOPS + 0.5 / PEAK_BF16_TFLOPS)
 
 # Algorithmic MFMA work each kernel performs under the FLOP convention, in
 # units of 2*B*H*Lq*Lk*D (one Lq x Lk x D product): the forward does QK^T and
@@ -247,6 +249,21 @@ def dq_ds_roofline(cfg: dict, timing: dict, steps: int, workload: str):
             "traffic": load_traffic("bwd_dq_ds", workload)}
 
 
+def ds_plan(cfg: dict, device) -> dict:
+    """How the backward staged dS for one KV chunk: the (fixed, per device)
+    budget, the (batch, kv head) pairs per pass and the number of passes."""
+    import avgen_amd
+
+    B, H, Lq, L, D, cp = cfg["B"], cfg["H"], cfg["Lq"], cfg["L"], cfg["D"], cfg["cp"]
+    lc = L // cp
+    per = avgen_amd.ops.ds_bytes_per_pair(1, Lq, lc)
+    budget = avgen_amd.ops._ds_budget(device)
+    _, staged = avgen_amd.ops.bwd_workspace_plan(B, H, H, Lq, lc, D, device)
+    pairs = min(B * H, budget // max(per, 1)) if staged else 0
+    passes = -(-(B * H) // pairs) if pairs else 0
+    return {"budget_bytes": budget, "bytes_per_pair": per, "staged": staged, "passes_per_chunk": passes}
+
+
 CALIBRATION_BYTES = 1 << 30  # float32 elements read and written by torch.neg
 
 
@@ -316,6 +333,98 @@ def ingest_pmc(fetch_csv: str, write_csv: str, kernel: str, workload: str) -> di
     return result
 
 
+MFMA_COUNTERS = ("SQ_INSTS_MFMA", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CYCLES", "SQ_WAVE_CYCLES", "SQ_INSTS_VALU",
+                 "SQ_WAIT_INST_LDS", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "GRBM_GUI_ACTIVE", "GRBM_COUNT")
+_KERNEL_SYMBOLS = {"attn_fwd": "attn_fwd_kernel", "bwd_dkdv": "bwd_dkdv_kernel", "bwd_dq_ds": "bwd_dq_ds_kernel",
+                   "bwd_dq": "bwd_dq_kernel"}
+# MFMA instructions each kernel issues per algorithmic unit of work beyond
+# the counted ones (the dK/dV kernel recomputes S = Q K^T: 4 hardware units
+# for 3 counted).
+KERNEL_HW_UNITS = {"attn_fwd": 2, "bwd_dkdv": 4, "bwd_dq": 3, "bwd_dq_ds": 1}
+N_XCD, N_CU = 8, 256
+
+
+def ingest_mfma(counter_csv: str, stats_csv: str, workload: str) -> str:
+    """MFMA-utilisation summary of the attention kernels from one rocprofv3
+    --pmc pass over MFMA_COUNTERS and the --kernel-trace --stats run of the
+    same command: per kernel the counters per dispatch (summed over the
+    chip), the clock they imply (GRBM_GUI_ACTIVE per XCD / kernel duration),
+    MFMA utilisation by issue count (SQ_INSTS_MFMA x 32 cycles per
+    32x32x16 bf16 MFMA / (1024 SIMDs x kernel cycles)) and by busy cycles
+    (SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x kernel cycles)), and the hardware
+    FLOP rate (MFMA work actually issued, recompute included) against the
+    peak at that clock.  Writes profiles/<workload>_mfma_counters.md."""
+    import collections
+    import csv
+
+    per = collections.defaultdict(lambda: collections.defaultdict(lambda: collections.defaultdict(float)))
+    with open(counter_csv) as fh:
+        for row in csv.DictReader(fh):
+            for short, sym in _KERNEL_SYMBOLS.items():
+                if sym in row["Kernel_Name"]:
+                    did = row.get("Dispatch_Id") or row.get("Correlation_Id")
+                    per[short][row["Counter_Name"]][did] += float(row["Counter_Value"])
+    dur = {}
+    with open(stats_csv) as fh:
+        for row in csv.DictReader(fh):
+            for short, sym in _KERNEL_SYMBOLS.items():
+                if sym in row["Name"]:
+                    dur[short] = float(row["AverageNs"]) / 1e6  # ms
+    cfg = CONFIGS[workload]
+    B, H, Lq, L, D, cp = cfg["B"], cfg["H"], cfg["Lq"], cfg["L"], cfg["D"], cfg["cp"]
+    unit = 2.0 * B * H * Lq * (L // cp) * D  # one product per KV chunk launch
+    lines = [f"# MFMA utilisation counters — {workload} ({cfg['desc']})", "",
+             "Commands (repo root `R` on the GPU box, after `cd /tmp && export TMPDIR=/tmp`):", "", "```",
+             "timeout -s KILL 120 rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) +
+             f" --output-format csv -d $R/gpurun_out/mfma -o pmc -- python3 $R/bench.py --config {workload} "
+             "--steps 1 --warmup 1 --no-cpu-baseline",
+             "rocprofv3 --kernel-trace --stats --output-format csv -d $R/gpurun_out/trace -o prof -- python3 "
+             f"$R/bench.py --config {workload} --steps 5 --warmup 2 --no-cpu-baseline",
+             f"python bench.py --ingest-mfma <pmc_counter_collection.csv> <prof_kernel_stats.csv> --config {workload}",
+             "```", "",
+             "Counters per dispatch, summed over the chip (rocprofv3 reports one row per hardware instance).  "
+             "Clock = GRBM_GUI_ACTIVE / 8 XCDs / average duration of the same kernel in the trace run.  "
+             "Issue util = SQ_INSTS_MFMA x 32 cycles / (1024 SIMDs x kernel cycles).  "
+             "Busy util = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x kernel cycles) (the counter is per SIMD: it reads 32 cycles per MFMA issued).  "
+             "HW rate = MFMA work issued (recompute included: forward 2, dK/dV 4, dQ-from-dS 1 products per "
+             f"launch of {unit:.4g} FLOP each) / duration; its peak at the measured clock is "
+             "2516.6 TFLOP/s x clock / 2400 MHz.", "",
+             "| kernel | dispatches | avg ms | clock MHz | SQ_INSTS_MFMA | issue util | busy util | HW TFLOP/s | "
+             "HW / peak at clock | HW / 2516.6 | VALU per MFMA | LDS insts per MFMA | LDS wait / wave cycles | "
+             "LDS bank conflicts per LDS inst |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    summary = {}
+    for short in ("attn_fwd", "bwd_dkdv", "bwd_dq_ds", "bwd_dq"):
+        cs = per.get(short)
+        if not cs or short not in dur:
+            continue
+        avg = {c: sum(v.values()) / len(v) for c, v in cs.items()}
+        n = len(next(iter(cs.values())))
+        ms = dur[short]
+        cycles = avg.get("GRBM_GUI_ACTIVE", 0.0) / N_XCD
+        mhz = cycles / (ms * 1e3) if ms else 0.0
+        mfma = avg.get("SQ_INSTS_MFMA", 0.0)
+        issue = mfma * 32.0 / (4 * N_CU * cycles) if cycles else 0.0
+        busy = avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (4 * N_CU * cycles) if cycles else 0.0
+        hw = KERNEL_HW_UNITS[short] * unit / (ms / 1e3) / 1e12
+        peak_clk = PEAK_BF16_TFLOPS * mhz / 2400.0
+        valu = avg.get("SQ_INSTS_VALU", 0.0) / mfma if mfma else 0.0
+        lds = avg.get("SQ_INSTS_LDS", 0.0) / mfma if mfma else 0.0
+        wait = avg.get("SQ_WAIT_INST_LDS", 0.0) / avg["SQ_WAVE_CYCLES"] if avg.get("SQ_WAVE_CYCLES") else 0.0
+        conf = avg.get("SQ_LDS_BANK_CONFLICT", 0.0) / avg["SQ_INSTS_LDS"] if avg.get("SQ_INSTS_LDS") else 0.0
+        lines.append(f"| {short} | {n} | {ms:.3f} | {mhz:.0f} | {mfma:.4g} | {100 * issue:.1f}% | {100 * busy:.1f}% | "
+                     f"{hw:.0f} | {100 * hw / peak_clk:.1f}% | {100 * hw / PEAK_BF16_TFLOPS:.1f}% | {valu:.2f} | "
+                     f"{lds:.2f} | {100 * wait:.1f}% | {conf:.3f} |")
+        summary[short] = {"avg_ms": ms, "clock_mhz": mhz, "issue_util": issue, "busy_util": busy, "hw_tflops": hw,
+                          "counters": avg}
+    lines += ["", "Raw counter averages per dispatch:", ""]
+    for short, s in summary.items():
+        lines.append(f"* `{short}`: " + ", ".join(f"{c} {v:.6g}" for c, v in sorted(s["counters"].items())))
+    text = "\n".join(lines) + "\n"
+    (ROOT / "profiles" / f"{workload}_mfma_counters.md").write_text(text)
+    return text
+
+
 def bench_c5(cfg: dict, steps: int, warmup: int) -> dict:
     """Sampling-time forward (BASELINE config c5): `steps` repeated calls of
     the bf16 forward and of the fp8 q k^T forward (per-head absmax scales
@@ -373,7 +482,13 @@ def bench_c5(cfg: dict, steps: int, warmup: int) -> dict:
         "data": "synthetic (seeded N(0,1)/sqrt(2) q/k/v, rotated by the 3D RoPE of an 8-fps 2x2-patch grid)",
         "config": {"workload": cfg["desc"], "name": "c5", "batch": cfg["B"], "heads": cfg["H"],
                    "head_dim": cfg["D"], "len_q": cfg["Lq"], "len_k": cfg["L"]},
-        "pct_of_peak_bf16": round(100.0 * flops / (r8["ms_per_call"] / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 2),
+        # Half of the forward's FLOPs (q k^T) run on fp8 MFMA, half (P V) on
+        # bf16: at the dense peaks (5033.2 / 2516.6 TFLOP/s) the step's
+        # shortest time is F/2/5033.2 + F/2/2516.6, i.e. a mixed peak of
+        # 3355.5 TFLOP/s for this work split.
+        "peak_mixed_tflops": round(PEAK_MIXED_FP8_BF16_TFLOPS, 1),
+        "pct_of_peak_mixed": round(100.0 * flops / (r8["ms_per_call"] / 1e3) / 1e12 / PEAK_MIXED_FP8_BF16_TFLOPS, 2),
+        "bf16_pct_of_peak_bf16": round(100.0 * flops / (r16["ms_per_call"] / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 2),
         "bf16": {"tflops": round(flops / (r16["ms_per_call"] / 1e3) / 1e12, 2),
                  "ms_per_call": round(r16["ms_per_call"], 3), "kernel_avg_ms": r16["kernel_avg_ms"]},
         "fp8": {"tflops": round(flops / (r8["ms_per_call"] / 1e3) / 1e12, 2),
@@ -538,7 +653,7 @@ def bench_qknorm(cfg: dict, steps: int, warmup: int) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 10; 50 calls for c5)")
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
@@ -548,11 +663,20 @@ def main() -> int:
     ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc CSVs into profiles/traffic_<kernel>_<config>.json and exit")
     ap.add_argument("--kernel", default="bwd_dkdv", choices=sorted([*KERNEL_UNITS, "qk_norm", "qk_norm_bwd"]))
+    ap.add_argument("--ingest-mfma", nargs=2, metavar=("COUNTER_CSV", "KERNEL_STATS_CSV"),
+                    help="turn a rocprofv3 --pmc pass over MFMA_COUNTERS and a --kernel-trace --stats summary into "
+                         "profiles/<config>_mfma_counters.md and exit")
     args = ap.parse_args()
 
     if args.ingest_pmc:
         print(json.dumps(ingest_pmc(args.ingest_pmc[0], args.ingest_pmc[1], args.kernel, args.config)))
         return 0
+    if args.ingest_mfma:
+        print(ingest_mfma(args.ingest_mfma[0], args.ingest_mfma[1], args.config))
+        return 0
+    if args.steps is None:
+        # c5 is quoted on 50 repeated sampling calls; the other workloads on 10 steps
+        args.steps = 50 if args.config == "c5" else 10
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the ring is emulated on one "
@@ -666,6 +790,7 @@ def main() -> int:
             "traffic": load_traffic(dominant, args.config),
         },
         "roofline_hbm": dq_ds_roofline(cfg, per_kernel["bwd_dq_ds"], args.steps, args.config),
+        "ds_staging": ds_plan(cfg, dev),
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
