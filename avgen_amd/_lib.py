@@ -266,6 +266,7 @@ KERNEL_IDS = {
     "qk_norm": 11,
     "qk_norm_bwd": 12,
     "ring_dq_finish": 13,
+    "dkv_reduce": 14,
 }
 
 

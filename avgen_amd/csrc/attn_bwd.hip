@@ -133,7 +133,19 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
 
   const int nkt = (a.Lk + BK - 1) / BK;
   const int total = nkt * a.nkv;
-  const int bid = xcd_remap(blockIdx.x, total);
+  // Key blocks 0 .. nfull-1 take one workgroup each (query tiles all); the
+  // last a.nsplit blocks (the grid's partial last round) take a.nparts
+  // workgroups each, one per range of query tiles, whose fp32 partial
+  // dK/dV dkv_reduce_kernel sums.
+  const int nfull = total - a.nsplit;
+  int bid, part = -1;
+  if ((int)blockIdx.x < nfull) {
+    bid = xcd_remap(blockIdx.x, nfull);
+  } else {
+    const int i = blockIdx.x - nfull;
+    bid = nfull + i / a.nparts;
+    part = i % a.nparts;
+  }
   const int kt = bid % nkt;
   const int bhk = a.kv0 + bid / nkt;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
@@ -239,6 +251,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     }
     w_ia = __builtin_amdgcn_readfirstlane(c_a);
     w_ib = __builtin_amdgcn_readfirstlane(c_b);
+  }
+  if (part >= 0) {  // this part's share of the tiles (possibly none)
+    const int p0 = ntq * part / a.nparts, p1 = ntq * (part + 1) / a.nparts;
+    tq0 += p0;
+    ntq = p1 - p0;
   }
   const int niter = ntq * group;
   auto tile_head = [&](int it) { return it / ntq; };     // query head within the group
@@ -587,7 +604,20 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     }
   }
 
-  if (key < a.Lk) {
+  if (part >= 0) {
+    // Unscaled fp32 partial sums (masked keys and keys past the end as 0);
+    // dkv_reduce_kernel scales, rounds and rotates their total.
+    float* pp = a.dkv_part +
+                ((((int64_t)(bid - nfull) * a.nparts + part) * 2 + role) * BK + kw * 32 + l32) * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f32x4 w = {0.f, 0.f, 0.f, 0.f};
+        if (kvalid) w = f32x4{acc[dt][4 * g], acc[dt][4 * g + 1], acc[dt][4 * g + 2], acc[dt][4 * g + 3]};
+        *reinterpret_cast<f32x4*>(pp + dt * 32 + 8 * g + 4 * hh) = w;
+      }
+  } else if (key < a.Lk) {
     const float sc = role == 0 ? 1.f : a.scale;
     bf16* op = role == 0 ? a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl
                          : a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl;
@@ -614,6 +644,43 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
         *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * g + 4 * hh) = w;
       }
   }
+}
+
+// dk/dv of the split key blocks: one thread per (block, role, key, 4
+// channels) adds the parts' fp32 sums in part order, then scales, rounds to
+// bf16 and rotates dk back as the dK/dV kernel's own epilogue does.
+template <int D>
+__global__ __launch_bounds__(256) void dkv_reduce_kernel(BwdArgs a) {
+  constexpr int BK = 128, CQ = D / 4;
+  const int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (u >= (int64_t)a.nsplit * 2 * BK * CQ) return;
+  const int c = (int)(u % CQ);
+  const int r = (int)((u / CQ) % BK);
+  const int role = (int)((u / (CQ * BK)) % 2);
+  const int s = (int)(u / (CQ * BK * 2));
+  const int nkt = (a.Lk + BK - 1) / BK;
+  const int bid = nkt * a.nkv - a.nsplit + s;
+  const int kt = bid % nkt;
+  const int bhk = a.kv0 + bid / nkt;
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int key = kt * BK + r;
+  if (key >= a.Lk) return;
+  f32x4 t = {0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < a.nparts; ++p)
+    t += *reinterpret_cast<const f32x4*>(a.dkv_part + ((((int64_t)s * a.nparts + p) * 2 + role) * BK + r) * D + 4 * c);
+  const float sc = role == 0 ? 1.f : a.scale;
+  u32x2 w;
+  w[0] = pack_bf16x2(t[0] * sc, t[1] * sc);
+  w[1] = pack_bf16x2(t[2] * sc, t[3] * sc);
+  if (role == 1 && a.cos_k != nullptr) {
+    const int64_t ti = b * a.rksb + (int64_t)key * (D / 2) + 2 * c;  // pairs 2c, 2c + 1
+    const f32x2 c2 = *reinterpret_cast<const f32x2*>(a.cos_k + ti);
+    const f32x2 s2 = *reinterpret_cast<const f32x2*>(a.sin_k + ti);
+    w = rotate4(w, c2[0], s2[0], c2[1], s2[1], true);
+  }
+  bf16* op = role == 0 ? a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl
+                       : a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl;
+  *reinterpret_cast<u32x2*>(op + 4 * c) = w;
 }
 
 // ---------------------------------------------------------------------------
@@ -1152,6 +1219,14 @@ static void launch_dq_ds_d(const BwdArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, false>), grid, dim3(512), 0, stream, a);
 }
 
+// Compute units of the current device (0 if the query fails: no split).
+static int cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return n;
+}
+
 template <int D>
 static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t stream) {
   const bool mask = a.mask != nullptr;
@@ -1187,12 +1262,28 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
   const int step = a.ds ? kv_per_pass : nkv_all;
   const int nkt = (a.Lk + 127) / 128;
   const int group = a.Hq / a.Hkv;
+  const int cus = cu_count();
   for (int kv0 = 0; kv0 < nkv_all; kv0 += step) {
     BwdArgs p = a;
     p.kv0 = kv0;
     p.nkv = min(step, nkv_all - kv0);
+    // One 128-key block per workgroup, one workgroup per CU: a grid of
+    // total blocks runs in ceil(total / cus) rounds, the last one with
+    // total % cus blocks and the other CUs idle.  Those blocks are split
+    // over up to 8 workgroups each (ranges of query tiles) so that the last
+    // round is about as full as the others and 1/8 as long.
+    const int total = nkt * p.nkv;
+    p.nsplit = p.nparts = 0;
+    if (p.dkv_part != nullptr && cus > 0 && total > cus) {
+      const int rem = total % cus;
+      const int np = rem ? min(8, min(cus, kDkvSplitSlots) / rem) : 0;
+      if (np >= 2) {
+        p.nsplit = rem;
+        p.nparts = np;
+      }
+    }
     {
-      const dim3 grid(nkt * p.nkv);
+      const dim3 grid(total - p.nsplit + p.nsplit * p.nparts);
       LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup (8 waves) per CU: LDS-bound occupancy
       if (p.wlo) {  // windows (staged dS only)
         if (mask)
@@ -1210,6 +1301,11 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
         else
           hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false, false>), grid, dim3(512), 0, stream, p);
       }
+    }
+    if (p.nsplit > 0) {
+      const int64_t threads = (int64_t)p.nsplit * 2 * 128 * (D / 4);
+      LaunchTimer timer(kKidDkdvReduce, stream);
+      hipLaunchKernelGGL(dkv_reduce_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, p);
     }
     if (p.ds && !p.defer_dq) launch_dq_ds_d<D>(p, stream);
   }

@@ -149,7 +149,21 @@ struct BwdArgs {
   const float* cos_k;
   const float* sin_k;
   int64_t rksb;
+  // Split of the dK/dV grid's partial last round (null: no split): the last
+  // nsplit 128-key blocks of a pass each go to nparts workgroups, one per
+  // range of query tiles, which store fp32 partial sums here, slot (block -
+  // first split block, part, role 0 dv / 1 dk) of 128 x D floats; a
+  // reduction kernel adds the parts in order and writes dk/dv.
+  float* dkv_part;
+  int nsplit, nparts;
 };
+
+// The dK/dV grid split: at most kDkvSplitSlots workgroups of partial sums
+// (one round of a 256-CU device), of 2 * 128 * D floats each.
+constexpr int kDkvSplitSlots = 256;
+inline size_t dkv_part_bytes(int64_t dkv_blocks, int D) {
+  return dkv_blocks > kDkvSplitSlots ? (size_t)kDkvSplitSlots * 2 * 128 * D * sizeof(float) : 0;
+}
 
 // Bytes of staged dS per (b, kv head) pair.
 inline size_t ds_bytes_per_kv(int group, int Lq, int Lk) {
@@ -173,6 +187,7 @@ enum KernelId : int {
   kKidQkNorm = 11,
   kKidQkNormBwd = 12,
   kKidDqFinish = 13,
+  kKidDkdvReduce = 14,
 };
 
 // Records HIP events around one launch on `stream` while timing is enabled.

@@ -732,7 +732,7 @@ def main() -> int:
         log("[bench] calibration kernel done")
     per_kernel = {}
     for name in ("attn_fwd", "bwd_dkdv", "bwd_dq", "bwd_dq_ds", "bwd_preprocess", "lse_merge", "rope_apply",
-                 "transpose", "ring_dq_finish"):
+                 "transpose", "ring_dq_finish", "dkv_reduce"):
         ms, n = timing.read(name)
         per_kernel[name] = {"total_ms": ms, "launches": n, "avg_ms": ms / n if n else 0.0}
     timing.close()

@@ -177,6 +177,9 @@ BWD_CASES = [
     (1, 4, 2, 130, 257, 128, False),
     (1, 4, 4, 512, 512, 64, False),
     (2, 2, 1, 65, 97, 64, True),
+    # 2 x 141 = 282 key blocks of 128: on a 256-CU device the last 26 (the
+    # ragged last block among them) are split over 8 workgroups each
+    (1, 4, 2, 640, 17965, 128, True),
 ]
 
 

@@ -67,6 +67,9 @@ CASES = [
     (1, 4, 4, (4, 10, 25), 250, 4, 128, False),
     (2, 4, 2, (3, 8, 16), 96, 4, 64, True),
     (1, 2, 2, (2, 9, 20), 360, 1, 128, False),
+    # 2 x 4 x 35 = 280 key blocks per chunk: the dK/dV grid's last round is
+    # split (partial sums, then dk rotated back in the reduction)
+    (2, 4, 4, (7, 32, 40), 512, 2, 128, True),
 ]
 
 
