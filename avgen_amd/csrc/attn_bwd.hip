@@ -607,7 +607,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   if (part >= 0) {
     // Unscaled fp32 partial sums (masked keys and keys past the end as 0);
     // dkv_reduce_kernel scales, rounds and rotates their total.
-    float* pp = a.dkv_part +
+    float* pp = a.split_part +
                 ((((int64_t)(bid - nfull) * a.nparts + part) * 2 + role) * BK + kw * 32 + l32) * D;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -667,7 +667,7 @@ __global__ __launch_bounds__(256) void dkv_reduce_kernel(BwdArgs a) {
   if (key >= a.Lk) return;
   f32x4 t = {0.f, 0.f, 0.f, 0.f};
   for (int p = 0; p < a.nparts; ++p)
-    t += *reinterpret_cast<const f32x4*>(a.dkv_part + ((((int64_t)s * a.nparts + p) * 2 + role) * BK + r) * D + 4 * c);
+    t += *reinterpret_cast<const f32x4*>(a.split_part + ((((int64_t)s * a.nparts + p) * 2 + role) * BK + r) * D + 4 * c);
   const float sc = role == 0 ? 1.f : a.scale;
   u32x2 w;
   w[0] = pack_bf16x2(t[0] * sc, t[1] * sc);
@@ -1205,6 +1205,14 @@ __global__ void zero_rows_kernel(bf16* x, int64_t sb, int64_t sh, int64_t sl, in
   }
 }
 
+// Compute units of the current device (0 if the query fails: no split).
+static int cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return n;
+}
+
 template <int D>
 static void launch_dq_ds_d(const BwdArgs& a, hipStream_t stream) {
   const int group = a.Hq / a.Hkv;
@@ -1212,19 +1220,14 @@ static void launch_dq_ds_d(const BwdArgs& a, hipStream_t stream) {
   const dim3 grid(nqb * a.nkv * group);
   LaunchTimer timer(kKidBwdDqDs, stream);
   // 64-key stages, three buffers: measured faster than 32-key stages with
-  // four or six buffers (4.75 vs 4.9-5.4 ms per c3 chunk).
+  // four or six buffers (4.75 vs 4.9-5.4 ms per c3 chunk).  The grid's
+  // partial last round is not split as the dK/dV one is: this kernel is
+  // bound by HBM, and the last round's workgroups share all of it (measured:
+  // no gain at c3).
   if (a.wlo)
     hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, true>), grid, dim3(512), 0, stream, a);
   else
     hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, false>), grid, dim3(512), 0, stream, a);
-}
-
-// Compute units of the current device (0 if the query fails: no split).
-static int cu_count() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  return n;
 }
 
 template <int D>
@@ -1270,18 +1273,12 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
     // One 128-key block per workgroup, one workgroup per CU: a grid of
     // total blocks runs in ceil(total / cus) rounds, the last one with
     // total % cus blocks and the other CUs idle.  Those blocks are split
-    // over up to 8 workgroups each (ranges of query tiles) so that the last
-    // round is about as full as the others and 1/8 as long.
+    // over several workgroups each (ranges of query tiles) so that the last
+    // round is fuller and shorter.
     const int total = nkt * p.nkv;
-    p.nsplit = p.nparts = 0;
-    if (p.dkv_part != nullptr && cus > 0 && total > cus) {
-      const int rem = total % cus;
-      const int np = rem ? min(8, min(cus, kDkvSplitSlots) / rem) : 0;
-      if (np >= 2) {
-        p.nsplit = rem;
-        p.nparts = np;
-      }
-    }
+    const TailSplit ts = p.split_part ? plan_tail_split(total, cus, kSplitSlots) : TailSplit{0, 0};
+    p.nsplit = ts.nsplit;
+    p.nparts = ts.nparts;
     {
       const dim3 grid(total - p.nsplit + p.nsplit * p.nparts);
       LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup (8 waves) per CU: LDS-bound occupancy

@@ -94,10 +94,11 @@ FwdWorkspace fwd_workspace(int32_t B, int32_t Hkv, int32_t Lk, int32_t D, bool f
 }
 
 // Backward workspace: [lse2 | ndelta | q rows | dout rows | q^T | dout^T |
-// k rows | v rows | k^T | key bias | key tile flags | dK/dV split partials
-// (problems of more than 256 key blocks)], each region 256-byte aligned.
+// k rows | v rows | k^T | key bias | key tile flags | dK/dV tail-split
+// partials (problems of more than 256 key blocks)], each region 256-byte
+// aligned.
 struct BwdWorkspace {
-  size_t lse2, ndelta, qr, dor, qt, dot, kr, vr, kt, kbias, kfull, dkvp, total;
+  size_t lse2, ndelta, qr, dor, qt, dot, kr, vr, kt, kbias, kfull, split, total;
 };
 
 BwdWorkspace bwd_workspace(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32_t D) {
@@ -117,8 +118,8 @@ BwdWorkspace bwd_workspace(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32
   w.kt = w.vr + kcopy;
   w.kbias = w.kt + kcopy;
   w.kfull = w.kbias + kbias_bytes(B, Lkp);
-  w.dkvp = w.kfull + kfull_bytes(B, Lkp);
-  w.total = w.dkvp + dkv_part_bytes((int64_t)B * Hkv * ((Lk + 127) / 128), D);
+  w.split = w.kfull + kfull_bytes(B, Lkp);
+  w.total = w.split + split_part_bytes((int64_t)B * Hkv * ((Lk + 127) / 128), D);
   return w;
 }
 
@@ -451,7 +452,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
   a.kt = reinterpret_cast<bf16*>(ws + wl.kt);
   a.kbias = reinterpret_cast<float*>(ws + wl.kbias);
   a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
-  a.dkv_part = wl.total > wl.dkvp ? reinterpret_cast<float*>(ws + wl.dkvp) : nullptr;
+  a.split_part = wl.total > wl.split ? reinterpret_cast<float*>(ws + wl.split) : nullptr;
   a.Lqp = transpose_padded_len(len_q);
   a.Lkp = transpose_padded_len(len_k);
   a.kv0 = 0;

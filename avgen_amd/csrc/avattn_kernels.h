@@ -149,20 +149,48 @@ struct BwdArgs {
   const float* cos_k;
   const float* sin_k;
   int64_t rksb;
-  // Split of the dK/dV grid's partial last round (null: no split): the last
-  // nsplit 128-key blocks of a pass each go to nparts workgroups, one per
-  // range of query tiles, which store fp32 partial sums here, slot (block -
-  // first split block, part, role 0 dv / 1 dk) of 128 x D floats; a
-  // reduction kernel adds the parts in order and writes dk/dv.
-  float* dkv_part;
+  // Split of the dK/dV grid's partial last round (null: no split; see
+  // plan_tail_split): the last nsplit 128-key blocks of a pass each go to
+  // nparts workgroups, one per range of query tiles, which store fp32
+  // partial sums in slot (block - first split block) * nparts + part of
+  // 256 x D floats (dv rows, then dk rows); a reduction kernel adds the
+  // parts in order and writes dk and dv.
+  float* split_part;
   int nsplit, nparts;
 };
 
-// The dK/dV grid split: at most kDkvSplitSlots workgroups of partial sums
-// (one round of a 256-CU device), of 2 * 128 * D floats each.
-constexpr int kDkvSplitSlots = 256;
-inline size_t dkv_part_bytes(int64_t dkv_blocks, int D) {
-  return dkv_blocks > kDkvSplitSlots ? (size_t)kDkvSplitSlots * 2 * 128 * D * sizeof(float) : 0;
+// Partial-sum slots of the dK/dV tail split, 256 x D floats each; the
+// region is there when the grid (one workgroup per 128-key block) has more
+// workgroups than a 256-CU device runs at once.
+constexpr int kSplitSlots = 512;
+inline size_t split_part_bytes(int64_t dkv_blocks, int D) {
+  return dkv_blocks > 256 ? (size_t)kSplitSlots * 256 * D * sizeof(float) : 0;
+}
+
+// Split of a grid's partial last round.  A grid of `total` equal workgroups,
+// one per CU at a time on `cus` CUs, leaves r = total % cus of them alone in
+// its last round; giving each of those r to p workgroups of 1/p the work
+// makes that round ceil(r p / cus) / p as long.  Returns the p in 2..8 (r p
+// within max_slots) that makes it shortest, the smaller on ties, or no split
+// ({0, 0}) when none is shorter or the grid fits in one round.
+struct TailSplit {
+  int nsplit, nparts;
+};
+inline TailSplit plan_tail_split(int64_t total, int cus, int max_slots) {
+  TailSplit t{0, 0};
+  if (cus <= 0 || total <= cus) return t;
+  const int r = (int)(total % cus);
+  if (r == 0) return t;
+  int best_num = 1, best_den = 1;  // round length best_num / best_den
+  for (int p = 2; p <= 8 && r * p <= max_slots; ++p) {
+    const int num = (r * p + cus - 1) / cus;
+    if (num * best_den < best_num * p) {
+      best_num = num;
+      best_den = p;
+      t = TailSplit{r, p};
+    }
+  }
+  return t;
 }
 
 // Bytes of staged dS per (b, kv head) pair.

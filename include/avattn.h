@@ -147,9 +147,10 @@ size_t avattn_fwd_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k,
  * (softmax statistics), row-major and head_dim-major copies of q and dout,
  * row-major copies of k and v and a head_dim-major copy of k (sequences
  * padded to multiples of 64), plus the padded per-key bias and per-32-key
- * flags, plus, when batch * heads_kv * ceil(len_k / 128) exceeds 256,
- * 256 * 2 * 128 * head_dim floats of partial dk/dv for the workgroups that
- * share the dK/dV grid's last round (0 when there is nothing to do).
+ * flags, plus, when batch * heads_kv * ceil(len_k / 128) (dK/dV
+ * workgroups) exceeds 256, 512 * 256 * head_dim floats of partial sums for
+ * the workgroups that share the dK/dV grid's last round (0 when there is
+ * nothing to do).
  */
 size_t avattn_bwd_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
                                  int32_t len_q, int32_t len_k, int32_t head_dim);
@@ -534,8 +535,8 @@ int avattn_qk_norm_rope_bwd(const void* x, const int64_t* x_strides,
  * 7 operand copies (forward and backward operand preparation, including the
  * fp8 forward's e4m3 k copy), 8 fp8 forward, 9 fp8 absmax scales,
  * 10 dQ from staged dS, 11 q/k norm + rotation, 12 its backward,
- * 13 the ring dq finish (avattn_ring_dq_finish), 14 the sum of the split
- * dK/dV blocks' partial results.
+ * 13 the ring dq finish (avattn_ring_dq_finish), 14 the sum of the
+ * partial results of split dK/dV workgroups.
  * avattn_timing_begin creates `capacity` event pairs (call it outside any
  * timed or captured region); launches beyond capacity are not recorded and
  * make avattn_timing_read return AVATTN_ERR_WORKSPACE.

@@ -180,6 +180,8 @@ BWD_CASES = [
     # 2 x 141 = 282 key blocks of 128: on a 256-CU device the last 26 (the
     # ragged last block among them) are split over 8 workgroups each
     (1, 4, 2, 640, 17965, 128, True),
+    # 8 x 34 = 272 dQ workgroups of 256 query rows (a partial last round)
+    (1, 8, 4, 8465, 300, 64, True),
 ]
 
 

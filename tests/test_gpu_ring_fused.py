@@ -70,6 +70,9 @@ CASES = [
     # 2 x 4 x 35 = 280 key blocks per chunk: the dK/dV grid's last round is
     # split (partial sums, then dk rotated back in the reduction)
     (2, 4, 4, (7, 32, 40), 512, 2, 128, True),
+    # 8 heads x 34 blocks of 256 query rows, 2 x 8 x 35 key blocks: a long
+    # query shard (the oracle checks every 16th row)
+    (1, 8, 8, (5, 40, 44), 8465, 2, 64, True),
 ]
 
 
@@ -93,18 +96,20 @@ def test_fused_ring_bitwise_equals_unfused(amd, case):
     un = _run(amd, q, k, v, do, cp, mask, tq, tk, fused=False)
     for name, a, b in zip(("out", "lse", "dq", "dk", "dv"), fu, un):
         assert torch.equal(a, b), name
-    # and against the oracle (rotated in float32 exactly as the reference)
-    cq, sq = (x.cpu().numpy() for x in (tq.cos, tq.sin))
+    # and against the oracle (rotated in float32 exactly as the reference), on
+    # at most ~512 query rows (rows are independent)
+    step = max(1, Lq // 512)
+    cq, sq = (x.cpu().numpy()[:, :, ::step] for x in (tq.cos, tq.sin))
     ck, sk = (x.cpu().numpy() for x in (tk.cos, tk.sin))
-    qr = R.apply_rotary_bf16(q.float().cpu().numpy(), cq, sq)
+    qr = R.apply_rotary_bf16(q.float().cpu().numpy()[:, :, ::step], cq, sq)
     kr = R.apply_rotary_bf16(k.float().cpu().numpy(), ck, sk)
     vv = v.float().cpu().numpy()
     bounds = [R.shard_bounds(L, cp, r) for r in range(cp)]
     mk = None if mask is None else mask.cpu().numpy()
     ro, rl = R.ring_forward_f64(qr, [kr[:, :, a:b] for a, b in bounds], [vv[:, :, a:b] for a, b in bounds],
                                 None if mk is None else [mk[:, a:b] for a, b in bounds])
-    assert np.abs(fu[0].float().cpu().numpy() - ro).max() <= OUT_TOL
-    assert np.abs(fu[1].cpu().numpy() - rl).max() <= LSE_TOL
+    assert np.abs(fu[0].float().cpu().numpy()[:, :, ::step] - ro).max() <= OUT_TOL
+    assert np.abs(fu[1].cpu().numpy()[:, :, ::step] - rl).max() <= LSE_TOL
 
 
 def test_ring_nan_in_one_key_row_of_chunk_2(amd):
