@@ -535,7 +535,9 @@ def bench_windowed(cfg: dict, name: str, steps: int, warmup: int) -> dict:
         one()
         torch.cuda.synchronize()
         log(f"[bench] {name} warmup {i + 1}/{warmup} done")
-    with _lib.LaunchTiming(16 * steps + 16) as timing:
+    # dS passes x (dK/dV, its tail reduction, dQ) plus the copies: up to ~25
+    # launches per step at these workloads
+    with _lib.LaunchTiming(64 * steps + 64) as timing:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
