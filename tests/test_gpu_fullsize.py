@@ -116,6 +116,76 @@ def test_c3_ring_equals_unchunked_attention(amd):
         assert (lse_r[0, h, rows] - rl).abs().max().item() <= LSE_TOL
 
 
+def _video_coords(frames, height, width):
+    """(1, F*H*W, 3) coordinates of an 8-fps latent with 2x2 patches: (t, row, col)."""
+    t = torch.arange(frames, dtype=torch.float32) / 8.0
+    r = torch.arange(height, dtype=torch.float32) * 2.0
+    c = torch.arange(width, dtype=torch.float32) * 2.0
+    return torch.stack(torch.meshgrid(t, r, c, indexing="ij"), -1).reshape(1, -1, 3)
+
+
+def _unrotate32(x, cos, sin):
+    """Transpose of the interleaved-pair rotation in float32 (the gradient
+    through apply_rotary): pair (e, o) -> (e c + o s, o c - e s)."""
+    e, o = x[..., 0::2], x[..., 1::2]
+    return torch.stack((e * cos + o * sin, o * cos - e * sin), -1).flatten(-2)
+
+
+def test_c3_fused_ring_all_heads(amd):
+    """The bench's own path at its own size: the c3 query shard (18,900 rows)
+    over 4 KV chunks of the 21x45x80 latent with the 3D RoPE fused into the
+    ring's kernels.  For every one of the 40 heads: sampled query rows'
+    output, LSE and dq, and sampled keys' dk and dv (of the UNROTATED keys)
+    against float32 on the rotated operands (rotated exactly as
+    apply_rotary rotates them, which the other tests pin bit for bit)."""
+    B, H, Lq, L, D, cp = 1, 40, 18900, 75600, 128, 4
+    print(f"c3 fused ring B={B} H={H} Lq={Lq} L={L} cp={cp}", flush=True)
+    scale = D ** -0.5
+    tables = amd.rope.build_rotary_tables(_video_coords(21, 45, 80).cuda(), head_dim=D)
+    tq = tables.slice(0, Lq)
+    q = _rand((B, H, Lq, D), 30, 2 ** -0.5)
+    k, v = _rand((B, H, L, D), 31, 2 ** -0.5), _rand((B, H, L, D), 32, 2 ** -0.5)
+    do = _rand((B, H, Lq, D), 33, 1.0)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out, lse = amd.ring.ring_attention(qg, kg, vg, cp=cp, tables_q=tq, tables_k=tables)
+    out.backward(do)
+    qr, kr = amd.rope.apply_rotary(q, tq), amd.rope.apply_rotary(k, tables)
+    torch.cuda.synchronize()
+    rows = torch.arange(3, Lq, 149, device="cuda")  # 127 query rows
+    keys = torch.arange(5, L, 593, device="cuda")   # 128 keys, in every chunk
+    cq, sq = tq.cos[0, 0, rows], tq.sin[0, 0, rows]
+    ck, sk = tables.cos[0, 0, keys], tables.sin[0, 0, keys]
+    worst = [0.0] * 5
+    for h in range(H):
+        qh, kh, vh = qr[0, h].float(), kr[0, h].float(), v[0, h].float()
+        doh, oh = do[0, h].float(), out[0, h].float()
+        # rows: forward and dq over all 75,600 keys
+        ro, rl = _ref_rows(qr[0, h, rows], kr[0, h], v[0, h], scale)
+        e_o = (oh[rows] - ro).abs().max().item()
+        e_l = (lse[0, h, rows] - rl).abs().max().item()
+        s = torch.mm(qh[rows], kh.t().contiguous()) * scale
+        p = torch.exp(s - rl[:, None])
+        delta = (doh[rows] * oh[rows]).sum(-1)
+        ds = p * (torch.mm(doh[rows], vh.t().contiguous()) - delta[:, None])
+        rq = _unrotate32(torch.mm(ds, kh) * scale, cq, sq)
+        e_q = _max_rel(qg.grad[0, h, rows], rq)
+        del s, p, ds
+        # keys: dk (unrotated) and dv over all 18,900 query rows
+        s = torch.mm(qh, kh[keys].t().contiguous()) * scale
+        p = torch.exp(s - lse[0, h][:, None])
+        delta = (doh * oh).sum(-1)
+        ds = p * (torch.mm(doh, vh[keys].t().contiguous()) - delta[:, None])
+        rk = _unrotate32(torch.mm(ds.t().contiguous(), qh) * scale, ck, sk)
+        rv = torch.mm(p.t().contiguous(), doh)
+        e_k, e_v = _max_rel(kg.grad[0, h, keys], rk), _max_rel(vg.grad[0, h, keys], rv)
+        del s, p, ds
+        worst = [max(a, b) for a, b in zip(worst, (e_o, e_l, e_q, e_k, e_v))]
+    print(f"  worst over 40 heads: out {worst[0]:.2e} lse {worst[1]:.2e} dq {worst[2]:.2e} dk {worst[3]:.2e} "
+          f"dv {worst[4]:.2e}", flush=True)
+    assert worst[0] <= OUT_TOL and worst[1] <= LSE_TOL
+    assert max(worst[2:]) <= GRAD_REL_TOL
+
+
 def test_c4_joint_text_video_masked(amd):
     """c4 joint attention (2, 40, 76112, 128): 75,600 video tokens + 512 text
     slots, text lengths uniform in [16, 512] per sample (masked as keys).
