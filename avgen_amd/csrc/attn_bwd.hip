@@ -3,8 +3,8 @@
 //   1. preprocess: per query row, lse2 = lse * log2(e) and
 //      ndelta = -rowsum(dout * out) (the `D` term of dS = P * (dP - D)), in
 //      arrays padded to whole 64-row tiles (+inf / 0 past the end so padded
-//      rows get P = 0); plus the padded row-major and head_dim-major operand
-//      copies (prep.hip);
+//      rows get P = 0); plus the padded operand copies (prep.hip): row-major
+//      q and dout, head_dim-major k (and row-major k, v for 3'');
 //   2. dK/dV: one workgroup per 128 keys (32 per wave, kept in registers as
 //      MFMA operands); loops over 64-row query tiles of every query head
 //      that reads this KV head; with staged dS it also stores dS (bf16) to
@@ -14,11 +14,11 @@
 //          per 256 query rows streaming the dS once (bwd_dq_ds_kernel), or
 //      3''. recomputing S and dP: one workgroup per 256 query rows (32 per
 //          wave), 32-key tiles (bwd_dq_kernel).
-// Every MFMA operand read from LDS is one 16-byte chunk of a tile row (or,
-// for the staged dS, two transposed reads): the products contracting over
-// the sequence read head_dim-major tiles of the copies, and the rows feeding
-// the first product are read in perm23 order so that their C layout lines up
-// with those chunks.
+// Every MFMA operand read from LDS is one 16-byte chunk of a tile row or two
+// 8-byte transposed reads (ds_read_b64_tr_b16) of a row-major tile: the
+// products contracting over the sequence read their operands across the
+// rows, and the rows feeding the first product are read in perm23 order so
+// that their C layout lines up with those eight consecutive rows.
 // With out/lse the merged result over all KV chunks, the outputs are one
 // chunk's contributions, which is how the ring backward calls the op
 // (torch/.../_context_parallel/_attention.py:567-575).
@@ -76,14 +76,15 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 // (lane l supplies query row 32*sub + perm23(l % 32) to the first products):
 //   P waves (w < 4):   S  = Q K^T      A = Q rows (LDS)   B = K^T (registers)
 //                      P  = exp2(S*c - lse2[q])   -> bf16, handed to the partner
-//                      dV^T += dO^T P  A = dO^T (LDS, head_dim-major), B = P
+//                      dV^T += dO^T P  A = dO^T (LDS, transposed reads), B = P
 //   dS waves (w >= 4): dP = dO V^T     A = dO rows (LDS)  B = V^T (registers)
 //                      dS = P * (dP + ndelta[q])  (P from the partner)
-//                      dK^T += Q^T dS  A = Q^T (LDS, head_dim-major), B = dS
+//                      dK^T += Q^T dS  A = Q^T (LDS, transposed reads), B = dS
 // C-layout register 8*k2 + e of lane l holds query 32*sub + 16*k2 + 8*(l/32)
-// + e, so the A operands of the last products and the row statistics are
-// 16-byte LDS reads, and P travels between the partners as each lane's own
-// registers (one 16-byte LDS write and read per 16 rows).
+// + e, so the A operands of the last products are two transposed reads of
+// the row tiles (rows +0..3, +4..7), the row statistics 16-byte LDS reads,
+// and P travels between the partners as each lane's own registers (one
+// 16-byte LDS write and read per 16 rows).
 //
 // Two barriers per tile: T (tile staged) and X (P written).  Between T and X
 // each SIMD runs the P wave's QK^T MFMAs and softmax beside the dS wave's
@@ -103,10 +104,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   constexpr int BK = 128, BQ = 64, NW = 8;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BQ * D;
-  // Two double-buffered halves of a tile: the rows (read before the P
-  // hand-over) and the head_dim-major columns (read after it).  Each half is
-  // refilled as soon as the phase that reads it is over, so the row tiles are
-  // loaded two tiles ahead and the column tiles one and a half.
+  // Three stages of query tiles, each holding the Q and dO rows (and the
+  // rows' statistics).  The first products read them as rows; the last two
+  // read the same tiles transposed (ds_read_b64_tr_b16), so no head_dim-major
+  // copy is staged.  A tile is read until the end of its iteration, so tile
+  // t + 2 is loaded during iteration t into the stage tile t - 1 used.
   struct RowStage {
     bf16 q[TE];     // Q rows: TileLayout<D>
     bf16 dout[TE];  // dO rows: TileLayout<D>
@@ -115,12 +117,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     int wlo[WIN ? BQ : 4];  // key windows of the tile's rows (WIN)
     int whi[WIN ? BQ : 4];
   };
-  struct ColStage {
-    bf16 qt[TE];   // Q^T: D rows of BQ, TileLayout<BQ>
-    bf16 dot[TE];  // dO^T: TileLayout<BQ>
-  };
-  __shared__ __attribute__((aligned(16))) RowStage rs0, rs1;
-  __shared__ __attribute__((aligned(16))) ColStage cs0, cs1;
+  __shared__ __attribute__((aligned(16))) RowStage rs0, rs1, rs2;
   // P hand-over: 1 KB per (key group, sub, k2), lane-major.
   __shared__ __attribute__((aligned(16))) u32x4 sxp[4 * 2 * 2 * 64];
 
@@ -187,9 +184,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   int ro[KS];  // row tiles: chunk (16*ks + 8*hh) of row perm23(l32)
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) ro[ks] = TileLayout<D>::off(prow, 16 * ks + 8 * hh);
-  int to[4];  // head_dim-major tiles: chunk (32*sub + 16*k2 + 8*hh) of row l32 (+32*dt rows)
+  // Transposed reads of the same tiles (A operands of dV^T += dO^T P and
+  // dK^T += Q^T dS): channel block dt, rows 16*(2*sub + k2) + 8*hh + 4*h ..
+  // +3 for the read h = 0, 1.  In 16-lane group g, lane i points at the four
+  // channels 32*dt + 16*(g%2) + 4*(i%4) .. +3 of row 8*(g/2) + 4*h + i/4 and
+  // receives channel 32*dt + 16*(g%2) + i (= lane % 32) of the four rows, so
+  // the two reads give the eight consecutive rows of the operand's k slots.
+  // Rows advance by 16 per (sub, k2), which keeps the row swizzle, so the
+  // offsets are loop-invariant.
+  int tro[DT][2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) to[j] = TileLayout<BQ>::off(l32, 16 * j + 8 * hh);
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      tro[dt][h] = TileLayout<D>::off(8 * (lane >> 5) + 4 * h + ((lane & 15) >> 2),
+                                      32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
   u32x4* xp = sxp + kw * 4 * 64 + lane;  // + 64*(2*sub + k2)
 
   const int nqt = a.Lqp / BQ;
@@ -265,8 +274,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   const uint32_t qbytes = (uint32_t)group * a.Lqp * D * 2;
   const u32x4 rq = make_rsrc(a.qr + bq0 * a.Lqp * D, qbytes);
   const u32x4 rdo = make_rsrc(a.dor + bq0 * a.Lqp * D, qbytes);
-  const u32x4 rqt = make_rsrc(a.qt + bq0 * D * a.Lqp, qbytes);
-  const u32x4 rdot = make_rsrc(a.dot + bq0 * D * a.Lqp, qbytes);
   const u32x4 rl2 = make_rsrc(a.lse2 + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
   const u32x4 rnd = make_rsrc(a.ndelta + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
   // With STAGE only the P waves load tiles, so the dS waves' vector-memory
@@ -276,21 +283,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   constexpr int NWL = STAGE ? 4 : NW;
   const bool loader = !STAGE || role == 0;
   TileStager<BQ, D, NWL> rst;  // 64 rows of D channels (row stride D)
-  TileStager<D, BQ, NWL> tst;  // D rows of 64 queries (row stride Lqp)
   rst.init(D, STAGE ? kw : wave, lane);
-  tst.init(a.Lqp, STAGE ? kw : wave, lane);
 
-  // The row half of a tile is kRowHalf loads per wave and the column half
-  // kColHalf, issued one at a time so they can be spread between MFMAs (a
-  // burst of them at the start of a phase would hold up the wave's
-  // instruction stream).
-  constexpr int kRowOps = TileStager<BQ, D, NWL>::kPer, kColOps = TileStager<D, BQ, NWL>::kPer;
-  constexpr int kRowHalf = 2 * kRowOps + 2 + (WIN ? 2 : 0), kColHalf = 2 * kColOps;
+  // A tile is kRowHalf loads per wave, issued one at a time so they can be
+  // spread between MFMAs (a burst of them at the start of a phase would hold
+  // up the wave's instruction stream).
+  constexpr int kRowOps = TileStager<BQ, D, NWL>::kPer;
+  constexpr int kRowHalf = 2 * kRowOps + 2 + (WIN ? 2 : 0);
   auto tile_rows = [&](int it) {  // first row of tile `it` in the group's copies
     return (uint32_t)tile_head(it) * a.Lqp + (uint32_t)tile_idx(it) * BQ;
-  };
-  auto tile_cols = [&](int it) {  // byte offset of tile `it` in the head_dim-major copies
-    return ((uint32_t)tile_head(it) * D * a.Lqp + (uint32_t)tile_idx(it) * BQ) * 2;
   };
   // Window arrays of this batch (WIN); rows past Lq read as 0 (empty).
   u32x4 rwl = {0u, 0u, 0u, 0u}, rwh = {0u, 0u, 0u, 0u};
@@ -298,8 +299,12 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     rwl = make_rsrc(a.wlo + b * a.wsb, (uint32_t)a.Lq * 4);
     rwh = make_rsrc(a.whi + b * a.wsb, (uint32_t)a.Lq * 4);
   }
+  auto stage = [&](auto bufc) -> RowStage& {
+    constexpr int s = decltype(bufc)::value;
+    return s == 0 ? rs0 : (s == 1 ? rs1 : rs2);
+  };
   auto row_op = [&](int it, auto bufc, int i) {
-    RowStage& rsg = decltype(bufc)::value == 0 ? rs0 : rs1;
+    RowStage& rsg = stage(bufc);
     const uint32_t row0 = tile_rows(it);
     if (i < kRowOps)
       rst.stage_one(rsg.q, rq, row0 * D * 2, i);
@@ -314,17 +319,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     else
       dma4(rwh, lds_addr(rsg.whi), lane * 4, (uint32_t)tile_idx(it) * BQ * 4);
   };
-  auto col_op = [&](int it, auto bufc, int i) {
-    ColStage& csg = decltype(bufc)::value == 0 ? cs0 : cs1;
-    if (i < kColOps)
-      tst.stage_one(csg.qt, rqt, tile_cols(it), i);
-    else
-      tst.stage_one(csg.dot, rdot, tile_cols(it), i - kColOps);
-  };
-  // Loads issued per wave between two consecutive waits: one row half and one
-  // column half.  Waiting until at most that many are outstanding retires the
-  // older half the coming phase reads.
-  constexpr int kInFlight = kRowHalf + kColHalf;
+  // Loads issued per wave between two consecutive T waits: one tile.  Waiting
+  // until at most that many are outstanding retires the older tile, the one
+  // the coming iteration reads.
+  constexpr int kInFlight = kRowHalf;
   // Slots of a phase that issue its `count` loads: every second slot from
   // slot kLoad0 on (the start of a phase is left to its operand and
   // statistics reads); the rest follow the phase's loop.  Load i goes in slot
@@ -357,16 +355,14 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // MFMA and bunch the loads and the VALU work).
   auto body_p = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    using NextBuf = std::integral_constant<int, buf ^ 1>;
-    wait_vmem_n<kInFlight>();  // this tile's rows landed (for this wave)
-    barrier_lds();             // T: ... for every wave; the other column half is free
+    using LoadBuf = std::integral_constant<int, (buf + 2) % 3>;  // tile it + 2 (tile it - 1 is done)
+    wait_vmem_n<kInFlight>();  // this tile landed (for this wave)
+    barrier_lds();             // T: ... for every wave; tile it - 1's stage is free
     // The wave whose phase ends in VALU-dependent work gets issue priority:
     // P waves between T and X (softmax after QK^T), dS waves after X.
     __builtin_amdgcn_s_setprio(2);
-    const RowStage& rsg = buf == 0 ? rs0 : rs1;
-    const ColStage& csg = buf == 0 ? cs0 : cs1;
-    const int itc = min(it + 1, niter - 1);  // column half loaded now (the last tiles re-load)
-    const int itr = min(it + 2, niter - 1);  // row half loaded after X
+    const RowStage& rsg = stage(bufc);
+    const int itr = min(it + 2, niter - 1);  // loaded after X (the last tiles re-load)
 
     constexpr int NS = 2 * KS;  // QK^T MFMAs: (sub, ks)
     auto qop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.q + (j / KS) * 32 * D + ro[j % KS]); };
@@ -423,7 +419,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int sub = j / KS, ks = j % KS;
       s[sub] = mfma32(qa[j % kRA], kv[ks], s[sub]);
       if (j + kRA < NS) qa[j % kRA] = qop(j + kRA);
-      if (load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / kLoadStep);
       if (j >= 1 && j <= 8) l2_read(j - 1);
       if (j >= kLo) {
         const int n = NS - kLo;
@@ -432,8 +427,6 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = loads_in_loop(NS); i < kColHalf; ++i) col_op(itc, NextBuf(), i);
-#pragma unroll
     for (int q8 = NS - 1; q8 < 8; ++q8) l2_read(q8);  // what the loop had no slot for
     if (kLo >= NS) {
 #pragma unroll
@@ -441,15 +434,16 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int st = 0; st < 8; ++st) smx(1, st >> 2, st & 3);
-    wait_vmem_n<kInFlight>();  // this tile's columns landed (for this wave)
-    barrier_lds();             // X: P handed over, columns visible; this row half is free
+    barrier_lds();  // X: P handed over
     __builtin_amdgcn_s_setprio(0);
 
     // dV^T += dO^T P over the (sub, k2, dt) steps, reads four steps ahead.
     constexpr int NJ = 4 * DT;
     auto dot_op = [&](int j) {
       const int sk = j / DT, dt = j % DT;  // sk = 2*sub + k2
-      return *reinterpret_cast<const bf16x8*>(csg.dot + dt * 32 * BQ + to[sk]);
+      const bf16* base = rsg.dout + 16 * sk * D;
+      const bf16x4 lo = lds_read_tr16(base + tro[dt][0]), hi = lds_read_tr16(base + tro[dt][1]);
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     };
     bf16x8 opq[kRA];
 #pragma unroll
@@ -461,27 +455,22 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (j + kRA < NJ) opq[j % kRA] = dot_op(j + kRA);
       const int sk = j / DT, dt = j % DT;
       acc[dt] = mfma32(op, pb[sk >> 1][sk & 1], acc[dt]);
-      if (load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / kLoadStep);
+      if (load_slot(j, NJ, kRowHalf)) row_op(itr, LoadBuf(), (j - kLoad0) / kLoadStep);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, bufc, i);
+    for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, LoadBuf(), i);
   };
 
   auto body_ds = [&](int it, auto bufc) {
     constexpr int buf = decltype(bufc)::value;
-    using NextBuf = std::integral_constant<int, buf ^ 1>;
+    using LoadBuf = std::integral_constant<int, (buf + 2) % 3>;
     // With STAGE the dS waves load nothing: the barriers alone order them
     // after the P waves' counted waits.
-    auto wait_loads = [&]() {
-      if constexpr (!STAGE) wait_vmem_n<kInFlight>();
-    };
-    wait_loads();
+    if constexpr (!STAGE) wait_vmem_n<kInFlight>();
     barrier_lds();  // T
     __builtin_amdgcn_s_setprio(0);
-    const RowStage& rsg = buf == 0 ? rs0 : rs1;
-    const ColStage& csg = buf == 0 ? cs0 : cs1;
-    const int itc = min(it + 1, niter - 1);
+    const RowStage& rsg = stage(bufc);
     const int itr = min(it + 2, niter - 1);
     // This tile's two dS units (query groups 2*tile_idx(it) and +1).
     u32x4 rds = {0u, 0u, 0u, 0u};
@@ -516,16 +505,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int sub = j / KS, ks = j % KS;
       dp[sub] = mfma32(da[j % kRA], kv[ks], dp[sub]);
       if (j + kRA < NS) da[j % kRA] = dop(j + kRA);
-      if (!STAGE && load_slot(j, NS, kColHalf)) col_op(itc, NextBuf(), (j - kLoad0) / kLoadStep);
       if (j < 4) nd_read(1, j);  // KS >= 4: before sub 1's first MFMA
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (!STAGE) {
-#pragma unroll
-      for (int i = loads_in_loop(NS); i < kColHalf; ++i) col_op(itc, NextBuf(), i);
-    }
-    wait_loads();
-    barrier_lds();  // X: partner's P available, columns visible
+    barrier_lds();  // X: partner's P available
     __builtin_amdgcn_s_setprio(2);
 
     // dS for group g = 2*sub + k2 (4 steps of two elements) interleaved with
@@ -537,7 +520,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     constexpr int NJ = 4 * DT;
     auto qt_op = [&](int j) {
       const int g = j / DT, dt = j % DT;
-      return *reinterpret_cast<const bf16x8*>(csg.qt + dt * 32 * BQ + to[g]);
+      const bf16* base = rsg.q + 16 * g * D;
+      const bf16x4 lo = lds_read_tr16(base + tro[dt][0]), hi = lds_read_tr16(base + tro[dt][1]);
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     };
     bf16x8 opq[kRA];
 #pragma unroll
@@ -572,35 +557,37 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if constexpr (STAGE) {
         if (dt == 0) ds_store(g);
       }
-      if (!STAGE && load_slot(j, NJ, kRowHalf)) row_op(itr, bufc, (j - kLoad0) / kLoadStep);
+      if (!STAGE && load_slot(j, NJ, kRowHalf)) row_op(itr, LoadBuf(), (j - kLoad0) / kLoadStep);
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (!STAGE) {
 #pragma unroll
-      for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, bufc, i);
+      for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, LoadBuf(), i);
     }
   };
 
   retire_prologue_loads();
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  using B2 = std::integral_constant<int, 2>;
   if (loader && niter > 0) {  // niter is 0 when no window meets this block's keys
-    using B0 = std::integral_constant<int, 0>;
-    using B1 = std::integral_constant<int, 1>;
 #pragma unroll
     for (int i = 0; i < kRowHalf; ++i) row_op(0, B0(), i);
 #pragma unroll
-    for (int i = 0; i < kColHalf; ++i) col_op(0, B0(), i);
-#pragma unroll
     for (int i = 0; i < kRowHalf; ++i) row_op(min(1, niter - 1), B1(), i);
   }
+  // Tile it lives in stage it % 3.
   if (role == 0) {
-    for (int it = 0; it < niter; it += 2) {
-      body_p(it, std::integral_constant<int, 0>());
-      if (it + 1 < niter) body_p(it + 1, std::integral_constant<int, 1>());
+    for (int it = 0; it < niter; it += 3) {
+      body_p(it, B0());
+      if (it + 1 < niter) body_p(it + 1, B1());
+      if (it + 2 < niter) body_p(it + 2, B2());
     }
   } else {
-    for (int it = 0; it < niter; it += 2) {
-      body_ds(it, std::integral_constant<int, 0>());
-      if (it + 1 < niter) body_ds(it + 1, std::integral_constant<int, 1>());
+    for (int it = 0; it < niter; it += 3) {
+      body_ds(it, B0());
+      if (it + 1 < niter) body_ds(it + 1, B1());
+      if (it + 2 < niter) body_ds(it + 2, B2());
     }
   }
 
@@ -1237,10 +1224,12 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
     LaunchTimer timer(kKidTranspose, stream);
     hipError_t e = hipSuccess;
     if (!a.reuse_q) {
-      e = launch_prep_copies(a.q, a.qsb, a.qsh, a.qsl, a.B, a.Hq, a.Lq, D, a.qr, a.qt, stream, nullptr, a.cos_q,
+      // Row-major copies only: the dK/dV kernel reads its head_dim-major
+      // operands from the same tiles by transposed LDS reads.
+      e = launch_prep_copies(a.q, a.qsb, a.qsh, a.qsl, a.B, a.Hq, a.Lq, D, a.qr, nullptr, stream, nullptr, a.cos_q,
                              a.sin_q, a.rqsb);
       if (e == hipSuccess)
-        e = launch_prep_copies(a.dout, a.dosb, a.dosh, a.dosl, a.B, a.Hq, a.Lq, D, a.dor, a.dot, stream);
+        e = launch_prep_copies(a.dout, a.dosb, a.dosh, a.dosl, a.B, a.Hq, a.Lq, D, a.dor, nullptr, stream);
     }
     // The dK/dV kernel reads its own key rows from k and v; the row-major
     // copies serve only the recomputing dQ kernel (no staged dS), the

@@ -93,12 +93,12 @@ FwdWorkspace fwd_workspace(int32_t B, int32_t Hkv, int32_t Lk, int32_t D, bool f
   return w;
 }
 
-// Backward workspace: [lse2 | ndelta | q rows | dout rows | q^T | dout^T |
+// Backward workspace: [lse2 | ndelta | q rows | dout rows |
 // k rows | v rows | k^T | key bias | key tile flags | dK/dV tail-split
 // partials (problems of more than 256 key blocks)], each region 256-byte
 // aligned.
 struct BwdWorkspace {
-  size_t lse2, ndelta, qr, dor, qt, dot, kr, vr, kt, kbias, kfull, split, total;
+  size_t lse2, ndelta, qr, dor, kr, vr, kt, kbias, kfull, split, total;
 };
 
 BwdWorkspace bwd_workspace(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32_t D) {
@@ -111,9 +111,7 @@ BwdWorkspace bwd_workspace(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32
   w.ndelta = w.lse2 + stats;
   w.qr = w.ndelta + stats;
   w.dor = w.qr + qcopy;
-  w.qt = w.dor + qcopy;
-  w.dot = w.qt + qcopy;
-  w.kr = w.dot + qcopy;
+  w.kr = w.dor + qcopy;
   w.vr = w.kr + kcopy;
   w.kt = w.vr + kcopy;
   w.kbias = w.kt + kcopy;
@@ -445,8 +443,6 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
   a.ndelta = reinterpret_cast<float*>(ws + wl.ndelta);
   a.qr = reinterpret_cast<bf16*>(ws + wl.qr);
   a.dor = reinterpret_cast<bf16*>(ws + wl.dor);
-  a.qt = reinterpret_cast<bf16*>(ws + wl.qt);
-  a.dot = reinterpret_cast<bf16*>(ws + wl.dot);
   a.kr = reinterpret_cast<bf16*>(ws + wl.kr);
   a.vr = reinterpret_cast<bf16*>(ws + wl.vr);
   a.kt = reinterpret_cast<bf16*>(ws + wl.kt);

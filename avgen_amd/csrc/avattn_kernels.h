@@ -100,8 +100,6 @@ struct BwdArgs {
   // + d, head_dim-major copies (*t) at ((b*H + h)*D + d)*Lp + j.
   bf16* qr;
   bf16* dor;
-  bf16* qt;
-  bf16* dot;
   bf16* kr;
   bf16* vr;
   bf16* kt;

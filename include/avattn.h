@@ -144,7 +144,7 @@ size_t avattn_fwd_workspace_size(int32_t batch, int32_t heads_kv, int32_t len_k,
 
 /*
  * Workspace bytes avattn_bwd needs for these sizes: two floats per query row
- * (softmax statistics), row-major and head_dim-major copies of q and dout,
+ * (softmax statistics), row-major copies of q and dout,
  * row-major copies of k and v and a head_dim-major copy of k (sequences
  * padded to multiples of 64), plus the padded per-key bias and per-32-key
  * flags, plus, when batch * heads_kv * ceil(len_k / 128) (dK/dV

@@ -77,29 +77,28 @@ def test_workspace_size(lib):
     assert lp == 18944
     copy = 2 * 40 * 128 * lp * 2  # one bf16 copy of a (2, 40, 18900, 128) tensor
     stats = 2 * 40 * lp * 4
-    # backward: lse2 + ndelta, q/dout row + head_dim-major copies, k/v rows +
-    # k^T, and when the dK/dV grid (one workgroup per 128 keys of a (batch,
+    # backward: lse2 + ndelta, q/dout row copies, k/v rows + k^T, and when the dK/dV grid (one workgroup per 128 keys of a (batch,
     # kv head)) has more than 256 workgroups, 512 slots of 256 x head_dim
     # fp32 partial sums for the split of the grid's last round
     def split(D):
         return 512 * 256 * D * 4
 
     assert lib.avattn_bwd_workspace_size(2, 40, 40, 18900, 18900, 128) == (
-        2 * stats + 7 * copy + _key_regions(2, lp) + split(128))
+        2 * stats + 5 * copy + _key_regions(2, lp) + split(128))
     # exactly 256 dK/dV blocks (1 x 2 x 128 of 128 keys) and 2 dQ blocks: no region
     lp2 = _pad64(128 * 128)
     assert lib.avattn_bwd_workspace_size(1, 2, 2, 64, 128 * 128, 64) == (
-        2 * (2 * 64 * 4) + 4 * (2 * 64 * 64 * 2) + 3 * (2 * 64 * lp2 * 2) + _key_regions(1, lp2))
+        2 * (2 * 64 * 4) + 2 * (2 * 64 * 64 * 2) + 3 * (2 * 64 * lp2 * 2) + _key_regions(1, lp2))
     lp3 = _pad64(128 * 128 + 1)
     assert lib.avattn_bwd_workspace_size(1, 2, 2, 64, 128 * 128 + 1, 64) == (
-        2 * (2 * 64 * 4) + 4 * (2 * 64 * 64 * 2) + 3 * (2 * 64 * lp3 * 2) + _key_regions(1, lp3) + split(64))
+        2 * (2 * 64 * 4) + 2 * (2 * 64 * 64 * 2) + 3 * (2 * 64 * lp3 * 2) + _key_regions(1, lp3) + split(64))
     # one dK/dV block per head (40 x 74 dQ workgroups do not count): no region
     assert lib.avattn_bwd_workspace_size(1, 40, 40, 18900, 64, 128) == (
-        2 * (40 * lp * 4) + 4 * (40 * 128 * lp * 2) + 3 * (40 * 128 * 64 * 2) + _key_regions(1, 64))
+        2 * (40 * lp * 4) + 2 * (40 * 128 * lp * 2) + 3 * (40 * 128 * 64 * 2) + _key_regions(1, 64))
     # GQA: k/v copies have heads_kv heads (len_k 70 pads to 128, len_q 10 to 64).
     got = lib.avattn_bwd_workspace_size(1, 4, 2, 10, 70, 64)
-    assert got == 2 * (4 * 64 * 4) + 4 * (4 * 64 * 64 * 2) + 3 * (2 * 64 * 128 * 2) + _key_regions(1, 128)
-    assert lib.avattn_bwd_workspace_size(1, 1, 1, 1, 1, 64) == 2 * 256 + 7 * 64 * 64 * 2 + _key_regions(1, 64)
+    assert got == 2 * (4 * 64 * 4) + 2 * (4 * 64 * 64 * 2) + 3 * (2 * 64 * 128 * 2) + _key_regions(1, 128)
+    assert lib.avattn_bwd_workspace_size(1, 1, 1, 1, 1, 64) == 2 * 256 + 5 * 64 * 64 * 2 + _key_regions(1, 64)
     assert lib.avattn_bwd_workspace_size(0, 40, 40, 10, 10, 128) == 0
     # forward: k rows + v^T copies of (B, Hkv, Lk, D), key bias/flags, one
     # max squared k row norm per (b, kv head, 64-key tile)
