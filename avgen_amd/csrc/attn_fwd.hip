@@ -24,14 +24,18 @@ namespace avattn {
 // workgroup per CU; K/V tiles of 64 keys.  Waves 0-3 (group A) and 4-7
 // (group B) share the SIMDs pairwise and run the same per-tile work
 //   S = K Q^T (16 MFMAs), softmax (VALU), O^T += V^T P^T (16 MFMAs)
-// in a staggered order: group A does QK^T(t), softmax(t), PV(t) in iteration
-// t; group B is one tile behind and does softmax(t-1), PV(t-1), QK^T(t) (its
-// scores are carried in registers across the barrier).  Each group's softmax
-// thus runs while the other group's MFMAs keep the matrix pipe busy, and wave
-// priorities (s_setprio) give the MFMA phases first claim on issue.  K rows
-// and V^T come from padded copies through four LDS stages: tile t+2 is loaded
-// during iteration t (spread between MFMAs), tile t-1 stays resident for
-// group B.
+// in a staggered order: in iteration t group A does PV(t-1), QK^T(t) and then
+// softmax(t) (its probabilities are carried in registers across the
+// barrier), group B does softmax(t-1) and then PV(t-1), QK^T(t) (its scores
+// are carried).  Each iteration of each wave is thus one MFMA phase and one
+// VALU phase, in opposite order in the two groups, so on every SIMD one
+// wave's softmax runs while the other wave's MFMAs keep the matrix pipe busy;
+// wave priorities (s_setprio) give the MFMA phases first claim on issue.  (With
+// group A in the order QK^T(t), softmax(t), PV(t) the two softmax phases
+// overlapped each other instead: 6.80 vs 5.84 ms per c3 chunk.)  K rows and
+// V^T come from padded copies through four LDS stages: tile t+2 is loaded
+// during iteration t (spread between MFMAs), tile t-1 stays resident for the
+// PV products.
 //
 // FP8: q k^T on e4m3 operands (v_mfma_f32_32x32x64_f8f6f4, twice the bf16
 // rate): q is quantized on load with its head's scale, K comes from the e4m3
@@ -425,36 +429,59 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
     bf16x8 pf[2][2];
     // Tile t0 + i uses stage i % 4.
     if (wave < NW / 2) {
-      // Group A: QK^T(t), softmax(t), PV(t).
+      // Group A: PV(t-1), QK^T(t), softmax(t); the probabilities of tile t
+      // are carried to the next iteration.  Each iteration is one MFMA
+      // phase (PV, QK^T) and then one VALU phase (softmax), the reverse of
+      // group B's, so on each SIMD one wave's softmax runs beside the other
+      // wave's MFMAs.
       auto body = [&](int t, auto bufc) __attribute__((always_inline)) {
         constexpr int buf = decltype(bufc)::value;
+        using Prev = std::integral_constant<int, (buf + 3) % 4>;
         using Next2 = std::integral_constant<int, (buf + 2) % 4>;
         top();
         const Stage& sg = stage_ref(bufc);
         __builtin_amdgcn_s_setprio(2);
         const int tl = min(t + 2, tend - 1);
         if constexpr (FP8) {
+          pv(stage_ref(Prev()), pf, loads_in(tl, Next2()));
+          loads_after(tl, Next2(), 4 * DT);
           scores(sg, sh, no_slot);
         } else {
+          pv(stage_ref(Prev()), pf, no_slot);
           scores(sg, sh, loads_in(tl, Next2()));
           loads_after(tl, Next2(), 2 * KS);
         }
         __builtin_amdgcn_s_setprio(0);
         softmax(sg, sh, pf, t);
+      };
+      {
+        // Iteration 0: QK^T(t0), softmax(t0).
+        using B0 = std::integral_constant<int, 0>;
+        using B2 = std::integral_constant<int, 2>;
+        top();
         __builtin_amdgcn_s_setprio(2);
         if constexpr (FP8) {
-          pv(sg, pf, loads_in(tl, Next2()));
-          loads_after(tl, Next2(), 4 * DT);
+          scores(stage_ref(B0()), sh, no_slot);
+#pragma unroll
+          for (int i = 0; i < kStageOps; ++i) stage_op(min(t0 + 2, tend - 1), B2(), i);
         } else {
-          pv(sg, pf, no_slot);
+          scores(stage_ref(B0()), sh, loads_in(min(t0 + 2, tend - 1), B2()));
+          loads_after(min(t0 + 2, tend - 1), B2(), 2 * KS);
         }
-      };
-      for (int t = t0; t < tend; t += 4) {
-        body(t, std::integral_constant<int, 0>());
-        if (t + 1 < tend) body(t + 1, std::integral_constant<int, 1>());
-        if (t + 2 < tend) body(t + 2, std::integral_constant<int, 2>());
-        if (t + 3 < tend) body(t + 3, std::integral_constant<int, 3>());
+        __builtin_amdgcn_s_setprio(0);
+        softmax(stage_ref(B0()), sh, pf, t0);
       }
+      for (int t = t0 + 1; t < tend; t += 4) {
+        body(t, std::integral_constant<int, 1>());
+        if (t + 1 < tend) body(t + 1, std::integral_constant<int, 2>());
+        if (t + 2 < tend) body(t + 2, std::integral_constant<int, 3>());
+        if (t + 3 < tend) body(t + 3, std::integral_constant<int, 0>());
+      }
+      // Tail: PV of the last tile (its stage is not refilled).
+      const int bl = (ntile - 1) % 4;
+      const Stage& sl = bl == 0 ? st0 : (bl == 1 ? st1 : (bl == 2 ? st2 : st3));
+      __builtin_amdgcn_s_setprio(2);
+      pv(sl, pf, no_slot);
     } else {
       // Group B: softmax(t-1), PV(t-1), QK^T(t); the scores of tile t are
       // carried to the next iteration.
