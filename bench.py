@@ -652,6 +652,34 @@ def bench_qknorm(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
+def gemm_reference(device, steps: int) -> dict:
+    """The vendor GEMM (torch.matmul in bf16, hipBLASLt/rocBLAS) on this box:
+    what a library kernel of pure MFMA work sustains under the same power
+    limit, as a reference for the attention kernels' rates (not part of the
+    metric)."""
+    out = {"metric": "torch.matmul bf16 TFLOP/s (vendor GEMM reference)", "unit": "TFLOP/s",
+           "peak_bf16": PEAK_BF16_TFLOPS, "sizes": []}
+    for n in (8192, 16384):
+        g = torch.Generator(device=device).manual_seed(n)
+        a = torch.randn(n, n, device=device, dtype=torch.bfloat16, generator=g)
+        b = torch.randn(n, n, device=device, dtype=torch.bfloat16, generator=g)
+        for _ in range(3):
+            c = a @ b
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        tf = 2.0 * n ** 3 / ms / 1e9
+        out["sizes"].append({"m_n_k": n, "ms": round(ms, 3), "tflops": round(tf, 1),
+                             "pct_of_peak": round(100.0 * tf / PEAK_BF16_TFLOPS, 2)})
+        del a, b, c
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -668,6 +696,8 @@ def main() -> int:
     ap.add_argument("--ingest-mfma", nargs=2, metavar=("COUNTER_CSV", "KERNEL_STATS_CSV"),
                     help="turn a rocprofv3 --pmc pass over MFMA_COUNTERS and a --kernel-trace --stats summary into "
                          "profiles/<config>_mfma_counters.md and exit")
+    ap.add_argument("--gemm-reference", action="store_true",
+                    help="time torch.matmul in bf16 (the vendor GEMM) on this box instead and exit")
     args = ap.parse_args()
 
     if args.ingest_pmc:
@@ -694,6 +724,9 @@ def main() -> int:
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.gemm_reference:
+        print(json.dumps(gemm_reference(dev, args.steps)), flush=True)
+        return 0
     if args.config == "c5":
         log(f"[bench] config c5: {cfg['desc']}")
         print(json.dumps(bench_c5(cfg, args.steps, args.warmup)), flush=True)
