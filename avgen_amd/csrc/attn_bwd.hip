@@ -186,19 +186,14 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   for (int ks = 0; ks < KS; ++ks) ro[ks] = TileLayout<D>::off(prow, 16 * ks + 8 * hh);
   // Transposed reads of the same tiles (A operands of dV^T += dO^T P and
   // dK^T += Q^T dS): channel block dt, rows 16*(2*sub + k2) + 8*hh + 4*h ..
-  // +3 for the read h = 0, 1.  In 16-lane group g, lane i points at the four
-  // channels 32*dt + 16*(g%2) + 4*(i%4) .. +3 of row 8*(g/2) + 4*h + i/4 and
-  // receives channel 32*dt + 16*(g%2) + i (= lane % 32) of the four rows, so
-  // the two reads give the eight consecutive rows of the operand's k slots.
-  // Rows advance by 16 per (sub, k2), which keeps the row swizzle, so the
-  // offsets are loop-invariant.
+  // +3 for the read h = 0, 1 (tr_read_off).  Rows advance by 16 per
+  // (sub, k2), which keeps the row swizzle, so the offsets are
+  // loop-invariant.
   int tro[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
-      tro[dt][h] = TileLayout<D>::off(8 * (lane >> 5) + 4 * h + ((lane & 15) >> 2),
-                                      32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
+    for (int h = 0; h < 2; ++h) tro[dt][h] = tr_read_off<D>(lane, dt, h);
   u32x4* xp = sxp + kw * 4 * 64 + lane;  // + 64*(2*sub + k2)
 
   const int nqt = a.Lqp / BQ;

@@ -269,6 +269,20 @@ struct TileLayout {
 // chunk from a transposed (sequence-contiguous) tile.
 __host__ __device__ __forceinline__ int perm23(int x) { return (x & ~12) | ((x & 4) << 1) | ((x & 8) >> 1); }
 
+// Element offset lane `lane` passes to transposed read h (0, 1) of a
+// row-major TileLayout<RL> tile, for the A operand of a product contracting
+// over the tile's rows (ds_read_b64_tr_b16: in each 16-lane group lane i
+// points at four consecutive elements of "row" i/4 and lane j receives
+// element j of the four rows).  Lane i of group g points at channels
+// 32*dt + 16*(g%2) + 4*(i%4) .. +3 of row 8*(g/2) + 4*h + i/4, so lane l
+// receives channel 32*dt + l%32 of rows 8*(l/32) + 4*h .. +3: the two reads
+// give the eight consecutive rows of its k slots.  For the 16-row step s add
+// 16*s*RL: the row swizzle repeats every 16 rows.
+template <int RL>
+__host__ __device__ __forceinline__ int tr_read_off(int lane, int dt, int h) {
+  return TileLayout<RL>::off(8 * (lane >> 5) + 4 * h + ((lane & 15) >> 2), 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3));
+}
+
 // 8 consecutive elements (one 16-byte chunk) of one row of a TileLayout<RL>
 // tile: an MFMA operand whose k index runs along the row.
 template <int RL>

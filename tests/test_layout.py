@@ -19,7 +19,10 @@ of 32 or 64 sequence positions, head_dim 64 and 128, 8 waves):
 * staged dS (``DsUnit``): the dK/dV kernel's stores cover every element of
   a unit once and stay in it, and the dQ kernel's stage loads plus
   transposed reads hand every lane the (row, key) pairs of its B operand,
-  for 64- and 32-key stages.
+  for 64- and 32-key stages;
+* ``tr_read_off``: the dK/dV kernel's transposed reads of the row-major Q
+  and dO tiles hand every lane channel ``32*dt + lane%32`` of the eight
+  consecutive rows of its A operand, for head_dim 128 and 64.
 """
 
 import shutil
@@ -154,7 +157,39 @@ void check_ds(int nkt) {
   }
 }
 
+// Transposed reads of row-major tiles (dK/dV kernel: Q^T and dO^T operands
+// from the Q and dO row tiles): lane l must receive channel 32*dt + l%32 of
+// rows 16*s + 8*(l/32) + 4*h + r, r = 0..3, for every 16-row step s.
+template <int RL, int ROWS>
+void check_tr_reads() {
+  using L = TileLayout<RL>;
+  // physical element -> (row, column)
+  std::vector<int> prow(ROWS * RL, -1), pcol(ROWS * RL, -1);
+  for (int r = 0; r < ROWS; ++r)
+    for (int c = 0; c < RL; ++c) {
+      const int o = L::off(r, c & ~3) + (c & 3);
+      prow[o] = r;
+      pcol[o] = c;
+    }
+  for (int s = 0; s < ROWS / 16; ++s)
+    for (int dt = 0; dt < RL / 32; ++dt)
+      for (int h = 0; h < 2; ++h)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int g = lane >> 4, j = lane & 15;
+          const int own = tr_read_off<RL>(lane, dt, h) + 16 * s * RL;
+          CHECK(own % 4 == 0 && own >= 0 && own + 4 <= ROWS * RL, "tr offset out of the tile\n");
+          for (int r = 0; r < 4; ++r) {
+            const int src_lane = 16 * g + 4 * r + j / 4;
+            const int el = tr_read_off<RL>(src_lane, dt, h) + 16 * s * RL + j % 4;
+            CHECK(prow[el] == 16 * s + 8 * (lane >> 5) + 4 * h + r && pcol[el] == 32 * dt + (lane & 31),
+                  "RL %d s %d dt %d h %d lane %d r %d: row %d col %d\n", RL, s, dt, h, lane, r, prow[el], pcol[el]);
+          }
+        }
+}
+
 int main() {
+  check_tr_reads<128, 64>();
+  check_tr_reads<64, 64>();
   check_ds<64>(3);
   check_ds<32>(2);
   check_tile<64, 128, 8>();  // forward K tile; dK/dV Q, dO row tiles (d128)
