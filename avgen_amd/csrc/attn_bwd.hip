@@ -86,11 +86,12 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 // and P travels between the partners as each lane's own registers (one
 // 16-byte LDS write and read per 16 rows).
 //
-// Two barriers per tile: T (tile staged) and X (P written).  Between T and X
-// each SIMD runs the P wave's QK^T MFMAs and softmax beside the dS wave's
-// dO V^T MFMAs; between X and the next T the P wave's dV MFMAs beside the dS
-// wave's dS arithmetic and dK MFMAs, so one wave's VALU work always has the
-// other's MFMAs to hide behind.  Keys that are masked (or past the end) are
+// One barrier per tile (T: tile staged).  The dS waves run their dS phase one
+// tile behind, so the P they need was written before the last barrier: in
+// iteration t a P wave runs QK^T and the softmax of tile t, then dV; its
+// partner runs dO V^T of tile t (low priority, MFMAs only), then dS and dK of
+// tile t - 1 (high priority), so one wave's VALU work always has the other's
+// MFMAs to hide behind.  Keys that are masked (or past the end) are
 // not special-cased in the loop: each key's dK/dV column depends only on that
 // key, and those columns are written as zeros (or not at all) at the end.
 // With STAGE the dS waves also store their dS tiles (BwdArgs::ds).  With WIN
@@ -104,22 +105,32 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   constexpr int BK = 128, BQ = 64, NW = 8;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BQ * D;
-  // Three stages of query tiles, each holding the Q and dO rows (and the
-  // rows' statistics).  The first products read them as rows; the last two
-  // read the same tiles transposed (ds_read_b64_tr_b16), so no head_dim-major
-  // copy is staged.  A tile is read until the end of its iteration, so tile
-  // t + 2 is loaded during iteration t into the stage tile t - 1 used.
+  // Query tiles are staged as Q rows and as dO rows plus the rows'
+  // statistics, three slots of each (tile t in slot t % 3).  The first
+  // products read the rows; the last two read the same tiles transposed
+  // (ds_read_b64_tr_b16), so no head_dim-major copy is staged.  Tile t's Q
+  // is read until the end of iteration t + 1 (dK^T), its dO and statistics
+  // until the end of iteration t: during iteration t the Q rows of tile t + 1
+  // and the rest of tile t + 2 are loaded, into the slots tiles t - 2 and
+  // t - 1 used.
   struct RowStage {
-    bf16 q[TE];     // Q rows: TileLayout<D>
     bf16 dout[TE];  // dO rows: TileLayout<D>
     float lse2[BQ];
     float ndl[BQ];  // ndelta: the dP accumulators start from it
     int wlo[WIN ? BQ : 4];  // key windows of the tile's rows (WIN)
     int whi[WIN ? BQ : 4];
   };
-  __shared__ __attribute__((aligned(16))) RowStage rs0, rs1, rs2;
-  // P hand-over: 1 KB per (key group, sub, k2), lane-major.
-  __shared__ __attribute__((aligned(16))) u32x4 sxp[4 * 2 * 2 * 64];
+  struct Smem {
+    bf16 q[3][TE];  // Q rows: TileLayout<D>
+    RowStage rs[3];
+    // P hand-over, one buffer per slot (tile t's P is written in iteration t
+    // and read in iteration t + 1): 1 KB per (key group, sub, k2),
+    // lane-major.
+    u32x4 xp[3][4 * 2 * 2 * 64];
+  };
+  __shared__ __attribute__((aligned(16))) Smem sm;
+  // Byte strides of the slots (the reads below add them to per-lane bases).
+  constexpr uint32_t kQS = TE * 2, kRS = sizeof(RowStage), kXS = sizeof(sm.xp[0]);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -194,7 +205,30 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int h = 0; h < 2; ++h) tro[dt][h] = tr_read_off<D>(lane, dt, h);
-  u32x4* xp = sxp + kw * 4 * 64 + lane;  // + 64*(2*sub + k2)
+  // Per-lane LDS byte addresses in slot 0 (opaque_lds: slot and row-block
+  // offsets go into the reads' offset fields).  P waves read Q as rows and
+  // dO transposed, dS waves dO as rows and Q transposed.
+  uint32_t rb[KS], tb[DT][2];
+  {
+    const uint32_t q0 = lds_addr(&sm.q[0][0]), d0 = lds_addr(&sm.rs[0].dout[0]);
+    const uint32_t rrow = role == 0 ? q0 : d0, rtr = role == 0 ? d0 : q0;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) rb[ks] = opaque_lds(rrow + 2 * ro[ks]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) tb[dt][h] = opaque_lds(rtr + 2 * tro[dt][h]);
+  }
+  // Row statistics of the lane's rows 8*hh + ...: lse2 at sb, ndelta and
+  // the windows at the offsets below.
+  const uint32_t sb = opaque_lds(lds_addr(&sm.rs[0].lse2[0]) + 32 * hh);
+  constexpr uint32_t kNdlOff = BQ * 4, kWloOff = 2 * BQ * 4, kWhiOff = kWloOff + sizeof(sm.rs[0].wlo);
+  static_assert(offsetof(RowStage, ndl) - offsetof(RowStage, lse2) == kNdlOff &&
+                    offsetof(RowStage, wlo) - offsetof(RowStage, lse2) == kWloOff &&
+                    offsetof(RowStage, whi) - offsetof(RowStage, lse2) == kWhiOff,
+                "row statistics offsets");
+  // This lane's 16 bytes of the P hand-over: + kXS*slot + 1024*(2*sub + k2).
+  const uint32_t xb = opaque_lds(lds_addr(&sm.xp[0][0]) + 16 * (kw * 4 * 64 + lane));
 
   const int nqt = a.Lqp / BQ;
   // Query tiles visited: tq0 .. tq0 + ntq - 1 of every query head of the
@@ -271,20 +305,15 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   const u32x4 rdo = make_rsrc(a.dor + bq0 * a.Lqp * D, qbytes);
   const u32x4 rl2 = make_rsrc(a.lse2 + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
   const u32x4 rnd = make_rsrc(a.ndelta + bq0 * a.Lqp, (uint32_t)group * a.Lqp * 4);
-  // With STAGE only the P waves load tiles, so the dS waves' vector-memory
-  // counter holds nothing but their dS stores, which no wait depends on (a
-  // load issued behind a store only counts as done once the store has been
-  // written).  Otherwise all eight waves share the loads.
-  constexpr int NWL = STAGE ? 4 : NW;
-  const bool loader = !STAGE || role == 0;
-  TileStager<BQ, D, NWL> rst;  // 64 rows of D channels (row stride D)
-  rst.init(D, STAGE ? kw : wave, lane);
-
-  // A tile is kRowHalf loads per wave, issued one at a time so they can be
-  // spread between MFMAs (a burst of them at the start of a phase would hold
-  // up the wave's instruction stream).
-  constexpr int kRowOps = TileStager<BQ, D, NWL>::kPer;
-  constexpr int kRowHalf = 2 * kRowOps + 2 + (WIN ? 2 : 0);
+  // A tile is loaded in two parts, one load at a time between MFMAs (a burst
+  // of them at the start of a phase would hold up the wave's instruction
+  // stream): the dS waves load its Q rows (kQOps loads per wave) during their
+  // dP phase of the iteration before, the P waves its dO rows and statistics
+  // (kROps) during their dV phase of the iteration before that.
+  TileStager<BQ, D, 4> rst;  // 64 rows of D channels (row stride D) over 4 waves
+  rst.init(D, kw, lane);
+  constexpr int kQOps = TileStager<BQ, D, 4>::kPer;
+  constexpr int kROps = kQOps + 2 + (WIN ? 2 : 0);
   auto tile_rows = [&](int it) {  // first row of tile `it` in the group's copies
     return (uint32_t)tile_head(it) * a.Lqp + (uint32_t)tile_idx(it) * BQ;
   };
@@ -294,42 +323,35 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     rwl = make_rsrc(a.wlo + b * a.wsb, (uint32_t)a.Lq * 4);
     rwh = make_rsrc(a.whi + b * a.wsb, (uint32_t)a.Lq * 4);
   }
-  auto stage = [&](auto bufc) -> RowStage& {
-    constexpr int s = decltype(bufc)::value;
-    return s == 0 ? rs0 : (s == 1 ? rs1 : rs2);
-  };
-  auto row_op = [&](int it, auto bufc, int i) {
-    RowStage& rsg = stage(bufc);
+  // Q load i of tile `it` into Q slot `qd`.
+  auto q_op = [&](int it, bf16* qd, int i) { rst.stage_one(qd, rq, tile_rows(it) * D * 2, i); };
+  // Row load i of tile `it` into row slot `rsg`.
+  auto r_op = [&](int it, RowStage& rsg, int i) {
     const uint32_t row0 = tile_rows(it);
-    if (i < kRowOps)
-      rst.stage_one(rsg.q, rq, row0 * D * 2, i);
-    else if (i < 2 * kRowOps)
-      rst.stage_one(rsg.dout, rdo, row0 * D * 2, i - kRowOps);
-    else if (i == 2 * kRowOps)
+    if (i < kQOps)
+      rst.stage_one(rsg.dout, rdo, row0 * D * 2, i);
+    else if (i == kQOps)
       dma4(rl2, lds_addr(rsg.lse2), lane * 4, row0 * 4);  // every wave loads the stats: no branch
-    else if (i == 2 * kRowOps + 1)
+    else if (i == kQOps + 1)
       dma4(rnd, lds_addr(rsg.ndl), lane * 4, row0 * 4);
-    else if (i == 2 * kRowOps + 2)
+    else if (i == kQOps + 2)
       dma4(rwl, lds_addr(rsg.wlo), lane * 4, (uint32_t)tile_idx(it) * BQ * 4);
     else
       dma4(rwh, lds_addr(rsg.whi), lane * 4, (uint32_t)tile_idx(it) * BQ * 4);
   };
-  // Loads issued per wave between two consecutive T waits: one tile.  Waiting
-  // until at most that many are outstanding retires the older tile, the one
-  // the coming iteration reads.
-  constexpr int kInFlight = kRowHalf;
-  // Slots of a phase that issue its `count` loads: every second slot from
-  // slot kLoad0 on (the start of a phase is left to its operand and
-  // statistics reads); the rest follow the phase's loop.  Load i goes in slot
-  // kLoad0 + 2*i.
-  // With STAGE the P waves issue twice as many loads: every slot from 4 on.
-  constexpr int kLoad0 = STAGE ? 4 : 6, kLoadStep = STAGE ? 1 : 2;
-  auto load_slot = [](int j, int nslots, int count) {
-    return j >= kLoad0 && (j - kLoad0) % kLoadStep == 0 && (j - kLoad0) / kLoadStep < count && j < nslots;
-  };
-  auto loads_in_loop = [](int nslots) {
-    return nslots > kLoad0 ? (nslots - kLoad0 + kLoadStep - 1) / kLoadStep : 0;
-  };
+  // Vector-memory operations complete in issue order (a load issued behind a
+  // store only counts as done once the store has been written).  A P wave
+  // issues rows(t + 1) in iteration t - 1 and rows(t + 2) in iteration t, so
+  // at tile t + 1's T wait only the kROps loads of rows(t + 2) may still be
+  // outstanding.  A dS wave issues Q(t + 1) in iteration t, followed only by
+  // the dS stores of tile t - 1 (STAGE, t >= 1): kDsStores of them.
+  constexpr int kDsStores = 4;
+  // Slots of a phase that issue its `count` loads: every slot from 4 on (the
+  // start of a phase is left to its operand and statistics reads); the rest
+  // follow the phase's loop.
+  constexpr int kLoad0 = 4;
+  auto load_slot = [](int j, int nslots, int count) { return j >= kLoad0 && j - kLoad0 < count && j < nslots; };
+  auto loads_in_loop = [](int nslots) { return nslots > kLoad0 ? nslots - kLoad0 : 0; };
   // Operand reads in flight ahead of the MFMAs (three measured faster than
   // four or six: fewer LDS requests queued at once).
   constexpr int kRA = 3;
@@ -348,19 +370,21 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // the next tile, and a share of the VALU work; sched_barrier(0) pins the
   // slot order (the scheduler would otherwise sink each read next to its
   // MFMA and bunch the loads and the VALU work).
-  auto body_p = [&](int it, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    using LoadBuf = std::integral_constant<int, (buf + 2) % 3>;  // tile it + 2 (tile it - 1 is done)
-    wait_vmem_n<kInFlight>();  // this tile landed (for this wave)
-    barrier_lds();             // T: ... for every wave; tile it - 1's stage is free
+  // Iteration `it` of a P wave; uc = it % 3 (compile-time), the slot.
+  auto body_p = [&](int it, auto uc) {
+    constexpr int u = decltype(uc)::value;
+    wait_vmem_n<kROps>();  // this tile's rows landed (for this wave)
+    barrier_lds();             // T: ... for every wave; the slots loaded into below are free
     // The wave whose phase ends in VALU-dependent work gets issue priority:
-    // P waves between T and X (softmax after QK^T), dS waves after X.
+    // P waves up to the end of the softmax, dS waves in their dS phase.
     __builtin_amdgcn_s_setprio(2);
-    const RowStage& rsg = stage(bufc);
-    const int itr = min(it + 2, niter - 1);  // loaded after X (the last tiles re-load)
+    // Loads during dV: rows of tile it + 2 (the last tiles re-load into
+    // slots nothing reads any more).
+    const int itr = min(it + 2, niter - 1);
+    RowStage& lrs = sm.rs[(u + 2) % 3];
 
     constexpr int NS = 2 * KS;  // QK^T MFMAs: (sub, ks)
-    auto qop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.q + (j / KS) * 32 * D + ro[j % KS]); };
+    auto qop = [&](int j) { return lds_ld<bf16x8>(rb[j % KS] + u * kQS + (j / KS) * 64 * D); };
     bf16x8 qa[kRA];
 #pragma unroll
     for (int j = 0; j < kRA; ++j) qa[j] = qop(j);
@@ -370,7 +394,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     f32x4 l2[2][2][2];
     auto l2_read = [&](int q8) {
       l2[q8 >> 2][(q8 >> 1) & 1][q8 & 1] =
-          *reinterpret_cast<const f32x4*>(rsg.lse2 + 32 * (q8 >> 2) + 16 * ((q8 >> 1) & 1) + 8 * hh + 4 * (q8 & 1));
+          lds_ld<f32x4>(sb + u * kRS + 4 * (32 * (q8 >> 2) + 16 * ((q8 >> 1) & 1) + 4 * (q8 & 1)));
     };
     __builtin_amdgcn_sched_barrier(0);
 
@@ -392,8 +416,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if constexpr (WIN) {
         if (edge) {
           // rows 32*sub + 16*k2 + 8*hh + e (+1) of the tile, this lane's key
-          const int r0 = 32 * sub + 16 * k2 + 8 * hh + e;
-          const int lo0 = rsg.wlo[r0], lo1 = rsg.wlo[r0 + 1], hi0 = rsg.whi[r0], hi1 = rsg.whi[r0 + 1];
+          const uint32_t r0 = sb + u * kRS + 4 * (32 * sub + 16 * k2 + e);
+          const int lo0 = lds_ld<int>(r0 + kWloOff), lo1 = lds_ld<int>(r0 + kWloOff + 4);
+          const int hi0 = lds_ld<int>(r0 + kWhiOff), hi1 = lds_ld<int>(r0 + kWhiOff + 4);
           if (key < lo0 || key >= hi0) s0 = kNegInf;
           if (key < lo1 || key >= hi1) s1 = kNegInf;
         }
@@ -402,7 +427,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const float p1 = __builtin_amdgcn_exp2f(fmaf(s1, c, -lv[(e & 3) + 1]));
       up[sub][k2][e2] = pack_bf16x2(p0, p1);
       if (e2 == 3) {
-        xp[64 * (2 * sub + k2)] = up[sub][k2];
+        lds_st<u32x4>(xb + u * kXS + 1024 * (2 * sub + k2), up[sub][k2]);
         pb[sub][k2] = bits_to_bf16x8(up[sub][k2]);
       }
     };
@@ -429,15 +454,16 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int st = 0; st < 8; ++st) smx(1, st >> 2, st & 3);
-    barrier_lds();  // X: P handed over
+    // P goes out with the next barrier (T of tile it + 1, where the partner
+    // picks it up for its dS phase).
     __builtin_amdgcn_s_setprio(0);
 
     // dV^T += dO^T P over the (sub, k2, dt) steps, reads four steps ahead.
     constexpr int NJ = 4 * DT;
     auto dot_op = [&](int j) {
       const int sk = j / DT, dt = j % DT;  // sk = 2*sub + k2
-      const bf16* base = rsg.dout + 16 * sk * D;
-      const bf16x4 lo = lds_read_tr16(base + tro[dt][0]), hi = lds_read_tr16(base + tro[dt][1]);
+      const uint32_t off = u * kRS + sk * 32 * D;
+      const bf16x4 lo = lds_read_tr16_at(tb[dt][0] + off), hi = lds_read_tr16_at(tb[dt][1] + off);
       return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     };
     bf16x8 opq[kRA];
@@ -450,45 +476,28 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (j + kRA < NJ) opq[j % kRA] = dot_op(j + kRA);
       const int sk = j / DT, dt = j % DT;
       acc[dt] = mfma32(op, pb[sk >> 1][sk & 1], acc[dt]);
-      if (load_slot(j, NJ, kRowHalf)) row_op(itr, LoadBuf(), (j - kLoad0) / kLoadStep);
+      if (load_slot(j, NJ, kROps)) r_op(itr, lrs, j - kLoad0);
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, LoadBuf(), i);
+    for (int i = loads_in_loop(NJ); i < kROps; ++i) r_op(itr, lrs, i);
   };
 
-  auto body_ds = [&](int it, auto bufc) {
-    constexpr int buf = decltype(bufc)::value;
-    using LoadBuf = std::integral_constant<int, (buf + 2) % 3>;
-    // With STAGE the dS waves load nothing: the barriers alone order them
-    // after the P waves' counted waits.
-    if constexpr (!STAGE) wait_vmem_n<kInFlight>();
-    barrier_lds();  // T
-    __builtin_amdgcn_s_setprio(0);
-    const RowStage& rsg = stage(bufc);
-    const int itr = min(it + 2, niter - 1);
-    // This tile's two dS units (query groups 2*tile_idx(it) and +1).
-    u32x4 rds = {0u, 0u, 0u, 0u};
-    uint32_t ds_unit1 = 0;
-    if constexpr (STAGE) {
-      const int64_t bq = (int64_t)(bhk - a.kv0) * group + tile_head(it);
-      const int64_t unit = (bq * (2 * nqt) + 2 * tile_idx(it)) * nkt + kt;
-      rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, (uint32_t)(nkt + 1) * 8192);
-      ds_unit1 = (uint32_t)nkt * 8192;
-    }
-
+  // dS waves, dP phase of the tile in slot uc: dp = dO V^T + ndelta, and the
+  // Q loads of tile itq into lq.
+  auto dp_phase = [&](auto uc, f32x16(&dp)[2], int itq, bf16* lq) {
+    constexpr int u = decltype(uc)::value;
     constexpr int NS = 2 * KS;  // dO V^T MFMAs: (sub, ks)
-    auto dop = [&](int j) { return *reinterpret_cast<const bf16x8*>(rsg.dout + (j / KS) * 32 * D + ro[j % KS]); };
+    auto dop = [&](int j) { return lds_ld<bf16x8>(rb[j % KS] + u * kRS + (j / KS) * 64 * D); };
     bf16x8 da[kRA];
 #pragma unroll
     for (int j = 0; j < kRA; ++j) da[j] = dop(j);
     // dP starts at ndelta of its row (registers 8*k2 + e: row 32*sub + 16*k2
     // + 8*hh + e), so the MFMAs deliver dP + ndelta directly.  Sub 0's values
     // are read now, sub 1's in the first slots (its MFMAs start at slot KS).
-    f32x16 dp[2];
     auto nd_read = [&](int sub, int q4) {
       const int k2 = q4 >> 1, hf = q4 & 1;
-      const f32x4 n4 = *reinterpret_cast<const f32x4*>(rsg.ndl + 32 * sub + 16 * k2 + 8 * hh + 4 * hf);
+      const f32x4 n4 = lds_ld<f32x4>(sb + u * kRS + kNdlOff + 4 * (32 * sub + 16 * k2 + 4 * hf));
 #pragma unroll
       for (int r = 0; r < 4; ++r) dp[sub][8 * k2 + 4 * hf + r] = n4[r];
     };
@@ -501,22 +510,40 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       dp[sub] = mfma32(da[j % kRA], kv[ks], dp[sub]);
       if (j + kRA < NS) da[j % kRA] = dop(j + kRA);
       if (j < 4) nd_read(1, j);  // KS >= 4: before sub 1's first MFMA
+      if (load_slot(j, NS, kQOps)) q_op(itq, lq, j - kLoad0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    barrier_lds();  // X: partner's P available
-    __builtin_amdgcn_s_setprio(2);
+#pragma unroll
+    for (int i = loads_in_loop(NS); i < kQOps; ++i) q_op(itq, lq, i);
+  };
+
+  // dS waves, dS phase of tile `it` (slot uc), one iteration after its dP
+  // phase, so the partner's P has been handed over by the barrier in
+  // between: dS = P * dp, dK^T += Q^T dS and, with STAGE, the dS stores
+  // (kDsStores per lane).
+  auto ds_phase = [&](int it, auto uc, const f32x16(&dp)[2]) {
+    constexpr uint32_t u = decltype(uc)::value;
+    // This tile's two dS units (query groups 2*tile_idx(it) and +1).
+    u32x4 rds = {0u, 0u, 0u, 0u};
+    uint32_t ds_unit1 = 0;
+    if constexpr (STAGE) {
+      const int64_t bq = (int64_t)(bhk - a.kv0) * group + tile_head(it);
+      const int64_t unit = (bq * (2 * nqt) + 2 * tile_idx(it)) * nkt + kt;
+      rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, (uint32_t)(nkt + 1) * 8192);
+      ds_unit1 = (uint32_t)nkt * 8192;
+    }
 
     // dS for group g = 2*sub + k2 (4 steps of two elements) interleaved with
     // the dK^T MFMAs of group g-1; every LDS read is issued up front or four
     // MFMAs ahead.
     u32x4 pv[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) pv[g] = xp[64 * g];
+    for (int g = 0; g < 4; ++g) pv[g] = lds_ld<u32x4>(xb + u * kXS + 1024 * g);
     constexpr int NJ = 4 * DT;
     auto qt_op = [&](int j) {
       const int g = j / DT, dt = j % DT;
-      const bf16* base = rsg.q + 16 * g * D;
-      const bf16x4 lo = lds_read_tr16(base + tro[dt][0]), hi = lds_read_tr16(base + tro[dt][1]);
+      const uint32_t off = u * kQS + g * 32 * D;
+      const bf16x4 lo = lds_read_tr16_at(tb[dt][0] + off), hi = lds_read_tr16_at(tb[dt][1] + off);
       return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
     };
     bf16x8 opq[kRA];
@@ -552,37 +579,62 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if constexpr (STAGE) {
         if (dt == 0) ds_store(g);
       }
-      if (!STAGE && load_slot(j, NJ, kRowHalf)) row_op(itr, LoadBuf(), (j - kLoad0) / kLoadStep);
       __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr (!STAGE) {
-#pragma unroll
-      for (int i = loads_in_loop(NJ); i < kRowHalf; ++i) row_op(itr, LoadBuf(), i);
     }
   };
 
   retire_prologue_loads();
-  using B0 = std::integral_constant<int, 0>;
-  using B1 = std::integral_constant<int, 1>;
-  using B2 = std::integral_constant<int, 2>;
-  if (loader && niter > 0) {  // niter is 0 when no window meets this block's keys
+  if (niter > 0 && role == 0) {  // niter is 0 when no window meets this block's keys
 #pragma unroll
-    for (int i = 0; i < kRowHalf; ++i) row_op(0, B0(), i);
+    for (int i = 0; i < kROps; ++i) r_op(0, sm.rs[0], i);
 #pragma unroll
-    for (int i = 0; i < kRowHalf; ++i) row_op(min(1, niter - 1), B1(), i);
+    for (int i = 0; i < kROps; ++i) r_op(min(1, niter - 1), sm.rs[1], i);
+  } else if (niter > 0) {
+#pragma unroll
+    for (int i = 0; i < kQOps; ++i) q_op(0, sm.q[0], i);
   }
-  // Tile it lives in stage it % 3.
-  if (role == 0) {
-    for (int it = 0; it < niter; it += 3) {
-      body_p(it, B0());
-      if (it + 1 < niter) body_p(it + 1, B1());
-      if (it + 2 < niter) body_p(it + 2, B2());
+  // Tile it lives in slot it % 3 (Q, rows and P hand-over); the loops are
+  // unrolled by 3 so that every slot is a compile-time constant.  Every wave
+  // passes one barrier per tile (T) and one after the last (F).
+  if (niter > 0 && role == 0) {
+    for (int it0 = 0;; it0 += 3) {
+      const bool more = unrolled_while<3>([&](auto uc) {
+        body_p(it0 + uc, uc);
+        return it0 + uc + 1 < niter;
+      });
+      if (!more) break;
     }
-  } else {
-    for (int it = 0; it < niter; it += 3) {
-      body_ds(it, B0());
-      if (it + 1 < niter) body_ds(it + 1, B1());
-      if (it + 2 < niter) body_ds(it + 2, B2());
+    barrier_lds();  // F: the last tile's P handed over
+  } else if (niter > 0) {
+    // dP of tile it (slot it % 3), kept for the tile's dS phase in the next
+    // iteration.
+    f32x16 dpb[3][2];
+    // Iterations 0 .. niter: iteration niter has only the last tile's dS
+    // phase (its barrier pairs with the P waves' F).
+    for (int it0 = 0;; it0 += 3) {
+      const bool more = unrolled_while<3>([&](auto uc) {
+        constexpr int u = decltype(uc)::value, up = (u + 2) % 3;  // slots of tiles it, it - 1
+        const int it = it0 + u;
+        // Q(it) landed: issued in iteration it - 1, followed there by the dS
+        // stores of tile it - 2 if that iteration had a dS phase.
+        if (STAGE && it >= 2)
+          wait_vmem_n<kDsStores>();
+        else
+          wait_vmem_n<0>();
+        barrier_lds();  // T: tile it staged, tile it - 1's P handed over
+        if (it < niter) {
+          __builtin_amdgcn_s_setprio(0);
+          // Loads: Q of tile it + 1 (the last tile re-loads into a slot
+          // nothing reads any more).
+          dp_phase(uc, dpb[u], min(it + 1, niter - 1), sm.q[(u + 1) % 3]);
+        }
+        if (it > 0) {
+          __builtin_amdgcn_s_setprio(2);
+          ds_phase(it - 1, std::integral_constant<int, up>(), dpb[up]);
+        }
+        return it < niter;
+      });
+      if (!more) break;
     }
   }
 

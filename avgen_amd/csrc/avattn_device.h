@@ -15,6 +15,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace avattn {
 
 typedef __bf16 bf16;
@@ -456,6 +459,28 @@ __device__ __forceinline__ bf16x4 lds_read_tr16(const bf16* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(const_cast<bf16*>(p)));
 }
 
+// LDS accesses at a byte address (lds_addr) held in a register.  With an
+// address made opaque by opaque_lds, a constant added to it goes into the
+// instruction's 16-bit offset field: loops over several LDS buffers then keep
+// one address register per lane offset instead of one per (offset, buffer)
+// pair, which the compiler otherwise hoists out of the loop.
+__device__ __forceinline__ uint32_t opaque_lds(uint32_t a) {
+  __asm__ volatile("" : "+v"(a));
+  return a;
+}
+template <class T>
+__device__ __forceinline__ T lds_ld(uint32_t a) {
+  return *(const __attribute__((address_space(3))) T*)a;
+}
+template <class T>
+__device__ __forceinline__ void lds_st(uint32_t a, const T& v) {
+  *(__attribute__((address_space(3))) T*)a = v;
+}
+__device__ __forceinline__ bf16x4 lds_read_tr16_at(uint32_t a) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a);
+}
+
 // Retire every outstanding memory operation of this wave, as an instruction
 // the compiler's wait-count bookkeeping sees: a loop that issues its tile
 // loads as inline assembly calls this first, so no compiler-inserted wait for
@@ -493,5 +518,25 @@ constexpr int kSchedDsRead = 0x100;
 constexpr int kSchedDsWrite = 0x200;
 constexpr int kSchedVmem = 0x010;
 constexpr int kSchedSalu = 0x004;
+
+// f(std::integral_constant<int, u>()) for u = 0 .. N-1 in order (a loop body
+// unrolled with its iteration index as a compile-time constant).
+template <class F, int... U>
+__device__ __forceinline__ void unrolled(F&& f, std::integer_sequence<int, U...>) {
+  (f(std::integral_constant<int, U>()), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void unrolled(F&& f) {
+  unrolled(f, std::make_integer_sequence<int, N>());
+}
+// The same while f returns true; returns whether every call did.
+template <class F, int... U>
+__device__ __forceinline__ bool unrolled_while(F&& f, std::integer_sequence<int, U...>) {
+  return (f(std::integral_constant<int, U>()) && ...);
+}
+template <int N, class F>
+__device__ __forceinline__ bool unrolled_while(F&& f) {
+  return unrolled_while(f, std::make_integer_sequence<int, N>());
+}
 
 }  // namespace avattn
