@@ -210,6 +210,26 @@ def test_backward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked, staged):
         assert err <= GRAD_REL_TOL * scale, name
 
 
+@pytest.mark.parametrize("ntiles", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("staged", [True, False])
+def test_backward_query_tile_counts(amd, ntiles, staged):
+    """dK/dV's tile loop (unrolled by three, the dS waves one tile behind and
+    one iteration longer) ending at every position: 1..7 query tiles of 64
+    rows, the last one ragged."""
+    Lq, Lk, D = 64 * ntiles - 5, 256, 128
+    q, k, v = _randn((1, 2, Lq, D), 60), _randn((1, 2, Lk, D), 61), _randn((1, 2, Lk, D), 62)
+    do = _randn((1, 2, Lq, D), 63)
+    print(f"tile-count case Lq={Lq} staged={staged}", flush=True)
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), None, None, None, D ** -0.5)
+    dq, dk, dv = amd.ops._bwd_impl(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, None, D ** -0.5,
+                                   stage_ds=staged)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v))
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        err = np.abs(_f64(got) - ref).max()
+        assert err <= GRAD_REL_TOL * max(np.abs(ref).max(), 1e-3), name
+
+
 def test_autograd_through_dropin(amd):
     q = _randn((1, 2, 96, 128), 50).cuda().requires_grad_(True)
     k = _randn((1, 2, 80, 128), 51).cuda().requires_grad_(True)
