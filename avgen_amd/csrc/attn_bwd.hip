@@ -205,7 +205,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int h = 0; h < 2; ++h) tro[dt][h] = tr_read_off<D>(lane, dt, h);
-  // Per-lane LDS byte addresses in slot 0 (opaque_lds: slot and row-block
+  // Per-lane LDS byte addresses in slot 0 (opaque: slot and row-block
   // offsets go into the reads' offset fields).  P waves read Q as rows and
   // dO transposed, dS waves dO as rows and Q transposed.
   uint32_t rb[KS], tb[DT][2];
@@ -213,22 +213,22 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     const uint32_t q0 = lds_addr(&sm.q[0][0]), d0 = lds_addr(&sm.rs[0].dout[0]);
     const uint32_t rrow = role == 0 ? q0 : d0, rtr = role == 0 ? d0 : q0;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) rb[ks] = opaque_lds(rrow + 2 * ro[ks]);
+    for (int ks = 0; ks < KS; ++ks) rb[ks] = opaque(rrow + 2 * ro[ks]);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) tb[dt][h] = opaque_lds(rtr + 2 * tro[dt][h]);
+      for (int h = 0; h < 2; ++h) tb[dt][h] = opaque(rtr + 2 * tro[dt][h]);
   }
   // Row statistics of the lane's rows 8*hh + ...: lse2 at sb, ndelta and
   // the windows at the offsets below.
-  const uint32_t sb = opaque_lds(lds_addr(&sm.rs[0].lse2[0]) + 32 * hh);
+  const uint32_t sb = opaque(lds_addr(&sm.rs[0].lse2[0]) + 32 * hh);
   constexpr uint32_t kNdlOff = BQ * 4, kWloOff = 2 * BQ * 4, kWhiOff = kWloOff + sizeof(sm.rs[0].wlo);
   static_assert(offsetof(RowStage, ndl) - offsetof(RowStage, lse2) == kNdlOff &&
                     offsetof(RowStage, wlo) - offsetof(RowStage, lse2) == kWloOff &&
                     offsetof(RowStage, whi) - offsetof(RowStage, lse2) == kWhiOff,
                 "row statistics offsets");
   // This lane's 16 bytes of the P hand-over: + kXS*slot + 1024*(2*sub + k2).
-  const uint32_t xb = opaque_lds(lds_addr(&sm.xp[0][0]) + 16 * (kw * 4 * 64 + lane));
+  const uint32_t xb = opaque(lds_addr(&sm.xp[0][0]) + 16 * (kw * 4 * 64 + lane));
 
   const int nqt = a.Lqp / BQ;
   // Query tiles visited: tq0 .. tq0 + ntq - 1 of every query head of the

@@ -73,10 +73,12 @@ __device__ __forceinline__ f32x16 zero16() {
 }
 
 // The same value, opaque to the optimizer at this point of the program: an
-// LDS offset passed through it is added to a stage's base where it is used
-// (folded into the instruction's offset field when that fits) instead of
-// being hoisted out of the loop as one extra register per stage.
-__device__ __forceinline__ int opaque(int x) {
+// LDS offset or address passed through it is added to a stage's base where
+// it is used (folded into the instruction's 16-bit offset field when that
+// fits) instead of being hoisted out of the loop as one extra register per
+// (offset, stage) pair.
+template <class T>
+__device__ __forceinline__ T opaque(T x) {
   __asm__ volatile("" : "+v"(x));
   return x;
 }
@@ -459,15 +461,8 @@ __device__ __forceinline__ bf16x4 lds_read_tr16(const bf16* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(const_cast<bf16*>(p)));
 }
 
-// LDS accesses at a byte address (lds_addr) held in a register.  With an
-// address made opaque by opaque_lds, a constant added to it goes into the
-// instruction's 16-bit offset field: loops over several LDS buffers then keep
-// one address register per lane offset instead of one per (offset, buffer)
-// pair, which the compiler otherwise hoists out of the loop.
-__device__ __forceinline__ uint32_t opaque_lds(uint32_t a) {
-  __asm__ volatile("" : "+v"(a));
-  return a;
-}
+// LDS accesses at a byte address (lds_addr) held in a register; with the
+// address made opaque, a constant added to it goes into the offset field.
 template <class T>
 __device__ __forceinline__ T lds_ld(uint32_t a) {
   return *(const __attribute__((address_space(3))) T*)a;
