@@ -514,17 +514,9 @@ constexpr int kSchedDsWrite = 0x200;
 constexpr int kSchedVmem = 0x010;
 constexpr int kSchedSalu = 0x004;
 
-// f(std::integral_constant<int, u>()) for u = 0 .. N-1 in order (a loop body
-// unrolled with its iteration index as a compile-time constant).
-template <class F, int... U>
-__device__ __forceinline__ void unrolled(F&& f, std::integer_sequence<int, U...>) {
-  (f(std::integral_constant<int, U>()), ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void unrolled(F&& f) {
-  unrolled(f, std::make_integer_sequence<int, N>());
-}
-// The same while f returns true; returns whether every call did.
+// f(std::integral_constant<int, u>()) for u = 0 .. N-1 in order while f
+// returns true (a loop body unrolled with its iteration index as a
+// compile-time constant); returns whether every call did.
 template <class F, int... U>
 __device__ __forceinline__ bool unrolled_while(F&& f, std::integer_sequence<int, U...>) {
   return (f(std::integral_constant<int, U>()) && ...);
