@@ -366,7 +366,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   const float c = a.scale_log2;
 
   // The loop bodies below are explicitly software-pipelined: each "slot" is
-  // one MFMA plus the LDS read it needs four slots later, at most one load of
+  // one MFMA plus the LDS read it needs kRA slots later, at most one load of
   // the next tile, and a share of the VALU work; sched_barrier(0) pins the
   // slot order (the scheduler would otherwise sink each read next to its
   // MFMA and bunch the loads and the VALU work).
@@ -460,7 +460,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     // picks it up for its dS phase).
     __builtin_amdgcn_s_setprio(0);
 
-    // dV^T += dO^T P over the (sub, k2, dt) steps, reads four steps ahead.
+    // dV^T += dO^T P over the (sub, k2, dt) steps, reads kRA steps ahead.
     constexpr int NJ = 4 * DT;
     auto dot_op = [&](int j) {
       const int sk = j / DT, dt = j % DT;  // sk = 2*sub + k2
@@ -536,7 +536,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     }
 
     // dS for group g = 2*sub + k2 (4 steps of two elements) interleaved with
-    // the dK^T MFMAs of group g-1; every LDS read is issued up front or four
+    // the dK^T MFMAs of group g-1; every LDS read is issued up front or kRA
     // MFMAs ahead.
     u32x4 pv[4];
 #pragma unroll
