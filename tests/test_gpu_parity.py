@@ -212,14 +212,16 @@ def test_backward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked, staged):
 
 @pytest.mark.parametrize("ntiles", [1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("staged", [True, False])
-def test_backward_query_tile_counts(amd, ntiles, staged):
+@pytest.mark.parametrize("D", [128, 64])
+def test_backward_query_tile_counts(amd, ntiles, staged, D):
     """dK/dV's tile loop (unrolled by three, the dS waves one tile behind and
     one iteration longer) ending at every position: 1..7 query tiles of 64
-    rows, the last one ragged."""
-    Lq, Lk, D = 64 * ntiles - 5, 256, 128
+    rows, the last one ragged, at both head dims (their phases have 16 and 8
+    MFMA slots)."""
+    Lq, Lk = 64 * ntiles - 5, 256
     q, k, v = _randn((1, 2, Lq, D), 60), _randn((1, 2, Lk, D), 61), _randn((1, 2, Lk, D), 62)
     do = _randn((1, 2, Lq, D), 63)
-    print(f"tile-count case Lq={Lq} staged={staged}", flush=True)
+    print(f"tile-count case Lq={Lq} D={D} staged={staged}", flush=True)
     out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), None, None, None, D ** -0.5)
     dq, dk, dv = amd.ops._bwd_impl(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, None, D ** -0.5,
                                    stage_ds=staged)
