@@ -1302,7 +1302,6 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
   const int nkv_all = a.B * a.Hkv;
   const int step = a.ds ? kv_per_pass : nkv_all;
   const int nkt = (a.Lk + 127) / 128;
-  const int group = a.Hq / a.Hkv;
   const int cus = cu_count();
   for (int kv0 = 0; kv0 < nkv_all; kv0 += step) {
     BwdArgs p = a;

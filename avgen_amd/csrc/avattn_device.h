@@ -465,15 +465,15 @@ __device__ __forceinline__ bf16x4 lds_read_tr16(const bf16* p) {
 // address made opaque, a constant added to it goes into the offset field.
 template <class T>
 __device__ __forceinline__ T lds_ld(uint32_t a) {
-  return *(const __attribute__((address_space(3))) T*)a;
+  return *(const __attribute__((address_space(3))) T*)(uintptr_t)a;
 }
 template <class T>
 __device__ __forceinline__ void lds_st(uint32_t a, const T& v) {
-  *(__attribute__((address_space(3))) T*)a = v;
+  *(__attribute__((address_space(3))) T*)(uintptr_t)a = v;
 }
 __device__ __forceinline__ bf16x4 lds_read_tr16_at(uint32_t a) {
   typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(uintptr_t)a);
 }
 
 // Retire every outstanding memory operation of this wave, as an instruction
