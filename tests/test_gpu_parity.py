@@ -232,6 +232,26 @@ def test_backward_query_tile_counts(amd, ntiles, staged, D):
         assert err <= GRAD_REL_TOL * max(np.abs(ref).max(), 1e-3), name
 
 
+@pytest.mark.parametrize("Lq", [60, 100, 250])
+@pytest.mark.parametrize("staged", [True, False])
+def test_backward_gqa_group_of_three(amd, Lq, staged):
+    """Three query heads per KV head: dK/dV's tile loop runs over the tiles of
+    every head of the group, so the head changes at different positions of
+    the three-slot rotation (1, 2 and 4 tiles per head)."""
+    Hq, Hkv, Lk, D = 6, 2, 200, 128
+    q, k, v = _randn((1, Hq, Lq, D), 70), _randn((1, Hkv, Lk, D), 71), _randn((1, Hkv, Lk, D), 72)
+    do = _randn((1, Hq, Lq, D), 73)
+    print(f"gqa-3 case Lq={Lq} staged={staged}", flush=True)
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), None, None, None, D ** -0.5)
+    dq, dk, dv = amd.ops._bwd_impl(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, None, D ** -0.5,
+                                   stage_ds=staged)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v))
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl)
+    for name, got, ref in (("dq", dq, rq), ("dk", dk, rk), ("dv", dv, rv)):
+        err = np.abs(_f64(got) - ref).max()
+        assert err <= GRAD_REL_TOL * max(np.abs(ref).max(), 1e-3), name
+
+
 def test_autograd_through_dropin(amd):
     q = _randn((1, 2, 96, 128), 50).cuda().requires_grad_(True)
     k = _randn((1, 2, 80, 128), 51).cuda().requires_grad_(True)
