@@ -34,6 +34,7 @@ from contextlib import AbstractContextManager, nullcontext
 from typing import Optional
 
 import torch
+from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import ops
 from .rope import RotaryTables
@@ -56,38 +57,93 @@ __all__ = [
     "windowed_attention",
 ]
 
-#: The single backend this package provides.
+#: Name of the kernel family behind every backend below: the hand-written
+#: gfx950 kernels serve any backend list a caller pins.
 BACKEND = "avattn_gfx950"
+
+# Architecture family per CUDA-style compute capability (major * 10 + minor),
+# read as "at least this capability", and the SDPA backend priority of each
+# family, MATH last: the classification of
+# src/avgen/models/attention.py:53-91, kept identical so that a caller's
+# backend lists and contexts compose with this module exactly as with the
+# reference's.  ROCm builds of PyTorch report gfx950 as capability (9, 5).
+_CAPABILITY_FLOORS: tuple[tuple[int, str], ...] = (
+    (100, "blackwell"),
+    (90, "hopper"),
+    (89, "ada"),
+    (80, "ampere"),
+    (0, "legacy"),
+)
+
+
+def _backend_table() -> dict[str, tuple[SDPBackend, ...]]:
+    flash, eff, math_, cudnn = (
+        SDPBackend.FLASH_ATTENTION,
+        SDPBackend.EFFICIENT_ATTENTION,
+        SDPBackend.MATH,
+        SDPBackend.CUDNN_ATTENTION,
+    )
+    return {
+        "blackwell": (cudnn, flash, eff, math_),
+        "hopper": (cudnn, flash, eff, math_),
+        "ada": (flash, eff, math_),
+        "ampere": (flash, eff, math_),
+        "legacy": (eff, math_),
+        "cpu": (math_,),
+    }
+
+
+_BACKENDS = _backend_table()
+_arch_by_index: dict[int, str] = {}
 
 
 def device_arch(device: torch.device | str | None = None) -> str:
-    """Architecture family for a device: ``"cdna4"`` on a ROCm GPU, else ``"cpu"``
-    (reference classification: src/avgen/models/attention.py:98-130)."""
+    """Architecture family of a device, as src/avgen/models/attention.py:98-130
+    classifies it: ``"cpu"`` for anything but an available GPU, else the
+    family of ``torch.cuda.get_device_capability`` (memoised per device
+    index).  An MI355X reports capability (9, 5) under ROCm, i.e.
+    ``"hopper"``, exactly what the reference returns on the same machine."""
     if device is None:
         resolved = torch.device("cuda" if torch.cuda.is_available() else "cpu")
     else:
         resolved = torch.device(device)
     if resolved.type != "cuda" or not torch.cuda.is_available():
         return "cpu"
-    return "cdna4"
+    index = resolved.index if resolved.index is not None else torch.cuda.current_device()
+    arch = _arch_by_index.get(index)
+    if arch is None:
+        major, minor = torch.cuda.get_device_capability(index)
+        cap = 10 * major + minor
+        arch = next(name for floor, name in _CAPABILITY_FLOORS if cap >= floor)
+        _arch_by_index[index] = arch
+    return arch
 
 
 def attention_backends(
     device: torch.device | str | None = None, *, allow_flash: bool = True
-) -> tuple[str, ...]:
-    """Backend priority list (src/avgen/models/attention.py:133-153).  There is
-    exactly one backend — the hand-written gfx950 kernel — and no fallback."""
-    del device, allow_flash
-    return (BACKEND,)
+) -> tuple[SDPBackend, ...]:
+    """Backend priority list of a device (src/avgen/models/attention.py:133-153):
+    the same ``SDPBackend`` tuple the reference returns, so callers can pass it
+    on to :func:`attention` or :func:`sdpa_context`.  Every entry is served by
+    the gfx950 kernels here (there is no dispatch between them)."""
+    chosen = _BACKENDS[device_arch(device)]
+    if not allow_flash:
+        chosen = tuple(b for b in chosen if b is not SDPBackend.FLASH_ATTENTION)
+    return chosen
 
 
 def sdpa_context(
-    device: torch.device | str | None = None, *, backends: Sequence[object] | None = None
+    device: torch.device | str | None = None, *, backends: Sequence[SDPBackend] | None = None
 ) -> AbstractContextManager[None]:
-    """No-op context (src/avgen/models/attention.py:156-180): this package does
-    not dispatch through PyTorch's SDPA backends."""
-    del device, backends
-    return nullcontext()
+    """Context pinning PyTorch's SDPA backend priority, as
+    src/avgen/models/attention.py:156-180 builds it: a no-op on CPU, else
+    ``sdpa_kernel`` over ``backends`` (default :func:`attention_backends`).
+    It governs PyTorch's own SDPA calls made inside it; the gfx950 kernels of
+    this package run whatever it pins."""
+    if device_arch(device) == "cpu":
+        return nullcontext()
+    chosen = tuple(backends) if backends is not None else attention_backends(device)
+    return sdpa_kernel(list(chosen))
 
 
 def key_padding_mask(mask: torch.Tensor | None, *, assume_dense: bool = False) -> torch.Tensor | None:
@@ -172,17 +228,19 @@ def attention(
             ``(batch, 1, 1, keys)``; True = attend.
         dropout_p, is_causal: must be 0 / False.
         enable_gqa: allow ``kv_heads`` dividing ``heads``.
-        backends: accepted for signature compatibility; ignored.
+        backends: SDPA backend priority for the call, pinned with
+            :func:`sdpa_context` around it as the reference does (:264);
+            the gfx950 kernel serves every list.
 
     Returns:
         ``(batch, heads, queries, head_dim)`` in query's dtype; differentiable.
     """
-    del backends
     if query.shape[-2] == 0 or key.shape[-2] == 0:
         return torch.zeros_like(query)
     _validate(query, key, value, dropout_p, is_causal, enable_gqa)
     mask = _as_key_mask(attn_mask, query.shape[0], query.shape[-2], key.shape[-2])
-    out, _ = ops.flash_fwd(query, key, value, mask, None, None, ops.default_scale(query.shape[-1]))
+    with sdpa_context(query.device, backends=backends):
+        out, _ = ops.flash_fwd(query, key, value, mask, None, None, ops.default_scale(query.shape[-1]))
     return out
 
 

@@ -191,3 +191,39 @@ def test_compiled_block_and_selective_checkpoint(amd):
     assert torch.equal(s_out, ref_out)
     for a, b in zip(s_grads, ref_grads):
         assert torch.equal(a, b)
+
+
+def test_dispatch_helpers_compose_on_the_device(amd):
+    """src/avgen/models/attention.py:264 runs every call under
+    ``sdpa_context(query.device, backends=backends)`` with the list from
+    ``attention_backends``: the same composition here gives the kernel's bits
+    whatever list is pinned, eagerly and compiled, and the device classifies
+    as the reference classifies it."""
+    from torch.nn.attention import SDPBackend
+
+    A = amd.attention
+    major, minor = torch.cuda.get_device_capability()
+    cap = 10 * major + minor
+    expect = "blackwell" if cap >= 100 else "hopper" if cap >= 90 else "ada" if cap >= 89 else (
+        "ampere" if cap >= 80 else "legacy")
+    print(f"device capability {(major, minor)} -> {A.device_arch('cuda')}", flush=True)
+    assert A.device_arch("cuda") == expect == A.device_arch(None)
+    dev = torch.device("cuda")
+    backends = A.attention_backends(dev)
+    assert backends[-1] is SDPBackend.MATH
+    q, k, v = (_rand((2, 2, 96, 64), s, 0.7) for s in (21, 22, 23))
+    valid = torch.ones(2, 96, dtype=torch.bool, device="cuda")
+    valid[0, 70:] = False
+    mask = A.key_padding_mask(valid)
+    ref = A.attention(q, k, v, attn_mask=mask)
+    assert torch.equal(A.attention(q, k, v, attn_mask=mask, backends=backends), ref)
+    with A.sdpa_context(dev, backends=[SDPBackend.MATH]):
+        assert not torch.backends.cuda.flash_sdp_enabled()
+        assert torch.equal(A.attention(q, k, v, attn_mask=mask, backends=[SDPBackend.MATH]), ref)
+    assert torch.backends.cuda.flash_sdp_enabled()  # restored on exit
+
+    def fn(q, k, v, m):
+        return A.attention(q, k, v, attn_mask=m, backends=A.attention_backends(q.device, allow_flash=False))
+
+    torch._dynamo.reset()
+    assert torch.equal(torch.compile(fn, fullgraph=True, dynamic=False)(q, k, v, mask), ref)
