@@ -254,8 +254,7 @@ def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, 
     dk = _out_or_new(None, k, name, "dk")
     dv = _out_or_new(None, v, name, "dv")
     lib = _lib.load()
-    nbytes, _ = bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds=True)
-    ws = _workspace(nbytes, q.device)
+    ws = _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds=True)
     st = lib.avattn_bwd_windowed(
         _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
         _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
@@ -320,9 +319,12 @@ def _out_or_new(t: Optional[torch.Tensor], like: torch.Tensor, name: str, label:
 # device memory it may take.  Fixed per device (never read from the
 # allocator's current state, so the pass count of a given shape does not
 # change from call to call): set_ds_budget(), else AVGEN_AMD_DS_BUDGET_GB
-# (0 turns staging off), else min(96 GiB, a third of the device's memory),
-# decided at first use.
-_DS_BUDGET_CAP = 96 << 30
+# (0 turns staging off), else the default below.  32 GiB holds a c3 ring
+# chunk's 40 (batch, head) pairs in one pass (26.7 GiB) and a c2 block's 40
+# pairs (20 GiB); a 76k-token pair (10.8 GiB) goes two per pass.  When the
+# allocator cannot provide a planned workspace the call retries with fewer
+# pairs per pass, then (where staging is optional) without staging.
+_DS_BUDGET_DEFAULT = 32 << 30
 _ds_budgets: dict[int, int] = {}
 
 
@@ -346,7 +348,7 @@ def _ds_budget(device: torch.device) -> int:
             _ds_budgets[idx] = int(float(env) * (1 << 30))
         else:
             total = torch.cuda.get_device_properties(idx).total_memory
-            _ds_budgets[idx] = min(_DS_BUDGET_CAP, total // 3)
+            _ds_budgets[idx] = min(_DS_BUDGET_DEFAULT, total // 3)
     return _ds_budgets[idx]
 
 
@@ -356,24 +358,53 @@ def ds_bytes_per_pair(group, Lq, Lk):
     return group * ((Lq + 63) // 64 * 64) * ((Lk + 127) // 128 * 128) * 2
 
 
+def _staged_pairs(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None) -> int:
+    """(batch, kv head) pairs per pass that a backward call stages dS for (0:
+    no staging): as many as the budget holds (``stage_ds`` None), at least one
+    (True), none (False); equal passes, as the library splits them."""
+    lib = _lib.load()
+    if stage_ds is False or lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D) == 0:
+        return 0
+    per = ds_bytes_per_pair(Hq // Hkv, Lq, Lk)
+    pairs = min(B * Hkv, _ds_budget(device) // max(per, 1))
+    if pairs == 0:
+        if not stage_ds:
+            return 0
+        pairs = 1
+    npass = -(-(B * Hkv) // pairs)
+    return -(-(B * Hkv) // npass)
+
+
 def bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None):
     """(bytes, staged) for one backward call: the workspace to allocate and
     whether dS is staged (``stage_ds`` None: when the staged dS of at least
     one (batch, kv head) pair fits the budget; True: at least one pair
     whatever the budget; False: never)."""
     lib = _lib.load()
-    base = lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D)
-    if stage_ds is False or base == 0:
-        return base, False
-    per = ds_bytes_per_pair(Hq // Hkv, Lq, Lk)
-    pairs = min(B * Hkv, _ds_budget(device) // max(per, 1))
+    pairs = _staged_pairs(B, Hq, Hkv, Lq, Lk, D, device, stage_ds)
     if pairs == 0:
-        if not stage_ds:
-            return base, False
-        pairs = 1
-    npass = -(-(B * Hkv) // pairs)
-    pairs = -(-(B * Hkv) // npass)  # equal passes, as the library splits them
+        return lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D), False
     return lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(pairs)), True
+
+
+def _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None) -> torch.Tensor:
+    """The workspace of :func:`bwd_workspace_plan`, allocated; if the caching
+    allocator cannot provide it (memory held by activations, say), the
+    staged pairs per pass halve until it can (more passes, the same
+    results), and with staging optional (``stage_ds`` not True) a last
+    attempt goes without staging (the recomputing dQ kernel)."""
+    lib = _lib.load()
+    pairs = _staged_pairs(B, Hq, Hkv, Lq, Lk, D, device, stage_ds)
+    while pairs > 0:
+        try:
+            return _workspace(lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(pairs)), device)
+        except torch.OutOfMemoryError:
+            if pairs == 1:
+                if stage_ds:
+                    raise
+                break
+            pairs = (pairs + 1) // 2
+    return _workspace(lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D), device)
 
 
 def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=None, *,
@@ -429,8 +460,9 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
     if workspace is None:
         if reuse_query_side:
             raise ValueError(f"{name}: reuse_query_side needs the caller's workspace")
-        nbytes, staged = bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds)
-        ws = _workspace(nbytes, q.device)
+        ws = _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds)
+        one = lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, 1)
+        staged = stage_ds is not False and one > 0 and ws.numel() >= one
     else:
         if workspace.dtype is not torch.uint8 or workspace.numel() < need or workspace.device != q.device:
             raise ValueError(f"{name}: workspace must be uint8 with at least {need} bytes on {q.device}")
@@ -480,13 +512,15 @@ def _bwd_dq_staged_impl(q, Hkv, Lk, scale, workspace, dq=None, dq_accumulate=Non
     return dq
 
 
-def _ring_tables(name, tables, batch, length, head_dim):
-    """(cos, sin, batch stride) of a RotaryTables (or None): shape (B|1, 1,
-    length, head_dim/2) float32 with contiguous rows of pairs, e.g. a slice
-    ``tables.slice(a, b)`` of full-sequence tables (no copy is made)."""
-    if tables is None:
+def _ring_tables(name, cos, sin, batch, length, head_dim):
+    """(cos, sin, batch stride) of one rotation table pair (or (None, None, 0)
+    without tables): shape (B|1, 1, length, head_dim/2) float32 with
+    contiguous rows of pairs, e.g. a slice of full-sequence tables along the
+    sequence (no copy is made)."""
+    if cos is None and sin is None:
         return None, None, 0
-    cos, sin = tables.cos, tables.sin
+    if cos is None or sin is None:
+        raise ValueError(f"{name}: pass both rotation tables or neither")
     if cos.ndim != 4 or cos.shape != sin.shape:
         raise ValueError(f"{name}: rotary tables must be (batch, 1, length, pairs) and agree")
     if cos.dtype is not torch.float32 or sin.dtype is not torch.float32:
@@ -514,15 +548,11 @@ def _ring_tables(name, tables, batch, length, head_dim):
     return cos, sin, stride_b
 
 
-def ring_fwd_step_(q, k, v, key_mask, tables_q, tables_k, scale, out_acc, lse_acc, out, *, first: bool,
-                   last: bool) -> None:
-    """One fused ring forward step (``avattn_ring_fwd_step``): attention of the
-    UNROTATED query shard ``q`` against one UNROTATED KV chunk, rotated on the
-    fly with ``tables_q`` / ``tables_k`` (RotaryTables or None), merged into
-    the running fp32 ``out_acc`` / ``lse_acc`` (``first``: they take this
-    chunk's result); with ``last`` the merged output is also written to
-    ``out`` (bf16, q's shape).  Replaces apply_rotary + the ring's local op +
-    ``_SDPAMerger.step`` (torch/.../_context_parallel/_attention.py:182-183)."""
+def _table_pair(tables):
+    return (None, None) if tables is None else (tables.cos, tables.sin)
+
+
+def _ring_fwd_step_impl(q, k, v, key_mask, cos_q, sin_q, cos_k, sin_k, scale, out_acc, lse_acc, out, first, last):
     name = "avgen_amd.ring_fwd_step"
     _check_qkv(name, q, k, v)
     _require_gpu(name, q, k, v, key_mask, out_acc, lse_acc, out)
@@ -537,8 +567,8 @@ def ring_fwd_step_(q, k, v, key_mask, tables_q, tables_k, scale, out_acc, lse_ac
         raise ValueError(f"{name}: the last step needs a kernel-ready bf16 output shaped like the query")
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     mask, msb = _normalise_mask(name, key_mask, B, Lk)
-    cq, sq, rqsb = _ring_tables(name, tables_q, B, Lq, D)
-    ck, sk, rksb = _ring_tables(name, tables_k, B, Lk, D)
+    cq, sq, rqsb = _ring_tables(name, cos_q, sin_q, B, Lq, D)
+    ck, sk, rksb = _ring_tables(name, cos_k, sin_k, B, Lk, D)
     flags = (_lib.RING_FIRST if first else 0) | (_lib.RING_LAST if last else 0)
     lib = _lib.load()
     ws = _workspace(lib.avattn_fwd_workspace_size(B, Hkv, Lk, D), q.device)
@@ -557,13 +587,8 @@ def ring_fwd_step_(q, k, v, key_mask, tables_q, tables_k, scale, out_acc, lse_ac
     _lib.check(st, name)
 
 
-def ring_bwd_step(dout, q, k, v, out, lse, key_mask, tables_q, tables_k, scale, dq_acc, dk, dv, *, workspace,
-                  reuse_query_side: bool) -> None:
-    """One fused ring backward step (``avattn_ring_bwd_step``): adds this
-    chunk's gradient of the rotated query to the fp32 ``dq_acc`` and writes the
-    chunk's ``dk`` (of the unrotated keys) and ``dv`` in place.  ``workspace``
-    is a uint8 device tensor of at least the plain backward's size; dS is
-    staged when it holds at least one (batch, kv head) pair's dS."""
+def _ring_bwd_step_impl(dout, q, k, v, out, lse, key_mask, cos_q, sin_q, cos_k, sin_k, scale, dq_acc, dk, dv,
+                        workspace, reuse_query_side):
     name = "avgen_amd.ring_bwd_step"
     _check_qkv(name, q, k, v)
     _require_gpu(name, dout, q, k, v, out, lse, key_mask, dq_acc, dk, dv, workspace)
@@ -571,11 +596,13 @@ def ring_bwd_step(dout, q, k, v, out, lse, key_mask, tables_q, tables_k, scale, 
     Hkv, Lk = k.shape[1], k.shape[2]
     if dq_acc.shape != q.shape or dq_acc.dtype is not torch.float32:
         raise ValueError(f"{name}: dq accumulator must be float32 {tuple(q.shape)}")
+    if workspace.dtype is not torch.uint8 or workspace.ndim != 1:
+        raise ValueError(f"{name}: workspace must be a 1-D uint8 tensor")
     dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
     lse = lse.contiguous()
     mask, msb = _normalise_mask(name, key_mask, B, Lk)
-    cq, sq, rqsb = _ring_tables(name, tables_q, B, Lq, D)
-    ck, sk, rksb = _ring_tables(name, tables_k, B, Lk, D)
+    cq, sq, rqsb = _ring_tables(name, cos_q, sin_q, B, Lq, D)
+    ck, sk, rksb = _ring_tables(name, cos_k, sin_k, B, Lk, D)
     lib = _lib.load()
     one = lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, 1)
     flags = _lib.BWD_STAGE_DS if (one > 0 and workspace.numel() >= one) else 0
@@ -596,17 +623,135 @@ def ring_bwd_step(dout, q, k, v, out, lse, key_mask, tables_q, tables_k, scale, 
     _lib.check(st, name)
 
 
-def ring_dq_finish(dq_acc, tables_q, dq) -> None:
-    """``dq`` (bf16) = transposed rotation of ``bf16(dq_acc)``
-    (``avattn_ring_dq_finish``); a plain cast without tables."""
+def _ring_dq_finish_impl(dq_acc, cos_q, sin_q, dq):
     name = "avgen_amd.ring_dq_finish"
     _require_gpu(name, dq_acc, dq)
     B, H, L, D = dq_acc.shape
-    cq, sq, rqsb = _ring_tables(name, tables_q, B, L, D)
+    if dq_acc.dtype is not torch.float32 or dq.dtype is not torch.bfloat16 or dq.shape != dq_acc.shape:
+        raise ValueError(f"{name}: dq_acc must be float32 and dq bfloat16 of the same shape")
+    cq, sq, rqsb = _ring_tables(name, cos_q, sin_q, B, L, D)
     st = _lib.load().avattn_ring_dq_finish(
         _ptr(dq_acc), _strides3(dq_acc), B, H, L, D, _ptr(cq), _ptr(sq), rqsb, _ptr(dq), _strides3(dq),
         _stream(dq.device))
     _lib.check(st, name)
+
+
+def _lse_merge_impl(out_acc, lse_acc, out_blk, lse_blk):
+    name = "avgen_amd.lse_merge_"
+    _require_gpu(name, out_acc, lse_acc, out_blk, lse_blk)
+    if out_acc.dtype is not torch.float32 or lse_acc.dtype is not torch.float32 or lse_blk.dtype is not torch.float32:
+        raise TypeError(f"{name}: accumulators and block LSE must be float32")
+    if out_blk.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{name}: block output must be bfloat16 or float32")
+    if out_blk.shape != out_acc.shape or lse_acc.shape != lse_blk.shape or out_acc.shape[:-1] != lse_acc.shape:
+        raise ValueError(f"{name}: shapes disagree")
+    if not (out_acc.is_contiguous() and lse_acc.is_contiguous()):
+        raise ValueError(f"{name}: accumulators must be contiguous (they are updated in place)")
+    out_blk = out_blk.contiguous()
+    lse_blk = lse_blk.contiguous()
+    D = out_acc.shape[-1]
+    rows = lse_acc.numel()
+    st = _lib.load().avattn_lse_merge(
+        _ptr(out_acc), _ptr(lse_acc), _ptr(out_blk), _ptr(lse_blk), rows, D,
+        1 if out_blk.dtype is torch.bfloat16 else 0, _stream(out_acc.device),
+    )
+    _lib.check(st, name)
+
+
+# The ring's per-chunk steps as ops that update their accumulators in place
+# (schema: Tensor(a!)), so a compiled region that calls them keeps them as
+# opaque, correctly ordered mutations.
+
+
+@torch.library.custom_op("avgen_amd::ring_fwd_step", mutates_args=("out_acc", "lse_acc", "out"))
+def _ring_fwd_step_op(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_mask: Optional[torch.Tensor],
+    cos_q: Optional[torch.Tensor], sin_q: Optional[torch.Tensor], cos_k: Optional[torch.Tensor],
+    sin_k: Optional[torch.Tensor], scale: float, out_acc: torch.Tensor, lse_acc: torch.Tensor,
+    out: Optional[torch.Tensor], first: bool, last: bool,
+) -> None:
+    _ring_fwd_step_impl(q, k, v, key_mask, cos_q, sin_q, cos_k, sin_k, scale, out_acc, lse_acc, out, first, last)
+
+
+@_ring_fwd_step_op.register_fake
+def _(q, k, v, key_mask, cos_q, sin_q, cos_k, sin_k, scale, out_acc, lse_acc, out, first, last):
+    return None
+
+
+@torch.library.custom_op("avgen_amd::ring_bwd_step", mutates_args=("dq_acc", "dk", "dv", "workspace"))
+def _ring_bwd_step_op(
+    dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
+    key_mask: Optional[torch.Tensor], cos_q: Optional[torch.Tensor], sin_q: Optional[torch.Tensor],
+    cos_k: Optional[torch.Tensor], sin_k: Optional[torch.Tensor], scale: float, dq_acc: torch.Tensor,
+    dk: torch.Tensor, dv: torch.Tensor, workspace: torch.Tensor, reuse_query_side: bool,
+) -> None:
+    _ring_bwd_step_impl(dout, q, k, v, out, lse, key_mask, cos_q, sin_q, cos_k, sin_k, scale, dq_acc, dk, dv,
+                        workspace, reuse_query_side)
+
+
+@_ring_bwd_step_op.register_fake
+def _(dout, q, k, v, out, lse, key_mask, cos_q, sin_q, cos_k, sin_k, scale, dq_acc, dk, dv, workspace,
+      reuse_query_side):
+    return None
+
+
+@torch.library.custom_op("avgen_amd::ring_dq_finish", mutates_args=("dq",))
+def _ring_dq_finish_op(dq_acc: torch.Tensor, cos_q: Optional[torch.Tensor], sin_q: Optional[torch.Tensor],
+                       dq: torch.Tensor) -> None:
+    _ring_dq_finish_impl(dq_acc, cos_q, sin_q, dq)
+
+
+@_ring_dq_finish_op.register_fake
+def _(dq_acc, cos_q, sin_q, dq):
+    return None
+
+
+@torch.library.custom_op("avgen_amd::lse_merge", mutates_args=("out_acc", "lse_acc"))
+def _lse_merge_op(out_acc: torch.Tensor, lse_acc: torch.Tensor, out_blk: torch.Tensor, lse_blk: torch.Tensor) -> None:
+    _lse_merge_impl(out_acc, lse_acc, out_blk, lse_blk)
+
+
+@_lse_merge_op.register_fake
+def _(out_acc, lse_acc, out_blk, lse_blk):
+    return None
+
+
+def ring_fwd_step_(q, k, v, key_mask, tables_q, tables_k, scale, out_acc, lse_acc, out, *, first: bool,
+                   last: bool) -> None:
+    """One fused ring forward step (op ``avgen_amd::ring_fwd_step`` over
+    ``avattn_ring_fwd_step``): attention of the UNROTATED query shard ``q``
+    against one UNROTATED KV chunk, rotated on the fly with ``tables_q`` /
+    ``tables_k`` (RotaryTables or None), merged into the running fp32
+    ``out_acc`` / ``lse_acc`` (``first``: they take this chunk's result);
+    with ``last`` the merged output is also written to ``out`` (bf16, q's
+    shape).  Replaces apply_rotary + the ring's local op +
+    ``_SDPAMerger.step`` (torch/.../_context_parallel/_attention.py:182-183)."""
+    cq, sq = _table_pair(tables_q)
+    ck, sk = _table_pair(tables_k)
+    _ring_fwd_step_op(q, k, v, key_mask, cq, sq, ck, sk, float(scale), out_acc, lse_acc, out, bool(first),
+                      bool(last))
+
+
+def ring_bwd_step(dout, q, k, v, out, lse, key_mask, tables_q, tables_k, scale, dq_acc, dk, dv, *, workspace,
+                  reuse_query_side: bool) -> None:
+    """One fused ring backward step (op ``avgen_amd::ring_bwd_step`` over
+    ``avattn_ring_bwd_step``): adds this chunk's gradient of the rotated query
+    to the fp32 ``dq_acc`` and writes the chunk's ``dk`` (of the unrotated
+    keys) and ``dv`` in place.  ``workspace`` is a uint8 device tensor of at
+    least the plain backward's size; dS is staged when it holds at least one
+    (batch, kv head) pair's dS (torch/.../_attention.py:567-575)."""
+    cq, sq = _table_pair(tables_q)
+    ck, sk = _table_pair(tables_k)
+    _ring_bwd_step_op(dout, q, k, v, out, lse, key_mask, cq, sq, ck, sk, float(scale), dq_acc, dk, dv, workspace,
+                      bool(reuse_query_side))
+
+
+def ring_dq_finish(dq_acc, tables_q, dq) -> None:
+    """``dq`` (bf16) = transposed rotation of ``bf16(dq_acc)`` (op
+    ``avgen_amd::ring_dq_finish`` over ``avattn_ring_dq_finish``); a plain cast
+    without tables."""
+    cq, sq = _table_pair(tables_q)
+    _ring_dq_finish_op(dq_acc, cq, sq, dq)
 
 
 def _rope_apply_impl(x, cos, sin, inverse):
@@ -934,30 +1079,13 @@ def fp8_absmax_scales(x: torch.Tensor) -> torch.Tensor:
 
 
 def lse_merge_(out_acc: torch.Tensor, lse_acc: torch.Tensor, out_blk: torch.Tensor, lse_blk: torch.Tensor) -> None:
-    """In-place fp32 online-softmax merge (torch/.../_attention.py:182-183).
+    """In-place fp32 online-softmax merge (op ``avgen_amd::lse_merge``;
+    torch/.../_attention.py:182-183).
 
     ``out_acc``: fp32 contiguous (..., D); ``lse_acc``: fp32 contiguous (...);
     ``out_blk``: bf16 or fp32 with out_acc's shape; ``lse_blk``: lse_acc's shape.
     """
-    name = "avgen_amd.lse_merge_"
-    _require_gpu(name, out_acc, lse_acc, out_blk, lse_blk)
-    if out_acc.dtype is not torch.float32 or lse_acc.dtype is not torch.float32 or lse_blk.dtype is not torch.float32:
-        raise TypeError(f"{name}: accumulators and block LSE must be float32")
-    if out_blk.dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"{name}: block output must be bfloat16 or float32")
-    if out_blk.shape != out_acc.shape or lse_acc.shape != lse_blk.shape or out_acc.shape[:-1] != lse_acc.shape:
-        raise ValueError(f"{name}: shapes disagree")
-    if not (out_acc.is_contiguous() and lse_acc.is_contiguous()):
-        raise ValueError(f"{name}: accumulators must be contiguous (they are updated in place)")
-    out_blk = out_blk.contiguous()
-    lse_blk = lse_blk.contiguous()
-    D = out_acc.shape[-1]
-    rows = lse_acc.numel()
-    st = _lib.load().avattn_lse_merge(
-        _ptr(out_acc), _ptr(lse_acc), _ptr(out_blk), _ptr(lse_blk), rows, D,
-        1 if out_blk.dtype is torch.bfloat16 else 0, _stream(out_acc.device),
-    )
-    _lib.check(st, name)
+    _lse_merge_op(out_acc, lse_acc, out_blk, lse_blk)
 
 
 def rope_tables(

@@ -27,6 +27,7 @@ import torch
 
 from . import ops
 from .context import shard_bounds
+from .rope import RotaryTables
 
 __all__ = [
     "SDPAMerger",
@@ -203,6 +204,13 @@ def ring_attention_backward(
     return dq_acc.to(query.dtype), dks, dvs
 
 
+def _ring_workspace(B, Hq, Hkv, Lq, D, bounds, device):
+    """One backward workspace for every chunk of the ring: that of the longest
+    chunk (chunks of a contiguous split differ by at most one key)."""
+    longest = max(b - a for a, b in bounds)
+    return ops._alloc_bwd_workspace(B, Hq, Hkv, Lq, longest, D, device)
+
+
 def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, scale, overlap=False):
     """The emulated ring's backward.  Each chunk's dk/dv goes straight into its
     slice of the full-sequence gradients (one chunk, one contribution, so no
@@ -255,8 +263,7 @@ def _ring_backward_into(grad_out, query, key, value, out, lse, key_mask, cp, sca
                 done[w].record(side)
         main.wait_stream(side)
     else:
-        need = max(ops.bwd_workspace_plan(B, Hq, Hkv, Lq, b - a, D, query.device)[0] for a, b in bounds)
-        ws = ops._workspace(need, query.device)
+        ws = _ring_workspace(B, Hq, Hkv, Lq, D, bounds, query.device)
         for r, (a, b) in enumerate(bounds):
             ops._bwd_impl(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse, masks[r], scale,
                           dk=dk[:, :, a:b], dv=dv[:, :, a:b], workspace=ws, reuse_query_side=r > 0,
@@ -308,8 +315,7 @@ def _ring_backward_fused(grad_out, query, key, value, out, lse, key_mask, cp, sc
         return dq.zero_(), dk.zero_(), dv.zero_()
     dq_acc = torch.zeros(query.shape, dtype=torch.float32, device=query.device)
     bounds = [shard_bounds(L, cp, r) for r in range(cp)]
-    need = max(ops.bwd_workspace_plan(B, Hq, Hkv, Lq, b - a, D, query.device)[0] for a, b in bounds)
-    ws = ops._workspace(need, query.device)
+    ws = _ring_workspace(B, Hq, Hkv, Lq, D, bounds, query.device)
     for r, (a, b) in enumerate(bounds):
         ops.ring_bwd_step(grad_out, query, key[:, :, a:b], value[:, :, a:b], out, lse,
                           None if key_mask is None else key_mask[:, a:b], tables_q, _chunk_tables(tables_k, a, b),
@@ -318,25 +324,60 @@ def _ring_backward_fused(grad_out, query, key, value, out, lse, key_mask, cp, sc
     return dq, dk, dv
 
 
-class _RingAttentionRope(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, query, key, value, key_mask, cp, scale, tables_q, tables_k):
-        s = ops.default_scale(query.shape[-1]) if scale is None else float(scale)
-        out, lse = _ring_forward_fused(query, key, value, key_mask, cp, s, tables_q, tables_k)
-        ctx.save_for_backward(query, key, value, out, lse, key_mask)
-        ctx.cp = cp
-        ctx.scale = s
-        ctx.tables = (tables_q, tables_k)
-        ctx.mark_non_differentiable(lse)
-        return out, lse
+# The RoPE-fused emulated ring as one op pair with registered autograd: a
+# compiled region (torch.compile per block, src/avgen/parallel/apply.py
+# :216-221) sees two opaque ops, whose implementations run the per-chunk
+# step ops above in ring order.
 
-    @staticmethod
-    def backward(ctx, grad_out, _grad_lse):
-        query, key, value, out, lse, key_mask = ctx.saved_tensors
-        tables_q, tables_k = ctx.tables
-        dq, dk, dv = _ring_backward_fused(grad_out.contiguous(), query, key, value, out, lse, key_mask, ctx.cp,
-                                          ctx.scale, tables_q, tables_k)
-        return dq, dk, dv, None, None, None, None, None
+
+@torch.library.custom_op("avgen_amd::ring_attention_rope", mutates_args=())
+def _ring_attention_rope_op(
+    query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, key_mask: Optional[torch.Tensor],
+    cos_q: torch.Tensor, sin_q: torch.Tensor, cos_k: torch.Tensor, sin_k: torch.Tensor, cp: int, scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    return _ring_forward_fused(query, key, value, key_mask, cp, scale, RotaryTables(cos_q, sin_q),
+                               RotaryTables(cos_k, sin_k))
+
+
+@_ring_attention_rope_op.register_fake
+def _(query, key, value, key_mask, cos_q, sin_q, cos_k, sin_k, cp, scale):
+    B, H, Lq, _ = query.shape
+    return torch.empty_like(query), query.new_empty((B, H, Lq), dtype=torch.float32)
+
+
+@torch.library.custom_op("avgen_amd::ring_attention_rope_bwd", mutates_args=())
+def _ring_attention_rope_bwd_op(
+    grad_out: torch.Tensor, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, out: torch.Tensor,
+    lse: torch.Tensor, key_mask: Optional[torch.Tensor], cos_q: torch.Tensor, sin_q: torch.Tensor,
+    cos_k: torch.Tensor, sin_k: torch.Tensor, cp: int, scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return _ring_backward_fused(grad_out.contiguous(), query, key, value, out, lse, key_mask, cp, scale,
+                                RotaryTables(cos_q, sin_q), RotaryTables(cos_k, sin_k))
+
+
+@_ring_attention_rope_bwd_op.register_fake
+def _(grad_out, query, key, value, out, lse, key_mask, cos_q, sin_q, cos_k, sin_k, cp, scale):
+    return torch.empty_like(query), key.new_empty(key.shape), value.new_empty(value.shape)
+
+
+def _ring_rope_setup(ctx, inputs, output):
+    query, key, value, key_mask, cos_q, sin_q, cos_k, sin_k, cp, scale = inputs
+    out, lse = output
+    ctx.cp = cp
+    ctx.scale = scale
+    ctx.save_for_backward(query, key, value, out, lse, key_mask, cos_q, sin_q, cos_k, sin_k)
+    ctx.mark_non_differentiable(lse)
+
+
+def _ring_rope_backward(ctx, grad_out, _grad_lse):
+    query, key, value, out, lse, key_mask, cos_q, sin_q, cos_k, sin_k = ctx.saved_tensors
+    dq, dk, dv = _ring_attention_rope_bwd_op(grad_out, query, key, value, out, lse, key_mask, cos_q, sin_q, cos_k,
+                                             sin_k, ctx.cp, ctx.scale)
+    return dq, dk, dv, None, None, None, None, None, None, None
+
+
+torch.library.register_autograd("avgen_amd::ring_attention_rope", _ring_rope_backward,
+                                setup_context=_ring_rope_setup)
 
 
 class _RingAttention(torch.autograd.Function):
@@ -389,5 +430,7 @@ def ring_attention(
         raise ValueError("pass both tables_q and tables_k, or neither")
     if tables_q is not None:
         shard_bounds(key.shape[2], cp, 0)  # ragged lengths raise before any launch
-        return _RingAttentionRope.apply(query, key, value, key_mask, cp, scale, tables_q, tables_k)
+        s = ops.default_scale(query.shape[-1]) if scale is None else float(scale)
+        return _ring_attention_rope_op(query, key, value, key_mask, tables_q.cos, tables_q.sin, tables_k.cos,
+                                       tables_k.sin, int(cp), s)
     return _RingAttention.apply(query, key, value, key_mask, cp, scale)
