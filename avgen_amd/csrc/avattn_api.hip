@@ -32,12 +32,22 @@ int check_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32
   const int64_t ktiles = ((int64_t)Lk + 127) / 128;
   if (qtiles * B * Hq > kMaxI32 || ktiles * B * Hkv > kMaxI32) return AVATTN_ERR_TOO_LARGE;
   if ((int64_t)B * Hq * Lq > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
-  // The kernels address one (batch, head) slice of a padded copy (and, in the
-  // backward, the query heads of one group) through 32-bit buffer ranges:
-  // group * Lqp * D and Lkp * D bf16 must stay below 2^32 bytes.
-  const int64_t Lqp = transpose_padded_len(Lq), Lkp = transpose_padded_len(Lk);
-  const int64_t lim = (int64_t)1 << 32;
-  if ((int64_t)(Hq / Hkv) * Lqp * D * 2 >= lim || Lkp * D * 2 >= lim) return AVATTN_ERR_TOO_LARGE;
+  // Every kernel addresses one (batch, kv head) slice of a padded key copy
+  // through a 32-bit buffer range: Lkp * D bf16 must stay below 2^32 bytes.
+  const int64_t Lkp = transpose_padded_len(Lk);
+  if (Lkp * D * 2 >= ((int64_t)1 << 32)) return AVATTN_ERR_TOO_LARGE;
+  return AVATTN_OK;
+}
+
+// check_dims, plus the backward's own range: its dK/dV kernel stages the
+// padded q and dout rows of all query heads of one group through one 32-bit
+// buffer range each (group * Lqp * D bf16 below 2^32 bytes).  The forward
+// builds no range over q, so long grouped-query shapes stay valid there.
+int check_bwd_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32_t D) {
+  const int st = check_dims(B, Hq, Hkv, Lq, Lk, D);
+  if (st != AVATTN_OK || Hkv == 0 || Hq == 0) return st;
+  const int64_t Lqp = transpose_padded_len(Lq);
+  if ((int64_t)(Hq / Hkv) * Lqp * D * 2 >= ((int64_t)1 << 32)) return AVATTN_ERR_TOO_LARGE;
   return AVATTN_OK;
 }
 
@@ -365,7 +375,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
                     const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
                     size_t workspace_bytes, uint32_t flags, avattn_stream_t stream, const int32_t* window_lo,
                     const int32_t* window_hi, int64_t window_batch_stride, const RingOpts* ring = nullptr) {
-  int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  int st = check_bwd_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32 | AVATTN_BWD_STAGE_DS |
                 AVATTN_BWD_DEFER_DQ))
     return AVATTN_ERR_ARGUMENT;
@@ -514,7 +524,7 @@ int avattn_bwd_windowed(const void* dout, const void* q, const void* k, const vo
 int avattn_bwd_dq_staged(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
                          int32_t head_dim, float scale, void* dq, const int64_t* dq_strides, void* workspace,
                          size_t workspace_bytes, uint32_t flags, avattn_stream_t stream) {
-  int st = check_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  int st = check_bwd_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (st != AVATTN_OK) return st;
   if (flags & ~AVATTN_BWD_DQ_ACCUMULATE_F32) return AVATTN_ERR_ARGUMENT;
   const bool dq_f32 = (flags & AVATTN_BWD_DQ_ACCUMULATE_F32) != 0;

@@ -229,9 +229,10 @@ class LaunchTimer {
   hipStream_t stream_;
 };
 
-// Sequence length of a head_dim-major copy (prep.hip): padded to whole
-// 64-row tiles.
-inline int transpose_padded_len(int L) { return (L + 63) / 64 * 64; }
+// Sequence length of a padded copy (prep.hip): whole 64-row tiles.  In 64
+// bits, so that the validation of a length near INT32_MAX sees the true
+// padded length; validated problems fit in int.
+inline int64_t transpose_padded_len(int64_t L) { return (L + 63) / 64 * 64; }
 
 // Padded key bias (B, Lkp) floats (0 attended / -inf) and per-32-key-tile
 // "all attended" flags (B, Lkp/32); mask may be null (only the tail is masked).

@@ -160,11 +160,15 @@ def test_fwd_validation_paths(lib):
     assert _fwd(lib, k=None) == _lib.ERR_NULL_POINTER
     assert _fwd(lib, mask=16, msb=2) == _lib.ERR_ARGUMENT
     assert _fwd(lib, B=1, Hq=1 << 30, Hkv=1, Lq=1 << 20) == _lib.ERR_TOO_LARGE
-    # 32-bit buffer ranges: one padded (b, head) slice of k (Lkp*D*2 bytes)
-    # and the query heads of one group in the backward (group*Lqp*D*2).
+    # 32-bit buffer ranges: one padded (b, head) slice of k (Lkp*D*2 bytes).
+    # The query heads of one group (group*Lqp*D*2) bound only the backward.
     assert _fwd(lib, Lk=(1 << 24) - 64) == _lib.ERR_WORKSPACE  # 4 GiB - 16 KiB per slice: still addressable
     assert _fwd(lib, Lk=1 << 24) == _lib.ERR_TOO_LARGE
-    assert _fwd(lib, Hq=40, Hkv=1, Lq=420_000) == _lib.ERR_TOO_LARGE  # MQA, 40 * 420k rows * 256 B >= 2^32
+    # lengths within 63 of INT32_MAX: the padded length is computed in 64 bits
+    assert _fwd(lib, Lk=(1 << 31) - 1) == _lib.ERR_TOO_LARGE
+    assert _fwd(lib, Lk=(1 << 31) - 40) == _lib.ERR_TOO_LARGE
+    # MQA with a long query: 40 * 420k rows * 256 B >= 2^32, fine for the forward
+    assert _fwd(lib, Hq=40, Hkv=1, Lq=420_000, ws=8) == _lib.ERR_WORKSPACE
     assert _fwd(lib, Hq=40, Hkv=1, Lq=400_000, ws=8) == _lib.ERR_WORKSPACE
     assert _fwd(lib, ws=None) == _lib.ERR_WORKSPACE
     assert _fwd(lib, wsb=100) == _lib.ERR_WORKSPACE  # needs more than 2 * (2*128*64*2) bytes
@@ -237,6 +241,14 @@ def test_bwd_validation_paths(lib):
     base = [16, 16, 16, 16, 16, 16, s, s, s, s, s, 1, 2, 2, 4, 4, 128, None, 0, 0.125,
             16, s, 16, s, 16, s, 16, 8, 0, None]
     assert lib.avattn_bwd(*base) == _lib.ERR_WORKSPACE  # 8 bytes < 2*1*2*4*4
+    # the query heads of one group go through one 32-bit range in the backward
+    mqa = list(base)
+    mqa[12], mqa[13], mqa[14] = 40, 1, 420_000  # heads_q, heads_kv, len_q
+    assert lib.avattn_bwd(*mqa) == _lib.ERR_TOO_LARGE
+    mqa[14] = 400_000  # 40 * 400k rows * 256 B < 2^32: valid, fails on the workspace
+    assert lib.avattn_bwd(*mqa) == _lib.ERR_WORKSPACE
+    assert lib.avattn_bwd_dq_staged(1, 40, 1, 420_000, 4, 128, 0.125, 16, s, 16, 1 << 20, 0, None) == \
+        _lib.ERR_TOO_LARGE
     bad = list(base)
     bad[28] = 8  # unknown flag
     assert lib.avattn_bwd(*bad) == _lib.ERR_ARGUMENT
