@@ -441,6 +441,49 @@ def test_staged_ds_in_passes_matches_recompute(amd, monkeypatch):
     assert np.abs(_f64(got[0]) - rq).max() <= GRAD_REL_TOL * np.abs(rq).max()
 
 
+def test_tail_split_changes_only_the_split_blocks(amd):
+    """dk/dv bits depend on the dK/dV grid's tail split, i.e. on the device's
+    CU count and on how the (batch, kv head) pairs are split into passes: a
+    pass whose 128-key blocks exceed one round of CUs gives its last
+    ``total % cus`` blocks to several workgroups, whose fp32 partial sums add
+    in another order.  Here 3 pairs x 100 blocks: one pass (300 blocks, split
+    tail) against three passes of 100 blocks (no split).  Keys outside the
+    split blocks are bit-identical; the split blocks agree to fp32
+    reassociation (then one bf16 rounding)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    B, H, Lq, D = 1, 3, 512, 128
+    nkt = 100
+    Lk = 128 * nkt
+    if H * nkt <= cus:
+        pytest.skip(f"{cus} CUs: 300 blocks fit one round, no tail split")
+    q, k, v = _randn((B, H, Lq, D), 84).cuda(), _randn((B, H, Lk, D), 85).cuda(), _randn((B, H, Lk, D), 86).cuda()
+    do = _randn((B, H, Lq, D), 87).cuda()
+    out, lse = amd.ops.flash_fwd(q, k, v, None, None, None, D ** -0.5)
+    per = amd.ops.ds_bytes_per_pair(1, Lq, Lk)
+    results = []
+    for budget in (H * per, per):  # one pass of 300 blocks; three of 100
+        amd.ops.set_ds_budget(budget, q.device)
+        try:
+            results.append(amd.ops._bwd_impl(do, q, k, v, out, lse, None, D ** -0.5))
+        finally:
+            amd.ops.set_ds_budget(None, q.device)
+    torch.cuda.synchronize()
+    (dq1, dk1, dv1), (dq3, dk3, dv3) = results
+    total = H * nkt
+    first_split = total - total % cus  # flat (pair, block) index of the first split block
+    split_keys = torch.zeros(B, H, Lk, dtype=torch.bool, device="cuda")
+    for flat in range(first_split, total):
+        split_keys[0, flat // nkt, 128 * (flat % nkt):128 * (flat % nkt + 1)] = True
+    for a_, b_ in ((dk1, dk3), (dv1, dv3)):
+        differs = (a_ != b_).any(-1)
+        assert not (differs & ~split_keys).any()
+        rel = ((a_.float() - b_.float()).abs().max() / b_.float().abs().max()).item()
+        assert rel <= 4e-3, rel
+    print(f"{cus} CUs: {int(split_keys.sum())} keys in split blocks, "
+          f"{int((dk1 != dk3).any(-1).sum())} dk rows differ", flush=True)
+    assert torch.equal(dq1, dq3)  # dq does not depend on the split
+
+
 @pytest.mark.parametrize("masked", [False, True])
 def test_ring_backward_overlapped_dq_is_identical(amd, masked):
     """The ring backward with each chunk's dq on a side stream (two

@@ -95,3 +95,41 @@ def test_noalloc_forward_equals_workspace_forward():
     assert _call(lib, "avattn_fwd_noalloc", q, k, v, None, None, out, lse) == _lib.ERR_SCRATCH
     torch.cuda.synchronize()
     assert (out == 7.0).all() and (lse == 7.0).all()
+
+
+def test_noalloc_forward_under_graph_capture():
+    """The entry point inside a captured HIP graph (torch.cuda.graph): after
+    one eager call (the first call per device looks the scratch array up),
+    a capture of avattn_fwd_noalloc replays three times, with eager work
+    between the replays, each time giving avattn_fwd's bits."""
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    import avgen_amd
+
+    lib = _lib.load()
+    B, Hq, Hkv, Lq, Lk, D = 2, 4, 2, 300, 1500, 128
+    print(f"noalloc graph capture: B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} mask rope", flush=True)
+    q = _rand((B, Hq, Lq, D), 71, 0.7)
+    k, v = _rand((B, Hkv, Lk, D), 72, 0.7), _rand((B, Hkv, Lk, D), 73, 0.7)
+    g = torch.Generator()
+    g.manual_seed(7)
+    mask = (torch.rand((B, Lk), generator=g) > 0.2).cuda().view(torch.uint8)
+    coords = torch.rand((B, Lq, 3), generator=torch.Generator().manual_seed(7)).cuda() * 10
+    tables = avgen_amd.rope.build_rotary_tables(coords, head_dim=D)
+    ws = torch.empty(lib.avattn_fwd_workspace_size(B, Hkv, Lk, D), dtype=torch.uint8, device="cuda")
+    out_a, lse_a = torch.empty_like(q), torch.empty((B, Hq, Lq), device="cuda")
+    assert _call(lib, "avattn_fwd", q, k, v, mask, tables, out_a, lse_a, ws) == _lib.OK
+    out_b, lse_b = torch.empty_like(q), torch.empty((B, Hq, Lq), device="cuda")
+    assert _call(lib, "avattn_fwd_noalloc", q, k, v, mask, tables, out_b, lse_b) == _lib.OK  # warm-up
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _call(lib, "avattn_fwd_noalloc", q, k, v, mask, tables, out_b, lse_b)
+    assert rc == _lib.OK
+    for rep in range(3):
+        out_b.fill_(float("nan"))
+        lse_b.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, out_b) and torch.equal(lse_a, lse_b), rep
