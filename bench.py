@@ -55,6 +55,14 @@ CONFIGS = {
                     "21x45x80 latent), 40 heads x d128, RoPE + ring fwd (merge) + ring bwd"),
     "c4": dict(B=2, H=40, Lq=76112, L=76112, D=128, cp=1, grid=(21, 45, 80), text=512,
                desc="c4 joint text+video: (2,40,76112,128), 512 text slots with key-padding mask"),
+    # CrossAttention of the video tokens into the text context
+    # (src/avgen/models/layers.py:629-670): 512 text slots, batch 0's text
+    # length U[16, 512], batch 1 the CFG unconditional pass's null text (an
+    # all-False key mask, src/avgen/infer/pipeline.py:818-822).  No RoPE.
+    "cross": dict(B=2, H=40, Lq=75600, L=512, D=128, cp=1, grid=(21, 45, 80), text=512, cross=True,
+                  null_text_rows=(1,),
+                  desc="cross-attention: (2,40,75600,128) video queries x 512 text keys, batch 0 text length "
+                       "U[16,512], batch 1 null text (all keys masked), fwd+bwd, no RoPE"),
     "c5": dict(B=2, H=40, Lq=75600, L=75600, D=128, cp=1, grid=(21, 45, 80), text=0,
                desc="c5 sampling with CFG batch: (2,40,75600,128) forward only, bf16 and fp8 (e4m3) q k^T "
                     "with per-head absmax scales, repeated calls"),
@@ -104,6 +112,13 @@ def make_inputs(cfg: dict, device) -> dict:
     k = rnd((B, H, L, D), 1, s)
     v = rnd((B, H, L, D), 2, s)
     do = rnd((B, H, Lq, D), 3, 1.0)
+    if cfg.get("cross"):
+        gen.manual_seed(4)
+        lengths = torch.randint(16, L + 1, (B,), device=device, generator=gen)
+        mask = torch.arange(L, device=device)[None, :] < lengths[:, None]
+        for b in cfg["null_text_rows"]:
+            mask[b] = False
+        return dict(q=q, k=k, v=v, do=do, tables_q=None, tables_k=None, mask=mask)
     F_, Hh, W = cfg["grid"]
     coords = video_coords(F_, Hh, W, B, device)
     mask = None
@@ -126,6 +141,13 @@ def step(cfg: dict, x: dict) -> None:
     q = x["q"].requires_grad_(True)
     k = x["k"].requires_grad_(True)
     v = x["v"].requires_grad_(True)
+    if cfg.get("cross"):
+        # CrossAttention's call (src/avgen/models/layers.py:656-669): a
+        # (batch, 1, 1, keys) text mask, no rotation.
+        out = avgen_amd.attention.attention(q, k, v, attn_mask=x["mask"][:, None, None, :])
+        out.backward(x["do"])
+        q.grad = k.grad = v.grad = None
+        return
     # RoPE fused into the ring's kernels (q rotated on load, k in its operand
     # copy, dq/dk rotated back in the backward's epilogues); cp = 1 is the
     # unchunked attention of the c2/c4 blocks.
@@ -753,7 +775,10 @@ def main() -> int:
         torch.cuda.synchronize()
         log(f"[bench] warmup {i + 1}/{args.warmup} done")
 
-    launches = 64 * args.steps + 64
+    # Per step: per KV chunk the forward and its copies, then per dS pass the
+    # dK/dV kernel, its tail reduction and dQ, plus the query-side copies.
+    passes = max(1, ds_plan(cfg, dev)["passes_per_chunk"])
+    launches = (8 * cfg["cp"] * (passes + 2) + 32) * args.steps + 64
     with _lib.LaunchTiming(launches) as timing:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -786,7 +811,7 @@ def main() -> int:
     }
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not cfg.get("cross"):
         log("[bench] CPU baseline ...")
         cpu = cpu_baseline(cfg, args.cpu_budget)
         log(f"[bench] CPU baseline {cpu['value']:.4f} TFLOP/s on {cpu['cores']} cores")

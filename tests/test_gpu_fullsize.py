@@ -410,3 +410,130 @@ def test_temporal_window_full_latent_equals_frame_blocks(amd):
         gv += rv[:, :, :T].float()
     assert _max_rel(dk[:, :, ks], gk) <= GRAD_REL_TOL
     assert _max_rel(dv[:, :, ks], gv) <= GRAD_REL_TOL
+
+
+def _bench_rand(shape, seed, scale):
+    """bench.py's input generator (make_inputs): float32 N(0,1) * scale, then bf16."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return (torch.randn(shape, device="cuda", dtype=torch.float32, generator=g) * scale).to(torch.bfloat16)
+
+
+def test_c4_bench_path_with_rope_and_text_mask(amd):
+    """c4 through the benchmark's own call: ``ring_attention(cp=1, key_mask,
+    tables_q, tables_k)`` on (2, 40, 76112, 128), the 3D RoPE over the
+    concatenated video+text coordinates fused into the kernels (text slots
+    at zero coordinates, so their rotation is the identity;
+    src/avgen/models/dit.py:849-904, RoPE over the concatenated coords at
+    :882), text keys masked past each sample's length.  Sampled video and
+    text query rows (output, LSE, dq) and sampled video and text keys, valid
+    or masked (dk of the unrotated keys, dv), against float32 on the rotated
+    operands; masked keys get exactly zero dk/dv."""
+    B, H, Lv, T, D = 2, 40, 75600, 512, 128
+    L = Lv + T
+    print(f"c4 bench path B={B} H={H} L={L} D={D} (RoPE + text mask)", flush=True)
+    scale = D ** -0.5
+    s2 = 2 ** -0.5
+    q, k, v = _bench_rand((B, H, L, D), 0, s2), _bench_rand((B, H, L, D), 1, s2), _bench_rand((B, H, L, D), 2, s2)
+    do = _bench_rand((B, H, L, D), 3, 1.0)
+    coords = torch.cat([_video_coords(21, 45, 80).expand(B, -1, -1), torch.zeros(B, T, 3)], dim=1).cuda()
+    tables = amd.rope.build_rotary_tables(coords, head_dim=D)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    lengths = torch.randint(16, T + 1, (B,), device="cuda", generator=g)
+    mask = torch.cat([torch.ones(B, Lv, dtype=torch.bool, device="cuda"),
+                      torch.arange(T, device="cuda")[None, :] < lengths[:, None]], dim=1)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out, lse = amd.ring.ring_attention(qg, kg, vg, cp=1, key_mask=mask, tables_q=tables, tables_k=tables)
+    out.backward(do)
+    qr, kr = amd.rope.apply_rotary(q, tables), amd.rope.apply_rotary(k, tables)
+    torch.cuda.synchronize()
+    assert torch.equal(qr[:, :, Lv:], q[:, :, Lv:]) and torch.equal(kr[:, :, Lv:], k[:, :, Lv:])
+    rows = torch.cat([torch.arange(0, Lv, 151, device="cuda")[:448], torch.arange(Lv, L, 8, device="cuda")])
+    keys = torch.cat([torch.arange(0, Lv, 997, device="cuda")[:64], torch.arange(Lv, L, 4, device="cuda")])
+    worst = [0.0] * 5
+    for b in range(B):
+        mb = mask[b]
+        cq, sq = tables.cos[b, 0, rows], tables.sin[b, 0, rows]
+        ck, sk = tables.cos[b, 0, keys], tables.sin[b, 0, keys]
+        for h in (0, 19, H - 1):
+            qh, kh, vh = qr[b, h].float(), kr[b, h].float(), v[b, h].float()
+            doh, oh = do[b, h].float(), out[b, h].float()
+            ro, rl = _ref_rows(qr[b, h, rows], kr[b, h], v[b, h], scale, mb)
+            e_o = (oh[rows] - ro).abs().max().item()
+            e_l = (lse[b, h, rows] - rl).abs().max().item()
+            s = (torch.mm(qh[rows], kh.t().contiguous()) * scale).masked_fill(~mb[None, :], float("-inf"))
+            p = torch.exp(s - rl[:, None])
+            delta = (doh[rows] * oh[rows]).sum(-1)
+            ds = p * (torch.mm(doh[rows], vh.t().contiguous()) - delta[:, None])
+            e_q = _max_rel(qg.grad[b, h, rows], _unrotate32(torch.mm(ds, kh) * scale, cq, sq))
+            del s, p, ds
+            s = (torch.mm(qh, kh[keys].t().contiguous()) * scale).masked_fill(~mb[keys][None, :], float("-inf"))
+            p = torch.exp(s - lse[b, h][:, None])
+            delta = (doh * oh).sum(-1)
+            ds = p * (torch.mm(doh, vh[keys].t().contiguous()) - delta[:, None])
+            rk = _unrotate32(torch.mm(ds.t().contiguous(), qh) * scale, ck, sk)
+            rv = torch.mm(p.t().contiguous(), doh)
+            e_k = (kg.grad[b, h, keys].float() - rk).abs().max().item() / kg.grad[b, h].float().abs().max().item()
+            e_v = (vg.grad[b, h, keys].float() - rv).abs().max().item() / vg.grad[b, h].float().abs().max().item()
+            del s, p, ds
+            worst = [max(a, c) for a, c in zip(worst, (e_o, e_l, e_q, e_k, e_v))]
+    print(f"  worst: out {worst[0]:.2e} lse {worst[1]:.2e} dq {worst[2]:.2e} dk {worst[3]:.2e} dv {worst[4]:.2e}",
+          flush=True)
+    assert worst[0] <= OUT_TOL and worst[1] <= LSE_TOL
+    assert max(worst[2:]) <= GRAD_REL_TOL
+    masked = (~mask)[:, None, :, None].expand_as(kg.grad)
+    assert torch.all(kg.grad[masked] == 0) and torch.all(vg.grad[masked] == 0)
+
+
+def test_cross_attention_real_shape_with_null_text(amd):
+    """CrossAttention at its real shape (src/avgen/models/layers.py:629-670):
+    (2, 40, 75600, 128) video queries against 512 text slots through
+    ``attention(q, k, v, attn_mask=mask[:, None, None, :])``, batch 0 with a
+    text length in [16, 512], batch 1 the null text of the CFG unconditional
+    pass (every key masked, src/avgen/infer/pipeline.py:818-822).  Batch 0:
+    whole heads (every query row, every key) against float32, forward and
+    backward.  Batch 1: output, LSE and every gradient exactly as SDPA gives
+    a fully masked row (zeros; LSE -inf)."""
+    B, H, Lq, T, D = 2, 40, 75600, 512, 128
+    print(f"cross-attention B={B} H={H} Lq={Lq} text={T} D={D} (batch 1 null text)", flush=True)
+    scale = D ** -0.5
+    s2 = 2 ** -0.5
+    q, k, v = _bench_rand((B, H, Lq, D), 0, s2), _bench_rand((B, H, T, D), 1, s2), _bench_rand((B, H, T, D), 2, s2)
+    do = _bench_rand((B, H, Lq, D), 3, 1.0)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    lengths = torch.randint(16, T + 1, (B,), device="cuda", generator=g)
+    mask = torch.arange(T, device="cuda")[None, :] < lengths[:, None]
+    mask[1] = False
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = amd.attention.attention(qg, kg, vg, attn_mask=mask[:, None, None, :])
+    out.backward(do)
+    _, lse = amd.ops.flash_fwd(q, k, v, mask, None, None, scale)
+    torch.cuda.synchronize()
+    print(f"  batch 0 text length {int(lengths[0])}", flush=True)
+    assert torch.all(out[1] == 0) and torch.all(lse[1] == float("-inf"))
+    for grad in (qg.grad, kg.grad, vg.grad):
+        assert torch.all(grad[1] == 0)
+    m0 = mask[0]
+    assert torch.all(kg.grad[0][:, ~m0] == 0) and torch.all(vg.grad[0][:, ~m0] == 0)
+    worst = [0.0] * 5
+    for h in (0, 20, H - 1):
+        qh, kh, vh, doh = q[0, h].float(), k[0, h].float(), v[0, h].float(), do[0, h].float()
+        s = (torch.mm(qh, kh.t().contiguous()) * scale).masked_fill(~m0[None, :], float("-inf"))
+        rl = torch.logsumexp(s, dim=-1)
+        p = torch.exp(s - rl[:, None])
+        ro = torch.mm(p, vh)
+        delta = (doh * ro).sum(-1)
+        ds = p * (torch.mm(doh, vh.t().contiguous()) - delta[:, None])
+        rq = torch.mm(ds, kh) * scale
+        rk = torch.mm(ds.t().contiguous(), qh) * scale
+        rv = torch.mm(p.t().contiguous(), doh)
+        e = ((out[0, h].float() - ro).abs().max().item(), (lse[0, h] - rl).abs().max().item(),
+             _max_rel(qg.grad[0, h], rq), _max_rel(kg.grad[0, h], rk), _max_rel(vg.grad[0, h], rv))
+        worst = [max(a, c) for a, c in zip(worst, e)]
+        del s, p, ds
+    print(f"  worst: out {worst[0]:.2e} lse {worst[1]:.2e} dq {worst[2]:.2e} dk {worst[3]:.2e} dv {worst[4]:.2e}",
+          flush=True)
+    assert worst[0] <= OUT_TOL and worst[1] <= LSE_TOL
+    assert max(worst[2:]) <= GRAD_REL_TOL
