@@ -436,10 +436,17 @@ struct TileStager {
 // 16 bytes per lane at byte base + voff + soff of a raw buffer, non-temporal
 // (streamed past the caches, so a large write does not evict the reader's
 // cached tiles).  Inline assembly like the loads above: the caller counts
-// these stores in its vmcnt waits.
+// these stores in its vmcnt waits.  A store of more than 8 bytes with an
+// SGPR offset reads its data registers for one more cycle: the next
+// instruction must not be a VALU write of them (one wait state).  The
+// compiler inserts that wait state after the stores it emits itself, not
+// after inline assembly, so the s_nop is part of the statement.
 __device__ __forceinline__ void store_b128_nt(const u32x4& r, uint32_t voff, uint32_t soff, const u32x4& data) {
-  __asm__ volatile("buffer_store_dwordx4 %0, %1, %2, %3 offen nt" ::"v"(data), "v"(voff), "s"(r), "s"(soff)
-                   : "memory");
+  __asm__ volatile(
+      "buffer_store_dwordx4 %0, %1, %2, %3 offen nt\n\t"
+      "s_nop 0" ::"v"(data),
+      "v"(voff), "s"(r), "s"(soff)
+      : "memory");
 }
 
 // dma16 with a non-temporal load (data read once).
