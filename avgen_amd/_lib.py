@@ -107,6 +107,21 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.c_uint32,
          c_ptr],
     ),
+    "avattn_bwd_windowed_compact": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_i64p, c_i64p, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_ptr, c_i64, c_i64,
+         c_f32,
+         c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
+         c_ptr, c_size,
+         ctypes.c_uint32,
+         c_ptr],
+    ),
+    "avattn_bwd_compact_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i64]),
     "avattn_ring_fwd_step": (
         ctypes.c_int,
         [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,

@@ -523,17 +523,53 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // phase, so the partner's P has been handed over by the barrier in
   // between: dS = P * dp, dK^T += Q^T dS and, with STAGE, the dS stores
   // (kDsStores per lane).
-  auto ds_phase = [&](int it, auto uc, const f32x16(&dp)[2]) {
-    constexpr uint32_t u = decltype(uc)::value;
-    // This tile's two dS units (query groups 2*tile_idx(it) and +1).
-    u32x4 rds = {0u, 0u, 0u, 0u};
-    uint32_t ds_unit1 = 0;
+  // Where tile `it`'s dS goes (STAGE): a buffer over its two units (query
+  // groups 2*tile_idx(it) and +1) and the byte distance between them.
+  // Computed at the top of the iteration whose dS phase stores them, so the
+  // compact layout's table load is in flight during the dP phase.
+  struct DsDest {
+    u32x4 rds;
+    uint32_t unit1;
+  };
+  auto ds_dest = [&](int it) {
+    DsDest d{{0u, 0u, 0u, 0u}, 0u};
     if constexpr (STAGE) {
       const int64_t bq = (int64_t)(bhk - a.kv0) * group + tile_head(it);
-      const int64_t unit = (bq * (2 * nqt) + 2 * tile_idx(it)) * nkt + kt;
-      rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, (uint32_t)(nkt + 1) * 8192);
-      ds_unit1 = (uint32_t)nkt * 8192;
+      if (WIN && a.ds_tab != nullptr) {
+        // Compact layout: the tile's entry gives its units; a block outside
+        // the entry's range (an inconsistent table) gets an empty buffer, so
+        // its stores are dropped.  Store offsets are then wholly per-lane
+        // (range-checked), see ds_store.
+        const int T = tile_idx(it);
+        const int* e = a.ds_tab + ((int64_t)b * a.ds_tsb + T) * 4;
+        const int kb_lo = __builtin_amdgcn_readfirstlane(e[0]);
+        const int nblk = __builtin_amdgcn_readfirstlane(e[1]);
+        const int gbase = __builtin_amdgcn_readfirstlane(e[2]);
+        const bool ok = kt >= kb_lo && kt - kb_lo < nblk && gbase >= 0 && (int64_t)gbase + 2 * nblk <= a.ds_units;
+        const int64_t unit = bq * a.ds_units + (ok ? gbase + (kt - kb_lo) : 0);
+        d.rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, ok ? (uint32_t)(nblk + 1) * 8192 : 0u);
+        d.unit1 = (uint32_t)nblk * 8192;
+      } else {
+        const int64_t unit = (bq * (2 * nqt) + 2 * tile_idx(it)) * nkt + kt;
+        d.rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, (uint32_t)(nkt + 1) * 8192);
+        d.unit1 = (uint32_t)nkt * 8192;
+      }
     }
+    return d;
+  };
+
+  // dS waves, dS phase of tile `it` (slot uc), one iteration after its dP
+  // phase, so the partner's P has been handed over by the barrier in
+  // between: dS = P * dp, dK^T += Q^T dS and, with STAGE, the dS stores
+  // (kDsStores per lane) to `dd`.
+  auto ds_phase = [&](int it, auto uc, const f32x16(&dp)[2], const DsDest& hoisted) {
+    constexpr uint32_t u = decltype(uc)::value;
+    // The compact layout's destination was computed at the top of the
+    // iteration (its table load needs time); the dense one here, where its
+    // few scalar operations schedule best.
+    const DsDest dd = (WIN && a.ds_tab != nullptr) ? hoisted : ds_dest(it);
+    const u32x4 rds = dd.rds;
+    const uint32_t ds_unit1 = dd.unit1;
 
     // dS for group g = 2*sub + k2 (4 steps of two elements) interleaved with
     // the dK^T MFMAs of group g-1; every LDS read is issued up front or kRA
@@ -563,7 +599,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     auto ds_store = [&](int g) {
       const int sub = g >> 1, k2 = g & 1;
       const u32x4 w = {ud[g][0] & ds_keep, ud[g][1] & ds_keep, ud[g][2] & ds_keep, ud[g][3] & ds_keep};
-      store_b128_nt(rds, ds_voff, (sub ? ds_unit1 : 0u) + (uint32_t)k2 * 4096, w);  // = DsUnit::store_offset
+      const uint32_t unit_off = (sub ? ds_unit1 : 0u) + (uint32_t)k2 * 4096;  // = DsUnit::store_offset
+      if (WIN && a.ds_tab != nullptr)
+        store_b128_nt(rds, ds_voff + unit_off, 0u, w);  // the whole offset range-checked
+      else
+        store_b128_nt(rds, ds_voff, unit_off, w);
     };
 #pragma unroll
     for (int e2 = 0; e2 < 4; ++e2) dstep(0, e2);
@@ -624,6 +664,8 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
         else
           wait_vmem_n<0>();
         barrier_lds();  // T: tile it staged, tile it - 1's P handed over
+        DsDest dd{{0u, 0u, 0u, 0u}, 0u};
+        if (WIN && a.ds_tab != nullptr && it > 0) dd = ds_dest(it - 1);
         if (it < niter) {
           __builtin_amdgcn_s_setprio(1);
           // Loads: Q of tile it + 1 (the last tile re-loads into a slot
@@ -632,7 +674,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
         }
         if (it > 0) {
           __builtin_amdgcn_s_setprio(2);
-          ds_phase(it - 1, std::integral_constant<int, up>(), dpb[up]);
+          ds_phase(it - 1, std::integral_constant<int, up>(), dpb[up], dd);
         }
         return it < niter;
       });
@@ -1143,8 +1185,29 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   }
 
   const u32x4 rkt = make_rsrc(a.kt + (int64_t)(b * a.Hkv + hk) * D * a.Lkp, (uint32_t)a.Lkp * D * 2);
-  const u32x4 rds =
-      make_rsrc(reinterpret_cast<const char*>(a.ds) + ((int64_t)bq_rel * nqg + qgl) * nkt * 8192, (uint32_t)nkt * 8192);
+  // This wave's dS units: dense, every 128-key block of its group in order;
+  // compact (WIN with a table), the blocks [kb_lo, kb_lo + nblk) of its
+  // tile.  A stage is loaded by every wave (the counted waits need the same
+  // loads everywhere); a stage outside this wave's blocks re-loads one of
+  // them, or the head's first unit when the tile has none, and is not
+  // multiplied (w0 .. w1 lies inside the tile's blocks).
+  u32x4 rds;
+  int ds_kb_lo = 0, ds_nblk = nkt;
+  if (WIN && a.ds_tab != nullptr) {
+    const int T = qgl >> 1;
+    const int* e = a.ds_tab + ((int64_t)b * a.ds_tsb + T) * 4;
+    const int kb_lo = __builtin_amdgcn_readfirstlane(e[0]);
+    const int nblk = __builtin_amdgcn_readfirstlane(e[1]);
+    const int gbase = __builtin_amdgcn_readfirstlane(e[2]);
+    const bool ok = nblk > 0 && gbase >= 0 && (int64_t)gbase + 2 * nblk <= a.ds_units;
+    const int64_t unit = (int64_t)bq_rel * a.ds_units + (ok ? gbase + (qgl & 1) * nblk : 0);
+    ds_kb_lo = ok ? kb_lo : 0;
+    ds_nblk = ok ? nblk : 1;
+    rds = make_rsrc(reinterpret_cast<const char*>(a.ds) + unit * 8192, (uint32_t)ds_nblk * 8192);
+  } else {
+    rds = make_rsrc(reinterpret_cast<const char*>(a.ds) + ((int64_t)bq_rel * nqg + qgl) * nkt * 8192,
+                    (uint32_t)nkt * 8192);
+  }
   using KtStager = TileStager<D, BK, NW>;
   KtStager ktst;
   ktst.init(a.Lkp, wave, lane);
@@ -1156,7 +1219,10 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   auto stage_load = [&](int s, Stage& sg) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < KtStager::kPer; ++i) ktst.stage_one(sg.kt, rkt, (uint32_t)s * BK * 2, i);
-    const uint32_t soff = DsUnit::stage_src<BK>(s, 0, 0);
+    // Unit of stage s among this wave's units (clamped into them), then the
+    // stage's keys within it.
+    const int ku = min(max(s * BK / 128 - ds_kb_lo, 0), ds_nblk - 1);
+    const uint32_t soff = (uint32_t)ku * 8192 + DsUnit::stage_src<BK>(s % (128 / BK), 0, 0);
 #pragma unroll
     for (int i = 0; i < kDsOps; ++i)
       dma16_nt(rds, lds_addr(&sg.ds[wave][512 * i]), DsUnit::stage_src<BK>(0, i, lane), soff);

@@ -201,7 +201,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 9; }
+int avattn_abi_version(void) { return 10; }
 
 }  // extern "C"
 
@@ -367,6 +367,24 @@ size_t avattn_bwd_staged_workspace_size(int32_t batch, int32_t heads_q, int32_t 
   return staged_ds_offset(wl) + (size_t)n * ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k);
 }
 
+// Compact staged-dS layout of a windowed backward (BwdArgs::ds_tab).
+struct CompactDs {
+  const int32_t* table = nullptr;
+  int64_t table_batch_stride = 0;  // in tiles
+  int64_t units_per_head = 0;
+};
+
+size_t avattn_bwd_compact_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
+                                         int32_t len_k, int32_t head_dim, int32_t pairs_per_pass,
+                                         int64_t ds_units_per_head) {
+  if (check_bwd_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim) != AVATTN_OK) return 0;
+  if ((int64_t)batch * heads_q == 0 || len_q == 0 || len_k == 0 || pairs_per_pass <= 0 || ds_units_per_head < 1)
+    return 0;
+  const BwdWorkspace wl = bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  const int64_t n = pairs_per_pass < (int64_t)batch * heads_kv ? pairs_per_pass : (int64_t)batch * heads_kv;
+  return staged_ds_offset(wl) + (size_t)n * ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k, ds_units_per_head);
+}
+
 static int bwd_impl(const void* dout, const void* q, const void* k, const void* v, const void* out, const float* lse,
                     const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
                     const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
@@ -374,7 +392,8 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
                     int64_t key_mask_batch_stride, float scale, void* dq, const int64_t* dq_strides, void* dk,
                     const int64_t* dk_strides, void* dv, const int64_t* dv_strides, void* workspace,
                     size_t workspace_bytes, uint32_t flags, avattn_stream_t stream, const int32_t* window_lo,
-                    const int32_t* window_hi, int64_t window_batch_stride, const RingOpts* ring = nullptr) {
+                    const int32_t* window_hi, int64_t window_batch_stride, const RingOpts* ring = nullptr,
+                    const CompactDs* compact = nullptr) {
   int st = check_bwd_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (flags & ~(AVATTN_BWD_REUSE_QUERY_SIDE | AVATTN_BWD_DQ_ACCUMULATE_F32 | AVATTN_BWD_STAGE_DS |
                 AVATTN_BWD_DEFER_DQ))
@@ -420,6 +439,17 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
   if (st != AVATTN_OK) return st;
   // Windows run on the staged-dS path only, and dq is not deferred.
   if (window_lo && (!(flags & AVATTN_BWD_STAGE_DS) || (flags & AVATTN_BWD_DEFER_DQ))) return AVATTN_ERR_ARGUMENT;
+  const int64_t ntiles = transpose_padded_len(len_q) / 64;
+  if (compact) {
+    // A table for every batch row (or one shared), 16-byte aligned; the
+    // units of one query head addressable through a 32-bit buffer range.
+    if (!window_lo || !compact->table) return AVATTN_ERR_ARGUMENT;
+    if (reinterpret_cast<uintptr_t>(compact->table) & 15u) return AVATTN_ERR_LAYOUT;
+    if (compact->table_batch_stride != 0 && compact->table_batch_stride < ntiles) return AVATTN_ERR_ARGUMENT;
+    if (compact->units_per_head < 1 || compact->units_per_head * 8192 >= ((int64_t)1 << 32))
+      return AVATTN_ERR_ARGUMENT;
+  }
+  const int64_t ds_units = compact ? compact->units_per_head : 0;
   const BwdWorkspace wl = bwd_workspace(batch, heads_q, heads_kv, len_q, len_k, head_dim);
   if (!workspace || workspace_bytes < wl.total || !aligned16(workspace)) return AVATTN_ERR_WORKSPACE;
 
@@ -468,6 +498,11 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
   a.wlo = window_lo;
   a.whi = window_hi;
   a.wsb = window_batch_stride;
+  if (compact) {
+    a.ds_tab = compact->table;
+    a.ds_tsb = compact->table_batch_stride;
+    a.ds_units = compact->units_per_head;
+  }
   if (ring) {
     a.cos_q = ring->cos_q;
     a.sin_q = ring->sin_q;
@@ -479,7 +514,7 @@ static int bwd_impl(const void* dout, const void* q, const void* k, const void* 
   int kv_per_pass = 0;
   if (flags & AVATTN_BWD_STAGE_DS) {
     const size_t off = staged_ds_offset(wl);
-    const size_t per = ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k);
+    const size_t per = ds_bytes_per_kv(heads_q / heads_kv, len_q, len_k, ds_units);
     // A deferred dq needs every pair's dS at once.
     const size_t need = off + (defer ? (size_t)a.nkv * per : per);
     if (workspace_bytes < need) return AVATTN_ERR_WORKSPACE;
@@ -519,6 +554,27 @@ int avattn_bwd_windowed(const void* dout, const void* q, const void* k, const vo
                   heads_kv, len_q, len_k, head_dim, key_mask, key_mask_batch_stride, scale, dq, dq_strides, dk,
                   dk_strides, dv, dv_strides, workspace, workspace_bytes, flags, stream, window_lo, window_hi,
                   window_batch_stride);
+}
+
+int avattn_bwd_windowed_compact(const void* dout, const void* q, const void* k, const void* v, const void* out,
+                                const float* lse, const int64_t* dout_strides, const int64_t* q_strides,
+                                const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                                int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
+                                int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                                const int32_t* window_lo, const int32_t* window_hi, int64_t window_batch_stride,
+                                const int32_t* ds_table, int64_t ds_table_batch_stride, int64_t ds_units_per_head,
+                                float scale, void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides,
+                                void* dv, const int64_t* dv_strides, void* workspace, size_t workspace_bytes,
+                                uint32_t flags, avattn_stream_t stream) {
+  if (!window_lo || !window_hi || !ds_table) return AVATTN_ERR_NULL_POINTER;
+  CompactDs c;
+  c.table = ds_table;
+  c.table_batch_stride = ds_table_batch_stride;
+  c.units_per_head = ds_units_per_head;
+  return bwd_impl(dout, q, k, v, out, lse, dout_strides, q_strides, k_strides, v_strides, out_strides, batch, heads_q,
+                  heads_kv, len_q, len_k, head_dim, key_mask, key_mask_batch_stride, scale, dq, dq_strides, dk,
+                  dk_strides, dv, dv_strides, workspace, workspace_bytes, flags, stream, window_lo, window_hi,
+                  window_batch_stride, nullptr, &c);
 }
 
 int avattn_bwd_dq_staged(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,

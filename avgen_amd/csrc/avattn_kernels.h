@@ -134,6 +134,17 @@ struct BwdArgs {
   const int* wlo;
   const int* whi;
   int64_t wsb;
+  // Compact dS layout for key windows (null: the dense unit layout above).
+  // Per 64-row query tile T of batch b, four ints at ds_tab + (b*ds_tsb +
+  // T)*4: the first 128-key block the tile's rows admit (kb_lo), the number
+  // of blocks (nblk; the dK/dV kernel visits tile T from block kt iff kb_lo
+  // <= kt < kb_lo + nblk), the unit index of the tile's first 32-row group
+  // within its query head's units (gbase), unused.  Group 2T + h, block kt is
+  // unit bq*ds_units + gbase + h*nblk + (kt - kb_lo); each query head of a
+  // pass owns ds_units units (at least twice the sum of nblk over its tiles).
+  const int* ds_tab;
+  int64_t ds_tsb;
+  int64_t ds_units;
   // RoPE fused into the backward (null: q and k are used as given): q and k
   // are the unrotated inputs; the query-side copies and the recomputing dQ
   // kernel rotate q with cos_q/sin_q (b*rqsb + i*(D/2) + pair), the k copies
@@ -191,8 +202,10 @@ inline TailSplit plan_tail_split(int64_t total, int cus, int max_slots) {
   return t;
 }
 
-// Bytes of staged dS per (b, kv head) pair.
-inline size_t ds_bytes_per_kv(int group, int Lq, int Lk) {
+// Bytes of staged dS per (b, kv head) pair: dense, or the compact layout's
+// units_per_head units per query head.
+inline size_t ds_bytes_per_kv(int group, int Lq, int Lk, int64_t units_per_head = 0) {
+  if (units_per_head > 0) return (size_t)group * (size_t)units_per_head * 8192;
   const size_t Lqp = (size_t)(Lq + 63) / 64 * 64;
   return (size_t)group * (Lqp / 32) * (size_t)((Lk + 127) / 128) * 8192;
 }

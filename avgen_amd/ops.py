@@ -234,11 +234,14 @@ def _fwd_windowed_impl(q, k, v, window_lo, window_hi, key_mask, scale):
     return out, lse
 
 
-def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale, check_monotone=True):
+def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, scale, check_monotone=True,
+                       compact=True):
     """Backward of _fwd_windowed_impl (windows non-decreasing in the row,
     verified with one host synchronisation unless ``check_monotone`` is
     False; always with staged dS, in passes if one pass does not fit the
-    budget)."""
+    budget).  ``compact``: stage only the key blocks each query tile's
+    windows admit (:func:`compact_ds_table`, one more host synchronisation
+    for its size); False: the dense layout, the same results."""
     name = "avgen_amd.flash_bwd_windowed"
     _check_qkv(name, q, k, v)
     _require_gpu(name, dout, q, k, v, out, lse, key_mask, window_lo, window_hi)
@@ -254,19 +257,35 @@ def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, 
     dk = _out_or_new(None, k, name, "dk")
     dv = _out_or_new(None, v, name, "dv")
     lib = _lib.load()
-    ws = _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds=True)
-    st = lib.avattn_bwd_windowed(
+    common_head = (
         _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
         _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
         B, Hq, Hkv, Lq, Lk, D,
         _ptr(mask), msb,
         _ptr(lo), _ptr(hi), wsb,
-        float(scale),
-        _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
-        _ptr(ws), ws.numel(),
-        _lib.BWD_STAGE_DS,
-        _stream(q.device),
     )
+    if compact:
+        table, units = compact_ds_table(lo, hi, Lq, Lk)
+        tsb = 0 if table.shape[0] == 1 else table.shape[1]
+        ws = _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds=True, ds_units=units)
+        st = lib.avattn_bwd_windowed_compact(
+            *common_head, _ptr(table), tsb, units,
+            float(scale),
+            _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
+            _ptr(ws), ws.numel(),
+            _lib.BWD_STAGE_DS,
+            _stream(q.device),
+        )
+    else:
+        ws = _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, q.device, stage_ds=True)
+        st = lib.avattn_bwd_windowed(
+            *common_head,
+            float(scale),
+            _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
+            _ptr(ws), ws.numel(),
+            _lib.BWD_STAGE_DS,
+            _stream(q.device),
+        )
     _lib.check(st, name)
     return dq, dk, dv
 
@@ -352,20 +371,53 @@ def _ds_budget(device: torch.device) -> int:
     return _ds_budgets[idx]
 
 
-def ds_bytes_per_pair(group, Lq, Lk):
+def ds_bytes_per_pair(group, Lq, Lk, ds_units=0):
     """Bytes of staged dS per (batch, kv head) pair: bf16 per (query head of
-    the group, query row padded to 64, key padded to 128)."""
+    the group, query row padded to 64, key padded to 128); with ``ds_units``
+    (the compact layout of key windows, :func:`compact_ds_table`) 8 KB per
+    unit of each query head."""
+    if ds_units:
+        return group * ds_units * 8192
     return group * ((Lq + 63) // 64 * 64) * ((Lk + 127) // 128 * 128) * 2
 
 
-def _staged_pairs(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None) -> int:
+def compact_ds_table(window_lo: torch.Tensor, window_hi: torch.Tensor, len_q: int, len_k: int):
+    """The compact staged-dS layout of a windowed backward
+    (``avattn_bwd_windowed_compact``): per 64-row query tile, the 128-key
+    blocks its rows' windows admit, as the dK/dV kernel visits them.
+
+    ``window_lo``/``window_hi``: int32 ``(rows, len_q)`` or ``(len_q,)``, one
+    window array per batch row (or one shared), non-decreasing along the
+    queries.  Returns ``(table, units)``: int32 ``(rows, tiles, 4)`` on the
+    windows' device holding ``[kb_lo, nblk, gbase, 0]`` per tile, and the
+    units one query head needs (the largest over the batch rows; at least 1)
+    -- read back to the host, one synchronisation."""
+    lo = window_lo.reshape(-1, len_q).to(torch.int64)
+    hi = window_hi.reshape(-1, len_q).to(torch.int64)
+    tiles = (len_q + 63) // 64
+    first = torch.arange(tiles, device=lo.device) * 64
+    last = torch.clamp(first + 63, max=len_q - 1)
+    lo0 = lo[:, first].clamp(0, len_k)
+    lo1 = lo[:, last].clamp(0, len_k)
+    hi1 = torch.maximum(hi[:, last], lo1).clamp(max=len_k)
+    kb_lo = lo0 // 128
+    kb_hi = (hi1 + 127) // 128
+    nblk = torch.where(lo0 < len_k, (kb_hi - kb_lo).clamp(min=0), torch.zeros_like(kb_lo))
+    two = 2 * nblk
+    gbase = torch.cumsum(two, 1) - two
+    table = torch.stack([kb_lo, nblk, gbase, torch.zeros_like(kb_lo)], -1).to(torch.int32).contiguous()
+    units = int(two.sum(1).max().item()) if tiles else 0
+    return table, max(units, 1)
+
+
+def _staged_pairs(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None, ds_units=0) -> int:
     """(batch, kv head) pairs per pass that a backward call stages dS for (0:
     no staging): as many as the budget holds (``stage_ds`` None), at least one
     (True), none (False); equal passes, as the library splits them."""
     lib = _lib.load()
     if stage_ds is False or lib.avattn_bwd_workspace_size(B, Hq, Hkv, Lq, Lk, D) == 0:
         return 0
-    per = ds_bytes_per_pair(Hq // Hkv, Lq, Lk)
+    per = ds_bytes_per_pair(Hq // Hkv, Lq, Lk, ds_units)
     pairs = min(B * Hkv, _ds_budget(device) // max(per, 1))
     if pairs == 0:
         if not stage_ds:
@@ -387,17 +439,24 @@ def bwd_workspace_plan(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None):
     return lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(pairs)), True
 
 
-def _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None) -> torch.Tensor:
+def _alloc_bwd_workspace(B, Hq, Hkv, Lq, Lk, D, device, stage_ds=None, ds_units=0) -> torch.Tensor:
     """The workspace of :func:`bwd_workspace_plan`, allocated; if the caching
     allocator cannot provide it (memory held by activations, say), the
     staged pairs per pass halve until it can (more passes, the same
     results), and with staging optional (``stage_ds`` not True) a last
-    attempt goes without staging (the recomputing dQ kernel)."""
+    attempt goes without staging (the recomputing dQ kernel).  ``ds_units``:
+    the compact layout of key windows (units per query head)."""
     lib = _lib.load()
-    pairs = _staged_pairs(B, Hq, Hkv, Lq, Lk, D, device, stage_ds)
+    pairs = _staged_pairs(B, Hq, Hkv, Lq, Lk, D, device, stage_ds, ds_units)
+
+    def staged_size(p):
+        if ds_units:
+            return lib.avattn_bwd_compact_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(p), int(ds_units))
+        return lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(p))
+
     while pairs > 0:
         try:
-            return _workspace(lib.avattn_bwd_staged_workspace_size(B, Hq, Hkv, Lq, Lk, D, int(pairs)), device)
+            return _workspace(staged_size(pairs), device)
         except torch.OutOfMemoryError:
             if pairs == 1:
                 if stage_ds:

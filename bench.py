@@ -546,6 +546,14 @@ def bench_windowed(cfg: dict, name: str, steps: int, warmup: int) -> dict:
         lo, hi = avgen_amd.attention.temporal_neighbour_windows(t, t, window_seconds=cfg["window_seconds"])
     pairs = float((hi.long() - lo.long()).sum().item()) * (B if lo.ndim == 1 else 1)
     scale = D ** -0.5
+    # The staged dS of the backward, stored compactly (only admitted key blocks).
+    _, units = avgen_amd.ops.compact_ds_table(lo, hi, L, L)
+    per_pair = avgen_amd.ops.ds_bytes_per_pair(1, L, L, units)
+    budget = avgen_amd.ops._ds_budget(dev)
+    fit = max(1, min(B * H, budget // per_pair))
+    ds_plan_w = {"budget_bytes": budget, "bytes_per_pair": per_pair,
+                 "dense_bytes_per_pair": avgen_amd.ops.ds_bytes_per_pair(1, L, L),
+                 "passes": -(-(B * H) // fit), "layout": "compact"}
 
     def one():
         qq, kk, vv = (t.requires_grad_(True) for t in (q, k, v))
@@ -600,6 +608,7 @@ def bench_windowed(cfg: dict, name: str, steps: int, warmup: int) -> dict:
         "roofline": {"kernel": dominant, "bound": "mfma", "achieved": round(rates[dominant], 1),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(rates[dominant] / PEAK_BF16_TFLOPS, 4),
                      "traffic": load_traffic(dominant, name)},
+        "ds_staging": ds_plan_w,
         "cpu_baseline": None,
     }
 

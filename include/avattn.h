@@ -330,6 +330,56 @@ int avattn_bwd_windowed(const void* dout, const void* q, const void* k, const vo
                         avattn_stream_t stream);
 
 /*
+ * avattn_bwd_windowed with the staged dS stored compactly: only the 128-key
+ * blocks each 64-row query tile's windows admit, so the workspace (and the
+ * number of passes) scales with the admitted (query, key) pairs instead of
+ * len_q * len_k.  ds_table (int32 device memory, 16-byte aligned) holds four
+ * ints per 64-row tile T = 0 .. ceil(len_q/64)-1 of batch row b at
+ * (b * ds_table_batch_stride + T) * 4 (stride 0: one table for every batch
+ * row; else at least ceil(len_q/64)):
+ *   [0] kb_lo  first 128-key block a row of the tile admits, floor(lo0/128)
+ *              with lo0 = clamp(window_lo[first row], 0, len_k);
+ *   [1] nblk   blocks kb_lo .. kb_lo+nblk-1: the blocks kt with
+ *              lo0 < min(128*(kt+1), len_k) and hi1 > 128*kt, where hi1 =
+ *              clamp(window_hi[last valid row], lo1, len_k) and lo1 the
+ *              clamped window_lo of that row (0 when lo0 == len_k);
+ *   [2] gbase  sum of 2*nblk over the tiles before T (the tile's first unit);
+ *   [3] unused.
+ * ds_units_per_head: at least 2 * (sum of nblk over a batch row's tiles) for
+ * every batch row, below 2^19.  Size the workspace with
+ * avattn_bwd_compact_workspace_size().  The results are those of
+ * avattn_bwd_windowed, bit for bit.  The table follows from the windows
+ * alone; a table that disagrees with them makes results wrong but writes no
+ * memory outside the workspace.  No counterpart in the reference (its dense
+ * masks have no staged dS).
+ */
+int avattn_bwd_windowed_compact(const void* dout, const void* q, const void* k, const void* v,
+                                const void* out, const float* lse,
+                                const int64_t* dout_strides, const int64_t* q_strides,
+                                const int64_t* k_strides, const int64_t* v_strides,
+                                const int64_t* out_strides,
+                                int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                int32_t len_q, int32_t len_k, int32_t head_dim,
+                                const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                                const int32_t* window_lo, const int32_t* window_hi,
+                                int64_t window_batch_stride,
+                                const int32_t* ds_table, int64_t ds_table_batch_stride,
+                                int64_t ds_units_per_head,
+                                float scale,
+                                void* dq, const int64_t* dq_strides,
+                                void* dk, const int64_t* dk_strides,
+                                void* dv, const int64_t* dv_strides,
+                                void* workspace, size_t workspace_bytes,
+                                uint32_t flags,
+                                avattn_stream_t stream);
+
+/* Workspace of avattn_bwd_windowed_compact staging the dS of
+ * pairs_per_pass (batch, kv head) pairs at once (0 for an empty problem). */
+size_t avattn_bwd_compact_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                         int32_t len_q, int32_t len_k, int32_t head_dim,
+                                         int32_t pairs_per_pass, int64_t ds_units_per_head);
+
+/*
  * Online-softmax merge of one chunk's (out_blk, lse_blk) into the running
  * (out_acc, lse_acc), in place, in fp32:
  *   out_acc <- out_acc - sigmoid(lse_blk - lse_acc) * (out_acc - out_blk)

@@ -147,18 +147,27 @@ def test_ring_nan_in_one_key_row_of_chunk_2(amd):
     assert (out0 == 0).all() and torch.isneginf(lse0).all()
 
 
+# The forward kernel's own error on bf16 inputs (test_c1_cpu_smoke_config).
+KERNEL_OUT_TOL = 5e-3
+KERNEL_LSE_TOL = 5e-5
+
+
 def test_c1_cpu_smoke_config(amd):
     """BASELINE config c1: one non-chunked self-attention, B=1, 4 heads,
     head_dim 64, a 4x16x16 latent (1,024 tokens), N(0,1) inputs, 3D RoPE
     theta 1e4 with the head_dim-64 split rope_axis_pairs(64) = (12, 10, 10)
     (the config's 22/21/21 is the head_dim-128 split), no mask, forward out +
-    LSE.  The config's tensors are float32; the HIP kernels compute in bf16, so
-    q/k/v are cast to bf16 first.  (1) Against the float64 oracle of the
-    bf16-cast inputs: the bf16 bar (out <= 2e-2, LSE <= 1e-3).  (2) Against
-    the float32 config itself (float64 rotation of the float32 inputs): the
-    cast alone moves the LSE by ~2.5e-3 at these N(0,1) inputs (the oracle
-    on the cast inputs shows it), so the kernel's error there must stay
-    within the cast's own error plus the bf16 bar."""
+    LSE.  The config's tensors are float32; the HIP kernels take bf16 only
+    (a float32 tensor raises TypeError), so q/k/v are cast to bf16 first and
+    the kernel's own error is bounded separately from the cast's.  (1)
+    Against the float64 oracle of the bf16-cast inputs, the kernel's
+    arithmetic alone: bf16 probabilities into the P V product and one bf16
+    rounding of the output (half an ulp: 3.9e-3 for |out| in [1, 2)), an fp32
+    LSE: out <= KERNEL_OUT_TOL, LSE <= KERNEL_LSE_TOL, four and twenty times
+    tighter than the bf16 bar, so a kernel error well below that bar trips
+    it.  (2) Against the float32 config itself (float64 rotation of the
+    float32 inputs): the cast alone moves the LSE by ~2.5e-3 at these N(0,1)
+    inputs, and the kernel may add no more than its own bound (1) on top."""
     B, H, D, grid = 1, 4, 64, (4, 16, 16)
     L = grid[0] * grid[1] * grid[2]
     assert R.rope_axis_pairs(D) == (12, 10, 10)
@@ -176,7 +185,9 @@ def test_c1_cpu_smoke_config(amd):
     qr = R.apply_rotary_bf16(q.float().cpu().numpy(), cos, sin)
     kr = R.apply_rotary_bf16(k.float().cpu().numpy(), cos, sin)
     ro, rl = R.attention_f64(qr, kr, v.float().cpu().numpy())
-    assert np.abs(o - ro).max() <= OUT_TOL and np.abs(l - rl).max() <= LSE_TOL
+    k_o, k_l = np.abs(o - ro).max(), np.abs(l - rl).max()
+    print(f"c1 kernel vs oracle on the bf16-cast inputs: out {k_o:.2e} lse {k_l:.2e}", flush=True)
+    assert k_o <= KERNEL_OUT_TOL and k_l <= KERNEL_LSE_TOL
     # (2) the float32 config itself: float64 rotation of the float32 inputs
     c64, s64 = R.rotary_tables_f64(coords.numpy(), D)
 
@@ -193,4 +204,4 @@ def test_c1_cpu_smoke_config(amd):
     cast_o, cast_l = np.abs(ro - fo).max(), np.abs(rl - fl).max()  # what the bf16 cast alone does
     print(f"c1 vs float32 config: kernel out {err_o:.2e} lse {err_l:.2e}; bf16 cast alone out {cast_o:.2e} "
           f"lse {cast_l:.2e}", flush=True)
-    assert err_o <= cast_o + OUT_TOL and err_l <= cast_l + LSE_TOL
+    assert err_o <= cast_o + KERNEL_OUT_TOL and err_l <= cast_l + KERNEL_LSE_TOL

@@ -253,3 +253,50 @@ def test_varlen_batch_of_packed_sequences(amd):
     out.backward(do.cuda())
     rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, attn_mask=dense)
     _check_grads((q.grad, k.grad, v.grad), (rq, rk, rv))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,width,per_batch,masked,budget_pairs", [
+    (2, 4, 2, 700, 900, 128, 300, True, True, 0),    # per-batch windows, GQA, masked
+    (1, 3, 3, 1000, 1000, 64, 200, False, False, 1),  # shared windows, three passes of one pair
+    (2, 2, 2, 333, 300, 128, 120, True, False, 0),   # neither length a multiple of 64 / 128
+])
+def test_compact_staged_ds_gives_the_dense_layouts_bits(amd, B, Hq, Hkv, Lq, Lk, D, width, per_batch, masked,
+                                                        budget_pairs):
+    """The windowed backward staging dS compactly (only the key blocks each
+    query tile's windows admit) gives the bits of the dense layout: the same
+    kernels and arithmetic, only dS lives elsewhere.  Also in passes (a
+    budget of one pair) and with a key mask."""
+    print(f"compact dS: B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} per_batch={per_batch} masked={masked}",
+          flush=True)
+    lo2, hi2 = _monotone_windows(B if per_batch else 1, Lq, Lk, seed=Lq + Lk, max_width=width, empty_tail=5)
+    lo, hi = (lo2, hi2) if per_batch else (lo2[0], hi2[0])
+    q = _randn((B, Hq, Lq, D), 1).cuda()
+    k, v = _randn((B, Hkv, Lk, D), 2).cuda(), _randn((B, Hkv, Lk, D), 3).cuda()
+    do = _randn((B, Hq, Lq, D), 4).cuda()
+    lo_t, hi_t = torch.from_numpy(lo).cuda(), torch.from_numpy(hi).cuda()
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(5)
+        mask = (torch.rand((B, Lk), generator=g) > 0.1).cuda()
+    scale = D ** -0.5
+    out, lse = amd.ops.flash_fwd_windowed(q, k, v, lo_t, hi_t, mask, scale)
+    table, units = amd.ops.compact_ds_table(lo_t, hi_t, Lq, Lk)
+    dense_units = (Lq + 63) // 64 * 2 * ((Lk + 127) // 128)
+    print(f"  units per head: compact {units}, dense {dense_units}", flush=True)
+    assert units <= dense_units
+    if budget_pairs:
+        amd.ops.set_ds_budget(budget_pairs * amd.ops.ds_bytes_per_pair(Hq // Hkv, Lq, Lk, units), q.device)
+    try:
+        got = amd.ops._bwd_windowed_impl(do, q, k, v, out, lse, lo_t, hi_t, mask, scale, compact=True)
+        ref = amd.ops._bwd_windowed_impl(do, q, k, v, out, lse, lo_t, hi_t, mask, scale, compact=False)
+        torch.cuda.synchronize()
+    finally:
+        amd.ops.set_ds_budget(None, q.device)
+    for name, a_, b_ in zip(("dq", "dk", "dv"), got, ref):
+        assert torch.equal(a_, b_), name
+    # and both against the oracle with the equivalent dense mask
+    km = None if mask is None else mask.cpu().numpy()
+    rq, rk, rv = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), _f64(out),
+                                     lse.cpu().numpy().astype(np.float64), km,
+                                     attn_mask=_window_mask(lo2, hi2, Lk))
+    _check_grads(got, (rq, rk, rv))
