@@ -99,9 +99,10 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(BwdArgs a) {
 // the workgroup visits only the 64-row tiles whose rows' window union meets
 // its keys, and the P waves set the scores outside a row's window to -inf
 // in tiles not inside every window (so P and dS are 0 there).
-template <int D, bool MASK, bool STAGE, bool WIN>
+template <int D, bool MASK, bool STAGE, bool WIN, bool CT>
 __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   static_assert(!WIN || STAGE, "windows with staged dS only");
+  static_assert(!CT || WIN, "the compact dS layout (BwdArgs::ds_tab) is for windows");
   constexpr int BK = 128, BQ = 64, NW = 8;
   constexpr int KS = D / 16, DT = D / 32;
   constexpr int TE = BQ * D;
@@ -519,36 +520,40 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     for (int i = loads_in_loop(NS); i < kQOps; ++i) q_op(itq, lq, i);
   };
 
-  // dS waves, dS phase of tile `it` (slot uc), one iteration after its dP
-  // phase, so the partner's P has been handed over by the barrier in
-  // between: dS = P * dp, dK^T += Q^T dS and, with STAGE, the dS stores
-  // (kDsStores per lane).
   // Where tile `it`'s dS goes (STAGE): a buffer over its two units (query
   // groups 2*tile_idx(it) and +1) and the byte distance between them.
-  // Computed at the top of the iteration whose dS phase stores them, so the
-  // compact layout's table load is in flight during the dP phase.
   struct DsDest {
     u32x4 rds;
     uint32_t unit1;
   };
-  auto ds_dest = [&](int it) {
+  // Compact layout (WIN with a table): the tile's table entry, read by a
+  // scalar load.  Scalar loads return out of order with LDS reads, so while
+  // one is outstanding every counted LDS wait would have to become a full
+  // one: the entry of the tile whose dS phase comes next is loaded at the
+  // end of an iteration (after its last LDS read) and used right after the
+  // next barrier, whose wait has drained it.
+  struct DsEntry {
+    int kb_lo, nblk, gbase;
+  };
+  auto ds_entry = [&](int it) {
+    const int64_t e = ((int64_t)b * a.ds_tsb + tile_idx(it)) * 4;
+    return DsEntry{__builtin_amdgcn_readfirstlane(load_const_i32(a.ds_tab, e)),
+                   __builtin_amdgcn_readfirstlane(load_const_i32(a.ds_tab, e + 1)),
+                   __builtin_amdgcn_readfirstlane(load_const_i32(a.ds_tab, e + 2))};
+  };
+  auto ds_dest = [&](int it, const DsEntry& en) {
     DsDest d{{0u, 0u, 0u, 0u}, 0u};
     if constexpr (STAGE) {
       const int64_t bq = (int64_t)(bhk - a.kv0) * group + tile_head(it);
-      if (WIN && a.ds_tab != nullptr) {
-        // Compact layout: the tile's entry gives its units; a block outside
-        // the entry's range (an inconsistent table) gets an empty buffer, so
-        // its stores are dropped.  Store offsets are then wholly per-lane
-        // (range-checked), see ds_store.
-        const int T = tile_idx(it);
-        const int* e = a.ds_tab + ((int64_t)b * a.ds_tsb + T) * 4;
-        const int kb_lo = __builtin_amdgcn_readfirstlane(e[0]);
-        const int nblk = __builtin_amdgcn_readfirstlane(e[1]);
-        const int gbase = __builtin_amdgcn_readfirstlane(e[2]);
-        const bool ok = kt >= kb_lo && kt - kb_lo < nblk && gbase >= 0 && (int64_t)gbase + 2 * nblk <= a.ds_units;
-        const int64_t unit = bq * a.ds_units + (ok ? gbase + (kt - kb_lo) : 0);
-        d.rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, ok ? (uint32_t)(nblk + 1) * 8192 : 0u);
-        d.unit1 = (uint32_t)nblk * 8192;
+      if (CT) {
+        // A block outside the entry's range (an inconsistent table) gets an
+        // empty buffer, so its stores are dropped; the store offsets are then
+        // wholly per-lane (range-checked), see ds_store.
+        const bool ok = kt >= en.kb_lo && kt - en.kb_lo < en.nblk && en.gbase >= 0 &&
+                        (int64_t)en.gbase + 2 * en.nblk <= a.ds_units;
+        const int64_t unit = bq * a.ds_units + (ok ? en.gbase + (kt - en.kb_lo) : 0);
+        d.rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, ok ? (uint32_t)(en.nblk + 1) * 8192 : 0u);
+        d.unit1 = (uint32_t)en.nblk * 8192;
       } else {
         const int64_t unit = (bq * (2 * nqt) + 2 * tile_idx(it)) * nkt + kt;
         d.rds = make_rsrc(reinterpret_cast<char*>(a.ds) + unit * 8192, (uint32_t)(nkt + 1) * 8192);
@@ -565,9 +570,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
   auto ds_phase = [&](int it, auto uc, const f32x16(&dp)[2], const DsDest& hoisted) {
     constexpr uint32_t u = decltype(uc)::value;
     // The compact layout's destination was computed at the top of the
-    // iteration (its table load needs time); the dense one here, where its
-    // few scalar operations schedule best.
-    const DsDest dd = (WIN && a.ds_tab != nullptr) ? hoisted : ds_dest(it);
+    // iteration (see DsEntry); the dense one here, where its few scalar
+    // operations schedule best.
+    const DsDest dd = (CT) ? hoisted : ds_dest(it, DsEntry{0, 0, 0});
     const u32x4 rds = dd.rds;
     const uint32_t ds_unit1 = dd.unit1;
 
@@ -600,7 +605,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       const int sub = g >> 1, k2 = g & 1;
       const u32x4 w = {ud[g][0] & ds_keep, ud[g][1] & ds_keep, ud[g][2] & ds_keep, ud[g][3] & ds_keep};
       const uint32_t unit_off = (sub ? ds_unit1 : 0u) + (uint32_t)k2 * 4096;  // = DsUnit::store_offset
-      if (WIN && a.ds_tab != nullptr)
+      if (CT)
         store_b128_nt(rds, ds_voff + unit_off, 0u, w);  // the whole offset range-checked
       else
         store_b128_nt(rds, ds_voff, unit_off, w);
@@ -651,6 +656,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     // dP of tile it (slot it % 3), kept for the tile's dS phase in the next
     // iteration.
     f32x16 dpb[3][2];
+    DsEntry ent{0, 0, 0};  // compact layout: tile it - 1's entry at the top of iteration it
     // Iterations 0 .. niter: iteration niter has only the last tile's dS
     // phase (its barrier pairs with the P waves' F).
     for (int it0 = 0;; it0 += 3) {
@@ -665,7 +671,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
           wait_vmem_n<0>();
         barrier_lds();  // T: tile it staged, tile it - 1's P handed over
         DsDest dd{{0u, 0u, 0u, 0u}, 0u};
-        if (WIN && a.ds_tab != nullptr && it > 0) dd = ds_dest(it - 1);
+        if (CT && it > 0) dd = ds_dest(it - 1, ent);
         if (it < niter) {
           __builtin_amdgcn_s_setprio(1);
           // Loads: Q of tile it + 1 (the last tile re-loads into a slot
@@ -676,6 +682,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
           __builtin_amdgcn_s_setprio(2);
           ds_phase(it - 1, std::integral_constant<int, up>(), dpb[up], dd);
         }
+        if (CT && it < niter) ent = ds_entry(it);
         return it < niter;
       });
       if (!more) break;
@@ -1127,8 +1134,9 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_kernel(BwdArgs a) {
 // windows are staged, and a wave multiplies only those that meet its own
 // 32 rows' windows (the dK/dV kernel wrote the dS of exactly those: a
 // group's window union lies inside its 64-row tile's).
-template <int D, int BK, int NSTG, bool WIN>
+template <int D, int BK, int NSTG, bool WIN, bool CT>
 __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
+  static_assert(!CT || WIN, "the compact dS layout (BwdArgs::ds_tab) is for windows");
   constexpr int NW = 8, DT = D / 32;
   static_assert(BK == 32 || BK == 64, "stage of 32 or 64 keys");
   struct Stage {
@@ -1193,12 +1201,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dq_ds_kernel(BwdArgs a) {
   // multiplied (w0 .. w1 lies inside the tile's blocks).
   u32x4 rds;
   int ds_kb_lo = 0, ds_nblk = nkt;
-  if (WIN && a.ds_tab != nullptr) {
-    const int T = qgl >> 1;
-    const int* e = a.ds_tab + ((int64_t)b * a.ds_tsb + T) * 4;
-    const int kb_lo = __builtin_amdgcn_readfirstlane(e[0]);
-    const int nblk = __builtin_amdgcn_readfirstlane(e[1]);
-    const int gbase = __builtin_amdgcn_readfirstlane(e[2]);
+  if (CT) {
+    const int64_t e = ((int64_t)b * a.ds_tsb + (qgl >> 1)) * 4;
+    const int kb_lo = __builtin_amdgcn_readfirstlane(load_const_i32(a.ds_tab, e));
+    const int nblk = __builtin_amdgcn_readfirstlane(load_const_i32(a.ds_tab, e + 1));
+    const int gbase = __builtin_amdgcn_readfirstlane(load_const_i32(a.ds_tab, e + 2));
     const bool ok = nblk > 0 && gbase >= 0 && (int64_t)gbase + 2 * nblk <= a.ds_units;
     const int64_t unit = (int64_t)bq_rel * a.ds_units + (ok ? gbase + (qgl & 1) * nblk : 0);
     ds_kb_lo = ok ? kb_lo : 0;
@@ -1326,10 +1333,12 @@ static void launch_dq_ds_d(const BwdArgs& a, hipStream_t stream) {
   // partial last round is not split as the dK/dV one is: this kernel is
   // bound by HBM, and the last round's workgroups share all of it (measured:
   // no gain at c3).
-  if (a.wlo)
-    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, true>), grid, dim3(512), 0, stream, a);
+  if (a.wlo && a.ds_tab)
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, true, true>), grid, dim3(512), 0, stream, a);
+  else if (a.wlo)
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, true, false>), grid, dim3(512), 0, stream, a);
   else
-    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, false>), grid, dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((bwd_dq_ds_kernel<D, 64, 3, false, false>), grid, dim3(512), 0, stream, a);
 }
 
 template <int D>
@@ -1385,21 +1394,26 @@ static hipError_t launch_bwd_d(const BwdArgs& a, int kv_per_pass, hipStream_t st
     {
       const dim3 grid(total - p.nsplit + p.nsplit * p.nparts);
       LaunchTimer timer(kKidBwdDkdv, stream);  // 1 workgroup (8 waves) per CU: LDS-bound occupancy
-      if (p.wlo) {  // windows (staged dS only)
+      if (p.wlo && p.ds_tab) {  // windows, compact dS layout
         if (mask)
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true, true>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true, true, true>), grid, dim3(512), 0, stream, p);
         else
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true, true>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true, true, true>), grid, dim3(512), 0, stream, p);
+      } else if (p.wlo) {  // windows (staged dS only)
+        if (mask)
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true, true, false>), grid, dim3(512), 0, stream, p);
+        else
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true, true, false>), grid, dim3(512), 0, stream, p);
       } else if (mask) {
         if (p.ds)
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true, false>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, true, false, false>), grid, dim3(512), 0, stream, p);
         else
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, false, false>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, true, false, false, false>), grid, dim3(512), 0, stream, p);
       } else {
         if (p.ds)
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true, false>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, true, false, false>), grid, dim3(512), 0, stream, p);
         else
-          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false, false>), grid, dim3(512), 0, stream, p);
+          hipLaunchKernelGGL((bwd_dkdv_kernel<D, false, false, false, false>), grid, dim3(512), 0, stream, p);
       }
     }
     if (p.nsplit > 0) {

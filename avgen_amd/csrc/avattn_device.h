@@ -237,6 +237,16 @@ __device__ __forceinline__ int xcd_remap(int bid, int total) {
   return xcd * per + (xcd < rem ? xcd : rem) + local;
 }
 
+// An int of device memory the kernel only reads, loaded through the constant
+// address space: with a wave-uniform address this is a scalar load.  (The
+// kernels' inline-asm stores clobber "memory", so the compiler cannot prove
+// such data unchanged and keeps a plain load a vector load, counted with the
+// hand-counted tile loads and waited for with them.)
+__device__ __forceinline__ int load_const_i32(const int* p, int64_t i) {
+  typedef __attribute__((address_space(4))) const int const_int;
+  return reinterpret_cast<const_int*>(reinterpret_cast<uintptr_t>(p))[i];
+}
+
 // ---------------------------------------------------------------------------
 // LDS tile layout
 // ---------------------------------------------------------------------------
