@@ -37,10 +37,15 @@ namespace avattn {
 // during iteration t (spread between MFMAs), tile t-1 stays resident for the
 // PV products.
 //
-// FP8: q k^T on e4m3 operands (v_mfma_f32_32x32x64_f8f6f4, twice the bf16
-// rate): q is quantized on load with its head's scale, K comes from the e4m3
-// copy (fp8.hip), and the per-head scales fold into the softmax constant and
-// the LSE.  P, V and O^T += V^T P^T stay bf16 / fp32 as above.
+// FP8: q k^T on e4m3 operands (v_mfma_scale_f32_32x32x64_f8f6f4, twice the
+// bf16 rate) producing the scores in log2 units with the lane's running
+// maximum already subtracted, so the softmax is one exp2 per score.  q is
+// quantized on load against the softmax constant and k's scale:
+// q8 = e4m3(q * g * 2^-eq), g = scale_log2 * k_scale[hk] and 2^eq the
+// smallest power of two >= g * q_scale[h] (fp32; so |q8| <= 448 wherever
+// |q| <= 448 * q_scale[h]); the MFMA's block scale restores 2^eq and its
+// accumulator starts from -m.  K comes from the e4m3 copy (fp8.hip).  P, V
+// and O^T += V^T P^T stay bf16 / fp32 as above.
 //
 // WIN: per-query-row key windows [wlo, whi) (FwdArgs::wlo/whi).  The
 // workgroup visits only the tiles that meet the union of its rows' windows,
@@ -170,13 +175,15 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   // channel order, the same order the K operand reads).
   using QFrag = std::conditional_t<FP8, i32x8, bf16x8>;
   QFrag qf[KS];
-  float c = a.scale_log2, sc = a.scale;  // softmax constants on raw q.k
+  float c = a.scale_log2, sc = a.scale;  // softmax constants on raw q.k (bf16 path)
+  int qe8 = 127;                         // fp8: E8M0 block scale of the q operand, 127 + eq
+  int eq = 0;
+  float qn2 = 0.f;  // this lane's share of the squared q row norm (fp8: of q8, e4m3 units)
   if constexpr (FP8) {
-    const float qs = a.q_scale[h];
-    const float qk = qs * a.k_scale[hk];
-    c *= qk;
-    sc *= qk;
-    const float qinv = 1.f / qs;
+    const float g = a.scale_log2 * a.k_scale[hk];
+    eq = ceil_log2_clamped(g * a.q_scale[h]);
+    const float qm = ldexpf(g, -eq);
+    qe8 = 127 + eq;
     const bf16* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)qrow * a.qsl + 32 * hh;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -185,11 +192,17 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const u32x4 w = *reinterpret_cast<const u32x4*>(qp + 64 * ks + 8 * q4);
-          x[2 * q4] = (int)pack_fp8x4(bf16_lo(w[0]) * qinv, bf16_hi(w[0]) * qinv, bf16_lo(w[1]) * qinv,
-                                      bf16_hi(w[1]) * qinv);
-          x[2 * q4 + 1] = (int)pack_fp8x4(bf16_lo(w[2]) * qinv, bf16_hi(w[2]) * qinv, bf16_lo(w[3]) * qinv,
-                                          bf16_hi(w[3]) * qinv);
+          x[2 * q4] = (int)pack_fp8x4(bf16_lo(w[0]) * qm, bf16_hi(w[0]) * qm, bf16_lo(w[1]) * qm,
+                                      bf16_hi(w[1]) * qm);
+          x[2 * q4 + 1] = (int)pack_fp8x4(bf16_lo(w[2]) * qm, bf16_hi(w[2]) * qm, bf16_lo(w[3]) * qm,
+                                          bf16_hi(w[3]) * qm);
         }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v0 = __builtin_amdgcn_cvt_f32_fp8(x[i], 0), v1 = __builtin_amdgcn_cvt_f32_fp8(x[i], 1);
+        const float v2 = __builtin_amdgcn_cvt_f32_fp8(x[i], 2), v3 = __builtin_amdgcn_cvt_f32_fp8(x[i], 3);
+        qn2 = fmaf(v0, v0, fmaf(v1, v1, fmaf(v2, v2, fmaf(v3, v3, qn2))));
       }
       qf[ks] = x;
     }
@@ -235,11 +248,24 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   // score can make a probability exceed 2^kBoundTau (far inside fp32/bf16
   // range, and O, l stay finite), so the wave stops tracking row maxima:
   // m_run is then final and the per-tile max and rescale test are skipped.
+  // The fp8 path bounds its log2-unit scores by 2^eq * |q8_row| * max_k |k8|
+  // (the products of e4m3 values are exact; same margin) against a maximum
+  // kept in log2 units.
   constexpr float kBoundTau = 32.f;
   float bound = kPosInf;
-  if constexpr (!FP8) {
+  if constexpr (FP8) {
     if (a.kmax2 != nullptr) {
-      float qn2 = 0.f;
+      qn2 = halves_sum(qn2);
+      const int ntk = a.Lkp / 64;
+      const uint32_t* km = a.kmax2 + bhk * ntk;
+      float km2 = 0.f;
+      for (int i = lane; i < ntk; i += 64) km2 = fmaxf(km2, __uint_as_float(km[i]));
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) km2 = fmaxf(km2, __shfl_xor(km2, off));
+      bound = ldexpf(sqrtf(qn2) * sqrtf(km2) * (1.f + 1.f / 1024.f), eq);
+    }
+  } else {
+    if (a.kmax2 != nullptr) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
@@ -259,7 +285,11 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
     }
   }
   int bounded = 0;  // wave-uniform
-  float m_run = kNegInf;             // reference max of raw scores for this lane's query
+  // Reference max for this lane's query: of the raw scores (bf16 path), of
+  // the log2-unit scores (fp8, where cneg holds -m_run in every register, 0
+  // while m_run is -inf: the accumulator the q k^T products start from).
+  float m_run = kNegInf;
+  f32x16 cneg = zero16();
   float l_run0 = 0.f, l_run1 = 0.f;  // this lane's share of the row sum
   f32x16 acc[DT];
 #pragma unroll
@@ -286,13 +316,15 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
     QFrag ka[R];
 #pragma unroll
     for (int j = 0; j < R; ++j) ka[j] = kop(j);
-    sh[0] = zero16();
-    sh[1] = zero16();
+    if constexpr (!FP8) {
+      sh[0] = zero16();
+      sh[1] = zero16();
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NS; ++j) {
       if constexpr (FP8)
-        sh[j / KS] = mfma32_fp8(ka[j % R], qf[j % KS], sh[j / KS]);
+        sh[j / KS] = mfma32_fp8_scaled(ka[j % R], qf[j % KS], j % KS == 0 ? cneg : sh[j / KS], 127, qe8);
       else
         sh[j / KS] = mfma32(ka[j % R], qf[j % KS], sh[j / KS]);
       if (j + R < NS) ka[j % R] = kop(j + R);
@@ -302,6 +334,72 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   };
   // Softmax of one tile's scores (both halves) into the bf16 PV operands.
   auto softmax = [&](const Stage& sg, f32x16* sh, bf16x8 (*pf)[2], int t) __attribute__((always_inline)) {
+    if constexpr (FP8) {
+      // sh: the tile's log2-unit scores minus m_run (plain scores while m_run
+      // is -inf), both halves formed against the same m_run, so one maximum
+      // per tile: a new reference moves m_run by the excess mx and shifts
+      // both halves by it (the next tiles' products start from the new
+      // -m_run).
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        if (!__builtin_amdgcn_readfirstlane(sg.flags[hf])) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 bb =
+                *reinterpret_cast<const f32x4*>(sg.bias + hf * 32 + 16 * (g >> 1) + 8 * hh + 4 * (g & 1));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sh[hf][4 * g + r] += bb[r];
+          }
+        }
+      }
+      if (!bounded) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sh[0][r], sh[1][r]));
+        mx = halves_max(mx);
+        const bool first = m_run == kNegInf;
+        if (first ? mx > kNegInf : mx > 8.f) {
+          if (first) {
+            m_run = mx;
+          } else {
+            const float alpha = __builtin_amdgcn_exp2f(-mx);
+            l_run0 *= alpha;
+            l_run1 *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+            m_run += mx;
+          }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            sh[0][r] -= mx;
+            sh[1][r] -= mx;
+          }
+          cneg = splat16(-m_run);
+        }
+        bounded = __all(bound - m_run <= kBoundTau);
+      }
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int k2 = 0; k2 < 2; ++k2) {
+          u32x4 u;
+#pragma unroll
+          for (int e2 = 0; e2 < 4; ++e2) {
+            const int r = 8 * k2 + 2 * e2;
+            const float p0 = __builtin_amdgcn_exp2f(sh[hf][r]);
+            const float p1 = __builtin_amdgcn_exp2f(sh[hf][r + 1]);
+            if (e2 & 1)
+              l_run1 += p0 + p1;
+            else
+              l_run0 += p0 + p1;
+            u[e2] = pack_bf16x2(p0, p1);
+          }
+          pf[hf][k2] = bits_to_bf16x8(u);
+        }
+      return;
+    }
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       f32x16& s_cur = sh[hf];
@@ -340,7 +438,7 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
             for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
           m_run = mx;
         }
-        if constexpr (!FP8) bounded = __all((bound - m_run) * c <= kBoundTau);
+        bounded = __all((bound - m_run) * c <= kBoundTau);
       }
       const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
 #pragma unroll
@@ -535,7 +633,8 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
   const float l_tot = halves_sum(l_run0 + l_run1);
   const float nan = __builtin_nanf("");
   const float inv = l_tot > 0.f ? 1.f / l_tot : (l_tot == 0.f ? 0.f : nan);
-  const float lse = l_tot > 0.f ? fmaf(m_run, sc, logf(l_tot)) : (l_tot == 0.f ? kNegInf : nan);
+  // m_run is in raw score units (bf16 path) or log2 units (fp8).
+  const float lse = l_tot > 0.f ? fmaf(m_run, FP8 ? kLn2 : sc, logf(l_tot)) : (l_tot == 0.f ? kNegInf : nan);
   if (qvalid) {
     bf16* op = a.o + b * a.osb + h * a.osh + (int64_t)qrow * a.osl;
     if (a.o_acc == nullptr) {
@@ -608,7 +707,8 @@ static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t stream) {
     LaunchTimer timer(kKidTranspose, stream);
     hipError_t e = launch_key_prep(a.mask, a.msb, a.B, a.Lk, a.kbias, a.kfull, stream);
     if (e == hipSuccess)
-      e = fp8 ? launch_quantize_rows(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.k_scale, a.k8, stream)
+      e = fp8 ? launch_quantize_rows(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.k_scale, a.k8, a.kmax2,
+                                     stream)
               : launch_prep_copies(a.k, a.ksb, a.ksh, a.ksl, a.B, a.Hkv, a.Lk, D, a.kr, nullptr, stream, a.kmax2,
                                    a.cos_k, a.sin_k, a.rksb);
     if (e == hipSuccess) e = launch_prep_copies(a.v, a.vsb, a.vsh, a.vsl, a.B, a.Hkv, a.Lk, D, nullptr, a.vt, stream);

@@ -269,7 +269,7 @@ int fwd_impl(const void* q, const void* k, const void* v, const int64_t* q_strid
   a.vt = reinterpret_cast<bf16*>(ws + wl.vt);
   a.kbias = reinterpret_cast<float*>(ws + wl.kbias);
   a.kfull = reinterpret_cast<int*>(ws + wl.kfull);
-  a.kmax2 = fp8 ? nullptr : reinterpret_cast<uint32_t*>(ws + wl.kmax2);
+  a.kmax2 = reinterpret_cast<uint32_t*>(ws + wl.kmax2);
   a.Lkp = transpose_padded_len(len_k);
   a.wlo = window_lo;
   a.whi = window_hi;

@@ -51,6 +51,26 @@ __device__ __forceinline__ f32x16 mfma32_fp8(const i32x8& a, const i32x8& b, con
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// The same product with block scales: c + 2^(sa-127) * 2^(sb-127) * (a . b),
+// sa and sb E8M0 exponents (byte 0 of the operand, 127 = 1.0) applied to the
+// products only, c added unscaled (checked on the GPU against the unscaled
+// product for exponents -27..13 with a nonzero c).
+__device__ __forceinline__ f32x16 mfma32_fp8_scaled(const i32x8& a, const i32x8& b, const f32x16& c, int sa,
+                                                    int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, sa, 0, sb);
+}
+
+// The smallest e with 2^e >= |t|, clamped to [-126, 127] (E8M0's range of
+// finite scales with a normal fp32 2^-e): a zero or subnormal t gives -126,
+// an infinite or NaN one 127.
+__device__ __forceinline__ int ceil_log2_clamped(float t) {
+  const uint32_t u = __float_as_uint(t) & 0x7fffffffu;
+  const int field = (int)(u >> 23);
+  if (field == 0) return -126;
+  const int e = field - 127 + ((u & 0x7fffffu) != 0u ? 1 : 0);
+  return e > 127 ? 127 : (e < -126 ? -126 : e);
+}
+
 // Four fp32 values -> four e4m3 bytes (byte i = value i), round to nearest
 // even, no saturation (|x| < 464 stays finite; the callers scale into
 // [-448, 448]); v_cvt_pk_fp8_f32 matches torch's float8_e4m3fn cast bit for

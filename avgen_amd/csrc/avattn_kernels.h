@@ -35,16 +35,17 @@ struct FwdArgs {
   float* kbias;  // (B, Lkp): 0 attended / -inf
   int* kfull;    // (B, Lkp/32): 1 if every key of the 32-key tile is attended
   int Lkp;
-  // fp8 variant only (null otherwise): per-head dequantization scales (q8 =
-  // e4m3(q / q_scale[h]), k8 likewise) and the e4m3 row-major k copy, element
-  // (b, h, j, d) at byte ((b*Hkv + h)*Lkp + j)*D + d.
+  // fp8 variant only (null otherwise): per-head scales and the e4m3
+  // row-major k copy k8 = e4m3(k / k_scale[hk]), element (b, h, j, d) at byte
+  // ((b*Hkv + h)*Lkp + j)*D + d.  q is quantized against the softmax
+  // constant and k's scale (attn_fwd.hip); q_scale[h] only bounds |q| / 448.
   const float* q_scale;
   const float* k_scale;
   uint8_t* k8;
-  // bf16 path: largest squared row norm of k per 64-key tile, (b, kv head,
-  // tile) at ((b*Hkv + h)*(Lkp/64) + tile), float bits (written by the k
-  // copy): the largest over a head bounds every score of a query row by
-  // |q_row| * sqrt(max).
+  // Largest squared row norm of k (bf16 path) or of k8 in e4m3 units (fp8)
+  // per 64-key tile, (b, kv head, tile) at ((b*Hkv + h)*(Lkp/64) + tile),
+  // float bits (written by the k copy): the largest over a head bounds every
+  // score of a query row by |q_row| * sqrt(max).
   uint32_t* kmax2;
   // Key windows (null: every key): query row i of batch b attends to keys
   // [wlo[b*wsb + i], whi[b*wsb + i]) (and the key mask), shared by all heads.
@@ -275,9 +276,11 @@ hipError_t launch_absmax_scales(const bf16* x, int64_t sb, int64_t sh, int64_t s
                                 float* scale, uint32_t* bits, hipStream_t stream);
 
 // x (B, H, L, D) strided -> e4m3 row-major copy (B*H, Lp, D) bytes of
-// x * (1 / scale[h]), zero padded to Lp = transpose_padded_len(L).
+// x * (1 / scale[h]), zero padded to Lp = transpose_padded_len(L); with
+// rowmax2 set, also the largest squared norm of the quantized rows of each
+// 64-row tile, rowmax2[(b*H + h)*(Lp/64) + tile] (float bits).
 hipError_t launch_quantize_rows(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
-                                const float* scale, uint8_t* out, hipStream_t stream);
+                                const float* scale, uint8_t* out, uint32_t* rowmax2, hipStream_t stream);
 
 // Forward; the fp8 q k^T variant when a.k8 is set (a.q_scale, a.k_scale too).
 hipError_t launch_fwd(const FwdArgs& a, int head_dim, hipStream_t stream);

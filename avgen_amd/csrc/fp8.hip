@@ -53,23 +53,32 @@ __global__ __launch_bounds__(256) void absmax_finish_kernel(const uint32_t* bits
 
 // Row-major e4m3 copy of x (B, H, L, D) strided, zero rows past L:
 // out[((b*H + h)*Lp + i)*D + d] = e4m3(x[b, h, i, d] * (1 / scale[h])).
-// One thread per 16 channels (32 bytes in, 16 bytes out).
+// One workgroup per 64 rows of one (b, h), one thread per 16 channels of a
+// row (32 bytes in, 16 bytes out).  With rowmax2 set it also writes the
+// largest squared norm of its tile's quantized rows (in e4m3 units, summed
+// in fp32) to rowmax2[(b*H + h)*(Lp/64) + tile] as float bits: the key-side
+// factor of the score bound the fp8 forward uses.
 template <int D>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const bf16* __restrict__ x, int64_t sb, int64_t sh,
-                                                            int64_t sl, int B, int H, int L, int Lp,
+                                                            int64_t sl, int H, int L, int Lp,
                                                             const float* __restrict__ scale,
-                                                            uint8_t* __restrict__ out) {
-  constexpr int CPR = D / 16;
-  const int64_t units = (int64_t)B * H * Lp * CPR;
-  for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units; u += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(u % CPR);
-    const int64_t row = u / CPR;
-    const int i = (int)(row % Lp);
-    const int bh = (int)(row / Lp);
-    const int h = bh % H, b = bh / H;
+                                                            uint8_t* __restrict__ out,
+                                                            uint32_t* __restrict__ rowmax2) {
+  constexpr int CPR = D / 16;     // threads per row
+  constexpr int RPP = 256 / CPR;  // rows per pass
+  __shared__ float wmax[4];
+  const int ntiles = Lp / 64;
+  const int tile = blockIdx.x % ntiles;
+  const int bh = blockIdx.x / ntiles;
+  const int h = bh % H, b = bh / H;
+  const int c = threadIdx.x % CPR;
+  const float inv = 1.f / scale[h];
+  float nmax = 0.f;
+#pragma unroll
+  for (int r0 = 0; r0 < 64; r0 += RPP) {
+    const int i = tile * 64 + r0 + threadIdx.x / CPR;
     u32x4 o = {0u, 0u, 0u, 0u};
     if (i < L) {
-      const float inv = 1.f / scale[h];
       const bf16* src = x + b * sb + h * sh + (int64_t)i * sl + 16 * c;
       const u32x4 w0 = *reinterpret_cast<const u32x4*>(src);
       const u32x4 w1 = *reinterpret_cast<const u32x4*>(src + 8);
@@ -81,7 +90,31 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const bf16* __restri
                               bf16_hi(w1[2 * j + 1]) * inv);
       }
     }
-    *reinterpret_cast<u32x4*>(out + row * D + 16 * c) = o;
+    *reinterpret_cast<u32x4*>(out + ((int64_t)bh * Lp + i) * D + 16 * c) = o;
+    if (rowmax2) {
+      float s2 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float v0 = __builtin_amdgcn_cvt_f32_fp8((int)o[j], 0);
+        const float v1 = __builtin_amdgcn_cvt_f32_fp8((int)o[j], 1);
+        const float v2 = __builtin_amdgcn_cvt_f32_fp8((int)o[j], 2);
+        const float v3 = __builtin_amdgcn_cvt_f32_fp8((int)o[j], 3);
+        s2 = fmaf(v0, v0, s2);
+        s2 = fmaf(v1, v1, s2);
+        s2 = fmaf(v2, v2, s2);
+        s2 = fmaf(v3, v3, s2);
+      }
+#pragma unroll
+      for (int off = CPR / 2; off > 0; off >>= 1) s2 += __shfl_xor(s2, off, CPR);
+      nmax = fmaxf(nmax, s2);
+    }
+  }
+  if (rowmax2) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) nmax = fmaxf(nmax, __shfl_xor(nmax, off));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = nmax;
+    __syncthreads();
+    if (threadIdx.x == 0) rowmax2[blockIdx.x] = __float_as_uint(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
   }
 }
 
@@ -106,18 +139,16 @@ hipError_t launch_absmax_scales(const bf16* x, int64_t sb, int64_t sh, int64_t s
 }
 
 hipError_t launch_quantize_rows(const bf16* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D,
-                                const float* scale, uint8_t* out, hipStream_t stream) {
+                                const float* scale, uint8_t* out, uint32_t* rowmax2, hipStream_t stream) {
   const int Lp = transpose_padded_len(L);
-  const int64_t units = (int64_t)B * H * Lp * (D / 16);
-  if (units == 0) return hipSuccess;
-  int64_t blocks = (units + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
+  const int64_t blocks = (int64_t)B * H * (Lp / 64);
+  if (blocks == 0) return hipSuccess;
   if (D == 128)
-    hipLaunchKernelGGL(quantize_rows_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, stream, x, sb, sh, sl, B, H, L,
-                       Lp, scale, out);
+    hipLaunchKernelGGL(quantize_rows_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, stream, x, sb, sh, sl, H, L,
+                       Lp, scale, out, rowmax2);
   else
-    hipLaunchKernelGGL(quantize_rows_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, stream, x, sb, sh, sl, B, H, L,
-                       Lp, scale, out);
+    hipLaunchKernelGGL(quantize_rows_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, stream, x, sb, sh, sl, H, L, Lp,
+                       scale, out, rowmax2);
   return hipGetLastError();
 }
 

@@ -169,12 +169,16 @@ size_t avattn_bwd_staged_workspace_size(int32_t batch, int32_t heads_q, int32_t 
                                         int32_t kv_pairs_per_pass);
 
 /*
- * Forward with q k^T on fp8 (OCP e4m3) operands: per-head dequantization
- * scales q_scale[heads_q], k_scale[heads_kv] (device float32, e.g. from
- * avattn_fp8_absmax_scales); q8 = e4m3(q * (1/q_scale[h])) and k8 likewise
- * (fp32 multiply by the correctly rounded reciprocal, round to nearest even,
- * no saturation: |q / q_scale| must stay below 464), scores =
- * (q8 . k8) * q_scale[h] * k_scale[hk] * scale.  P, V and the output
+ * Forward with q k^T on fp8 (OCP e4m3) operands: per-head scales
+ * q_scale[heads_q], k_scale[heads_kv] (device float32, e.g. from
+ * avattn_fp8_absmax_scales).  k8 = e4m3(k * (1/k_scale[hk])) (fp32 multiply
+ * by the correctly rounded reciprocal); q is quantized against the softmax
+ * constant and k's scale, q8 = e4m3(q * (g * 2^-eq)) with
+ * g = (scale * log2 e) * k_scale[hk] and 2^eq the smallest power of two
+ * >= g * q_scale[h] (fp32 products, eq clamped to [-126, 127]); scores =
+ * 2^eq * (q8 . k8) * ln 2 (~ scale * q.k).  Round to nearest even, no
+ * saturation: |q / q_scale| and |k / k_scale| must stay below 448 (464
+ * for k).  P, V and the output
  * accumulation are as in avattn_fwd (bf16 P, fp32 accumulate), and so are
  * the arguments, masks, GQA, lse and zero-length behaviour; there is no RoPE
  * argument (pass rotated q and k).  workspace must hold

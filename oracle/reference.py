@@ -345,8 +345,9 @@ def packed_attention_mask(lengths: Sequence[int], capacity: int) -> np.ndarray:
 # ---------------------------------------------------------------------------
 # fp8 (e4m3) q k^T variant.  The reference has no fp8 path (its attention is
 # bf16 SDPA, src/avgen/models/attention.py:265-273); this is the sampling-time
-# configuration's definition: per-head absmax scales, OCP e4m3 operands,
-# scores dequantized by the two scales, everything else as attention_f64.
+# configuration's definition: per-head absmax scales, OCP e4m3 operands (k
+# quantized with its scale, q against the softmax constant and k's scale
+# with a power-of-two block exponent), everything else as attention_f64.
 # ---------------------------------------------------------------------------
 
 E4M3_MAX = 448.0
@@ -387,19 +388,55 @@ def fp8_quantize(x: np.ndarray, scale: np.ndarray) -> np.ndarray:
     return e4m3_round(np.asarray(x, np.float32) * inv[None, :, None, None])
 
 
+LOG2E_F32 = np.float32(1.4426950408889634)
+
+
+def ceil_log2_clamped(t: np.ndarray) -> np.ndarray:
+    """The smallest integer e with 2**e >= |t| for float32 t, clamped to
+    [-126, 127]: zero and subnormal t give -126, infinite or NaN t 127."""
+    a = np.abs(np.asarray(t, np.float32)).astype(np.float64)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        f, ex = np.frexp(a)  # a = f * 2**ex, 0.5 <= f < 1
+    e = np.where(f == 0.5, ex - 1, ex).astype(np.int64)
+    e = np.where(a < 2.0**-126, -126, e)
+    e = np.where(~np.isfinite(a), 127, e)
+    return np.clip(e, -126, 127)
+
+
+def fp8_q_operand(q: np.ndarray, q_scale: np.ndarray, k_scale: np.ndarray, scale: float):
+    """The fp8 forward's q operand and its block exponent, per head h with
+    kv head hk = h // (Hq // Hkv): g = f32(f32(scale * log2 e) * k_scale[hk]),
+    eq = ceil_log2_clamped(f32(g * q_scale[h])) (so 2**eq >= g * q_scale[h]),
+    q8 = e4m3(f32(q * f32(g * 2**-eq))).  The scores the kernel forms are
+    ``2**eq * (q8 . k8)`` in log2 units (k8 = fp8_quantize(k, k_scale)).
+    Returns ``(q8, eq)``: q8 float32 e4m3 values, eq int64 (Hq,)."""
+    q = np.asarray(q, np.float32)
+    hq, hkv = q.shape[1], np.asarray(k_scale).shape[0]
+    ks = np.asarray(k_scale, np.float32)[np.arange(hq) // (hq // hkv)]
+    sl2 = np.float32(np.float32(scale) * LOG2E_F32)
+    g = (sl2 * ks).astype(np.float32)
+    eq = ceil_log2_clamped((g * np.asarray(q_scale, np.float32)).astype(np.float32))
+    mult = np.ldexp(g, -eq).astype(np.float32)
+    return e4m3_round((q * mult[None, :, None, None]).astype(np.float32)), eq
+
+
 def attention_fp8_f64(
     q: np.ndarray, k: np.ndarray, v: np.ndarray, q_scale: np.ndarray, k_scale: np.ndarray,
     key_mask: np.ndarray | None = None, scale: float | None = None,
 ) -> tuple[np.ndarray, np.ndarray]:
-    """attention_f64 with scores ``(q8 . k8) * q_scale[h] * k_scale[hk] * scale``,
-    ``q8 = fp8_quantize(q, q_scale)``, ``k8 = fp8_quantize(k, k_scale)``.
+    """attention_f64 on the fp8 forward's scores: ``2**eq[h] * (q8 . k8)``
+    log2-unit scores (fp8_q_operand, fp8_quantize), i.e. natural-log scores
+    ``ln 2 * 2**eq[h] * (q8 . k8)``, which approximate ``scale * (q . k)``.
 
-    The dequantized operands ``q8 * q_scale`` are exact in float64 (4 + 24
-    significant bits), so this is attention_f64 on them.
+    q8, k8 and the power of two are exact in float64, so this is
+    attention_f64 on ``q8 * 2**eq * ln 2`` and ``k8`` with unit scale.
     """
-    qd = fp8_quantize(q, q_scale).astype(np.float64) * np.asarray(q_scale, np.float64)[None, :, None, None]
-    kd = fp8_quantize(k, k_scale).astype(np.float64) * np.asarray(k_scale, np.float64)[None, :, None, None]
-    return attention_f64(qd, kd, v, key_mask, scale)
+    D = np.asarray(q).shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    q8, eq = fp8_q_operand(q, q_scale, k_scale, scale)
+    qd = q8.astype(np.float64) * np.ldexp(1.0, eq)[None, :, None, None] * math.log(2.0)
+    kd = fp8_quantize(k, k_scale).astype(np.float64)
+    return attention_f64(qd, kd, v, key_mask, 1.0)
 
 
 def attention_bwd_f64(

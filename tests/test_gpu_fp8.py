@@ -2,10 +2,12 @@
 (through the C ABI) against the CPU oracle.
 
 The oracle quantizes exactly as the kernels do (oracle/reference.py
-fp8_quantize: fp32 product with the correctly rounded reciprocal, e4m3
-round-to-nearest-even), so the bar is the bf16 forward's: output max-abs
-<= 2e-2 and LSE <= 1e-3 against float64 attention on the dequantized
-operands, masks bit-exact.  The per-head scales are bit-exact.
+fp8_quantize for k: fp32 product with the correctly rounded reciprocal;
+fp8_q_operand for q: fp32 product with the softmax constant, k's scale and
+a power-of-two block exponent; e4m3 round-to-nearest-even), so the bar is
+the bf16 forward's: output max-abs <= 2e-2 and LSE <= 1e-3 against float64
+attention on the dequantized operands, masks bit-exact.  The per-head
+scales are bit-exact.
 """
 
 from __future__ import annotations
@@ -95,6 +97,41 @@ def test_fp8_forward_matches_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
     assert np.abs(l[fin] - rl[fin]).max(initial=0.0) <= LSE_TOL
     if masked and B > 1:
         assert np.all(o[0] == 0)
+
+
+def test_fp8_forward_wide_score_range(amd):
+    """Scores spanning hundreds of log2 units: every query's maximum first
+    appears late in the sequence (far above the earlier tiles' maxima, the
+    running-maximum rescale), some queries meet a key equal to themselves
+    (a score at the Cauchy-Schwarz bound the kernel uses to stop tracking
+    maxima), heads of very different magnitudes (different block exponents),
+    GQA, and one query row anti-aligned with every key (all scores far
+    below zero)."""
+    B, Hq, Hkv, Lq, Lk, D = 1, 4, 2, 200, 900, 128
+    q = _randn((B, Hq, Lq, D), 60).float() * 4
+    k = _randn((B, Hkv, Lk, D), 61).float() * 4
+    q[:, 1] *= 0.01  # tiny head
+    q[:, 3] *= 3.0   # large head
+    k[:, :, 800:820] = q[:, ::2, :20] * 1.5  # late keys aligned with the first 20 queries of heads 0, 2
+    k[:, :, 850] = q[:, ::2, 30]  # a key equal to query 30 (heads 0, 2)
+    q[:, :, 40] = -k[:, [0, 0, 1, 1], :].mean(dim=2) * 50  # anti-aligned with every key
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    v = _randn((B, Hkv, Lk, D), 62)
+    qs, ks = R.fp8_absmax_scale(_np(q)), R.fp8_absmax_scale(_np(k))
+    print("fp8 wide score range", flush=True)
+    out, lse = amd.ops.flash_fwd_fp8(q.cuda(), k.cuda(), v.cuda(), None, torch.from_numpy(qs).cuda(),
+                                     torch.from_numpy(ks).cuda(), D ** -0.5)
+    ro, rl = R.attention_fp8_f64(_np(q), _np(k), _np(v), qs, ks)
+    o = out.float().cpu().numpy().astype(np.float64)
+    l = lse.cpu().numpy().astype(np.float64)
+    assert np.abs(rl).max() > 100  # the range is wide
+    assert np.abs(o - ro).max() <= OUT_TOL
+    # The e4m3 MFMA sums its products at fixed point below the largest one
+    # (measured on gfx950: 448*448 + 31*(1*1) sums to 200728, not 200735),
+    # so a score carries a relative error up to ~2^-16 of its largest
+    # product: rows with one dominant key of x ~ 200 log2 units see LSE
+    # errors ~2e-3.  The bar adds 2^-14 of |lse| to the bf16 one.
+    assert (np.abs(l - rl) <= LSE_TOL + 2.0**-14 * np.abs(rl)).all()
 
 
 def test_fp8_masked_keys_bit_exact(amd):

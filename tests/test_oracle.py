@@ -584,11 +584,38 @@ def test_fp8_absmax_scale_and_quantize(rng):
     assert (np.abs(q8 - y) <= np.maximum(np.abs(y) * 2.0**-4, 2.0**-10) + 1e-12).all()
 
 
+def _pow2_scale(e):
+    """A float32 softmax scale whose float32 product with log2(e) is 2**e."""
+    s = np.float32(2.0**e / np.log2(np.e))
+    assert np.float32(s * R.LOG2E_F32) == np.float32(2.0**e)
+    return float(s)
+
+
+def test_fp8_q_operand_closed_forms(rng):
+    """q's operand: its block exponent is the smallest power of two covering
+    g * q_scale (so the absmax element lands in (224, 448]), and q8 * 2**eq / g
+    is q to within half an e4m3 step; GQA picks each q head's kv scale."""
+    q = rng.standard_normal((2, 4, 33, 16)).astype(np.float32) * 3
+    qs = R.fp8_absmax_scale(q)
+    ks = np.array([0.37, 5.1], np.float32)  # kv heads: q heads 0,1 -> 0; 2,3 -> 1
+    scale = 0.125
+    q8, eq = R.fp8_q_operand(q, qs, ks, scale)
+    g = (np.float32(np.float32(scale) * R.LOG2E_F32) * ks[[0, 0, 1, 1]]).astype(np.float32)
+    t = (g * qs).astype(np.float32).astype(np.float64)
+    assert np.all(np.ldexp(1.0, eq) >= t) and np.all(np.ldexp(1.0, eq - 1) < t)
+    amax = np.abs(q8).max(axis=(0, 2, 3))
+    assert np.all(amax <= 448.0) and np.all(amax > 224.0)
+    assert np.array_equal(R.e4m3_round(q8), q8)
+    y = q.astype(np.float64) * (g.astype(np.float64) * np.ldexp(1.0, -eq))[None, :, None, None]
+    assert (np.abs(q8 - y) <= np.maximum(np.abs(y) * 2.0**-4, 2.0**-10) * (1 + 1e-6)).all()
+
+
 def test_attention_fp8_reduces_to_bf16_attention(rng):
-    """With e4m3-representable q, k and unit scales the fp8 variant is plain
-    attention; scaling q (or k) and its scale by the same power of two gives
-    plain attention of the scaled operands (quantization commutes with powers
-    of two in range)."""
+    """With e4m3-representable q, k, unit scales and a softmax scale whose
+    log2(e) product is a power of two, the fp8 operands are q and k
+    themselves and the fp8 variant is plain attention; scaling q (or k) and
+    its scale by the same power of two gives plain attention of the scaled
+    operands (quantization commutes with powers of two in range)."""
     fin = _e4m3_finite_values().numpy()
     small = fin[(np.abs(fin) <= 2.0) & (np.abs(fin) >= 2.0**-3)]
     q = rng.choice(small, size=(1, 2, 9, 16)).astype(np.float32)
@@ -597,14 +624,24 @@ def test_attention_fp8_reduces_to_bf16_attention(rng):
     mask = np.ones((1, 11), bool)
     mask[0, 3] = False
     one_q, one_k = np.ones(2, np.float32), np.ones(1, np.float32)
-    o8, l8 = R.attention_fp8_f64(q, k, v, one_q, one_k, mask)
-    o, l = R.attention_f64(q, k, v, mask)
-    assert np.array_equal(o8, o) and np.array_equal(l8, l)
-    # q * 8 with scale 8 quantizes to the same e4m3 values and dequantizes to q * 8
-    o8b, l8b = R.attention_fp8_f64(q * 8, k / 4, v, one_q * 8, one_k / 4, mask)
-    ob, lb = R.attention_f64(q * 8, k / 4, v, mask)
-    assert np.array_equal(o8b, ob) and np.array_equal(l8b, lb)
-    # and a non-representable q is rounded: the result moves off plain attention
-    o8c, _ = R.attention_fp8_f64(q * 1.03, k, v, one_q, one_k, mask)
-    oc, _ = R.attention_f64(q * 1.03, k, v, mask)
+    sc = _pow2_scale(-3)
+    q8, eq = R.fp8_q_operand(q, one_q, one_k, sc)
+    assert np.array_equal(q8, q) and np.array_equal(eq, [-3, -3])
+    o8, l8 = R.attention_fp8_f64(q, k, v, one_q, one_k, mask, scale=sc)
+    o, l = R.attention_f64(q, k, v, mask, scale=sc)
+    np.testing.assert_allclose(o8, o, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(l8, l, rtol=1e-6, atol=1e-9)
+    # q * 8 with scale 8, k / 4 with scale 1/4: the same e4m3 operands, and
+    # plain attention of the scaled operands
+    o8b, l8b = R.attention_fp8_f64(q * 8, k / 4, v, one_q * 8, one_k / 4, mask, scale=sc)
+    ob, lb = R.attention_f64(q * 8, k / 4, v, mask, scale=sc)
+    np.testing.assert_allclose(o8b, ob, rtol=1e-6, atol=1e-9)
+    np.testing.assert_allclose(l8b, lb, rtol=1e-6, atol=1e-9)
+    # a softmax scale that is no power of two rounds q: off plain attention
+    o8c, _ = R.attention_fp8_f64(q, k, v, one_q, one_k, mask, scale=sc * 1.03)
+    oc, _ = R.attention_f64(q, k, v, mask, scale=sc * 1.03)
     assert not np.allclose(o8c, oc, rtol=0, atol=1e-9)
+    # and an unquantized q is rounded the same way
+    o8d, _ = R.attention_fp8_f64(q * 1.03, k, v, one_q, one_k, mask, scale=sc)
+    od, _ = R.attention_f64(q * 1.03, k, v, mask, scale=sc)
+    assert not np.allclose(o8d, od, rtol=0, atol=1e-9)
