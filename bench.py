@@ -362,8 +362,26 @@ _KERNEL_SYMBOLS = {"attn_fwd": "attn_fwd_kernel", "bwd_dkdv": "bwd_dkdv_kernel",
 # MFMA instructions each kernel issues per algorithmic unit of work beyond
 # the counted ones (the dK/dV kernel recomputes S = Q K^T: 4 hardware units
 # for 3 counted).
-KERNEL_HW_UNITS = {"attn_fwd": 2, "bwd_dkdv": 4, "bwd_dq": 3, "bwd_dq_ds": 1}
+KERNEL_HW_UNITS = {"attn_fwd": 2, "attn_fwd_fp8": 2, "bwd_dkdv": 4, "bwd_dq": 3, "bwd_dq_ds": 1}
+# Matrix-pipe cycles per MFMA: 32 for 32x32x16 bf16; the fp8 forward issues
+# 4 e4m3 32x32x64 (64 cycles) per 16 bf16 ones.
+MFMA_CYCLES = {"attn_fwd_fp8": (16 * 32 + 4 * 64) / 20}
+# The fp8 forward's peak: half its products at the fp8 rate, half at bf16.
+PEAK_MIXED_TFLOPS = 1.0 / (0.5 / PEAK_BF16_TFLOPS + 0.5 / PEAK_FP8_TFLOPS)
 N_XCD, N_CU = 8, 256
+
+
+def _kernel_short(name: str) -> str | None:
+    """Short name of an attention kernel from its demangled symbol; the fp8
+    forward is attn_fwd_kernel<D, ROPE, FP8 = true, WIN>."""
+    for short, sym in _KERNEL_SYMBOLS.items():
+        if sym in name:
+            if short == "attn_fwd":
+                args = name.split("<", 1)[1].split(">", 1)[0].split(",") if "<" in name else []
+                if len(args) >= 3 and args[2].strip() == "true":
+                    return "attn_fwd_fp8"
+            return short
+    return None
 
 
 def ingest_mfma(counter_csv: str, stats_csv: str, workload: str) -> str:
@@ -382,16 +400,16 @@ def ingest_mfma(counter_csv: str, stats_csv: str, workload: str) -> str:
     per = collections.defaultdict(lambda: collections.defaultdict(lambda: collections.defaultdict(float)))
     with open(counter_csv) as fh:
         for row in csv.DictReader(fh):
-            for short, sym in _KERNEL_SYMBOLS.items():
-                if sym in row["Kernel_Name"]:
-                    did = row.get("Dispatch_Id") or row.get("Correlation_Id")
-                    per[short][row["Counter_Name"]][did] += float(row["Counter_Value"])
+            short = _kernel_short(row["Kernel_Name"])
+            if short:
+                did = row.get("Dispatch_Id") or row.get("Correlation_Id")
+                per[short][row["Counter_Name"]][did] += float(row["Counter_Value"])
     dur = {}
     with open(stats_csv) as fh:
         for row in csv.DictReader(fh):
-            for short, sym in _KERNEL_SYMBOLS.items():
-                if sym in row["Name"]:
-                    dur[short] = float(row["AverageNs"]) / 1e6  # ms
+            short = _kernel_short(row["Name"])
+            if short:
+                dur[short] = float(row["AverageNs"]) / 1e6  # ms
     cfg = CONFIGS[workload]
     B, H, Lq, L, D, cp = cfg["B"], cfg["H"], cfg["Lq"], cfg["L"], cfg["D"], cfg["cp"]
     unit = 2.0 * B * H * Lq * (L // cp) * D  # one product per KV chunk launch
@@ -406,17 +424,20 @@ def ingest_mfma(counter_csv: str, stats_csv: str, workload: str) -> str:
              "```", "",
              "Counters per dispatch, summed over the chip (rocprofv3 reports one row per hardware instance).  "
              "Clock = GRBM_GUI_ACTIVE / 8 XCDs / average duration of the same kernel in the trace run.  "
-             "Issue util = SQ_INSTS_MFMA x 32 cycles / (1024 SIMDs x kernel cycles).  "
+             "Issue util = SQ_INSTS_MFMA x cycles per MFMA (32 for 32x32x16 bf16; the fp8 forward's mix of 4 "
+             "e4m3 32x32x64 at 64 and 16 bf16 averages 38.4) / (1024 SIMDs x kernel cycles).  "
              "Busy util = SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x kernel cycles) (the counter is per SIMD: it reads 32 cycles per MFMA issued).  "
              "HW rate = MFMA work issued (recompute included: forward 2, dK/dV 4, dQ-from-dS 1 products per "
              f"launch of {unit:.4g} FLOP each) / duration; its peak at the measured clock is "
-             "2516.6 TFLOP/s x clock / 2400 MHz.", "",
+             "2516.6 TFLOP/s x clock / 2400 MHz (the fp8 forward: half its products at the fp8 peak, "
+             f"{PEAK_MIXED_TFLOPS:.1f} TFLOP/s at 2400 MHz).  VALU per MFMA counts VALU instructions "
+             "(SQ_INSTS_VALU) per MFMA instruction.", "",
              "| kernel | dispatches | avg ms | clock MHz | SQ_INSTS_MFMA | issue util | busy util | HW TFLOP/s | "
-             "HW / peak at clock | HW / 2516.6 | VALU per MFMA | LDS insts per MFMA | LDS wait / wave cycles | "
+             "HW / peak at clock | HW / peak | VALU per MFMA | LDS insts per MFMA | LDS wait / wave cycles | "
              "LDS bank conflicts per LDS inst |",
              "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
     summary = {}
-    for short in ("attn_fwd", "bwd_dkdv", "bwd_dq_ds", "bwd_dq"):
+    for short in ("attn_fwd", "attn_fwd_fp8", "bwd_dkdv", "bwd_dq_ds", "bwd_dq"):
         cs = per.get(short)
         if not cs or short not in dur:
             continue
@@ -426,16 +447,17 @@ def ingest_mfma(counter_csv: str, stats_csv: str, workload: str) -> str:
         cycles = avg.get("GRBM_GUI_ACTIVE", 0.0) / N_XCD
         mhz = cycles / (ms * 1e3) if ms else 0.0
         mfma = avg.get("SQ_INSTS_MFMA", 0.0)
-        issue = mfma * 32.0 / (4 * N_CU * cycles) if cycles else 0.0
+        issue = mfma * MFMA_CYCLES.get(short, 32.0) / (4 * N_CU * cycles) if cycles else 0.0
         busy = avg.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (4 * N_CU * cycles) if cycles else 0.0
         hw = KERNEL_HW_UNITS[short] * unit / (ms / 1e3) / 1e12
-        peak_clk = PEAK_BF16_TFLOPS * mhz / 2400.0
+        peak = PEAK_MIXED_TFLOPS if short == "attn_fwd_fp8" else PEAK_BF16_TFLOPS
+        peak_clk = peak * mhz / 2400.0
         valu = avg.get("SQ_INSTS_VALU", 0.0) / mfma if mfma else 0.0
         lds = avg.get("SQ_INSTS_LDS", 0.0) / mfma if mfma else 0.0
         wait = avg.get("SQ_WAIT_INST_LDS", 0.0) / avg["SQ_WAVE_CYCLES"] if avg.get("SQ_WAVE_CYCLES") else 0.0
         conf = avg.get("SQ_LDS_BANK_CONFLICT", 0.0) / avg["SQ_INSTS_LDS"] if avg.get("SQ_INSTS_LDS") else 0.0
         lines.append(f"| {short} | {n} | {ms:.3f} | {mhz:.0f} | {mfma:.4g} | {100 * issue:.1f}% | {100 * busy:.1f}% | "
-                     f"{hw:.0f} | {100 * hw / peak_clk:.1f}% | {100 * hw / PEAK_BF16_TFLOPS:.1f}% | {valu:.2f} | "
+                     f"{hw:.0f} | {100 * hw / peak_clk:.1f}% | {100 * hw / peak:.1f}% | {valu:.2f} | "
                      f"{lds:.2f} | {100 * wait:.1f}% | {conf:.3f} |")
         summary[short] = {"avg_ms": ms, "clock_mhz": mhz, "issue_util": issue, "busy_util": busy, "hw_tflops": hw,
                           "counters": avg}
