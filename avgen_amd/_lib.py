@@ -182,6 +182,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "avattn_timing_end": (ctypes.c_int, []),
     "avattn_timing_read": (ctypes.c_int, [c_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]),
     "avattn_timing_reset": (ctypes.c_int, []),
+    "avattn_diag_dq_partials": (ctypes.c_int, [ctypes.c_void_p] + [c_i32] * 6 + [ctypes.c_void_p]),
 }
 
 # Status codes (include/avattn.h).
@@ -282,6 +283,7 @@ KERNEL_IDS = {
     "qk_norm_bwd": 12,
     "ring_dq_finish": 13,
     "dkv_reduce": 14,
+    "diag_dq_partials": 15,
 }
 
 

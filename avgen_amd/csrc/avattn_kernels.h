@@ -228,6 +228,7 @@ enum KernelId : int {
   kKidQkNormBwd = 12,
   kKidDqFinish = 13,
   kKidDkdvReduce = 14,
+  kKidDiag = 15,
 };
 
 // Records HIP events around one launch on `stream` while timing is enabled.

@@ -733,6 +733,51 @@ def gemm_reference(device, steps: int) -> dict:
     return out
 
 
+def dq_atomics_probe(device, steps: int) -> dict:
+    """What a dQ that never stages dS would cost at the c3 chunk: the
+    library's diagnostic replays the fused backward's dQ accumulation (one
+    64x128 fp32 partial tile per 128-key block and 64-row query tile, 40
+    heads, 148 key blocks, 296 query tiles) as fp32 atomics and, for the
+    memory system's rate on the same bytes, as plain stores.  Each launch
+    does a quarter of the pattern (74 tiles per key block); the full-pattern
+    time per c3 chunk is 4x that.  Not part of the metric."""
+    from avgen_amd import _lib
+
+    lib = _lib.load()
+    H, nkb, ntiles, tpb, D = 40, 148, 296, 74, 128
+    acc = torch.zeros(H * ntiles * 64 * D, dtype=torch.float32, device=device)
+    payload = 4.0 * H * nkb * tpb * 64 * D  # bytes added (or stored) per launch
+    out = {"metric": "dQ accumulation without staged dS: fp32 atomics vs plain stores (c3 chunk pattern)",
+           "unit": "TB/s", "pattern": {"heads": H, "key_blocks": nkb, "query_tiles": ntiles,
+                                       "tiles_per_block_per_launch": tpb, "head_dim": D,
+                                       "payload_bytes_per_launch": payload}, "modes": {}}
+    stream = torch.cuda.current_stream(device).cuda_stream
+    for name, atomic in (("plain_store", 0), ("atomic_add_f32", 1)):
+        acc.zero_()
+        _lib.check(lib.avattn_diag_dq_partials(acc.data_ptr(), H, nkb, ntiles, tpb, D, atomic, stream),
+                   "avattn_diag_dq_partials")
+        torch.cuda.synchronize()
+        with _lib.LaunchTiming(steps + 4) as timing:
+            for _ in range(steps):
+                _lib.check(lib.avattn_diag_dq_partials(acc.data_ptr(), H, nkb, ntiles, tpb, D, atomic, stream),
+                           "avattn_diag_dq_partials")
+            torch.cuda.synchronize()
+            ms, n = timing.read("diag_dq_partials")
+            timing.close()
+        avg = ms / n
+        out["modes"][name] = {"ms_per_launch": round(avg, 3), "tb_per_s": round(payload / (avg / 1e3) / 1e12, 3),
+                              "ms_per_c3_chunk": round(4 * avg, 2)}
+        if atomic:
+            # every element of a tile gets 1.0 from each visiting key block, per launch
+            t = torch.arange(ntiles, device=device)
+            kb = torch.arange(nkb, device=device)
+            visits = (((t[None, :] - 2 * kb[:, None]) % ntiles) < tpb).sum(0).float()
+            want = visits * (steps + 1)
+            got = acc.view(H, ntiles, 64 * D)
+            out["modes"][name]["sums_exact"] = bool(torch.equal(got, want[None, :, None].expand_as(got)))
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -751,6 +796,8 @@ def main() -> int:
                          "profiles/<config>_mfma_counters.md and exit")
     ap.add_argument("--gemm-reference", action="store_true",
                     help="time torch.matmul in bf16 (the vendor GEMM) on this box instead and exit")
+    ap.add_argument("--dq-atomics-probe", action="store_true",
+                    help="time the fused backward's dQ accumulation as fp32 atomics vs plain stores and exit")
     args = ap.parse_args()
 
     if args.ingest_pmc:
@@ -779,6 +826,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.gemm_reference:
         print(json.dumps(gemm_reference(dev, args.steps)), flush=True)
+        return 0
+    if args.dq_atomics_probe:
+        print(json.dumps(dq_atomics_probe(dev, args.steps)), flush=True)
         return 0
     if args.config == "c5":
         log(f"[bench] config c5: {cfg['desc']}")

@@ -590,7 +590,7 @@ int avattn_qk_norm_rope_bwd(const void* x, const int64_t* x_strides,
  * fp8 forward's e4m3 k copy), 8 fp8 forward, 9 fp8 absmax scales,
  * 10 dQ from staged dS, 11 q/k norm + rotation, 12 its backward,
  * 13 the ring dq finish (avattn_ring_dq_finish), 14 the sum of the
- * partial results of split dK/dV workgroups.
+ * partial results of split dK/dV workgroups, 15 avattn_diag_dq_partials.
  * avattn_timing_begin creates `capacity` event pairs (call it outside any
  * timed or captured region); launches beyond capacity are not recorded and
  * make avattn_timing_read return AVATTN_ERR_WORKSPACE.
@@ -599,6 +599,23 @@ int avattn_timing_begin(int32_t capacity);
 int avattn_timing_end(void);
 int avattn_timing_read(int32_t kernel_id, double* total_ms, int32_t* launches);
 int avattn_timing_reset(void);
+
+/*
+ * Diagnostic (no counterpart in the reference): replays the dQ accumulation
+ * a backward without staged dS would issue, with synthetic partials of 1.0
+ * and no other work.  One 512-thread workgroup per (head, 128-key block)
+ * adds (atomic != 0: fp32 vector atomics, agent scope) or stores
+ * (atomic == 0) one 64 x head_dim fp32 tile for each of tiles_per_block
+ * query tiles, starting at tile 2*key_block (mod query_tiles), into
+ * acc[heads][query_tiles][64][head_dim] (device float32, 16-byte aligned;
+ * the caller's allocation must hold that many floats).  With atomics every
+ * element ends up incremented by the number of key blocks that visited its
+ * tile.  Time it with the avattn_timing_* diagnostics (kernel id 15).
+ */
+int avattn_diag_dq_partials(float* acc, int32_t heads, int32_t key_blocks,
+                            int32_t query_tiles, int32_t tiles_per_block,
+                            int32_t head_dim, int32_t atomic,
+                            avattn_stream_t stream);
 
 #ifdef __cplusplus
 }
