@@ -404,28 +404,37 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
     f32x16 s[2] = {zero16(), zero16()};
     bf16x8 pb[2][2];
     u32x4 up[2][2];
-    // Softmax step (sub, k2, e2): two probabilities, packed; the last step
-    // of a (sub, k2) hands its 16 bytes to the partner wave.
-    // WIN: a tile outside [w_ia, w_ib) masks scores per (row, key).
+    // WIN: a tile outside [w_ia, w_ib) masks the scores of a row half per
+    // (row, key) before its softmax steps: one wave-uniform branch per half,
+    // not taken on the (common) inside tiles.
     bool edge = false;
     if constexpr (WIN) {
       const int T = tile_idx(it);
       edge = T < w_ia || T >= w_ib;
     }
+    auto mask_sub = [&](int sub) {
+      if constexpr (WIN) {
+        if (__builtin_expect(edge, 0)) {
+#pragma unroll
+          for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+            for (int h4 = 0; h4 < 2; ++h4) {
+              // rows 32*sub + 16*k2 + 8*hh + 4*h4 + [0, 4) of the tile
+              const uint32_t r0 = sb + u * kRS + 4 * (32 * sub + 16 * k2 + 4 * h4);
+              const u32x4 lo = lds_ld<u32x4>(r0 + kWloOff), hi = lds_ld<u32x4>(r0 + kWhiOff);
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (key < (int)lo[r] || key >= (int)hi[r]) s[sub][8 * k2 + 4 * h4 + r] = kNegInf;
+            }
+        }
+      }
+    };
+    // Softmax step (sub, k2, e2): two probabilities, packed; the last step
+    // of a (sub, k2) hands its 16 bytes to the partner wave.
     auto smx = [&](int sub, int k2, int e2) {
       const int e = 2 * e2;
       const f32x4& lv = l2[sub][k2][e >> 2];
-      float s0 = s[sub][8 * k2 + e], s1 = s[sub][8 * k2 + e + 1];
-      if constexpr (WIN) {
-        if (edge) {
-          // rows 32*sub + 16*k2 + 8*hh + e (+1) of the tile, this lane's key
-          const uint32_t r0 = sb + u * kRS + 4 * (32 * sub + 16 * k2 + e);
-          const int lo0 = lds_ld<int>(r0 + kWloOff), lo1 = lds_ld<int>(r0 + kWloOff + 4);
-          const int hi0 = lds_ld<int>(r0 + kWhiOff), hi1 = lds_ld<int>(r0 + kWhiOff + 4);
-          if (key < lo0 || key >= hi0) s0 = kNegInf;
-          if (key < lo1 || key >= hi1) s1 = kNegInf;
-        }
-      }
+      const float s0 = s[sub][8 * k2 + e], s1 = s[sub][8 * k2 + e + 1];
       const float p0 = __builtin_amdgcn_exp2f(fmaf(s0, c, -lv[e & 3]));
       const float p1 = __builtin_amdgcn_exp2f(fmaf(s1, c, -lv[(e & 3) + 1]));
       up[sub][k2][e2] = pack_bf16x2(p0, p1);
@@ -445,6 +454,7 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (j >= 1 && j <= 8) l2_read(j - 1);
       if (j >= kLo) {
         const int n = NS - kLo;
+        if (j == kLo) mask_sub(0);
         for (int st = (j - kLo) * 8 / n; st < (j - kLo + 1) * 8 / n; ++st) smx(0, st >> 2, st & 3);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -452,9 +462,11 @@ __global__ __launch_bounds__(512, 1) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
     for (int q8 = NS - 1; q8 < 8; ++q8) l2_read(q8);  // what the loop had no slot for
     if (kLo >= NS) {
+      mask_sub(0);
 #pragma unroll
       for (int st = 0; st < 8; ++st) smx(0, st >> 2, st & 3);
     }
+    mask_sub(1);
 #pragma unroll
     for (int st = 0; st < 8; ++st) smx(1, st >> 2, st & 3);
     // P goes out with the next barrier (T of tile it + 1, where the partner
