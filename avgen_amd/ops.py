@@ -338,12 +338,16 @@ def _out_or_new(t: Optional[torch.Tensor], like: torch.Tensor, name: str, label:
 # device memory it may take.  Fixed per device (never read from the
 # allocator's current state, so the pass count of a given shape does not
 # change from call to call): set_ds_budget(), else AVGEN_AMD_DS_BUDGET_GB
-# (0 turns staging off), else the default below.  32 GiB holds a c3 ring
-# chunk's 40 (batch, head) pairs in one pass (26.7 GiB) and a c2 block's 40
-# pairs (20 GiB); a 76k-token pair (10.8 GiB) goes two per pass.  When the
-# allocator cannot provide a planned workspace the call retries with fewer
-# pairs per pass, then (where staging is optional) without staging.
-_DS_BUDGET_DEFAULT = 32 << 30
+# (0 turns staging off), else the default below, capped at a third of the
+# device.  64 GiB holds a c3 ring chunk's 40 (batch, head) pairs in one pass
+# (26.7 GiB) and a c2 block's 40 pairs (20 GiB); 76k-token pairs (10.8 GiB)
+# go five per pass, and the compact dS of the temporal-window and varlen
+# workloads (2.4 / 3.0 GiB per pair) twenty per pass.  Fewer, larger passes
+# keep the dK/dV and dQ grids many rounds deep: against 32 GiB, c4 ran 2.4%
+# and varlen 2.3% faster (window and c3 unchanged).  When the allocator
+# cannot provide a planned workspace the call retries with fewer pairs per
+# pass, then (where staging is optional) without staging.
+_DS_BUDGET_DEFAULT = 64 << 30
 _ds_budgets: dict[int, int] = {}
 
 

@@ -2,8 +2,8 @@
 functions and the host plan only; no launch).
 
 * the default budget keeps the benchmark's shapes in the pass counts the
-  plan states (c3 ring chunk and c2 block in one pass, a 76k-token pair two
-  per pass), whatever the device's total memory above 96 GiB;
+  plan states (c3 ring chunk and c2 block in one pass, 76k-token pairs five
+  per pass), whatever the device's total memory above 192 GiB;
 * passes are equal, the fewest that fit;
 * a workspace the allocator cannot provide is retried with half the pairs
   per pass down to one, then (staging optional) without staging, and raises
@@ -41,17 +41,17 @@ DEV = torch.device("cuda", 0)
 
 
 def test_default_budget_pass_counts(device_props):
-    assert ops._ds_budget(DEV) == 32 * GIB
+    assert ops._ds_budget(DEV) == 64 * GIB
     # c3 ring chunk: 40 pairs of 18,944 x 18,944 bf16 = 26.7 GiB, one pass
     per = ops.ds_bytes_per_pair(1, 18900, 18900)
-    assert per == 18944 * 18944 * 2 and 40 * per < 32 * GIB
+    assert per == 18944 * 18944 * 2 and 40 * per < 64 * GIB
     assert ops._staged_pairs(1, 40, 40, 18900, 18900, 128, DEV) == 40
     # c2 block: (2, 20, 16384) -> 40 pairs of 512 MiB, one pass
     assert ops._staged_pairs(2, 20, 20, 16384, 16384, 128, DEV) == 40
-    # c4: 76,112 tokens, 10.8 GiB per pair -> 2 per pass, 40 passes
+    # c4: 76,112 tokens, 10.8 GiB per pair -> 5 per pass (80 pairs: 16 passes)
     per4 = ops.ds_bytes_per_pair(1, 76112, 76112)
-    assert 2 * per4 <= 32 * GIB < 3 * per4
-    assert ops._staged_pairs(2, 40, 40, 76112, 76112, 128, DEV) == 2
+    assert 5 * per4 <= 64 * GIB < 6 * per4
+    assert ops._staged_pairs(2, 40, 40, 76112, 76112, 128, DEV) == 5
     # the plan's workspace: the library's staged size for that many pairs
     nbytes, staged = ops.bwd_workspace_plan(1, 40, 40, 18900, 18900, 128, DEV)
     assert staged and nbytes == _lib.load().avattn_bwd_staged_workspace_size(1, 40, 40, 18900, 18900, 128, 40)
@@ -70,7 +70,7 @@ def test_equal_passes_and_overrides(device_props):
     assert ops._staged_pairs(1, 18, 18, 1000, 1000, 64, DEV) == 0
     assert ops._staged_pairs(1, 18, 18, 1000, 1000, 64, DEV, stage_ds=True) == 1
     ops.set_ds_budget(None, DEV)
-    assert ops._ds_budget(DEV) == 32 * GIB
+    assert ops._ds_budget(DEV) == 64 * GIB
     assert ops._staged_pairs(1, 18, 18, 1000, 1000, 64, DEV, stage_ds=False) == 0
 
 
