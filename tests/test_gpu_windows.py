@@ -142,6 +142,44 @@ def test_windowed_forward_accepts_any_windows(amd):
         amd.ops.flash_bwd_windowed(q.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, lo_t, hi_t, None, D ** -0.5)
 
 
+def test_nan_key_reaches_only_workgroups_that_visit_its_tile(amd):
+    """The documented deviation from the dense-mask reference, whose additive
+    -inf mask turns a NaN score into NaN on every row: the windowed forward
+    visits, per 256-row workgroup, only the 64-key tiles its rows' windows
+    meet, so a NaN key row reaches the output rows of the workgroups that
+    visit its tile (through a window holding the key, or 0 x NaN in P V for
+    rows whose window excludes it) and the LSE of the rows whose window holds
+    it, and nothing else, which equals the run with that key zeroed."""
+    B, H, Lq, Lk, D = 1, 2, 1300, 2000, 128
+    q, k, v = _randn((B, H, Lq, D), 31), _randn((B, H, Lk, D), 32), _randn((B, H, Lk, D), 33)
+    rows = np.arange(Lq)
+    lo = np.minimum(rows * Lk // Lq, Lk).astype(np.int32)
+    hi = np.minimum(lo + 150, Lk).astype(np.int32)
+    j = 1033
+    kz, vz = k.clone(), v.clone()
+    kz[:, :, j], vz[:, :, j] = 0, 0
+    kn, vn = kz.clone(), vz.clone()
+    kn[:, :, j], vn[:, :, j] = float("nan"), float("nan")
+    lo_t, hi_t = torch.from_numpy(lo).cuda(), torch.from_numpy(hi).cuda()
+    print("window NaN key", flush=True)
+    o_n, l_n = amd.ops.flash_fwd_windowed(q.cuda(), kn.cuda(), vn.cuda(), lo_t, hi_t, None, D ** -0.5)
+    o_z, l_z = amd.ops.flash_fwd_windowed(q.cuda(), kz.cuda(), vz.cuda(), lo_t, hi_t, None, D ** -0.5)
+    # workgroups of 256 rows: tiles [lo(first) // 64, ceil(hi(last) / 64))
+    reach = np.zeros(Lq, dtype=bool)
+    for r0 in range(0, Lq, 256):
+        r1 = min(r0 + 256, Lq)
+        if lo[r0] // 64 <= j // 64 < (hi[r1 - 1] + 63) // 64:
+            reach[r0:r1] = True
+    assert reach.any() and (~reach).any()
+    reach_t = torch.from_numpy(reach).cuda()
+    holds = torch.from_numpy((lo <= j) & (j < hi)).cuda()
+    assert torch.isnan(o_n[:, :, reach_t]).all()
+    # the LSE (no P V product) is NaN exactly on the rows whose window holds the key
+    assert torch.equal(torch.isnan(l_n[0]), holds[None].expand(H, Lq))
+    assert torch.equal(l_n[:, :, ~holds], l_z[:, :, ~holds])
+    assert torch.equal(o_n[:, :, ~reach_t], o_z[:, :, ~reach_t])
+
+
 def test_full_windows_equal_the_unwindowed_kernel(amd):
     """Windows [0, Lk) on every row: the windowed forward is the plain one."""
     B, Hq, Hkv, Lq, Lk, D = 1, 8, 8, 4096, 4096, 128
