@@ -137,6 +137,26 @@ def build() -> dict[str, dict[str, np.ndarray]]:
         "norm_bits": R.bf16_bits(n), "out_bits": R.bf16_bits(y), "dy_bits": R.bf16_bits(dy),
         "dx": dx.astype(np.float32), "dw": dw,
     }
+
+    # fp8 (e4m3) q k^T forward: per-head absmax scales, GQA, a key mask with
+    # one fully masked batch row; the quantized operands and the block
+    # exponent are stored with the expected output.
+    B, H, Hk, Lq, Lk, d = 2, 4, 2, 48, 80, 128
+    q = _bf16(rng, (B, H, Lq, d), 2.0)
+    k = _bf16(rng, (B, Hk, Lk, d))
+    v = _bf16(rng, (B, Hk, Lk, d))
+    mask = np.ones((B, Lk), bool)
+    mask[0, 61:] = False
+    mask[1, :] = False
+    qs, ks = R.fp8_absmax_scale(q), R.fp8_absmax_scale(k)
+    sc = np.float32(d ** -0.5)
+    q8, eq = R.fp8_q_operand(q, qs, ks, float(sc))
+    o, lse = R.attention_fp8_f64(q, k, v, qs, ks, mask, float(sc))
+    out["attn_fp8_d128"] = {
+        "q_bits": R.bf16_bits(q), "k_bits": R.bf16_bits(k), "v_bits": R.bf16_bits(v), "mask": mask,
+        "q_scale": qs, "k_scale": ks, "scale": sc, "q8": q8, "eq": eq, "k8": R.fp8_quantize(k, ks),
+        "out": o.astype(np.float32), "lse": lse,
+    }
     return out
 
 

@@ -12,7 +12,7 @@ import torch
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 NAMES = ["rope_tables_d12", "rope_tables_d128", "rope_tables_d128_ntk", "rope_apply_d64", "attn_d64", "attn_d128",
-         "ring_3chunks", "packed_attention", "temporal_attention", "qk_norm_rope_d128"]
+         "ring_3chunks", "packed_attention", "temporal_attention", "qk_norm_rope_d128", "attn_fp8_d128"]
 
 
 def load(name: str) -> dict[str, np.ndarray]:
@@ -52,6 +52,23 @@ def test_attention_fixtures_agree_with_torch_cpu():
         ref = F.scaled_dot_product_attention(q, k.repeat_interleave(rep, 1), v.repeat_interleave(rep, 1),
                                              attn_mask=m[:, None, None, :])
         assert np.abs(ref.numpy() - g["out"]).max() < 1e-6
+
+
+def test_fp8_fixture_operands_agree_with_torch_float8():
+    # The stored e4m3 operands, independently of the oracle's e4m3_round:
+    # torch's float8_e4m3fn cast of the fp32 products the kernels form.
+    g = load("attn_fp8_d128")
+    q, k = bits_to_f32(g["q_bits"]), bits_to_f32(g["k_bits"])
+    H, Hk = q.shape[1], k.shape[1]
+    ks_h = g["k_scale"][np.arange(H) // (H // Hk)]
+    gq = (np.float32(g["scale"]) * np.float32(1.4426950408889634) * ks_h).astype(np.float32)
+    mult = np.ldexp(gq, -g["eq"]).astype(np.float32)
+    q8 = torch.from_numpy((q * mult[None, :, None, None]).astype(np.float32)).to(torch.float8_e4m3fn).float()
+    assert np.array_equal(q8.numpy(), g["q8"])
+    kinv = (np.float32(1) / g["k_scale"]).astype(np.float32)
+    k8 = torch.from_numpy((k * kinv[None, :, None, None]).astype(np.float32)).to(torch.float8_e4m3fn).float()
+    assert np.array_equal(k8.numpy(), g["k8"])
+    assert np.all(np.ldexp(1.0, g["eq"]) >= (gq * g["q_scale"]).astype(np.float32))
 
 
 @pytest.fixture(scope="module")
@@ -174,3 +191,18 @@ def test_gpu_qk_norm_matches_golden(amd):
     dx, dw = amd.ops.qk_norm_rope_bwd(bits_to_bf16(g["dy_bits"]).cuda(), x.detach(), w, float(g["eps"]), cos, sin)
     assert np.abs(dx.float().cpu().numpy() - g["dx"]).max() <= 2e-2 * np.abs(g["dx"]).max()
     assert np.abs(dw.cpu().numpy() - g["dw"]).max() <= 1e-3 * np.abs(g["dw"]).max()
+
+
+@pytest.mark.gpu
+def test_gpu_fp8_matches_golden(amd):
+    g = load("attn_fp8_d128")
+    q, k, v = (bits_to_bf16(g[f"{t}_bits"]).cuda() for t in "qkv")
+    qs, ks = torch.from_numpy(g["q_scale"]).cuda(), torch.from_numpy(g["k_scale"]).cuda()
+    out, lse = amd.ops.flash_fwd_fp8(q, k, v, torch.from_numpy(g["mask"]).cuda(), qs, ks, float(g["scale"]))
+    o = out.float().cpu().numpy()
+    l = lse.cpu().numpy().astype(np.float64)
+    assert np.abs(o - g["out"]).max() <= 2e-2
+    fin = np.isfinite(g["lse"])
+    assert np.array_equal(np.isneginf(l), ~fin)
+    assert np.abs(l[fin] - g["lse"][fin]).max() <= 1e-3
+    assert np.all(o[1] == 0)  # batch 1 has every key masked
