@@ -400,6 +400,10 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
         }
       return;
     }
+    // Masks of both halves first, then one reference max for the tile: the
+    // probabilities of both halves are formed against the same m_run (a
+    // half processed against a reference the other half then moves would
+    // enter P V at the wrong scale while the row sum is rescaled).
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
       f32x16& s_cur = sh[hf];
@@ -422,33 +426,36 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
           for (int r = 0; r < 4; ++r) s_cur[4 * g + r] += bb[r];
         }
       }
-      if (!bounded) {
-        float mx = kNegInf;
+    }
+    if (!bounded) {
+      float mx = kNegInf;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_cur[r]);
-        mx = halves_max(mx);
-        if (mx > m_run + tau) {
-          // New reference max (both lanes of a query agree: mx is shared).
-          const float alpha = __builtin_amdgcn_exp2f((m_run - mx) * c);
-          l_run0 *= alpha;
-          l_run1 *= alpha;
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(sh[0][r], sh[1][r]));
+      mx = halves_max(mx);
+      if (mx > m_run + tau) {
+        // New reference max (both lanes of a query agree: mx is shared).
+        const float alpha = __builtin_amdgcn_exp2f((m_run - mx) * c);
+        l_run0 *= alpha;
+        l_run1 *= alpha;
 #pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-          m_run = mx;
-        }
-        bounded = __all((bound - m_run) * c <= kBoundTau);
+          for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+        m_run = mx;
       }
-      const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
+      bounded = __all((bound - m_run) * c <= kBoundTau);
+    }
+    const float mc = (m_run == kNegInf) ? 0.f : m_run * c;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int k2 = 0; k2 < 2; ++k2) {
         u32x4 u;
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
           const int r = 8 * k2 + 2 * e2;
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[r], c, -mc));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[r + 1], c, -mc));
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sh[hf][r], c, -mc));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sh[hf][r + 1], c, -mc));
           if (e2 & 1)
             l_run1 += p0 + p1;
           else
@@ -457,7 +464,6 @@ __global__ __launch_bounds__(512, 1) void attn_fwd_kernel(FwdArgs a) {
         }
         pf[hf][k2] = bits_to_bf16x8(u);
       }
-    }
   };
   // O^T += V^T P^T over the (half, k2, dt) steps; B operand slot (hh, e) of
   // pf[hf][k2] is key 32*hf + 16*k2 + 8*hh + e: one 16-byte chunk of a V^T

@@ -114,6 +114,38 @@ def test_forward_score_bound_paths(amd):
     assert np.abs(lse.cpu().numpy() - rl).max() <= LSE_TOL
 
 
+def test_max_raised_by_the_second_half_of_a_tile(amd):
+    """The forward processes a 64-key tile as two 32-key halves; when the
+    second half holds a key that raises a row's maximum far (here by tens of
+    log2 units) above the first half's, both halves' probabilities must still
+    enter P V against the same reference: in the first tile and in a later
+    one, on the plain, windowed and fp8 forwards."""
+    B, H, Lq, Lk, D = 1, 2, 96, 700, 128
+    q = _randn((B, H, Lq, D), 90, 0.7).float()
+    k = _randn((B, H, Lk, D), 91, 0.7).float()
+    v = _randn((B, H, Lk, D), 92)
+    k[:, :, 40] = q[:, :, 0] * 4.0     # tile 0, second half: dominates row 0
+    k[:, :, 370] = q[:, :, 40] * 4.0   # tile 5, second half: dominates row 40
+    k[:, :, 690] = q[:, :, 70] * 2.0   # tile 10, second half
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v))
+    outs = {"plain": amd.ops.flash_fwd(qc, kc, vc, None, None, None, D ** -0.5)}
+    lo = torch.zeros(Lq, dtype=torch.int32, device="cuda")
+    hi = torch.full((Lq,), Lk, dtype=torch.int32, device="cuda")
+    outs["windowed"] = amd.ops.flash_fwd_windowed(qc, kc, vc, lo, hi, None, D ** -0.5)
+    for name, (out, lse) in outs.items():
+        print(f"second-half max {name}", flush=True)
+        assert np.abs(_f64(out) - ro).max() <= OUT_TOL, name
+        assert np.abs(lse.cpu().numpy() - rl).max() <= LSE_TOL, name
+    qs, ks = R.fp8_absmax_scale(_f64(q)), R.fp8_absmax_scale(_f64(k))
+    out8, lse8 = amd.ops.flash_fwd_fp8(qc, kc, vc, None, torch.from_numpy(qs).cuda(), torch.from_numpy(ks).cuda(),
+                                       D ** -0.5)
+    r8, l8 = R.attention_fp8_f64(_f64(q), _f64(k), _f64(v), qs, ks)
+    assert np.abs(_f64(out8) - r8).max() <= OUT_TOL
+    assert (np.abs(lse8.cpu().numpy() - l8) <= LSE_TOL + 2.0 ** -14 * np.abs(l8)).all()
+
+
 def test_attention_dropin_matches_torch_restatement(amd):
     q, k, v = _randn((1, 4, 256, 128), 10), _randn((1, 4, 384, 128), 11), _randn((1, 4, 384, 128), 12)
     out = amd.attention.attention(q.cuda(), k.cuda(), v.cuda())
