@@ -183,6 +183,34 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "avattn_timing_read": (ctypes.c_int, [c_i32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]),
     "avattn_timing_reset": (ctypes.c_int, []),
     "avattn_diag_dq_partials": (ctypes.c_int, [ctypes.c_void_p] + [c_i32] * 6 + [ctypes.c_void_p]),
+    "avattn_fwd_f32": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p,
+         c_ptr,
+         c_ptr],
+    ),
+    "avattn_bwd_f32_workspace_size": (c_size, [c_i32, c_i32, c_i32]),
+    "avattn_bwd_f32": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_i64p, c_i64p, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
+         c_ptr, c_size,
+         c_ptr],
+    ),
+    "avattn_rope_apply_f32": (
+        ctypes.c_int,
+        [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_ptr, c_i64, c_i32,
+         c_ptr, c_i64p, c_ptr],
+    ),
 }
 
 # Status codes (include/avattn.h).

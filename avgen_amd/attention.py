@@ -10,7 +10,10 @@ Semantics kept from the reference: zero-length query or key sequences
 return ``zeros_like(query)`` (:261-262); the default scale is
 ``1/sqrt(head_dim)``; a boolean mask is ``True`` = attend.  Scope of the
 kernel (anything else raises rather than silently running elsewhere):
-bf16 tensors on a ROCm GPU, head_dim 64 or 128, ``dropout_p == 0``,
+bf16 tensors on a ROCm GPU (:func:`attention` and :func:`rotary_attention`
+also take float32 tensors, computed in fp32 by their own kernels, as the
+reference's SDPA computes in the caller's dtype), head_dim 64 or 128,
+``dropout_p == 0``,
 ``is_causal == False`` (video DiT attention is bidirectional), and masks
 that are key-padding masks — boolean, broadcastable as ``(batch, 1, 1,
 keys)`` — which is what :func:`key_padding_mask` and CrossAttention build
@@ -222,7 +225,8 @@ def attention(
     (signature of src/avgen/models/attention.py:227-237).
 
     Args:
-        query: ``(batch, heads, queries, head_dim)`` bf16 on a ROCm GPU.
+        query: ``(batch, heads, queries, head_dim)`` bf16 or float32 on a
+            ROCm GPU (key and value in the same dtype).
         key/value: ``(batch, kv_heads, keys, head_dim)``.
         attn_mask: ``None`` or a boolean key-padding mask broadcastable as
             ``(batch, 1, 1, keys)``; True = attend.

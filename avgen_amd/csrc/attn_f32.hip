@@ -1,0 +1,578 @@
+// Attention on float32 tensors.  The reference's attention() computes in the
+// caller's dtype (src/avgen/models/attention.py:227-273 hands q, k, v to
+// F.scaled_dot_product_attention as they come), and its fp32 tensors are
+// rotated in fp32 (src/avgen/models/rope.py:332-338, a cast back to fp32 is
+// the identity).  These kernels keep every operand and every product in
+// fp32 on the vector ALUs (gfx950's fp32 matrix rate is no higher than its
+// fp32 vector rate, so the matrix cores buy nothing here):
+//   * forward: two lanes per query row (half of head_dim each), 32-key tiles
+//     of K and V through LDS, the online softmax in the exp2 domain;
+//   * backward, without atomics: row statistics (lse2 = lse*log2 e, +inf
+//     for a row without keys; ndelta = -rowsum(dO*O)), then dK/dV with four
+//     lanes per key looping over 16-row query tiles of every query head of
+//     its group, and dQ with four lanes per query row looping over 32-key
+//     tiles;
+//   * the interleaved-pair rotation of fp32 tensors (and its transpose),
+//     with the reference's operation order (two products, one sum, no FMA).
+// They are the exact-dtype path for fp32 callers at moderate sizes; the
+// bf16 kernels are the fast path.
+#include "avattn.h"
+
+#include <math.h>
+
+#include "avattn_device.h"
+#include "avattn_kernels.h"
+
+namespace avattn {
+namespace {
+
+struct F32Args {
+  const float *q, *k, *v;
+  int64_t qsb, qsh, qsl, ksb, ksh, ksl, vsb, vsh, vsl;
+  int B, Hq, Hkv, Lq, Lk, D;
+  const uint8_t* mask;
+  int64_t msb;
+  float scale, c;  // c = scale * log2(e)
+  // forward
+  float* o;
+  int64_t osb, osh, osl;
+  float* lse;
+  // backward
+  const float *dout, *out, *lse_in;
+  int64_t dosb, dosh, dosl, oisb, oish, oisl;
+  float *dq, *dk, *dv;
+  int64_t dqsb, dqsh, dqsl, dksb, dksh, dksl, dvsb, dvsh, dvsl;
+  float *lse2, *ndelta;  // workspace, (B, Hq, Lq) each
+};
+
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ void st4(float* p, const f32x4& v) { *reinterpret_cast<f32x4*>(p) = v; }
+
+__device__ __forceinline__ bool key_ok(const F32Args& a, int b, int key) {
+  return key < a.Lk && (a.mask == nullptr || a.mask[b * a.msb + key] != 0);
+}
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
+  constexpr int HD = D / 2, KT = 32, ROWS = 128;
+  __shared__ __attribute__((aligned(16))) float ks[KT][D];
+  __shared__ __attribute__((aligned(16))) float vs[KT][D];
+  __shared__ float bias[KT];
+  const int tid = threadIdx.x, half = tid & 1;
+  const int nqb = (a.Lq + ROWS - 1) / ROWS;
+  const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
+  const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
+  const int row = qb * ROWS + (tid >> 1);
+  const bool valid = row < a.Lq;
+
+  float q[HD], o[HD];
+  {
+    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl + half * HD;
+#pragma unroll
+    for (int d = 0; d < HD; d += 4) {
+      const f32x4 x = valid ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      q[d] = x[0], q[d + 1] = x[1], q[d + 2] = x[2], q[d + 3] = x[3];
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < HD; ++d) o[d] = 0.f;
+  float m = kNegInf, l = 0.f;
+  const float* kb = a.k + b * a.ksb + hk * a.ksh;
+  const float* vb = a.v + b * a.vsb + hk * a.vsh;
+
+  for (int k0 = 0; k0 < a.Lk; k0 += KT) {
+    __syncthreads();  // the previous tile is consumed
+    for (int u = tid; u < KT * D / 4; u += 256) {
+      const int j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = k0 + j;
+      const bool in = key < a.Lk;
+      st4(&ks[j][c4], in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+      st4(&vs[j][c4], in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+    }
+    if (tid < KT) bias[tid] = key_ok(a, b, k0 + tid) ? 0.f : kNegInf;
+    __syncthreads();
+
+    float s[KT];
+    float mt = kNegInf;
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      float acc = 0.f;
+#pragma unroll
+      for (int d = 0; d < HD; d += 4) {
+        const f32x4 kk = ld4(&ks[j][half * HD + d]);
+        acc = fmaf(q[d], kk[0], acc);
+        acc = fmaf(q[d + 1], kk[1], acc);
+        acc = fmaf(q[d + 2], kk[2], acc);
+        acc = fmaf(q[d + 3], kk[3], acc);
+      }
+      // The row's two halves (addition commutes: both lanes hold the same bits).
+      s[j] = acc + __shfl_xor(acc, 1) + bias[j];
+      mt = fmaxf(mt, s[j]);
+    }
+    const float mn = fmaxf(m, mt);
+    if (mn != kNegInf) {
+      const float alpha = m == kNegInf ? 0.f : exp2f((m - mn) * a.c);
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) o[d] *= alpha;
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        const float p = exp2f((s[j] - mn) * a.c);
+        l += p;
+#pragma unroll
+        for (int d = 0; d < HD; d += 4) {
+          const f32x4 vv = ld4(&vs[j][half * HD + d]);
+          o[d] = fmaf(p, vv[0], o[d]);
+          o[d + 1] = fmaf(p, vv[1], o[d + 1]);
+          o[d + 2] = fmaf(p, vv[2], o[d + 2]);
+          o[d + 3] = fmaf(p, vv[3], o[d + 3]);
+        }
+      }
+      m = mn;
+    }
+  }
+
+  // l > 0: normal row; l == 0: no valid key (out 0, lse -inf); NaN: a NaN or
+  // +inf score reached the row (out and lse NaN).
+  if (!valid) return;
+  const float nan = __builtin_nanf("");
+  const float inv = l > 0.f ? 1.f / l : (l == 0.f ? 0.f : nan);
+  float* op = a.o + b * a.osb + h * a.osh + (int64_t)row * a.osl + half * HD;
+#pragma unroll
+  for (int d = 0; d < HD; d += 4) st4(op + d, f32x4{o[d] * inv, o[d + 1] * inv, o[d + 2] * inv, o[d + 3] * inv});
+  if (half == 0) a.lse[(int64_t)bh * a.Lq + row] = l > 0.f ? fmaf(m, a.scale, logf(l)) : (l == 0.f ? kNegInf : nan);
+}
+
+// Zeros to out and -inf to lse (no keys at all).
+__global__ void empty_f32_kernel(F32Args a) {
+  const int64_t n = (int64_t)a.B * a.Hq * a.Lq;
+  const int D = a.D;
+  for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r < n; r += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(r % a.Lq);
+    const int h = (int)((r / a.Lq) % a.Hq);
+    const int b = (int)(r / ((int64_t)a.Lq * a.Hq));
+    float* op = a.o + b * a.osb + h * a.osh + (int64_t)i * a.osl;
+    for (int d = 0; d < D; d += 4) st4(op + d, f32x4{0.f, 0.f, 0.f, 0.f});
+    a.lse[r] = kNegInf;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(256) void bwd_pre_f32_kernel(F32Args a) {
+  const int64_t n = (int64_t)a.B * a.Hq * a.Lq;
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const int i = (int)(r % a.Lq);
+  const int h = (int)((r / a.Lq) % a.Hq);
+  const int b = (int)(r / ((int64_t)a.Lq * a.Hq));
+  const float* dp = a.dout + b * a.dosb + h * a.dosh + (int64_t)i * a.dosl;
+  const float* op = a.out + b * a.oisb + h * a.oish + (int64_t)i * a.oisl;
+  float acc = 0.f;
+#pragma unroll
+  for (int d = 0; d < D; d += 4) {
+    const f32x4 x = ld4(dp + d), y = ld4(op + d);
+    acc = fmaf(x[0], y[0], fmaf(x[1], y[1], fmaf(x[2], y[2], fmaf(x[3], y[3], acc))));
+  }
+  a.ndelta[r] = -acc;
+  const float l = a.lse_in[r];
+  a.lse2[r] = l == kNegInf ? kPosInf : l * kLog2e;
+}
+
+// Sum over the four lanes of a group (lanes 4g .. 4g+3), the same bits in
+// each of them.
+__device__ __forceinline__ float sum4(float x) {
+  x += __shfl_xor(x, 1);
+  return x + __shfl_xor(x, 2);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
+  constexpr int QD = D / 4, KPB = 64, QT = 16;
+  __shared__ __attribute__((aligned(16))) float qs[QT][D];
+  __shared__ __attribute__((aligned(16))) float dos[QT][D];
+  __shared__ float l2s[QT], nds[QT];
+  const int tid = threadIdx.x, part = tid & 3;
+  const int nkb = (a.Lk + KPB - 1) / KPB;
+  const int kb = blockIdx.x % nkb, bhk = blockIdx.x / nkb;
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int group = a.Hq / a.Hkv;
+  const int key = kb * KPB + (tid >> 2);
+  const bool kin = key < a.Lk, kvalid = key_ok(a, b, key);
+  float k[QD], v[QD], dk[QD], dv[QD];
+  {
+    const float* kp = a.k + b * a.ksb + hk * a.ksh + (int64_t)key * a.ksl + part * QD;
+    const float* vp = a.v + b * a.vsb + hk * a.vsh + (int64_t)key * a.vsl + part * QD;
+#pragma unroll
+    for (int d = 0; d < QD; d += 4) {
+      const f32x4 x = kin ? ld4(kp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 y = kin ? ld4(vp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      k[d] = x[0], k[d + 1] = x[1], k[d + 2] = x[2], k[d + 3] = x[3];
+      v[d] = y[0], v[d + 1] = y[1], v[d + 2] = y[2], v[d + 3] = y[3];
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < QD; ++d) dk[d] = 0.f, dv[d] = 0.f;
+
+  for (int gi = 0; gi < group; ++gi) {
+    const int h = hk * group + gi;
+    const int64_t rbase = ((int64_t)b * a.Hq + h) * a.Lq;
+    const float* qb = a.q + b * a.qsb + h * a.qsh;
+    const float* db = a.dout + b * a.dosb + h * a.dosh;
+    for (int q0 = 0; q0 < a.Lq; q0 += QT) {
+      __syncthreads();  // the previous tile is consumed
+      for (int u = tid; u < QT * D / 4; u += 256) {
+        const int r = u / (D / 4), c4 = 4 * (u % (D / 4)), i = q0 + r;
+        const bool in = i < a.Lq;
+        st4(&qs[r][c4], in ? ld4(qb + (int64_t)i * a.qsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+        st4(&dos[r][c4], in ? ld4(db + (int64_t)i * a.dosl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+      }
+      if (tid < QT) {
+        const int i = q0 + tid;
+        l2s[tid] = i < a.Lq ? a.lse2[rbase + i] : kPosInf;  // rows past the end get P = 0
+        nds[tid] = i < a.Lq ? a.ndelta[rbase + i] : 0.f;
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int r = 0; r < QT; ++r) {
+        float s = 0.f, dp = 0.f;
+#pragma unroll
+        for (int d = 0; d < QD; d += 4) {
+          const f32x4 x = ld4(&qs[r][part * QD + d]);
+          const f32x4 y = ld4(&dos[r][part * QD + d]);
+          s = fmaf(k[d], x[0], fmaf(k[d + 1], x[1], fmaf(k[d + 2], x[2], fmaf(k[d + 3], x[3], s))));
+          dp = fmaf(v[d], y[0], fmaf(v[d + 1], y[1], fmaf(v[d + 2], y[2], fmaf(v[d + 3], y[3], dp))));
+        }
+        s = sum4(s);
+        dp = sum4(dp);
+        const float p = kvalid ? exp2f(s * a.c - l2s[r]) : 0.f;
+        const float ds = p * (dp + nds[r]);
+#pragma unroll
+        for (int d = 0; d < QD; d += 4) {
+          const f32x4 x = ld4(&qs[r][part * QD + d]);
+          const f32x4 y = ld4(&dos[r][part * QD + d]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            dv[d + e] = fmaf(p, y[e], dv[d + e]);
+            dk[d + e] = fmaf(ds, x[e], dk[d + e]);
+          }
+        }
+      }
+    }
+  }
+  if (!kin) return;
+  // Masked keys: exactly zero (their P is 0; a non-finite dO or V elsewhere
+  // in the row must not reach them through 0 * inf).
+  float* kp = a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl + part * QD;
+  float* vp = a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl + part * QD;
+#pragma unroll
+  for (int d = 0; d < QD; d += 4) {
+    st4(kp + d, kvalid ? f32x4{dk[d] * a.scale, dk[d + 1] * a.scale, dk[d + 2] * a.scale, dk[d + 3] * a.scale}
+                       : f32x4{0.f, 0.f, 0.f, 0.f});
+    st4(vp + d, kvalid ? f32x4{dv[d], dv[d + 1], dv[d + 2], dv[d + 3]} : f32x4{0.f, 0.f, 0.f, 0.f});
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void bwd_dq_f32_kernel(F32Args a) {
+  constexpr int QD = D / 4, RPB = 64, KT = 32;
+  __shared__ __attribute__((aligned(16))) float ks[KT][D];
+  __shared__ __attribute__((aligned(16))) float vs[KT][D];
+  __shared__ int kok[KT];
+  const int tid = threadIdx.x, part = tid & 3;
+  const int nqb = (a.Lq + RPB - 1) / RPB;
+  const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
+  const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
+  const int row = qb * RPB + (tid >> 2);
+  const bool valid = row < a.Lq;
+  float q[QD], g[QD], dq[QD];
+  {
+    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl + part * QD;
+    const float* dp = a.dout + b * a.dosb + h * a.dosh + (int64_t)row * a.dosl + part * QD;
+#pragma unroll
+    for (int d = 0; d < QD; d += 4) {
+      const f32x4 x = valid ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 y = valid ? ld4(dp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      q[d] = x[0], q[d + 1] = x[1], q[d + 2] = x[2], q[d + 3] = x[3];
+      g[d] = y[0], g[d + 1] = y[1], g[d + 2] = y[2], g[d + 3] = y[3];
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < QD; ++d) dq[d] = 0.f;
+  const int64_t r = (int64_t)bh * a.Lq + row;
+  const float l2 = valid ? a.lse2[r] : kPosInf;
+  const float nd = valid ? a.ndelta[r] : 0.f;
+  const float* kb = a.k + b * a.ksb + hk * a.ksh;
+  const float* vb = a.v + b * a.vsb + hk * a.vsh;
+
+  for (int k0 = 0; k0 < a.Lk; k0 += KT) {
+    __syncthreads();
+    for (int u = tid; u < KT * D / 4; u += 256) {
+      const int j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = k0 + j;
+      const bool in = key < a.Lk;
+      st4(&ks[j][c4], in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+      st4(&vs[j][c4], in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+    }
+    if (tid < KT) kok[tid] = key_ok(a, b, k0 + tid) ? 1 : 0;
+    __syncthreads();
+    for (int j = 0; j < KT; ++j) {
+      if (!kok[j]) continue;  // the same for every lane: masked keys add nothing
+      float s = 0.f, dp = 0.f;
+#pragma unroll
+      for (int d = 0; d < QD; d += 4) {
+        const f32x4 x = ld4(&ks[j][part * QD + d]);
+        const f32x4 y = ld4(&vs[j][part * QD + d]);
+        s = fmaf(q[d], x[0], fmaf(q[d + 1], x[1], fmaf(q[d + 2], x[2], fmaf(q[d + 3], x[3], s))));
+        dp = fmaf(g[d], y[0], fmaf(g[d + 1], y[1], fmaf(g[d + 2], y[2], fmaf(g[d + 3], y[3], dp))));
+      }
+      s = sum4(s);
+      dp = sum4(dp);
+      const float p = exp2f(s * a.c - l2);
+      const float ds = p * (dp + nd);
+#pragma unroll
+      for (int d = 0; d < QD; d += 4) {
+        const f32x4 x = ld4(&ks[j][part * QD + d]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dq[d + e] = fmaf(ds, x[e], dq[d + e]);
+      }
+    }
+  }
+  if (!valid) return;
+  float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)row * a.dqsl + part * QD;
+#pragma unroll
+  for (int d = 0; d < QD; d += 4)
+    st4(op + d, f32x4{dq[d] * a.scale, dq[d + 1] * a.scale, dq[d + 2] * a.scale, dq[d + 3] * a.scale});
+}
+
+// Zeros over a (B, H, L, D) fp32 tensor (gradients of an empty side).
+__global__ void zero_f32_kernel(float* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D) {
+  const int64_t n = (int64_t)B * H * L * (D / 4);
+  for (int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; u < n; u += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(u % (D / 4));
+    const int64_t rw = u / (D / 4);
+    const int i = (int)(rw % L);
+    const int h = (int)((rw / L) % H);
+    const int b = (int)(rw / ((int64_t)L * H));
+    st4(x + b * sb + h * sh + (int64_t)i * sl + 4 * c, f32x4{0.f, 0.f, 0.f, 0.f});
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rotation of fp32 tensors: channels 4c .. 4c+3 of a row are pairs 2c, 2c+1;
+// (e, o) -> (e*cos - o*sin, e*sin + o*cos), or the transpose with `inverse`,
+// each product and sum rounded on its own as the reference's fp32 torch ops
+// round them.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rope_apply_f32_kernel(const float* __restrict__ x, int64_t xsb, int64_t xsh,
+                                                             int64_t xsl, int B, int H, int L, int D,
+                                                             const float* __restrict__ ct,
+                                                             const float* __restrict__ st, int64_t tsb, int inverse,
+                                                             float* __restrict__ out, int64_t osb, int64_t osh,
+                                                             int64_t osl) {
+#pragma clang fp contract(off)
+  const int cpr = D / 4;
+  const int64_t n = (int64_t)B * H * L * cpr;
+  for (int64_t u = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; u < n; u += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(u % cpr);
+    const int64_t rw = u / cpr;
+    const int i = (int)(rw % L);
+    const int h = (int)((rw / L) % H);
+    const int b = (int)(rw / ((int64_t)L * H));
+    const f32x4 v = ld4(x + b * xsb + h * xsh + (int64_t)i * xsl + 4 * c);
+    const int64_t t = b * tsb + (int64_t)i * (D / 2) + 2 * c;
+    f32x4 r;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const float e = v[2 * p], od = v[2 * p + 1], cs = ct[t + p], sn = st[t + p];
+      const float ec = e * cs, os = od * sn, es = e * sn, oc = od * cs;
+      if (!inverse) {
+        r[2 * p] = ec - os;
+        r[2 * p + 1] = es + oc;
+      } else {
+        r[2 * p] = ec + os;
+        r[2 * p + 1] = oc - es;
+      }
+    }
+    st4(out + b * osb + h * osh + (int64_t)i * osl + 4 * c, r);
+  }
+}
+
+int grid_of(int64_t n, int per = 256) {
+  const int64_t g = (n + per - 1) / per;
+  return (int)(g < 1 ? 1 : (g > 65535 ? 65535 : g));
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool str4(const int64_t* s) { return s && s[0] % 4 == 0 && s[1] % 4 == 0 && s[2] % 4 == 0; }
+
+int check_f32_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, int32_t D) {
+  if (B < 0 || Hq < 0 || Hkv < 0 || Lq < 0 || Lk < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (D != 64 && D != 128) return AVATTN_ERR_HEAD_DIM;
+  if (Hkv == 0 || Hq == 0) return (B == 0) ? AVATTN_OK : AVATTN_ERR_GQA;
+  if (Hq % Hkv != 0) return AVATTN_ERR_GQA;
+  // Grids: B*Hq*ceil(Lq/64) and B*Hkv*ceil(Lk/64) workgroups; row indices
+  // (b*Hq + h)*Lq + i in 64 bits.
+  const int64_t lim = 2147483647;
+  if ((int64_t)B * Hq * (((int64_t)Lq + 63) / 64) > lim || (int64_t)B * Hkv * (((int64_t)Lk + 63) / 64) > lim)
+    return AVATTN_ERR_TOO_LARGE;
+  if ((int64_t)B * Hq * Lq > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
+  return AVATTN_OK;
+}
+
+size_t r256(size_t x) { return (x + 255) / 256 * 256; }
+
+template <int D>
+void launch_fwd_f32(const F32Args& a, hipStream_t s) {
+  const int nqb = (a.Lq + 127) / 128;
+  hipLaunchKernelGGL(fwd_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
+}
+
+template <int D>
+void launch_bwd_f32(const F32Args& a, hipStream_t s) {
+  const int64_t rows = (int64_t)a.B * a.Hq * a.Lq;
+  hipLaunchKernelGGL(bwd_pre_f32_kernel<D>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a);
+  const int nkb = (a.Lk + 63) / 64;
+  hipLaunchKernelGGL(bwd_dkdv_f32_kernel<D>, dim3((unsigned)(nkb * a.B * a.Hkv)), dim3(256), 0, s, a);
+  const int nqb = (a.Lq + 63) / 64;
+  hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
+}
+
+}  // namespace
+}  // namespace avattn
+
+using namespace avattn;
+
+extern "C" {
+
+int avattn_fwd_f32(const float* q, const float* k, const float* v, const int64_t* q_strides,
+                   const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
+                   int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                   int64_t key_mask_batch_stride, float scale, float* out, const int64_t* out_strides, float* lse,
+                   avattn_stream_t stream) {
+  const int st = check_f32_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  if (!q_strides || !k_strides || !v_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * heads_q * len_q == 0) return AVATTN_OK;
+  if (!q || !out || !lse) return AVATTN_ERR_NULL_POINTER;
+  if (!al16(q) || !al16(out) || !str4(q_strides) || !str4(out_strides)) return AVATTN_ERR_LAYOUT;
+  if (!(scale > 0.f) || !isfinite(scale)) return AVATTN_ERR_ARGUMENT;
+  F32Args a{};
+  a.q = q, a.k = k, a.v = v;
+  a.qsb = q_strides[0], a.qsh = q_strides[1], a.qsl = q_strides[2];
+  a.ksb = k_strides[0], a.ksh = k_strides[1], a.ksl = k_strides[2];
+  a.vsb = v_strides[0], a.vsh = v_strides[1], a.vsl = v_strides[2];
+  a.B = batch, a.Hq = heads_q, a.Hkv = heads_kv, a.Lq = len_q, a.Lk = len_k, a.D = head_dim;
+  a.mask = key_mask, a.msb = key_mask_batch_stride;
+  a.o = out, a.osb = out_strides[0], a.osh = out_strides[1], a.osl = out_strides[2];
+  a.lse = lse;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (len_k == 0) {  // src/avgen/models/attention.py:261-262: zeros
+    hipLaunchKernelGGL(empty_f32_kernel, dim3(grid_of((int64_t)batch * heads_q * len_q)), dim3(256), 0, s, a);
+    return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+  }
+  if (!k || !v) return AVATTN_ERR_NULL_POINTER;
+  if (!al16(k) || !al16(v) || !str4(k_strides) || !str4(v_strides)) return AVATTN_ERR_LAYOUT;
+  if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
+  a.scale = scale, a.c = scale * kLog2e;
+  if (head_dim == 128)
+    launch_fwd_f32<128>(a, s);
+  else
+    launch_fwd_f32<64>(a, s);
+  return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+}
+
+size_t avattn_bwd_f32_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q) {
+  if (batch <= 0 || heads_q <= 0 || len_q <= 0) return 0;
+  return 2 * r256((size_t)batch * heads_q * len_q * sizeof(float));
+}
+
+int avattn_bwd_f32(const float* dout, const float* q, const float* k, const float* v, const float* out,
+                   const float* lse, const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
+                   int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                   int64_t key_mask_batch_stride, float scale, float* dq, const int64_t* dq_strides, float* dk,
+                   const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* workspace,
+                   size_t workspace_bytes, avattn_stream_t stream) {
+  const int st = check_f32_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  if (!dout_strides || !q_strides || !k_strides || !v_strides || !out_strides || !dq_strides || !dk_strides ||
+      !dv_strides)
+    return AVATTN_ERR_NULL_POINTER;
+  if (!(scale > 0.f) || !isfinite(scale)) return AVATTN_ERR_ARGUMENT;
+  const bool qside = (int64_t)batch * heads_q * len_q > 0, kside = (int64_t)batch * heads_kv * len_k > 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (qside && !kside) {  // no keys: dq = 0
+    if (!dq) return AVATTN_ERR_NULL_POINTER;
+    if (!al16(dq) || !str4(dq_strides)) return AVATTN_ERR_LAYOUT;
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_of((int64_t)batch * heads_q * len_q * (head_dim / 4))), dim3(256),
+                       0, s, dq, dq_strides[0], dq_strides[1], dq_strides[2], batch, heads_q, len_q, head_dim);
+    return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+  }
+  if (kside && !qside) {  // no queries: dk = dv = 0
+    if (!dk || !dv) return AVATTN_ERR_NULL_POINTER;
+    if (!al16(dk) || !al16(dv) || !str4(dk_strides) || !str4(dv_strides)) return AVATTN_ERR_LAYOUT;
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_of((int64_t)batch * heads_kv * len_k * (head_dim / 4))), dim3(256),
+                       0, s, dk, dk_strides[0], dk_strides[1], dk_strides[2], batch, heads_kv, len_k, head_dim);
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_of((int64_t)batch * heads_kv * len_k * (head_dim / 4))), dim3(256),
+                       0, s, dv, dv_strides[0], dv_strides[1], dv_strides[2], batch, heads_kv, len_k, head_dim);
+    return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+  }
+  if (!qside) return AVATTN_OK;
+  if (!dout || !q || !k || !v || !out || !lse || !dq || !dk || !dv) return AVATTN_ERR_NULL_POINTER;
+  for (const void* p : {(const void*)dout, (const void*)q, (const void*)k, (const void*)v, (const void*)out,
+                        (const void*)dq, (const void*)dk, (const void*)dv})
+    if (!al16(p)) return AVATTN_ERR_LAYOUT;
+  for (const int64_t* sp : {dout_strides, q_strides, k_strides, v_strides, out_strides, dq_strides, dk_strides,
+                            dv_strides})
+    if (!str4(sp)) return AVATTN_ERR_LAYOUT;
+  if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
+  const size_t need = avattn_bwd_f32_workspace_size(batch, heads_q, len_q);
+  if (!workspace || workspace_bytes < need) return AVATTN_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u) return AVATTN_ERR_LAYOUT;
+  F32Args a{};
+  a.q = q, a.k = k, a.v = v;
+  a.qsb = q_strides[0], a.qsh = q_strides[1], a.qsl = q_strides[2];
+  a.ksb = k_strides[0], a.ksh = k_strides[1], a.ksl = k_strides[2];
+  a.vsb = v_strides[0], a.vsh = v_strides[1], a.vsl = v_strides[2];
+  a.B = batch, a.Hq = heads_q, a.Hkv = heads_kv, a.Lq = len_q, a.Lk = len_k, a.D = head_dim;
+  a.mask = key_mask, a.msb = key_mask_batch_stride;
+  a.scale = scale, a.c = scale * kLog2e;
+  a.dout = dout, a.out = out, a.lse_in = lse;
+  a.dosb = dout_strides[0], a.dosh = dout_strides[1], a.dosl = dout_strides[2];
+  a.oisb = out_strides[0], a.oish = out_strides[1], a.oisl = out_strides[2];
+  a.dq = dq, a.dqsb = dq_strides[0], a.dqsh = dq_strides[1], a.dqsl = dq_strides[2];
+  a.dk = dk, a.dksb = dk_strides[0], a.dksh = dk_strides[1], a.dksl = dk_strides[2];
+  a.dv = dv, a.dvsb = dv_strides[0], a.dvsh = dv_strides[1], a.dvsl = dv_strides[2];
+  a.lse2 = static_cast<float*>(workspace);
+  a.ndelta = a.lse2 + need / 2 / sizeof(float);
+  if (head_dim == 128)
+    launch_bwd_f32<128>(a, s);
+  else
+    launch_bwd_f32<64>(a, s);
+  return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+}
+
+int avattn_rope_apply_f32(const float* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,
+                          int32_t head_dim, const float* cos_tab, const float* sin_tab, int64_t table_batch_stride,
+                          int32_t inverse, float* out, const int64_t* out_strides, avattn_stream_t stream) {
+  if (batch < 0 || heads < 0 || len < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (head_dim < 4 || head_dim > 128 || head_dim % 4 != 0) return AVATTN_ERR_HEAD_DIM;
+  if (!x_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * heads * len == 0) return AVATTN_OK;
+  if (!x || !out || !cos_tab || !sin_tab) return AVATTN_ERR_NULL_POINTER;
+  if (!al16(x) || !al16(out) || !str4(x_strides) || !str4(out_strides) || table_batch_stride < 0)
+    return AVATTN_ERR_LAYOUT;
+  if ((int64_t)batch * heads > 2147483647 || len > 2147483647) return AVATTN_ERR_TOO_LARGE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t n = (int64_t)batch * heads * len * (head_dim / 4);
+  hipLaunchKernelGGL(rope_apply_f32_kernel, dim3(grid_of(n)), dim3(256), 0, s, x, x_strides[0], x_strides[1],
+                     x_strides[2], batch, heads, len, head_dim, cos_tab, sin_tab, table_batch_stride,
+                     inverse ? 1 : 0, out, out_strides[0], out_strides[1], out_strides[2]);
+  return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -14,6 +14,11 @@ Ops (namespace ``avgen_amd``):
   the ring backward step (torch/.../_context_parallel/_attention.py:567-575).
 * ``rope_apply(x, cos, sin, inverse) -> x_rot`` — src/avgen/models/rope.py
   :297-338, differentiable.
+
+``flash_fwd``, ``flash_bwd`` and ``rope_apply`` take float32 tensors too
+(all of q, k, v and dout/out, or x), computed in fp32 by the library's fp32
+kernels (the reference's attention runs in the caller's dtype); every other
+op is bf16 only.
 * ``flash_fwd_fp8(q, k, v, key_mask, q_scale, k_scale, scale) -> (out, lse)``
   — forward with q k^T on e4m3 operands and per-head scales (no reference
   counterpart; the sampling-time fp8 variant of ``flash_fwd``), forward only.
@@ -93,11 +98,19 @@ def _require_gpu(name: str, *tensors: Optional[torch.Tensor]) -> None:
             )
 
 
-def _check_qkv(name: str, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+def _check_qkv(name: str, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, allow_f32: bool = False) -> None:
+    """Shapes and dtypes: bf16, or (``allow_f32``: the plain forward and
+    backward) float32 for all three."""
     for label, t in (("query", q), ("key", k), ("value", v)):
         if t.ndim != 4:
             raise ValueError(f"{name}: {label} must be (batch, heads, seq, head_dim); got {tuple(t.shape)}")
-        if t.dtype is not torch.bfloat16:
+    f32 = allow_f32 and q.dtype is torch.float32
+    want = torch.float32 if f32 else torch.bfloat16
+    for label, t in (("query", q), ("key", k), ("value", v)):
+        if t.dtype is not want:
+            if allow_f32:
+                raise TypeError(f"{name}: {label} must be bfloat16 or float32 like the query; got {t.dtype} "
+                                f"(query {q.dtype})")
             raise TypeError(f"{name}: {label} must be bfloat16; got {t.dtype}")
     if k.shape != v.shape:
         raise ValueError(f"{name}: key {tuple(k.shape)} and value {tuple(v.shape)} shapes differ")
@@ -161,8 +174,10 @@ def _check_tables(name: str, cos: torch.Tensor, sin: torch.Tensor, batch: int, l
 
 def _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale):
     name = "avgen_amd.flash_fwd"
-    _check_qkv(name, q, k, v)
+    _check_qkv(name, q, k, v, allow_f32=True)
     _require_gpu(name, q, k, v, key_mask, rope_cos, rope_sin)
+    if q.dtype is torch.float32:
+        return _fwd_f32_impl(name, q, k, v, key_mask, rope_cos, rope_sin, scale)
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
@@ -189,6 +204,73 @@ def _fwd_impl(q, k, v, key_mask, rope_cos, rope_sin, scale):
     )
     _lib.check(st, name)
     return out, lse
+
+
+def _f32_ready(t: torch.Tensor) -> torch.Tensor:
+    """float32 rows for the fp32 kernels: head_dim contiguous, 16-byte aligned
+    row starts (strides a multiple of 4 elements)."""
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+    ok = ok and all(s % 4 == 0 or n == 1 for s, n in zip(t.stride()[:3], t.shape[:3]))
+    return t if ok else t.contiguous()
+
+
+def _fwd_f32_impl(name, q, k, v, key_mask, rope_cos, rope_sin, scale):
+    """The float32 forward (``avattn_fwd_f32``); rotary tables rotate q first
+    (``avattn_rope_apply_f32``), the same result as rotating it before the
+    call."""
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if (rope_cos is None) != (rope_sin is None):
+        raise ValueError(f"{name}: pass both rotary tables or neither")
+    if rope_cos is not None:
+        q = _rope_apply_impl(q, rope_cos, rope_sin, False)
+    q, k, v = _f32_ready(q), _f32_ready(k), _f32_ready(v)
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    out = _f32_ready(torch.empty_like(q, memory_format=torch.preserve_format))
+    lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32)
+    st = _lib.load().avattn_fwd_f32(
+        _ptr(q), _ptr(k), _ptr(v), _strides3(q), _strides3(k), _strides3(v),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        float(scale),
+        _ptr(out), _strides3(out), _ptr(lse),
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return out, lse
+
+
+def _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale):
+    """The float32 backward (``avattn_bwd_f32``): new dq, dk, dv."""
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    for label, t in (("grad_out", dout), ("out", out)):
+        if t.shape != q.shape:
+            raise ValueError(f"{name}: {label} must have the query's shape {tuple(q.shape)}")
+        if t.dtype is not torch.float32:
+            raise TypeError(f"{name}: {label} must be float32 like the query; got {t.dtype}")
+    if lse.shape != (B, Hq, Lq) or lse.dtype is not torch.float32:
+        raise ValueError(f"{name}: logsumexp must be float32 (batch, heads, queries)")
+    dout, q, k, v, out = (_f32_ready(t) for t in (dout, q, k, v, out))
+    lse = lse.contiguous()
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    dq = _f32_ready(torch.empty_like(q))
+    dk = _f32_ready(torch.empty_like(k))
+    dv = _f32_ready(torch.empty_like(v))
+    lib = _lib.load()
+    ws = _workspace(lib.avattn_bwd_f32_workspace_size(B, Hq, Lq), q.device)
+    st = lib.avattn_bwd_f32(
+        _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
+        _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        float(scale),
+        _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
+        _ptr(ws), ws.numel(),
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return dq, dk, dv
 
 
 def _check_windows(name, lo, hi, B, Lq):
@@ -487,8 +569,13 @@ def _bwd_impl(dout, q, k, v, out, lse, key_mask, scale, dq=None, dk=None, dv=Non
     returned as None); _bwd_dq_staged_impl on that workspace computes dq.
     """
     name = "avgen_amd.flash_bwd"
-    _check_qkv(name, q, k, v)
+    _check_qkv(name, q, k, v, allow_f32=True)
     _require_gpu(name, dout, q, k, v, out, lse, key_mask)
+    if q.dtype is torch.float32:
+        if (dq is not None or dk is not None or dv is not None or workspace is not None or reuse_query_side
+                or dq_accumulate is not None or defer_dq):
+            raise TypeError(f"{name}: the ring-step options take bfloat16 tensors only")
+        return _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale)
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     if dout.shape != q.shape or out.shape != q.shape:
@@ -821,11 +908,20 @@ def _rope_apply_impl(x, cos, sin, inverse):
     name = "avgen_amd.rope_apply"
     if x.ndim != 4:
         raise ValueError(f"rotary input must be (batch, heads, length, head_dim); got {tuple(x.shape)}")
-    if x.dtype is not torch.bfloat16:
-        raise TypeError(f"{name}: input must be bfloat16; got {x.dtype}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{name}: input must be bfloat16 or float32; got {x.dtype}")
     B, H, L, D = x.shape
     cos, sin, tsb = _check_tables(name, cos, sin, B, L, D)
     _require_gpu(name, x, cos, sin)
+    if x.dtype is torch.float32:
+        x = _f32_ready(x)
+        out = _f32_ready(torch.empty_like(x, memory_format=torch.preserve_format))
+        st = _lib.load().avattn_rope_apply_f32(
+            _ptr(x), _strides3(x), B, H, L, D, _ptr(cos), _ptr(sin), tsb, 1 if inverse else 0,
+            _ptr(out), _strides3(out), _stream(x.device),
+        )
+        _lib.check(st, name)
+        return out
     x = _kernel_ready(x)
     out = _kernel_ready(torch.empty_like(x, memory_format=torch.preserve_format))
     st = _lib.load().avattn_rope_apply(

@@ -41,6 +41,10 @@
  *                       block-diagonal mask) as per-row key windows
  *   avattn_qk_norm_rope, src/avgen/models/layers.py:530-536 (q_norm/k_norm
  *   avattn_qk_norm_rope_bwd  then apply_rotary) and their autograd backward
+ *   avattn_fwd_f32,     the same interfaces as avattn_fwd / avattn_bwd /
+ *   avattn_bwd_f32,     avattn_rope_apply for float32 tensors (the
+ *   avattn_rope_apply_f32  reference's attention and rotation run in the
+ *                       caller's dtype)
  */
 #ifndef AVATTN_H
 #define AVATTN_H
@@ -616,6 +620,61 @@ int avattn_diag_dq_partials(float* acc, int32_t heads, int32_t key_blocks,
                             int32_t query_tiles, int32_t tiles_per_block,
                             int32_t head_dim, int32_t atomic,
                             avattn_stream_t stream);
+
+/*
+ * float32 attention: the same contract as avattn_fwd / avattn_bwd /
+ * avattn_rope_apply with every tensor (q, k, v, out, dout, dq, dk, dv, x)
+ * float32 instead of bf16 and every product computed in fp32, for callers
+ * whose tensors are float32 — the reference's attention() runs in the
+ * caller's dtype (src/avgen/models/attention.py:227-273 ->
+ * F.scaled_dot_product_attention), its rotation in fp32
+ * (src/avgen/models/rope.py:332-338), and BASELINE config c1 is float32.
+ * Strides are in elements, multiples of 4 (16-byte aligned rows); head_dim
+ * 64 or 128 (rotation: any multiple of 4 up to 128).  No rotation is fused
+ * into the attention calls: rotate with avattn_rope_apply_f32 first.
+ * lse, the key mask and the row states (no valid key: out 0, lse -inf; a
+ * NaN or +inf score: NaN) are as for avattn_fwd.  The backward needs
+ * avattn_bwd_f32_workspace_size() bytes of workspace (256-byte aligned:
+ * the row statistics), uses no atomics and is bitwise reproducible; a
+ * masked key's dk and dv are exactly 0.  Rotation: each product and sum
+ * rounded on its own, no final rounding (the output is fp32), so it equals
+ * torch's fp32 ops bit for bit.
+ */
+int avattn_fwd_f32(const float* q, const float* k, const float* v,
+                   const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides,
+                   int32_t batch, int32_t heads_q, int32_t heads_kv,
+                   int32_t len_q, int32_t len_k, int32_t head_dim,
+                   const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                   float scale,
+                   float* out, const int64_t* out_strides,
+                   float* lse,
+                   avattn_stream_t stream);
+
+size_t avattn_bwd_f32_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q);
+
+int avattn_bwd_f32(const float* dout, const float* q, const float* k, const float* v,
+                   const float* out, const float* lse,
+                   const int64_t* dout_strides, const int64_t* q_strides,
+                   const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* out_strides,
+                   int32_t batch, int32_t heads_q, int32_t heads_kv,
+                   int32_t len_q, int32_t len_k, int32_t head_dim,
+                   const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                   float scale,
+                   float* dq, const int64_t* dq_strides,
+                   float* dk, const int64_t* dk_strides,
+                   float* dv, const int64_t* dv_strides,
+                   void* workspace, size_t workspace_bytes,
+                   avattn_stream_t stream);
+
+int avattn_rope_apply_f32(const float* x, const int64_t* x_strides,
+                          int32_t batch, int32_t heads, int32_t len,
+                          int32_t head_dim,
+                          const float* cos_tab, const float* sin_tab,
+                          int64_t table_batch_stride, int32_t inverse,
+                          float* out, const int64_t* out_strides,
+                          avattn_stream_t stream);
 
 #ifdef __cplusplus
 }

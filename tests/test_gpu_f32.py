@@ -1,0 +1,217 @@
+"""GPU parity of the float32 path (avattn_fwd_f32 / avattn_bwd_f32 /
+avattn_rope_apply_f32 through the C ABI) against the float64 oracle.
+
+The reference's attention runs in the caller's dtype
+(src/avgen/models/attention.py:227-273 -> F.scaled_dot_product_attention),
+so float32 tensors are computed with float32 operands and products.  The bar
+is float32's, about 500x tighter than the bf16 one: output 2e-5 of max(1,
+|out|), LSE 2e-5 of max(1, |lse|), gradients 1e-4 of their largest
+magnitude; masks and the row states (no valid key: out 0, LSE -inf) exact;
+the rotation equal bit for bit to torch's float32 ops on the reference's
+formula (src/avgen/models/rope.py:332-338).  BASELINE config c1 (float32,
+1x4x1024x64 with its 3D RoPE) runs here without a bf16 cast.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as R
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL, LSE_TOL, GRAD_REL_TOL = 2e-5, 2e-5, 1e-4
+
+
+@pytest.fixture(scope="module")
+def amd():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm GPU")
+    import avgen_amd
+
+    return avgen_amd
+
+
+def _randn(shape, seed, scale=1.0):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return torch.randn(shape, generator=g) * scale
+
+
+def _f64(t):
+    return t.detach().cpu().numpy().astype(np.float64)
+
+
+def _check_fwd(o, l, ro, rl):
+    assert np.array_equal(np.isnan(o), np.isnan(ro))
+    fin = np.isfinite(rl)
+    assert np.array_equal(np.isneginf(l), np.isneginf(rl))
+    ok = ~np.isnan(ro)
+    assert np.abs(o[ok] - ro[ok]).max(initial=0.0) <= OUT_TOL * max(1.0, np.abs(ro[ok]).max(initial=0.0))
+    assert (np.abs(l[fin] - rl[fin]) <= LSE_TOL * np.maximum(1.0, np.abs(rl[fin]))).all()
+
+
+CASES = [
+    # B, Hq, Hkv, Lq, Lk, D, masked
+    (1, 2, 2, 128, 128, 128, False),
+    (2, 4, 2, 200, 333, 128, True),
+    (1, 3, 1, 77, 1000, 64, True),
+    (2, 2, 2, 1, 5, 64, False),
+    (1, 2, 1, 513, 31, 128, True),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,masked", CASES)
+def test_f32_forward_backward_match_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
+    print(f"f32 case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked}", flush=True)
+    q, k, v, do = _randn((B, Hq, Lq, D), 1), _randn((B, Hkv, Lk, D), 2), _randn((B, Hkv, Lk, D), 3), _randn(
+        (B, Hq, Lq, D), 4)
+    mask = None
+    if masked:
+        g = torch.Generator()
+        g.manual_seed(5)
+        mask = torch.rand((B, Lk), generator=g) < 0.7
+        mask[0, 0] = True
+        if B > 1:
+            mask[-1] = False  # a batch row without valid keys
+    mk = None if mask is None else mask.cuda()
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), mk, None, None, D ** -0.5)
+    assert out.dtype is torch.float32
+    km = None if mask is None else mask.numpy()
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), km)
+    o, l = _f64(out), _f64(lse)
+    _check_fwd(o, l, ro, rl)
+    if masked and B > 1:
+        assert np.all(o[-1] == 0) and np.all(np.isneginf(l[-1]))
+    dq, dk, dv = amd.ops.flash_bwd(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, mk, D ** -0.5)
+    ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), o, l, km)
+    for name, got, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+        assert got.dtype is torch.float32
+        err = np.abs(_f64(got) - r).max()
+        print(f"  {name}: max err {err:.3e} (ref max {np.abs(r).max():.3e})", flush=True)
+        assert err <= GRAD_REL_TOL * max(np.abs(r).max(), 1e-6), name
+    if mask is not None:
+        gone = np.broadcast_to(~mask.numpy()[:, None, :, None], dk.shape)
+        assert np.all(_f64(dk)[gone] == 0) and np.all(_f64(dv)[gone] == 0)
+
+
+def test_f32_rotation_bit_exact(amd):
+    """rope_apply on float32 equals torch's float32 ops on the reference's
+    formula bit for bit, forward and transpose; its autograd is the
+    transpose."""
+    B, H, L, D = 2, 3, 257, 128
+    coords = torch.stack(torch.meshgrid(torch.arange(1.0) / 8, torch.arange(257.0) * 2, torch.arange(1.0),
+                                        indexing="ij"), -1).reshape(1, L, 3).expand(B, -1, -1).contiguous()
+    tables = amd.rope.build_rotary_tables(coords.cuda(), head_dim=D)
+    x = _randn((B, H, L, D), 7, 3.0).cuda()
+    c, s = tables.cos, tables.sin
+    e, o = x[..., 0::2], x[..., 1::2]
+    ref = torch.stack((e * c - o * s, e * s + o * c), -1).flatten(-2)
+    ref_t = torch.stack((e * c + o * s, o * c - e * s), -1).flatten(-2)
+    got = amd.rope.apply_rotary(x, tables)
+    assert got.dtype is torch.float32
+    assert torch.equal(got, ref)
+    assert torch.equal(amd.ops.rope_apply(x, c, s, True), ref_t)
+    xg = x.clone().requires_grad_(True)
+    amd.rope.apply_rotary(xg, tables).backward(x)
+    assert torch.equal(xg.grad, ref_t)
+
+
+def _coords(frames, height, width, batch):
+    t = torch.arange(frames, dtype=torch.float32) / 8.0
+    r = torch.arange(height, dtype=torch.float32) * 2.0
+    c = torch.arange(width, dtype=torch.float32) * 2.0
+    g = torch.stack(torch.meshgrid(t, r, c, indexing="ij"), -1).reshape(1, -1, 3)
+    return g.expand(batch, -1, -1).contiguous()
+
+
+def test_c1_config_in_float32(amd):
+    """BASELINE config c1 as stated: float32 q/k/v (B=1, 4 heads, head_dim 64,
+    a 4x16x16 latent = 1,024 tokens, N(0,1)), the 3D RoPE with theta 1e4 and
+    the head_dim-64 split (12, 10, 10), no mask, forward out + LSE, against
+    float64 attention on the float64 rotation of the same float32 inputs."""
+    B, H, D, grid = 1, 4, 64, (4, 16, 16)
+    L = grid[0] * grid[1] * grid[2]
+    g = torch.Generator()
+    g.manual_seed(0)
+    q32, k32, v32 = (torch.randn((B, H, L, D), generator=g) for _ in range(3))
+    coords = _coords(*grid, B)
+    tables = amd.rope.build_rotary_tables(coords.cuda(), head_dim=D)
+    out, lse = amd.ops.flash_fwd(q32.cuda(), amd.rope.apply_rotary(k32.cuda(), tables), v32.cuda(), None,
+                                 tables.cos, tables.sin, D ** -0.5)
+    c64, s64 = R.rotary_tables_f64(coords.numpy(), D)
+
+    def rot64(x):
+        x = x.numpy().astype(np.float64)
+        e, od = x[..., 0::2], x[..., 1::2]
+        y = np.empty_like(x)
+        y[..., 0::2] = e * c64 - od * s64
+        y[..., 1::2] = e * s64 + od * c64
+        return y
+
+    fo, fl = R.attention_f64(rot64(q32), rot64(k32), v32.numpy().astype(np.float64))
+    o, l = _f64(out), _f64(lse)
+    print(f"c1 float32: out err {np.abs(o - fo).max():.2e}, lse err {np.abs(l - fl).max():.2e}", flush=True)
+    _check_fwd(o, l, fo, fl)
+
+
+def test_f32_attention_dropin_autograd(amd):
+    """attention() and rotary_attention() with float32 tensors through
+    autograd, against float64 gradients."""
+    B, H, L, D = 1, 2, 300, 128
+    q, k, v, do = (_randn((B, H, L, D), s) for s in (11, 12, 13, 14))
+    mask = torch.ones(B, L, dtype=torch.bool)
+    mask[:, 250:] = False
+    qg, kg, vg = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    out = amd.attention.attention(qg, kg, vg, attn_mask=amd.attention.key_padding_mask(mask.cuda()))
+    out.backward(do.cuda())
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), mask.numpy())
+    assert np.abs(_f64(out) - ro).max() <= OUT_TOL * max(1.0, np.abs(ro).max())
+    ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, mask.numpy())
+    for got, r in zip((qg.grad, kg.grad, vg.grad), ref):
+        assert np.abs(_f64(got) - r).max() <= GRAD_REL_TOL * np.abs(r).max()
+    # the rotary drop-in: same as rotating first (fp32 rotation is exact torch ops)
+    coords = _coords(3, 10, 10, B)
+    tables = amd.rope.build_rotary_tables(coords.cuda(), head_dim=D)
+    qa, ka, va = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    oa = amd.attention.rotary_attention(qa, ka, va, tables)
+    oa.backward(do.cuda())
+    qb, kb, vb = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    ob = amd.attention.attention(amd.rope.apply_rotary(qb, tables), amd.rope.apply_rotary(kb, tables), vb)
+    ob.backward(do.cuda())
+    assert torch.equal(oa, ob)
+    for a_, b_ in ((qa.grad, qb.grad), (ka.grad, kb.grad), (va.grad, vb.grad)):
+        assert torch.equal(a_, b_)
+
+
+def test_f32_edges(amd):
+    """Zero-length sequences, a NaN key reaching every row of its head (as
+    the float64 math gives), and run-to-run bits."""
+    q = _randn((1, 2, 40, 64), 20).cuda()
+    k0 = torch.empty((1, 2, 0, 64), device="cuda")
+    out, lse = amd.ops.flash_fwd(q, k0, k0, None, None, None, 0.125)
+    assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
+    assert torch.all(amd.attention.attention(q, k0, k0) == 0)
+    dq, dk, dv = amd.ops.flash_bwd(q, q, k0, k0, out, lse, None, 0.125)
+    assert torch.all(dq == 0) and dk.numel() == 0
+    k = _randn((1, 2, 70, 64), 21).cuda()
+    k[0, 1, 33, 5] = float("nan")
+    out, lse = amd.ops.flash_fwd(q, k, k, None, None, None, 0.125)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(k), None, 0.125)
+    _check_fwd(_f64(out), _f64(lse), ro, rl)
+    assert torch.isnan(out[0, 1]).all() and not torch.isnan(out[0, 0]).any()
+    k = _randn((2, 1, 700, 128), 22).cuda()
+    q = _randn((2, 4, 300, 128), 23).cuda()
+    do = _randn((2, 4, 300, 128), 24).cuda()
+    m = torch.rand((2, 700), device="cuda") < 0.9
+
+    def run():
+        o, l = amd.ops.flash_fwd(q, k, k, m, None, None, 0.09)
+        return (o, l, *amd.ops.flash_bwd(do, q, k, k, o, l, m, 0.09))
+
+    first = run()
+    torch.randn(1 << 20, device="cuda").sum().item()
+    for a_, b_ in zip(first, run()):
+        assert torch.equal(a_, b_)

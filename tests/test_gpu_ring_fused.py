@@ -157,9 +157,10 @@ def test_c1_cpu_smoke_config(amd):
     head_dim 64, a 4x16x16 latent (1,024 tokens), N(0,1) inputs, 3D RoPE
     theta 1e4 with the head_dim-64 split rope_axis_pairs(64) = (12, 10, 10)
     (the config's 22/21/21 is the head_dim-128 split), no mask, forward out +
-    LSE.  The config's tensors are float32; the HIP kernels take bf16 only
-    (a float32 tensor raises TypeError), so q/k/v are cast to bf16 first and
-    the kernel's own error is bounded separately from the cast's.  (1)
+    LSE.  The config's tensors are float32 (run as such on the fp32 path by
+    tests/test_gpu_f32.py::test_c1_config_in_float32); here they are cast to
+    bf16 for the bf16 kernels, whose own error is bounded separately from
+    the cast's.  (1)
     Against the float64 oracle of the bf16-cast inputs, the kernel's
     arithmetic alone: bf16 probabilities into the P V product and one bf16
     rounding of the output (half an ulp: 3.9e-3 for |out| in [1, 2)), an fp32
