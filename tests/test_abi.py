@@ -407,3 +407,87 @@ def test_fp8_absmax_validation_paths(lib):
     assert f(16, s, 1, 2, 4, 128, 18, None) == _lib.ERR_LAYOUT
     assert f(16, s, 1, 1 << 17, 4, 128, 16, None) == _lib.ERR_TOO_LARGE
     assert f(16, s, 1, 0, 4, 128, 16, None) == _lib.OK
+
+
+def _fwd_f32(lib, **over):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+    args = dict(q=16, k=16, v=16, qs=s, ks=s, vs=s, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
+                scale=0.125, out=16, os=s, lse=16, stream=None)
+    args.update(over)
+    return lib.avattn_fwd_f32(args["q"], args["k"], args["v"], args["qs"], args["ks"], args["vs"], args["B"],
+                              args["Hq"], args["Hkv"], args["Lq"], args["Lk"], args["D"], args["mask"], args["msb"],
+                              args["scale"], args["out"], args["os"], args["lse"], args["stream"])
+
+
+@cpu_only
+def test_fwd_f32_validation_paths(lib):
+    assert _fwd_f32(lib, D=96) == _lib.ERR_HEAD_DIM
+    assert _fwd_f32(lib, Hq=3, Hkv=2) == _lib.ERR_GQA
+    assert _fwd_f32(lib, Lq=-1) == _lib.ERR_BAD_SHAPE
+    assert _fwd_f32(lib, qs=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_f32(lib, q=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_f32(lib, lse=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_f32(lib, q=8) == _lib.ERR_LAYOUT
+    assert _fwd_f32(lib, os=_lib.i64_array([1024 * 128, 1024 * 128, 130])) == _lib.ERR_LAYOUT
+    assert _fwd_f32(lib, scale=0.0) == _lib.ERR_ARGUMENT
+    assert _fwd_f32(lib, scale=float("inf")) == _lib.ERR_ARGUMENT
+    assert _fwd_f32(lib, k=None) == _lib.ERR_NULL_POINTER
+    assert _fwd_f32(lib, v=24) == _lib.ERR_LAYOUT
+    assert _fwd_f32(lib, mask=16, msb=2) == _lib.ERR_ARGUMENT
+    # nothing to compute: success without a launch
+    assert _fwd_f32(lib, Lq=0) == _lib.OK
+    assert _fwd_f32(lib, B=0) == _lib.OK
+
+
+def _bwd_f32(lib, **over):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+    args = dict(do=16, q=16, k=16, v=16, o=16, lse=16, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0,
+                scale=0.125, dq=16, dk=16, dv=16, ws=256, wsb=1 << 20, stream=None)
+    args.update(over)
+    st = {k_: args.get(k_ + "s", s) for k_ in ("do", "q", "k", "v", "o", "dq", "dk", "dv")}
+    return lib.avattn_bwd_f32(args["do"], args["q"], args["k"], args["v"], args["o"], args["lse"],
+                              st["do"], st["q"], st["k"], st["v"], st["o"],
+                              args["B"], args["Hq"], args["Hkv"], args["Lq"], args["Lk"], args["D"],
+                              args["mask"], args["msb"], args["scale"],
+                              args["dq"], st["dq"], args["dk"], st["dk"], args["dv"], st["dv"],
+                              args["ws"], args["wsb"], args["stream"])
+
+
+@cpu_only
+def test_bwd_f32_validation_paths(lib):
+    assert lib.avattn_bwd_f32_workspace_size(2, 40, 18900) == 2 * _round256(2 * 40 * 18900 * 4)
+    assert lib.avattn_bwd_f32_workspace_size(0, 4, 10) == 0
+    assert _bwd_f32(lib, D=32) == _lib.ERR_HEAD_DIM
+    assert _bwd_f32(lib, Hq=4, Hkv=3) == _lib.ERR_GQA
+    assert _bwd_f32(lib, Lk=-2) == _lib.ERR_BAD_SHAPE
+    assert _bwd_f32(lib, qs=None) == _lib.ERR_NULL_POINTER
+    assert _bwd_f32(lib, scale=-1.0) == _lib.ERR_ARGUMENT
+    assert _bwd_f32(lib, lse=None) == _lib.ERR_NULL_POINTER
+    assert _bwd_f32(lib, dv=None) == _lib.ERR_NULL_POINTER
+    assert _bwd_f32(lib, o=40) == _lib.ERR_LAYOUT
+    assert _bwd_f32(lib, dks=_lib.i64_array([1024 * 128, 1024 * 128, 126])) == _lib.ERR_LAYOUT
+    assert _bwd_f32(lib, mask=16, msb=1) == _lib.ERR_ARGUMENT
+    assert _bwd_f32(lib, ws=None) == _lib.ERR_WORKSPACE
+    assert _bwd_f32(lib, wsb=16) == _lib.ERR_WORKSPACE
+    assert _bwd_f32(lib, ws=272) == _lib.ERR_LAYOUT  # the row statistics need 256-byte alignment
+    assert _bwd_f32(lib, Lq=0, Lk=0) == _lib.OK
+
+
+@cpu_only
+def test_rope_f32_validation_paths(lib):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+
+    def call(**over):
+        a = dict(x=16, xs=s, B=1, H=2, L=4, D=128, c=16, sn=16, tsb=0, inv=0, out=16, os=s)
+        a.update(over)
+        return lib.avattn_rope_apply_f32(a["x"], a["xs"], a["B"], a["H"], a["L"], a["D"], a["c"], a["sn"],
+                                         a["tsb"], a["inv"], a["out"], a["os"], None)
+
+    assert call(D=130) == _lib.ERR_HEAD_DIM
+    assert call(D=6) == _lib.ERR_HEAD_DIM
+    assert call(L=-1) == _lib.ERR_BAD_SHAPE
+    assert call(c=None) == _lib.ERR_NULL_POINTER
+    assert call(x=8) == _lib.ERR_LAYOUT
+    assert call(os=_lib.i64_array([1024 * 128, 1024 * 128, 2])) == _lib.ERR_LAYOUT
+    assert call(tsb=-4) == _lib.ERR_LAYOUT
+    assert call(L=0) == _lib.OK
