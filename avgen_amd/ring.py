@@ -398,6 +398,16 @@ class _RingAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_out, _grad_lse):
         query, key, value, out, lse, key_mask = ctx.saved_tensors
+        if query.dtype is torch.float32:
+            # float32: the per-chunk backward op (its fp32 kernels) in ring
+            # order; the workspace-sharing ring steps are bf16 kernels.
+            bounds = [shard_bounds(key.shape[2], ctx.cp, r) for r in range(ctx.cp)]
+            masks = None if key_mask is None else [key_mask[:, a:b] for a, b in bounds]
+            dq, dks, dvs = ring_attention_backward(grad_out.contiguous(), query,
+                                                   [key[:, :, a:b] for a, b in bounds],
+                                                   [value[:, :, a:b] for a, b in bounds], out, lse,
+                                                   key_masks=masks, scale=ctx.scale)
+            return dq, torch.cat(dks, 2), torch.cat(dvs, 2), None, None, None
         dq, dk, dv = _ring_backward_into(grad_out.contiguous(), query, key, value, out, lse, key_mask, ctx.cp,
                                          ctx.scale)
         return dq, dk, dv, None, None, None
@@ -430,6 +440,14 @@ def ring_attention(
         raise ValueError("pass both tables_q and tables_k, or neither")
     if tables_q is not None:
         shard_bounds(key.shape[2], cp, 0)  # ragged lengths raise before any launch
+        if query.dtype is torch.float32:
+            # The fused ring steps are bf16 kernels; float32 rotates first (the
+            # reference's own order: apply_rotary, then attention) and runs
+            # the ring on its fp32 kernels.
+            from .rope import apply_rotary
+
+            return _RingAttention.apply(apply_rotary(query, tables_q), apply_rotary(key, tables_k), value, key_mask,
+                                        cp, scale)
         s = ops.default_scale(query.shape[-1]) if scale is None else float(scale)
         return _ring_attention_rope_op(query, key, value, key_mask, tables_q.cos, tables_q.sin, tables_k.cos,
                                        tables_k.sin, int(cp), s)
