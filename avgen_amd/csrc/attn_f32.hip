@@ -5,13 +5,14 @@
 // the identity).  These kernels keep every operand and every product in
 // fp32 on the vector ALUs (gfx950's fp32 matrix rate is no higher than its
 // fp32 vector rate, so the matrix cores buy nothing here):
-//   * forward: two lanes per query row (half of head_dim each), 32-key tiles
-//     of K and V through LDS, the online softmax in the exp2 domain;
+//   * forward: four lanes per pair of query rows (a quarter of head_dim
+//     each), 32-key tiles of K and V through LDS, the online softmax in the
+//     exp2 domain;
 //   * backward, without atomics: row statistics (lse2 = lse*log2 e, +inf
 //     for a row without keys; ndelta = -rowsum(dO*O)), then dK/dV with four
 //     lanes per key looping over 16-row query tiles of every query head of
-//     its group, and dQ with four lanes per query row looping over 32-key
-//     tiles;
+//     its group, and dQ with four lanes per pair of query rows looping
+//     over 32-key tiles;
 //   * the interleaved-pair rotation of fp32 tensors (and its transpose),
 //     with the reference's operation order (two products, one sum, no FMA).
 // They are the exact-dtype path for fp32 callers at moderate sizes; the
@@ -52,34 +53,46 @@ __device__ __forceinline__ bool key_ok(const F32Args& a, int b, int key) {
   return key < a.Lk && (a.mask == nullptr || a.mask[b * a.msb + key] != 0);
 }
 
+// Sum over the four lanes of a group (lanes 4g .. 4g+3), the same bits in
+// each of them (addition commutes), by DPP quad permutations [1,0,3,2] and
+// [2,3,0,1] (no LDS traffic).
+__device__ __forceinline__ float sum4(float x) {
+  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
+  return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
+}
+
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
+// Four lanes per pair of query rows (rows r and r + 64 of the workgroup's
+// 128; a quarter of head_dim each): every K or V value read from LDS feeds
+// the products of both rows, half the LDS reads per FMA of one row per lane.
 template <int D>
 __global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
-  constexpr int HD = D / 2, KT = 32, ROWS = 128;
+  constexpr int QD = D / 4, KT = 32, ROWS = 128;
   __shared__ __attribute__((aligned(16))) float ks[KT][D];
   __shared__ __attribute__((aligned(16))) float vs[KT][D];
   __shared__ float bias[KT];
-  const int tid = threadIdx.x, half = tid & 1;
+  const int tid = threadIdx.x, part = tid & 3;
   const int nqb = (a.Lq + ROWS - 1) / ROWS;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
-  const int row = qb * ROWS + (tid >> 1);
-  const bool valid = row < a.Lq;
+  const int row[2] = {qb * ROWS + (tid >> 2), qb * ROWS + (tid >> 2) + ROWS / 2};
+  const bool valid[2] = {row[0] < a.Lq, row[1] < a.Lq};
 
-  float q[HD], o[HD];
-  {
-    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl + half * HD;
+  float q[2][QD], o[2][QD];
 #pragma unroll
-    for (int d = 0; d < HD; d += 4) {
-      const f32x4 x = valid ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      q[d] = x[0], q[d + 1] = x[1], q[d + 2] = x[2], q[d + 3] = x[3];
+  for (int w = 0; w < 2; ++w) {
+    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row[w] * a.qsl + part * QD;
+#pragma unroll
+    for (int d = 0; d < QD; d += 4) {
+      const f32x4 x = valid[w] ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      q[w][d] = x[0], q[w][d + 1] = x[1], q[w][d + 2] = x[2], q[w][d + 3] = x[3];
     }
-  }
 #pragma unroll
-  for (int d = 0; d < HD; ++d) o[d] = 0.f;
-  float m = kNegInf, l = 0.f;
+    for (int d = 0; d < QD; ++d) o[w][d] = 0.f;
+  }
+  float m[2] = {kNegInf, kNegInf}, l[2] = {0.f, 0.f};
   const float* kb = a.k + b * a.ksb + hk * a.ksh;
   const float* vb = a.v + b * a.vsb + hk * a.vsh;
 
@@ -94,55 +107,71 @@ __global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
     if (tid < KT) bias[tid] = key_ok(a, b, k0 + tid) ? 0.f : kNegInf;
     __syncthreads();
 
-    float s[KT];
-    float mt = kNegInf;
+    float s[2][KT];
+    float mt[2] = {kNegInf, kNegInf};
 #pragma unroll
     for (int j = 0; j < KT; ++j) {
-      float acc = 0.f;
+      float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
-      for (int d = 0; d < HD; d += 4) {
-        const f32x4 kk = ld4(&ks[j][half * HD + d]);
-        acc = fmaf(q[d], kk[0], acc);
-        acc = fmaf(q[d + 1], kk[1], acc);
-        acc = fmaf(q[d + 2], kk[2], acc);
-        acc = fmaf(q[d + 3], kk[3], acc);
-      }
-      // The row's two halves (addition commutes: both lanes hold the same bits).
-      s[j] = acc + __shfl_xor(acc, 1) + bias[j];
-      mt = fmaxf(mt, s[j]);
-    }
-    const float mn = fmaxf(m, mt);
-    if (mn != kNegInf) {
-      const float alpha = m == kNegInf ? 0.f : exp2f((m - mn) * a.c);
-      l *= alpha;
+      for (int d = 0; d < QD; d += 4) {
+        const f32x4 kk = ld4(&ks[j][part * QD + d]);
 #pragma unroll
-      for (int d = 0; d < HD; ++d) o[d] *= alpha;
-#pragma unroll
-      for (int j = 0; j < KT; ++j) {
-        const float p = exp2f((s[j] - mn) * a.c);
-        l += p;
-#pragma unroll
-        for (int d = 0; d < HD; d += 4) {
-          const f32x4 vv = ld4(&vs[j][half * HD + d]);
-          o[d] = fmaf(p, vv[0], o[d]);
-          o[d + 1] = fmaf(p, vv[1], o[d + 1]);
-          o[d + 2] = fmaf(p, vv[2], o[d + 2]);
-          o[d + 3] = fmaf(p, vv[3], o[d + 3]);
+        for (int e = 0; e < 4; ++e) {
+          acc0 = fmaf(q[0][d + e], kk[e], acc0);
+          acc1 = fmaf(q[1][d + e], kk[e], acc1);
         }
       }
-      m = mn;
+      // The row's four quarters (the same bits in each lane of the group).
+      s[0][j] = sum4(acc0) + bias[j];
+      s[1][j] = sum4(acc1) + bias[j];
+      mt[0] = fmaxf(mt[0], s[0][j]);
+      mt[1] = fmaxf(mt[1], s[1][j]);
+    }
+    float p[2][KT];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const float mn = fmaxf(m[w], mt[w]);
+      // mn = -inf: no valid key so far (the row's o and l stay 0)
+      const float alpha = (m[w] == kNegInf || mn == kNegInf) ? 0.f : exp2f((m[w] - mn) * a.c);
+      l[w] *= alpha;
+#pragma unroll
+      for (int d = 0; d < QD; ++d) o[w][d] *= alpha;
+#pragma unroll
+      for (int j = 0; j < KT; ++j) {
+        p[w][j] = mn == kNegInf ? 0.f : exp2f((s[w][j] - mn) * a.c);
+        l[w] += p[w][j];
+      }
+      m[w] = mn;
+    }
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+#pragma unroll
+      for (int d = 0; d < QD; d += 4) {
+        const f32x4 vv = ld4(&vs[j][part * QD + d]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[0][d + e] = fmaf(p[0][j], vv[e], o[0][d + e]);
+          o[1][d + e] = fmaf(p[1][j], vv[e], o[1][d + e]);
+        }
+      }
     }
   }
 
   // l > 0: normal row; l == 0: no valid key (out 0, lse -inf); NaN: a NaN or
   // +inf score reached the row (out and lse NaN).
-  if (!valid) return;
   const float nan = __builtin_nanf("");
-  const float inv = l > 0.f ? 1.f / l : (l == 0.f ? 0.f : nan);
-  float* op = a.o + b * a.osb + h * a.osh + (int64_t)row * a.osl + half * HD;
 #pragma unroll
-  for (int d = 0; d < HD; d += 4) st4(op + d, f32x4{o[d] * inv, o[d + 1] * inv, o[d + 2] * inv, o[d + 3] * inv});
-  if (half == 0) a.lse[(int64_t)bh * a.Lq + row] = l > 0.f ? fmaf(m, a.scale, logf(l)) : (l == 0.f ? kNegInf : nan);
+  for (int w = 0; w < 2; ++w) {
+    if (!valid[w]) continue;
+    const float inv = l[w] > 0.f ? 1.f / l[w] : (l[w] == 0.f ? 0.f : nan);
+    float* op = a.o + b * a.osb + h * a.osh + (int64_t)row[w] * a.osl + part * QD;
+#pragma unroll
+    for (int d = 0; d < QD; d += 4)
+      st4(op + d, f32x4{o[w][d] * inv, o[w][d + 1] * inv, o[w][d + 2] * inv, o[w][d + 3] * inv});
+    if (part == 0)
+      a.lse[(int64_t)bh * a.Lq + row[w]] =
+          l[w] > 0.f ? fmaf(m[w], a.scale, logf(l[w])) : (l[w] == 0.f ? kNegInf : nan);
+  }
 }
 
 // Zeros to out and -inf to lse (no keys at all).
@@ -183,12 +212,6 @@ __global__ __launch_bounds__(256) void bwd_pre_f32_kernel(F32Args a) {
   a.lse2[r] = l == kNegInf ? kPosInf : l * kLog2e;
 }
 
-// Sum over the four lanes of a group (lanes 4g .. 4g+3), the same bits in
-// each of them.
-__device__ __forceinline__ float sum4(float x) {
-  x += __shfl_xor(x, 1);
-  return x + __shfl_xor(x, 2);
-}
 
 template <int D>
 __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
@@ -237,7 +260,10 @@ __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
         nds[tid] = i < a.Lq ? a.ndelta[rbase + i] : 0.f;
       }
       __syncthreads();
-#pragma unroll 4
+      // One row at a time: unrolled further, the rows' q and dO values
+      // outgrow the registers (AGPR copies; 584 against 436 ms at
+      // (2,20,16384,128) for unroll 4).
+#pragma unroll 1
       for (int r = 0; r < QT; ++r) {
         float s = 0.f, dp = 0.f;
 #pragma unroll
@@ -277,9 +303,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
   }
 }
 
+// Four lanes per pair of query rows (r and r + 64 of the workgroup's 128),
+// as in the forward: each K or V value read from LDS serves both rows.
 template <int D>
 __global__ __launch_bounds__(256) void bwd_dq_f32_kernel(F32Args a) {
-  constexpr int QD = D / 4, RPB = 64, KT = 32;
+  constexpr int QD = D / 4, RPB = 128, KT = 32;
   __shared__ __attribute__((aligned(16))) float ks[KT][D];
   __shared__ __attribute__((aligned(16))) float vs[KT][D];
   __shared__ int kok[KT];
@@ -287,25 +315,24 @@ __global__ __launch_bounds__(256) void bwd_dq_f32_kernel(F32Args a) {
   const int nqb = (a.Lq + RPB - 1) / RPB;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
-  const int row = qb * RPB + (tid >> 2);
-  const bool valid = row < a.Lq;
-  float q[QD], g[QD], dq[QD];
-  {
-    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl + part * QD;
-    const float* dp = a.dout + b * a.dosb + h * a.dosh + (int64_t)row * a.dosl + part * QD;
+  const int row[2] = {qb * RPB + (tid >> 2), qb * RPB + (tid >> 2) + RPB / 2};
+  const bool valid[2] = {row[0] < a.Lq, row[1] < a.Lq};
+  float q[2][QD], g[2][QD], dq[2][QD], l2[2], nd[2];
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row[w] * a.qsl + part * QD;
+    const float* dp = a.dout + b * a.dosb + h * a.dosh + (int64_t)row[w] * a.dosl + part * QD;
 #pragma unroll
     for (int d = 0; d < QD; d += 4) {
-      const f32x4 x = valid ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 y = valid ? ld4(dp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      q[d] = x[0], q[d + 1] = x[1], q[d + 2] = x[2], q[d + 3] = x[3];
-      g[d] = y[0], g[d + 1] = y[1], g[d + 2] = y[2], g[d + 3] = y[3];
-    }
-  }
+      const f32x4 x = valid[w] ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 y = valid[w] ? ld4(dp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int d = 0; d < QD; ++d) dq[d] = 0.f;
-  const int64_t r = (int64_t)bh * a.Lq + row;
-  const float l2 = valid ? a.lse2[r] : kPosInf;
-  const float nd = valid ? a.ndelta[r] : 0.f;
+      for (int e = 0; e < 4; ++e) q[w][d + e] = x[e], g[w][d + e] = y[e], dq[w][d + e] = 0.f;
+    }
+    const int64_t r = (int64_t)bh * a.Lq + row[w];
+    l2[w] = valid[w] ? a.lse2[r] : kPosInf;
+    nd[w] = valid[w] ? a.ndelta[r] : 0.f;
+  }
   const float* kb = a.k + b * a.ksb + hk * a.ksh;
   const float* vb = a.v + b * a.vsb + hk * a.vsh;
 
@@ -321,31 +348,41 @@ __global__ __launch_bounds__(256) void bwd_dq_f32_kernel(F32Args a) {
     __syncthreads();
     for (int j = 0; j < KT; ++j) {
       if (!kok[j]) continue;  // the same for every lane: masked keys add nothing
-      float s = 0.f, dp = 0.f;
+      float s0 = 0.f, s1 = 0.f, dp0 = 0.f, dp1 = 0.f;
 #pragma unroll
       for (int d = 0; d < QD; d += 4) {
         const f32x4 x = ld4(&ks[j][part * QD + d]);
         const f32x4 y = ld4(&vs[j][part * QD + d]);
-        s = fmaf(q[d], x[0], fmaf(q[d + 1], x[1], fmaf(q[d + 2], x[2], fmaf(q[d + 3], x[3], s))));
-        dp = fmaf(g[d], y[0], fmaf(g[d + 1], y[1], fmaf(g[d + 2], y[2], fmaf(g[d + 3], y[3], dp))));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s0 = fmaf(q[0][d + e], x[e], s0);
+          s1 = fmaf(q[1][d + e], x[e], s1);
+          dp0 = fmaf(g[0][d + e], y[e], dp0);
+          dp1 = fmaf(g[1][d + e], y[e], dp1);
+        }
       }
-      s = sum4(s);
-      dp = sum4(dp);
-      const float p = exp2f(s * a.c - l2);
-      const float ds = p * (dp + nd);
+      const float ds0 = exp2f(sum4(s0) * a.c - l2[0]) * (sum4(dp0) + nd[0]);
+      const float ds1 = exp2f(sum4(s1) * a.c - l2[1]) * (sum4(dp1) + nd[1]);
 #pragma unroll
       for (int d = 0; d < QD; d += 4) {
         const f32x4 x = ld4(&ks[j][part * QD + d]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dq[d + e] = fmaf(ds, x[e], dq[d + e]);
+        for (int e = 0; e < 4; ++e) {
+          dq[0][d + e] = fmaf(ds0, x[e], dq[0][d + e]);
+          dq[1][d + e] = fmaf(ds1, x[e], dq[1][d + e]);
+        }
       }
     }
   }
-  if (!valid) return;
-  float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)row * a.dqsl + part * QD;
 #pragma unroll
-  for (int d = 0; d < QD; d += 4)
-    st4(op + d, f32x4{dq[d] * a.scale, dq[d + 1] * a.scale, dq[d + 2] * a.scale, dq[d + 3] * a.scale});
+  for (int w = 0; w < 2; ++w) {
+    if (!valid[w]) continue;
+    float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)row[w] * a.dqsl + part * QD;
+#pragma unroll
+    for (int d = 0; d < QD; d += 4)
+      st4(op + d, f32x4{dq[w][d] * a.scale, dq[w][d + 1] * a.scale, dq[w][d + 2] * a.scale,
+                        dq[w][d + 3] * a.scale});
+  }
 }
 
 // Zeros over a (B, H, L, D) fp32 tensor (gradients of an empty side).
@@ -437,7 +474,7 @@ void launch_bwd_f32(const F32Args& a, hipStream_t s) {
   hipLaunchKernelGGL(bwd_pre_f32_kernel<D>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a);
   const int nkb = (a.Lk + 63) / 64;
   hipLaunchKernelGGL(bwd_dkdv_f32_kernel<D>, dim3((unsigned)(nkb * a.B * a.Hkv)), dim3(256), 0, s, a);
-  const int nqb = (a.Lq + 63) / 64;
+  const int nqb = (a.Lq + 127) / 128;
   hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
 }
 
