@@ -10,7 +10,8 @@ with holes and fully masked batch rows.
   dS, one pass or one (batch, kv head) pair per pass;
 - fp8: per-head absmax scales, quantized exactly as the kernels do;
 - ring: cp 1-4 equal chunks of the key sequence, with and without the fused
-  3D RoPE (whose results must equal the unfused composition bit for bit).
+  3D RoPE (whose results must equal the unfused composition bit for bit);
+- float32: the fp32 forward and backward at float32's bar.
 
 The bars are the kernels' usual ones, scaled with the data: output 2e-2 of
 max(1, its largest magnitude), LSE 1e-3 (fp8: plus 2^-14 of |lse|, the e4m3
@@ -208,3 +209,37 @@ def test_ring_random_shapes_match_oracle(amd, seed):
         ref = R.attention_bwd_f64(_f64(do), qn.astype(np.float64), kn.astype(np.float64), vn.astype(np.float64),
                                   o, l, km)
         _check_grads(fu[2:], ref)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_f32_random_shapes_match_oracle(amd, seed):
+    """The float32 path on random shapes at float32's bar: output 2e-5 of
+    max(1, |out|), LSE 2e-5 of max(1, |lse|), gradients 1e-4 of their
+    largest magnitude."""
+    rng = np.random.default_rng(5000 + seed)
+    c = _shape(rng)
+    g = torch.Generator()
+    g.manual_seed(seed)
+    B, Hq, Hkv, Lq, Lk, D = c["B"], c["Hq"], c["Hkv"], c["Lq"], c["Lk"], c["D"]
+    q, k, v, do = (torch.randn(s, generator=g) * c["scale"]
+                   for s in ((B, Hq, Lq, D), (B, Hkv, Lk, D), (B, Hkv, Lk, D), (B, Hq, Lq, D)))
+    mask = None
+    if c["masked"]:
+        mask = torch.rand((B, Lk), generator=g) < 0.8
+        mask[0, : max(1, Lk // 3)] = True
+        if B > 1:
+            mask[-1] = False
+    print(f"f32 sweep seed={seed} {c}", flush=True)
+    mk = None if mask is None else mask.cuda()
+    out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), mk, None, None, D ** -0.5)
+    dq, dk, dv = amd.ops.flash_bwd(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, mk, D ** -0.5)
+    km = None if mask is None else mask.numpy()
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), km)
+    o, l = _f64(out), lse.cpu().numpy().astype(np.float64)
+    assert np.abs(o - ro).max() <= 2e-5 * max(1.0, np.abs(ro).max())
+    fin = np.isfinite(rl)
+    assert np.array_equal(np.isneginf(l), ~fin)
+    assert (np.abs(l[fin] - rl[fin]) <= 2e-5 * np.maximum(1.0, np.abs(rl[fin]))).all()
+    ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), o, l, km)
+    for got, r, name in zip((dq, dk, dv), ref, ("dq", "dk", "dv")):
+        assert np.abs(_f64(got) - r).max() <= 1e-4 * max(np.abs(r).max(), 1e-6), name
