@@ -476,6 +476,43 @@ def attention_bwd_f64(
     return dq, dk, dv
 
 
+def attention_bwd_magnitudes_f64(
+    dout: np.ndarray, q: np.ndarray, k: np.ndarray, v: np.ndarray, out: np.ndarray, lse: np.ndarray,
+    key_mask: np.ndarray | None = None, scale: float | None = None, attn_mask: np.ndarray | None = None,
+) -> tuple[np.ndarray, np.ndarray]:
+    """The size of the terms dq and dk are computed from, for error floors:
+    ``s (P * (|dP| + |Dr|)) |K|`` and ``s (P * (|dP| + |Dr|))^T |Q|``, the
+    formulas of :func:`attention_bwd_f64` with every factor of ``dS = P *
+    (dP - Dr)`` taken in absolute value (dK summed over a GQA group).
+    ``dP - Dr`` cancels where one key carries the row's weight (one key:
+    ``dP == Dr`` exactly, so dq = dk = 0), and any finite-precision
+    evaluation of it carries a rounding error proportional to ``|dP| +
+    |Dr|``, not to the result; these are the scales of that error."""
+    q = np.asarray(q, np.float64)
+    hq, hk = q.shape[1], np.asarray(k).shape[1]
+    kk = _expand_kv(np.asarray(k, np.float64), hq)
+    vv = _expand_kv(np.asarray(v, np.float64), hq)
+    do = np.asarray(dout, np.float64)
+    o = np.asarray(out, np.float64)
+    lse = np.asarray(lse, np.float64)
+    D = q.shape[-1]
+    scale = 1.0 / math.sqrt(D) if scale is None else scale
+    s = np.einsum("bhqd,bhkd->bhqk", q, kk) * scale
+    lse_b = np.where(np.isfinite(lse), lse, np.inf)[..., None]
+    p = np.exp(s - lse_b)
+    m = _dense_mask(key_mask, attn_mask)
+    if m is not None:
+        p = np.where(m, p, 0.0)
+    dp = np.einsum("bhqd,bhkd->bhqk", do, vv)
+    dr = (do * o).sum(-1, keepdims=True)
+    w = p * (np.abs(dp) + np.abs(dr))
+    mq = np.einsum("bhqk,bhkd->bhqd", w, np.abs(kk)) * scale
+    mk = np.einsum("bhqk,bhqd->bhkd", w, np.abs(q)) * scale
+    if hk != hq:
+        mk = mk.reshape(mk.shape[0], hk, hq // hk, *mk.shape[2:]).sum(2)
+    return mq, mk
+
+
 # ---------------------------------------------------------------------------
 # Ring merge and ring loops  (torch/.../_context_parallel/_attention.py)
 # ---------------------------------------------------------------------------

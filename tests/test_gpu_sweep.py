@@ -6,8 +6,9 @@ occurs), head dims 64 and 128, input scales 0.1-4, key-padding masks with
 holes and fully masked batch rows.  The bar is the kernels' usual one,
 scaled with the data: output 2e-2 of max(1, its largest magnitude) (bf16
 outputs of magnitude 10 carry rounding of 0.03 on their own), LSE 1e-3,
-gradients 2e-2 of their largest magnitude; masked keys get exactly zero
-dK/dV."""
+gradients 2e-2 of their largest magnitude, plus for dq and dk 2^-20 of
+the size of the terms dS = P (dP - Dr) cancels (a single key makes the
+true dq and dk exactly 0); masked keys get exactly zero dK/dV."""
 
 from __future__ import annotations
 
@@ -73,9 +74,14 @@ def test_random_shapes_match_oracle(amd, seed):
     assert np.array_equal(np.isneginf(l), ~fin)
     assert np.abs(l[fin] - rl[fin]).max(initial=0.0) <= LSE_TOL
     grads = R.attention_bwd_f64(f64(do), f64(q), f64(k), f64(v), o, l, km)
-    for got, ref, name in zip((dq, dk, dv), grads, ("dq", "dk", "dv")):
+    mags = (*R.attention_bwd_magnitudes_f64(f64(do), f64(q), f64(k), f64(v), o, l, km), None)
+    for got, ref, mag, name in zip((dq, dk, dv), grads, mags, ("dq", "dk", "dv")):
         err = np.abs(f64(got) - ref).max()
-        assert err <= GRAD_REL_TOL * max(np.abs(ref).max(), 1e-3), (name, err)
+        # dq and dk come from dS = P (dP - Dr), which cancels where one key
+        # carries the row (one key: exactly 0); its rounding scales with the
+        # cancelling terms: 2^-20 of their size (16 float32 ulps)
+        floor = 0.0 if mag is None else 2.0**-20 * mag.max(initial=0.0)
+        assert err <= GRAD_REL_TOL * max(np.abs(ref).max(), 1e-3) + floor, (name, err)
     if mask is not None:
         gone = ~mask.numpy()[:, None, :, None]
         assert np.all(f64(dk)[np.broadcast_to(gone, dk.shape)] == 0)

@@ -645,3 +645,25 @@ def test_attention_fp8_reduces_to_bf16_attention(rng):
     o8d, _ = R.attention_fp8_f64(q * 1.03, k, v, one_q, one_k, mask, scale=sc)
     od, _ = R.attention_f64(q * 1.03, k, v, mask, scale=sc)
     assert not np.allclose(o8d, od, rtol=0, atol=1e-9)
+
+def test_backward_magnitudes_bound_the_gradients():
+    """attention_bwd_magnitudes_f64 is the dq/dk formula with every factor of
+    dS in absolute value: by the triangle inequality it bounds |dq| and |dk|
+    elementwise (GQA included); with a single key dS cancels (dP == Dr),
+    the gradients vanish to float64 rounding while the magnitudes do not."""
+    rng = np.random.default_rng(11)
+    q, do = rng.standard_normal((2, 4, 9, 16)), rng.standard_normal((2, 4, 9, 16))
+    k, v = rng.standard_normal((2, 2, 13, 16)), rng.standard_normal((2, 2, 13, 16))
+    mask = rng.random((2, 13)) < 0.7
+    o, l = R.attention_f64(q, k, v, mask)
+    dq, dk, _ = R.attention_bwd_f64(do, q, k, v, o, l, mask)
+    mq, mk = R.attention_bwd_magnitudes_f64(do, q, k, v, o, l, mask)
+    assert mq.shape == dq.shape and mk.shape == dk.shape
+    assert np.all(np.abs(dq) <= mq * (1 + 1e-12)) and np.all(np.abs(dk) <= mk * (1 + 1e-12))
+    assert mq.max() > 0 and mk.max() > 0
+    k1, v1 = k[:, :, :1] * 4, v[:, :, :1] * 4
+    o, l = R.attention_f64(q * 4, k1, v1)
+    dq, dk, _ = R.attention_bwd_f64(do, q * 4, k1, v1, o, l)
+    mq, mk = R.attention_bwd_magnitudes_f64(do, q * 4, k1, v1, o, l)
+    assert np.abs(dq).max() <= 1e-12 * mq.max() and np.abs(dk).max() <= 1e-12 * mk.max()
+    assert mq.max() > 1.0
