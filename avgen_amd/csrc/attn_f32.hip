@@ -3,16 +3,17 @@
 // F.scaled_dot_product_attention as they come), and its fp32 tensors are
 // rotated in fp32 (src/avgen/models/rope.py:332-338, a cast back to fp32 is
 // the identity).  These kernels keep every operand and every product in
-// fp32 on the vector ALUs (gfx950's fp32 matrix rate is no higher than its
-// fp32 vector rate, so the matrix cores buy nothing here):
-//   * forward: four lanes per pair of query rows (a quarter of head_dim
-//     each), 32-key tiles of K and V through LDS, the online softmax in the
-//     exp2 domain;
-//   * backward, without atomics: row statistics (lse2 = lse*log2 e, +inf
-//     for a row without keys; ndelta = -rowsum(dO*O)), then dK/dV with four
-//     lanes per key looping over 16-row query tiles of every query head of
-//     its group, and dQ with four lanes per pair of query rows looping
-//     over 32-key tiles;
+// fp32:
+//   * forward on the fp32 matrix cores (v_mfma_f32_32x32x2f32; its peak,
+//     157.3 TFLOP/s, equals the vector ALUs', but it takes one operand
+//     float per lane per 4,096 FLOP where the vector FMAs need LDS reads
+//     for every four): 32-key tiles of K and V through LDS, the online
+//     softmax in the exp2 domain;
+//   * backward on the vector ALUs, without atomics: row statistics (lse2 =
+//     lse*log2 e, +inf for a row without keys; ndelta = -rowsum(dO*O)), then
+//     dK/dV with four lanes per key looping over 16-row query tiles of every
+//     query head of its group, and dQ with four lanes per pair of query rows
+//     looping over 32-key tiles;
 //   * the interleaved-pair rotation of fp32 tensors (and its transpose),
 //     with the reference's operation order (two products, one sum, no FMA).
 // They are the exact-dtype path for fp32 callers at moderate sizes; the
@@ -64,114 +65,148 @@ __device__ __forceinline__ float sum4(float x) {
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
-// Four lanes per pair of query rows (rows r and r + 64 of the workgroup's
-// 128; a quarter of head_dim each): every K or V value read from LDS feeds
-// the products of both rows, half the LDS reads per FMA of one row per lane.
+// On the fp32 matrix cores (v_mfma_f32_32x32x2f32: A one float per lane,
+// A[m = l%32][k = l/32]; B[k = l/32][n = l%32]; D register i of lane l at
+// [8*(i/4) + 4*(l/32) + i%4][l%32], checked on the GPU).  One wave per 32
+// query rows, four per workgroup, 32-key tiles.  Scores are formed
+// transposed, S^T = K Q^T, k-step j contracting channels j and D/2 + j (the
+// lane's half of head_dim, held in registers as B operands), so lane l holds
+// 16 keys of query l%32; those are exactly the keys its B operand of
+// O^T += V^T P^T needs in k-step j (key 8*(j/4) + 4*(l/32) + j%4), so P
+// never moves.  K and V tiles go through LDS with rows padded by 4 floats
+// (the 32 lanes of a K read hit different banks), staged one tile ahead
+// through registers.
 template <int D>
 __global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
-  constexpr int QD = D / 4, KT = 32, ROWS = 128;
-  __shared__ __attribute__((aligned(16))) float ks[KT][D];
-  __shared__ __attribute__((aligned(16))) float vs[KT][D];
-  __shared__ float bias[KT];
-  const int tid = threadIdx.x, part = tid & 3;
+  constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
+  constexpr int PER = KT * D / 4 / 256;  // float4 loads per thread per tensor and tile
+  __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
+  __shared__ __attribute__((aligned(16))) float vs[2][KT * PITCH];
+  __shared__ __attribute__((aligned(16))) float bias[2][KT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
   const int nqb = (a.Lq + ROWS - 1) / ROWS;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
-  const int row[2] = {qb * ROWS + (tid >> 2), qb * ROWS + (tid >> 2) + ROWS / 2};
-  const bool valid[2] = {row[0] < a.Lq, row[1] < a.Lq};
+  const int row = qb * ROWS + wave * 32 + l32;
+  const bool valid = row < a.Lq;
 
-  float q[2][QD], o[2][QD];
+  float q[HD];  // channels hh*HD .. +HD-1 of this lane's query row
+  {
+    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl + hh * HD;
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row[w] * a.qsl + part * QD;
-#pragma unroll
-    for (int d = 0; d < QD; d += 4) {
-      const f32x4 x = valid[w] ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      q[w][d] = x[0], q[w][d + 1] = x[1], q[w][d + 2] = x[2], q[w][d + 3] = x[3];
+    for (int d = 0; d < HD; d += 4) {
+      const f32x4 x = valid ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      q[d] = x[0], q[d + 1] = x[1], q[d + 2] = x[2], q[d + 3] = x[3];
     }
-#pragma unroll
-    for (int d = 0; d < QD; ++d) o[w][d] = 0.f;
   }
-  float m[2] = {kNegInf, kNegInf}, l[2] = {0.f, 0.f};
+  f32x16 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  float m = kNegInf, l = 0.f;
   const float* kb = a.k + b * a.ksb + hk * a.ksh;
   const float* vb = a.v + b * a.vsb + hk * a.vsh;
 
-  for (int k0 = 0; k0 < a.Lk; k0 += KT) {
-    __syncthreads();  // the previous tile is consumed
-    for (int u = tid; u < KT * D / 4; u += 256) {
-      const int j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = k0 + j;
+  // Tile staging: thread tid moves float4 chunks u = tid + 256*i of the
+  // tile's K and V rows.
+  f32x4 pk[PER], pv[PER];
+  float pbias = 0.f;
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = k0 + j;
       const bool in = key < a.Lk;
-      st4(&ks[j][c4], in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
-      st4(&vs[j][c4], in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+      pk[i] = in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      pv[i] = in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    if (tid < KT) bias[tid] = key_ok(a, b, k0 + tid) ? 0.f : kNegInf;
-    __syncthreads();
+    if (tid < KT) pbias = key_ok(a, b, k0 + tid) ? 0.f : kNegInf;
+  };
+  auto store = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4));
+      st4(&ks[buf][j * PITCH + c4], pk[i]);
+      st4(&vs[buf][j * PITCH + c4], pv[i]);
+    }
+    if (tid < KT) bias[buf][tid] = pbias;
+  };
 
-    float s[2][KT];
-    float mt[2] = {kNegInf, kNegInf};
+  const int ntile = (a.Lk + KT - 1) / KT;
+  if (ntile > 0) {
+    fetch(0);
+    store(0);
+  }
+  for (int t = 0; t < ntile; ++t) {
+    const int buf = t & 1;
+    __syncthreads();  // tile t stored; every wave is done with tile t - 1
+    if (t + 1 < ntile) fetch((t + 1) * KT);
+    const float* kt = ks[buf];
+    const float* vt = vs[buf];
+    // S^T = K Q^T: k-step j takes channels j (lanes 0-31) and HD + j (32-63)
+    f32x16 s;
 #pragma unroll
-    for (int j = 0; j < KT; ++j) {
-      float acc0 = 0.f, acc1 = 0.f;
+    for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
-      for (int d = 0; d < QD; d += 4) {
-        const f32x4 kk = ld4(&ks[j][part * QD + d]);
+    for (int j = 0; j < HD; j += 4) {
+      const f32x4 kk = ld4(kt + l32 * PITCH + hh * HD + j);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc0 = fmaf(q[0][d + e], kk[e], acc0);
-          acc1 = fmaf(q[1][d + e], kk[e], acc1);
-        }
-      }
-      // The row's four quarters (the same bits in each lane of the group).
-      s[0][j] = sum4(acc0) + bias[j];
-      s[1][j] = sum4(acc1) + bias[j];
-      mt[0] = fmaxf(mt[0], s[0][j]);
-      mt[1] = fmaxf(mt[1], s[1][j]);
+      for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[e], q[j + e], s, 0, 0, 0);
     }
-    float p[2][KT];
+    // register i: key 8*(i/4) + 4*hh + i%4 of the tile, query l32
+    float mt = kNegInf;
 #pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      const float mn = fmaxf(m[w], mt[w]);
-      // mn = -inf: no valid key so far (the row's o and l stay 0)
-      const float alpha = (m[w] == kNegInf || mn == kNegInf) ? 0.f : exp2f((m[w] - mn) * a.c);
-      l[w] *= alpha;
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 bb = ld4(&bias[buf][8 * g + 4 * hh]);
 #pragma unroll
-      for (int d = 0; d < QD; ++d) o[w][d] *= alpha;
-#pragma unroll
-      for (int j = 0; j < KT; ++j) {
-        p[w][j] = mn == kNegInf ? 0.f : exp2f((s[w][j] - mn) * a.c);
-        l[w] += p[w][j];
-      }
-      m[w] = mn;
-    }
-#pragma unroll
-    for (int j = 0; j < KT; ++j) {
-#pragma unroll
-      for (int d = 0; d < QD; d += 4) {
-        const f32x4 vv = ld4(&vs[j][part * QD + d]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          o[0][d + e] = fmaf(p[0][j], vv[e], o[0][d + e]);
-          o[1][d + e] = fmaf(p[1][j], vv[e], o[1][d + e]);
-        }
+      for (int r = 0; r < 4; ++r) {
+        s[4 * g + r] += bb[r];
+        mt = fmaxf(mt, s[4 * g + r]);
       }
     }
+    mt = fmaxf(mt, __shfl_xor(mt, 32));  // the query's other 16 keys
+    const float mn = fmaxf(m, mt);
+    const float alpha = (m == kNegInf || mn == kNegInf) ? 0.f : exp2f((m - mn) * a.c);
+    l *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+    m = mn;
+    f32x16 p;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      p[i] = mn == kNegInf ? 0.f : exp2f((s[i] - mn) * a.c);
+      l += p[i];
+    }
+    // O^T += V^T P^T: k-step j takes keys 8*(j/4) + j%4 (+4 for lanes 32-63),
+    // this lane's register j of P; A is channel 32*dt + l32 of that key.
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int key = 8 * (j / 4) + 4 * hh + (j % 4);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[key * PITCH + 32 * dt + l32], p[j], o[dt], 0, 0, 0);
+    }
+    if (t + 1 < ntile) store(buf ^ 1);
   }
 
-  // l > 0: normal row; l == 0: no valid key (out 0, lse -inf); NaN: a NaN or
-  // +inf score reached the row (out and lse NaN).
+  // The row sum over both halves of the keys; l > 0: normal row; l == 0: no
+  // valid key (out 0, lse -inf); NaN: a NaN or +inf score reached the row.
+  l += __shfl_xor(l, 32);
+  if (!valid) return;
   const float nan = __builtin_nanf("");
+  const float inv = l > 0.f ? 1.f / l : (l == 0.f ? 0.f : nan);
+  float* op = a.o + b * a.osb + h * a.osh + (int64_t)row * a.osl;
+  // o[dt] register i: channel 32*dt + 8*(i/4) + 4*hh + i%4 of this lane's query
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    if (!valid[w]) continue;
-    const float inv = l[w] > 0.f ? 1.f / l[w] : (l[w] == 0.f ? 0.f : nan);
-    float* op = a.o + b * a.osb + h * a.osh + (int64_t)row[w] * a.osl + part * QD;
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-    for (int d = 0; d < QD; d += 4)
-      st4(op + d, f32x4{o[w][d] * inv, o[w][d + 1] * inv, o[w][d + 2] * inv, o[w][d + 3] * inv});
-    if (part == 0)
-      a.lse[(int64_t)bh * a.Lq + row[w]] =
-          l[w] > 0.f ? fmaf(m[w], a.scale, logf(l[w])) : (l[w] == 0.f ? kNegInf : nan);
-  }
+    for (int g = 0; g < 4; ++g)
+      st4(op + 32 * dt + 8 * g + 4 * hh,
+          f32x4{o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv});
+  if (hh == 0) a.lse[(int64_t)bh * a.Lq + row] = l > 0.f ? fmaf(m, a.scale, logf(l)) : (l == 0.f ? kNegInf : nan);
 }
 
 // Zeros to out and -inf to lse (no keys at all).
