@@ -3,17 +3,17 @@
 // F.scaled_dot_product_attention as they come), and its fp32 tensors are
 // rotated in fp32 (src/avgen/models/rope.py:332-338, a cast back to fp32 is
 // the identity).  These kernels keep every operand and every product in
-// fp32:
-//   * forward on the fp32 matrix cores (v_mfma_f32_32x32x2f32; its peak,
-//     157.3 TFLOP/s, equals the vector ALUs', but it takes one operand
-//     float per lane per 4,096 FLOP where the vector FMAs need LDS reads
-//     for every four): 32-key tiles of K and V through LDS, the online
-//     softmax in the exp2 domain;
-//   * backward on the vector ALUs, without atomics: row statistics (lse2 =
-//     lse*log2 e, +inf for a row without keys; ndelta = -rowsum(dO*O)), then
-//     dK/dV with four lanes per key looping over 16-row query tiles of every
-//     query head of its group, and dQ with four lanes per pair of query rows
-//     looping over 32-key tiles;
+// fp32, the products on the fp32 matrix cores (v_mfma_f32_32x32x2f32: its
+// peak, 157.3 TFLOP/s, equals the vector ALUs', but it takes one operand
+// float per lane per 4,096 FLOP where vector FMAs need LDS reads for every
+// four):
+//   * forward: one wave per 32 query rows, 32-key tiles of K and V through
+//     LDS, the online softmax in the exp2 domain;
+//   * backward, without atomics: row statistics (lse2 = lse*log2 e, +inf
+//     for a row without keys; ndelta = -rowsum(dO*O)), then dK/dV with one
+//     wave per 32 keys looping over 32-row query tiles of every query head
+//     of its group, and dQ with one wave per 32 query rows looping over
+//     32-key tiles;
 //   * the interleaved-pair rotation of fp32 tensors (and its transpose),
 //     with the reference's operation order (two products, one sum, no FMA).
 // They are the exact-dtype path for fp32 callers at moderate sizes; the
@@ -52,14 +52,6 @@ __device__ __forceinline__ void st4(float* p, const f32x4& v) { *reinterpret_cas
 
 __device__ __forceinline__ bool key_ok(const F32Args& a, int b, int key) {
   return key < a.Lk && (a.mask == nullptr || a.mask[b * a.msb + key] != 0);
-}
-
-// Sum over the four lanes of a group (lanes 4g .. 4g+3), the same bits in
-// each of them (addition commutes), by DPP quad permutations [1,0,3,2] and
-// [2,3,0,1] (no LDS traffic).
-__device__ __forceinline__ float sum4(float x) {
-  x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, true));
-  return x + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, true));
 }
 
 // ---------------------------------------------------------------------------
@@ -248,175 +240,261 @@ __global__ __launch_bounds__(256) void bwd_pre_f32_kernel(F32Args a) {
 }
 
 
+// dK/dV on the fp32 matrix cores: one wave per 32 keys (lane l%32's key in
+// registers, its half of head_dim as B operands), 32-row query tiles of Q
+// and dO through LDS.  S = Q K^T and dP = dO V^T put row 8*(i/4) + 4*(l/32)
+// + i%4 of the tile in register i of lane l, against the lane's key: so P
+// and dS registers j are the A operands of dV += P^T dO and dK += dS^T Q in
+// k-step j as they stand.
 template <int D>
 __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
-  constexpr int QD = D / 4, KPB = 64, QT = 16;
-  __shared__ __attribute__((aligned(16))) float qs[QT][D];
-  __shared__ __attribute__((aligned(16))) float dos[QT][D];
-  __shared__ float l2s[QT], nds[QT];
-  const int tid = threadIdx.x, part = tid & 3;
+  constexpr int QT = 32, KPB = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
+  constexpr int PER = QT * D / 4 / 256;
+  __shared__ __attribute__((aligned(16))) float qs[2][QT * PITCH];
+  __shared__ __attribute__((aligned(16))) float dos[2][QT * PITCH];
+  __shared__ __attribute__((aligned(16))) float l2s[2][QT];
+  __shared__ __attribute__((aligned(16))) float nds[2][QT];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
   const int nkb = (a.Lk + KPB - 1) / KPB;
   const int kb = blockIdx.x % nkb, bhk = blockIdx.x / nkb;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int group = a.Hq / a.Hkv;
-  const int key = kb * KPB + (tid >> 2);
-  const bool kin = key < a.Lk, kvalid = key_ok(a, b, key);
-  float k[QD], v[QD], dk[QD], dv[QD];
+  const int k0 = kb * KPB + wave * 32;  // this wave's first key
+  const int key = k0 + l32;
+  const bool kvalid = key_ok(a, b, key);
+  float kr[HD], vr[HD];  // channels hh*HD .. +HD-1 of the lane's key
   {
-    const float* kp = a.k + b * a.ksb + hk * a.ksh + (int64_t)key * a.ksl + part * QD;
-    const float* vp = a.v + b * a.vsb + hk * a.vsh + (int64_t)key * a.vsl + part * QD;
+    const bool in = key < a.Lk;
+    const float* kp = a.k + b * a.ksb + hk * a.ksh + (int64_t)key * a.ksl + hh * HD;
+    const float* vp = a.v + b * a.vsb + hk * a.vsh + (int64_t)key * a.vsl + hh * HD;
 #pragma unroll
-    for (int d = 0; d < QD; d += 4) {
-      const f32x4 x = kin ? ld4(kp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 y = kin ? ld4(vp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      k[d] = x[0], k[d + 1] = x[1], k[d + 2] = x[2], k[d + 3] = x[3];
-      v[d] = y[0], v[d + 1] = y[1], v[d + 2] = y[2], v[d + 3] = y[3];
+    for (int d = 0; d < HD; d += 4) {
+      const f32x4 x = in ? ld4(kp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 y = in ? ld4(vp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) kr[d + e] = x[e], vr[d + e] = y[e];
     }
   }
+  f32x16 dk[DT], dv[DT];
 #pragma unroll
-  for (int d = 0; d < QD; ++d) dk[d] = 0.f, dv[d] = 0.f;
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dk[dt][i] = 0.f, dv[dt][i] = 0.f;
 
+  const int ntile = (a.Lq + QT - 1) / QT;
   for (int gi = 0; gi < group; ++gi) {
     const int h = hk * group + gi;
     const int64_t rbase = ((int64_t)b * a.Hq + h) * a.Lq;
     const float* qb = a.q + b * a.qsb + h * a.qsh;
     const float* db = a.dout + b * a.dosb + h * a.dosh;
-    for (int q0 = 0; q0 < a.Lq; q0 += QT) {
-      __syncthreads();  // the previous tile is consumed
-      for (int u = tid; u < QT * D / 4; u += 256) {
-        const int r = u / (D / 4), c4 = 4 * (u % (D / 4)), i = q0 + r;
-        const bool in = i < a.Lq;
-        st4(&qs[r][c4], in ? ld4(qb + (int64_t)i * a.qsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
-        st4(&dos[r][c4], in ? ld4(db + (int64_t)i * a.dosl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+    f32x4 pq[PER], pd[PER];
+    float pl2 = kPosInf, pnd = 0.f;
+    auto fetch = [&](int r0) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int u = tid + 256 * i, r = u / (D / 4), c4 = 4 * (u % (D / 4)), row = r0 + r;
+        const bool in = row < a.Lq;
+        pq[i] = in ? ld4(qb + (int64_t)row * a.qsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        pd[i] = in ? ld4(db + (int64_t)row * a.dosl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
       }
       if (tid < QT) {
-        const int i = q0 + tid;
-        l2s[tid] = i < a.Lq ? a.lse2[rbase + i] : kPosInf;  // rows past the end get P = 0
-        nds[tid] = i < a.Lq ? a.ndelta[rbase + i] : 0.f;
+        const int row = r0 + tid;
+        pl2 = row < a.Lq ? a.lse2[rbase + row] : kPosInf;  // rows past the end get P = 0
+        pnd = row < a.Lq ? a.ndelta[rbase + row] : 0.f;
       }
-      __syncthreads();
-      // One row at a time: unrolled further, the rows' q and dO values
-      // outgrow the registers (AGPR copies; 584 against 436 ms at
-      // (2,20,16384,128) for unroll 4).
-#pragma unroll 1
-      for (int r = 0; r < QT; ++r) {
-        float s = 0.f, dp = 0.f;
+    };
+    auto store = [&](int buf) {
 #pragma unroll
-        for (int d = 0; d < QD; d += 4) {
-          const f32x4 x = ld4(&qs[r][part * QD + d]);
-          const f32x4 y = ld4(&dos[r][part * QD + d]);
-          s = fmaf(k[d], x[0], fmaf(k[d + 1], x[1], fmaf(k[d + 2], x[2], fmaf(k[d + 3], x[3], s))));
-          dp = fmaf(v[d], y[0], fmaf(v[d + 1], y[1], fmaf(v[d + 2], y[2], fmaf(v[d + 3], y[3], dp))));
-        }
-        s = sum4(s);
-        dp = sum4(dp);
-        const float p = kvalid ? exp2f(s * a.c - l2s[r]) : 0.f;
-        const float ds = p * (dp + nds[r]);
+      for (int i = 0; i < PER; ++i) {
+        const int u = tid + 256 * i, r = u / (D / 4), c4 = 4 * (u % (D / 4));
+        st4(&qs[buf][r * PITCH + c4], pq[i]);
+        st4(&dos[buf][r * PITCH + c4], pd[i]);
+      }
+      if (tid < QT) l2s[buf][tid] = pl2, nds[buf][tid] = pnd;
+    };
+    __syncthreads();  // the previous head's last tiles are consumed
+    fetch(0);
+    store(0);
+    for (int t = 0; t < ntile; ++t) {
+      const int buf = t & 1;
+      __syncthreads();  // tile t stored; every wave is done with tile t - 1
+      if (t + 1 < ntile) fetch((t + 1) * QT);
+      const float* qt = qs[buf];
+      const float* dt_ = dos[buf];
+      f32x16 s, dp;
 #pragma unroll
-        for (int d = 0; d < QD; d += 4) {
-          const f32x4 x = ld4(&qs[r][part * QD + d]);
-          const f32x4 y = ld4(&dos[r][part * QD + d]);
+      for (int i = 0; i < 16; ++i) s[i] = 0.f, dp[i] = 0.f;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            dv[d + e] = fmaf(p, y[e], dv[d + e]);
-            dk[d + e] = fmaf(ds, x[e], dk[d + e]);
-          }
+      for (int j = 0; j < HD; j += 4) {
+        const f32x4 x = ld4(qt + l32 * PITCH + hh * HD + j);
+        const f32x4 y = ld4(dt_ + l32 * PITCH + hh * HD + j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s = __builtin_amdgcn_mfma_f32_32x32x2f32(x[e], kr[j + e], s, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_32x32x2f32(y[e], vr[j + e], dp, 0, 0, 0);
         }
       }
+      // register i: row 8*(i/4) + 4*hh + i%4 of the tile, this lane's key
+      f32x16 p, ds;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 L = ld4(&l2s[buf][8 * g + 4 * hh]);
+        const f32x4 N = ld4(&nds[buf][8 * g + 4 * hh]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = 4 * g + r;
+          p[i] = kvalid ? exp2f(s[i] * a.c - L[r]) : 0.f;
+          ds[i] = p[i] * (dp[i] + N[r]);
+        }
+      }
+      // k-step j: rows 8*(j/4) + j%4 (+4 for lanes 32-63), registers j
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int row = 8 * (j / 4) + 4 * hh + (j % 4);
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          dv[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(p[j], dt_[row * PITCH + 32 * d + l32], dv[d], 0, 0, 0);
+          dk[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[j], qt[row * PITCH + 32 * d + l32], dk[d], 0, 0, 0);
+        }
+      }
+      if (t + 1 < ntile) store(buf ^ 1);
     }
   }
-  if (!kin) return;
+  // dk[d] / dv[d] register i: key k0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32.
   // Masked keys: exactly zero (their P is 0; a non-finite dO or V elsewhere
   // in the row must not reach them through 0 * inf).
-  float* kp = a.dk + b * a.dksb + hk * a.dksh + (int64_t)key * a.dksl + part * QD;
-  float* vp = a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)key * a.dvsl + part * QD;
 #pragma unroll
-  for (int d = 0; d < QD; d += 4) {
-    st4(kp + d, kvalid ? f32x4{dk[d] * a.scale, dk[d + 1] * a.scale, dk[d + 2] * a.scale, dk[d + 3] * a.scale}
-                       : f32x4{0.f, 0.f, 0.f, 0.f});
-    st4(vp + d, kvalid ? f32x4{dv[d], dv[d + 1], dv[d + 2], dv[d + 3]} : f32x4{0.f, 0.f, 0.f, 0.f});
+  for (int i = 0; i < 16; ++i) {
+    const int kk = k0 + 8 * (i / 4) + 4 * hh + (i % 4);
+    if (kk >= a.Lk) continue;
+    const bool ok = key_ok(a, b, kk);
+    float* kp = a.dk + b * a.dksb + hk * a.dksh + (int64_t)kk * a.dksl + l32;
+    float* vp = a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)kk * a.dvsl + l32;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      kp[32 * d] = ok ? dk[d][i] * a.scale : 0.f;
+      vp[32 * d] = ok ? dv[d][i] : 0.f;
+    }
   }
 }
 
-// Four lanes per pair of query rows (r and r + 64 of the workgroup's 128),
-// as in the forward: each K or V value read from LDS serves both rows.
+// dQ on the fp32 matrix cores: one wave per 32 query rows (q and dO halves
+// as B operands), 32-key tiles of K and V through LDS.  S^T = K Q^T and
+// dP^T = V dO^T put key 8*(i/4) + 4*(l/32) + i%4 in register i of lane l,
+// against the lane's row, so dS register j is the A operand of dQ += dS K
+// in k-step j.
 template <int D>
 __global__ __launch_bounds__(256) void bwd_dq_f32_kernel(F32Args a) {
-  constexpr int QD = D / 4, RPB = 128, KT = 32;
-  __shared__ __attribute__((aligned(16))) float ks[KT][D];
-  __shared__ __attribute__((aligned(16))) float vs[KT][D];
-  __shared__ int kok[KT];
-  const int tid = threadIdx.x, part = tid & 3;
-  const int nqb = (a.Lq + RPB - 1) / RPB;
+  constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
+  constexpr int PER = KT * D / 4 / 256;
+  __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
+  __shared__ __attribute__((aligned(16))) float vs[2][KT * PITCH];
+  __shared__ __attribute__((aligned(16))) float kok[2][KT];  // 1: valid key, 0: masked or past the end
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int nqb = (a.Lq + ROWS - 1) / ROWS;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
-  const int row[2] = {qb * RPB + (tid >> 2), qb * RPB + (tid >> 2) + RPB / 2};
-  const bool valid[2] = {row[0] < a.Lq, row[1] < a.Lq};
-  float q[2][QD], g[2][QD], dq[2][QD], l2[2], nd[2];
+  const int r0 = qb * ROWS + wave * 32;  // this wave's first row
+  const int row = r0 + l32;
+  const bool valid = row < a.Lq;
+  float qr[HD], gr[HD];
+  {
+    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl + hh * HD;
+    const float* dp = a.dout + b * a.dosb + h * a.dosh + (int64_t)row * a.dosl + hh * HD;
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row[w] * a.qsl + part * QD;
-    const float* dp = a.dout + b * a.dosb + h * a.dosh + (int64_t)row[w] * a.dosl + part * QD;
+    for (int d = 0; d < HD; d += 4) {
+      const f32x4 x = valid ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 y = valid ? ld4(dp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < QD; d += 4) {
-      const f32x4 x = valid[w] ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 y = valid[w] ? ld4(dp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) q[w][d + e] = x[e], g[w][d + e] = y[e], dq[w][d + e] = 0.f;
+      for (int e = 0; e < 4; ++e) qr[d + e] = x[e], gr[d + e] = y[e];
     }
-    const int64_t r = (int64_t)bh * a.Lq + row[w];
-    l2[w] = valid[w] ? a.lse2[r] : kPosInf;
-    nd[w] = valid[w] ? a.ndelta[r] : 0.f;
   }
+  const int64_t rr = (int64_t)bh * a.Lq + row;
+  const float l2 = valid ? a.lse2[rr] : kPosInf;
+  const float nd = valid ? a.ndelta[rr] : 0.f;
+  f32x16 dq[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) dq[d][i] = 0.f;
   const float* kb = a.k + b * a.ksb + hk * a.ksh;
   const float* vb = a.v + b * a.vsb + hk * a.vsh;
-
-  for (int k0 = 0; k0 < a.Lk; k0 += KT) {
-    __syncthreads();
-    for (int u = tid; u < KT * D / 4; u += 256) {
-      const int j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = k0 + j;
+  f32x4 pk[PER], pv[PER];
+  float pok = 0.f;
+  auto fetch = [&](int c0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = c0 + j;
       const bool in = key < a.Lk;
-      st4(&ks[j][c4], in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
-      st4(&vs[j][c4], in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+      pk[i] = in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      pv[i] = in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    if (tid < KT) kok[tid] = key_ok(a, b, k0 + tid) ? 1 : 0;
-    __syncthreads();
-    for (int j = 0; j < KT; ++j) {
-      if (!kok[j]) continue;  // the same for every lane: masked keys add nothing
-      float s0 = 0.f, s1 = 0.f, dp0 = 0.f, dp1 = 0.f;
+    if (tid < KT) pok = key_ok(a, b, c0 + tid) ? 1.f : 0.f;
+  };
+  auto store = [&](int buf) {
 #pragma unroll
-      for (int d = 0; d < QD; d += 4) {
-        const f32x4 x = ld4(&ks[j][part * QD + d]);
-        const f32x4 y = ld4(&vs[j][part * QD + d]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s0 = fmaf(q[0][d + e], x[e], s0);
-          s1 = fmaf(q[1][d + e], x[e], s1);
-          dp0 = fmaf(g[0][d + e], y[e], dp0);
-          dp1 = fmaf(g[1][d + e], y[e], dp1);
-        }
-      }
-      const float ds0 = exp2f(sum4(s0) * a.c - l2[0]) * (sum4(dp0) + nd[0]);
-      const float ds1 = exp2f(sum4(s1) * a.c - l2[1]) * (sum4(dp1) + nd[1]);
-#pragma unroll
-      for (int d = 0; d < QD; d += 4) {
-        const f32x4 x = ld4(&ks[j][part * QD + d]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dq[0][d + e] = fmaf(ds0, x[e], dq[0][d + e]);
-          dq[1][d + e] = fmaf(ds1, x[e], dq[1][d + e]);
-        }
-      }
+    for (int i = 0; i < PER; ++i) {
+      const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4));
+      st4(&ks[buf][j * PITCH + c4], pk[i]);
+      st4(&vs[buf][j * PITCH + c4], pv[i]);
     }
+    if (tid < KT) kok[buf][tid] = pok;
+  };
+  const int ntile = (a.Lk + KT - 1) / KT;
+  if (ntile > 0) {
+    fetch(0);
+    store(0);
   }
+  for (int t = 0; t < ntile; ++t) {
+    const int buf = t & 1;
+    __syncthreads();
+    if (t + 1 < ntile) fetch((t + 1) * KT);
+    const float* kt = ks[buf];
+    const float* vt = vs[buf];
+    f32x16 s, dp;
 #pragma unroll
-  for (int w = 0; w < 2; ++w) {
-    if (!valid[w]) continue;
-    float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)row[w] * a.dqsl + part * QD;
+    for (int i = 0; i < 16; ++i) s[i] = 0.f, dp[i] = 0.f;
 #pragma unroll
-    for (int d = 0; d < QD; d += 4)
-      st4(op + d, f32x4{dq[w][d] * a.scale, dq[w][d + 1] * a.scale, dq[w][d + 2] * a.scale,
-                        dq[w][d + 3] * a.scale});
+    for (int j = 0; j < HD; j += 4) {
+      const f32x4 x = ld4(kt + l32 * PITCH + hh * HD + j);
+      const f32x4 y = ld4(vt + l32 * PITCH + hh * HD + j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(x[e], qr[j + e], s, 0, 0, 0);
+        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(y[e], gr[j + e], dp, 0, 0, 0);
+      }
+    }
+    // register i: key 8*(i/4) + 4*hh + i%4 of the tile, this lane's row;
+    // masked keys add nothing (dS exactly 0)
+    f32x16 ds;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 ok = ld4(&kok[buf][8 * g + 4 * hh]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 4 * g + r;
+        ds[i] = ok[r] != 0.f ? exp2f(s[i] * a.c - l2) * (dp[i] + nd) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int kk = 8 * (j / 4) + 4 * hh + (j % 4);
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+        dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[j], kt[kk * PITCH + 32 * d + l32], dq[d], 0, 0, 0);
+    }
+    if (t + 1 < ntile) store(buf ^ 1);
+  }
+  // dq[d] register i: row r0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int rw = r0 + 8 * (i / 4) + 4 * hh + (i % 4);
+    if (rw >= a.Lq) continue;
+    float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)rw * a.dqsl + l32;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) op[32 * d] = dq[d][i] * a.scale;
   }
 }
 
@@ -507,7 +585,7 @@ template <int D>
 void launch_bwd_f32(const F32Args& a, hipStream_t s) {
   const int64_t rows = (int64_t)a.B * a.Hq * a.Lq;
   hipLaunchKernelGGL(bwd_pre_f32_kernel<D>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a);
-  const int nkb = (a.Lk + 63) / 64;
+  const int nkb = (a.Lk + 127) / 128;
   hipLaunchKernelGGL(bwd_dkdv_f32_kernel<D>, dim3((unsigned)(nkb * a.B * a.Hkv)), dim3(256), 0, s, a);
   const int nqb = (a.Lq + 127) / 128;
   hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
