@@ -37,6 +37,7 @@ ROOT = Path(__file__).resolve().parent
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (AMD spec)
 PEAK_HBM_GBS = 8000.0
 PEAK_FP8_TFLOPS = 5033.2  # MI355X dense fp8 MFMA (AMD spec)
+PEAK_FP32_TFLOPS = 157.3  # MI355X fp32 (matrix and vector, AMD spec)
 PEAK_MIXED_FP8_BF16_TFLOPS = 1.0 / (0.5 / PEAK_FP8_TFLOPS + 0.5 / PEAK_BF16_TFLOPS)
 
 # Algorithmic MFMA work each kernel performs under the FLOP convention, in
@@ -48,6 +49,11 @@ KERNEL_UNITS = {"attn_fwd": 2, "bwd_dkdv": 3, "bwd_dq": 1, "bwd_dq_ds": 1}
 
 CONFIGS = {
     # name: (B, H, Lq_shard, L_total, D, cp, grid(F,H,W), text_slots)
+    # The reference's CPU smoke configuration, float32 as stated (the
+    # library's fp32 path): forward out + LSE with the head_dim-64 RoPE.
+    "c1": dict(B=1, H=4, Lq=1024, L=1024, D=64, cp=1, grid=(4, 16, 16), text=0,
+               desc="c1 smoke: (1,4,1024,64) float32 self-attention forward (out + LSE) with 3D RoPE, "
+                    "4x16x16 latent"),
     "c2": dict(B=2, H=20, Lq=16384, L=16384, D=128, cp=1, grid=(16, 32, 32), text=0,
                desc="c2 small DiT block: (2,20,16384,128) self-attention fwd+bwd with 3D RoPE"),
     "c3": dict(B=1, H=40, Lq=18900, L=75600, D=128, cp=4, grid=(21, 45, 80), text=0,
@@ -543,6 +549,59 @@ def bench_c5(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
+def bench_c1(cfg: dict, steps: int, warmup: int) -> dict:
+    """BASELINE config c1 in its own dtype: `steps` float32 forwards (q
+    rotated in the call, k rotated once), 4*B*H*L^2*D FLOP per call, timed
+    with HIP events on the launch stream; the peak is the fp32 matrix
+    one."""
+    import avgen_amd
+
+    dev = torch.device("cuda", 0)
+    B, H, L, D = cfg["B"], cfg["H"], cfg["L"], cfg["D"]
+    gen = torch.Generator(device=dev)
+    qkv = []
+    for seed in range(3):
+        gen.manual_seed(seed)
+        qkv.append(torch.randn((B, H, L, D), device=dev, dtype=torch.float32, generator=gen))
+    q, k, v = qkv
+    tables = avgen_amd.rope.build_rotary_tables(video_coords(*cfg["grid"], B, dev), head_dim=D)
+    with torch.no_grad():
+        k = avgen_amd.rope.apply_rotary(k, tables)
+        fwd = avgen_amd.ops.flash_fwd
+        for _ in range(warmup):
+            fwd(q, k, v, None, tables.cos, tables.sin, D ** -0.5)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            out, lse = fwd(q, k, v, None, tables.cos, tables.sin, D ** -0.5)
+        e1.record()
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 4.0 * B * H * L * L * D
+    log(f"[bench] c1: {ms:.4f} ms per call")
+    return {
+        "metric": "attention fwd TFLOP/s (c1 smoke: float32 (1,4,1024,64) with 3D RoPE)",
+        "value": round(flops / (ms / 1e3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) q/k/v, rotated by the 3D RoPE of an 8-fps 2x2-patch 4x16x16 grid)",
+        "config": {"workload": cfg["desc"], "name": "c1", "batch": B, "heads": H, "head_dim": D, "len_q": L,
+                   "len_k": L},
+        "peak_fp32_tflops": PEAK_FP32_TFLOPS,
+        "pct_of_peak_fp32": round(100.0 * flops / (ms / 1e3) / 1e12 / PEAK_FP32_TFLOPS, 2),
+        "lse_finite": bool(torch.isfinite(lse).all().item()),
+        "flops_per_call": flops,
+    }
+
+
 def bench_windowed(cfg: dict, name: str, steps: int, warmup: int) -> dict:
     """fwd+bwd through the key-window kernels (`flash_fwd_windowed` and its
     autograd backward) on the `varlen` or `window` workload.  The windows are
@@ -807,8 +866,9 @@ def main() -> int:
         print(ingest_mfma(args.ingest_mfma[0], args.ingest_mfma[1], args.config))
         return 0
     if args.steps is None:
-        # c5 is quoted on 50 repeated sampling calls; the other workloads on 10 steps
-        args.steps = 50 if args.config == "c5" else 10
+        # c5 is quoted on 50 repeated sampling calls, c1 (a 0.1 ms call) timed
+        # over 200; the other workloads on 10 steps
+        args.steps = {"c5": 50, "c1": 200}.get(args.config, 10)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the ring is emulated on one "
@@ -833,6 +893,10 @@ def main() -> int:
     if args.config == "c5":
         log(f"[bench] config c5: {cfg['desc']}")
         print(json.dumps(bench_c5(cfg, args.steps, args.warmup)), flush=True)
+        return 0
+    if args.config == "c1":
+        log(f"[bench] config c1: {cfg['desc']}")
+        print(json.dumps(bench_c1(cfg, args.steps, args.warmup)), flush=True)
         return 0
     if args.config == "qknorm":
         log(f"[bench] config qknorm: {cfg['desc']}")
