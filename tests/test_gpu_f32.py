@@ -247,3 +247,26 @@ def test_f32_ring_matches_oracle(amd):
     ob.backward(do.cuda())
     for a_, b_ in ((oa, ob), (la, lb), (qa.grad, qb.grad), (ka.grad, kb.grad), (va.grad, vb.grad)):
         assert torch.equal(a_, b_)
+
+
+def test_f32_compiles_to_the_eager_bits(amd):
+    """torch.compile(fullgraph=True) over float32 attention with rotation and
+    its backward: the same bits as eager (the ops' fake kernels give float32
+    outputs)."""
+    B, H, L, D = 1, 2, 200, 64
+    q, k, v, do = (_randn((B, H, L, D), s).cuda() for s in (40, 41, 42, 43))
+    tables = amd.rope.build_rotary_tables(_coords(2, 10, 10, B).cuda(), head_dim=D)
+
+    def f(q, k, v):
+        return amd.attention.rotary_attention(q, k, v, tables)
+
+    def run(fn):
+        qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+        out = fn(qg, kg, vg)
+        out.backward(do)
+        return out.detach(), qg.grad, kg.grad, vg.grad
+
+    eager = run(f)
+    compiled = run(torch.compile(f, fullgraph=True))
+    for a_, b_ in zip(eager, compiled):
+        assert a_.dtype is torch.float32 and torch.equal(a_, b_)
