@@ -54,6 +54,9 @@ CONFIGS = {
     "c1": dict(B=1, H=4, Lq=1024, L=1024, D=64, cp=1, grid=(4, 16, 16), text=0,
                desc="c1 smoke: (1,4,1024,64) float32 self-attention forward (out + LSE) with 3D RoPE, "
                     "4x16x16 latent"),
+    # c2's shape on the float32 path (the library's fp32 kernels), fwd+bwd.
+    "c2f32": dict(B=2, H=20, Lq=16384, L=16384, D=128, cp=1, grid=(16, 32, 32), text=0,
+                  desc="c2 shape in float32: (2,20,16384,128) self-attention fwd+bwd with 3D RoPE on the fp32 path"),
     "c2": dict(B=2, H=20, Lq=16384, L=16384, D=128, cp=1, grid=(16, 32, 32), text=0,
                desc="c2 small DiT block: (2,20,16384,128) self-attention fwd+bwd with 3D RoPE"),
     "c3": dict(B=1, H=40, Lq=18900, L=75600, D=128, cp=4, grid=(21, 45, 80), text=0,
@@ -602,6 +605,70 @@ def bench_c1(cfg: dict, steps: int, warmup: int) -> dict:
     }
 
 
+def bench_f32(cfg: dict, name: str, steps: int, warmup: int) -> dict:
+    """fwd+bwd on float32 tensors (the fp32 kernels): per step the rotary
+    forward (q rotated in the call, k rotated once outside) and its backward
+    through autograd, 12*B*H*L^2*D FLOP; HIP events on the launch stream
+    around the whole step and around the forward alone."""
+    import avgen_amd
+
+    dev = torch.device("cuda", 0)
+    B, H, L, D = cfg["B"], cfg["H"], cfg["L"], cfg["D"]
+    gen = torch.Generator(device=dev)
+    t = []
+    for seed, sc in ((0, 2 ** -0.5), (1, 2 ** -0.5), (2, 2 ** -0.5), (3, 1.0)):
+        gen.manual_seed(seed)
+        t.append(torch.randn((B, H, L, D), device=dev, dtype=torch.float32, generator=gen) * sc)
+    q, k, v, do = t
+    tables = avgen_amd.rope.build_rotary_tables(video_coords(*cfg["grid"], B, dev), head_dim=D)
+    k = avgen_amd.rope.apply_rotary(k, tables)
+
+    def step():
+        qg, kg, vg = (x.detach().requires_grad_(True) for x in (q, k, v))
+        out, _ = avgen_amd.ops.flash_fwd(qg, kg, vg, None, tables.cos, tables.sin, D ** -0.5)
+        out.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ev[0].record()
+    for _ in range(steps):
+        step()
+    ev[1].record()
+    with torch.no_grad():
+        ev[2].record()
+        for _ in range(steps):
+            avgen_amd.ops.flash_fwd(q, k, v, None, tables.cos, tables.sin, D ** -0.5)
+        ev[3].record()
+    torch.cuda.synchronize()
+    ms, fwd_ms = ev[0].elapsed_time(ev[1]) / steps, ev[2].elapsed_time(ev[3]) / steps
+    flops = 12.0 * B * H * L * L * D
+    log(f"[bench] {name}: {ms:.2f} ms per step, forward {fwd_ms:.2f} ms")
+    return {
+        "metric": f"attention fwd+bwd TFLOP/s ({name}: float32 path)",
+        "value": round(flops / (ms / 1e3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1)/sqrt(2) q/k/v, N(0,1) dO, 8-fps 2x2-patch coords)",
+        "config": {"workload": cfg["desc"], "name": name, "batch": B, "heads": H, "head_dim": D, "len_q": L,
+                   "len_k": L},
+        "peak_fp32_tflops": PEAK_FP32_TFLOPS,
+        "pct_of_peak_fp32": round(100.0 * flops / (ms / 1e3) / 1e12 / PEAK_FP32_TFLOPS, 2),
+        "forward_ms": round(fwd_ms, 3),
+        "forward_tflops": round(flops / 3 / (fwd_ms / 1e3) / 1e12, 2),
+        "backward_ms": round(ms - fwd_ms, 3),
+        "backward_tflops": round(2 * flops / 3 / ((ms - fwd_ms) / 1e3) / 1e12, 2),
+    }
+
+
 def bench_windowed(cfg: dict, name: str, steps: int, warmup: int) -> dict:
     """fwd+bwd through the key-window kernels (`flash_fwd_windowed` and its
     autograd backward) on the `varlen` or `window` workload.  The windows are
@@ -868,7 +935,7 @@ def main() -> int:
     if args.steps is None:
         # c5 is quoted on 50 repeated sampling calls, c1 (a 0.1 ms call) timed
         # over 200; the other workloads on 10 steps
-        args.steps = {"c5": 50, "c1": 200}.get(args.config, 10)
+        args.steps = {"c5": 50, "c1": 200, "c2f32": 3}.get(args.config, 10)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the ring is emulated on one "
@@ -897,6 +964,10 @@ def main() -> int:
     if args.config == "c1":
         log(f"[bench] config c1: {cfg['desc']}")
         print(json.dumps(bench_c1(cfg, args.steps, args.warmup)), flush=True)
+        return 0
+    if args.config == "c2f32":
+        log(f"[bench] config c2f32: {cfg['desc']}")
+        print(json.dumps(bench_f32(cfg, "c2f32", args.steps, args.warmup)), flush=True)
         return 0
     if args.config == "qknorm":
         log(f"[bench] config qknorm: {cfg['desc']}")
