@@ -65,15 +65,24 @@ __device__ __forceinline__ bool key_ok(const F32Args& a, int b, int key) {
 // lane's half of head_dim, held in registers as B operands), so lane l holds
 // 16 keys of query l%32; those are exactly the keys its B operand of
 // O^T += V^T P^T needs in k-step j (key 8*(j/4) + 4*(l/32) + j%4), so P
-// never moves.  K and V tiles go through LDS with rows padded by 4 floats
-// (the 32 lanes of a K read hit different banks), staged one tile ahead
-// through registers.
+// never moves.  K tiles sit in LDS row-major with rows padded by 4 floats
+// (the 32 lanes of a K read hit different banks); V tiles with channel
+// 32*t + m of a key at m*(D/32) + t, so one read gives a lane the D/32
+// channels its products for one key take.  Both are staged one tile ahead
+// through registers, and the next operands are read while the current
+// ones' products issue.  The running maximum is raised only when a score
+// exceeds it by more than 2^8 in the exp2 domain (any lane of the wave: the
+// branch is uniform), so the rescale of the output accumulator is rare;
+// the probabilities stay at most 2^8 and out = O / l is unchanged in exact
+// arithmetic.
 template <int D>
-__global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
+__global__ __launch_bounds__(256, 2) void fwd_f32_kernel(F32Args a) {
   constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
-  constexpr int PER = KT * D / 4 / 256;  // float4 loads per thread per tensor and tile
+  constexpr int PER = KT * D / 4 / 256;  // K float4 chunks per thread and tile
+  constexpr int VPER = KT * 32 / 256;    // V (key, lane) slots per thread and tile
+  using vdt = float __attribute__((ext_vector_type(DT)));
   __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
-  __shared__ __attribute__((aligned(16))) float vs[2][KT * PITCH];
+  __shared__ __attribute__((aligned(16))) float vs[2][KT * D];
   __shared__ __attribute__((aligned(16))) float bias[2][KT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
@@ -94,24 +103,29 @@ __global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
   }
   f32x16 o[DT];
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+  for (int dt = 0; dt < DT; ++dt) o[dt] = zero16();
   float m = kNegInf, l = 0.f;
   const float* kb = a.k + b * a.ksb + hk * a.ksh;
   const float* vb = a.v + b * a.vsb + hk * a.vsh;
 
-  // Tile staging: thread tid moves float4 chunks u = tid + 256*i of the
-  // tile's K and V rows.
-  f32x4 pk[PER], pv[PER];
+  // Tile staging: thread tid moves K float4 chunks u = tid + 256*i (key u /
+  // (D/4), channels 4*(u % (D/4)) ..) and V slots u = tid + 256*i (key u/32,
+  // channels 32*t + u%32).
+  f32x4 pk[PER];
+  float pv[VPER][DT];
   float pbias = 0.f;
   auto fetch = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = k0 + j;
-      const bool in = key < a.Lk;
-      pk[i] = in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
-      pv[i] = in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      pk[i] = key < a.Lk ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < VPER; ++i) {
+      const int u = tid + 256 * i, key = k0 + u / 32;
+      const float* vp = vb + (int64_t)key * a.vsl + (u % 32);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) pv[i][t] = key < a.Lk ? vp[32 * t] : 0.f;
     }
     if (tid < KT) pbias = key_ok(a, b, k0 + tid) ? 0.f : kNegInf;
   };
@@ -120,7 +134,14 @@ __global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
     for (int i = 0; i < PER; ++i) {
       const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4));
       st4(&ks[buf][j * PITCH + c4], pk[i]);
-      st4(&vs[buf][j * PITCH + c4], pv[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < VPER; ++i) {
+      const int u = tid + 256 * i;
+      vdt x;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) x[t] = pv[i][t];
+      *reinterpret_cast<vdt*>(&vs[buf][(u / 32) * D + (u % 32) * DT]) = x;
     }
     if (tid < KT) bias[buf][tid] = pbias;
   };
@@ -134,17 +155,19 @@ __global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
     const int buf = t & 1;
     __syncthreads();  // tile t stored; every wave is done with tile t - 1
     if (t + 1 < ntile) fetch((t + 1) * KT);
-    const float* kt = ks[buf];
-    const float* vt = vs[buf];
     // S^T = K Q^T: k-step j takes channels j (lanes 0-31) and HD + j (32-63)
-    f32x16 s;
+    const float* kr = ks[buf] + l32 * PITCH + hh * HD;
+    f32x16 s = zero16();
+    f32x4 k0 = ld4(kr), k1 = ld4(kr + 4);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f;
+    for (int j = 0; j < HD; j += 8) {
+      f32x4 n0 = k0, n1 = k1;
+      if (j + 8 < HD) n0 = ld4(kr + j + 8), n1 = ld4(kr + j + 12);
 #pragma unroll
-    for (int j = 0; j < HD; j += 4) {
-      const f32x4 kk = ld4(kt + l32 * PITCH + hh * HD + j);
+      for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(k0[e], q[j + e], s, 0, 0, 0);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[e], q[j + e], s, 0, 0, 0);
+      for (int e = 0; e < 4; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(k1[e], q[j + 4 + e], s, 0, 0, 0);
+      k0 = n0, k1 = n1;
     }
     // register i: key 8*(i/4) + 4*hh + i%4 of the tile, query l32
     float mt = kNegInf;
@@ -157,36 +180,46 @@ __global__ __launch_bounds__(256) void fwd_f32_kernel(F32Args a) {
         mt = fmaxf(mt, s[4 * g + r]);
       }
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));  // the query's other 16 keys
-    const float mn = fmaxf(m, mt);
-    const float alpha = (m == kNegInf || mn == kNegInf) ? 0.f : exp2f((m - mn) * a.c);
-    l *= alpha;
+    mt = halves_max(mt);  // the query's other 16 keys
+    // (mt - m)*c is NaN when both are -inf (no key yet: nothing to raise)
+    if (__builtin_amdgcn_ballot_w64((mt - m) * a.c > 8.f)) {
+      const float mn = fmaxf(m, mt);
+      const float alpha = (m == kNegInf || mn == kNegInf) ? 0.f : __builtin_amdgcn_exp2f((m - mn) * a.c);
+      l *= alpha;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-    m = mn;
+        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+      m = mn;
+    }
+    const float mc = m * a.c;
     f32x16 p;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      p[i] = mn == kNegInf ? 0.f : exp2f((s[i] - mn) * a.c);
+      p[i] = m == kNegInf ? 0.f : __builtin_amdgcn_exp2f(fmaf(s[i], a.c, -mc));
       l += p[i];
     }
-    // O^T += V^T P^T: k-step j takes keys 8*(j/4) + j%4 (+4 for lanes 32-63),
-    // this lane's register j of P; A is channel 32*dt + l32 of that key.
+    // O^T += V^T P^T: k-step j takes key 8*(j/4) + 4*hh + j%4, this lane's
+    // register j of P; A is channel 32*dt + l32 of that key.
+    const float* vr = vs[buf] + 4 * hh * D + l32 * DT;
+    auto vkey = [&](int j) { return *reinterpret_cast<const vdt*>(vr + (8 * (j / 4) + (j % 4)) * D); };
+    vdt v0 = vkey(0), v1 = vkey(1);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int key = 8 * (j / 4) + 4 * hh + (j % 4);
+    for (int j = 0; j < 16; j += 2) {
+      vdt n0 = v0, n1 = v1;
+      if (j + 2 < 16) n0 = vkey(j + 2), n1 = vkey(j + 3);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[key * PITCH + 32 * dt + l32], p[j], o[dt], 0, 0, 0);
+      for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(v0[dt], p[j], o[dt], 0, 0, 0);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1[dt], p[j + 1], o[dt], 0, 0, 0);
+      v0 = n0, v1 = n1;
     }
     if (t + 1 < ntile) store(buf ^ 1);
   }
 
   // The row sum over both halves of the keys; l > 0: normal row; l == 0: no
   // valid key (out 0, lse -inf); NaN: a NaN or +inf score reached the row.
-  l += __shfl_xor(l, 32);
+  l = halves_sum(l);
   if (!valid) return;
   const float nan = __builtin_nanf("");
   const float inv = l > 0.f ? 1.f / l : (l == 0.f ? 0.f : nan);
@@ -240,47 +273,86 @@ __global__ __launch_bounds__(256) void bwd_pre_f32_kernel(F32Args a) {
 }
 
 
-// dK/dV on the fp32 matrix cores: one wave per 32 keys (lane l%32's key in
-// registers, its half of head_dim as B operands), 32-row query tiles of Q
-// and dO through LDS.  S = Q K^T and dP = dO V^T put row 8*(i/4) + 4*(l/32)
-// + i%4 of the tile in register i of lane l, against the lane's key: so P
-// and dS registers j are the A operands of dV += P^T dO and dK += dS^T Q in
-// k-step j as they stand.
+// Backward tiles of 32 rows sit in LDS with channel 32*t + m of a row at
+// m*(D/32) + t (rows padded by 4 floats), so one read gives a lane either the
+// D/32 channels 32*t + m its products against a row take, or, for the
+// contraction over head_dim, the channels of D/32 k-steps: k-step D/32*u + e
+// contracts channels 32*e + u (lanes 0-31) and 32*e + u + 16 (lanes 32-63),
+// and the operands held in registers follow the same order.
 template <int D>
-__global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
+__device__ __forceinline__ void load_row_ksteps(float (&r)[D / 2], const float* p, bool in, int hh) {
+  constexpr int DT = D / 32;
+#pragma unroll
+  for (int u = 0; u < 16; ++u)
+#pragma unroll
+    for (int e = 0; e < DT; ++e) r[DT * u + e] = in ? p[32 * e + u + 16 * hh] : 0.f;
+}
+
+// Staging of one 32-row tile in that layout by 512 threads: thread slot v =
+// tid + 512*i holds row v/32, channels 32*t + v%32.
+template <int D>
+struct Tile32 {
+  static constexpr int DT = D / 32, PITCH = D + 4, SL = 32 * 32 / 512;
+  using vdt = float __attribute__((ext_vector_type(DT)));
+  float x[SL][DT];
+  __device__ __forceinline__ void fetch(const float* base, int64_t rs, int r0, int n, int tid) {
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+      const int v = tid + 512 * i, row = r0 + v / 32;
+      const float* p = base + (int64_t)row * rs + (v % 32);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) x[i][t] = row < n ? p[32 * t] : 0.f;
+    }
+  }
+  __device__ __forceinline__ void store(float* tile, int tid) const {
+#pragma unroll
+    for (int i = 0; i < SL; ++i) {
+      const int v = tid + 512 * i;
+      vdt y;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) y[t] = x[i][t];
+      *reinterpret_cast<vdt*>(tile + (v / 32) * PITCH + (v % 32) * DT) = y;
+    }
+  }
+};
+
+// dK/dV on the fp32 matrix cores: per 32 keys a pair of waves on one SIMD,
+// eight waves per workgroup.  The P wave holds the keys' K halves (B
+// operands) and the dV accumulators: S = Q K^T, P = exp2(S*c - lse2), dV +=
+// P^T dO.  The dS wave holds the V halves and the dK accumulators: dP = dO
+// V^T, dS = P*(dP + ndelta) with P handed over through LDS (the two waves
+// hold the same key and rows in the same lanes and registers), dK += dS^T Q.
+// S and dP put row 8*(i/4) + 4*(l/32) + i%4 of the tile in register i of lane
+// l, against the lane's key, so P and dS registers j are the A operands of
+// the second products in k-step j as they stand.
+template <int D>
+__global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   constexpr int QT = 32, KPB = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
-  constexpr int PER = QT * D / 4 / 256;
+  using vdt = float __attribute__((ext_vector_type(DT)));
   __shared__ __attribute__((aligned(16))) float qs[2][QT * PITCH];
   __shared__ __attribute__((aligned(16))) float dos[2][QT * PITCH];
   __shared__ __attribute__((aligned(16))) float l2s[2][QT];
   __shared__ __attribute__((aligned(16))) float nds[2][QT];
+  __shared__ __attribute__((aligned(16))) float px[4][16 * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
+  const int pair = wave & 3, role = wave >> 2;  // role 0: P wave, 1: dS wave
   const int nkb = (a.Lk + KPB - 1) / KPB;
   const int kb = blockIdx.x % nkb, bhk = blockIdx.x / nkb;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int group = a.Hq / a.Hkv;
-  const int k0 = kb * KPB + wave * 32;  // this wave's first key
+  const int k0 = kb * KPB + pair * 32;  // the pair's first key
   const int key = k0 + l32;
   const bool kvalid = key_ok(a, b, key);
-  float kr[HD], vr[HD];  // channels hh*HD .. +HD-1 of the lane's key
-  {
-    const bool in = key < a.Lk;
-    const float* kp = a.k + b * a.ksb + hk * a.ksh + (int64_t)key * a.ksl + hh * HD;
-    const float* vp = a.v + b * a.vsb + hk * a.vsh + (int64_t)key * a.vsl + hh * HD;
+  float kv[HD];  // K (P wave) or V (dS wave) of the lane's key, k-step order
+  load_row_ksteps<D>(kv,
+                     role == 0 ? a.k + b * a.ksb + hk * a.ksh + (int64_t)key * a.ksl
+                               : a.v + b * a.vsb + hk * a.vsh + (int64_t)key * a.vsl,
+                     key < a.Lk, hh);
+  f32x16 acc[DT];  // dV (P wave) or dK (dS wave)
 #pragma unroll
-    for (int d = 0; d < HD; d += 4) {
-      const f32x4 x = in ? ld4(kp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 y = in ? ld4(vp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) kr[d + e] = x[e], vr[d + e] = y[e];
-    }
-  }
-  f32x16 dk[DT], dv[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) dk[dt][i] = 0.f, dv[dt][i] = 0.f;
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
+  float* const pxw = px[pair] + lane * 4;
 
   const int ntile = (a.Lq + QT - 1) / QT;
   for (int gi = 0; gi < group; ++gi) {
@@ -288,16 +360,11 @@ __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
     const int64_t rbase = ((int64_t)b * a.Hq + h) * a.Lq;
     const float* qb = a.q + b * a.qsb + h * a.qsh;
     const float* db = a.dout + b * a.dosb + h * a.dosh;
-    f32x4 pq[PER], pd[PER];
+    Tile32<D> sq, sd;
     float pl2 = kPosInf, pnd = 0.f;
     auto fetch = [&](int r0) {
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int u = tid + 256 * i, r = u / (D / 4), c4 = 4 * (u % (D / 4)), row = r0 + r;
-        const bool in = row < a.Lq;
-        pq[i] = in ? ld4(qb + (int64_t)row * a.qsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
-        pd[i] = in ? ld4(db + (int64_t)row * a.dosl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+      sq.fetch(qb, a.qsl, r0, a.Lq, tid);
+      sd.fetch(db, a.dosl, r0, a.Lq, tid);
       if (tid < QT) {
         const int row = r0 + tid;
         pl2 = row < a.Lq ? a.lse2[rbase + row] : kPosInf;  // rows past the end get P = 0
@@ -305,12 +372,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
       }
     };
     auto store = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int u = tid + 256 * i, r = u / (D / 4), c4 = 4 * (u % (D / 4));
-        st4(&qs[buf][r * PITCH + c4], pq[i]);
-        st4(&dos[buf][r * PITCH + c4], pd[i]);
-      }
+      sq.store(qs[buf], tid);
+      sd.store(dos[buf], tid);
       if (tid < QT) l2s[buf][tid] = pl2, nds[buf][tid] = pnd;
     };
     __syncthreads();  // the previous head's last tiles are consumed
@@ -320,126 +383,117 @@ __global__ __launch_bounds__(256) void bwd_dkdv_f32_kernel(F32Args a) {
       const int buf = t & 1;
       __syncthreads();  // tile t stored; every wave is done with tile t - 1
       if (t + 1 < ntile) fetch((t + 1) * QT);
-      const float* qt = qs[buf];
-      const float* dt_ = dos[buf];
-      f32x16 s, dp;
+      // S = Q K^T (P wave) or dP = dO V^T (dS wave)
+      const float* at = (role == 0 ? qs[buf] : dos[buf]) + l32 * PITCH + 16 * hh * DT;
+      f32x16 s = zero16();
 #pragma unroll
-      for (int i = 0; i < 16; ++i) s[i] = 0.f, dp[i] = 0.f;
+      for (int u = 0; u < 16; ++u) {
+        const vdt x = *reinterpret_cast<const vdt*>(at + u * DT);
 #pragma unroll
-      for (int j = 0; j < HD; j += 4) {
-        const f32x4 x = ld4(qt + l32 * PITCH + hh * HD + j);
-        const f32x4 y = ld4(dt_ + l32 * PITCH + hh * HD + j);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s = __builtin_amdgcn_mfma_f32_32x32x2f32(x[e], kr[j + e], s, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_32x32x2f32(y[e], vr[j + e], dp, 0, 0, 0);
-        }
+        for (int e = 0; e < DT; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(x[e], kv[DT * u + e], s, 0, 0, 0);
       }
       // register i: row 8*(i/4) + 4*hh + i%4 of the tile, this lane's key
-      f32x16 p, ds;
+      f32x16 w;
+      if (role == 0) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 L = ld4(&l2s[buf][8 * g + 4 * hh]);
-        const f32x4 N = ld4(&nds[buf][8 * g + 4 * hh]);
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 L = ld4(&l2s[buf][8 * g + 4 * hh]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 4 * g + r;
-          p[i] = kvalid ? exp2f(s[i] * a.c - L[r]) : 0.f;
-          ds[i] = p[i] * (dp[i] + N[r]);
+          for (int r = 0; r < 4; ++r)
+            w[4 * g + r] = kvalid ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + r], a.c, -L[r])) : 0.f;
+          st4(pxw + 256 * g, f32x4{w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]});
         }
       }
-      // k-step j: rows 8*(j/4) + j%4 (+4 for lanes 32-63), registers j
+      __syncthreads();  // P handed over
+      if (role == 1) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 N = ld4(&nds[buf][8 * g + 4 * hh]);
+          const f32x4 P = ld4(pxw + 256 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w[4 * g + r] = P[r] * (s[4 * g + r] + N[r]);
+        }
+      }
+      // dV += P^T dO (P wave) or dK += dS^T Q (dS wave); k-step j: rows
+      // 8*(j/4) + j%4 (+4 for lanes 32-63), registers j
+      const float* bt = (role == 0 ? dos[buf] : qs[buf]) + l32 * DT;
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int row = 8 * (j / 4) + 4 * hh + (j % 4);
+        const vdt y = *reinterpret_cast<const vdt*>(bt + row * PITCH);
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-          dv[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(p[j], dt_[row * PITCH + 32 * d + l32], dv[d], 0, 0, 0);
-          dk[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[j], qt[row * PITCH + 32 * d + l32], dk[d], 0, 0, 0);
-        }
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[j], y[dt], acc[dt], 0, 0, 0);
       }
       if (t + 1 < ntile) store(buf ^ 1);
     }
   }
-  // dk[d] / dv[d] register i: key k0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32.
+  // acc[d] register i: key k0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32.
   // Masked keys: exactly zero (their P is 0; a non-finite dO or V elsewhere
   // in the row must not reach them through 0 * inf).
+  float* const gb = role == 0 ? a.dv + b * a.dvsb + hk * a.dvsh : a.dk + b * a.dksb + hk * a.dksh;
+  const int64_t gs = role == 0 ? a.dvsl : a.dksl;
+  const float f = role == 0 ? 1.f : a.scale;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int kk = k0 + 8 * (i / 4) + 4 * hh + (i % 4);
     if (kk >= a.Lk) continue;
     const bool ok = key_ok(a, b, kk);
-    float* kp = a.dk + b * a.dksb + hk * a.dksh + (int64_t)kk * a.dksl + l32;
-    float* vp = a.dv + b * a.dvsb + hk * a.dvsh + (int64_t)kk * a.dvsl + l32;
+    float* gp = gb + (int64_t)kk * gs + l32;
 #pragma unroll
-    for (int d = 0; d < DT; ++d) {
-      kp[32 * d] = ok ? dk[d][i] * a.scale : 0.f;
-      vp[32 * d] = ok ? dv[d][i] : 0.f;
-    }
+    for (int d = 0; d < DT; ++d) gp[32 * d] = ok ? acc[d][i] * f : 0.f;
   }
 }
 
-// dQ on the fp32 matrix cores: one wave per 32 query rows (q and dO halves
-// as B operands), 32-key tiles of K and V through LDS.  S^T = K Q^T and
-// dP^T = V dO^T put key 8*(i/4) + 4*(l/32) + i%4 in register i of lane l,
-// against the lane's row, so dS register j is the A operand of dQ += dS K
+// dQ on the fp32 matrix cores: per 32 query rows a pair of waves on one
+// SIMD, eight waves per workgroup, 32-key tiles of K and V through LDS.  One
+// wave holds the rows' q halves and forms S^T = K Q^T and P, the other holds
+// the dO halves and forms dP^T = V dO^T; both put key 8*(i/4) + 4*(l/32) +
+// i%4 in register i of lane l against the lane's row.  They exchange P and dP
+// through LDS, both form dS = P*(dP + ndelta) (the same bits), and each adds
+// dS K into half of dQ's channel blocks, dS register j being the A operand
 // in k-step j.
 template <int D>
-__global__ __launch_bounds__(256) void bwd_dq_f32_kernel(F32Args a) {
-  constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
-  constexpr int PER = KT * D / 4 / 256;
+__global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
+  constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32, DH = DT / 2;
+  using vdt = float __attribute__((ext_vector_type(DT)));
   __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
   __shared__ __attribute__((aligned(16))) float vs[2][KT * PITCH];
   __shared__ __attribute__((aligned(16))) float kok[2][KT];  // 1: valid key, 0: masked or past the end
+  __shared__ __attribute__((aligned(16))) float xs[2][4][16 * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
+  const int pair = wave & 3, role = wave >> 2;  // role 0: q and P, 1: dO and dP
   const int nqb = (a.Lq + ROWS - 1) / ROWS;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
   const int b = bh / a.Hq, h = bh % a.Hq, hk = h / (a.Hq / a.Hkv);
-  const int r0 = qb * ROWS + wave * 32;  // this wave's first row
+  const int r0 = qb * ROWS + pair * 32;  // the pair's first row
   const int row = r0 + l32;
   const bool valid = row < a.Lq;
-  float qr[HD], gr[HD];
-  {
-    const float* qp = a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl + hh * HD;
-    const float* dp = a.dout + b * a.dosb + h * a.dosh + (int64_t)row * a.dosl + hh * HD;
-#pragma unroll
-    for (int d = 0; d < HD; d += 4) {
-      const f32x4 x = valid ? ld4(qp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x4 y = valid ? ld4(dp + d) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) qr[d + e] = x[e], gr[d + e] = y[e];
-    }
-  }
+  float qg[HD];  // q (role 0) or dO (role 1) of the lane's row, k-step order
+  load_row_ksteps<D>(qg,
+                     role == 0 ? a.q + b * a.qsb + h * a.qsh + (int64_t)row * a.qsl
+                               : a.dout + b * a.dosb + h * a.dosh + (int64_t)row * a.dosl,
+                     valid, hh);
   const int64_t rr = (int64_t)bh * a.Lq + row;
   const float l2 = valid ? a.lse2[rr] : kPosInf;
   const float nd = valid ? a.ndelta[rr] : 0.f;
-  f32x16 dq[DT];
+  f32x16 dq[DH];  // channel blocks role*DH .. +DH-1
 #pragma unroll
-  for (int d = 0; d < DT; ++d)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) dq[d][i] = 0.f;
+  for (int d = 0; d < DH; ++d) dq[d] = zero16();
   const float* kb = a.k + b * a.ksb + hk * a.ksh;
   const float* vb = a.v + b * a.vsb + hk * a.vsh;
-  f32x4 pk[PER], pv[PER];
+  float* const mine = xs[role][pair] + lane * 4;
+  const float* const other = xs[role ^ 1][pair] + lane * 4;
+  Tile32<D> sk, sv;
   float pok = 0.f;
   auto fetch = [&](int c0) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4)), key = c0 + j;
-      const bool in = key < a.Lk;
-      pk[i] = in ? ld4(kb + (int64_t)key * a.ksl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
-      pv[i] = in ? ld4(vb + (int64_t)key * a.vsl + c4) : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    sk.fetch(kb, a.ksl, c0, a.Lk, tid);
+    sv.fetch(vb, a.vsl, c0, a.Lk, tid);
     if (tid < KT) pok = key_ok(a, b, c0 + tid) ? 1.f : 0.f;
   };
   auto store = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = tid + 256 * i, j = u / (D / 4), c4 = 4 * (u % (D / 4));
-      st4(&ks[buf][j * PITCH + c4], pk[i]);
-      st4(&vs[buf][j * PITCH + c4], pv[i]);
-    }
+    sk.store(ks[buf], tid);
+    sv.store(vs[buf], tid);
     if (tid < KT) kok[buf][tid] = pok;
   };
   const int ntile = (a.Lk + KT - 1) / KT;
@@ -449,52 +503,56 @@ __global__ __launch_bounds__(256) void bwd_dq_f32_kernel(F32Args a) {
   }
   for (int t = 0; t < ntile; ++t) {
     const int buf = t & 1;
-    __syncthreads();
+    __syncthreads();  // tile t stored; every wave is done with tile t - 1
     if (t + 1 < ntile) fetch((t + 1) * KT);
-    const float* kt = ks[buf];
-    const float* vt = vs[buf];
-    f32x16 s, dp;
+    // S^T = K Q^T (role 0) or dP^T = V dO^T (role 1)
+    const float* at = (role == 0 ? ks[buf] : vs[buf]) + l32 * PITCH + 16 * hh * DT;
+    f32x16 s = zero16();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) s[i] = 0.f, dp[i] = 0.f;
+    for (int u = 0; u < 16; ++u) {
+      const vdt x = *reinterpret_cast<const vdt*>(at + u * DT);
 #pragma unroll
-    for (int j = 0; j < HD; j += 4) {
-      const f32x4 x = ld4(kt + l32 * PITCH + hh * HD + j);
-      const f32x4 y = ld4(vt + l32 * PITCH + hh * HD + j);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s = __builtin_amdgcn_mfma_f32_32x32x2f32(x[e], qr[j + e], s, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_32x32x2f32(y[e], gr[j + e], dp, 0, 0, 0);
-      }
+      for (int e = 0; e < DT; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(x[e], qg[DT * u + e], s, 0, 0, 0);
     }
-    // register i: key 8*(i/4) + 4*hh + i%4 of the tile, this lane's row;
-    // masked keys add nothing (dS exactly 0)
+    // register i: key 8*(i/4) + 4*hh + i%4 of the tile, this lane's row
+    if (role == 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[i] = __builtin_amdgcn_exp2f(fmaf(s[i], a.c, -l2));
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) st4(mine + 256 * g, f32x4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]});
+    __syncthreads();  // P and dP exchanged
+    // dS; masked keys add nothing (dS exactly 0)
     f32x16 ds;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const f32x4 ok = ld4(&kok[buf][8 * g + 4 * hh]);
+      const f32x4 o = ld4(other + 256 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 4 * g + r;
-        ds[i] = ok[r] != 0.f ? exp2f(s[i] * a.c - l2) * (dp[i] + nd) : 0.f;
+        const float p = role == 0 ? s[4 * g + r] : o[r], dp = role == 0 ? o[r] : s[4 * g + r];
+        ds[4 * g + r] = ok[r] != 0.f ? p * (dp + nd) : 0.f;
       }
     }
+    // dQ += dS K over this wave's channel blocks
+    const float* bt = ks[buf] + l32 * DT + role * DH;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int kk = 8 * (j / 4) + 4 * hh + (j % 4);
+      const float* y = bt + kk * PITCH;
 #pragma unroll
-      for (int d = 0; d < DT; ++d)
-        dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[j], kt[kk * PITCH + 32 * d + l32], dq[d], 0, 0, 0);
+      for (int d = 0; d < DH; ++d) dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[j], y[d], dq[d], 0, 0, 0);
     }
     if (t + 1 < ntile) store(buf ^ 1);
   }
-  // dq[d] register i: row r0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32
+  // dq[d] register i: row r0 + 8*(i/4) + 4*hh + i%4, channel 32*(role*DH + d) + l32
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int rw = r0 + 8 * (i / 4) + 4 * hh + (i % 4);
     if (rw >= a.Lq) continue;
-    float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)rw * a.dqsl + l32;
+    float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)rw * a.dqsl + l32 + 32 * role * DH;
 #pragma unroll
-    for (int d = 0; d < DT; ++d) op[32 * d] = dq[d][i] * a.scale;
+    for (int d = 0; d < DH; ++d) op[32 * d] = dq[d][i] * a.scale;
   }
 }
 
@@ -586,9 +644,9 @@ void launch_bwd_f32(const F32Args& a, hipStream_t s) {
   const int64_t rows = (int64_t)a.B * a.Hq * a.Lq;
   hipLaunchKernelGGL(bwd_pre_f32_kernel<D>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a);
   const int nkb = (a.Lk + 127) / 128;
-  hipLaunchKernelGGL(bwd_dkdv_f32_kernel<D>, dim3((unsigned)(nkb * a.B * a.Hkv)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(bwd_dkdv_f32_kernel<D>, dim3((unsigned)(nkb * a.B * a.Hkv)), dim3(512), 0, s, a);
   const int nqb = (a.Lq + 127) / 128;
-  hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(512), 0, s, a);
 }
 
 }  // namespace
