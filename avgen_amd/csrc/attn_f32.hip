@@ -324,16 +324,18 @@ struct Tile32 {
 // hold the same key and rows in the same lanes and registers), dK += dS^T Q.
 // S and dP put row 8*(i/4) + 4*(l/32) + i%4 of the tile in register i of lane
 // l, against the lane's key, so P and dS registers j are the A operands of
-// the second products in k-step j as they stand.
+// the second products in k-step j as they stand.  The dS wave runs its dS
+// step one tile behind (Q tiles in three slots, P in two), so one barrier
+// per tile serves the staging and the hand-over.
 template <int D>
 __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   constexpr int QT = 32, KPB = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
   using vdt = float __attribute__((ext_vector_type(DT)));
-  __shared__ __attribute__((aligned(16))) float qs[2][QT * PITCH];
+  __shared__ __attribute__((aligned(16))) float qs[3][QT * PITCH];
   __shared__ __attribute__((aligned(16))) float dos[2][QT * PITCH];
   __shared__ __attribute__((aligned(16))) float l2s[2][QT];
-  __shared__ __attribute__((aligned(16))) float nds[2][QT];
-  __shared__ __attribute__((aligned(16))) float px[4][16 * 64];
+  __shared__ __attribute__((aligned(16))) float nds[3][QT];
+  __shared__ __attribute__((aligned(16))) float px[2][4][16 * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const int pair = wave & 3, role = wave >> 2;  // role 0: P wave, 1: dS wave
@@ -352,7 +354,31 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   f32x16 acc[DT];  // dV (P wave) or dK (dS wave)
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = zero16();
-  float* const pxw = px[pair] + lane * 4;
+
+  // dV += P^T dO (P wave) or dK += dS^T Q (dS wave) over one tile; k-step j:
+  // rows 8*(j/4) + j%4 (+4 for lanes 32-63), registers j
+  auto second = [&](const f32x16& w, const float* tile) {
+    const float* bt = tile + l32 * DT;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const vdt y = *reinterpret_cast<const vdt*>(bt + (8 * (j / 4) + 4 * hh + (j % 4)) * PITCH);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[j], y[dt], acc[dt], 0, 0, 0);
+    }
+  };
+  // dS of tile u from its P (LDS) and dP (registers), then dK
+  auto ds_step = [&](const f32x16& dp, int u) {
+    const float* pp = px[u & 1][pair] + lane * 4;
+    f32x16 w;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 N = ld4(&nds[u % 3][8 * g + 4 * hh]);
+      const f32x4 P = ld4(pp + 256 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) w[4 * g + r] = P[r] * (dp[4 * g + r] + N[r]);
+    }
+    second(w, qs[u % 3]);
+  };
 
   const int ntile = (a.Lq + QT - 1) / QT;
   for (int gi = 0; gi < group; ++gi) {
@@ -371,61 +397,48 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
         pnd = row < a.Lq ? a.ndelta[rbase + row] : 0.f;
       }
     };
-    auto store = [&](int buf) {
-      sq.store(qs[buf], tid);
-      sd.store(dos[buf], tid);
-      if (tid < QT) l2s[buf][tid] = pl2, nds[buf][tid] = pnd;
+    auto store = [&](int u) {
+      sq.store(qs[u % 3], tid);
+      sd.store(dos[u & 1], tid);
+      if (tid < QT) l2s[u & 1][tid] = pl2, nds[u % 3][tid] = pnd;
     };
     __syncthreads();  // the previous head's last tiles are consumed
     fetch(0);
     store(0);
+    f32x16 s;
     for (int t = 0; t < ntile; ++t) {
-      const int buf = t & 1;
-      __syncthreads();  // tile t stored; every wave is done with tile t - 1
+      // tile t stored, P of tile t-1 handed over; every wave is done with
+      // the slots the next store reuses
+      __syncthreads();
       if (t + 1 < ntile) fetch((t + 1) * QT);
+      if (role == 1 && t > 0) ds_step(s, t - 1);
       // S = Q K^T (P wave) or dP = dO V^T (dS wave)
-      const float* at = (role == 0 ? qs[buf] : dos[buf]) + l32 * PITCH + 16 * hh * DT;
-      f32x16 s = zero16();
+      const float* at = (role == 0 ? qs[t % 3] : dos[t & 1]) + l32 * PITCH + 16 * hh * DT;
+      s = zero16();
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const vdt x = *reinterpret_cast<const vdt*>(at + u * DT);
 #pragma unroll
         for (int e = 0; e < DT; ++e) s = __builtin_amdgcn_mfma_f32_32x32x2f32(x[e], kv[DT * u + e], s, 0, 0, 0);
       }
-      // register i: row 8*(i/4) + 4*hh + i%4 of the tile, this lane's key
-      f32x16 w;
       if (role == 0) {
+        // register i: row 8*(i/4) + 4*hh + i%4 of the tile, this lane's key
+        f32x16 w;
+        float* pw = px[t & 1][pair] + lane * 4;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 L = ld4(&l2s[buf][8 * g + 4 * hh]);
+          const f32x4 L = ld4(&l2s[t & 1][8 * g + 4 * hh]);
 #pragma unroll
           for (int r = 0; r < 4; ++r)
             w[4 * g + r] = kvalid ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + r], a.c, -L[r])) : 0.f;
-          st4(pxw + 256 * g, f32x4{w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]});
+          st4(pw + 256 * g, f32x4{w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]});
         }
+        second(w, dos[t & 1]);
       }
-      __syncthreads();  // P handed over
-      if (role == 1) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 N = ld4(&nds[buf][8 * g + 4 * hh]);
-          const f32x4 P = ld4(pxw + 256 * g);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) w[4 * g + r] = P[r] * (s[4 * g + r] + N[r]);
-        }
-      }
-      // dV += P^T dO (P wave) or dK += dS^T Q (dS wave); k-step j: rows
-      // 8*(j/4) + j%4 (+4 for lanes 32-63), registers j
-      const float* bt = (role == 0 ? dos[buf] : qs[buf]) + l32 * DT;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int row = 8 * (j / 4) + 4 * hh + (j % 4);
-        const vdt y = *reinterpret_cast<const vdt*>(bt + row * PITCH);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[j], y[dt], acc[dt], 0, 0, 0);
-      }
-      if (t + 1 < ntile) store(buf ^ 1);
+      if (t + 1 < ntile) store(t + 1);
     }
+    __syncthreads();  // P of the last tile handed over
+    if (role == 1 && ntile > 0) ds_step(s, ntile - 1);
   }
   // acc[d] register i: key k0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32.
   // Masked keys: exactly zero (their P is 0; a non-finite dO or V elsewhere
@@ -451,15 +464,16 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
 // i%4 in register i of lane l against the lane's row.  They exchange P and dP
 // through LDS, both form dS = P*(dP + ndelta) (the same bits), and each adds
 // dS K into half of dQ's channel blocks, dS register j being the A operand
-// in k-step j.
+// in k-step j.  The dS step runs one tile behind (K tiles in three slots,
+// the exchange in two), so one barrier per tile serves both.
 template <int D>
 __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
   constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32, DH = DT / 2;
   using vdt = float __attribute__((ext_vector_type(DT)));
-  __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
+  __shared__ __attribute__((aligned(16))) float ks[3][KT * PITCH];
   __shared__ __attribute__((aligned(16))) float vs[2][KT * PITCH];
-  __shared__ __attribute__((aligned(16))) float kok[2][KT];  // 1: valid key, 0: masked or past the end
-  __shared__ __attribute__((aligned(16))) float xs[2][4][16 * 64];
+  __shared__ __attribute__((aligned(16))) float kok[3][KT];  // 1: valid key, 0: masked or past the end
+  __shared__ __attribute__((aligned(16))) float xs[2][2][4][16 * 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const int pair = wave & 3, role = wave >> 2;  // role 0: q and P, 1: dO and dP
@@ -482,8 +496,34 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
   for (int d = 0; d < DH; ++d) dq[d] = zero16();
   const float* kb = a.k + b * a.ksb + hk * a.ksh;
   const float* vb = a.v + b * a.vsb + hk * a.vsh;
-  float* const mine = xs[role][pair] + lane * 4;
-  const float* const other = xs[role ^ 1][pair] + lane * 4;
+
+  // dS of tile u from this wave's P or dP (registers) and the partner's
+  // (LDS), then dQ += dS K over this wave's channel blocks.  Masked keys add
+  // nothing (dS exactly 0).  The K reads take a lane's D/32 channels whole
+  // (conflict-free) and keep this wave's half.
+  auto ds_step = [&](const f32x16& mine, int u) {
+    const float* other = xs[u & 1][role ^ 1][pair] + lane * 4;
+    f32x16 ds;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 ok = ld4(&kok[u % 3][8 * g + 4 * hh]);
+      const f32x4 o = ld4(other + 256 * g);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = role == 0 ? mine[4 * g + r] : o[r], dp = role == 0 ? o[r] : mine[4 * g + r];
+        ds[4 * g + r] = ok[r] != 0.f ? p * (dp + nd) : 0.f;
+      }
+    }
+    const float* bt = ks[u % 3] + l32 * DT;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const vdt y = *reinterpret_cast<const vdt*>(bt + (8 * (j / 4) + 4 * hh + (j % 4)) * PITCH);
+#pragma unroll
+      for (int d = 0; d < DH; ++d)
+        dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[j], role == 0 ? y[d] : y[DH + d], dq[d], 0, 0, 0);
+    }
+  };
+
   Tile32<D> sk, sv;
   float pok = 0.f;
   auto fetch = [&](int c0) {
@@ -491,23 +531,26 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
     sv.fetch(vb, a.vsl, c0, a.Lk, tid);
     if (tid < KT) pok = key_ok(a, b, c0 + tid) ? 1.f : 0.f;
   };
-  auto store = [&](int buf) {
-    sk.store(ks[buf], tid);
-    sv.store(vs[buf], tid);
-    if (tid < KT) kok[buf][tid] = pok;
+  auto store = [&](int u) {
+    sk.store(ks[u % 3], tid);
+    sv.store(vs[u & 1], tid);
+    if (tid < KT) kok[u % 3][tid] = pok;
   };
   const int ntile = (a.Lk + KT - 1) / KT;
   if (ntile > 0) {
     fetch(0);
     store(0);
   }
+  f32x16 s;
   for (int t = 0; t < ntile; ++t) {
-    const int buf = t & 1;
-    __syncthreads();  // tile t stored; every wave is done with tile t - 1
+    // tile t stored, tile t-1's P and dP exchanged; every wave is done with
+    // the slots the next store reuses
+    __syncthreads();
     if (t + 1 < ntile) fetch((t + 1) * KT);
+    if (t > 0) ds_step(s, t - 1);
     // S^T = K Q^T (role 0) or dP^T = V dO^T (role 1)
-    const float* at = (role == 0 ? ks[buf] : vs[buf]) + l32 * PITCH + 16 * hh * DT;
-    f32x16 s = zero16();
+    const float* at = (role == 0 ? ks[t % 3] : vs[t & 1]) + l32 * PITCH + 16 * hh * DT;
+    s = zero16();
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const vdt x = *reinterpret_cast<const vdt*>(at + u * DT);
@@ -519,32 +562,13 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s[i] = __builtin_amdgcn_exp2f(fmaf(s[i], a.c, -l2));
     }
+    float* mine = xs[t & 1][role][pair] + lane * 4;
 #pragma unroll
     for (int g = 0; g < 4; ++g) st4(mine + 256 * g, f32x4{s[4 * g], s[4 * g + 1], s[4 * g + 2], s[4 * g + 3]});
-    __syncthreads();  // P and dP exchanged
-    // dS; masked keys add nothing (dS exactly 0)
-    f32x16 ds;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 ok = ld4(&kok[buf][8 * g + 4 * hh]);
-      const f32x4 o = ld4(other + 256 * g);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = role == 0 ? s[4 * g + r] : o[r], dp = role == 0 ? o[r] : s[4 * g + r];
-        ds[4 * g + r] = ok[r] != 0.f ? p * (dp + nd) : 0.f;
-      }
-    }
-    // dQ += dS K over this wave's channel blocks
-    const float* bt = ks[buf] + l32 * DT + role * DH;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int kk = 8 * (j / 4) + 4 * hh + (j % 4);
-      const float* y = bt + kk * PITCH;
-#pragma unroll
-      for (int d = 0; d < DH; ++d) dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[j], y[d], dq[d], 0, 0, 0);
-    }
-    if (t + 1 < ntile) store(buf ^ 1);
+    if (t + 1 < ntile) store(t + 1);
   }
+  __syncthreads();  // the last tile's P and dP exchanged
+  if (ntile > 0) ds_step(s, ntile - 1);
   // dq[d] register i: row r0 + 8*(i/4) + 4*hh + i%4, channel 32*(role*DH + d) + l32
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
