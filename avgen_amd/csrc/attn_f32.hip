@@ -10,14 +10,15 @@
 //   * forward: one wave per 32 query rows, 32-key tiles of K and V through
 //     LDS, the online softmax in the exp2 domain;
 //   * backward, without atomics: row statistics (lse2 = lse*log2 e, +inf
-//     for a row without keys; ndelta = -rowsum(dO*O)), then dK/dV with one
-//     wave per 32 keys looping over 32-row query tiles of every query head
-//     of its group, and dQ with one wave per 32 query rows looping over
-//     32-key tiles;
+//     for a row without keys; ndelta = -rowsum(dO*O)), then dK/dV with a
+//     pair of waves per 32 keys looping over 32-row query tiles of every
+//     query head of its group, and dQ with a pair of waves per 32 query rows
+//     looping over 32-key tiles;
 //   * the interleaved-pair rotation of fp32 tensors (and its transpose),
 //     with the reference's operation order (two products, one sum, no FMA).
-// They are the exact-dtype path for fp32 callers at moderate sizes; the
-// bf16 kernels are the fast path.
+// Every kernel is sized for two waves per SIMD (at most 256 registers).
+// They are the exact-dtype path for fp32 callers; the bf16 kernels are the
+// fast path.
 #include "avattn.h"
 
 #include <math.h>
