@@ -194,6 +194,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr],
     ),
     "avattn_bwd_f32_workspace_size": (c_size, [c_i32, c_i32, c_i32]),
+    "avattn_bwd_f32_staged_workspace_size": (c_size, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "avattn_bwd_f32": (
         ctypes.c_int,
         [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,

@@ -46,6 +46,12 @@ struct F32Args {
   float *dq, *dk, *dv;
   int64_t dqsb, dqsh, dqsl, dksb, dksh, dksl, dvsb, dvsh, dvsl;
   float *lse2, *ndelta;  // workspace, (B, Hq, Lq) each
+  // staged dS: pairs pair0 .. of this pass, dsp floats per (batch, kv head)
+  // pair, 32x32 row-major blocks ordered (query head of the group, row tile,
+  // key tile) with ceil(Lq/32) row tiles and 4*ceil(Lk/128) key tiles
+  float* ds;
+  int64_t dsp;
+  int pair0;
 };
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
@@ -327,8 +333,9 @@ struct Tile32 {
 // l, against the lane's key, so P and dS registers j are the A operands of
 // the second products in k-step j as they stand.  The dS wave runs its dS
 // step one tile behind (Q tiles in three slots, P in two), so one barrier
-// per tile serves the staging and the hand-over.
-template <int D>
+// per tile serves the staging and the hand-over.  STAGE: the dS wave also
+// stores dS (0 for masked keys) for bwd_dq_ds_f32_kernel.
+template <int D, bool STAGE>
 __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   constexpr int QT = 32, KPB = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
   using vdt = float __attribute__((ext_vector_type(DT)));
@@ -341,7 +348,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   const int l32 = lane & 31, hh = lane >> 5;
   const int pair = wave & 3, role = wave >> 2;  // role 0: P wave, 1: dS wave
   const int nkb = (a.Lk + KPB - 1) / KPB;
-  const int kb = blockIdx.x % nkb, bhk = blockIdx.x / nkb;
+  const int kb = blockIdx.x % nkb, bhk = a.pair0 + blockIdx.x / nkb;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int group = a.Hq / a.Hkv;
   const int k0 = kb * KPB + pair * 32;  // the pair's first key
@@ -367,8 +374,12 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
       for (int dt = 0; dt < DT; ++dt) acc[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(w[j], y[dt], acc[dt], 0, 0, 0);
     }
   };
-  // dS of tile u from its P (LDS) and dP (registers), then dK
-  auto ds_step = [&](const f32x16& dp, int u) {
+  // dS of tile u from its P (LDS) and dP (registers), then dK; staged: dS
+  // row 8*(i/4) + 4*hh + i%4, this lane's key, to block (gi, u, key tile)
+  const int nrt = (a.Lq + 31) / 32, nkt = 4 * nkb;
+  float* dsw = nullptr;
+  if constexpr (STAGE) dsw = a.ds + (bhk - a.pair0) * a.dsp + (int64_t)(kb * 4 + pair) * 1024 + l32;
+  auto ds_step = [&](const f32x16& dp, int u, int gi) {
     const float* pp = px[u & 1][pair] + lane * 4;
     f32x16 w;
 #pragma unroll
@@ -377,6 +388,11 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
       const f32x4 P = ld4(pp + 256 * g);
 #pragma unroll
       for (int r = 0; r < 4; ++r) w[4 * g + r] = P[r] * (dp[4 * g + r] + N[r]);
+    }
+    if constexpr (STAGE) {
+      float* o = dsw + ((int64_t)gi * nrt + u) * nkt * 1024;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[(8 * (i / 4) + 4 * hh + (i % 4)) * 32] = kvalid ? w[i] : 0.f;
     }
     second(w, qs[u % 3]);
   };
@@ -412,7 +428,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
       // the slots the next store reuses
       __syncthreads();
       if (t + 1 < ntile) fetch((t + 1) * QT);
-      if (role == 1 && t > 0) ds_step(s, t - 1);
+      if (role == 1 && t > 0) ds_step(s, t - 1, gi);
       // S = Q K^T (P wave) or dP = dO V^T (dS wave)
       const float* at = (role == 0 ? qs[t % 3] : dos[t & 1]) + l32 * PITCH + 16 * hh * DT;
       s = zero16();
@@ -439,7 +455,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
       if (t + 1 < ntile) store(t + 1);
     }
     __syncthreads();  // P of the last tile handed over
-    if (role == 1 && ntile > 0) ds_step(s, ntile - 1);
+    if (role == 1 && ntile > 0) ds_step(s, ntile - 1, gi);
   }
   // acc[d] register i: key k0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32.
   // Masked keys: exactly zero (their P is 0; a non-finite dO or V elsewhere
@@ -581,6 +597,71 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
   }
 }
 
+// dQ = scale * dS K from the staged dS: eight waves per workgroup, 32 query
+// rows each, 32-key tiles of K in LDS (the backward tile layout).  A lane
+// reads its row's dS over keys 16*(l/32) .. +15 of a tile (64 contiguous
+// bytes of the tile's 32x32 block) straight into registers, a tile ahead;
+// k-step j contracts keys j and 16 + j, so one LDS read gives the lane its
+// D/32 channel blocks of K's row 16*(l/32) + j.
+template <int D>
+__global__ __launch_bounds__(512) void bwd_dq_ds_f32_kernel(F32Args a) {
+  constexpr int KT = 32, ROWS = 256, PITCH = D + 4, DT = D / 32;
+  using vdt = float __attribute__((ext_vector_type(DT)));
+  __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  const int group = a.Hq / a.Hkv;
+  const int nrb = (a.Lq + ROWS - 1) / ROWS;
+  const int rb = blockIdx.x % nrb, pg = blockIdx.x / nrb;
+  const int gi = pg % group, bhk = a.pair0 + pg / group;
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv, h = hk * group + gi;
+  const int r0 = rb * ROWS + wave * 32;  // this wave's first row
+  const int nrt = (a.Lq + 31) / 32, nkt = 4 * ((a.Lk + 127) / 128), ntile = (a.Lk + KT - 1) / KT;
+  const bool rows_in = r0 < a.Lq;
+  // this lane's dS: row r0 + l32, keys 16*hh .. of key tile t at dsr + 1024*t
+  const float* dsr = a.ds + (bhk - a.pair0) * a.dsp + ((int64_t)gi * nrt + r0 / 32) * nkt * 1024 + l32 * 32 + 16 * hh;
+  f32x16 dq[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) dq[d] = zero16();
+  const float* kb = a.k + b * a.ksb + hk * a.ksh;
+  Tile32<D> sk;
+  f32x4 pa[4];
+  auto fetch = [&](int t) {
+    sk.fetch(kb, a.ksl, t * KT, a.Lk, tid);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pa[e] = rows_in ? ld4(dsr + (int64_t)t * 1024 + 4 * e) : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  if (ntile > 0) {
+    fetch(0);
+    sk.store(ks[0], tid);
+  }
+  for (int t = 0; t < ntile; ++t) {
+    const int buf = t & 1;
+    __syncthreads();  // tile t stored; every wave is done with tile t - 1
+    f32x4 ca[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ca[e] = pa[e];
+    if (t + 1 < ntile) fetch(t + 1);
+    const float* bt = ks[buf] + (16 * hh) * PITCH + l32 * DT;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const vdt y = *reinterpret_cast<const vdt*>(bt + j * PITCH);
+#pragma unroll
+      for (int d = 0; d < DT; ++d) dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[j / 4][j % 4], y[d], dq[d], 0, 0, 0);
+    }
+    if (t + 1 < ntile) sk.store(ks[buf ^ 1], tid);
+  }
+  // dq[d] register i: row r0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int rw = r0 + 8 * (i / 4) + 4 * hh + (i % 4);
+    if (rw >= a.Lq) continue;
+    float* op = a.dq + b * a.dqsb + h * a.dqsh + (int64_t)rw * a.dqsl + l32;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) op[32 * d] = dq[d][i] * a.scale;
+  }
+}
+
 // Zeros over a (B, H, L, D) fp32 tensor (gradients of an empty side).
 __global__ void zero_f32_kernel(float* x, int64_t sb, int64_t sh, int64_t sl, int B, int H, int L, int D) {
   const int64_t n = (int64_t)B * H * L * (D / 4);
@@ -664,14 +745,33 @@ void launch_fwd_f32(const F32Args& a, hipStream_t s) {
   hipLaunchKernelGGL(fwd_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
 }
 
+// Staged dS floats per (batch, kv head) pair (see F32Args::ds).
+int64_t ds_floats_per_pair(int group, int Lq, int Lk) {
+  return (int64_t)group * ((Lq + 31) / 32) * 32 * ((Lk + 127) / 128) * 128;
+}
+
+// pairs_per_pass 0: dQ recomputes S and dP; else dS is staged for that many
+// (batch, kv head) pairs at a time.
 template <int D>
-void launch_bwd_f32(const F32Args& a, hipStream_t s) {
+void launch_bwd_f32(F32Args a, int pairs_per_pass, hipStream_t s) {
   const int64_t rows = (int64_t)a.B * a.Hq * a.Lq;
   hipLaunchKernelGGL(bwd_pre_f32_kernel<D>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a);
   const int nkb = (a.Lk + 127) / 128;
-  hipLaunchKernelGGL(bwd_dkdv_f32_kernel<D>, dim3((unsigned)(nkb * a.B * a.Hkv)), dim3(512), 0, s, a);
-  const int nqb = (a.Lq + 127) / 128;
-  hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(512), 0, s, a);
+  const int pairs = a.B * a.Hkv;
+  if (pairs_per_pass == 0) {
+    a.pair0 = 0;
+    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, false>), dim3((unsigned)(nkb * pairs)), dim3(512), 0, s, a);
+    const int nqb = (a.Lq + 127) / 128;
+    hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(512), 0, s, a);
+    return;
+  }
+  const int group = a.Hq / a.Hkv, nrb = (a.Lq + 255) / 256;
+  for (int p0 = 0; p0 < pairs; p0 += pairs_per_pass) {
+    const int np = pairs - p0 < pairs_per_pass ? pairs - p0 : pairs_per_pass;
+    a.pair0 = p0;
+    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, true>), dim3((unsigned)(nkb * np)), dim3(512), 0, s, a);
+    hipLaunchKernelGGL(bwd_dq_ds_f32_kernel<D>, dim3((unsigned)(nrb * np * group)), dim3(512), 0, s, a);
+  }
 }
 
 }  // namespace
@@ -721,6 +821,16 @@ int avattn_fwd_f32(const float* q, const float* k, const float* v, const int64_t
 size_t avattn_bwd_f32_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q) {
   if (batch <= 0 || heads_q <= 0 || len_q <= 0) return 0;
   return 2 * r256((size_t)batch * heads_q * len_q * sizeof(float));
+}
+
+size_t avattn_bwd_f32_staged_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q,
+                                            int32_t len_k, int32_t kv_pairs_per_pass) {
+  const size_t base = avattn_bwd_f32_workspace_size(batch, heads_q, len_q);
+  if (base == 0 || heads_kv <= 0 || heads_q % heads_kv != 0 || len_k <= 0 || kv_pairs_per_pass <= 0) return base;
+  const int64_t pairs = (int64_t)batch * heads_kv;
+  const int64_t pp = kv_pairs_per_pass < pairs ? kv_pairs_per_pass : pairs;
+  return (base + 4095) / 4096 * 4096 +
+         (size_t)pp * (size_t)ds_floats_per_pair(heads_q / heads_kv, len_q, len_k) * sizeof(float);
 }
 
 int avattn_bwd_f32(const float* dout, const float* q, const float* k, const float* v, const float* out,
@@ -782,10 +892,27 @@ int avattn_bwd_f32(const float* dout, const float* q, const float* k, const floa
   a.dv = dv, a.dvsb = dv_strides[0], a.dvsh = dv_strides[1], a.dvsl = dv_strides[2];
   a.lse2 = static_cast<float*>(workspace);
   a.ndelta = a.lse2 + need / 2 / sizeof(float);
+  // Workspace beyond the statistics (from the next 4 KB) holding the staged
+  // dS of at least one (batch, kv head) pair: stage dS, in equal passes of
+  // as many pairs as fit.
+  int pp = 0;
+  {
+    const size_t off = (need + 4095) / 4096 * 4096;
+    const size_t per = (size_t)ds_floats_per_pair(heads_q / heads_kv, len_q, len_k) * sizeof(float);
+    const int64_t pairs = (int64_t)batch * heads_kv;
+    if (workspace_bytes >= off + per) {
+      int64_t fit = (int64_t)((workspace_bytes - off) / per);
+      if (fit > pairs) fit = pairs;
+      const int64_t npass = (pairs + fit - 1) / fit;
+      pp = (int)((pairs + npass - 1) / npass);
+      a.ds = reinterpret_cast<float*>(static_cast<char*>(workspace) + off);
+      a.dsp = (int64_t)(per / sizeof(float));
+    }
+  }
   if (head_dim == 128)
-    launch_bwd_f32<128>(a, s);
+    launch_bwd_f32<128>(a, pp, s);
   else
-    launch_bwd_f32<64>(a, s);
+    launch_bwd_f32<64>(a, pp, s);
   return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
 }
 

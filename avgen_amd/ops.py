@@ -258,7 +258,7 @@ def _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale):
     dk = _f32_ready(torch.empty_like(k))
     dv = _f32_ready(torch.empty_like(v))
     lib = _lib.load()
-    ws = _workspace(lib.avattn_bwd_f32_workspace_size(B, Hq, Lq), q.device)
+    ws = _alloc_bwd_f32_workspace(B, Hq, Hkv, Lq, Lk, q.device)
     st = lib.avattn_bwd_f32(
         _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
         _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
@@ -271,6 +271,33 @@ def _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale):
     )
     _lib.check(st, name)
     return dq, dk, dv
+
+
+def f32_ds_bytes_per_pair(group, Lq, Lk):
+    """Bytes of staged fp32 dS per (batch, kv head) pair: float32 per (query
+    head of the group, query row padded to 32, key padded to 128)."""
+    return 4 * group * ((Lq + 31) // 32 * 32) * ((Lk + 127) // 128 * 128)
+
+
+def _alloc_bwd_f32_workspace(B, Hq, Hkv, Lq, Lk, device) -> torch.Tensor:
+    """The float32 backward's workspace: with the staged-dS budget (the one
+    the bf16 backward uses) holding at least one (batch, kv head) pair's fp32
+    dS, the staged size for as many pairs per pass as fit in equal passes
+    (halving while the allocator cannot provide it), else the statistics
+    alone (dq recomputes S and dP)."""
+    lib = _lib.load()
+    pairs = 0
+    if B * Hkv > 0 and Lq > 0 and Lk > 0:
+        pairs = min(B * Hkv, _ds_budget(device) // f32_ds_bytes_per_pair(Hq // Hkv, Lq, Lk))
+    if pairs > 0:
+        npass = -(-(B * Hkv) // pairs)
+        pairs = -(-(B * Hkv) // npass)
+    while pairs > 0:
+        try:
+            return _workspace(lib.avattn_bwd_f32_staged_workspace_size(B, Hq, Hkv, Lq, Lk, int(pairs)), device)
+        except torch.OutOfMemoryError:
+            pairs = 0 if pairs == 1 else (pairs + 1) // 2
+    return _workspace(lib.avattn_bwd_f32_workspace_size(B, Hq, Lq), device)
 
 
 def _check_windows(name, lo, hi, B, Lq):

@@ -43,8 +43,8 @@
  *   avattn_qk_norm_rope_bwd  then apply_rotary) and their autograd backward
  *   avattn_fwd_f32,     the same interfaces as avattn_fwd / avattn_bwd /
  *   avattn_bwd_f32,     avattn_rope_apply for float32 tensors (the
- *   avattn_rope_apply_f32  reference's attention and rotation run in the
- *                       caller's dtype)
+ *   avattn_bwd_f32_staged_workspace_size  reference's attention and
+ *   avattn_rope_apply_f32  rotation run in the caller's dtype)
  */
 #ifndef AVATTN_H
 #define AVATTN_H
@@ -636,7 +636,13 @@ int avattn_diag_dq_partials(float* acc, int32_t heads, int32_t key_blocks,
  * NaN or +inf score: NaN) are as for avattn_fwd.  The backward needs
  * avattn_bwd_f32_workspace_size() bytes of workspace (256-byte aligned:
  * the row statistics), uses no atomics and is bitwise reproducible; a
- * masked key's dk and dv are exactly 0.  Rotation: each product and sum
+ * masked key's dk and dv are exactly 0.  With a workspace of at least
+ * avattn_bwd_f32_staged_workspace_size(..., 1) bytes the dK/dV kernel also
+ * stores dS (fp32) past the statistics and dq is one product of dS with k,
+ * in equal passes of as many (batch, kv head) pairs as the workspace holds
+ * (the same results to rounding as recomputing dq, bitwise independent of
+ * the pass size); a smaller workspace recomputes S and dP for dq.
+ * Rotation: each product and sum
  * rounded on its own, no final rounding (the output is fp32), so it equals
  * torch's fp32 ops bit for bit.
  */
@@ -652,6 +658,14 @@ int avattn_fwd_f32(const float* q, const float* k, const float* v,
                    avattn_stream_t stream);
 
 size_t avattn_bwd_f32_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q);
+
+/* Workspace bytes for avattn_bwd_f32 staging the dS of kv_pairs_per_pass
+ * (batch, kv head) pairs per pass: the statistics rounded up to 4 KB, plus
+ * per pair 4 * (heads_q/heads_kv) * roundup(len_q, 32) * roundup(len_k, 128)
+ * bytes. */
+size_t avattn_bwd_f32_staged_workspace_size(int32_t batch, int32_t heads_q, int32_t heads_kv,
+                                            int32_t len_q, int32_t len_k,
+                                            int32_t kv_pairs_per_pass);
 
 int avattn_bwd_f32(const float* dout, const float* q, const float* k, const float* v,
                    const float* out, const float* lse,

@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 11
+    assert lib.avattn_abi_version() == 12
     for code in range(0, 11):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)
@@ -457,6 +457,12 @@ def _bwd_f32(lib, **over):
 def test_bwd_f32_validation_paths(lib):
     assert lib.avattn_bwd_f32_workspace_size(2, 40, 18900) == 2 * _round256(2 * 40 * 18900 * 4)
     assert lib.avattn_bwd_f32_workspace_size(0, 4, 10) == 0
+    base = 2 * _round256(2 * 40 * 18900 * 4)
+    per = 4 * 2 * 18912 * 18944  # group 2: rows to 32, keys to 128
+    assert lib.avattn_bwd_f32_staged_workspace_size(2, 40, 20, 18900, 18900, 3) == (base + 4095) // 4096 * 4096 + 3 * per
+    assert lib.avattn_bwd_f32_staged_workspace_size(2, 40, 20, 18900, 18900, 99) == (base + 4095) // 4096 * 4096 + 40 * per
+    assert lib.avattn_bwd_f32_staged_workspace_size(2, 40, 20, 18900, 18900, 0) == base
+    assert lib.avattn_bwd_f32_staged_workspace_size(0, 40, 20, 18900, 18900, 1) == 0
     assert _bwd_f32(lib, D=32) == _lib.ERR_HEAD_DIM
     assert _bwd_f32(lib, Hq=4, Hkv=3) == _lib.ERR_GQA
     assert _bwd_f32(lib, Lk=-2) == _lib.ERR_BAD_SHAPE

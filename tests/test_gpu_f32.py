@@ -63,9 +63,10 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("staged", [True, False], ids=["staged_ds", "recompute"])
 @pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,masked", CASES)
-def test_f32_forward_backward_match_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
-    print(f"f32 case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked}", flush=True)
+def test_f32_forward_backward_match_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked, staged):
+    print(f"f32 case B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} masked={masked} staged={staged}", flush=True)
     q, k, v, do = _randn((B, Hq, Lq, D), 1), _randn((B, Hkv, Lk, D), 2), _randn((B, Hkv, Lk, D), 3), _randn(
         (B, Hq, Lq, D), 4)
     mask = None
@@ -85,7 +86,12 @@ def test_f32_forward_backward_match_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
     _check_fwd(o, l, ro, rl)
     if masked and B > 1:
         assert np.all(o[-1] == 0) and np.all(np.isneginf(l[-1]))
-    dq, dk, dv = amd.ops.flash_bwd(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, mk, D ** -0.5)
+    dev = torch.device("cuda", 0)
+    amd.ops.set_ds_budget(None if staged else 0, dev)
+    try:
+        dq, dk, dv = amd.ops.flash_bwd(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, mk, D ** -0.5)
+    finally:
+        amd.ops.set_ds_budget(None, dev)
     ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), o, l, km)
     for name, got, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
         assert got.dtype is torch.float32
@@ -95,6 +101,41 @@ def test_f32_forward_backward_match_oracle(amd, B, Hq, Hkv, Lq, Lk, D, masked):
     if mask is not None:
         gone = np.broadcast_to(~mask.numpy()[:, None, :, None], dk.shape)
         assert np.all(_f64(dk)[gone] == 0) and np.all(_f64(dv)[gone] == 0)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D", [(3, 4, 2, 300, 700, 128), (2, 3, 1, 129, 250, 64)])
+def test_f32_staged_ds_passes_and_recompute(amd, B, Hq, Hkv, Lq, Lk, D):
+    """The staged-dS backward in passes of 1, some and all (batch, kv head)
+    pairs, and the recomputing one: dk and dv are the same bits every way
+    (the dK/dV kernel's arithmetic does not change when it also stores dS),
+    dq from the staged dS the same bits for every pass size (pairs are
+    independent) and within fp32 rounding of the recomputed dq."""
+    print(f"f32 staged passes B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D}", flush=True)
+    dev = torch.device("cuda", 0)
+    q, k, v, do = (_randn(s, 10 + i).cuda() for i, s in enumerate(
+        ((B, Hq, Lq, D), (B, Hkv, Lk, D), (B, Hkv, Lk, D), (B, Hq, Lq, D))))
+    g = torch.Generator()
+    g.manual_seed(11)
+    mask = (torch.rand((B, Lk), generator=g) < 0.8).cuda()
+    out, lse = amd.ops.flash_fwd(q, k, v, mask, None, None, D ** -0.5)
+    per = amd.ops.f32_ds_bytes_per_pair(Hq // Hkv, Lq, Lk)
+    runs = {}
+    for label, budget in (("recompute", 0), ("one pair", per), ("passes", 2 * per + 1), ("one pass", None)):
+        amd.ops.set_ds_budget(budget, dev)
+        try:
+            runs[label] = amd.ops.flash_bwd(do, q, k, v, out, lse, mask, D ** -0.5)
+        finally:
+            amd.ops.set_ds_budget(None, dev)
+    torch.cuda.synchronize()
+    base = runs["one pass"]
+    for label, got in runs.items():
+        assert torch.equal(got[1], base[1]) and torch.equal(got[2], base[2]), label
+        if label != "recompute":
+            assert torch.equal(got[0], base[0]), label
+    diff = (runs["recompute"][0] - base[0]).abs().max().item()
+    top = base[0].abs().max().item()
+    print(f"  dq staged vs recomputed: {diff:.3e} of {top:.3e}", flush=True)
+    assert diff <= 1e-5 * top
 
 
 def test_f32_rotation_bit_exact(amd):
