@@ -206,6 +206,29 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr, c_size,
          c_ptr],
     ),
+    "avattn_fwd_windowed_f32": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p,
+         c_ptr,
+         c_ptr],
+    ),
+    "avattn_bwd_windowed_f32": (
+        ctypes.c_int,
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr,
+         c_i64p, c_i64p, c_i64p, c_i64p, c_i64p,
+         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+         c_ptr, c_i64,
+         c_ptr, c_ptr, c_i64,
+         c_f32,
+         c_ptr, c_i64p, c_ptr, c_i64p, c_ptr, c_i64p,
+         c_ptr, c_size,
+         c_ptr],
+    ),
     "avattn_rope_apply_f32": (
         ctypes.c_int,
         [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32,

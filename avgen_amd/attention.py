@@ -10,9 +10,11 @@ Semantics kept from the reference: zero-length query or key sequences
 return ``zeros_like(query)`` (:261-262); the default scale is
 ``1/sqrt(head_dim)``; a boolean mask is ``True`` = attend.  Scope of the
 kernel (anything else raises rather than silently running elsewhere):
-bf16 tensors on a ROCm GPU (:func:`attention` and :func:`rotary_attention`
-also take float32 tensors, computed in fp32 by their own kernels, as the
-reference's SDPA computes in the caller's dtype), head_dim 64 or 128,
+bf16 tensors on a ROCm GPU (:func:`attention`, :func:`rotary_attention`,
+:func:`windowed_attention`, :func:`temporal_neighbour_attention` and
+:func:`varlen_attention` also take float32 tensors, computed in fp32 by
+their own kernels, as the reference's SDPA computes in the caller's dtype),
+head_dim 64 or 128,
 ``dropout_p == 0``,
 ``is_causal == False`` (video DiT attention is bidirectional), and masks
 that are key-padding masks — boolean, broadcastable as ``(batch, 1, 1,

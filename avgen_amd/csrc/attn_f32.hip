@@ -52,6 +52,10 @@ struct F32Args {
   float* ds;
   int64_t dsp;
   int pair0;
+  // per-row key windows (WIN kernels): row r of batch b attends keys in
+  // [wlo[b*wsb + r], whi[b*wsb + r]), clamped into 0 <= lo <= hi <= Lk
+  const int32_t *wlo, *whi;
+  int64_t wsb;
 };
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
@@ -59,6 +63,39 @@ __device__ __forceinline__ void st4(float* p, const f32x4& v) { *reinterpret_cas
 
 __device__ __forceinline__ bool key_ok(const F32Args& a, int b, int key) {
   return key < a.Lk && (a.mask == nullptr || a.mask[b * a.msb + key] != 0);
+}
+
+// The clamped key window of row r of batch b.
+__device__ __forceinline__ void row_window(const F32Args& a, int b, int r, int& lo, int& hi) {
+  const int64_t i = (int64_t)b * a.wsb + r;
+  lo = min(max(a.wlo[i], 0), a.Lk);
+  hi = min(max(a.whi[i], lo), a.Lk);
+}
+
+// The 32-key tiles [t0, t1) meeting the union of the non-empty windows held
+// by the lanes of a workgroup's NW waves (every thread calls it: it holds a
+// barrier; red: 2*NW ints of LDS).
+template <int NW>
+__device__ __forceinline__ void window_tiles(int lo, int hi, bool use, int* red, int& t0, int& t1) {
+  int mn = use && lo < hi ? lo : 0x7fffffff, mx = use && lo < hi ? hi : -1;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mn = min(mn, __shfl_xor(mn, o)), mx = max(mx, __shfl_xor(mx, o));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[wave] = mn, red[NW + wave] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) mn = min(mn, red[w]), mx = max(mx, red[NW + w]);
+  // the same in every lane; said so, so the tile loops run on scalar
+  // counters and uniform branches (barriers inside them)
+  t0 = __builtin_amdgcn_readfirstlane(mn < mx ? mn / 32 : 0);
+  t1 = __builtin_amdgcn_readfirstlane(mn < mx ? (mx + 31) / 32 : 0);
+}
+
+// Does any of the wave's rows (lanes' windows, both halves alike) meet key
+// block kb (keys [128*kb, min(128*kb + 128, Lk))?  Wave-uniform.
+__device__ __forceinline__ bool rows_meet_block(const F32Args& a, int lo, int hi, bool use, int kb) {
+  const int k0 = 128 * kb, k1 = min(k0 + 128, a.Lk);
+  return __builtin_amdgcn_ballot_w64(use && lo < k1 && hi > k0) != 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -81,8 +118,10 @@ __device__ __forceinline__ bool key_ok(const F32Args& a, int b, int key) {
 // exceeds it by more than 2^8 in the exp2 domain (any lane of the wave: the
 // branch is uniform), so the rescale of the output accumulator is rare;
 // the probabilities stay at most 2^8 and out = O / l is unchanged in exact
-// arithmetic.
-template <int D>
+// arithmetic.  WIN: per-row key windows (F32Args::wlo/whi): the workgroup
+// visits the tiles meeting its rows' windows and masks each score outside
+// its row's window.
+template <int D, bool WIN>
 __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(F32Args a) {
   constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
   constexpr int PER = KT * D / 4 / 256;  // K float4 chunks per thread and tile
@@ -153,13 +192,18 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(F32Args a) {
     if (tid < KT) bias[buf][tid] = pbias;
   };
 
-  const int ntile = (a.Lk + KT - 1) / KT;
-  if (ntile > 0) {
-    fetch(0);
+  int t0 = 0, ntile = (a.Lk + KT - 1) / KT, wl = 0, wh = a.Lk;
+  if constexpr (WIN) {
+    __shared__ int red[8];
+    if (valid) row_window(a, b, row, wl, wh);
+    window_tiles<4>(wl, wh, valid, red, t0, ntile);
+  }
+  if (t0 < ntile) {
+    fetch(t0 * KT);
     store(0);
   }
-  for (int t = 0; t < ntile; ++t) {
-    const int buf = t & 1;
+  for (int t = t0; t < ntile; ++t) {
+    const int buf = (t - t0) & 1;
     __syncthreads();  // tile t stored; every wave is done with tile t - 1
     if (t + 1 < ntile) fetch((t + 1) * KT);
     // S^T = K Q^T: k-step j takes channels j (lanes 0-31) and HD + j (32-63)
@@ -184,6 +228,10 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(F32Args a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         s[4 * g + r] += bb[r];
+        if constexpr (WIN) {
+          const int key = t * KT + 8 * g + 4 * hh + r;
+          if (key < wl || key >= wh) s[4 * g + r] = kNegInf;
+        }
         mt = fmaxf(mt, s[4 * g + r]);
       }
     }
@@ -334,8 +382,11 @@ struct Tile32 {
 // the second products in k-step j as they stand.  The dS wave runs its dS
 // step one tile behind (Q tiles in three slots, P in two), so one barrier
 // per tile serves the staging and the hand-over.  STAGE: the dS wave also
-// stores dS (0 for masked keys) for bwd_dq_ds_f32_kernel.
-template <int D, bool STAGE>
+// stores dS (0 for masked keys) for bwd_dq_ds_f32_kernel.  WIN: per-row key
+// windows, non-decreasing in the row: the workgroup visits the query tiles
+// holding the rows whose windows meet its keys (a contiguous range, found
+// by binary search) and P is 0 outside each row's window.
+template <int D, bool STAGE, bool WIN>
 __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   constexpr int QT = 32, KPB = 128, PITCH = D + 4, HD = D / 2, DT = D / 32;
   using vdt = float __attribute__((ext_vector_type(DT)));
@@ -344,6 +395,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   __shared__ __attribute__((aligned(16))) float l2s[2][QT];
   __shared__ __attribute__((aligned(16))) float nds[3][QT];
   __shared__ __attribute__((aligned(16))) float px[2][4][16 * 64];
+  __shared__ __attribute__((aligned(16))) int wls[WIN ? 2 : 1][QT], whs[WIN ? 2 : 1][QT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
   const int pair = wave & 3, role = wave >> 2;  // role 0: P wave, 1: dS wave
@@ -397,7 +449,28 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
     second(w, qs[u % 3]);
   };
 
-  const int ntile = (a.Lq + QT - 1) / QT;
+  // query tiles [tb, ntile)
+  int tb = 0, ntile = (a.Lq + QT - 1) / QT;
+  if constexpr (WIN) {
+    // rows meeting keys [K0, K1): from the first row with hi > K0 to the
+    // first with lo >= K1 (both bounds non-decreasing in the row)
+    const int K0 = kb * KPB, K1 = min(K0 + KPB, a.Lk);
+    int lo = 0, hi = a.Lq, wl, wh;
+    while (lo < hi) {
+      const int m = (lo + hi) >> 1;
+      row_window(a, b, m, wl, wh);
+      if (wh > K0) hi = m; else lo = m + 1;
+    }
+    const int r1 = lo;
+    hi = a.Lq;
+    while (lo < hi) {
+      const int m = (lo + hi) >> 1;
+      row_window(a, b, m, wl, wh);
+      if (wl >= K1) hi = m; else lo = m + 1;
+    }
+    tb = __builtin_amdgcn_readfirstlane(r1 / QT);
+    ntile = __builtin_amdgcn_readfirstlane(lo > r1 ? (lo + QT - 1) / QT : r1 / QT);
+  }
   for (int gi = 0; gi < group; ++gi) {
     const int h = hk * group + gi;
     const int64_t rbase = ((int64_t)b * a.Hq + h) * a.Lq;
@@ -405,6 +478,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
     const float* db = a.dout + b * a.dosb + h * a.dosh;
     Tile32<D> sq, sd;
     float pl2 = kPosInf, pnd = 0.f;
+    int pwl = 0, pwh = 0;
     auto fetch = [&](int r0) {
       sq.fetch(qb, a.qsl, r0, a.Lq, tid);
       sd.fetch(db, a.dosl, r0, a.Lq, tid);
@@ -412,23 +486,31 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
         const int row = r0 + tid;
         pl2 = row < a.Lq ? a.lse2[rbase + row] : kPosInf;  // rows past the end get P = 0
         pnd = row < a.Lq ? a.ndelta[rbase + row] : 0.f;
+        if constexpr (WIN) {
+          if (row < a.Lq) row_window(a, b, row, pwl, pwh);
+        }
       }
     };
     auto store = [&](int u) {
       sq.store(qs[u % 3], tid);
       sd.store(dos[u & 1], tid);
-      if (tid < QT) l2s[u & 1][tid] = pl2, nds[u % 3][tid] = pnd;
+      if (tid < QT) {
+        l2s[u & 1][tid] = pl2, nds[u % 3][tid] = pnd;
+        if constexpr (WIN) wls[u & 1][tid] = pwl, whs[u & 1][tid] = pwh;
+      }
     };
     __syncthreads();  // the previous head's last tiles are consumed
-    fetch(0);
-    store(0);
+    if (tb < ntile) {
+      fetch(tb * QT);
+      store(tb);
+    }
     f32x16 s;
-    for (int t = 0; t < ntile; ++t) {
+    for (int t = tb; t < ntile; ++t) {
       // tile t stored, P of tile t-1 handed over; every wave is done with
       // the slots the next store reuses
       __syncthreads();
       if (t + 1 < ntile) fetch((t + 1) * QT);
-      if (role == 1 && t > 0) ds_step(s, t - 1, gi);
+      if (role == 1 && t > tb) ds_step(s, t - 1, gi);
       // S = Q K^T (P wave) or dP = dO V^T (dS wave)
       const float* at = (role == 0 ? qs[t % 3] : dos[t & 1]) + l32 * PITCH + 16 * hh * DT;
       s = zero16();
@@ -446,8 +528,14 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
         for (int g = 0; g < 4; ++g) {
           const f32x4 L = ld4(&l2s[t & 1][8 * g + 4 * hh]);
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            w[4 * g + r] = kvalid ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + r], a.c, -L[r])) : 0.f;
+          for (int r = 0; r < 4; ++r) {
+            bool in = kvalid;
+            if constexpr (WIN) {
+              const int rr = 8 * g + 4 * hh + r;
+              in = in && key >= wls[t & 1][rr] && key < whs[t & 1][rr];
+            }
+            w[4 * g + r] = in ? __builtin_amdgcn_exp2f(fmaf(s[4 * g + r], a.c, -L[r])) : 0.f;
+          }
           st4(pw + 256 * g, f32x4{w[4 * g], w[4 * g + 1], w[4 * g + 2], w[4 * g + 3]});
         }
         second(w, dos[t & 1]);
@@ -455,7 +543,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
       if (t + 1 < ntile) store(t + 1);
     }
     __syncthreads();  // P of the last tile handed over
-    if (role == 1 && ntile > 0) ds_step(s, ntile - 1, gi);
+    if (role == 1 && ntile > tb) ds_step(s, ntile - 1, gi);
   }
   // acc[d] register i: key k0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32.
   // Masked keys: exactly zero (their P is 0; a non-finite dO or V elsewhere
@@ -482,8 +570,10 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
 // through LDS, both form dS = P*(dP + ndelta) (the same bits), and each adds
 // dS K into half of dQ's channel blocks, dS register j being the A operand
 // in k-step j.  The dS step runs one tile behind (K tiles in three slots,
-// the exchange in two), so one barrier per tile serves both.
-template <int D>
+// the exchange in two), so one barrier per tile serves both.  WIN: per-row
+// key windows; the workgroup visits the tiles meeting its rows' windows and
+// dS is 0 outside each row's window.
+template <int D, bool WIN>
 __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
   constexpr int KT = 32, ROWS = 128, PITCH = D + 4, HD = D / 2, DT = D / 32, DH = DT / 2;
   using vdt = float __attribute__((ext_vector_type(DT)));
@@ -508,6 +598,10 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
   const int64_t rr = (int64_t)bh * a.Lq + row;
   const float l2 = valid ? a.lse2[rr] : kPosInf;
   const float nd = valid ? a.ndelta[rr] : 0.f;
+  int wl = 0, wh = a.Lk;
+  if constexpr (WIN) {
+    if (valid) row_window(a, b, row, wl, wh);
+  }
   f32x16 dq[DH];  // channel blocks role*DH .. +DH-1
 #pragma unroll
   for (int d = 0; d < DH; ++d) dq[d] = zero16();
@@ -528,7 +622,12 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float p = role == 0 ? mine[4 * g + r] : o[r], dp = role == 0 ? o[r] : mine[4 * g + r];
-        ds[4 * g + r] = ok[r] != 0.f ? p * (dp + nd) : 0.f;
+        bool in = ok[r] != 0.f;
+        if constexpr (WIN) {
+          const int key = u * KT + 8 * g + 4 * hh + r;
+          in = in && key >= wl && key < wh;
+        }
+        ds[4 * g + r] = in ? p * (dp + nd) : 0.f;
       }
     }
     const float* bt = ks[u % 3] + l32 * DT;
@@ -553,18 +652,22 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
     sv.store(vs[u & 1], tid);
     if (tid < KT) kok[u % 3][tid] = pok;
   };
-  const int ntile = (a.Lk + KT - 1) / KT;
-  if (ntile > 0) {
-    fetch(0);
-    store(0);
+  int t0 = 0, ntile = (a.Lk + KT - 1) / KT;
+  if constexpr (WIN) {
+    __shared__ int red[16];
+    window_tiles<8>(wl, wh, valid, red, t0, ntile);
+  }
+  if (t0 < ntile) {
+    fetch(t0 * KT);
+    store(t0);
   }
   f32x16 s;
-  for (int t = 0; t < ntile; ++t) {
+  for (int t = t0; t < ntile; ++t) {
     // tile t stored, tile t-1's P and dP exchanged; every wave is done with
     // the slots the next store reuses
     __syncthreads();
     if (t + 1 < ntile) fetch((t + 1) * KT);
-    if (t > 0) ds_step(s, t - 1);
+    if (t > t0) ds_step(s, t - 1);
     // S^T = K Q^T (role 0) or dP^T = V dO^T (role 1)
     const float* at = (role == 0 ? ks[t % 3] : vs[t & 1]) + l32 * PITCH + 16 * hh * DT;
     s = zero16();
@@ -585,7 +688,7 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
     if (t + 1 < ntile) store(t + 1);
   }
   __syncthreads();  // the last tile's P and dP exchanged
-  if (ntile > 0) ds_step(s, ntile - 1);
+  if (ntile > t0) ds_step(s, ntile - 1);
   // dq[d] register i: row r0 + 8*(i/4) + 4*hh + i%4, channel 32*(role*DH + d) + l32
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -602,8 +705,10 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
 // reads its row's dS over keys 16*(l/32) .. +15 of a tile (64 contiguous
 // bytes of the tile's 32x32 block) straight into registers, a tile ahead;
 // k-step j contracts keys j and 16 + j, so one LDS read gives the lane its
-// D/32 channel blocks of K's row 16*(l/32) + j.
-template <int D>
+// D/32 channel blocks of K's row 16*(l/32) + j.  WIN: the workgroup stages
+// the tiles meeting its rows' windows, and a wave multiplies only the key
+// blocks its rows meet (the blocks the windowed dK/dV kernel wrote).
+template <int D, bool WIN>
 __global__ __launch_bounds__(512) void bwd_dq_ds_f32_kernel(F32Args a) {
   constexpr int KT = 32, ROWS = 256, PITCH = D + 4, DT = D / 32;
   using vdt = float __attribute__((ext_vector_type(DT)));
@@ -618,6 +723,18 @@ __global__ __launch_bounds__(512) void bwd_dq_ds_f32_kernel(F32Args a) {
   const int r0 = rb * ROWS + wave * 32;  // this wave's first row
   const int nrt = (a.Lq + 31) / 32, nkt = 4 * ((a.Lk + 127) / 128), ntile = (a.Lk + KT - 1) / KT;
   const bool rows_in = r0 < a.Lq;
+  const bool valid = r0 + l32 < a.Lq;
+  int wl = 0, wh = a.Lk, t0 = 0, ntile_w = ntile;
+  if constexpr (WIN) {
+    __shared__ int red[16];
+    if (valid) row_window(a, b, r0 + l32, wl, wh);
+    window_tiles<8>(wl, wh, valid, red, t0, ntile_w);
+  }
+  // does this wave multiply key tile t
+  auto takes = [&](int t) {
+    if constexpr (WIN) return rows_meet_block(a, wl, wh, valid, t / 4);
+    return rows_in;
+  };
   // this lane's dS: row r0 + l32, keys 16*hh .. of key tile t at dsr + 1024*t
   const float* dsr = a.ds + (bhk - a.pair0) * a.dsp + ((int64_t)gi * nrt + r0 / 32) * nkt * 1024 + l32 * 32 + 16 * hh;
   f32x16 dq[DT];
@@ -628,28 +745,33 @@ __global__ __launch_bounds__(512) void bwd_dq_ds_f32_kernel(F32Args a) {
   f32x4 pa[4];
   auto fetch = [&](int t) {
     sk.fetch(kb, a.ksl, t * KT, a.Lk, tid);
+    const bool take = takes(t);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pa[e] = rows_in ? ld4(dsr + (int64_t)t * 1024 + 4 * e) : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < 4; ++e) pa[e] = take ? ld4(dsr + (int64_t)t * 1024 + 4 * e) : f32x4{0.f, 0.f, 0.f, 0.f};
   };
-  if (ntile > 0) {
-    fetch(0);
+  if (t0 < ntile_w) {
+    fetch(t0);
     sk.store(ks[0], tid);
   }
-  for (int t = 0; t < ntile; ++t) {
-    const int buf = t & 1;
+  for (int t = t0; t < ntile_w; ++t) {
+    const int buf = (t - t0) & 1;
     __syncthreads();  // tile t stored; every wave is done with tile t - 1
     f32x4 ca[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) ca[e] = pa[e];
-    if (t + 1 < ntile) fetch(t + 1);
-    const float* bt = ks[buf] + (16 * hh) * PITCH + l32 * DT;
+    const bool take = takes(t);
+    if (t + 1 < ntile_w) fetch(t + 1);
+    if (take) {
+      const float* bt = ks[buf] + (16 * hh) * PITCH + l32 * DT;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const vdt y = *reinterpret_cast<const vdt*>(bt + j * PITCH);
+      for (int j = 0; j < 16; ++j) {
+        const vdt y = *reinterpret_cast<const vdt*>(bt + j * PITCH);
 #pragma unroll
-      for (int d = 0; d < DT; ++d) dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[j / 4][j % 4], y[d], dq[d], 0, 0, 0);
+        for (int d = 0; d < DT; ++d)
+          dq[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[j / 4][j % 4], y[d], dq[d], 0, 0, 0);
+      }
     }
-    if (t + 1 < ntile) sk.store(ks[buf ^ 1], tid);
+    if (t + 1 < ntile_w) sk.store(ks[buf ^ 1], tid);
   }
   // dq[d] register i: row r0 + 8*(i/4) + 4*hh + i%4, channel 32*d + l32
 #pragma unroll
@@ -739,10 +861,10 @@ int check_f32_dims(int32_t B, int32_t Hq, int32_t Hkv, int32_t Lq, int32_t Lk, i
 
 size_t r256(size_t x) { return (x + 255) / 256 * 256; }
 
-template <int D>
+template <int D, bool WIN>
 void launch_fwd_f32(const F32Args& a, hipStream_t s) {
   const int nqb = (a.Lq + 127) / 128;
-  hipLaunchKernelGGL(fwd_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((fwd_f32_kernel<D, WIN>), dim3((unsigned)(nqb * a.B * a.Hq)), dim3(256), 0, s, a);
 }
 
 // Staged dS floats per (batch, kv head) pair (see F32Args::ds).
@@ -752,7 +874,7 @@ int64_t ds_floats_per_pair(int group, int Lq, int Lk) {
 
 // pairs_per_pass 0: dQ recomputes S and dP; else dS is staged for that many
 // (batch, kv head) pairs at a time.
-template <int D>
+template <int D, bool WIN>
 void launch_bwd_f32(F32Args a, int pairs_per_pass, hipStream_t s) {
   const int64_t rows = (int64_t)a.B * a.Hq * a.Lq;
   hipLaunchKernelGGL(bwd_pre_f32_kernel<D>, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, a);
@@ -760,18 +882,28 @@ void launch_bwd_f32(F32Args a, int pairs_per_pass, hipStream_t s) {
   const int pairs = a.B * a.Hkv;
   if (pairs_per_pass == 0) {
     a.pair0 = 0;
-    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, false>), dim3((unsigned)(nkb * pairs)), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, false, WIN>), dim3((unsigned)(nkb * pairs)), dim3(512), 0, s, a);
     const int nqb = (a.Lq + 127) / 128;
-    hipLaunchKernelGGL(bwd_dq_f32_kernel<D>, dim3((unsigned)(nqb * a.B * a.Hq)), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((bwd_dq_f32_kernel<D, WIN>), dim3((unsigned)(nqb * a.B * a.Hq)), dim3(512), 0, s, a);
     return;
   }
   const int group = a.Hq / a.Hkv, nrb = (a.Lq + 255) / 256;
   for (int p0 = 0; p0 < pairs; p0 += pairs_per_pass) {
     const int np = pairs - p0 < pairs_per_pass ? pairs - p0 : pairs_per_pass;
     a.pair0 = p0;
-    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, true>), dim3((unsigned)(nkb * np)), dim3(512), 0, s, a);
-    hipLaunchKernelGGL(bwd_dq_ds_f32_kernel<D>, dim3((unsigned)(nrb * np * group)), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((bwd_dkdv_f32_kernel<D, true, WIN>), dim3((unsigned)(nkb * np)), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((bwd_dq_ds_f32_kernel<D, WIN>), dim3((unsigned)(nrb * np * group)), dim3(512), 0, s, a);
   }
+}
+
+// Optional key windows: both null (none) or both given, 4-byte aligned,
+// batch stride 0 or >= len_q.
+int check_f32_windows(const int32_t* lo, const int32_t* hi, int64_t batch_stride, int32_t len_q) {
+  if (!lo && !hi) return AVATTN_OK;
+  if (!lo || !hi) return AVATTN_ERR_NULL_POINTER;
+  if (((reinterpret_cast<uintptr_t>(lo) | reinterpret_cast<uintptr_t>(hi)) & 3u) != 0) return AVATTN_ERR_LAYOUT;
+  if (batch_stride != 0 && batch_stride < len_q) return AVATTN_ERR_ARGUMENT;
+  return AVATTN_OK;
 }
 
 }  // namespace
@@ -781,12 +913,15 @@ using namespace avattn;
 
 extern "C" {
 
-int avattn_fwd_f32(const float* q, const float* k, const float* v, const int64_t* q_strides,
-                   const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
-                   int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
-                   int64_t key_mask_batch_stride, float scale, float* out, const int64_t* out_strides, float* lse,
-                   avattn_stream_t stream) {
-  const int st = check_f32_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+static int fwd_f32_entry(const float* q, const float* k, const float* v, const int64_t* q_strides,
+                         const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
+                         int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                         int64_t key_mask_batch_stride, const int32_t* window_lo, const int32_t* window_hi,
+                         int64_t window_batch_stride, float scale, float* out, const int64_t* out_strides,
+                         float* lse, avattn_stream_t stream) {
+  int st = check_f32_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  st = check_f32_windows(window_lo, window_hi, window_batch_stride, len_q);
   if (st != AVATTN_OK) return st;
   if (!q_strides || !k_strides || !v_strides || !out_strides) return AVATTN_ERR_NULL_POINTER;
   if ((int64_t)batch * heads_q * len_q == 0) return AVATTN_OK;
@@ -811,11 +946,38 @@ int avattn_fwd_f32(const float* q, const float* k, const float* v, const int64_t
   if (!al16(k) || !al16(v) || !str4(k_strides) || !str4(v_strides)) return AVATTN_ERR_LAYOUT;
   if (key_mask && key_mask_batch_stride != 0 && key_mask_batch_stride < len_k) return AVATTN_ERR_ARGUMENT;
   a.scale = scale, a.c = scale * kLog2e;
-  if (head_dim == 128)
-    launch_fwd_f32<128>(a, s);
-  else
-    launch_fwd_f32<64>(a, s);
+  a.wlo = window_lo, a.whi = window_hi, a.wsb = window_batch_stride;
+  if (window_lo) {
+    if (head_dim == 128)
+      launch_fwd_f32<128, true>(a, s);
+    else
+      launch_fwd_f32<64, true>(a, s);
+  } else if (head_dim == 128) {
+    launch_fwd_f32<128, false>(a, s);
+  } else {
+    launch_fwd_f32<64, false>(a, s);
+  }
   return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+}
+
+int avattn_fwd_f32(const float* q, const float* k, const float* v, const int64_t* q_strides,
+                   const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
+                   int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                   int64_t key_mask_batch_stride, float scale, float* out, const int64_t* out_strides, float* lse,
+                   avattn_stream_t stream) {
+  return fwd_f32_entry(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
+                       key_mask, key_mask_batch_stride, nullptr, nullptr, 0, scale, out, out_strides, lse, stream);
+}
+
+int avattn_fwd_windowed_f32(const float* q, const float* k, const float* v, const int64_t* q_strides,
+                            const int64_t* k_strides, const int64_t* v_strides, int32_t batch, int32_t heads_q,
+                            int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim,
+                            const uint8_t* key_mask, int64_t key_mask_batch_stride, const int32_t* window_lo,
+                            const int32_t* window_hi, int64_t window_batch_stride, float scale, float* out,
+                            const int64_t* out_strides, float* lse, avattn_stream_t stream) {
+  return fwd_f32_entry(q, k, v, q_strides, k_strides, v_strides, batch, heads_q, heads_kv, len_q, len_k, head_dim,
+                       key_mask, key_mask_batch_stride, window_lo, window_hi, window_batch_stride, scale, out,
+                       out_strides, lse, stream);
 }
 
 size_t avattn_bwd_f32_workspace_size(int32_t batch, int32_t heads_q, int32_t len_q) {
@@ -833,14 +995,18 @@ size_t avattn_bwd_f32_staged_workspace_size(int32_t batch, int32_t heads_q, int3
          (size_t)pp * (size_t)ds_floats_per_pair(heads_q / heads_kv, len_q, len_k) * sizeof(float);
 }
 
-int avattn_bwd_f32(const float* dout, const float* q, const float* k, const float* v, const float* out,
-                   const float* lse, const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
-                   const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
-                   int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
-                   int64_t key_mask_batch_stride, float scale, float* dq, const int64_t* dq_strides, float* dk,
-                   const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* workspace,
-                   size_t workspace_bytes, avattn_stream_t stream) {
-  const int st = check_f32_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+static int bwd_f32_entry(const float* dout, const float* q, const float* k, const float* v, const float* out,
+                         const float* lse, const int64_t* dout_strides, const int64_t* q_strides,
+                         const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                         int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
+                         int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                         const int32_t* window_lo, const int32_t* window_hi, int64_t window_batch_stride,
+                         float scale, float* dq, const int64_t* dq_strides, float* dk, const int64_t* dk_strides,
+                         float* dv, const int64_t* dv_strides, void* workspace, size_t workspace_bytes,
+                         avattn_stream_t stream) {
+  int st = check_f32_dims(batch, heads_q, heads_kv, len_q, len_k, head_dim);
+  if (st != AVATTN_OK) return st;
+  st = check_f32_windows(window_lo, window_hi, window_batch_stride, len_q);
   if (st != AVATTN_OK) return st;
   if (!dout_strides || !q_strides || !k_strides || !v_strides || !out_strides || !dq_strides || !dk_strides ||
       !dv_strides)
@@ -909,11 +1075,45 @@ int avattn_bwd_f32(const float* dout, const float* q, const float* k, const floa
       a.dsp = (int64_t)(per / sizeof(float));
     }
   }
-  if (head_dim == 128)
-    launch_bwd_f32<128>(a, pp, s);
-  else
-    launch_bwd_f32<64>(a, pp, s);
+  a.wlo = window_lo, a.whi = window_hi, a.wsb = window_batch_stride;
+  if (window_lo) {
+    if (head_dim == 128)
+      launch_bwd_f32<128, true>(a, pp, s);
+    else
+      launch_bwd_f32<64, true>(a, pp, s);
+  } else if (head_dim == 128) {
+    launch_bwd_f32<128, false>(a, pp, s);
+  } else {
+    launch_bwd_f32<64, false>(a, pp, s);
+  }
   return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+}
+
+int avattn_bwd_f32(const float* dout, const float* q, const float* k, const float* v, const float* out,
+                   const float* lse, const int64_t* dout_strides, const int64_t* q_strides, const int64_t* k_strides,
+                   const int64_t* v_strides, const int64_t* out_strides, int32_t batch, int32_t heads_q,
+                   int32_t heads_kv, int32_t len_q, int32_t len_k, int32_t head_dim, const uint8_t* key_mask,
+                   int64_t key_mask_batch_stride, float scale, float* dq, const int64_t* dq_strides, float* dk,
+                   const int64_t* dk_strides, float* dv, const int64_t* dv_strides, void* workspace,
+                   size_t workspace_bytes, avattn_stream_t stream) {
+  return bwd_f32_entry(dout, q, k, v, out, lse, dout_strides, q_strides, k_strides, v_strides, out_strides, batch,
+                       heads_q, heads_kv, len_q, len_k, head_dim, key_mask, key_mask_batch_stride, nullptr, nullptr,
+                       0, scale, dq, dq_strides, dk, dk_strides, dv, dv_strides, workspace, workspace_bytes, stream);
+}
+
+int avattn_bwd_windowed_f32(const float* dout, const float* q, const float* k, const float* v, const float* out,
+                            const float* lse, const int64_t* dout_strides, const int64_t* q_strides,
+                            const int64_t* k_strides, const int64_t* v_strides, const int64_t* out_strides,
+                            int32_t batch, int32_t heads_q, int32_t heads_kv, int32_t len_q, int32_t len_k,
+                            int32_t head_dim, const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                            const int32_t* window_lo, const int32_t* window_hi, int64_t window_batch_stride,
+                            float scale, float* dq, const int64_t* dq_strides, float* dk, const int64_t* dk_strides,
+                            float* dv, const int64_t* dv_strides, void* workspace, size_t workspace_bytes,
+                            avattn_stream_t stream) {
+  return bwd_f32_entry(dout, q, k, v, out, lse, dout_strides, q_strides, k_strides, v_strides, out_strides, batch,
+                       heads_q, heads_kv, len_q, len_k, head_dim, key_mask, key_mask_batch_stride, window_lo,
+                       window_hi, window_batch_stride, scale, dq, dq_strides, dk, dk_strides, dv, dv_strides,
+                       workspace, workspace_bytes, stream);
 }
 
 int avattn_rope_apply_f32(const float* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,

@@ -201,7 +201,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 12; }
+int avattn_abi_version(void) { return 13; }
 
 }  // extern "C"
 

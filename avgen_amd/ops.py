@@ -15,10 +15,10 @@ Ops (namespace ``avgen_amd``):
 * ``rope_apply(x, cos, sin, inverse) -> x_rot`` — src/avgen/models/rope.py
   :297-338, differentiable.
 
-``flash_fwd``, ``flash_bwd`` and ``rope_apply`` take float32 tensors too
-(all of q, k, v and dout/out, or x), computed in fp32 by the library's fp32
-kernels (the reference's attention runs in the caller's dtype); every other
-op is bf16 only.
+``flash_fwd``, ``flash_bwd``, ``flash_fwd_windowed``, ``flash_bwd_windowed``
+and ``rope_apply`` take float32 tensors too (all of q, k, v and dout/out, or
+x), computed in fp32 by the library's fp32 kernels (the reference's
+attention runs in the caller's dtype); every other op is bf16 only.
 * ``flash_fwd_fp8(q, k, v, key_mask, q_scale, k_scale, scale) -> (out, lse)``
   — forward with q k^T on e4m3 operands and per-head scales (no reference
   counterpart; the sampling-time fp8 variant of ``flash_fwd``), forward only.
@@ -240,8 +240,33 @@ def _fwd_f32_impl(name, q, k, v, key_mask, rope_cos, rope_sin, scale):
     return out, lse
 
 
-def _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale):
-    """The float32 backward (``avattn_bwd_f32``): new dq, dk, dv."""
+def _fwd_windowed_f32_impl(name, q, k, v, lo, hi, wsb, key_mask, scale):
+    """The float32 forward with per-row key windows
+    (``avattn_fwd_windowed_f32``); ``lo``/``hi``/``wsb`` as checked by
+    ``_check_windows``."""
+    B, Hq, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    q, k, v = _f32_ready(q), _f32_ready(k), _f32_ready(v)
+    mask, msb = _normalise_mask(name, key_mask, B, Lk)
+    out = _f32_ready(torch.empty_like(q, memory_format=torch.preserve_format))
+    lse = torch.empty((B, Hq, Lq), device=q.device, dtype=torch.float32)
+    st = _lib.load().avattn_fwd_windowed_f32(
+        _ptr(q), _ptr(k), _ptr(v), _strides3(q), _strides3(k), _strides3(v),
+        B, Hq, Hkv, Lq, Lk, D,
+        _ptr(mask), msb,
+        _ptr(lo), _ptr(hi), wsb,
+        float(scale),
+        _ptr(out), _strides3(out), _ptr(lse),
+        _stream(q.device),
+    )
+    _lib.check(st, name)
+    return out, lse
+
+
+def _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale, windows=None):
+    """The float32 backward (``avattn_bwd_f32``; with ``windows`` = (lo, hi,
+    batch stride), non-decreasing along the queries,
+    ``avattn_bwd_windowed_f32``): new dq, dk, dv."""
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     for label, t in (("grad_out", dout), ("out", out)):
@@ -259,11 +284,19 @@ def _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale):
     dv = _f32_ready(torch.empty_like(v))
     lib = _lib.load()
     ws = _alloc_bwd_f32_workspace(B, Hq, Hkv, Lq, Lk, q.device)
-    st = lib.avattn_bwd_f32(
+    head = (
         _ptr(dout), _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse),
         _strides3(dout), _strides3(q), _strides3(k), _strides3(v), _strides3(out),
         B, Hq, Hkv, Lq, Lk, D,
         _ptr(mask), msb,
+    )
+    if windows is not None:
+        lo, hi, wsb = windows
+        entry, head = lib.avattn_bwd_windowed_f32, head + (_ptr(lo), _ptr(hi), wsb)
+    else:
+        entry = lib.avattn_bwd_f32
+    st = entry(
+        *head,
         float(scale),
         _ptr(dq), _strides3(dq), _ptr(dk), _strides3(dk), _ptr(dv), _strides3(dv),
         _ptr(ws), ws.numel(),
@@ -318,11 +351,13 @@ def _check_windows(name, lo, hi, B, Lq):
 
 def _fwd_windowed_impl(q, k, v, window_lo, window_hi, key_mask, scale):
     name = "avgen_amd.flash_fwd_windowed"
-    _check_qkv(name, q, k, v)
+    _check_qkv(name, q, k, v, allow_f32=True)
     _require_gpu(name, q, k, v, key_mask, window_lo, window_hi)
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     lo, hi, wsb = _check_windows(name, window_lo, window_hi, B, Lq)
+    if q.dtype is torch.float32:
+        return _fwd_windowed_f32_impl(name, q, k, v, lo, hi, wsb, key_mask, scale)
     q, k, v = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     mask, msb = _normalise_mask(name, key_mask, B, Lk)
     out = _kernel_ready(torch.empty_like(q, memory_format=torch.preserve_format))
@@ -352,13 +387,15 @@ def _bwd_windowed_impl(dout, q, k, v, out, lse, window_lo, window_hi, key_mask, 
     windows admit (:func:`compact_ds_table`, one more host synchronisation
     for its size); False: the dense layout, the same results."""
     name = "avgen_amd.flash_bwd_windowed"
-    _check_qkv(name, q, k, v)
+    _check_qkv(name, q, k, v, allow_f32=True)
     _require_gpu(name, dout, q, k, v, out, lse, key_mask, window_lo, window_hi)
     B, Hq, Lq, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     lo, hi, wsb = _check_windows(name, window_lo, window_hi, B, Lq)
     if check_monotone and Lq > 1 and bool(((lo[..., 1:] < lo[..., :-1]) | (hi[..., 1:] < hi[..., :-1])).any()):
         raise ValueError(f"{name}: the backward needs window_lo and window_hi non-decreasing along the queries")
+    if q.dtype is torch.float32:
+        return _bwd_f32_impl(name, dout, q, k, v, out, lse, key_mask, scale, windows=(lo, hi, wsb))
     dout, q, k, v, out = (_kernel_ready(t) for t in (dout, q, k, v, out))
     lse = lse.contiguous()
     mask, msb = _normalise_mask(name, key_mask, B, Lk)

@@ -42,9 +42,11 @@
  *   avattn_qk_norm_rope, src/avgen/models/layers.py:530-536 (q_norm/k_norm
  *   avattn_qk_norm_rope_bwd  then apply_rotary) and their autograd backward
  *   avattn_fwd_f32,     the same interfaces as avattn_fwd / avattn_bwd /
- *   avattn_bwd_f32,     avattn_rope_apply for float32 tensors (the
- *   avattn_bwd_f32_staged_workspace_size  reference's attention and
- *   avattn_rope_apply_f32  rotation run in the caller's dtype)
+ *   avattn_bwd_f32,     avattn_rope_apply / avattn_fwd_windowed /
+ *   avattn_fwd_windowed_f32,  avattn_bwd_windowed for float32 tensors (the
+ *   avattn_bwd_windowed_f32,  reference's attention and rotation run in
+ *   avattn_bwd_f32_staged_workspace_size,  the caller's dtype; its CPU
+ *   avattn_rope_apply_f32  tests and config c1 are float32)
  */
 #ifndef AVATTN_H
 #define AVATTN_H
@@ -681,6 +683,50 @@ int avattn_bwd_f32(const float* dout, const float* q, const float* k, const floa
                    float* dv, const int64_t* dv_strides,
                    void* workspace, size_t workspace_bytes,
                    avattn_stream_t stream);
+
+/*
+ * avattn_fwd_f32 / avattn_bwd_f32 with per-query-row key windows, as
+ * avattn_fwd_windowed / avattn_bwd_windowed (src/avgen/models/blocks.py:
+ * 54-104, the temporal neighbour mask with sorted time coordinates;
+ * src/avgen/data/packing.py:181-200, the packed block-diagonal mask): row i
+ * of batch b attends the keys j with window_lo[b*wsb + i] <= j <
+ * window_hi[b*wsb + i] (and key_mask), values clamped into 0 <= lo <= hi <=
+ * len_k; a row with an empty window gets out 0 and lse -inf.  The forward
+ * visits only the key tiles meeting its rows' windows.  The backward
+ * requires lo and hi non-decreasing in the row; it then visits only the
+ * query tiles whose rows meet each key block and, with staged dS, multiplies
+ * only the (rows, key block) pairs the dK/dV kernel wrote.  Workspace and
+ * errors as avattn_bwd_f32 (staged dS with the staged size).
+ */
+int avattn_fwd_windowed_f32(const float* q, const float* k, const float* v,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides,
+                            int32_t batch, int32_t heads_q, int32_t heads_kv,
+                            int32_t len_q, int32_t len_k, int32_t head_dim,
+                            const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                            const int32_t* window_lo, const int32_t* window_hi,
+                            int64_t window_batch_stride,
+                            float scale,
+                            float* out, const int64_t* out_strides,
+                            float* lse,
+                            avattn_stream_t stream);
+
+int avattn_bwd_windowed_f32(const float* dout, const float* q, const float* k, const float* v,
+                            const float* out, const float* lse,
+                            const int64_t* dout_strides, const int64_t* q_strides,
+                            const int64_t* k_strides, const int64_t* v_strides,
+                            const int64_t* out_strides,
+                            int32_t batch, int32_t heads_q, int32_t heads_kv,
+                            int32_t len_q, int32_t len_k, int32_t head_dim,
+                            const uint8_t* key_mask, int64_t key_mask_batch_stride,
+                            const int32_t* window_lo, const int32_t* window_hi,
+                            int64_t window_batch_stride,
+                            float scale,
+                            float* dq, const int64_t* dq_strides,
+                            float* dk, const int64_t* dk_strides,
+                            float* dv, const int64_t* dv_strides,
+                            void* workspace, size_t workspace_bytes,
+                            avattn_stream_t stream);
 
 int avattn_rope_apply_f32(const float* x, const int64_t* x_strides,
                           int32_t batch, int32_t heads, int32_t len,

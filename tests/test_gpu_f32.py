@@ -311,3 +311,150 @@ def test_f32_compiles_to_the_eager_bits(amd):
     compiled = run(torch.compile(f, fullgraph=True))
     for a_, b_ in zip(eager, compiled):
         assert a_.dtype is torch.float32 and torch.equal(a_, b_)
+
+
+# ---------------------------------------------------------------------------
+# float32 with per-row key windows (avattn_fwd_windowed_f32 /
+# avattn_bwd_windowed_f32): the reference's temporal neighbour mask
+# (src/avgen/models/blocks.py:54-104) and packed block-diagonal mask
+# (src/avgen/data/packing.py:181-200) in the caller's dtype.
+# ---------------------------------------------------------------------------
+
+
+def _window_mask(lo, hi, Lk):
+    j = np.arange(Lk)
+    return (j >= np.asarray(lo)[..., None]) & (j < np.asarray(hi)[..., None])
+
+
+def _monotone_windows(B, Lq, Lk, seed, max_width, empty_tail=0):
+    """Non-decreasing (lo, hi) with widths up to max_width and some empty
+    rows; the last empty_tail rows get the empty window [Lk, Lk)."""
+    rng = np.random.default_rng(seed)
+    lo = np.sort(rng.integers(0, Lk + 1, (B, Lq)), axis=1)
+    hi = np.maximum.accumulate(np.minimum(lo + rng.integers(0, max_width + 1, (B, Lq)), Lk), axis=1)
+    if empty_tail:
+        lo[:, Lq - empty_tail:] = Lk
+        hi[:, Lq - empty_tail:] = Lk
+    return lo.astype(np.int32), hi.astype(np.int32)
+
+
+F32_WIN_CASES = [
+    # B, Hq, Hkv, Lq, Lk, D, width, empty tail, per-batch windows
+    (1, 2, 2, 300, 500, 128, 120, 0, False),
+    (2, 4, 2, 257, 700, 64, 300, 17, True),
+    (2, 2, 1, 1000, 333, 128, 60, 5, True),
+]
+
+
+@pytest.mark.parametrize("staged", [True, False], ids=["staged_ds", "recompute"])
+@pytest.mark.parametrize("B,Hq,Hkv,Lq,Lk,D,width,tail,per_batch", F32_WIN_CASES)
+def test_f32_windowed_forward_backward_match_oracle(amd, B, Hq, Hkv, Lq, Lk, D, width, tail, per_batch, staged):
+    print(f"f32 windowed B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} D={D} width={width} tail={tail} "
+          f"per_batch={per_batch} staged={staged}", flush=True)
+    q, k, v, do = (_randn(s, 60 + i) for i, s in enumerate(
+        ((B, Hq, Lq, D), (B, Hkv, Lk, D), (B, Hkv, Lk, D), (B, Hq, Lq, D))))
+    lo, hi = _monotone_windows(B if per_batch else 1, Lq, Lk, 65, width, tail)
+    km = np.random.default_rng(66).random((B, Lk)) < 0.8
+    lo_t, hi_t = torch.from_numpy(lo).cuda(), torch.from_numpy(hi).cuda()
+    if not per_batch:
+        lo_t, hi_t = lo_t[0], hi_t[0]
+    kmc = torch.from_numpy(km).cuda()
+    scale = D ** -0.5
+    out, lse = amd.ops.flash_fwd_windowed(q.cuda(), k.cuda(), v.cuda(), lo_t, hi_t, kmc, scale)
+    assert out.dtype is torch.float32
+    dense = _window_mask(lo, hi, Lk)  # (B|1, Lq, Lk)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), km, attn_mask=dense)
+    o, l = _f64(out), _f64(lse)
+    _check_fwd(o, l, ro, rl)
+    dev = torch.device("cuda", 0)
+    amd.ops.set_ds_budget(None if staged else 0, dev)
+    try:
+        grads = amd.ops.flash_bwd_windowed(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, lo_t, hi_t, kmc, scale)
+    finally:
+        amd.ops.set_ds_budget(None, dev)
+    ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), o, l, km, attn_mask=dense)
+    for name, got, r in zip(("dq", "dk", "dv"), grads, ref):
+        assert got.dtype is torch.float32
+        err = np.abs(_f64(got) - r).max()
+        print(f"  {name}: max err {err:.3e} (ref max {np.abs(r).max():.3e})", flush=True)
+        assert err <= GRAD_REL_TOL * max(np.abs(r).max(), 1e-6), name
+    # keys no row reaches (window or key mask): exactly zero dK/dV
+    reached = np.broadcast_to(dense.any(axis=-2), (B, Lk)) & km
+    for g in grads[1:]:
+        gz = _f64(g)
+        for b in range(B):
+            assert (gz[b][:, ~reached[b]] == 0).all()
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_f32_full_windows_equal_the_unwindowed_kernels(amd, D):
+    """Windows [0, Lk) for every row: the windowed kernels visit the same
+    tiles and compute the same values, so forward and backward (staged and
+    recomputing) give the unwindowed kernels' bits.  (A tile loop whose
+    bounds the compiler could not prove wave-uniform once ran as a divergent
+    loop around its barriers and gave garbage at head_dim 64.)"""
+    B, Hq, Hkv, Lq, Lk = 2, 4, 2, 200, 300
+    q, k, v, do = (_randn(s, 70 + i).cuda() for i, s in enumerate(
+        ((B, Hq, Lq, D), (B, Hkv, Lk, D), (B, Hkv, Lk, D), (B, Hq, Lq, D))))
+    lo = torch.zeros(Lq, dtype=torch.int32, device="cuda")
+    hi = torch.full((Lq,), Lk, dtype=torch.int32, device="cuda")
+    out, lse = amd.ops.flash_fwd(q, k, v, None, None, None, D ** -0.5)
+    wout, wlse = amd.ops.flash_fwd_windowed(q, k, v, lo, hi, None, D ** -0.5)
+    assert torch.equal(out, wout) and torch.equal(lse, wlse)
+    dev = torch.device("cuda", 0)
+    for budget in (None, 0):
+        amd.ops.set_ds_budget(budget, dev)
+        try:
+            g = amd.ops.flash_bwd(do, q, k, v, out, lse, None, D ** -0.5)
+            wg = amd.ops.flash_bwd_windowed(do, q, k, v, out, lse, lo, hi, None, D ** -0.5)
+        finally:
+            amd.ops.set_ds_budget(None, dev)
+        for name, x, y in zip(("dq", "dk", "dv"), g, wg):
+            assert torch.equal(x, y), (budget, name)
+
+
+def test_f32_varlen_attention_matches_the_packed_mask(amd):
+    lengths, capacity, H, D = [700, 129, 64, 1000], 2048, 2, 128
+    q, k, v = (_randn((1, H, capacity, D), s).cuda().requires_grad_(True) for s in (81, 82, 83))
+    do = _randn((1, H, capacity, D), 84)
+    cu = torch.tensor(R.packed_cu_seqlens(lengths))
+    out = amd.attention.varlen_attention(q, k, v, cu)
+    assert out.dtype is torch.float32
+    dense = R.packed_attention_mask(lengths, capacity)[None]
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), attn_mask=dense)
+    o = _f64(out)
+    assert np.abs(o - ro).max() <= OUT_TOL * max(1.0, np.abs(ro).max())
+    assert (o[:, :, sum(lengths):] == 0).all()
+    out.backward(do.cuda())
+    ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, attn_mask=dense)
+    for name, got, r in zip(("dq", "dk", "dv"), (q.grad, k.grad, v.grad), ref):
+        assert np.abs(_f64(got) - r).max() <= GRAD_REL_TOL * max(np.abs(r).max(), 1e-6), name
+
+
+def test_f32_temporal_neighbour_attention_matches_the_dense_mask(amd):
+    """Video queries (frames of 48 tokens at 24 fps) against audio keys, a
+    0.1 s window, shuffled token order and masked keys, in float32; the last
+    frames have no key in range and fall back to every key."""
+    B, Hq, Hkv, D = 2, 4, 2, 64
+    tq = np.stack([(np.arange(960) // 48) / 24.0, 0.05 + (np.arange(960) // 48) / 24.0]).astype(np.float32)
+    tk = np.stack([np.arange(260) / 43.0, 0.2 + np.arange(260) / 43.0]).astype(np.float32)
+    Lq, Lk = tq.shape[1], tk.shape[1]
+    rng = np.random.default_rng(91)
+    km = rng.random((B, Lk)) < 0.7
+    pq, pk = rng.permutation(Lq), rng.permutation(Lk)
+    tq, tk = tq[:, pq], tk[:, pk]
+    q = _randn((B, Hq, Lq, D), 92).cuda().requires_grad_(True)
+    k = _randn((B, Hkv, Lk, D), 93).cuda().requires_grad_(True)
+    v = _randn((B, Hkv, Lk, D), 94).cuda().requires_grad_(True)
+    do = _randn((B, Hq, Lq, D), 95)
+    out = amd.attention.temporal_neighbour_attention(
+        q, k, v, torch.from_numpy(tq).cuda(), torch.from_numpy(tk).cuda(), window_seconds=0.1,
+        key_mask=torch.from_numpy(km).cuda(), enable_gqa=True)
+    assert out.dtype is torch.float32
+    dense = R.temporal_neighbour_mask(tq, tk, 0.1, km)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), attn_mask=dense)
+    assert np.abs(_f64(out) - ro).max() <= OUT_TOL * max(1.0, np.abs(ro).max())
+    out.backward(do.cuda())
+    ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, attn_mask=dense)
+    for name, got, r in zip(("dq", "dk", "dv"), (q.grad, k.grad, v.grad), ref):
+        assert np.abs(_f64(got) - r).max() <= GRAD_REL_TOL * max(np.abs(r).max(), 1e-6), name
