@@ -11,7 +11,8 @@ with holes and fully masked batch rows.
 - fp8: per-head absmax scales, quantized exactly as the kernels do;
 - ring: cp 1-4 equal chunks of the key sequence, with and without the fused
   3D RoPE (whose results must equal the unfused composition bit for bit);
-- float32: the fp32 forward and backward at float32's bar.
+- float32: the fp32 forward and backward at float32's bar, and with random
+  key windows (shuffled for a forward check; staged or recomputed dq).
 
 The bars are the kernels' usual ones, scaled with the data: output 2e-2 of
 max(1, its largest magnitude), LSE 1e-3 (fp8: plus 2^-14 of |lse|, the e4m3
@@ -250,3 +251,57 @@ def test_f32_random_shapes_match_oracle(amd, seed):
     args = (_f64(do), _f64(q), _f64(k), _f64(v), o, l, km)
     _check_grads((dq, dk, dv), R.attention_bwd_f64(*args), R.attention_bwd_magnitudes_f64(*args), rel=1e-4,
                  floor=1e-6)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_f32_windowed_random_shapes_match_oracle(amd, seed):
+    """float32 with random per-row key windows at float32's bar: the
+    backward (staged dS or recomputed dq) on non-decreasing windows, the
+    forward also on the same windows shuffled across rows (it takes any)."""
+    rng = np.random.default_rng(6000 + seed)
+    c = _shape(rng)
+    per_batch, staged = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+    B, Hq, Hkv, Lq, Lk, D = c["B"], c["Hq"], c["Hkv"], c["Lq"], c["Lk"], c["D"]
+    lo, hi = _windows(rng, B if per_batch else 1, Lq, Lk)
+    g = torch.Generator()
+    g.manual_seed(seed)
+    q, k, v, do = (torch.randn(s, generator=g) * c["scale"]
+                   for s in ((B, Hq, Lq, D), (B, Hkv, Lk, D), (B, Hkv, Lk, D), (B, Hq, Lq, D)))
+    mask = (torch.rand((B, Lk), generator=g) < 0.8) if c["masked"] else None
+    print(f"f32 windowed sweep seed={seed} {c} per_batch={per_batch} staged={staged}", flush=True)
+    dev = torch.device("cuda", 0)
+    mk = None if mask is None else mask.cuda()
+    km = None if mask is None else mask.numpy()
+    j = np.arange(Lk)
+
+    def run_fwd(lo_np, hi_np):
+        lo_t, hi_t = torch.from_numpy(lo_np).cuda(), torch.from_numpy(hi_np).cuda()
+        if not per_batch:
+            lo_t, hi_t = lo_t[0], hi_t[0]
+        out, lse = amd.ops.flash_fwd_windowed(q.cuda(), k.cuda(), v.cuda(), lo_t, hi_t, mk, D ** -0.5)
+        dense = (j >= lo_np[..., None]) & (j < hi_np[..., None])
+        ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), km, attn_mask=dense)
+        o, l = _f64(out), lse.cpu().numpy().astype(np.float64)
+        assert np.abs(o - ro).max() <= 2e-5 * max(1.0, np.abs(ro).max())
+        fin = np.isfinite(rl)
+        assert np.array_equal(np.isneginf(l), ~fin)
+        assert (np.abs(l[fin] - rl[fin]) <= 2e-5 * np.maximum(1.0, np.abs(rl[fin]))).all()
+        return out, lse, lo_t, hi_t, dense, o, l
+
+    perm = rng.permutation(Lq)
+    run_fwd(np.ascontiguousarray(lo[:, perm]), np.ascontiguousarray(hi[:, perm]))
+    out, lse, lo_t, hi_t, dense, o, l = run_fwd(lo, hi)
+    amd.ops.set_ds_budget(None if staged else 0, dev)
+    try:
+        grads = amd.ops.flash_bwd_windowed(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, lo_t, hi_t, mk,
+                                           D ** -0.5)
+    finally:
+        amd.ops.set_ds_budget(None, dev)
+    args = (_f64(do), _f64(q), _f64(k), _f64(v), o, l, km)
+    _check_grads(grads, R.attention_bwd_f64(*args, attn_mask=dense),
+                 R.attention_bwd_magnitudes_f64(*args, attn_mask=dense), rel=1e-4, floor=1e-6)
+    reached = dense.any(axis=1)
+    if km is not None:
+        reached = reached & km
+    gone = np.broadcast_to(~reached[:, None, :, None], grads[1].shape)
+    assert np.all(_f64(grads[1])[gone] == 0) and np.all(_f64(grads[2])[gone] == 0)
