@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(F32Args a) {
   __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
   __shared__ __attribute__((aligned(16))) float vs[2][KT * D];
   __shared__ __attribute__((aligned(16))) float bias[2][KT];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
   const int nqb = (a.Lq + ROWS - 1) / ROWS;
   const int qb = blockIdx.x % nqb, bh = blockIdx.x / nqb;
@@ -396,7 +396,7 @@ __global__ __launch_bounds__(512) void bwd_dkdv_f32_kernel(F32Args a) {
   __shared__ __attribute__((aligned(16))) float nds[3][QT];
   __shared__ __attribute__((aligned(16))) float px[2][4][16 * 64];
   __shared__ __attribute__((aligned(16))) int wls[WIN ? 2 : 1][QT], whs[WIN ? 2 : 1][QT];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
   const int pair = wave & 3, role = wave >> 2;  // role 0: P wave, 1: dS wave
   const int nkb = (a.Lk + KPB - 1) / KPB;
@@ -581,7 +581,7 @@ __global__ __launch_bounds__(512) void bwd_dq_f32_kernel(F32Args a) {
   __shared__ __attribute__((aligned(16))) float vs[2][KT * PITCH];
   __shared__ __attribute__((aligned(16))) float kok[3][KT];  // 1: valid key, 0: masked or past the end
   __shared__ __attribute__((aligned(16))) float xs[2][2][4][16 * 64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
   const int pair = wave & 3, role = wave >> 2;  // role 0: q and P, 1: dO and dP
   const int nqb = (a.Lq + ROWS - 1) / ROWS;
@@ -713,7 +713,7 @@ __global__ __launch_bounds__(512) void bwd_dq_ds_f32_kernel(F32Args a) {
   constexpr int KT = 32, ROWS = 256, PITCH = D + 4, DT = D / 32;
   using vdt = float __attribute__((ext_vector_type(DT)));
   __shared__ __attribute__((aligned(16))) float ks[2][KT * PITCH];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5;
   const int group = a.Hq / a.Hkv;
   const int nrb = (a.Lq + ROWS - 1) / ROWS;
