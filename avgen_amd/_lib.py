@@ -229,6 +229,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_ptr, c_size,
          c_ptr],
     ),
+    "avattn_qk_norm_rope_f32": (
+        ctypes.c_int,
+        [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_f32, c_ptr, c_ptr, c_i64,
+         c_ptr, c_i64p, c_ptr],
+    ),
+    "avattn_qk_norm_rope_bwd_f32": (
+        ctypes.c_int,
+        [c_ptr, c_i64p, c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32, c_ptr, c_f32, c_ptr, c_ptr, c_i64,
+         c_ptr, c_i64p, c_ptr, c_ptr, c_size, c_ptr],
+    ),
     "avattn_rope_apply_f32": (
         ctypes.c_int,
         [c_ptr, c_i64p, c_i32, c_i32, c_i32, c_i32,

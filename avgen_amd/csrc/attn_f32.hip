@@ -837,6 +837,164 @@ __global__ __launch_bounds__(256) void rope_apply_f32_kernel(const float* __rest
   }
 }
 
+// ---------------------------------------------------------------------------
+// Per-head RMSNorm + rotation on float32 rows (a float32 model's q_norm /
+// k_norm then apply_rotary, src/avgen/models/layers.py:106-118, 530-536:
+// F.rms_norm with the gain in the activation's dtype, then the fp32
+// rotation of src/avgen/models/rope.py:332-338).  Forward per row:
+//   rstd = 1/sqrt(mean(x^2) + eps),  n = (x*rstd)*w,  y = rotate(n)
+// backward given dy: g = rotate^T(dy), xh = x*rstd, wg = w*g,
+//   dx = rstd*(wg - xh*mean(wg*xh)),  dw = sum over rows of g*xh (per-block
+//   partials, then one fixed-order reduction: deterministic).
+// One wave per token, D/4 lanes per head row holding 4 floats (16 bytes)
+// each, 64/(D/4) heads at a time; the token's rotation values are read
+// once.  HBM-bound: one read and one write of the rows (two reads back).
+// ---------------------------------------------------------------------------
+struct NormF32Args {
+  const float* x;
+  int64_t xsb, xsh, xsl;
+  int B, H, L;
+  const float* w;  // (head_dim) gain, or null
+  float eps;
+  const float *ct, *st;  // rotation tables at b*tsb + i*head_dim/2 + pair; null: no rotation
+  int64_t tsb;
+  float* out;
+  int64_t osb, osh, osl;
+  const float* dy;
+  int64_t dsb, dsh, dsl;
+  float* dx;
+  int64_t xgb, xgh, xgl;
+  float* wpart;  // backward: per-block dW partials, null without a gain
+};
+constexpr int kNormF32Blocks = 4096;  // fixed grid of the backward (dW partials per block)
+
+template <int R>
+__device__ __forceinline__ float lane_group_sum(float v) {
+#pragma unroll
+  for (int off = R / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// The rotation of a lane's two interleaved pairs (as rope_apply_f32_kernel).
+__device__ __forceinline__ f32x4 rotate4(const f32x4& v, const float* cs, const float* sn, bool inverse) {
+#pragma clang fp contract(off)
+  f32x4 r;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float e = v[2 * p], od = v[2 * p + 1];
+    const float ec = e * cs[p], os = od * sn[p], es = e * sn[p], oc = od * cs[p];
+    r[2 * p] = inverse ? ec + os : ec - os;
+    r[2 * p + 1] = inverse ? oc - es : es + oc;
+  }
+  return r;
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void qk_norm_f32_fwd_kernel(NormF32Args a) {
+#pragma clang fp contract(off)
+  constexpr int R = D / 4, HPW = 64 / R;
+  const int c = threadIdx.x % R, hg = threadIdx.x / R;
+  const f32x4 w = a.w ? ld4(a.w + 4 * c) : f32x4{1.f, 1.f, 1.f, 1.f};
+  const int64_t ntok = (int64_t)a.B * a.L;
+  for (int64_t tok = blockIdx.x; tok < ntok; tok += gridDim.x) {
+    const int b = (int)(tok / a.L), i = (int)(tok % a.L);
+    float cs[2] = {1.f, 1.f}, sn[2] = {0.f, 0.f};
+    if (a.ct) {
+      const int64_t t = b * a.tsb + (int64_t)i * (D / 2) + 2 * c;
+      cs[0] = a.ct[t], cs[1] = a.ct[t + 1], sn[0] = a.st[t], sn[1] = a.st[t + 1];
+    }
+    const float* xrow = a.x + b * a.xsb + (int64_t)i * a.xsl + 4 * c;
+    for (int h = hg; h < a.H; h += HPW) {  // uniform over the row's lanes
+      const f32x4 x = ld4(xrow + h * a.xsh);
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss += x[j] * x[j];
+      ss = lane_group_sum<R>(ss);
+      const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
+      f32x4 n;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) n[j] = (x[j] * rstd) * w[j];
+      if (a.ct) n = rotate4(n, cs, sn, false);
+      st4(a.out + b * a.osb + h * a.osh + (int64_t)i * a.osl + 4 * c, n);
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void qk_norm_f32_bwd_kernel(NormF32Args a) {
+#pragma clang fp contract(off)
+  constexpr int R = D / 4, HPW = 64 / R;
+  __shared__ float red[HPW][D];
+  const int c = threadIdx.x % R, hg = threadIdx.x / R;
+  const f32x4 w = a.w ? ld4(a.w + 4 * c) : f32x4{1.f, 1.f, 1.f, 1.f};
+  float dw[4] = {0.f, 0.f, 0.f, 0.f};
+  const int64_t ntok = (int64_t)a.B * a.L;
+  for (int64_t tok = blockIdx.x; tok < ntok; tok += gridDim.x) {
+    const int b = (int)(tok / a.L), i = (int)(tok % a.L);
+    float cs[2] = {1.f, 1.f}, sn[2] = {0.f, 0.f};
+    if (a.ct) {
+      const int64_t t = b * a.tsb + (int64_t)i * (D / 2) + 2 * c;
+      cs[0] = a.ct[t], cs[1] = a.ct[t + 1], sn[0] = a.st[t], sn[1] = a.st[t + 1];
+    }
+    const float* xrow = a.x + b * a.xsb + (int64_t)i * a.xsl + 4 * c;
+    const float* grow = a.dy + b * a.dsb + (int64_t)i * a.dsl + 4 * c;
+    for (int h = hg; h < a.H; h += HPW) {
+      const f32x4 x = ld4(xrow + h * a.xsh);
+      f32x4 g = ld4(grow + h * a.dsh);
+      if (a.ct) g = rotate4(g, cs, sn, true);
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ss += x[j] * x[j];
+      ss = lane_group_sum<R>(ss);
+      const float rstd = 1.f / __builtin_sqrtf(ss / (float)D + a.eps);
+      float xh[4], wg[4], dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xh[j] = x[j] * rstd;
+        wg[j] = w[j] * g[j];
+        dot += wg[j] * xh[j];
+        dw[j] += g[j] * xh[j];
+      }
+      const float m = lane_group_sum<R>(dot) / (float)D;
+      f32x4 dx;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dx[j] = rstd * (wg[j] - xh[j] * m);
+      st4(a.dx + b * a.xgb + h * a.xgh + (int64_t)i * a.xgl + 4 * c, dx);
+    }
+  }
+  if (!a.wpart) return;  // uniform: no gain, no dW
+#pragma unroll
+  for (int j = 0; j < 4; ++j) red[hg][4 * c + j] = dw[j];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 64) {
+    float s = 0.f;
+    for (int r = 0; r < HPW; ++r) s += red[r][d];
+    a.wpart[(int64_t)blockIdx.x * D + d] = s;
+  }
+}
+
+// dw[d] = the backward blocks' partials summed in a fixed order (one
+// workgroup per d: strided shares, then a tree over the threads).
+__global__ __launch_bounds__(256) void qk_norm_f32_dw_kernel(const float* __restrict__ part, int nblocks, int D,
+                                                             float* __restrict__ dw) {
+  __shared__ float red[256];
+  const int d = blockIdx.x;
+  float s = 0.f;
+  for (int k = threadIdx.x; k < nblocks; k += 256) s += part[(int64_t)k * D + d];
+  red[threadIdx.x] = s;
+  __syncthreads();
+#pragma unroll
+  for (int off = 128; off > 0; off >>= 1) {
+    if ((int)threadIdx.x < off) red[threadIdx.x] += red[threadIdx.x + off];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) dw[d] = red[0];
+}
+
+__global__ void qk_norm_f32_dw_zero_kernel(int D, float* __restrict__ dw) {
+  if ((int)threadIdx.x < D) dw[threadIdx.x] = 0.f;
+}
+
 int grid_of(int64_t n, int per = 256) {
   const int64_t g = (n + per - 1) / per;
   return (int)(g < 1 ? 1 : (g > 65535 ? 65535 : g));
@@ -1132,6 +1290,96 @@ int avattn_rope_apply_f32(const float* x, const int64_t* x_strides, int32_t batc
   hipLaunchKernelGGL(rope_apply_f32_kernel, dim3(grid_of(n)), dim3(256), 0, s, x, x_strides[0], x_strides[1],
                      x_strides[2], batch, heads, len, head_dim, cos_tab, sin_tab, table_batch_stride,
                      inverse ? 1 : 0, out, out_strides[0], out_strides[1], out_strides[2]);
+  return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+}
+
+
+// Arguments of the float32 q/k norm entry points (as check_qk_norm of the
+// bf16 ones).
+static int check_norm_f32(const float* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,
+                          int32_t head_dim, const float* weight, float eps, const float* cos_tab,
+                          const float* sin_tab, int64_t table_batch_stride) {
+  if (batch < 0 || heads < 0 || len < 0) return AVATTN_ERR_BAD_SHAPE;
+  if (head_dim != 64 && head_dim != 128) return AVATTN_ERR_HEAD_DIM;
+  if (!x_strides) return AVATTN_ERR_NULL_POINTER;
+  if (!(eps >= 0.f) || !isfinite(eps)) return AVATTN_ERR_ARGUMENT;
+  if (!cos_tab != !sin_tab) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * heads * len == 0) return AVATTN_OK;
+  if (!x) return AVATTN_ERR_NULL_POINTER;
+  if (!al16(x) || !str4(x_strides) || (weight && !al16(weight))) return AVATTN_ERR_LAYOUT;
+  if (cos_tab && (!al16(cos_tab) || !al16(sin_tab) || table_batch_stride % 4 != 0)) return AVATTN_ERR_LAYOUT;
+  if ((int64_t)batch * heads > 2147483647 || (int64_t)batch * len > ((int64_t)1 << 40)) return AVATTN_ERR_TOO_LARGE;
+  return AVATTN_OK;
+}
+
+static NormF32Args norm_f32_args(const float* x, const int64_t* xs, int32_t batch, int32_t heads, int32_t len,
+                                 const float* weight, float eps, const float* cos_tab, const float* sin_tab,
+                                 int64_t tsb) {
+  NormF32Args a{};
+  a.x = x, a.xsb = xs[0], a.xsh = xs[1], a.xsl = xs[2];
+  a.B = batch, a.H = heads, a.L = len;
+  a.w = weight, a.eps = eps;
+  a.ct = cos_tab, a.st = sin_tab, a.tsb = tsb;
+  return a;
+}
+
+int avattn_qk_norm_rope_f32(const float* x, const int64_t* x_strides, int32_t batch, int32_t heads, int32_t len,
+                            int32_t head_dim, const float* weight, float eps, const float* cos_tab,
+                            const float* sin_tab, int64_t table_batch_stride, float* out,
+                            const int64_t* out_strides, avattn_stream_t stream) {
+  int st = check_norm_f32(x, x_strides, batch, heads, len, head_dim, weight, eps, cos_tab, sin_tab,
+                          table_batch_stride);
+  if (st != AVATTN_OK) return st;
+  if (!out_strides) return AVATTN_ERR_NULL_POINTER;
+  if ((int64_t)batch * heads * len == 0) return AVATTN_OK;
+  if (!out) return AVATTN_ERR_NULL_POINTER;
+  if (!al16(out) || !str4(out_strides)) return AVATTN_ERR_LAYOUT;
+  NormF32Args a = norm_f32_args(x, x_strides, batch, heads, len, weight, eps, cos_tab, sin_tab, table_batch_stride);
+  a.out = out, a.osb = out_strides[0], a.osh = out_strides[1], a.osl = out_strides[2];
+  const int64_t tokens = (int64_t)batch * len;
+  const dim3 grid((unsigned)(tokens > (1 << 20) ? (1 << 20) : tokens));
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(qk_norm_f32_fwd_kernel<128>, grid, dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL(qk_norm_f32_fwd_kernel<64>, grid, dim3(64), 0, s, a);
+  return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+}
+
+int avattn_qk_norm_rope_bwd_f32(const float* x, const int64_t* x_strides, const float* dy,
+                                const int64_t* dy_strides, int32_t batch, int32_t heads, int32_t len,
+                                int32_t head_dim, const float* weight, float eps, const float* cos_tab,
+                                const float* sin_tab, int64_t table_batch_stride, float* dx,
+                                const int64_t* dx_strides, float* dweight, void* workspace, size_t workspace_bytes,
+                                avattn_stream_t stream) {
+  int st = check_norm_f32(x, x_strides, batch, heads, len, head_dim, weight, eps, cos_tab, sin_tab,
+                          table_batch_stride);
+  if (st != AVATTN_OK) return st;
+  if (!dy_strides || !dx_strides) return AVATTN_ERR_NULL_POINTER;
+  if (weight && !dweight) return AVATTN_ERR_NULL_POINTER;
+  if (weight && (!workspace || workspace_bytes < (size_t)kNormF32Blocks * head_dim * sizeof(float) ||
+                 !al16(workspace)))
+    return AVATTN_ERR_WORKSPACE;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if ((int64_t)batch * heads * len == 0) {
+    if (!weight) return AVATTN_OK;
+    // no rows: the gain's gradient is zero (the reduction over no blocks)
+    hipLaunchKernelGGL(qk_norm_f32_dw_zero_kernel, dim3(1), dim3(128), 0, s, head_dim, dweight);
+    return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
+  }
+  if (!dy || !dx) return AVATTN_ERR_NULL_POINTER;
+  if (!al16(dy) || !al16(dx) || !str4(dy_strides) || !str4(dx_strides)) return AVATTN_ERR_LAYOUT;
+  NormF32Args a = norm_f32_args(x, x_strides, batch, heads, len, weight, eps, cos_tab, sin_tab, table_batch_stride);
+  a.dy = dy, a.dsb = dy_strides[0], a.dsh = dy_strides[1], a.dsl = dy_strides[2];
+  a.dx = dx, a.xgb = dx_strides[0], a.xgh = dx_strides[1], a.xgl = dx_strides[2];
+  a.wpart = weight ? static_cast<float*>(workspace) : nullptr;
+  const int64_t tokens = (int64_t)batch * len;
+  const int nb = (int)(tokens > kNormF32Blocks ? kNormF32Blocks : tokens);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(qk_norm_f32_bwd_kernel<128>, dim3(nb), dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL(qk_norm_f32_bwd_kernel<64>, dim3(nb), dim3(64), 0, s, a);
+  if (weight) hipLaunchKernelGGL(qk_norm_f32_dw_kernel, dim3(head_dim), dim3(256), 0, s, a.wpart, nb, head_dim, dweight);
   return hipGetLastError() == hipSuccess ? AVATTN_OK : AVATTN_ERR_LAUNCH;
 }
 

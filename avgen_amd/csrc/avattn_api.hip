@@ -201,7 +201,7 @@ const char* avattn_strerror(int status) {
   }
 }
 
-int avattn_abi_version(void) { return 13; }
+int avattn_abi_version(void) { return 14; }
 
 }  // extern "C"
 

@@ -15,8 +15,8 @@ Ops (namespace ``avgen_amd``):
 * ``rope_apply(x, cos, sin, inverse) -> x_rot`` — src/avgen/models/rope.py
   :297-338, differentiable.
 
-``flash_fwd``, ``flash_bwd``, ``flash_fwd_windowed``, ``flash_bwd_windowed``
-and ``rope_apply`` take float32 tensors too (all of q, k, v and dout/out, or
+``flash_fwd``, ``flash_bwd``, ``flash_fwd_windowed``, ``flash_bwd_windowed``,
+``qk_norm_rope(_bwd)`` and ``rope_apply`` take float32 tensors too (all of q, k, v and dout/out, or
 x), computed in fp32 by the library's fp32 kernels (the reference's
 attention runs in the caller's dtype); every other op is bf16 only.
 * ``flash_fwd_fp8(q, k, v, key_mask, q_scale, k_scale, scale) -> (out, lse)``
@@ -999,15 +999,16 @@ def _rope_apply_impl(x, cos, sin, inverse):
 def _qk_norm_common(name, x, weight, eps, cos, sin):
     if x.ndim != 4:
         raise ValueError(f"{name}: input must be (batch, heads, length, head_dim); got {tuple(x.shape)}")
-    if x.dtype is not torch.bfloat16:
-        raise TypeError(f"{name}: input must be bfloat16; got {x.dtype}")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"{name}: input must be bfloat16 or float32; got {x.dtype}")
     B, H, L, D = x.shape
     if D not in SUPPORTED_HEAD_DIMS:
         raise ValueError(f"{name}: head_dim {D} not supported (supported: {SUPPORTED_HEAD_DIMS})")
     if weight is not None:
         if weight.shape != (D,):
             raise ValueError(f"{name}: weight must be ({D},); got {tuple(weight.shape)}")
-        weight = weight.to(torch.bfloat16).contiguous()
+        # the gain in the activation's dtype (src/avgen/models/layers.py:114-116)
+        weight = weight.to(x.dtype).contiguous()
     tsb = 0
     if cos is not None or sin is not None:
         if cos is None or sin is None:
@@ -1016,15 +1017,18 @@ def _qk_norm_common(name, x, weight, eps, cos, sin):
     if not (eps >= 0.0 and math.isfinite(eps)):
         raise ValueError(f"{name}: eps must be finite and >= 0; got {eps}")
     _require_gpu(name, x, weight, cos, sin)
-    return _kernel_ready(x), weight, cos, sin, tsb
+    return (_f32_ready(x) if x.dtype is torch.float32 else _kernel_ready(x)), weight, cos, sin, tsb
 
 
 def _qk_norm_rope_impl(x, weight, eps, cos, sin):
     name = "avgen_amd.qk_norm_rope"
     x, w, cos, sin, tsb = _qk_norm_common(name, x, weight, eps, cos, sin)
     B, H, L, D = x.shape
-    out = _kernel_ready(torch.empty_like(x, memory_format=torch.preserve_format))
-    st = _lib.load().avattn_qk_norm_rope(
+    f32 = x.dtype is torch.float32
+    out = torch.empty_like(x, memory_format=torch.preserve_format)
+    out = _f32_ready(out) if f32 else _kernel_ready(out)
+    lib = _lib.load()
+    st = (lib.avattn_qk_norm_rope_f32 if f32 else lib.avattn_qk_norm_rope)(
         _ptr(x), _strides3(x), B, H, L, D, _ptr(w), float(eps), _ptr(cos), _ptr(sin), tsb,
         _ptr(out), _strides3(out), _stream(x.device))
     _lib.check(st, name)
@@ -1035,17 +1039,19 @@ def _qk_norm_rope_bwd_impl(dy, x, weight, eps, cos, sin):
     name = "avgen_amd.qk_norm_rope_bwd"
     x, w, cos, sin, tsb = _qk_norm_common(name, x, weight, eps, cos, sin)
     B, H, L, D = x.shape
-    if dy.shape != x.shape or dy.dtype is not torch.bfloat16:
-        raise ValueError(f"{name}: dy must be bf16 {tuple(x.shape)}")
+    f32 = x.dtype is torch.float32
+    if dy.shape != x.shape or dy.dtype is not x.dtype:
+        raise ValueError(f"{name}: dy must be {x.dtype} {tuple(x.shape)}")
     _require_gpu(name, dy)
-    dy = _kernel_ready(dy)
-    dx = _kernel_ready(torch.empty_like(x, memory_format=torch.preserve_format))
+    ready = _f32_ready if f32 else _kernel_ready
+    dy = ready(dy)
+    dx = ready(torch.empty_like(x, memory_format=torch.preserve_format))
     lib = _lib.load()
     dw = ws = None
     if w is not None:
         dw = torch.empty(D, device=x.device, dtype=torch.float32)
         ws = _workspace(lib.avattn_qk_norm_rope_bwd_workspace_size(D), x.device)
-    st = lib.avattn_qk_norm_rope_bwd(
+    st = (lib.avattn_qk_norm_rope_bwd_f32 if f32 else lib.avattn_qk_norm_rope_bwd)(
         _ptr(x), _strides3(x), _ptr(dy), _strides3(dy), B, H, L, D, _ptr(w), float(eps),
         _ptr(cos), _ptr(sin), tsb, _ptr(dx), _strides3(dx), _ptr(dw), _ptr(ws), 0 if ws is None else ws.numel(),
         _stream(x.device))
@@ -1200,7 +1206,8 @@ def qk_norm_rope(
     x: torch.Tensor, weight: Optional[torch.Tensor], eps: float, cos: Optional[torch.Tensor],
     sin: Optional[torch.Tensor],
 ) -> torch.Tensor:
-    """Per-head RMSNorm (gain ``weight`` cast to bf16) then the rotation; see module docstring."""
+    """Per-head RMSNorm (gain ``weight`` cast to the input's dtype, bf16 or
+    float32) then the rotation; see module docstring."""
     return _qk_norm_rope_impl(x, weight, eps, cos, sin)
 
 

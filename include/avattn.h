@@ -46,7 +46,10 @@
  *   avattn_fwd_windowed_f32,  avattn_bwd_windowed for float32 tensors (the
  *   avattn_bwd_windowed_f32,  reference's attention and rotation run in
  *   avattn_bwd_f32_staged_workspace_size,  the caller's dtype; its CPU
- *   avattn_rope_apply_f32  tests and config c1 are float32)
+ *   avattn_rope_apply_f32,  tests and config c1 are float32)
+ *   avattn_qk_norm_rope_f32,  avattn_qk_norm_rope(_bwd) for float32 rows
+ *   avattn_qk_norm_rope_bwd_f32  (a float32 model's q_norm/k_norm, with
+ *                       the gain in fp32, then apply_rotary)
  */
 #ifndef AVATTN_H
 #define AVATTN_H
@@ -727,6 +730,35 @@ int avattn_bwd_windowed_f32(const float* dout, const float* q, const float* k, c
                             float* dv, const int64_t* dv_strides,
                             void* workspace, size_t workspace_bytes,
                             avattn_stream_t stream);
+
+/*
+ * avattn_qk_norm_rope / avattn_qk_norm_rope_bwd on float32 rows with a
+ * float32 gain (src/avgen/models/layers.py:106-118: outside autocast the
+ * gain stays in the activation's dtype, fp32): n = (x*rstd)*w and its
+ * rotation in fp32 (each product and sum rounded on its own), no final
+ * rounding; backward as the bf16 one in fp32 (dx, and dweight summed in a
+ * fixed order).  Arguments, layouts and errors as the bf16 functions
+ * (float* instead of void*); the backward workspace is
+ * avattn_qk_norm_rope_bwd_workspace_size(head_dim) bytes, used with a gain.
+ */
+int avattn_qk_norm_rope_f32(const float* x, const int64_t* x_strides,
+                            int32_t batch, int32_t heads, int32_t len,
+                            int32_t head_dim, const float* weight, float eps,
+                            const float* cos_tab, const float* sin_tab,
+                            int64_t table_batch_stride,
+                            float* out, const int64_t* out_strides,
+                            avattn_stream_t stream);
+
+int avattn_qk_norm_rope_bwd_f32(const float* x, const int64_t* x_strides,
+                                const float* dy, const int64_t* dy_strides,
+                                int32_t batch, int32_t heads, int32_t len,
+                                int32_t head_dim, const float* weight, float eps,
+                                const float* cos_tab, const float* sin_tab,
+                                int64_t table_batch_stride,
+                                float* dx, const int64_t* dx_strides,
+                                float* dweight,
+                                void* workspace, size_t workspace_bytes,
+                                avattn_stream_t stream);
 
 int avattn_rope_apply_f32(const float* x, const int64_t* x_strides,
                           int32_t batch, int32_t heads, int32_t len,

@@ -143,15 +143,31 @@ def rms_norm_bf16(x: np.ndarray, weight: np.ndarray | None, eps: float = 1e-6) -
     return bf16_round(t)
 
 
+def rms_norm_f64(x: np.ndarray, weight: np.ndarray | None, eps: float = 1e-6) -> np.ndarray:
+    """F.rms_norm over the last axis in float64 with the gain as given: a
+    float32 model's FusedRMSNorm outside autocast
+    (src/avgen/models/layers.py:106-118, the gain kept in fp32)."""
+    x = np.asarray(x, np.float64)
+    y = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+    return y if weight is None else y * np.asarray(weight, np.float64)
+
+
 def rms_norm_bwd_f64(
-    x: np.ndarray, weight: np.ndarray | None, g: np.ndarray, eps: float = 1e-6
+    x: np.ndarray, weight: np.ndarray | None, g: np.ndarray, eps: float = 1e-6, round_gain: bool = True
 ) -> tuple[np.ndarray, np.ndarray | None]:
     """Gradients of ``y = x * rstd(x) * w`` over the last axis in float64:
     ``dx = rstd * (w*g - xh * mean(w*g*xh))``, ``xh = x*rstd``, and
-    ``dw = sum(g * xh)`` over every other axis (None without a gain)."""
+    ``dw = sum(g * xh)`` over every other axis (None without a gain).  The
+    gain is rounded to bf16 first (bf16 activations), unless ``round_gain``
+    is False (float32 activations keep it in fp32)."""
     x = np.asarray(x, np.float64)
     g = np.asarray(g, np.float64)
-    w = np.ones(x.shape[-1]) if weight is None else bf16_round(np.asarray(weight, np.float32)).astype(np.float64)
+    if weight is None:
+        w = np.ones(x.shape[-1])
+    elif round_gain:
+        w = bf16_round(np.asarray(weight, np.float32)).astype(np.float64)
+    else:
+        w = np.asarray(weight, np.float64)
     rstd = 1.0 / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
     xh = x * rstd
     wg = w * g

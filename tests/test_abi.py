@@ -51,7 +51,7 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_strerror_and_version(lib):
-    assert lib.avattn_abi_version() == 13
+    assert lib.avattn_abi_version() == 14
     for code in range(0, 11):
         assert lib.avattn_strerror(code)
     assert b"unknown" in lib.avattn_strerror(12345)

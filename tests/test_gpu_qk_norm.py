@@ -162,3 +162,103 @@ def test_self_attention_core_variants(amd, norm, rope):
     ro, _ = R.attention_f64(prep(qp), prep(kp), _f(vp).reshape(B, L, H, D).transpose(0, 2, 1, 3))
     ro = ro.transpose(0, 2, 1, 3).reshape(B, L, H * D)
     assert np.abs(_f(out) - ro).max() <= 2e-2
+
+
+# ---------------------------------------------------------------------------
+# float32 rows (avattn_qk_norm_rope_f32 / _bwd_f32): a float32 model outside
+# autocast keeps the gain in fp32 (src/avgen/models/layers.py:106-118).
+# References in float64: the norm from the pinned oracle, the rotation as a
+# complex multiplication by cos + i*sin (its transpose: by the conjugate).
+# ---------------------------------------------------------------------------
+
+
+def _f32(shape, seed, scale=1.0):
+    g = torch.Generator()
+    g.manual_seed(seed)
+    return torch.randn(shape, generator=g) * scale
+
+
+def _rot64(x, cos, sin, inverse=False):
+    z = x[..., 0::2].astype(np.float64) + 1j * x[..., 1::2].astype(np.float64)
+    r = np.asarray(cos, np.float64) + 1j * np.asarray(sin, np.float64)
+    z = z * (np.conj(r) if inverse else r)
+    out = np.empty(x.shape, np.float64)
+    out[..., 0::2], out[..., 1::2] = z.real, z.imag
+    return out
+
+
+@pytest.mark.parametrize("B,H,grid,D,layout,gain,rope", CASES)
+def test_f32_qk_norm_rope_matches_oracle(amd, B, H, grid, D, layout, gain, rope):
+    L = grid[0] * grid[1] * grid[2]
+    print(f"f32 qk_norm case B={B} H={H} L={L} D={D} layout={layout} gain={gain} rope={rope}", flush=True)
+    if layout == "blhd":
+        x = _f32((B, L, H * D), 41).cuda().unflatten(-1, (H, D)).transpose(1, 2)
+    else:
+        x = _f32((B, H, L, D), 41).cuda()
+    x.requires_grad_(True)
+    w = ((torch.rand(D, generator=torch.Generator().manual_seed(42)) + 0.5 + 1e-4).cuda().requires_grad_(True)
+         if gain else None)
+    tables = _tables(amd, B, grid, D) if rope else None
+    y = amd.layers.qk_norm_rope(x, w, eps=1e-6, tables=tables)
+    assert y.dtype is torch.float32 and y.stride() == x.stride()
+    wn = None if w is None else _f(w)
+    ref = R.rms_norm_f64(_f(x), wn, 1e-6)
+    if tables is not None:
+        ref = _rot64(ref, _f(tables.cos), _f(tables.sin))
+    err = np.abs(_f(y) - ref).max()
+    print(f"  y err {err:.3e} (ref max {np.abs(ref).max():.3e})", flush=True)
+    assert err <= 1e-6 * max(1.0, np.abs(ref).max())
+    dy = _f32((B, H, L, D), 43).cuda()
+    y.backward(dy)
+    g = _f(dy) if tables is None else _rot64(_f(dy), _f(tables.cos), _f(tables.sin), inverse=True)
+    rdx, rdw = R.rms_norm_bwd_f64(_f(x), wn, g, 1e-6, round_gain=False)
+    err = np.abs(_f(x.grad) - rdx).max()
+    print(f"  dx err {err:.3e} (ref max {np.abs(rdx).max():.3e})", flush=True)
+    assert x.grad.dtype is torch.float32 and err <= 2e-5 * np.abs(rdx).max()
+    if gain:
+        derr = np.abs(_f(w.grad) - rdw).max()
+        print(f"  dw err {derr:.3e} (ref max {np.abs(rdw).max():.3e})", flush=True)
+        assert w.grad.dtype is torch.float32 and derr <= 1e-4 * np.abs(rdw).max()
+
+
+def test_f32_qk_norm_dw_is_deterministic(amd):
+    x = _f32((1, 8, 3000, 128), 45).cuda()
+    w = torch.rand(128, device="cuda") + 0.5
+    dy = _f32((1, 8, 3000, 128), 46).cuda()
+    a = amd.ops.qk_norm_rope_bwd(dy, x, w, 1e-6, None, None)
+    b = amd.ops.qk_norm_rope_bwd(dy, x, w, 1e-6, None, None)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_f32_self_attention_core_matches_oracle(amd):
+    """The attention section of SelfAttention on float32 projections: fp32
+    norm with fp32 gains, fp32 rotation and fp32 attention against the
+    float64 composition; gradients reach every input."""
+    B, Hq, Hkv, D, grid = 2, 4, 2, 128, (3, 8, 12)
+    L = grid[0] * grid[1] * grid[2]
+    qp = _f32((B, L, Hq * D), 51).cuda().requires_grad_(True)
+    kp = _f32((B, L, Hkv * D), 52).cuda().requires_grad_(True)
+    vp = _f32((B, L, Hkv * D), 53).cuda().requires_grad_(True)
+    wq = (torch.rand(D, generator=torch.Generator().manual_seed(54)) + 0.5).cuda().requires_grad_(True)
+    wk = (torch.rand(D, generator=torch.Generator().manual_seed(55)) + 0.5).cuda().requires_grad_(True)
+    tables = _tables(amd, B, grid, D)
+    km = torch.ones(B, L, dtype=torch.bool)
+    km[1, L - 50:] = False
+    mask = amd.attention.key_padding_mask(km.cuda())
+    out = amd.layers.self_attention_core(qp, kp, vp, head_dim=D, q_norm_weight=wq, k_norm_weight=wk,
+                                         rope=tables, key_mask=mask)
+    assert out.dtype is torch.float32 and out.shape == (B, L, Hq * D)
+
+    def prep(t, w, H):
+        x = R.rms_norm_f64(_f(t).reshape(B, L, H, D).transpose(0, 2, 1, 3), _f(w), 1e-6)
+        return _rot64(x, _f(tables.cos), _f(tables.sin))
+
+    ro, _ = R.attention_f64(prep(qp, wq, Hq), prep(kp, wk, Hkv), _f(vp).reshape(B, L, Hkv, D).transpose(0, 2, 1, 3),
+                            km.numpy())
+    ro = ro.transpose(0, 2, 1, 3).reshape(B, L, Hq * D)
+    err = np.abs(_f(out) - ro).max()
+    print(f"  f32 self-attention out err {err:.3e}", flush=True)
+    assert err <= 2e-5 * max(1.0, np.abs(ro).max())
+    out.backward(_f32((B, L, Hq * D), 56).cuda())
+    for t in (qp, kp, vp, wq, wk):
+        assert t.grad is not None and t.grad.dtype is torch.float32 and torch.isfinite(t.grad).all()

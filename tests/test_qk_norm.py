@@ -50,6 +50,27 @@ def test_rms_norm_hand_worked():
                                rtol=2 ** -7)
 
 
+def test_rms_norm_f64_matches_torch_and_autograd_with_an_fp32_gain():
+    """The float32 model's norm: F.rms_norm in float64 with a gain that is
+    not a bf16 value (so a stray bf16 rounding of the gain would show), its
+    autograd gradients against rms_norm_bwd_f64 with round_gain=False."""
+    x = torch.randn(2, 7, 128, dtype=torch.float64, requires_grad=True)
+    w = (torch.rand(128, dtype=torch.float64) + 0.5 + 1e-4).requires_grad_(True)
+    assert not torch.equal(w.to(torch.bfloat16).double(), w)
+    np.testing.assert_allclose(R.rms_norm_f64(x.detach().numpy(), w.detach().numpy(), 1e-6),
+                               F.rms_norm(x, (128,), w, 1e-6).detach().numpy(), rtol=1e-13, atol=1e-15)
+    np.testing.assert_allclose(R.rms_norm_f64(x.detach().numpy(), None, 1e-6),
+                               F.rms_norm(x, (128,), None, 1e-6).detach().numpy(), rtol=1e-13, atol=1e-15)
+    g = torch.randn(2, 7, 128, dtype=torch.float64)
+    F.rms_norm(x, (128,), w, 1e-6).backward(g)
+    dx, dw = R.rms_norm_bwd_f64(x.detach().numpy(), w.detach().numpy(), g.numpy(), 1e-6, round_gain=False)
+    np.testing.assert_allclose(dx, x.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, w.grad.numpy(), rtol=1e-10, atol=1e-12)
+    # the default rounds the gain: a different (wrong here) dx
+    dx_r, _ = R.rms_norm_bwd_f64(x.detach().numpy(), w.detach().numpy(), g.numpy(), 1e-6)
+    assert np.abs(dx_r - x.grad.numpy()).max() > 1e-6
+
+
 def test_rms_norm_backward_oracle_matches_autograd():
     x = torch.randn(3, 5, 64, dtype=torch.float64, requires_grad=True)
     w = (torch.rand(64, dtype=torch.float64) + 0.5).to(torch.bfloat16).double().requires_grad_(True)
