@@ -497,3 +497,69 @@ def test_rope_f32_validation_paths(lib):
     assert call(os=_lib.i64_array([1024 * 128, 1024 * 128, 2])) == _lib.ERR_LAYOUT
     assert call(tsb=-4) == _lib.ERR_LAYOUT
     assert call(L=0) == _lib.OK
+
+
+@cpu_only
+def test_windowed_f32_validation_paths(lib):
+    s = _lib.i64_array([1024 * 128, 1024 * 128, 128])
+
+    def fwd(**over):
+        a = dict(q=16, k=16, v=16, B=1, Hq=2, Hkv=2, Lq=4, Lk=4, D=128, mask=None, msb=0, lo=16, hi=32, wsb=0,
+                 scale=0.125, out=16, lse=16)
+        a.update(over)
+        return lib.avattn_fwd_windowed_f32(a["q"], a["k"], a["v"], s, s, s, a["B"], a["Hq"], a["Hkv"], a["Lq"],
+                                           a["Lk"], a["D"], a["mask"], a["msb"], a["lo"], a["hi"], a["wsb"],
+                                           a["scale"], a["out"], s, a["lse"], None)
+
+    def bwd(**over):
+        a = dict(lo=16, hi=32, wsb=0, D=128, ws=256, wsb_ws=1 << 20)
+        a.update(over)
+        return lib.avattn_bwd_windowed_f32(16, 16, 16, 16, 16, 16, s, s, s, s, s, 1, 2, 2, 4, 4, a["D"], None, 0,
+                                           a["lo"], a["hi"], a["wsb"], 0.125, 16, s, 16, s, 16, s, a["ws"],
+                                           a["wsb_ws"], None)
+
+    assert fwd(D=96) == _lib.ERR_HEAD_DIM
+    assert fwd(lo=None) == _lib.ERR_NULL_POINTER  # one bound without the other
+    assert fwd(hi=None) == _lib.ERR_NULL_POINTER
+    assert fwd(lo=18) == _lib.ERR_LAYOUT  # int32 windows 4-byte aligned
+    assert fwd(wsb=2) == _lib.ERR_ARGUMENT  # a batch stride shorter than len_q
+    assert fwd(wsb=-4) == _lib.ERR_ARGUMENT
+    assert fwd(q=8) == _lib.ERR_LAYOUT
+    assert fwd(Lq=0) == _lib.OK
+    assert bwd(D=96) == _lib.ERR_HEAD_DIM
+    assert bwd(hi=None) == _lib.ERR_NULL_POINTER
+    assert bwd(wsb=3) == _lib.ERR_ARGUMENT
+    assert bwd(ws=None) == _lib.ERR_WORKSPACE
+
+
+@cpu_only
+def test_qk_norm_f32_validation_paths(lib):
+    s = _lib.i64_array([1 << 20, 128, 1 << 12])
+
+    def fwd(**o):
+        a = dict(x=16, xs=s, B=1, H=2, L=4, D=128, w=16, eps=1e-6, cos=None, sin=None, tsb=0, out=16, os=s)
+        a.update(o)
+        return lib.avattn_qk_norm_rope_f32(a["x"], a["xs"], a["B"], a["H"], a["L"], a["D"], a["w"], a["eps"],
+                                           a["cos"], a["sin"], a["tsb"], a["out"], a["os"], None)
+
+    def bwd(ws=256, wsb=4096 * 128 * 4, dw=16, w=16, x=16):
+        return lib.avattn_qk_norm_rope_bwd_f32(x, s, 16, s, 1, 2, 4, 128, w, 1e-6, None, None, 0, 16, s, dw, ws,
+                                               wsb, None)
+
+    assert fwd(D=96) == _lib.ERR_HEAD_DIM
+    assert fwd(L=-1) == _lib.ERR_BAD_SHAPE
+    assert fwd(eps=-1.0) == _lib.ERR_ARGUMENT
+    assert fwd(eps=float("nan")) == _lib.ERR_ARGUMENT
+    assert fwd(cos=16) == _lib.ERR_NULL_POINTER
+    assert fwd(x=None) == _lib.ERR_NULL_POINTER
+    assert fwd(out=None) == _lib.ERR_NULL_POINTER
+    assert fwd(x=8) == _lib.ERR_LAYOUT
+    assert fwd(w=8) == _lib.ERR_LAYOUT
+    assert fwd(cos=16, sin=16, tsb=2) == _lib.ERR_LAYOUT
+    assert fwd(os=_lib.i64_array([1 << 20, 128, 102])) == _lib.ERR_LAYOUT  # rows 16-byte aligned: 4 floats
+    assert fwd(L=0) == _lib.OK
+    assert bwd(dw=None) == _lib.ERR_NULL_POINTER
+    assert bwd(ws=None) == _lib.ERR_WORKSPACE
+    assert bwd(wsb=100) == _lib.ERR_WORKSPACE
+    assert bwd(ws=8) == _lib.ERR_WORKSPACE  # workspace 16-byte aligned
+    assert bwd(x=8) == _lib.ERR_LAYOUT
