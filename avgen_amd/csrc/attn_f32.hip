@@ -12,11 +12,17 @@
 //   * backward, without atomics: row statistics (lse2 = lse*log2 e, +inf
 //     for a row without keys; ndelta = -rowsum(dO*O)), then dK/dV with a
 //     pair of waves per 32 keys looping over 32-row query tiles of every
-//     query head of its group, and dQ with a pair of waves per 32 query rows
-//     looping over 32-key tiles;
+//     query head of its group, and dQ either from the dS the dK/dV kernel
+//     staged (one product, in passes of (batch, kv head) pairs) or with a
+//     pair of waves per 32 query rows recomputing S and dP;
+//   * per-row key windows in all of them (the temporal neighbour and packed
+//     varlen masks of src/avgen/models/blocks.py:54-104 and
+//     src/avgen/data/packing.py:181-200), visiting only the tiles that meet;
 //   * the interleaved-pair rotation of fp32 tensors (and its transpose),
-//     with the reference's operation order (two products, one sum, no FMA).
-// Every kernel is sized for two waves per SIMD (at most 256 registers).
+//     with the reference's operation order (two products, one sum, no FMA),
+//     and the per-head RMSNorm fused with it (q_norm/k_norm, fp32 gain).
+// Every attention kernel is sized for two waves per SIMD (at most 256
+// registers).
 // They are the exact-dtype path for fp32 callers; the bf16 kernels are the
 // fast path.
 #include "avattn.h"
