@@ -458,3 +458,42 @@ def test_f32_temporal_neighbour_attention_matches_the_dense_mask(amd):
     ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), ro, rl, attn_mask=dense)
     for name, got, r in zip(("dq", "dk", "dv"), (q.grad, k.grad, v.grad), ref):
         assert np.abs(_f64(got) - r).max() <= GRAD_REL_TOL * max(np.abs(r).max(), 1e-6), name
+
+
+@pytest.mark.parametrize("staged", [True, False], ids=["staged_ds", "recompute"])
+@pytest.mark.parametrize("windowed", [False, True], ids=["plain", "windowed"])
+def test_f32_large_query_group(amd, staged, windowed):
+    """Five query heads per kv head (the dK/dV kernel's loop over the group),
+    plain and with per-batch windows, against float64."""
+    B, Hq, Hkv, Lq, Lk, D = 2, 10, 2, 300, 260, 64
+    print(f"f32 group-5 staged={staged} windowed={windowed}", flush=True)
+    q, k, v, do = (_randn(s, 100 + i) for i, s in enumerate(
+        ((B, Hq, Lq, D), (B, Hkv, Lk, D), (B, Hkv, Lk, D), (B, Hq, Lq, D))))
+    km = np.random.default_rng(105).random((B, Lk)) < 0.85
+    kmc = torch.from_numpy(km).cuda()
+    dev = torch.device("cuda", 0)
+    dense = None
+    if windowed:
+        lo, hi = _monotone_windows(B, Lq, Lk, 106, 90, 7)
+        lo_t, hi_t = torch.from_numpy(lo).cuda(), torch.from_numpy(hi).cuda()
+        dense = _window_mask(lo, hi, Lk)
+        out, lse = amd.ops.flash_fwd_windowed(q.cuda(), k.cuda(), v.cuda(), lo_t, hi_t, kmc, D ** -0.5)
+    else:
+        out, lse = amd.ops.flash_fwd(q.cuda(), k.cuda(), v.cuda(), kmc, None, None, D ** -0.5)
+    ro, rl = R.attention_f64(_f64(q), _f64(k), _f64(v), km, attn_mask=dense)
+    o, l = _f64(out), _f64(lse)
+    _check_fwd(o, l, ro, rl)
+    amd.ops.set_ds_budget(None if staged else 0, dev)
+    try:
+        if windowed:
+            grads = amd.ops.flash_bwd_windowed(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, lo_t, hi_t, kmc,
+                                               D ** -0.5)
+        else:
+            grads = amd.ops.flash_bwd(do.cuda(), q.cuda(), k.cuda(), v.cuda(), out, lse, kmc, D ** -0.5)
+    finally:
+        amd.ops.set_ds_budget(None, dev)
+    ref = R.attention_bwd_f64(_f64(do), _f64(q), _f64(k), _f64(v), o, l, km, attn_mask=dense)
+    for name, got, r in zip(("dq", "dk", "dv"), grads, ref):
+        err = np.abs(_f64(got) - r).max()
+        print(f"  {name}: max err {err:.3e} (ref max {np.abs(r).max():.3e})", flush=True)
+        assert err <= GRAD_REL_TOL * max(np.abs(r).max(), 1e-6), name
