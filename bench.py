@@ -320,7 +320,8 @@ def ingest_pmc(fetch_csv: str, write_csv: str, kernel: str, workload: str) -> di
 
     symbol = {"attn_fwd": "attn_fwd_kernel", "bwd_dkdv": "bwd_dkdv_kernel", "bwd_dq": "bwd_dq_kernel",
               "bwd_dq_ds": "bwd_dq_ds_kernel", "qk_norm": "qk_norm_fwd_kernel",
-              "qk_norm_bwd": "qk_norm_bwd_kernel"}[kernel]
+              "qk_norm_bwd": "qk_norm_bwd_kernel", "fwd_f32": "fwd_f32_kernel",
+              "bwd_dkdv_f32": "bwd_dkdv_f32_kernel", "bwd_dq_ds_f32": "bwd_dq_ds_f32_kernel"}[kernel]
 
     def read(path: str, counter: str) -> tuple[float, float, int]:
         kern, cal = [], []
@@ -916,7 +917,8 @@ def main() -> int:
                     help="also run the known-size calibration kernel (for rocprofv3 --pmc byte counters)")
     ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn two rocprofv3 --pmc CSVs into profiles/traffic_<kernel>_<config>.json and exit")
-    ap.add_argument("--kernel", default="bwd_dkdv", choices=sorted([*KERNEL_UNITS, "qk_norm", "qk_norm_bwd"]))
+    ap.add_argument("--kernel", default="bwd_dkdv", choices=sorted([*KERNEL_UNITS, "qk_norm", "qk_norm_bwd", "fwd_f32",
+                                                                    "bwd_dkdv_f32", "bwd_dq_ds_f32"]))
     ap.add_argument("--ingest-mfma", nargs=2, metavar=("COUNTER_CSV", "KERNEL_STATS_CSV"),
                     help="turn a rocprofv3 --pmc pass over MFMA_COUNTERS and a --kernel-trace --stats summary into "
                          "profiles/<config>_mfma_counters.md and exit")
@@ -968,6 +970,8 @@ def main() -> int:
     if args.config == "c2f32":
         log(f"[bench] config c2f32: {cfg['desc']}")
         print(json.dumps(bench_f32(cfg, "c2f32", args.steps, args.warmup)), flush=True)
+        if args.pmc_calibration:
+            pmc_calibration(dev)
         return 0
     if args.config == "qknorm":
         log(f"[bench] config qknorm: {cfg['desc']}")
