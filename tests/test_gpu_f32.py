@@ -1,5 +1,6 @@
-"""GPU parity of the float32 path (avattn_fwd_f32 / avattn_bwd_f32 /
-avattn_rope_apply_f32 through the C ABI) against the float64 oracle.
+"""GPU parity of the float32 path (avattn_fwd_f32 / avattn_bwd_f32 with
+staged or recomputed dq, avattn_fwd_windowed_f32 / avattn_bwd_windowed_f32,
+avattn_rope_apply_f32, through the C ABI) against the float64 oracle.
 
 The reference's attention runs in the caller's dtype
 (src/avgen/models/attention.py:227-273 -> F.scaled_dot_product_attention),
